@@ -1,0 +1,22 @@
+"""cppmega_amd — MI355X (gfx950) DeepSeek Sparse Attention hot path.
+
+Host code mirrors cppmega's Python surface (``sparse_mla_ops``,
+``dsa_indexer_fused_patch``, top-k, ``index_cache_patch``) and calls the
+hand-written HIP kernels of ``_lib/libdsa_hip.so`` through the C-ABI declared
+in ``include/dsa_hip.h``.
+"""
+from . import _lib
+from .dsa_indexer_fused_patch import apply_dsa_indexer_fused_patch, compute_index_scores_fused_bf16, index_scores
+from .dsa_topk import fused_qk_topk_naive, indexer_topk, topk_indices
+from .index_cache_patch import IndexCacheSchedule, apply_index_cache_patch
+
+__all__ = [
+    "IndexCacheSchedule",
+    "apply_dsa_indexer_fused_patch",
+    "apply_index_cache_patch",
+    "compute_index_scores_fused_bf16",
+    "fused_qk_topk_naive",
+    "index_scores",
+    "indexer_topk",
+    "topk_indices",
+]

@@ -1,0 +1,100 @@
+"""DSA indexer scores on gfx950 and the Megatron ``_compute_index_scores`` patch.
+
+Drop-in for cppmega/megatron/dsa_indexer_fused_patch.py:
+  * ``compute_index_scores_fused_bf16(q, weights, k, use_relu=True)`` (:71-133)
+    -> [b, sq, sk] fp32 with score = sum_h w * ReLU(q_h . k), fp32 accumulate;
+  * ``apply_dsa_indexer_fused_patch(force=False)`` (:136-173) installs it as
+    ``megatron...dsa._compute_index_scores``.
+
+The reference loops over heads with one fp32 bmm + 3 elementwise passes per
+head; here one MFMA kernel computes every head and reduces over heads in
+registers, writing each score once.  ``index_scores`` adds the causal modes the
+fused top-k path uses (entries above the diagonal written as -inf or not at
+all) and the e4m3 form with per-tensor scales.
+"""
+from __future__ import annotations
+
+import logging
+
+import torch
+
+from . import _lib
+
+log = logging.getLogger(__name__)
+
+__all__ = ["apply_dsa_indexer_fused_patch", "compute_index_scores_fused_bf16", "index_scores"]
+
+_PATCH_MARKER = "__cppmega_amd_dsa_indexer_fused_patched__"
+
+CAUSAL_NONE = 0       # every (t, s)
+CAUSAL_NEG_INF = 1    # s > t written as -inf
+CAUSAL_LOWER = 2      # only s <= t written
+
+
+def index_scores(q, weights, k, use_relu=True, causal=CAUSAL_NONE, q_scale=None, k_scale=None, out=None):
+    """q [sq,b,h,d] (bf16 or e4m3), weights [sq,b,h] (f32 or bf16), k [sk,b,d] -> [b,sq,sk] f32.
+
+    For e4m3 q / k, q_scale and k_scale are one-element f32 tensors (per-tensor
+    dequant factors, real = fp8 * scale).
+    """
+    assert q.dim() == 4, f"q must be [sq,b,h,d], got {tuple(q.shape)}"
+    assert k.dim() == 3, f"k must be [sk,b,d], got {tuple(k.shape)}"
+    assert weights.dim() == 3, f"weights must be [sq,b,h], got {tuple(weights.shape)}"
+    sq, b, h, d = q.shape
+    sk, bk, dk = k.shape
+    assert bk == b and dk == d, f"shape mismatch q={tuple(q.shape)} k={tuple(k.shape)}"
+    assert tuple(weights.shape) == (sq, b, h), f"weights {tuple(weights.shape)} != {(sq, b, h)}"
+    fp8 = q.dtype == torch.float8_e4m3fn
+    if fp8:
+        assert k.dtype == torch.float8_e4m3fn, "q and k must both be e4m3"
+        assert q_scale is not None and k_scale is not None, "e4m3 indexer inputs need q_scale and k_scale"
+        q_scale = q_scale.reshape(-1)[:1].to(torch.float32).contiguous()
+        k_scale = k_scale.reshape(-1)[:1].to(torch.float32).contiguous()
+    else:
+        if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
+            raise TypeError(f"indexer q/k must be bf16 or float8_e4m3fn, got {q.dtype}/{k.dtype}")
+    if weights.dtype not in (torch.float32, torch.bfloat16):
+        weights = weights.float()
+    q, k, weights = q.contiguous(), k.contiguous(), weights.contiguous()
+    if out is None:
+        out = torch.empty((b, sq, sk), dtype=torch.float32, device=q.device)
+    else:
+        assert out.shape == (b, sq, sk) and out.dtype == torch.float32 and out.is_contiguous()
+    dev = _lib.ensure_device(q)
+    rc = _lib.load().dsa_indexer_scores(
+        q.data_ptr(), weights.data_ptr(), k.data_ptr(), out.data_ptr(), b, sq, sk, h, d,
+        _lib.DTYPE_E4M3 if fp8 else _lib.DTYPE_BF16,
+        _lib.DTYPE_F32 if weights.dtype == torch.float32 else _lib.DTYPE_BF16,
+        _lib.ptr(q_scale), _lib.ptr(k_scale), int(causal), 1 if use_relu else 0, _lib.stream_ptr(dev))
+    _lib.check(rc, "dsa_indexer_scores")
+    return out
+
+
+def compute_index_scores_fused_bf16(q, weights, k, use_relu: bool = True):
+    """Drop-in for Megatron DSA ``_compute_index_scores`` (bf16): [b, sq, sk] fp32, unmasked."""
+    return index_scores(q, weights, k, use_relu=use_relu, causal=CAUSAL_NONE)
+
+
+def apply_dsa_indexer_fused_patch(*, force: bool = False) -> bool:
+    """Install ``compute_index_scores_fused_bf16`` as Megatron's ``dsa._compute_index_scores``.
+
+    Idempotent; raises if the Megatron DSA module or the attribute is absent.
+    """
+    from megatron.core.transformer.experimental_attention_variant import dsa as dsa_mod
+
+    existing = getattr(dsa_mod, "_compute_index_scores", None)
+    if existing is None:
+        raise RuntimeError(
+            "megatron.core.transformer.experimental_attention_variant.dsa."
+            "_compute_index_scores not found — Megatron version mismatch?")
+    if getattr(existing, _PATCH_MARKER, False) and not force:
+        log.info("cppmega_amd DSA indexer patch already applied")
+        return True
+
+    def _compute_index_scores_fused(q, weights, k, use_relu: bool = True, **kwargs):
+        return compute_index_scores_fused_bf16(q, weights, k, use_relu=use_relu)
+
+    setattr(_compute_index_scores_fused, _PATCH_MARKER, True)
+    dsa_mod._compute_index_scores = _compute_index_scores_fused
+    log.info("cppmega_amd DSA indexer patch applied (gfx950 MFMA, heads reduced in registers)")
+    return True

@@ -1,0 +1,52 @@
+"""Shared host-side helpers of the SparseMLA entry points."""
+from __future__ import annotations
+
+import os
+
+import torch
+
+from .. import _lib
+
+
+def normalize_sm_scale(sm_scale, d_qk: int) -> float:
+    """None -> d_qk^-0.5; a tensor is read once on the host (as the reference
+    does, cppmega/megatron/sparse_mla_ops/tilelang_sparse_mla_fwd.py:74-82)."""
+    if sm_scale is None:
+        return float(d_qk) ** -0.5
+    if isinstance(sm_scale, torch.Tensor):
+        return float(sm_scale.detach().item())
+    return float(sm_scale)
+
+
+def env_int(name: str, default: int) -> int:
+    """Same parsing as the reference's _env_int (tilelang_sparse_mla_fwd.py:43-51)."""
+    value = os.getenv(name)
+    if value is None:
+        return default
+    try:
+        parsed = int(value)
+    except ValueError:
+        return default
+    return parsed if parsed > 0 else default
+
+
+def unwrap_quantized(t):
+    """Dequantise a Transformer-Engine QuantizedTensor if one is passed (TE is
+    optional; plain tensors are returned unchanged)."""
+    try:
+        from transformer_engine.pytorch.tensor import QuantizedTensor  # type: ignore
+    except ImportError:
+        return t
+    if isinstance(t, QuantizedTensor):
+        return t.dequantize()
+    return t
+
+
+def stream_of(t: torch.Tensor) -> tuple[int, int]:
+    dev = _lib.ensure_device(t)
+    return dev, _lib.stream_ptr(dev)
+
+
+def check_same_device(*ts):
+    devs = {t.device for t in ts if t is not None}
+    assert len(devs) == 1, f"all tensors must be on one device, got {sorted(map(str, devs))}"

@@ -1,0 +1,167 @@
+/*
+ * dsa_hip.h — C-ABI of the MI355X (gfx950) DeepSeek Sparse Attention hot path.
+ *
+ * Every entry point is stateless, stream-ordered and returns an int status
+ * (DSA_OK == 0, negative on error; dsa_last_error() holds a per-thread
+ * message).  All device buffers are caller-owned.  `stream` is a hipStream_t
+ * passed as void* so that this header needs no HIP include; NULL means the
+ * null stream.  Tensors are dense, row-major and contiguous in the shapes
+ * given below.  No entry point allocates device memory; scratch space comes
+ * from a caller-provided workspace sized by the matching *_workspace_size().
+ *
+ * Index convention (all SparseMLA entry points): indices are int32 and any
+ * value outside [0, S_kv) — in particular the -1 sentinel — marks a masked
+ * slot.  Duplicate indices are legal and counted once per occurrence.
+ * LSE is returned in log2 units: lse2 = log2(sum_j exp(sm_scale * q.k_j)).
+ * A (token, head) whose slots are all masked yields out = 0, lse2 = -inf and
+ * zero gradients.
+ */
+#ifndef DSA_HIP_H_
+#define DSA_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum dsa_status {
+  DSA_OK = 0,
+  DSA_ERR_INVALID_ARG = -1,  /* shape / pointer / range violation           */
+  DSA_ERR_UNSUPPORTED = -2,  /* valid request this build has no kernel for  */
+  DSA_ERR_HIP = -3,          /* HIP runtime error (launch, device query)    */
+  DSA_ERR_WORKSPACE = -4     /* workspace missing or smaller than required  */
+};
+
+enum dsa_dtype {
+  DSA_DTYPE_BF16 = 0,        /* bfloat16                                     */
+  DSA_DTYPE_E4M3 = 1,        /* OCP float8 e4m3fn (max 448), gfx950 native   */
+  DSA_DTYPE_F32 = 2          /* float32                                      */
+};
+
+/* Per-thread message for the last non-zero status returned on this thread. */
+const char *dsa_last_error(void);
+
+/* ABI version (major * 100 + minor). */
+int dsa_abi_version(void);
+
+/* Returns DSA_OK when `device` is a gfx950 (MI355X-class) GPU, otherwise
+ * DSA_ERR_UNSUPPORTED with the architecture named in dsa_last_error(). */
+int dsa_device_check(int device);
+
+/*
+ * SparseMLA forward (MQA, packed latent KV).
+ * Replaces sparse_mla_fwd_interface / the TileLang `sparse_mla_fwd` kernel
+ *   (cppmega/megatron/sparse_mla_ops/tilelang_sparse_mla_fwd.py:128-290,293-391)
+ * and, with dtype == DSA_DTYPE_E4M3, sparse_mla_fwd_fp8_interface
+ *   (cppmega/megatron/sparse_mla_ops/tilelang_sparse_mla_fwd_fp8.py:178-393,415-559).
+ *
+ *   q       [B, S, H, D_qk]      bf16 or e4m3 (dtype)
+ *   kv      [B, S_kv, G, D_qk]   bf16 or e4m3 (dtype); V = kv[..., :D_v]
+ *   indices [B, S, G, topk]      int32
+ *   out     [B, S, H, D_v]       bf16
+ *   lse2    [B, S, H]            f32 (log2 units)
+ *   q_scale [B, S], kv_scale [B, S_kv]  f32 dequant factors (real = fp8 * scale),
+ *                                 required for e4m3, ignored (may be NULL) for bf16.
+ * Head h reads kv group h / (H / G).  sm_scale multiplies the raw q.k dot.
+ */
+int dsa_sparse_mla_fwd(const void *q, const void *kv, const int32_t *indices,
+                       void *out, float *lse2, int64_t B, int64_t S,
+                       int64_t S_kv, int64_t H, int64_t G, int64_t D_qk,
+                       int64_t D_v, int64_t topk, float sm_scale, int dtype,
+                       const float *q_scale, const float *kv_scale,
+                       void *stream);
+
+/* Bytes of workspace dsa_sparse_mla_bwd needs for these dimensions. */
+size_t dsa_sparse_mla_bwd_workspace_size(int64_t B, int64_t S, int64_t S_kv,
+                                         int64_t H, int64_t G, int64_t D_qk,
+                                         int64_t D_v, int64_t topk);
+
+/*
+ * SparseMLA backward.
+ * Replaces sparse_mla_bwd = preprocess + bwd + postprocess
+ *   (cppmega/megatron/sparse_mla_ops/tilelang_sparse_mla_bwd.py:114-201,204-419,422-531)
+ * and, with dtype == DSA_DTYPE_E4M3, sparse_mla_bwd_fp8
+ *   (cppmega/megatron/sparse_mla_ops/tilelang_sparse_mla_bwd_fp8.py:191-489,492-630).
+ *
+ *   q, kv, indices, q_scale, kv_scale as in dsa_sparse_mla_fwd
+ *   o   [B, S, H, D_v] bf16 (forward output), dO [B, S, H, D_v] bf16
+ *   lse2 [B, S, H] f32 (forward LSE, log2 units)
+ *   delta [B, S, H] f32 = sum_d o * dO, or NULL to compute it from o and dO
+ *   dq  [B, S, H, D_qk] bf16 (written), dkv [B, S_kv, G, D_qk] bf16 (written)
+ * dKV is reduced deterministically: every kv row sums its per-(token, slot)
+ * contributions in ascending (token, slot) order in fp32, so repeated calls
+ * are bitwise identical.  Gradients are with respect to the dequantised
+ * values for e4m3 inputs.
+ */
+int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o,
+                       const void *dO, const int32_t *indices,
+                       const float *lse2, const float *delta, void *dq,
+                       void *dkv, void *workspace,
+                       size_t workspace_bytes, int64_t B, int64_t S,
+                       int64_t S_kv, int64_t H, int64_t G, int64_t D_qk,
+                       int64_t D_v, int64_t topk, float sm_scale, int dtype,
+                       const float *q_scale, const float *kv_scale,
+                       void *stream);
+
+/*
+ * DSA indexer scores: score[b, t, s] = sum_h w[t, b, h] * act(q[t, b, h, :] . k[s, b, :])
+ * with act = ReLU when use_relu != 0, identity otherwise; fp32 accumulate.
+ * Replaces Megatron `_compute_index_scores` as patched by
+ *   compute_index_scores_fused_bf16 (cppmega/megatron/dsa_indexer_fused_patch.py:71-133).
+ *
+ *   q [Sq, B, H, D] (dtype), w [Sq, B, H] (w_dtype: bf16 or f32),
+ *   k [Sk, B, D] (dtype), scores [B, Sq, Sk] f32.
+ *   dtype e4m3: q_scale / k_scale point to one f32 each (per-tensor dequant).
+ * causal: 0 = every (t, s) computed;
+ *         1 = s > t written as -inf;
+ *         2 = only s <= t written (the rest of each row is left untouched).
+ */
+int dsa_indexer_scores(const void *q, const void *w, const void *k,
+                       float *scores, int64_t B, int64_t Sq, int64_t Sk,
+                       int64_t H, int64_t D, int dtype, int w_dtype,
+                       const float *q_scale, const float *k_scale, int causal,
+                       int use_relu, void *stream);
+
+/*
+ * Per-row top-k selection over fp32 scores.
+ * Replaces the top-k of Megatron `fused_qk_topk_naive`
+ *   (restated in scripts/modal_dsa_indexer_bench.py:188-194) with a stricter,
+ * deterministic contract: the candidates of row r are columns [start, end);
+ * the min(topk, end - start) largest are selected, ties break to the lower
+ * column, NaN ranks as +inf, -0.0 equals +0.0; selected columns are written
+ * in ascending order and the row is padded with -1.
+ *
+ *   scores  rows of `row_len` f32, row r at scores + r * row_stride
+ *   out_idx [rows, topk] int32
+ *   starts/ends: per-row int32 window; when NULL the window is
+ *     causal != 0 : [0, min(row_len, (r % seq_q) + 1 + causal_offset))
+ *     causal == 0 : [0, row_len)
+ */
+int dsa_topk(const float *scores, int64_t rows, int64_t row_len,
+             int64_t row_stride, int64_t seq_q, int causal,
+             int64_t causal_offset, const int32_t *starts,
+             const int32_t *ends, int64_t topk, int32_t *out_idx,
+             void *stream);
+
+/*
+ * Tensorwise (current-scaling) quantisation to OCP e4m3:
+ *   amax = max|x|, scale = 448 / amax (1 when amax == 0),
+ *   out = e4m3(RNE(x * scale)) saturated to +-448, scale_inv = 1 / scale.
+ * Replaces the TE Float8CurrentScalingQuantizer call in per_token_cast_to_fp8
+ *   (cppmega/megatron/sparse_mla_ops/tilelang_sparse_mla_fwd_fp8.py:74-99,396-412).
+ *   x [n] (in_dtype bf16 or f32), out_fp8 [n] e4m3, scale_inv [1] f32,
+ *   workspace >= dsa_fp8_quantize_workspace_size() bytes.
+ */
+size_t dsa_fp8_quantize_workspace_size(void);
+int dsa_fp8_tensorwise_quantize(const void *x, int64_t n, int in_dtype,
+                                uint8_t *out_fp8, float *scale_inv,
+                                void *workspace, size_t workspace_bytes,
+                                void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSA_HIP_H_ */

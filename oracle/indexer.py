@@ -1,0 +1,73 @@
+"""CPU restatement of the DSA indexer scores.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+
+compute_index_scores follows compute_index_scores_fused_bf16
+(cppmega/megatron/dsa_indexer_fused_patch.py:71-133): a per-head loop that
+upcasts q and k to fp32, forms q_h . k with a batched matmul, applies ReLU,
+multiplies by the fp32 head weight and accumulates into a [b, sq, sk] fp32
+buffer.  compute_index_scores_einsum restates the upstream Megatron form
+that the reference test clones (tests/test_dsa_indexer_fused_patch.py:18-30).
+The FP8 form dequantises e4m3 codes with one per-tensor scale for q and one
+for k before the same arithmetic.
+"""
+from __future__ import annotations
+
+import torch
+
+
+def compute_index_scores(q, weights, k, use_relu=True, q_scale=None, k_scale=None):
+    """q [sq,b,h,d], weights [sq,b,h], k [sk,b,d] -> [b, sq, sk] fp32."""
+    sq, b, h, d = q.shape
+    sk = k.shape[0]
+    qs = 1.0 if q_scale is None else float(q_scale)
+    ks = 1.0 if k_scale is None else float(k_scale)
+    out = torch.zeros((b, sq, sk), dtype=torch.float32)
+    k_bds = k.float().permute(1, 2, 0).contiguous()           # [b, d, sk]
+    for hi in range(h):
+        q_h = q[:, :, hi, :].float().permute(1, 0, 2).contiguous()  # [b, sq, d]
+        logits = torch.bmm(q_h, k_bds)
+        if q_scale is not None or k_scale is not None:
+            logits = logits * (qs * ks)
+        if use_relu:
+            logits = torch.relu(logits)
+        w_h = weights[:, :, hi].float().transpose(0, 1).unsqueeze(-1)
+        out.add_(logits * w_h)
+    return out
+
+
+def compute_index_scores_einsum(q, weights, k, use_relu=True):
+    """Upstream Megatron `_compute_index_scores` (einsum form)."""
+    s = torch.einsum("sbhd,tbd->sbht", q.float(), k.float())
+    if use_relu:
+        s = torch.relu(s)
+    s = s * weights.float().unsqueeze(-1)
+    return s.sum(dim=2).transpose(0, 1)
+
+
+def compute_index_scores_f64(q, weights, k, use_relu=True):
+    """Float64 brute force over explicit loops of heads (tiny shapes only)."""
+    sq, b, h, d = q.shape
+    sk = k.shape[0]
+    qd, kd, wd = q.double(), k.double(), weights.double()
+    out = torch.zeros((b, sq, sk), dtype=torch.float64)
+    for bi in range(b):
+        for hi in range(h):
+            logits = qd[:, bi, hi, :] @ kd[:, bi, :].T           # [sq, sk]
+            if use_relu:
+                logits = logits.clamp_min(0)
+            out[bi] += logits * wd[:, bi, hi][:, None]
+    return out
+
+
+def causal_mask_(scores, fill=float("-inf")):
+    """Set score[b, t, s] = fill for s > t (in place) and return it."""
+    sq, sk = scores.shape[-2:]
+    mask = torch.ones(sq, sk, dtype=torch.bool).triu(1)
+    scores.masked_fill_(mask, fill)
+    return scores
+
+
+def flops_causal(b, s, h, d):
+    """Algorithmic causal FLOPs: 2 * b * h * d * s (s + 1) / 2."""
+    return 2 * b * h * d * s * (s + 1) // 2

@@ -1,0 +1,81 @@
+"""CPU restatement of the deterministic per-row top-k.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+
+The reference top-k is Megatron's `fused_qk_topk_naive`, inlined as
+`index_scores.topk(min(topk, seqlen), dim=-1)[1]`
+(scripts/modal_dsa_indexer_bench.py:188-194), with masked picks turned into
+-1 (cppmega/megatron/upstream_patches/apply_dsa_cg_patches.py:267-291).
+torch.topk leaves the order of ties unspecified; the contract restated here
+fixes it: candidates of row r are the columns [start, end), the
+min(topk, end - start) largest scores are selected, equal scores prefer the
+lower column, NaN ranks as +inf, -0.0 equals +0.0, the chosen columns are
+returned in ascending order and the row is padded with -1.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def causal_windows(rows, seq_q, row_len, offset=0):
+    """Per-row [start, end) of the causal window: end = min(row_len, r % seq_q + 1 + offset)."""
+    r = np.arange(rows)
+    ends = np.minimum(row_len, (r % seq_q) + 1 + offset).astype(np.int64)
+    return np.zeros(rows, dtype=np.int64), np.maximum(ends, 0)
+
+
+def topk_ascending(scores, topk, starts=None, ends=None):
+    """scores [rows, n] float32 -> idx [rows, topk] int32 (ascending, -1 padded).
+
+    Vectorised: one stable descending sort by score keeps the lower column first
+    among equal scores; the window is enforced by a second stable sort on an
+    out-of-window flag.
+    """
+    scores = np.asarray(scores, dtype=np.float32)
+    rows, n = scores.shape
+    if starts is None:
+        starts = np.zeros(rows, dtype=np.int64)
+    if ends is None:
+        ends = np.full(rows, n, dtype=np.int64)
+    starts = np.asarray(starts, dtype=np.int64)
+    ends = np.asarray(ends, dtype=np.int64)
+    col = np.arange(n)[None, :]
+    inwin = (col >= starts[:, None]) & (col < ends[:, None])
+    key = np.where(np.isnan(scores), np.float32(np.inf), scores).astype(np.float64)
+    key = key + 0.0  # -0.0 -> +0.0
+    order = np.argsort(-key, axis=1, kind="stable")
+    flag = (~np.take_along_axis(inwin, order, axis=1)).astype(np.int8)
+    order2 = np.argsort(flag, axis=1, kind="stable")
+    order = np.take_along_axis(order, order2, axis=1)
+    nvalid = np.clip(ends - starts, 0, None)
+    count = np.minimum(nvalid, topk)
+    out = np.full((rows, topk), -1, dtype=np.int32)
+    kk = min(topk, n)
+    sel = order[:, :kk]
+    take = np.arange(kk)[None, :] < count[:, None]
+    sel = np.where(take, sel, np.iinfo(np.int64).max)
+    sel.sort(axis=1)
+    sel = np.where(sel == np.iinfo(np.int64).max, -1, sel)
+    out[:, :kk] = sel.astype(np.int32)
+    return out
+
+
+def topk_bruteforce_row(row, topk, start=0, end=None):
+    """Pure-Python reference for one row (tiny rows only)."""
+    n = len(row)
+    end = n if end is None else end
+
+    def k(i):
+        v = float(row[i])
+        if v != v:
+            v = float("inf")
+        return (-v, i)
+
+    cand = sorted(range(start, max(start, end)), key=k)[:topk]
+    cand.sort()
+    return cand + [-1] * (topk - len(cand))
+
+
+def topk_bytes(b, s, topk):
+    """Algorithmic HBM bytes of causal top-k: fp32 causal scores read + int32 indices written."""
+    return 4 * b * s * (s + 1) // 2 + 4 * b * s * topk

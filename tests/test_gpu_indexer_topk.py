@@ -1,0 +1,168 @@
+"""GPU parity of the indexer-score, top-k and FP8-quantiser HIP kernels.
+
+Bars: indexer scores within fp32 reassociation error of the oracle
+(rel 1e-3 of the row scale, as the reference test uses); top-k indices
+bit-exact against the oracle given the same fp32 scores; e4m3 quantisation
+bit-exact (data and scale_inv) against the oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+from cppmega_amd import compute_index_scores_fused_bf16, index_scores, indexer_topk, topk_indices
+from cppmega_amd.dsa_topk import fused_qk_topk_naive
+from cppmega_amd.sparse_mla_ops import tensorwise_quantize
+from cppmega_amd import synthetic
+from oracle import fp8 as ofp8
+from oracle import indexer as oix
+from oracle import topk as otk
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel_err(a, e):
+    a, e = a.float().cpu(), e.float().cpu()
+    fin = torch.isfinite(e)
+    return float((a[fin] - e[fin]).abs().max() / e[fin].abs().max().clamp_min(1e-6))
+
+
+@pytest.mark.parametrize("S,B,H,D,wdt", [
+    (128, 2, 8 * 2, 64, torch.bfloat16),
+    (200, 1, 16, 64, torch.float32),
+    (96, 2, 32, 64, torch.float32),
+    (64, 1, 64, 64, torch.float32),
+    (72, 1, 16, 128, torch.float32),
+    (130, 1, 64, 128, torch.bfloat16),
+])
+def test_indexer_scores_match_oracle(dev, S, B, H, D, wdt):
+    inp = synthetic.indexer_inputs(B, S, H, D, seed=3, w_dtype=wdt)
+    q, k, w = inp["q"].to(dev), inp["k"].to(dev), inp["w"].to(dev)
+    got = compute_index_scores_fused_bf16(q, w, k, use_relu=True)
+    ref = oix.compute_index_scores(inp["q"], inp["w"], inp["k"], use_relu=True)
+    assert got.shape == (B, S, S) and got.dtype == torch.float32
+    assert _rel_err(got, ref) < 1e-3
+    got_nr = compute_index_scores_fused_bf16(q, w, k, use_relu=False)
+    ref_nr = oix.compute_index_scores(inp["q"], inp["w"], inp["k"], use_relu=False)
+    assert _rel_err(got_nr, ref_nr) < 1e-3
+
+
+def test_indexer_causal_modes(dev):
+    S, B, H, D = 300, 2, 16, 64
+    inp = synthetic.indexer_inputs(B, S, H, D, seed=5)
+    q, k, w = inp["q"].to(dev), inp["k"].to(dev), inp["w"].to(dev)
+    ref = oix.compute_index_scores(inp["q"], inp["w"], inp["k"])
+    neg = index_scores(q, w, k, causal=1).cpu()
+    assert _rel_err(neg, oix.causal_mask_(ref.clone())) < 1e-3
+    assert torch.isneginf(neg[:, torch.ones(S, S, dtype=torch.bool).triu(1)]).all()
+    sentinel = torch.full((B, S, S), 7.0, device=dev)
+    low = index_scores(q, w, k, causal=2, out=sentinel).cpu()
+    tri = torch.ones(S, S, dtype=torch.bool).tril()
+    assert _rel_err(low[:, tri], ref[:, tri]) < 1e-3
+    assert (low[:, ~tri] == 7.0).all()
+
+
+def test_indexer_fp8(dev):
+    S, B, H, D = 128, 1, 64, 128
+    inp = synthetic.indexer_inputs(B, S, H, D, seed=9)
+    q8, qs = ofp8.tensorwise_quantize(inp["q"])
+    k8, ks = ofp8.tensorwise_quantize(inp["k"])
+    got = index_scores(q8.to(dev), inp["w"].to(dev), k8.to(dev), q_scale=qs.to(dev), k_scale=ks.to(dev))
+    ref = oix.compute_index_scores(q8.float(), inp["w"], k8.float(), q_scale=qs, k_scale=ks)
+    assert _rel_err(got, ref) < 1e-3
+
+
+def _tie_heavy_scores(rows, n, seed):
+    g = np.random.default_rng(seed)
+    s = g.standard_normal((rows, n)).astype(np.float32)
+    s[:, ::3] = 0.0                                   # exact-zero ties (ReLU)
+    s[:, 1::7] = -0.0                                 # negative zero equals zero
+    s[g.random((rows, n)) < 0.05] = 1.5               # repeated positive value
+    s[g.random((rows, n)) < 0.01] = np.nan            # NaN ranks as +inf
+    s[g.random((rows, n)) < 0.01] = -np.inf
+    s[g.random((rows, n)) < 0.01] = np.inf
+    return s
+
+
+@pytest.mark.parametrize("rows,n,topk,causal", [
+    (300, 1000, 64, True),
+    (257, 4096, 256, True),
+    (64, 4096, 256, False),
+    (40, 5000, 300, False),
+    (16, 16384, 2048, False),
+    (8, 20000, 2048, True),
+])
+def test_topk_bit_exact(dev, rows, n, topk, causal):
+    s = _tie_heavy_scores(rows, n, seed=rows + n)
+    seq_q = rows if causal else 1
+    got = topk_indices(torch.from_numpy(s).to(dev), topk, causal=causal, seq_q=seq_q if causal else None).cpu()
+    st, en = otk.causal_windows(rows, seq_q, n) if causal else (None, None)
+    ref = otk.topk_ascending(s, topk, st, en)
+    assert got.dtype == torch.int32
+    np.testing.assert_array_equal(got.numpy(), ref)
+
+
+def test_topk_windows_and_all_equal(dev):
+    rows, n, topk = 50, 700, 32
+    s = np.zeros((rows, n), dtype=np.float32)          # all equal: lowest columns win
+    s[10] = np.arange(n, dtype=np.float32)             # strictly increasing row
+    g = np.random.default_rng(1)
+    starts = g.integers(0, n, rows).astype(np.int32)
+    ends = np.minimum(n, starts + g.integers(0, 100, rows)).astype(np.int32)
+    got = topk_indices(torch.from_numpy(s).to(dev), topk, causal=False,
+                       starts=torch.from_numpy(starts).to(dev), ends=torch.from_numpy(ends).to(dev)).cpu()
+    ref = otk.topk_ascending(s, topk, starts, ends)
+    np.testing.assert_array_equal(got.numpy(), ref)
+
+
+def test_cfg3_indexer_topk_full_scale(dev):
+    """cfg3: b=2 s=4096 h=16 d=64, causal top-256: GPU top-k == oracle top-k on the GPU's scores."""
+    B, S, H, D, K = 2, 4096, 16, 64, 256
+    inp = synthetic.indexer_inputs(B, S, H, D, seed=1234)
+    inp["w"] = inp["w"] * (16 ** 0.5) / 4                # w ~ N(0,1)/4 (cfg3)
+    q, k, w = inp["q"].to(dev), inp["k"].to(dev), inp["w"].to(dev)
+    scores, idx = indexer_topk(q, k, w, K, return_scores=True)
+    sc = scores.cpu().numpy().reshape(B * S, S)
+    st, en = otk.causal_windows(B * S, S, S)
+    ref = otk.topk_ascending(np.where(np.arange(S)[None, :] < en[:, None], sc, 0), K, st, en)
+    np.testing.assert_array_equal(idx.cpu().numpy().reshape(B * S, K), ref)
+    # scores themselves vs the oracle on sampled rows
+    rows = [0, 1, 255, 2048, 4095]
+    ref_s = oix.compute_index_scores(inp["q"][rows], inp["w"][rows], inp["k"])
+    got_s = scores.cpu()[:, rows]
+    tri = torch.arange(S)[None, :] <= torch.tensor(rows)[:, None]
+    assert _rel_err(got_s[:, tri], ref_s[:, tri]) < 1e-3
+
+
+def test_fused_qk_topk_naive_contract(dev):
+    S, B, H, D, K = 96, 2, 16, 64, 40
+    inp = synthetic.indexer_inputs(B, S, H, D, seed=11)
+    q, k, w = inp["q"].to(dev), inp["k"].to(dev), inp["w"].to(dev)
+    scores, idx = fused_qk_topk_naive(q, k, w, K)
+    assert idx.dtype == torch.int64 and idx.shape == (B, S, K)
+    ref = otk.topk_ascending(scores.cpu().numpy().reshape(B * S, S), K)
+    np.testing.assert_array_equal(idx.cpu().numpy().reshape(B * S, K), ref)
+    mask = torch.full((S, S), float("-inf")).triu(1).to(dev)
+    _, idx_c = fused_qk_topk_naive(q, k, w, K, mask=mask)
+    st, en = otk.causal_windows(B * S, S, S)
+    ref_c = otk.topk_ascending(scores.cpu().numpy().reshape(B * S, S), K, st, en)
+    np.testing.assert_array_equal(idx_c.cpu().numpy().reshape(B * S, K), ref_c)
+
+
+@pytest.mark.parametrize("n,dt", [(1, torch.float32), (1000, torch.bfloat16), (1 << 20, torch.bfloat16),
+                                  (4099, torch.float32)])
+def test_fp8_quantize_bit_exact(dev, n, dt):
+    x = synthetic.outlier_values((n,), seed=n).to(dt)
+    x8, si = tensorwise_quantize(x.to(dev))
+    r8, rsi = ofp8.tensorwise_quantize(x)
+    assert torch.equal(x8.cpu().view(torch.uint8), r8.view(torch.uint8))
+    assert torch.equal(si.cpu(), rsi)
+
+
+def test_fp8_quantize_zero_and_specials(dev):
+    x = torch.zeros(64)
+    x8, si = tensorwise_quantize(x.to(dev))
+    assert float(si) == 1.0 and torch.all(x8.cpu().float() == 0)
+    x = torch.tensor([1e-30, -1e-9, 3.0, -448.0 * 2, 5e-3, -0.0] * 8)
+    x8, si = tensorwise_quantize(x.to(dev))
+    r8, rsi = ofp8.tensorwise_quantize(x)
+    assert torch.equal(x8.cpu().view(torch.uint8), r8.view(torch.uint8)) and torch.equal(si.cpu(), rsi)

@@ -1,0 +1,189 @@
+"""GPU parity of the SparseMLA HIP kernels against the CPU oracle.
+
+Bar: bf16 out, LSE (log2 units) and gradients within 2e-2 relative / 1e-2
+absolute of the oracle (which restates the reference kernels, including the
+bf16 rounding of P and dS); dKV bitwise identical across repeated calls.
+"""
+import pytest
+import torch
+
+from cppmega_amd import synthetic
+from cppmega_amd.sparse_mla_ops import (SparseMLA, sparse_mla_as_unfused_dsa, sparse_mla_bwd,
+                                        sparse_mla_fwd_interface)
+from oracle import sparse_mla as orc
+from tests._util import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _fwd(inp, dev, d_v):
+    q, kv, idx = inp["q"].to(dev), inp["kv"].to(dev), inp["indices"].to(dev)
+    return sparse_mla_fwd_interface(q, kv, idx, sm_scale=inp["scale"], d_v=d_v)
+
+
+def _inputs(B, S, H, D, DV, topk, G=1, seed=7, std=0.5, S_kv=None):
+    inp = synthetic.sparse_mla_inputs(B, S, H, D, DV, topk, std=std, seed=seed, S_kv=S_kv)
+    if G > 1:
+        g = torch.Generator().manual_seed(seed + 99)
+        S_kv = inp["kv"].shape[1]
+        inp["kv"] = (torch.randn((B, S_kv, G, D), generator=g) * std).to(torch.bfloat16)
+        idx = [synthetic.causal_indices(B, S, topk, seed=seed + 10 * gg, S_kv=S_kv) for gg in range(G)]
+        inp["indices"] = torch.cat(idx, dim=2).contiguous()
+    return inp
+
+
+def test_fwd_cfg1_matches_oracle(dev):
+    inp = synthetic.sparse_mla_inputs(1, 512, 16, 128, 64, 64, std=0.5, seed=1234, grad=False)
+    inp["scale"] = 1.0 / 128 ** 0.5
+    out, lse = _fwd(inp, dev, 64)
+    ro, rl = orc.sparse_mla_fwd(inp["q"], inp["kv"], inp["indices"], inp["scale"], 64)
+    assert out.dtype == torch.bfloat16 and lse.dtype == torch.float32
+    assert_close(out, ro, what="out")
+    assert_close(lse, rl, what="lse2")
+
+
+@pytest.mark.parametrize("B,S,H,G,D,DV,topk", [
+    (2, 128, 32, 1, 128, 64, 64),
+    (1, 200, 64, 1, 128, 64, 100),
+    (1, 96, 128, 1, 128, 64, 40),
+    (1, 80, 40, 1, 128, 64, 72),
+    (1, 64, 32, 2, 128, 128, 32),
+    (1, 64, 16, 1, 64, 32, 48),
+    (1, 72, 32, 1, 192, 128, 96),
+])
+def test_fwd_shapes(dev, B, S, H, G, D, DV, topk):
+    inp = _inputs(B, S, H, D, DV, topk, G=G)
+    out, lse = _fwd(inp, dev, DV)
+    ro, rl = orc.sparse_mla_fwd(inp["q"], inp["kv"], inp["indices"], inp["scale"], DV)
+    assert_close(out, ro, what="out")
+    assert_close(lse, rl, what="lse2")
+
+
+def test_fwd_edge_indices(dev):
+    B, S, H, D, DV, topk = 1, 64, 32, 128, 64, 64
+    inp = _inputs(B, S, H, D, DV, topk)
+    idx = inp["indices"].clone()
+    idx[0, 5, 0, :] = -1                       # all masked
+    idx[0, 6, 0, :8] = 3                       # duplicates count per occurrence
+    idx[0, 7, 0, 10:20] = -7                   # other negatives are masked
+    idx[0, 8, 0, 0:4] = torch.tensor([S, S + 5, 10 ** 6, -(2 ** 31)], dtype=torch.int32)  # out of range
+    idx[0, 9, 0, :] = -1
+    idx[0, 9, 0, 33] = 2                       # single valid slot, in the second block
+    inp["indices"] = idx
+    out, lse = _fwd(inp, dev, DV)
+    ro, rl = orc.sparse_mla_fwd(inp["q"], inp["kv"], idx, inp["scale"], DV)
+    assert_close(out, ro, what="out")
+    assert_close(lse, rl, what="lse2")
+    assert torch.all(out[0, 5] == 0) and torch.all(torch.isneginf(lse[0, 5]))
+    # single valid slot: out = V[idx] exactly (P = 1), lse2 = scale * q.k * log2(e)
+    v = inp["kv"][0, 2, 0, :DV].float()
+    assert_close(out[0, 9].float().cpu(), v.expand(H, DV), rtol=0, atol=0, what="single-slot out")
+
+
+def _bwd_case(dev, B, S, H, D, DV, topk, G=1, seed=7):
+    inp = _inputs(B, S, H, D, DV, topk, G=G, seed=seed)
+    q, kv, idx, do = (inp[k].to(dev) for k in ("q", "kv", "indices", "do"))
+    out, lse = sparse_mla_fwd_interface(q, kv, idx, sm_scale=inp["scale"], d_v=DV)
+    dq, dkv = sparse_mla_bwd(q, kv, out, do, idx, lse, sm_scale=inp["scale"])
+    rdq, rdkv = orc.sparse_mla_bwd(inp["q"], inp["kv"], out.cpu(), inp["do"], inp["indices"], lse.cpu(),
+                                   inp["scale"], DV)
+    return inp, (q, kv, idx, do, out, lse), (dq, dkv), (rdq, rdkv)
+
+
+@pytest.mark.parametrize("B,S,H,G,D,DV,topk", [
+    (1, 128, 32, 1, 128, 64, 64),
+    (2, 96, 64, 1, 128, 64, 80),
+    (1, 64, 16, 1, 128, 64, 40),
+    (1, 64, 32, 2, 128, 128, 32),
+    (1, 64, 16, 1, 64, 32, 48),
+    (1, 72, 32, 1, 192, 128, 96),
+])
+def test_bwd_matches_oracle(dev, B, S, H, G, D, DV, topk):
+    _, _, (dq, dkv), (rdq, rdkv) = _bwd_case(dev, B, S, H, D, DV, topk, G=G)
+    assert dq.dtype == torch.bfloat16 and dkv.dtype == torch.bfloat16
+    assert_close(dq, rdq, what="dq")
+    assert_close(dkv, rdkv, what="dkv")
+
+
+def test_bwd_bitwise_deterministic(dev):
+    _, (q, kv, idx, do, out, lse), (dq, dkv), _ = _bwd_case(dev, 1, 256, 32, 128, 64, 64)
+    for _ in range(2):
+        dq2, dkv2 = sparse_mla_bwd(q, kv, out, do, idx, lse)
+        assert torch.equal(dq, dq2) and torch.equal(dkv, dkv2)
+
+
+def test_bwd_edge_indices(dev):
+    B, S, H, D, DV, topk = 1, 64, 32, 128, 64, 64
+    inp = _inputs(B, S, H, D, DV, topk)
+    idx = inp["indices"].clone()
+    idx[0, 5, 0, :] = -1
+    idx[0, 6, 0, :8] = 3
+    idx[0, 8, 0, 0:4] = torch.tensor([S, S + 5, 10 ** 6, -3], dtype=torch.int32)
+    q, kv, idxd, do = inp["q"].to(dev), inp["kv"].to(dev), idx.to(dev), inp["do"].to(dev)
+    out, lse = sparse_mla_fwd_interface(q, kv, idxd, sm_scale=inp["scale"], d_v=DV)
+    dq, dkv = sparse_mla_bwd(q, kv, out, do, idxd, lse, sm_scale=inp["scale"])
+    rdq, rdkv = orc.sparse_mla_bwd(inp["q"], inp["kv"], out.cpu(), inp["do"], idx, lse.cpu(), inp["scale"], DV)
+    assert_close(dq, rdq, what="dq")
+    assert_close(dkv, rdkv, what="dkv")
+    assert torch.all(dq[0, 5] == 0)
+
+
+def test_autograd_and_adapter(dev):
+    B, S, H, D, DV, topk = 2, 64, 16, 128, 64, 32
+    inp = _inputs(B, S, H, D, DV, topk)
+    q = inp["q"].to(dev).requires_grad_()
+    kv = inp["kv"].to(dev).requires_grad_()
+    out, lse = SparseMLA.apply(q, kv, inp["indices"].to(dev), inp["scale"], DV)
+    out.backward(inp["do"].to(dev))
+    ro, rl = orc.sparse_mla_fwd(inp["q"], inp["kv"], inp["indices"], inp["scale"], DV)
+    rdq, rdkv = orc.sparse_mla_bwd(inp["q"], inp["kv"], out.detach().cpu(), inp["do"], inp["indices"],
+                                   lse.detach().cpu(), inp["scale"], DV)
+    assert_close(out, ro, what="out")
+    assert_close(q.grad, rdq, what="dq")
+    assert_close(kv.grad, rdkv, what="dkv")
+    # Megatron unfused_dsa_fn layout: query [sq,b,np,hn], key [sk,b,np,hn], topk [b,sq,topk] int64
+    query = inp["q"].permute(1, 0, 2, 3).contiguous()
+    key = inp["kv"].permute(1, 0, 2, 3).expand(S, B, H, D).contiguous()
+    value = key[..., :DV].contiguous()
+    topk_idx = inp["indices"][:, :, 0, :].to(torch.int64)
+    res = sparse_mla_as_unfused_dsa(query.to(dev), key.to(dev), value.to(dev), topk_idx.to(dev), inp["scale"])
+    assert res.shape == (S, B, H * DV)
+    assert_close(res, ro.permute(1, 0, 2, 3).reshape(S, B, H * DV), what="unfused adapter")
+
+
+def test_three_dim_inputs(dev):
+    inp = _inputs(1, 64, 32, 128, 64, 32)
+    q, kv, idx = inp["q"][0].to(dev), inp["kv"][0].to(dev), inp["indices"][0].to(dev)
+    out, lse = sparse_mla_fwd_interface(q, kv, idx, sm_scale=inp["scale"], d_v=64)
+    assert out.shape == (64, 32, 64) and lse.shape == (64, 32)
+    ro, rl = orc.sparse_mla_fwd(inp["q"], inp["kv"], inp["indices"], inp["scale"], 64)
+    assert_close(out, ro[0], what="out")
+
+
+def test_cfg2_full_scale(dev):
+    """cfg2 at full size: sampled tokens vs the oracle, sampled kv rows of dKV vs
+    the oracle restricted to the tokens that reference them, determinism."""
+    B, S, H, D, DV, topk = 2, 4096, 32, 128, 64, 256
+    inp = synthetic.sparse_mla_inputs(B, S, H, D, DV, topk, std=0.5, seed=1234)
+    q, kv, idx, do = (inp[k].to(dev) for k in ("q", "kv", "indices", "do"))
+    out, lse = sparse_mla_fwd_interface(q, kv, idx, sm_scale=inp["scale"], d_v=DV)
+    dq, dkv = sparse_mla_bwd(q, kv, out, do, idx, lse, sm_scale=inp["scale"])
+    dq2, dkv2 = sparse_mla_bwd(q, kv, out, do, idx, lse, sm_scale=inp["scale"])
+    assert torch.equal(dkv, dkv2) and torch.equal(dq, dq2)
+    outc, lsec = out.cpu(), lse.cpu()
+    b = 1
+    toks = torch.tensor([0, 1, 255, 256, 1000, 2047, 3000, 4095])
+    sub = lambda x: x[b:b + 1, toks].contiguous()
+    ro, rl = orc.sparse_mla_fwd(sub(inp["q"]), inp["kv"][b:b + 1], sub(inp["indices"]), inp["scale"], DV)
+    assert_close(outc[b:b + 1, toks], ro, what="out (sampled)")
+    assert_close(lsec[b:b + 1, toks], rl, what="lse2 (sampled)")
+    rdq, _ = orc.sparse_mla_bwd(sub(inp["q"]), inp["kv"][b:b + 1], sub(outc), sub(inp["do"]),
+                                sub(inp["indices"]), sub(lsec), inp["scale"], DV)
+    assert_close(dq.cpu()[b:b + 1, toks], rdq, what="dq (sampled)")
+    rows = torch.tensor([0, 7, 100, 2048, 4000])
+    ref_tok = (inp["indices"][b, :, 0, :, None] == rows[None, None, :]).any(-1).any(-1).nonzero()[:, 0]
+    _, rdkv = orc.sparse_mla_bwd(inp["q"][b:b + 1, ref_tok].contiguous(), inp["kv"][b:b + 1],
+                                 outc[b:b + 1, ref_tok].contiguous(), inp["do"][b:b + 1, ref_tok].contiguous(),
+                                 inp["indices"][b:b + 1, ref_tok].contiguous(), lsec[b:b + 1, ref_tok].contiguous(),
+                                 inp["scale"], DV)
+    assert_close(dkv.cpu()[b, rows], rdkv[0, rows], what="dkv (sampled rows)")
