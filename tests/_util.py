@@ -23,5 +23,22 @@ def assert_close(actual, expected, rtol=RTOL, atol=ATOL, what=""):
             f"actual {float(a.flatten()[i]):.6g} expected {float(e.flatten()[i]):.6g}")
 
 
+def assert_mostly_close(actual, expected, rtol=RTOL, atol=ATOL, max_bad_frac=1e-2, max_rel_l2=5e-3, what=""):
+    """Looser bar for gradients on outlier-heavy FP8 data: with 20-sigma entries the
+    softmax is near one-hot, dP - Delta cancels, and a bf16 rounding flip of one dS
+    element is multiplied by |K| or |Q| values of ~20 sigma, so up to 1% of the
+    elements may leave the elementwise band; the relative L2 error must stay
+    below 5e-3."""
+    a = actual.detach().float().cpu()
+    e = expected.detach().float().cpu()
+    assert a.shape == e.shape, f"{what}: shape {tuple(a.shape)} != {tuple(e.shape)}"
+    diff = (a - e).abs()
+    bad = diff > atol + rtol * e.abs()
+    frac = float(bad.float().mean())
+    rel = float((a - e).norm() / e.norm().clamp_min(1e-30))
+    assert frac <= max_bad_frac and rel <= max_rel_l2, \
+        f"{what}: {int(bad.sum())}/{bad.numel()} outside band (frac {frac:.2e}), rel L2 {rel:.3e}"
+
+
 def to_dev(d, dev):
     return {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in d.items()}
