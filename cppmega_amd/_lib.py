@@ -24,6 +24,8 @@ DTYPE_BF16 = 0
 DTYPE_E4M3 = 1
 DTYPE_F32 = 2
 
+BWD_FP32_PARTIALS = 1
+
 # Every symbol include/dsa_hip.h declares (checked by the CPU test suite).
 EXPORTED_SYMBOLS = (
     "dsa_last_error",
@@ -51,11 +53,11 @@ _SIGNATURES = {
     "dsa_sparse_mla_fwd": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                   _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                   _f32, _i32, _c_void_p, _c_void_p, _c_void_p]),
-    "dsa_sparse_mla_bwd_workspace_size": (_size_t, [_i64] * 8),
+    "dsa_sparse_mla_bwd_workspace_size": (_size_t, [_i64] * 8 + [_i32]),
     "dsa_sparse_mla_bwd": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                   _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _size_t,
                                   _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-                                  _f32, _i32, _c_void_p, _c_void_p, _c_void_p]),
+                                  _f32, _i32, _c_void_p, _c_void_p, _i32, _c_void_p]),
     "dsa_indexer_scores": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                   _i64, _i64, _i64, _i64, _i64, _i32, _i32,
                                   _c_void_p, _c_void_p, _i32, _i32, _c_void_p]),

@@ -33,10 +33,43 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   u += 0x7fffu + ((u >> 16) & 1u);
   return u >> 16;
 }
-// Pack two floats into one dword of bf16 (lo in the low half).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+// Pack two floats into one dword of bf16 (lo in the low half), round to
+// nearest even (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
+// Same for fp16 (v_cvt_pk_f16_f32, round to nearest even).
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  const f16x2_t v = {(_Float16)lo, (_Float16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// ---------------------------------------------------------------------------
+// Power-of-two scaled fp16 rows (dKV partial rows of the backward)
+// ---------------------------------------------------------------------------
+// Scale exponent s for a row whose max magnitude is amax: amax * 2^s lies in
+// [2^13, 2^14), so the whole row fits fp16 with 11 significant bits relative
+// to its max.  Zero, inf or NaN rows use s = 0.  |s| <= 127 fits an int8.
+__device__ __forceinline__ int partial_row_exponent(float amax) {
+  if (!(amax > 0.0f) || !(amax <= 3.402823466e38f)) return 0;
+  int ex;
+  (void)frexpf(amax, &ex);  // amax = m * 2^ex, m in [0.5, 1)
+  int s = 14 - ex;
+  s = s > 127 ? 127 : (s < -114 ? -114 : s);
+  return s;
+}
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  const _Float16 h = (_Float16)f;  // round to nearest even
+  return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+// 2^s as a float for |s| <= 127 (exact).
+__device__ __forceinline__ float exp2i(int s) { return ldexpf(1.0f, s); }
 
 // ---------------------------------------------------------------------------
 // OCP e4m3fn (bias 7, 3 mantissa bits, 0x7f / 0xff = NaN, max 448)
@@ -92,6 +125,38 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(i32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// ---------------------------------------------------------------------------
+// Transposed LDS reads (ds_read_b64_tr_b16, gfx950)
+// ---------------------------------------------------------------------------
+// Within each group of 16 lanes, lane k supplies the address of 4 consecutive
+// 16-bit elements M[k][0..3]; lane i receives {M[i/4][i%4], M[4 + i/4][i%4],
+// M[8 + i/4][i%4], M[12 + i/4][i%4]}.  With lane k = 4j + q pointing at
+// T[row_j][col0 + 4q], lane i therefore receives column col0 + i of rows
+// row_0..row_3: a 4x16 block of a row-major tile, transposed.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+__device__ __forceinline__ i32x2 ds_read_tr16(const unsigned char *p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(const_cast<unsigned char *>(p)));
+  return __builtin_bit_cast(i32x2, v);
+}
+
+// 32x32x16 MFMA operand whose M/N index (lane & 31) is column col0 + (lane & 31)
+// of the row-major bf16 tile T (row stride `stride` bytes) and whose eight
+// K elements e = 4h + j (h = 0, 1; j = 0..3) are rows
+//   row(e) = rows_base + h * h_step + (lane >> 5) * g_step + j.
+// (h_step, g_step) = (4, 8) gives rows rows_base + 8 * (lane >> 5) + e; (8, 4)
+// gives the accumulator order rows_base + 8h + 4 * (lane >> 5) + j.
+__device__ __forceinline__ i32x4 tr_operand(const unsigned char *T, int stride, int col0, int rows_base,
+                                            int h_step, int g_step) {
+  const int lane = lane_id();
+  const int k = lane & 15, j = k >> 2, q = k & 3, cb = (lane >> 4) & 1, gg = lane >> 5;
+  const unsigned char *base = T + (col0 + cb * 16 + 4 * q) * 2 + (rows_base + gg * g_step + j) * stride;
+  const i32x2 r0 = ds_read_tr16(base);
+  const i32x2 r1 = ds_read_tr16(base + h_step * stride);
+  return i32x4{r0[0], r0[1], r1[0], r1[1]};
+}
 
 __device__ __forceinline__ i32x4 ld_global_16(const void *p) {
   return *reinterpret_cast<const i32x4 *>(p);

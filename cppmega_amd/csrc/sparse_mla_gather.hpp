@@ -1,0 +1,141 @@
+// Row gather shared by the SparseMLA forward and backward kernels.
+//
+// A wave gathers the 32 kv rows selected by one block of 32 top-k slots.  The
+// work is split into units of (4 consecutive slots x one 16-byte chunk); lane
+// u handles chunk u % NCH of slots 4*(u / NCH) .. +3, so 16 consecutive lanes
+// read one 256-byte row contiguously.  gather_issue() only issues the loads
+// (masked slots read row 0 and are zeroed at store time, so the loads carry no
+// branches); the stores to LDS happen later, so a block's loads overlap the
+// previous block's compute.  Every tile is stored row-major: MFMA operands
+// that need a transposed view read it with ds_read_b64_tr_b16 (tr_operand).
+#pragma once
+
+#include <type_traits>
+
+#include "dsa_common.hpp"
+
+namespace dsa {
+
+template <int D_QK, int D_V, bool FP8>
+struct GatherCfg {
+  static constexpr int kDqk = D_QK;
+  static constexpr int kDv = D_V;
+  static constexpr bool kFp8 = FP8;
+  static constexpr int ELT = FP8 ? 1 : 2;          // bytes per element in HBM
+  static constexpr int ROWB = D_QK * ELT;          // bytes per kv row
+  static constexpr int CH = 16 / ELT;              // elements per 16-byte chunk
+  static constexpr int NCH = D_QK / CH;            // chunks per row
+  static constexpr int NCH_V = D_V / CH;           // chunks of the V prefix
+  static constexpr int UNITS = 8 * NCH;            // (4 rows x 1 chunk) units per block
+  static constexpr int UPL = (UNITS + 63) / 64;    // units per lane
+  static constexpr int KL_STRIDE = ROWB + 16;      // LDS row stride of the raw tile
+  static_assert(NCH * CH == D_QK && NCH_V * CH == D_V, "head dims must be whole 16-byte chunks");
+  struct Regs {
+    i32x4 v[UPL][4];
+    float sc[UPL][4];
+    uint32_t valid;  // bit 4*uu + r: row r of unit uu is a real (unmasked) slot
+  };
+};
+
+// Index of slot blk*32 + l32 of this row, or -1 when masked / past topk.
+__device__ __forceinline__ int load_slot_index(const int32_t *idx_row, int blk, int l32, int64_t topk,
+                                               int64_t s_kv) {
+  const int64_t sl = (int64_t)blk * 32 + l32;
+  if (sl >= topk) return -1;
+  const int v = idx_row[sl];
+  return (v >= 0 && v < s_kv) ? v : -1;
+}
+
+// kv_b points at row 0 of this (batch, kv group); row_pitch = G * ROWB bytes.
+template <class Gat>
+__device__ __forceinline__ void gather_issue(typename Gat::Regs &rg, const unsigned char *kv_b,
+                                             const float *kv_scale_b, int my_idx, uint32_t row_pitch) {
+  const int lane = lane_id();
+  uint32_t valid = 0;
+#pragma unroll
+  for (int uu = 0; uu < Gat::UPL; ++uu) {
+    const int u = lane + 64 * uu;
+    const int c = u % Gat::NCH;
+    const int quad = (u / Gat::NCH) & 7;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ri = __shfl(my_idx, quad * 4 + r, 64);
+      const bool ok = ri >= 0 && u < Gat::UNITS;
+      const uint32_t row = ok ? (uint32_t)ri : 0u;
+      rg.v[uu][r] = ld_global_16(kv_b + row * row_pitch + c * 16);
+      if constexpr (Gat::kFp8) rg.sc[uu][r] = kv_scale_b[row];
+      valid |= (ok ? 1u : 0u) << (4 * uu + r);
+    }
+  }
+  rg.valid = valid;
+}
+
+// K rows, row-major (raw bf16 / e4m3 bytes): Kl[slot][chunk]; masked slots zero.
+template <class Gat>
+__device__ __forceinline__ void gather_store_k(const typename Gat::Regs &rg, unsigned char *Kl) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int uu = 0; uu < Gat::UPL; ++uu) {
+    const int u = lane + 64 * uu;
+    if (u >= Gat::UNITS) break;
+    const int c = u % Gat::NCH, quad = u / Gat::NCH;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bool ok = (rg.valid >> (4 * uu + r)) & 1u;
+      const i32x4 z = {0, 0, 0, 0};
+      *reinterpret_cast<i32x4 *>(Kl + (quad * 4 + r) * Gat::KL_STRIDE + c * 16) = ok ? rg.v[uu][r] : z;
+    }
+  }
+}
+
+// e4m3 only: rows dequantised to bf16 (value * kv_scale, RNE), row-major,
+// for the chunks c < NCH_D (the V prefix or the whole row).
+template <class Gat, int NCH_D>
+__device__ __forceinline__ void gather_store_dequant(const typename Gat::Regs &rg, unsigned char *Kd, int stride) {
+  static_assert(Gat::kFp8, "dequantised rows exist for e4m3 input only");
+  const int lane = lane_id();
+#pragma unroll
+  for (int uu = 0; uu < Gat::UPL; ++uu) {
+    const int u = lane + 64 * uu;
+    if (u >= Gat::UNITS) break;
+    const int c = u % Gat::NCH, quad = u / Gat::NCH;
+    if (c < NCH_D) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool ok = (rg.valid >> (4 * uu + r)) & 1u;
+        const float s = ok ? rg.sc[uu][r] : 0.0f;
+        uint32_t w[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t word = (uint32_t)rg.v[uu][r][e >> 1];
+          const uint32_t sh = 16 * (e & 1);
+          w[e] = pack_bf16x2(e4m3_to_f32((word >> sh) & 0xffu) * s, e4m3_to_f32((word >> (sh + 8)) & 0xffu) * s);
+        }
+        unsigned char *dst = Kd + (quad * 4 + r) * stride + c * 32;
+        *reinterpret_cast<i32x4 *>(dst) = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+        *reinterpret_cast<i32x4 *>(dst + 16) = i32x4{(int)w[4], (int)w[5], (int)w[6], (int)w[7]};
+      }
+    }
+  }
+}
+
+// e4m3 only: per-slot kv dequant scale (0 for masked slots).
+template <class Gat>
+__device__ __forceinline__ void gather_store_scale(const typename Gat::Regs &rg, float *Ksc) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int uu = 0; uu < Gat::UPL; ++uu) {
+    const int u = lane + 64 * uu;
+    if (u >= Gat::UNITS) break;
+    const int c = u % Gat::NCH, quad = u / Gat::NCH;
+    if (c == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool ok = (rg.valid >> (4 * uu + r)) & 1u;
+        Ksc[quad * 4 + r] = ok ? rg.sc[uu][r] : 0.0f;
+      }
+    }
+  }
+}
+
+}  // namespace dsa

@@ -10,19 +10,32 @@ carried by the indices, and there is no JIT kernel object to return.
 """
 from __future__ import annotations
 
+import os
+
 import torch
 
 from .. import _lib
 from ._common import check_same_device, normalize_sm_scale, stream_of, unwrap_quantized
 
 
-def _launch_bwd(q, kv, o, do, indices, lse, delta, sm_scale, dtype_code, q_scale=None, kv_scale=None):
+def fp32_partials_default() -> bool:
+    """CPPMEGA_AMD_BWD_FP32_PARTIALS=1 keeps the per-(token, slot) dKV rows in fp32
+    (exact fp32 accumulation, 2x the workspace traffic); the default rounds
+    each row to bf16 before the deterministic fp32 reduction."""
+    return os.getenv("CPPMEGA_AMD_BWD_FP32_PARTIALS", "0").strip().lower() in {"1", "true", "yes", "on"}
+
+
+def _launch_bwd(q, kv, o, do, indices, lse, delta, sm_scale, dtype_code, q_scale=None, kv_scale=None,
+                fp32_partials=None):
     B, S, H, D = q.shape
     _, S_kv, G, _ = kv.shape
     d_v = o.shape[-1]
     topk = indices.shape[-1]
+    if fp32_partials is None:
+        fp32_partials = fp32_partials_default()
+    flags = _lib.BWD_FP32_PARTIALS if fp32_partials else 0
     L = _lib.load()
-    ws_bytes = int(L.dsa_sparse_mla_bwd_workspace_size(B, S, S_kv, H, G, D, d_v, topk))
+    ws_bytes = int(L.dsa_sparse_mla_bwd_workspace_size(B, S, S_kv, H, G, D, d_v, topk, flags))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     dq = torch.empty((B, S, H, D), dtype=torch.bfloat16, device=q.device)
     dkv = torch.empty((B, S_kv, G, D), dtype=torch.bfloat16, device=q.device)
@@ -31,7 +44,7 @@ def _launch_bwd(q, kv, o, do, indices, lse, delta, sm_scale, dtype_code, q_scale
         q.data_ptr(), kv.data_ptr(), o.data_ptr(), do.data_ptr(), indices.data_ptr(),
         lse.data_ptr(), _lib.ptr(delta), dq.data_ptr(), dkv.data_ptr(), ws.data_ptr(), ws_bytes,
         B, S, S_kv, H, G, D, d_v, topk, float(sm_scale), dtype_code,
-        _lib.ptr(q_scale), _lib.ptr(kv_scale), stream)
+        _lib.ptr(q_scale), _lib.ptr(kv_scale), flags, stream)
     _lib.check(rc, "dsa_sparse_mla_bwd")
     return dq, dkv
 
@@ -46,12 +59,13 @@ def _prep_delta(delta, B, S, H):
 
 
 def sparse_mla_bwd(q, kv, o, do, indices, lse, sm_scale=None, d_v=None, is_casual=True,
-                   return_kernel=False, delta=None):
+                   return_kernel=False, delta=None, *, fp32_partials=None):
     """Run the sparse-MLA backward and return (dq, dkv), both bf16.
 
     Accepts 3-D [seq, heads, dim] or 4-D [batch, seq, heads, dim] tensors;
     ``lse`` is the forward's log2-unit LSE.  grad of lse is not an input (the
-    reference ignores it too).
+    reference ignores it too).  ``fp32_partials`` (keyword only; default from
+    CPPMEGA_AMD_BWD_FP32_PARTIALS) keeps the dKV contribution rows in fp32.
     """
     q = unwrap_quantized(q)
     kv = unwrap_quantized(kv)
@@ -87,7 +101,8 @@ def sparse_mla_bwd(q, kv, o, do, indices, lse, sm_scale=None, d_v=None, is_casua
     delta = _prep_delta(delta, B, S, H)
 
     scale = normalize_sm_scale(sm_scale, dim_plus_tail_dim)
-    dq, dkv = _launch_bwd(q, kv, o, do, indices, lse, delta, scale, _lib.DTYPE_BF16)
+    dq, dkv = _launch_bwd(q, kv, o, do, indices, lse, delta, scale, _lib.DTYPE_BF16,
+                          fp32_partials=fp32_partials)
     if squeeze_batch:
         dq, dkv = dq.squeeze(0), dkv.squeeze(0)
     return dq, dkv

@@ -73,10 +73,17 @@ int dsa_sparse_mla_fwd(const void *q, const void *kv, const int32_t *indices,
                        const float *q_scale, const float *kv_scale,
                        void *stream);
 
-/* Bytes of workspace dsa_sparse_mla_bwd needs for these dimensions. */
+/* dsa_sparse_mla_bwd flags */
+enum dsa_bwd_flags {
+  /* Keep the per-(token, slot) dKV rows in fp32 instead of bf16 before the
+   * deterministic fp32 reduction (2x the workspace traffic, fp32-exact rows). */
+  DSA_BWD_FP32_PARTIALS = 1
+};
+
+/* Bytes of workspace dsa_sparse_mla_bwd needs for these dimensions and flags. */
 size_t dsa_sparse_mla_bwd_workspace_size(int64_t B, int64_t S, int64_t S_kv,
                                          int64_t H, int64_t G, int64_t D_qk,
-                                         int64_t D_v, int64_t topk);
+                                         int64_t D_v, int64_t topk, int flags);
 
 /*
  * SparseMLA backward.
@@ -91,9 +98,11 @@ size_t dsa_sparse_mla_bwd_workspace_size(int64_t B, int64_t S, int64_t S_kv,
  *   delta [B, S, H] f32 = sum_d o * dO, or NULL to compute it from o and dO
  *   dq  [B, S, H, D_qk] bf16 (written), dkv [B, S_kv, G, D_qk] bf16 (written)
  * dKV is reduced deterministically: every kv row sums its per-(token, slot)
- * contributions in ascending (token, slot) order in fp32, so repeated calls
- * are bitwise identical.  Gradients are with respect to the dequantised
- * values for e4m3 inputs.
+ * contribution rows (fp16 with a per-row power-of-two scale, i.e. 11
+ * significant bits relative to the row max; fp32 with DSA_BWD_FP32_PARTIALS) in
+ * ascending (token, kv group, slot) order in fp32, so repeated calls are
+ * bitwise identical.  Gradients are with respect to the dequantised values
+ * for e4m3 inputs.  Limits: S_kv * G <= 32768, B * S * G * topk < 2^31.
  */
 int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o,
                        const void *dO, const int32_t *indices,
@@ -103,7 +112,7 @@ int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o,
                        int64_t S_kv, int64_t H, int64_t G, int64_t D_qk,
                        int64_t D_v, int64_t topk, float sm_scale, int dtype,
                        const float *q_scale, const float *kv_scale,
-                       void *stream);
+                       int flags, void *stream);
 
 /*
  * DSA indexer scores: score[b, t, s] = sum_h w[t, b, h] * act(q[t, b, h, :] . k[s, b, :])

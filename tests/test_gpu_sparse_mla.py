@@ -128,6 +128,38 @@ def test_bwd_edge_indices(dev):
     assert torch.all(dq[0, 5] == 0)
 
 
+def test_bwd_unsorted_and_duplicate_indices(dev):
+    """Unsorted slot order and repeated rows inside a token take the serial CSR path."""
+    B, S, H, D, DV, topk = 2, 96, 32, 128, 64, 64
+    inp = _inputs(B, S, H, D, DV, topk, seed=3)
+    g = torch.Generator().manual_seed(3)
+    perm = torch.argsort(torch.rand(B, S, 1, topk, generator=g), dim=-1)
+    idx = torch.gather(inp["indices"], -1, perm)
+    idx[0, 50, 0, 10:20] = idx[0, 50, 0, 0]
+    idx[1, 70, 0, :] = 5
+    q, kv, idxd, do = inp["q"].to(dev), inp["kv"].to(dev), idx.contiguous().to(dev), inp["do"].to(dev)
+    out, lse = sparse_mla_fwd_interface(q, kv, idxd, sm_scale=inp["scale"], d_v=DV)
+    dq, dkv = sparse_mla_bwd(q, kv, out, do, idxd, lse, sm_scale=inp["scale"])
+    rdq, rdkv = orc.sparse_mla_bwd(inp["q"], inp["kv"], out.cpu(), inp["do"], idx, lse.cpu(), inp["scale"], DV)
+    assert_close(dq, rdq, what="dq")
+    assert_close(dkv, rdkv, what="dkv")
+    dq2, dkv2 = sparse_mla_bwd(q, kv, out, do, idxd, lse, sm_scale=inp["scale"])
+    assert torch.equal(dkv, dkv2) and torch.equal(dq, dq2)
+
+
+def test_bwd_fp32_partials(dev):
+    """fp32 dKV rows: same parity bar, deterministic, and at least as close to the oracle."""
+    _, (q, kv, idx, do, out, lse), (dq, dkv), (rdq, rdkv) = _bwd_case(dev, 1, 256, 32, 128, 64, 128)
+    dq32, dkv32 = sparse_mla_bwd(q, kv, out, do, idx, lse, fp32_partials=True)
+    assert_close(dkv32, rdkv, what="dkv fp32 partials")
+    assert torch.equal(dq32, dq)
+    dq32b, dkv32b = sparse_mla_bwd(q, kv, out, do, idx, lse, fp32_partials=True)
+    assert torch.equal(dkv32, dkv32b)
+    err16 = float((dkv.float().cpu() - rdkv).abs().mean())
+    err32 = float((dkv32.float().cpu() - rdkv).abs().mean())
+    assert err32 <= err16 * 1.05 + 1e-6, (err32, err16)
+
+
 def test_autograd_and_adapter(dev):
     B, S, H, D, DV, topk = 2, 64, 16, 128, 64, 32
     inp = _inputs(B, S, H, D, DV, topk)
