@@ -375,8 +375,8 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct BwdWorkspace {
-  size_t partials, pexp, hist, tot, rowptr, refs, total;
-  int CT, NC;
+  size_t partials, pexp, hist, gsum, tot, rowptr, refs, total;
+  int CT, NC, NQ;
 };
 
 static BwdWorkspace bwd_layout(int64_t B, int64_t S, int64_t S_kv, int64_t H, int64_t G, int64_t D_qk,
@@ -386,9 +386,7 @@ static BwdWorkspace bwd_layout(int64_t B, int64_t S, int64_t S_kv, int64_t H, in
   const size_t entries = (size_t)B * S * G * topk;
   const int64_t R = S_kv * G;
   BwdWorkspace L;
-  L.CT = 64;  // tokens per CSR chunk
-  while ((int64_t)((S + L.CT - 1) / L.CT) * R > (1ll << 24) && L.CT < 4096) L.CT *= 2;
-  L.NC = (int)((S + L.CT - 1) / L.CT);
+  csr_plan(S, R, &L.CT, &L.NC, &L.NQ);
   const size_t psz = (flags & DSA_BWD_FP32_PARTIALS) ? 4 : 2;
   size_t off = 0;
   L.partials = off;
@@ -397,6 +395,8 @@ static BwdWorkspace bwd_layout(int64_t B, int64_t S, int64_t S_kv, int64_t H, in
   off += align256(entries * ntiles);
   L.hist = off;
   off += align256((size_t)B * L.NC * R * 4);
+  L.gsum = off;
+  off += align256((size_t)B * L.NQ * R * 4);
   L.tot = off;
   off += align256((size_t)B * R * 4);
   L.rowptr = off;
@@ -511,8 +511,10 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
   cp.G = G;
   cp.topk = topk;
   cp.R = R;
+  cp.gsum = reinterpret_cast<int32_t *>(ws + L.gsum);
   cp.CT = L.CT;
   cp.NC = L.NC;
+  cp.NQ = L.NQ;
   int rc = launch_csr(cp, B, st);
   if (rc) return rc;
 

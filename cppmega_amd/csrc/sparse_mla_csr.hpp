@@ -11,17 +11,28 @@ namespace dsa {
 // ---------------------------------------------------------------------------
 // Entry e = ((b*S + t)*G + g)*topk + slot; its row (within batch b) is
 // r = j*G + g for a valid index j.  Tokens are grouped into chunks of CT
-// within one batch; hist[b][chunk][r] counts a chunk's entries per row.
+// within one batch (NC chunks per batch); chunks form groups of CG = 16.
+//   csr_hist     hist[b][c][r]  = entries of chunk c in row r
+//   csr_gsum     gsum[b][q][r]  = sum of hist over the chunks of group q
+//   csr_rows     tot[b*R + r]   = row total; gsum -> exclusive prefix over groups
+//   csr_scan     rowptr         = exclusive prefix of tot
+//   csr_bases    hist[b][c][r] <- rowptr + entries of row r in earlier chunks
+//   csr_scatter  refs[...]      = entries placed token by token (stable)
+// Every thread touches at most CG chunks, so no kernel walks a long serial
+// chain of global loads.
+
+constexpr int kChunkGroup = 16;
 
 struct CsrParams {
   const int32_t *idx;
   int32_t *hist;    // [B][NC][R]
+  int32_t *gsum;    // [B][NQ][R]
   int32_t *tot;     // [B*R]
   int32_t *rowptr;  // [B*R + 1]
   int32_t *refs;    // [entries]
   int64_t S, S_kv, G, topk;
   int64_t R;        // rows per batch = S_kv * G
-  int CT, NC;       // tokens per chunk, chunks per batch
+  int CT, NC, NQ;   // tokens per chunk, chunks per batch, chunk groups per batch
 };
 
 __global__ void fill_i32_kernel(int32_t *p, int64_t n, int32_t v) {
@@ -52,15 +63,35 @@ __global__ void __launch_bounds__(256) csr_hist_kernel(const CsrParams p) {
   for (int64_t r = threadIdx.x; r < p.R; r += 256) h[r] = cnt[r];
 }
 
-// one thread per (b, r): total over chunks
-__global__ void csr_rowsum_kernel(const CsrParams p, int64_t B) {
+// one thread per (b, q, r): sum of hist over the chunks of group q
+__global__ void csr_gsum_kernel(const CsrParams p, int64_t B) {
+  const int64_t x = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (x >= B * p.NQ * p.R) return;
+  const int64_t r = x % p.R, bq = x / p.R, q = bq % p.NQ, b = bq / p.NQ;
+  const int c0 = (int)q * kChunkGroup;
+  const int32_t *h = p.hist + (b * p.NC + c0) * p.R + r;
+  int32_t v[kChunkGroup];
+#pragma unroll
+  for (int k = 0; k < kChunkGroup; ++k) v[k] = (c0 + k < p.NC) ? h[(int64_t)k * p.R] : 0;
+  int32_t s = 0;
+#pragma unroll
+  for (int k = 0; k < kChunkGroup; ++k) s += v[k];
+  p.gsum[x] = s;
+}
+
+// one thread per (b, r): row total, and gsum -> exclusive prefix over groups
+__global__ void csr_rows_kernel(const CsrParams p, int64_t B) {
   const int64_t x = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (x >= B * p.R) return;
   const int64_t b = x / p.R, r = x % p.R;
-  const int32_t *h = p.hist + b * p.NC * p.R + r;
-  int32_t s = 0;
-  for (int c = 0; c < p.NC; ++c) s += h[(int64_t)c * p.R];
-  p.tot[x] = s;
+  int32_t *gs = p.gsum + b * p.NQ * p.R + r;
+  int32_t run = 0;
+  for (int q = 0; q < p.NQ; ++q) {
+    const int32_t t = gs[(int64_t)q * p.R];
+    gs[(int64_t)q * p.R] = run;
+    run += t;
+  }
+  p.tot[x] = run;
 }
 
 // Exclusive scan of cnt[0..n) into rowptr[0..n] with one 1024-thread workgroup.
@@ -98,27 +129,34 @@ __global__ void __launch_bounds__(1024) csr_scan_kernel(const int32_t *cnt, int3
   if (tid == 1023) rowptr[n] = wsum[15];
 }
 
-// one thread per (b, r): hist[b][c][r] <- absolute start of chunk c's entries of row r
+// one thread per (b, q, r): hist[b][c][r] <- absolute start of chunk c's entries of row r
 __global__ void csr_bases_kernel(const CsrParams p, int64_t B) {
   const int64_t x = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (x >= B * p.R) return;
-  const int64_t b = x / p.R, r = x % p.R;
-  int32_t *h = p.hist + b * p.NC * p.R + r;
-  int32_t run = p.rowptr[x];
-  for (int c = 0; c < p.NC; ++c) {
-    const int32_t t = h[(int64_t)c * p.R];
-    h[(int64_t)c * p.R] = run;
-    run += t;
+  if (x >= B * p.NQ * p.R) return;
+  const int64_t r = x % p.R, bq = x / p.R, q = bq % p.NQ, b = bq / p.NQ;
+  const int c0 = (int)q * kChunkGroup;
+  int32_t *h = p.hist + (b * p.NC + c0) * p.R + r;
+  int32_t v[kChunkGroup];
+#pragma unroll
+  for (int k = 0; k < kChunkGroup; ++k) v[k] = (c0 + k < p.NC) ? h[(int64_t)k * p.R] : 0;
+  int32_t run = p.rowptr[b * p.R + r] + p.gsum[x];
+#pragma unroll
+  for (int k = 0; k < kChunkGroup; ++k) {
+    if (c0 + k < p.NC) h[(int64_t)k * p.R] = run;
+    run += v[k];
   }
 }
 
-// grid (NC, B), 256 threads, dynamic LDS = R ints.  Tokens of the chunk are
-// placed one after another; within a token the slots take LDS cursors
-// concurrently, which is order-independent as long as no row repeats inside
-// the token.  A token whose valid indices are not strictly increasing (so a
-// row could repeat) is placed by one thread in slot order instead.
+// grid (NC, B), 256 threads, dynamic LDS = R ints + 2 * topk ints.  Tokens of
+// the chunk are placed one after another (their indices are staged in LDS one
+// token ahead); within a token the slots take LDS cursors concurrently, which
+// is order-independent as long as no row repeats inside the token.  A token
+// whose valid indices are not strictly increasing (so a row could repeat) is
+// placed by one thread in slot order instead.
 __global__ void __launch_bounds__(256) csr_scatter_kernel(const CsrParams p) {
-  extern __shared__ int32_t cur[];
+  extern __shared__ int32_t lds_i32[];
+  int32_t *cur = lds_i32;                 // [R]
+  int32_t *tidx = lds_i32 + p.R;          // [2][topk]
   __shared__ int32_t wmax[4];
   __shared__ int32_t unordered;
   const int c = blockIdx.x;
@@ -128,158 +166,187 @@ __global__ void __launch_bounds__(256) csr_scatter_kernel(const CsrParams p) {
   for (int64_t r = tid; r < p.R; r += 256) cur[r] = h[r];
   const int64_t t0 = (int64_t)c * p.CT;
   const int64_t t1 = t0 + p.CT < p.S ? t0 + p.CT : p.S;
-  for (int64_t t = t0; t < t1; ++t) {
-    for (int64_t g = 0; g < p.G; ++g) {
-      const int64_t e0 = ((b * p.S + t) * p.G + g) * p.topk;
-      if (tid == 0) unordered = 0;
-      __syncthreads();
-      // strictly-increasing check over valid slots, in chunks of 256 slots
-      int32_t carry = -1;
-      for (int64_t s0 = 0; s0 < p.topk; s0 += 256) {
-        const int64_t s = s0 + tid;
-        int32_t j = -1;
-        if (s < p.topk) {
-          j = p.idx[e0 + s];
-          if (j < 0 || j >= p.S_kv) j = -1;
-        }
-        // inclusive max-scan of j over the chunk
-        int32_t m = j;
+  const int64_t nseg = (t1 - t0) * p.G;  // (token, group) segments of topk entries
+  const int64_t e_first = ((b * p.S + t0) * p.G) * p.topk;
+  // stage segment 0
+  for (int64_t s = tid; s < p.topk; s += 256) tidx[s] = p.idx[e_first + s];
+  for (int64_t sg = 0; sg < nseg; ++sg) {
+    const int64_t e0 = e_first + sg * p.topk;
+    const int64_t g = sg % p.G;
+    int32_t *cur_idx = tidx + (sg & 1) * p.topk;
+    int32_t *nxt_idx = tidx + ((sg + 1) & 1) * p.topk;
+    __syncthreads();  // segment sg staged; every thread is done with segment sg - 1
+    // (the first barrier of the check loop below orders this reset before
+    // any thread sets the flag)
+    if (tid == 0) unordered = 0;
+    // prefetch the next segment while this one is placed
+    if (sg + 1 < nseg)
+      for (int64_t s = tid; s < p.topk; s += 256) nxt_idx[s] = p.idx[e0 + p.topk + s];
+    // strictly-increasing check over valid slots, in chunks of 256 slots
+    int32_t carry = -1;
+    for (int64_t s0 = 0; s0 < p.topk; s0 += 256) {
+      const int64_t s = s0 + tid;
+      int32_t j = -1;
+      if (s < p.topk) {
+        j = cur_idx[s];
+        if (j < 0 || j >= p.S_kv) j = -1;
+      }
+      int32_t m = j;  // inclusive max-scan within the wave
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-          const int32_t o = __shfl_up(m, off, 64);
-          if (lane >= off) m = max(m, o);
-        }
-        const int32_t m_prev_lane = __shfl_up(m, 1, 64);  // inclusive max up to lane - 1
-        if (lane == 63) wmax[w] = m;
-        __syncthreads();
-        int32_t before = carry;  // max over all earlier slots of the token
-        for (int i = 0; i < w; ++i) before = max(before, wmax[i]);
-        const int32_t prev = lane > 0 ? max(before, m_prev_lane) : before;
-        if (j >= 0 && prev >= j) unordered = 1;
-        const int32_t chunk_max = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
-        carry = max(carry, chunk_max);
-        __syncthreads();
+      for (int off = 1; off < 64; off <<= 1) {
+        const int32_t o = __shfl_up(m, off, 64);
+        if (lane >= off) m = max(m, o);
       }
-      if (!unordered) {
-        for (int64_t s = tid; s < p.topk; s += 256) {
-          const int32_t j = p.idx[e0 + s];
-          if (j >= 0 && j < p.S_kv) {
-            const int32_t pos = atomicAdd(&cur[j * p.G + g], 1);
-            p.refs[pos] = (int32_t)(e0 + s);
-          }
-        }
-      } else if (tid == 0) {
-        for (int64_t s = 0; s < p.topk; ++s) {
-          const int32_t j = p.idx[e0 + s];
-          if (j >= 0 && j < p.S_kv) p.refs[cur[j * p.G + g]++] = (int32_t)(e0 + s);
-        }
-      }
+      const int32_t m_prev_lane = __shfl_up(m, 1, 64);
+      if (lane == 63) wmax[w] = m;
       __syncthreads();
+      int32_t before = carry;
+      for (int i = 0; i < w; ++i) before = max(before, wmax[i]);
+      const int32_t prev = lane > 0 ? max(before, m_prev_lane) : before;
+      if (j >= 0 && prev >= j) unordered = 1;
+      carry = max(carry, max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3])));
+      __syncthreads();
+    }
+    if (!unordered) {
+      for (int64_t s = tid; s < p.topk; s += 256) {
+        const int32_t j = cur_idx[s];
+        if (j >= 0 && j < p.S_kv) {
+          const int32_t pos = atomicAdd(&cur[j * p.G + g], 1);
+          p.refs[pos] = (int32_t)(e0 + s);
+        }
+      }
+    } else if (tid == 0) {
+      for (int64_t s = 0; s < p.topk; ++s) {
+        const int32_t j = cur_idx[s];
+        if (j >= 0 && j < p.S_kv) p.refs[cur[j * p.G + g]++] = (int32_t)(e0 + s);
+      }
     }
   }
 }
 
-// One workgroup per kv row: the row's entries (CSR order) are split into four
-// contiguous quarters, one per wave; each wave sums its quarter in order in
-// fp32 and the four partial sums are combined as ((q0 + q1) + q2) + q3.  The
-// association is fixed by the entry count alone, so results are bitwise
-// reproducible.  Lane l handles element pairs l, l + 64, ...
+// One workgroup per kv row.  The row's work items are its (entry, head tile)
+// partial rows in CSR order, item k = entry k / ntiles, tile k % ntiles; they
+// are split into four contiguous quarters, one per wave.  A partial row is
+// read as 16-byte chunks by a group of LPE lanes, so one load instruction
+// covers EPI = 64 / LPE items and every lane keeps U loads in flight.  Lane
+// group g of a wave sums items g, g + EPI, ... of its quarter in order (fp32);
+// the groups are combined by a fixed xor tree and the four waves as
+// ((w0 + w1) + w2) + w3.  The association depends on the item count alone,
+// so the result is bitwise reproducible.
 template <int D_QK, bool F32P>
 __global__ void __launch_bounds__(256)
 dkv_reduce_kernel(const int32_t *rowptr, const int32_t *refs, const unsigned char *partials,
                   const int8_t *partial_exp, uint16_t *dkv, int64_t nrows, int ntiles) {
-  constexpr int NP = D_QK / 2;          // element pairs per row
-  constexpr int PPL = (NP + 63) / 64;   // pairs per lane
-  constexpr int U = 8;                  // entries in flight per wave
-  constexpr int64_t ROWB = (int64_t)D_QK * (F32P ? 4 : 2);
-  __shared__ float part[4][2 * 64 * PPL];
+  constexpr int ROWB = D_QK * (F32P ? 4 : 2);  // bytes per partial row
+  constexpr int NCR = ROWB / 16;                // 16-byte chunks per partial row
+  constexpr int LPE = NCR <= 8 ? 8 : (NCR <= 16 ? 16 : (NCR <= 32 ? 32 : 64));  // lanes per item
+  constexpr int EPI = 64 / LPE;                 // items per load instruction
+  constexpr int EPC = F32P ? 4 : 8;             // elements per chunk
+  constexpr int U = 8;                          // loads in flight per lane
+  static_assert(NCR * 16 == ROWB && NCR <= 64, "partial rows must be whole 16-byte chunks, at most 1 KiB");
+  __shared__ float part[4][D_QK];
   const int lane = lane_id(), w = wave_id();
+  const int grp = lane / LPE, c = lane % LPE;
+  const bool active = c < NCR;
   const int64_t r = blockIdx.x;
   if (r >= nrows) return;
   const int32_t base = rowptr[r], n = rowptr[r + 1] - base;
-  const int q0 = (int)((int64_t)n * w / 4), q1 = (int)((int64_t)n * (w + 1) / 4);
-  float acc[PPL][2];
+  const int64_t k0 = (int64_t)n * w / 4 * ntiles, k1 = (int64_t)n * (w + 1) / 4 * ntiles;
+  // partial row of item k (relative to this row's first entry), -1 past the quarter
+  auto item_row = [&](int64_t k) -> int64_t {
+    if (k >= k1) return -1;
+    const int64_t ent = k / ntiles;
+    return (int64_t)refs[base + ent] * ntiles + (k - ent * ntiles);
+  };
+  float acc[EPC];
 #pragma unroll
-  for (int k = 0; k < PPL; ++k) acc[k][0] = acc[k][1] = 0.0f;
-  int32_t e_next[U];
+  for (int x = 0; x < EPC; ++x) acc[x] = 0.0f;
+  int64_t pr_next[U];
 #pragma unroll
-  for (int u = 0; u < U; ++u) e_next[u] = (q0 + u < q1) ? refs[base + q0 + u] : 0;
-  for (int i = q0; i < q1; i += U) {
-    int32_t e[U];
+  for (int u = 0; u < U; ++u) pr_next[u] = item_row(k0 + EPI * u + grp);
+  for (int64_t kb = k0; kb < k1; kb += EPI * U) {
+    int64_t pr[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) e[u] = e_next[u];
+    for (int u = 0; u < U; ++u) pr[u] = pr_next[u];
 #pragma unroll
-    for (int u = 0; u < U; ++u) e_next[u] = (i + U + u < q1) ? refs[base + i + U + u] : 0;
-    for (int t = 0; t < ntiles; ++t) {
-      float v[U][PPL][2];
+    for (int u = 0; u < U; ++u) pr_next[u] = item_row(kb + EPI * (U + u) + grp);
+    i32x4 v[U];
+    float sc[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int64_t pr = (int64_t)e[u] * ntiles + t;
-        const unsigned char *row = partials + pr * ROWB;
-        float sc = 1.0f;
-        if constexpr (!F32P) sc = exp2i(-(int)partial_exp[pr]);
-#pragma unroll
-        for (int k = 0; k < PPL; ++k) {
-          const int pi = lane + 64 * k;
-          v[u][k][0] = v[u][k][1] = 0.0f;
-          if (pi < NP) {
-            if constexpr (F32P) {
-              const float2 x = reinterpret_cast<const float2 *>(row)[pi];
-              v[u][k][0] = x.x;
-              v[u][k][1] = x.y;
-            } else {
-              const uint32_t x = reinterpret_cast<const uint32_t *>(row)[pi];
-              v[u][k][0] = f16_bits_to_f32(x & 0xffffu) * sc;  // exact: sc is a power of two
-              v[u][k][1] = f16_bits_to_f32(x >> 16) * sc;
-            }
-          }
-        }
+    for (int u = 0; u < U; ++u) {
+      v[u] = i32x4{0, 0, 0, 0};
+      sc[u] = 0.0f;
+      if (pr[u] >= 0 && active) {
+        v[u] = ld_global_16(partials + pr[u] * ROWB + c * 16);
+        if constexpr (!F32P) sc[u] = exp2i(-(int)partial_exp[pr[u]]);
       }
+    }
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if (i + u < q1) {
+    for (int u = 0; u < U; ++u) {
 #pragma unroll
-          for (int k = 0; k < PPL; ++k) {
-            acc[k][0] += v[u][k][0];
-            acc[k][1] += v[u][k][1];
-          }
+      for (int x = 0; x < EPC; ++x) {
+        if constexpr (F32P) {
+          acc[x] += __int_as_float(v[u][x]);
+        } else {
+          const uint32_t h = ((uint32_t)v[u][x >> 1] >> (16 * (x & 1))) & 0xffffu;
+          acc[x] += f16_bits_to_f32(h) * sc[u];  // exact: sc is a power of two
         }
       }
     }
   }
 #pragma unroll
-  for (int k = 0; k < PPL; ++k) {
-    part[w][2 * (lane + 64 * k)] = acc[k][0];
-    part[w][2 * (lane + 64 * k) + 1] = acc[k][1];
+  for (int off = LPE; off < 64; off *= 2) {
+#pragma unroll
+    for (int x = 0; x < EPC; ++x) acc[x] += __shfl_xor(acc[x], off, 64);
+  }
+  if (grp == 0 && active) {
+#pragma unroll
+    for (int x = 0; x < EPC; ++x) part[w][c * EPC + x] = acc[x];
   }
   __syncthreads();
   uint32_t *out = reinterpret_cast<uint32_t *>(dkv + r * D_QK);
-  for (int pi = threadIdx.x; pi < NP; pi += 256) {
+  for (int pi = threadIdx.x; pi < D_QK / 2; pi += 256) {
     const float x0 = ((part[0][2 * pi] + part[1][2 * pi]) + part[2][2 * pi]) + part[3][2 * pi];
     const float x1 = ((part[0][2 * pi + 1] + part[1][2 * pi + 1]) + part[2][2 * pi + 1]) + part[3][2 * pi + 1];
     out[pi] = pack_bf16x2(x0, x1);
   }
 }
 
-// Host side: build the inverse index (five stream-ordered kernels).
+// Chunking of the inverse index: 16 tokens per chunk unless the chunk
+// histogram (NC * R counters per batch) would exceed 2^24 entries.
+static void csr_plan(int64_t S, int64_t R, int *CT, int *NC, int *NQ) {
+  int ct = 16;
+  while ((int64_t)((S + ct - 1) / ct) * R > (1ll << 24) && ct < (1 << 20)) ct *= 2;
+  *CT = ct;
+  *NC = (int)((S + ct - 1) / ct);
+  *NQ = (*NC + kChunkGroup - 1) / kChunkGroup;
+}
+
+// Host side: build the inverse index (six stream-ordered kernels, no atomics
+// on global memory, no memset).
 static int launch_csr(const CsrParams &cp, int64_t B, hipStream_t st) {
   const size_t hist_lds = (size_t)cp.R * 4;
-  if (hist_lds > 64 * 1024) {
-    hipError_t e1 = hipFuncSetAttribute((const void *)csr_hist_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        (int)hist_lds);
-    hipError_t e2 = hipFuncSetAttribute((const void *)csr_scatter_kernel,
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)hist_lds);
-    if (e1 != hipSuccess || e2 != hipSuccess)
-      return set_error(DSA_ERR_HIP, "sparse_mla_bwd: csr LDS attribute failed");
-  }
+  const size_t scat_lds = hist_lds + 2 * (size_t)cp.topk * 4;
+  if (scat_lds > 160 * 1024)
+    return set_error(DSA_ERR_UNSUPPORTED, "sparse_mla_bwd: inverse index needs %zu bytes of LDS", scat_lds);
+  if (hist_lds > 64 * 1024 &&
+      hipFuncSetAttribute((const void *)csr_hist_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)hist_lds) != hipSuccess)
+    return set_error(DSA_ERR_HIP, "sparse_mla_bwd: csr LDS attribute failed");
+  if (scat_lds > 64 * 1024 &&
+      hipFuncSetAttribute((const void *)csr_scatter_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)scat_lds) != hipSuccess)
+    return set_error(DSA_ERR_HIP, "sparse_mla_bwd: csr LDS attribute failed");
   const int64_t rows = B * cp.R;
   const dim3 cgrid((unsigned)cp.NC, (unsigned)B);
   const unsigned rgrid = (unsigned)((rows + 255) / 256);
+  const unsigned qgrid = (unsigned)((B * cp.NQ * cp.R + 255) / 256);
   hipLaunchKernelGGL(csr_hist_kernel, cgrid, dim3(256), hist_lds, st, cp);
-  hipLaunchKernelGGL(csr_rowsum_kernel, dim3(rgrid), dim3(256), 0, st, cp, B);
+  hipLaunchKernelGGL(csr_gsum_kernel, dim3(qgrid), dim3(256), 0, st, cp, B);
+  hipLaunchKernelGGL(csr_rows_kernel, dim3(rgrid), dim3(256), 0, st, cp, B);
   hipLaunchKernelGGL(csr_scan_kernel, dim3(1), dim3(1024), 0, st, cp.tot, cp.rowptr, rows);
-  hipLaunchKernelGGL(csr_bases_kernel, dim3(rgrid), dim3(256), 0, st, cp, B);
-  hipLaunchKernelGGL(csr_scatter_kernel, cgrid, dim3(256), hist_lds, st, cp);
+  hipLaunchKernelGGL(csr_bases_kernel, dim3(qgrid), dim3(256), 0, st, cp, B);
+  hipLaunchKernelGGL(csr_scatter_kernel, cgrid, dim3(256), scat_lds, st, cp);
   return check_launch("sparse_mla_bwd(csr)");
 }
 
