@@ -2,16 +2,19 @@
 
 Drop-in for cppmega/megatron/index_cache_patch.py:37-278.  DSA layers are
 numbered in construction order ("DSA ranks").  Full ranks (default 0,3,6 from
-CPPMEGA_INDEX_CACHE_FULL_LAYERS) run the indexer and cache their top-k
-indices; Shared ranks skip the indexer and reuse the indices of the nearest
-preceding Full rank; a Shared rank with no preceding Full rank in the cache is
-promoted to Full (:168-184).  The cache is cleared when the lowest Full rank
-runs, i.e. once per micro-batch (:115-117).
+CPPMEGA_INDEX_CACHE_FULL_LAYERS, :68-69) run the original forward and cache
+their top-k indices; Shared ranks skip the indexer and run sparse attention
+with the indices of the nearest preceding cached rank (:160-166); a Shared
+rank with nothing cached before it is promoted to Full for good (:168-184).
+The cache is cleared when the lowest Full rank runs, i.e. once per
+micro-batch (:115-117).
 
 The schedule itself lives in ``IndexCacheSchedule`` (no Megatron needed);
-``apply_index_cache_patch`` wires it into Megatron's ``DSAttention`` the same
-way the reference does, re-deriving Full-layer indices with this package's
-deterministic indexer + top-k.
+``apply_index_cache_patch`` wires it into Megatron's ``DSAttention`` as the
+reference does, re-deriving Full-layer indices with this package's
+deterministic gfx950 indexer + top-k (``fused_qk_topk_naive``) instead of
+Megatron's torch one.  Context-parallel gathers go through Megatron's
+``gather_from_sequence_parallel_region`` exactly where the reference calls it.
 """
 from __future__ import annotations
 
@@ -20,28 +23,41 @@ import os
 
 import torch
 
+from .dsa_topk import fused_qk_topk_naive
+
 log = logging.getLogger(__name__)
+
+_MARKER = "__cppmega_amd_index_cache__"
 
 
 def parse_full_ranks(spec: str | None = None) -> set[int]:
+    """"0,3,6" -> {0, 3, 6} (index_cache_patch.py:67-69)."""
     spec = os.environ.get("CPPMEGA_INDEX_CACHE_FULL_LAYERS", "0,3,6") if spec is None else spec
     return {int(x.strip()) for x in spec.split(",") if x.strip()}
 
 
 class IndexCacheSchedule:
-    """Full / Shared bookkeeping of IndexCache, independent of Megatron."""
+    """Full / Shared bookkeeping of IndexCache, independent of Megatron.
+
+    ``cache`` maps DSA rank -> topk_indices [b, sq, topk] (index_cache_patch.py:33-34);
+    ``step`` counts micro-batches (the reference's _CACHE_STEP).
+    """
 
     def __init__(self, full_ranks=None):
-        self.full_ranks = parse_full_ranks() if full_ranks is None else set(full_ranks)
-        self.min_full = min(self.full_ranks) if self.full_ranks else 0
+        self.set_full_ranks(parse_full_ranks() if full_ranks is None else full_ranks)
         self.cache: dict[int, torch.Tensor] = {}
         self.step = -1
         self.promoted: set[int] = set()
+
+    def set_full_ranks(self, ranks) -> None:
+        self.full_ranks = set(ranks)
+        self.min_full = min(self.full_ranks) if self.full_ranks else 0
 
     def is_full(self, rank: int) -> bool:
         return rank in self.full_ranks or rank in self.promoted
 
     def begin_layer(self, rank: int) -> None:
+        """Called at the top of every DSA forward: the lowest Full rank starts a micro-batch."""
         if rank == self.min_full:
             self.step += 1
             self.cache.clear()
@@ -59,6 +75,12 @@ class IndexCacheSchedule:
     def promote(self, rank: int) -> None:
         self.promoted.add(rank)
 
+    def savings(self, n_layers: int = 9) -> tuple[int, int, int]:
+        """(full, shared, percent of indexer work saved) for n_layers DSA layers (:264-267)."""
+        n_full = len(self.full_ranks)
+        n_shared = n_layers - n_full
+        return n_full, n_shared, int(n_shared / n_layers * 100)
+
 
 _SCHEDULE: IndexCacheSchedule | None = None
 
@@ -70,29 +92,52 @@ def get_schedule() -> IndexCacheSchedule:
     return _SCHEDULE
 
 
+def _cp_info(indexer):
+    cp_group = getattr(getattr(indexer, "pg_collection", None), "cp", None)
+    size = cp_group.size() if cp_group is not None else 1
+    rank = cp_group.rank() if cp_group is not None else 0
+    return cp_group, size, rank
+
+
 def apply_index_cache_patch(force: bool = False, dsa_module=None) -> bool:
-    """Monkey-patch Megatron ``DSAttention`` (or ``dsa_module.DSAttention``) for IndexCache."""
+    """Monkey-patch Megatron ``DSAttention`` (or ``dsa_module.DSAttention``) for IndexCache.
+
+    Mirrors cppmega/megatron/index_cache_patch.py:37-278: same marker
+    semantics (a second call is a no-op unless ``force``), same Full / Shared
+    / promote flow, same helpers taken from the dsa module for the Shared
+    fast path (_run_sparse_attention, _ensure_sbhd,
+    _normalize_dsattention_output_rank, _build_dsattention_forward_mask,
+    _normalize_cp_comm_type).
+    """
     if dsa_module is None:
         from megatron.core.transformer.experimental_attention_variant import dsa as dsa_module
-    from .dsa_topk import fused_qk_topk_naive
 
     cls = getattr(dsa_module, "DSAttention", None)
     assert cls is not None, "DSAttention not found in dsa module"
-    marker = "__cppmega_amd_index_cache__"
-    if getattr(cls, marker, False) and not force:
+    if getattr(cls, _MARKER, False) and not force:
         return True
 
+    run_sparse = dsa_module._run_sparse_attention
+    ensure_sbhd = dsa_module._ensure_sbhd
+    normalize_rank = dsa_module._normalize_dsattention_output_rank
+    build_mask = dsa_module._build_dsattention_forward_mask
+    normalize_cp = dsa_module._normalize_cp_comm_type
+    try:
+        from megatron.core.tensor_parallel.mappings import gather_from_sequence_parallel_region as cp_gather
+    except ImportError:
+        cp_gather = None
+
     sched = get_schedule()
-    sched.full_ranks = parse_full_ranks()
-    sched.min_full = min(sched.full_ranks) if sched.full_ranks else 0
+    sched.set_full_ranks(parse_full_ranks())
+    log.info("IndexCache: Full DSA layer ranks: %s", sorted(sched.full_ranks))
     counter = [0]
     orig_init = cls.__init__
     orig_forward = cls.forward
-    run_sparse = getattr(dsa_module, "_run_sparse_attention", None)
 
     def _ic_init(self, *args, **kwargs):
         orig_init(self, *args, **kwargs)
         self._ic_dsa_rank = counter[0]
+        self._ic_is_full = counter[0] in sched.full_ranks
         counter[0] += 1
 
     def _ic_forward(self, query, key, value, attention_mask, x, qr, position_ids=None, attn_mask_type=None,
@@ -101,28 +146,60 @@ def apply_index_cache_patch(force: bool = False, dsa_module=None) -> bool:
         sched.begin_layer(rank)
         kw = dict(position_ids=position_ids, attn_mask_type=attn_mask_type, attention_bias=attention_bias,
                   packed_seq_params=packed_seq_params, up_v_weight=up_v_weight)
-        cached = None if sched.is_full(rank) else sched.lookup(rank)
-        if cached is None:
-            if not sched.is_full(rank):
+        cached = None
+        if not (self._ic_is_full or sched.is_full(rank)):
+            cached = sched.lookup(rank)
+            if cached is None:
+                self._ic_is_full = True
                 sched.promote(rank)
-                log.info("IndexCache: DSA rank %d promoted to FULL (no preceding Full rank)", rank)
+                log.info("IndexCache: DSA rank %d auto-promoted to FULL (no preceding Full rank)", rank)
+        if cached is None:
             result = orig_forward(self, query, key, value, attention_mask, x, qr, **kw)
             with torch.no_grad():
                 q_idx, k_idx, w_idx = self.indexer.forward_before_topk(x.detach(), qr.detach(), packed_seq_params)
+                cp_group, cp_size, _ = _cp_info(self.indexer)
+                if cp_size > 1 and k_idx.size(0) == query.size(0) and cp_gather is not None:
+                    k_idx = cp_gather(k_idx, group=cp_group)
                 _, idx = fused_qk_topk_naive(q_idx, k_idx, w_idx, self.indexer.index_topk, mask=None,
-                                             use_relu=getattr(self.config, "dsa_indexer_scoring_relu", True))
+                                             use_relu=getattr(self.config, "dsa_indexer_scoring_relu", False))
                 sched.store(rank, idx)
             return result
-        if run_sparse is None:
-            raise RuntimeError("dsa module has no _run_sparse_attention for the Shared fast path")
-        output, _ = run_sparse(query=query, key=key, value=value, up_v_weight=up_v_weight,
-                               topk_indices=cached, softmax_scale=self.softmax_scale, config=self.config)
-        return output
+
+        # Shared fast path: sparse attention on the cached indices, no indexer, no indexer loss
+        query, _ = ensure_sbhd(query, "query")
+        key, _ = ensure_sbhd(key, "key")
+        if value is not None:
+            value, _ = ensure_sbhd(value, "value")
+        if up_v_weight is not None:
+            up_v_weight = up_v_weight.to(device=query.device, dtype=query.dtype).contiguous()
+        latent = int(getattr(self.config, "kv_lora_rank", 0) or 0)
+        pos = int(getattr(self.config, "qk_pos_emb_head_dim", 0) or 0)
+        absorbed = (latent > 0 and latent + pos > 0 and key.size(2) == 1
+                    and query.size(-1) == key.size(-1) == latent + pos)
+        sq, b = query.size(0), query.size(1)
+        cp_group, cp_size, cp_rank = _cp_info(self.indexer)
+        if cp_size > 1 and cp_gather is not None:
+            if key.size(0) == sq:
+                key = cp_gather(key, group=cp_group)
+            if value is not None and value.size(0) == sq:
+                value = cp_gather(value, group=cp_group)
+        float_mask, varlen = build_mask(
+            sq=sq, skv=key.size(0), b=b, device=x.device, cp_size=cp_size, cp_rank=cp_rank,
+            cp_comm_type=normalize_cp(getattr(self, "cp_comm_type", None)), cp_group=cp_group,
+            attn_mask_type=attn_mask_type, attention_mask=attention_mask, position_ids=position_ids,
+            packed_seq_params=packed_seq_params, packed_query_positions=None)
+        starts, ends, key_positions = varlen if varlen is not None else (None, None, None)
+        output, _ = run_sparse(absorbed_mla=absorbed, query=query, key=key, value=value, up_v_weight=up_v_weight,
+                               topk_indices=cached, softmax_scale=self.softmax_scale, config=self.config,
+                               mask=float_mask, varlen_starts=starts, varlen_ends=ends,
+                               key_positions=key_positions)
+        return normalize_rank(output, x.ndim)
 
     cls.__init__ = _ic_init
     cls.forward = _ic_forward
-    setattr(cls, marker, True)
-    log.info("IndexCache installed: Full ranks %s", sorted(sched.full_ranks))
+    setattr(cls, _MARKER, True)
+    n_full, n_shared, pct = sched.savings()
+    log.info("IndexCache installed: %d Full + %d Shared = %d%% indexer savings", n_full, n_shared, pct)
     return True
 
 

@@ -1,6 +1,9 @@
 """Shared test helpers (tolerance checks, device moves)."""
 from __future__ import annotations
 
+import os
+
+import numpy as np
 import torch
 
 # Tolerance contract for bf16 SparseMLA outputs, LSE and gradients vs the oracle.
@@ -42,3 +45,17 @@ def assert_mostly_close(actual, expected, rtol=RTOL, atol=ATOL, max_bad_frac=1e-
 
 def to_dev(d, dev):
     return {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in d.items()}
+
+
+GOLDEN_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def load_golden(name):
+    """Known-answer fixture written by tests/golden/make_golden.py (dict of numpy arrays)."""
+    with np.load(os.path.join(GOLDEN_DIR, name), allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def bf16_from_bits(bits):
+    """uint16 bf16 bit patterns (numpy) -> torch.bfloat16 tensor."""
+    return torch.from_numpy(np.ascontiguousarray(bits).astype(np.uint16).view(np.int16)).view(torch.bfloat16)

@@ -1,0 +1,108 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function
+include/dsa_hip.h declares with the ctypes signatures the host uses, and its
+argument validation returns the documented status codes before any device
+work (so no call below touches a GPU)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from cppmega_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dsa_hip.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return sorted(set(re.findall(r"\b(dsa_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        from cppmega_amd import build_lib
+        build_lib.build()
+    return _lib.load()
+
+
+def test_header_and_binding_agree():
+    declared = _declared_functions()
+    assert declared == sorted(_lib.EXPORTED_SYMBOLS)
+    assert set(_lib._SIGNATURES) == set(declared)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    raw = ctypes.CDLL(_lib.LIB_PATH)
+    for name in _declared_functions():
+        assert hasattr(raw, name), f"{name} missing from libdsa_hip.so"
+
+
+def test_abi_version_and_status_codes(lib):
+    assert lib.dsa_abi_version() == 100
+    text = open(HEADER).read()
+    for name, val in (("DSA_OK", 0), ("DSA_ERR_INVALID_ARG", -1), ("DSA_ERR_UNSUPPORTED", -2),
+                      ("DSA_ERR_HIP", -3), ("DSA_ERR_WORKSPACE", -4)):
+        assert re.search(rf"\b{name}\s*=\s*{val}\b", text), name
+        assert getattr(_lib, name) == val
+
+
+def _err(lib):
+    return lib.dsa_last_error().decode()
+
+
+def test_fwd_rejects_bad_arguments(lib):
+    # (B, S, S_kv, H, G, D_qk, D_v, topk, dtype)
+    bad = [
+        (1, 4, 0, 16, 1, 128, 64, 32, 0),     # S_kv = 0
+        (1, 4, 8, 16, 3, 128, 64, 32, 0),     # H not divisible by G
+        (1, 4, 8, 16, 1, 128, 256, 32, 0),    # d_v > d_qk
+        (1, 4, 8, 16, 1, 128, 64, 32, 7),     # unknown dtype
+        (1, 4, 8, 16, 1, 128, 64, 0, 0),      # topk = 0
+        (1, 4, 8, 16, 1, 128, 64, 32, 0),     # null pointers
+        (1, 4, 8, 16, 1, 128, 64, 32, 1),     # e4m3 without scales (and null pointers)
+    ]
+    for B, S, Skv, H, G, D, dv, k, dt in bad:
+        rc = lib.dsa_sparse_mla_fwd(None, None, None, None, None, B, S, Skv, H, G, D, dv, k,
+                                    0.1, dt, None, None, None)
+        assert rc == _lib.DSA_ERR_INVALID_ARG, (B, S, Skv, H, G, D, dv, k, dt)
+        assert "dsa_sparse_mla_fwd" in _err(lib)
+    # empty problems are a no-op success
+    assert lib.dsa_sparse_mla_fwd(None, None, None, None, None, 0, 4, 8, 16, 1, 128, 64, 32,
+                                  0.1, 0, None, None, None) == _lib.DSA_OK
+
+
+def test_bwd_workspace_and_validation(lib):
+    ws = lib.dsa_sparse_mla_bwd_workspace_size
+    a = ws(2, 4096, 4096, 32, 1, 128, 64, 256, 0)
+    b = ws(2, 4096, 4096, 32, 1, 128, 64, 256, _lib.BWD_FP32_PARTIALS)
+    c = ws(1, 4096, 4096, 32, 1, 128, 64, 256, 0)
+    # fp16 partial rows: 2 * 4096 * 256 entries x 256 B, fp32 doubles them
+    assert a >= 2 * 4096 * 256 * 128 * 2 and b > a and c < a
+    assert ws(2, 4096, 4096, 32, 1, 128, 64, 256, 0) == a      # deterministic
+    rc = lib.dsa_sparse_mla_bwd(*([None] * 10), 0, 1, 4, 8, 16, 1, 128, 64, 32, 0.1, 0, None, None, 8, None)
+    assert rc == _lib.DSA_ERR_INVALID_ARG and "flags" in _err(lib)
+    rc = lib.dsa_sparse_mla_bwd(*([None] * 10), 0, 1, 4, 70000, 16, 1, 128, 64, 32, 0.1, 0, None, None, 0, None)
+    assert rc == _lib.DSA_ERR_INVALID_ARG
+
+
+def test_indexer_and_topk_validation(lib):
+    rc = lib.dsa_indexer_scores(None, None, None, None, 1, 8, 8, 16, 64, 0, 2, None, None, 0, 1, None)
+    assert rc == _lib.DSA_ERR_INVALID_ARG
+    rc = lib.dsa_indexer_scores(None, None, None, None, 1, 8, 8, 16, 64, 0, 2, None, None, 5, 1, None)
+    assert rc == _lib.DSA_ERR_INVALID_ARG
+    # row_stride < row_len
+    rc = lib.dsa_topk(None, 4, 100, 50, 4, 0, 0, None, None, 8, None, None)
+    assert rc == _lib.DSA_ERR_INVALID_ARG
+    assert lib.dsa_topk(None, 0, 100, 100, 4, 0, 0, None, None, 8, None, None) == _lib.DSA_OK
+
+
+def test_fp8_quantize_validation(lib):
+    assert lib.dsa_fp8_quantize_workspace_size() >= 4 * 1024
+    rc = lib.dsa_fp8_tensorwise_quantize(None, 16, 9, None, None, None, 0, None)
+    assert rc == _lib.DSA_ERR_INVALID_ARG

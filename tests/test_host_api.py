@@ -1,0 +1,189 @@
+"""Host-side behaviour that needs no GPU: the product path refuses CPU tensors
+(no fallback), the reference's assertion / error contract, the IndexCache
+schedule wired into a stand-in Megatron dsa module, and bench.py's one-GPU
+rule."""
+from __future__ import annotations
+
+import ast
+import os
+import subprocess
+import sys
+import types
+
+import pytest
+import torch
+
+import cppmega_amd
+from cppmega_amd import index_cache_patch as icp
+from cppmega_amd.dsa_indexer_fused_patch import compute_index_scores_fused_bf16, index_scores
+from cppmega_amd.dsa_topk import topk_indices
+from cppmega_amd.sparse_mla_ops import (SparseMLA, SparseMLA_FP8, sparse_mla_bwd, sparse_mla_fwd_interface,
+                                        sparse_mla_fwd_fp8_interface)
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _inputs(B=1, S=8, H=16, D=128, K=16):
+    q = torch.randn(B, S, H, D).to(torch.bfloat16)
+    kv = torch.randn(B, S, 1, D).to(torch.bfloat16)
+    idx = torch.zeros(B, S, 1, K, dtype=torch.int32)
+    return q, kv, idx
+
+
+def test_product_path_has_no_cpu_fallback():
+    q, kv, idx = _inputs()
+    with pytest.raises(RuntimeError, match="gfx950"):
+        sparse_mla_fwd_interface(q, kv, idx, d_v=64)
+    with pytest.raises(RuntimeError, match="gfx950"):
+        SparseMLA.apply(q, kv, idx, 0.1, 64)
+    with pytest.raises(RuntimeError, match="gfx950"):
+        compute_index_scores_fused_bf16(torch.randn(8, 1, 16, 64).bfloat16(), torch.randn(8, 1, 16),
+                                        torch.randn(8, 1, 64).bfloat16())
+    with pytest.raises(RuntimeError, match="gfx950"):
+        topk_indices(torch.randn(1, 8, 8), 4)
+
+
+def test_product_package_never_imports_the_oracle():
+    pkg = os.path.join(ROOT, "cppmega_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if not f.endswith(".py"):
+                continue
+            tree = ast.parse(open(os.path.join(dirpath, f)).read())
+            for node in ast.walk(tree):
+                names = []
+                if isinstance(node, ast.Import):
+                    names = [a.name for a in node.names]
+                elif isinstance(node, ast.ImportFrom) and node.module:
+                    names = [node.module]
+                assert not any(n == "oracle" or n.startswith("oracle.") for n in names), f"{f} imports oracle"
+
+
+def test_reference_assertions():
+    q, kv, idx = _inputs()
+    with pytest.raises(AssertionError):
+        sparse_mla_fwd_interface(q, kv, idx, d_v=64, return_p_sum=True)
+    with pytest.raises(AssertionError):
+        sparse_mla_fwd_interface(q, kv[..., :64].contiguous(), idx, d_v=64)      # dim mismatch
+    with pytest.raises(AssertionError):
+        sparse_mla_fwd_interface(q, kv, idx, d_v=256)                             # d_v > d_qk
+    with pytest.raises(AssertionError):
+        sparse_mla_fwd_interface(q, kv, idx.long(), d_v=64)                       # int64 indices
+    with pytest.raises(AssertionError):
+        sparse_mla_fwd_interface(q.transpose(1, 2), kv, idx, d_v=64)             # non-contiguous
+    with pytest.raises(AssertionError):
+        sparse_mla_bwd(q, kv, q[..., :64], q[..., :64], idx.long(), torch.zeros(1, 8, 16))
+
+
+def test_raw_fp8_without_scale_is_a_value_error():
+    q, kv, idx = _inputs()
+    with pytest.raises(ValueError):
+        SparseMLA_FP8.apply(q.float().to(torch.float8_e4m3fn), kv.float().to(torch.float8_e4m3fn), idx, 0.1, 64)
+    with pytest.raises(RuntimeError, match="gfx950"):
+        sparse_mla_fwd_fp8_interface(q, kv, idx, d_v=64)                          # quantises on the GPU only
+
+
+def test_indexer_shape_checks():
+    with pytest.raises(AssertionError):
+        index_scores(torch.randn(8, 1, 16, 64).bfloat16(), torch.randn(8, 1, 16), torch.randn(8, 2, 64).bfloat16())
+    with pytest.raises(TypeError):
+        index_scores(torch.randn(8, 1, 16, 64), torch.randn(8, 1, 16), torch.randn(8, 1, 64))
+
+
+def test_package_exports():
+    from cppmega_amd import sparse_mla_ops
+    for name in ("SparseMLA", "SparseMLA_FP8", "sparse_mla_fwd_interface", "sparse_mla_bwd",
+                 "sparse_mla_fwd_fp8_interface", "sparse_mla_bwd_fp8", "per_token_cast_to_fp8",
+                 "sparse_mla_as_unfused_dsa", "sparse_mla_fp8_as_unfused_dsa"):
+        assert hasattr(sparse_mla_ops, name), name
+    assert cppmega_amd is not None
+
+
+# ---------------------------------------------------------------------------
+# IndexCache schedule
+# ---------------------------------------------------------------------------
+def test_schedule_semantics():
+    s = icp.IndexCacheSchedule(full_ranks={0, 3, 6})
+    assert [s.is_full(r) for r in range(9)] == [r in (0, 3, 6) for r in range(9)]
+    assert s.savings(9) == (3, 6, 66)
+    s.begin_layer(0)
+    assert s.step == 0
+    s.store(0, "i0")
+    assert s.lookup(1) == "i0" and s.lookup(2) == "i0"
+    s.store(3, "i3")
+    assert s.lookup(4) == "i3" and s.lookup(8) == "i3"
+    s.begin_layer(0)                      # next micro-batch clears the cache
+    assert s.step == 1 and s.lookup(5) is None
+    assert icp.parse_full_ranks(" 1, 4 ,7,") == {1, 4, 7}
+
+
+class _FakeIndexer:
+    index_topk = 2
+    pg_collection = None
+
+    def forward_before_topk(self, x, qr, packed):
+        return x, qr, packed
+
+
+def _fake_dsa_module(calls):
+    class DSAttention:
+        def __init__(self, layer_number):
+            self.layer_number = layer_number
+            self.indexer = _FakeIndexer()
+            self.config = types.SimpleNamespace(kv_lora_rank=0, qk_pos_emb_head_dim=0)
+            self.softmax_scale = 0.5
+
+        def forward(self, query, key, value, attention_mask, x, qr, **kw):
+            calls.append(("full", self._ic_dsa_rank))
+            return "full-out"
+
+    def run_sparse(**kw):
+        calls.append(("shared", kw["topk_indices"]))
+        return "shared-out", "path"
+
+    return types.SimpleNamespace(
+        DSAttention=DSAttention,
+        _run_sparse_attention=run_sparse,
+        _ensure_sbhd=lambda t, name: (t, None),
+        _normalize_dsattention_output_rank=lambda out, nd: out,
+        _build_dsattention_forward_mask=lambda **kw: (None, None),
+        _normalize_cp_comm_type=lambda t: t,
+    )
+
+
+def test_index_cache_patch_full_shared_promote(monkeypatch):
+    monkeypatch.setenv("CPPMEGA_INDEX_CACHE_FULL_LAYERS", "1,3")
+    monkeypatch.setattr(icp, "_SCHEDULE", None)
+    picks = []
+
+    def fake_topk(q, k, w, topk, mask=None, use_relu=False, **kw):
+        picks.append(use_relu)
+        return None, f"idx-from-{int(q)}"
+
+    monkeypatch.setattr(icp, "fused_qk_topk_naive", fake_topk)
+    calls = []
+    mod = _fake_dsa_module(calls)
+    assert icp.apply_index_cache_patch(dsa_module=mod)
+    assert icp.apply_index_cache_patch(dsa_module=mod)          # second call: no-op
+    layers = [mod.DSAttention(i) for i in range(5)]
+    q4 = torch.zeros(4, 1, 2, 8)
+    for step in range(2):
+        calls.clear()
+        outs = [layer.forward(q4, q4, None, None, torch.tensor(10 * step + i), torch.tensor(0), None)
+                for i, layer in enumerate(layers)]
+        # rank 0 has no preceding Full rank: promoted; 1 and 3 are Full; 2 reuses 1, 4 reuses 3
+        assert outs == ["full-out", "full-out", "shared-out", "full-out", "shared-out"]
+        assert calls == [("full", 0), ("full", 1), ("shared", f"idx-from-{10 * step + 1}"), ("full", 3),
+                         ("shared", f"idx-from-{10 * step + 3}")]
+    assert layers[0]._ic_is_full and not layers[2]._ic_is_full
+    assert picks and not any(picks)            # relu defaults to the config's False, as the reference
+
+
+# ---------------------------------------------------------------------------
+# bench.py: one GPU only
+# ---------------------------------------------------------------------------
+def test_bench_refuses_more_than_one_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=300, cwd=ROOT)
+    assert r.returncode != 0
+    assert "one GPU" in (r.stdout + r.stderr) or "1 GPU" in (r.stdout + r.stderr)

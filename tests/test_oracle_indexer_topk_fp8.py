@@ -1,0 +1,157 @@
+"""Pins the indexer, top-k and FP8 quantiser oracles (CPU): known-answer
+fixtures, the upstream einsum form, float64 brute force, torch.topk,
+torch's float8_e4m3fn cast, and hypothesis properties."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+from hypothesis import given, settings
+from hypothesis import strategies as st
+
+from oracle import fp8 as of8
+from oracle import indexer as oidx
+from oracle import topk as otk
+from tests._util import assert_close, bf16_from_bits, load_golden
+
+
+# ---------------------------------------------------------------------------
+# Indexer
+# ---------------------------------------------------------------------------
+def _golden_indexer():
+    g = load_golden("indexer.npz")
+    return g, bf16_from_bits(g["q_bits"]), torch.from_numpy(g["w"]), bf16_from_bits(g["k_bits"])
+
+
+def test_indexer_matches_golden():
+    g, q, w, k = _golden_indexer()
+    expect = torch.from_numpy(g["scores"])
+    assert_close(oidx.compute_index_scores(q, w, k), expect, rtol=1e-5, atol=1e-4, what="per-head loop")
+    assert_close(oidx.compute_index_scores_einsum(q, w, k), expect, rtol=1e-5, atol=1e-4, what="einsum")
+    assert_close(oidx.compute_index_scores_f64(q, w, k), expect.double(), rtol=1e-9, atol=1e-9, what="f64")
+
+
+def test_indexer_relu_off_and_planted_mistake():
+    g, q, w, k = _golden_indexer()
+    a = oidx.compute_index_scores(q, w, k, use_relu=False)
+    b = oidx.compute_index_scores_f64(q, w, k, use_relu=False)
+    assert_close(a, b, rtol=1e-5, atol=1e-4, what="no relu")
+    with pytest.raises(AssertionError):  # ReLU dropped: the fixture catches it
+        assert_close(a, torch.from_numpy(g["scores"]), rtol=1e-3, atol=1e-3, what="relu dropped")
+    with pytest.raises(AssertionError):  # weights of the wrong head
+        assert_close(oidx.compute_index_scores(q, w.flip(-1), k), torch.from_numpy(g["scores"]),
+                     rtol=1e-3, atol=1e-3, what="heads swapped")
+
+
+def test_indexer_fp8_scales_dequantise():
+    g, q, w, k = _golden_indexer()
+    q8 = (q.float() * 8).to(torch.float8_e4m3fn)
+    k8 = (k.float() * 4).to(torch.float8_e4m3fn)
+    a = oidx.compute_index_scores(q8, w, k8, q_scale=0.125, k_scale=0.25)
+    b = oidx.compute_index_scores_f64(q8.double() * 0.125, w, k8.double() * 0.25)
+    assert_close(a, b, rtol=1e-5, atol=1e-4, what="fp8 indexer")
+
+
+def test_causal_mask_and_flops():
+    s = torch.zeros(2, 4, 4)
+    oidx.causal_mask_(s)
+    assert torch.isinf(s).sum() == 2 * 6 and torch.all(s.tril() == 0)
+    assert oidx.flops_causal(2, 4096, 16, 64) == 34_368_126_976
+
+
+# ---------------------------------------------------------------------------
+# Top-k
+# ---------------------------------------------------------------------------
+def test_topk_matches_golden():
+    g = load_golden("topk.npz")
+    k = int(g["topk"])
+    out = otk.topk_ascending(g["scores"], k, g["starts"], g["ends"])
+    np.testing.assert_array_equal(out, g["out"])
+    for r in range(len(g["out"])):
+        row = otk.topk_bruteforce_row(g["scores"][r], k, int(g["starts"][r]), int(g["ends"][r]))
+        assert row == list(g["out"][r])
+
+
+def test_topk_vs_torch_topk_on_distinct_rows():
+    gen = torch.Generator().manual_seed(3)
+    s = torch.randn(64, 500, generator=gen)
+    for k in (1, 7, 64, 499, 500):
+        mine = otk.topk_ascending(s.numpy(), k)
+        ref = torch.topk(s, k, dim=-1).indices.sort(-1).values.numpy()
+        np.testing.assert_array_equal(mine, ref)
+
+
+def test_topk_causal_windows_and_padding():
+    rows, n, k = 12, 10, 4
+    starts, ends = otk.causal_windows(rows, seq_q=6, row_len=n)
+    assert list(ends[:6]) == [1, 2, 3, 4, 5, 6] and list(ends[6:]) == [1, 2, 3, 4, 5, 6]
+    s = np.arange(rows * n, dtype=np.float32).reshape(rows, n)
+    out = otk.topk_ascending(s, k, starts, ends)
+    assert list(out[0]) == [0, -1, -1, -1]            # t + 1 < k: padded with -1
+    assert list(out[5]) == [2, 3, 4, 5]               # largest in the window, ascending
+    _, e2 = otk.causal_windows(4, seq_q=4, row_len=8, offset=2)
+    assert list(e2) == [3, 4, 5, 6]
+
+
+def test_topk_bytes():
+    assert otk.topk_bytes(2, 4096, 256) == 75_513_856
+
+
+_score = st.one_of(st.sampled_from([0.0, -0.0, 1.0, -1.0, 2.5, math.inf, -math.inf, math.nan]),
+                   st.floats(-4, 4, width=32))
+
+
+@settings(max_examples=200, deadline=None)
+@given(st.lists(_score, min_size=1, max_size=40), st.integers(1, 45), st.data())
+def test_topk_property_bruteforce(row, k, data):
+    n = len(row)
+    start = data.draw(st.integers(0, n))
+    end = data.draw(st.integers(start, n))
+    arr = np.array([row], dtype=np.float32)
+    out = otk.topk_ascending(arr, k, np.array([start]), np.array([end]))[0]
+    assert list(out) == otk.topk_bruteforce_row(arr[0], k, start, end)
+    sel = [i for i in out if i >= 0]
+    assert sel == sorted(sel) and len(set(sel)) == len(sel)
+    assert len(sel) == min(k, end - start) and all(start <= i < end for i in sel)
+
+
+# ---------------------------------------------------------------------------
+# FP8 e4m3fn
+# ---------------------------------------------------------------------------
+def test_e4m3_decode_all_codes_vs_torch():
+    codes = torch.arange(256, dtype=torch.uint8)
+    ref = codes.view(torch.float8_e4m3fn).float()
+    for c in range(256):
+        v = of8.e4m3_value(c)
+        r = float(ref[c])
+        assert (math.isnan(v) and math.isnan(r)) or (v == r and math.copysign(1, v) == math.copysign(1, r)), c
+
+
+def test_quantize_matches_golden_and_torch_cast():
+    g = load_golden("fp8.npz")
+    x = torch.from_numpy(g["x"])
+    y, scale_inv = of8.tensorwise_quantize(x)
+    codes = y.view(torch.uint8).numpy()
+    np.testing.assert_array_equal(codes, g["codes"])
+    assert float(scale_inv) == float(g["scale_inv"])
+    # every finite code round-trips through decode / encode
+    vals = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float()
+    finite = torch.isfinite(vals)
+    back = vals[finite].to(torch.float8_e4m3fn).view(torch.uint8)
+    assert torch.equal(back, torch.arange(256, dtype=torch.uint8)[finite])
+
+
+def test_quantize_special_cases():
+    y, si = of8.tensorwise_quantize(torch.zeros(16))
+    assert float(si) == 1.0 and torch.all(y.float() == 0)
+    x = torch.tensor([1.0, float("nan"), -3.0, 0.5])
+    y, si = of8.tensorwise_quantize(x)
+    assert float(si) == pytest.approx(3.0 / 448.0, rel=1e-7)   # NaN does not enter amax
+    assert float(y[2].float()) == -448.0
+    assert torch.isnan(y[1].float())
+    back = of8.dequantize(y, si)
+    assert float(back[2]) == pytest.approx(-3.0, rel=1e-6)
+    # saturation: values beyond 448 after scaling clamp to +-448
+    assert float(torch.tensor([1e9]).clamp(-448, 448).to(torch.float8_e4m3fn).float()) == 448.0
