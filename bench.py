@@ -9,13 +9,23 @@ One step is one DSA layer on b*s = 8192 tokens:
 Inputs are synthetic, generated on the CPU with a fixed seed and resident in
 HBM before timing.  Prints one JSON line (see the fields below).
 
+The backward is three stream-ordered stages (inverse index, main kernel, dKV
+reduction); their durations come from HIP events the library records on its
+own stream during the timed steps (dsa_stage_timing).  The roofline object is
+for the single kernel with the longest median duration; its `traffic` field is
+read from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed under
+profiles/ (null when that kernel has no such summary).
+
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+                       [--calib-copy-mib N]   (one N MiB device copy before timing,
+                                               the calibration kernel of PMC runs)
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -32,22 +42,88 @@ B, S, H, D_QK, D_V, TOPK = 2, 4096, 32, 128, 64, 256
 H_IDX, D_IDX = 16, 64
 
 
+ENTRIES = B * S * TOPK                 # (token, slot) pairs of the backward (one kv group)
+KV_ROWS = B * S                        # dKV rows
+CSR_CHUNKS = (S + 15) // 16            # inverse-index chunks per batch (16 tokens each)
+
+
 def algorithmic_work():
-    """Per-launch algorithmic work of each kernel at cfg2 / cfg3."""
+    """Per-launch algorithmic work of each kernel at cfg2 / cfg3.
+
+    `flops` follow the reference's FLOP conventions (0 for pure data-movement
+    kernels); `bytes` are the HBM bytes the kernel must move by design (every
+    input read once, every output written once).  The roofline bound of a
+    kernel is the resource with the longer floor at MI355X peak."""
+    MiB = 1 << 20
+    bwd_flops = 2 * B * S * H * TOPK * (3 * D_QK + 2 * D_V)
+    q_b, kv_b, idx_b = B * S * H * D_QK * 2, B * S * D_QK * 2, ENTRIES * 4
+    o_b, lse_b = B * S * H * D_V * 2, B * S * H * 4
     return {
-        "indexer": {"bound": "mfma", "work": 2 * B * H_IDX * D_IDX * S * (S + 1) // 2, "unit": "TFLOP/s",
-                    "peak": PEAK_BF16_TFLOPS},
-        "topk": {"bound": "hbm", "work": 4 * B * S * (S + 1) // 2 + 4 * B * S * TOPK, "unit": "GB/s",
-                 "peak": PEAK_HBM_GBS},
-        "fwd": {"bound": "mfma", "work": 2 * B * S * H * TOPK * (D_QK + D_V), "unit": "TFLOP/s",
-                "peak": PEAK_BF16_TFLOPS},
-        "bwd": {"bound": "mfma", "work": 2 * B * S * H * TOPK * (3 * D_QK + 2 * D_V), "unit": "TFLOP/s",
-                "peak": PEAK_BF16_TFLOPS},
+        # q, k, w read; lower-triangle fp32 scores written
+        "indexer": {"flops": 2 * B * H_IDX * D_IDX * S * (S + 1) // 2,
+                    "bytes": B * S * H_IDX * D_IDX * 2 + B * S * D_IDX * 2 + B * S * H_IDX * 4
+                    + 4 * B * S * (S + 1) // 2},
+        # causal scores read, int32 indices written
+        "topk": {"flops": 0, "bytes": 4 * B * S * (S + 1) // 2 + 4 * B * S * TOPK},
+        # q, kv, indices read; out, lse written (the kv gather itself hits L2)
+        "fwd": {"flops": 2 * B * S * H * TOPK * (D_QK + D_V), "bytes": q_b + kv_b + idx_b + o_b + lse_b},
+        # whole backward op (three stages); the stages below split its time
+        "bwd": {"flops": bwd_flops, "bytes": None},
+        # inverse index: indices read twice (histogram, scatter), refs written once,
+        # 16-token chunk histogram written once and read three times
+        "bwd_csr": {"flops": 0, "bytes": 3 * 4 * ENTRIES + 4 * 4 * B * CSR_CHUNKS * S},
+        # every backward FLOP; reads q, kv, o, dO, indices, lse; writes dq and one fp16
+        # partial dKV row (+ int8 exponent) per (token, slot)
+        "bwd_main": {"flops": bwd_flops,
+                     "bytes": q_b + kv_b + 2 * o_b + idx_b + lse_b + q_b + ENTRIES * (2 * D_QK + 1)},
+        # partial rows + exponents + refs read once, bf16 dKV written once
+        "bwd_reduce": {"flops": 0, "bytes": ENTRIES * (2 * D_QK + 1 + 4) + 2 * KV_ROWS * D_QK},
     }
 
 
-def rate(work, seconds, unit):
-    return work / seconds / (1e12 if unit == "TFLOP/s" else 1e9)
+def roofline_entry(w, seconds):
+    """Achieved rate against the binding peak (MFMA bf16 or HBM) for one kernel."""
+    t_mfma = w["flops"] / (PEAK_BF16_TFLOPS * 1e12)
+    t_hbm = (w["bytes"] or 0) / (PEAK_HBM_GBS * 1e9)
+    if t_mfma >= t_hbm:
+        ach = w["flops"] / seconds / 1e12
+        e = {"bound": "mfma", "achieved": ach, "unit": "TFLOP/s", "peak": PEAK_BF16_TFLOPS}
+    else:
+        ach = w["bytes"] / seconds / 1e9
+        e = {"bound": "hbm", "achieved": ach, "unit": "GB/s", "peak": PEAK_HBM_GBS}
+    e["frac"] = e["achieved"] / e["peak"]
+    e["floor_us"] = {"mfma": round(t_mfma * 1e6, 2), "hbm": round(t_hbm * 1e6, 2)}
+    if w["flops"]:
+        e["tflops"] = round(w["flops"] / seconds / 1e12, 2)
+    if w["bytes"]:
+        e["gbs"] = round(w["bytes"] / seconds / 1e9, 1)
+    return e
+
+
+# rocprofv3 kernel-name prefix of each timed kernel (for the traffic summary)
+KERNEL_NAMES = {
+    "indexer": "indexer_score_kernel",
+    "topk": "topk_select_kernel",
+    "fwd": "sparse_mla_fwd_kernel",
+    "bwd_main": "sparse_mla_bwd_main_kernel",
+    "bwd_reduce": "dkv_reduce_kernel",
+}
+
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "hbm_traffic_dsa_layer_step_cfg2_cfg3.md")
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary, or None."""
+    try:
+        text = open(TRAFFIC_SUMMARY).read()
+    except OSError:
+        return None
+    m = re.search(r"```json\n(.*?)\n```", text, re.S)
+    if not m:
+        return None
+    table = json.loads(m.group(1)).get("traffic_bytes_per_launch", {})
+    v = table.get(KERNEL_NAMES.get(kernel, kernel))
+    return None if v is None else int(v)
 
 
 def main():
@@ -57,7 +133,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=4096)
+    ap.add_argument("--calib-copy-mib", type=int, default=0)
     args = ap.parse_args()
+    if args.steps > 256:
+        print("--steps must be at most 256 (the stage-timing ring holds 256 calls)", file=sys.stderr)
+        sys.exit(2)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the DSA hot path is built and "
               "measured on a single MI355X in this build.", file=sys.stderr)
@@ -78,6 +158,14 @@ def main():
     cfg3["w"] = cfg3["w"] * (H_IDX ** 0.5) / 4.0   # w ~ N(0,1)/4
     q, kv, idx, do = (cfg2[k].to(dev) for k in ("q", "kv", "indices", "do"))
     iq, ik, iw = cfg3["q"].to(dev), cfg3["k"].to(dev), cfg3["w"].to(dev)
+    if args.calib_copy_mib > 0:
+        # calibration kernel for PMC runs: reads and writes exactly N MiB once
+        src = torch.ones(args.calib_copy_mib << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     torch.cuda.synchronize()
 
     ev = {k: [] for k in ("indexer", "topk", "fwd", "bwd")}
@@ -104,15 +192,22 @@ def main():
         step(False)
     torch.cuda.synchronize()
     all_marks = []
+    _lib.stage_timing(True)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         m, _res = step(True)
         all_marks.append(m)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    _lib.stage_timing(False)
     for m in all_marks:
         for i, k in enumerate(("indexer", "topk", "fwd", "bwd")):
             ev[k].append(m[i].elapsed_time(m[i + 1]) / 1e3)
+    for k in _lib.BWD_STAGES:
+        ev["bwd_" + k] = []
+    for back in range(args.steps):
+        for k, ms in zip(_lib.BWD_STAGES, _lib.stage_times(back)):
+            ev["bwd_" + k].append(ms / 1e3)
     ms_per_step = wall / args.steps * 1e3
     tokens = B * S
     value = tokens * args.steps / wall
@@ -120,14 +215,15 @@ def main():
     work = algorithmic_work()
     kernels = {}
     for k, w in work.items():
-        t = sorted(ev[k])[len(ev[k]) // 2]
-        ach = rate(w["work"], t, w["unit"])
-        kernels[k] = {"ms": round(t * 1e3, 4), "bound": w["bound"], "achieved": round(ach, 2), "unit": w["unit"],
-                      "peak": w["peak"], "frac": round(ach / w["peak"], 4)}
-    dom = max(kernels, key=lambda k: kernels[k]["ms"])
+        t = sum(ev[k]) / len(ev[k])            # average launch duration
+        e = roofline_entry(w, t)
+        kernels[k] = {"ms": round(t * 1e3, 4), **e, "achieved": round(e["achieved"], 2),
+                      "frac": round(e["frac"], 4)}
+    singles = [k for k in kernels if k != "bwd"]          # "bwd" spans three kernels
+    dom = max(singles, key=lambda k: kernels[k]["ms"])
     roof = dict(kernels[dom])
-    roof_obj = {"kernel": dom, "bound": roof["bound"], "achieved": roof["achieved"], "peak": roof["peak"],
-                "unit": roof["unit"], "frac": roof["frac"], "traffic": None}
+    roof_obj = {"kernel": KERNEL_NAMES.get(dom, dom), "bound": roof["bound"], "achieved": roof["achieved"],
+                "peak": roof["peak"], "unit": roof["unit"], "frac": roof["frac"], "traffic": measured_traffic(dom)}
     t_idx = kernels["indexer"]["ms"] + kernels["topk"]["ms"]
     t_att = kernels["fwd"]["ms"] + kernels["bwd"]["ms"]
     amortised = 9 * tokens / ((3 * t_idx + 9 * t_att) / 1e3)

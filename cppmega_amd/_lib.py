@@ -38,6 +38,8 @@ EXPORTED_SYMBOLS = (
     "dsa_topk",
     "dsa_fp8_quantize_workspace_size",
     "dsa_fp8_tensorwise_quantize",
+    "dsa_stage_timing",
+    "dsa_stage_times",
 )
 
 _c_void_p = ctypes.c_void_p
@@ -66,6 +68,8 @@ _SIGNATURES = {
     "dsa_fp8_quantize_workspace_size": (_size_t, []),
     "dsa_fp8_tensorwise_quantize": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p,
                                            _c_void_p, _size_t, _c_void_p]),
+    "dsa_stage_timing": (_i32, [_i32]),
+    "dsa_stage_times": (_i32, [_i32, ctypes.POINTER(ctypes.c_float), _i32]),
 }
 
 _lock = threading.Lock()
@@ -126,3 +130,20 @@ def stream_ptr(device: int) -> int:
 
 def ptr(t) -> int | None:
     return None if t is None else t.data_ptr()
+
+
+BWD_STAGES = ("csr", "main", "reduce")
+
+
+def stage_timing(enable: bool) -> None:
+    """Turn per-stage HIP-event timing of dsa_sparse_mla_bwd on or off for this thread."""
+    load().dsa_stage_timing(1 if enable else 0)
+
+
+def stage_times(back: int = 0, max_stages: int = 8) -> list[float]:
+    """Elapsed ms per stage of the timed call `back` calls ago (waits for its events)."""
+    buf = (ctypes.c_float * max_stages)()
+    n = load().dsa_stage_times(int(back), buf, max_stages)
+    if n < 0:
+        check(n, "dsa_stage_times")
+    return [float(buf[i]) for i in range(n)]

@@ -41,3 +41,78 @@ extern "C" int dsa_device_check(int device) {
                           device, prop.gcnArchName);
   return DSA_OK;
 }
+
+// ---------------------------------------------------------------------------
+// Stage timing: a ring of HIP events per thread.  When enabled, each call of a
+// multi-kernel entry point takes the next ring record and marks its stage
+// boundaries on its own stream; nothing waits until dsa_stage_times() reads a
+// record back.
+// ---------------------------------------------------------------------------
+namespace dsa {
+
+constexpr int kStageRing = 256;
+constexpr int kStageMarks = 8;
+
+struct StageRecord {
+  int n = 0;
+  int device = -1;
+  hipEvent_t ev[kStageMarks] = {};
+};
+
+static thread_local bool g_stage_on = false;
+static thread_local long long g_stage_calls = 0;
+static thread_local StageRecord g_stage_ring[kStageRing];
+static thread_local StageRecord *g_stage_cur = nullptr;
+
+void stage_begin(hipStream_t st) {
+  g_stage_cur = nullptr;
+  if (!g_stage_on) return;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return;
+  StageRecord &r = g_stage_ring[g_stage_calls % kStageRing];
+  if (r.device != dev) {
+    for (int i = 0; i < kStageMarks; ++i) {
+      if (r.ev[i]) (void)hipEventDestroy(r.ev[i]);
+      r.ev[i] = nullptr;
+    }
+    for (int i = 0; i < kStageMarks; ++i)
+      if (hipEventCreate(&r.ev[i]) != hipSuccess) return;
+    r.device = dev;
+  }
+  ++g_stage_calls;
+  r.n = 0;
+  g_stage_cur = &r;
+  stage_mark(st);
+}
+
+void stage_mark(hipStream_t st) {
+  StageRecord *r = g_stage_cur;
+  if (!r || r->n >= kStageMarks) return;
+  if (hipEventRecord(r->ev[r->n], st) == hipSuccess) ++r->n;
+}
+
+}  // namespace dsa
+
+extern "C" int dsa_stage_timing(int enable) {
+  dsa::g_stage_on = enable != 0;
+  dsa::g_stage_cur = nullptr;
+  return DSA_OK;
+}
+
+extern "C" int dsa_stage_times(int back, float *ms, int max_stages) {
+  using namespace dsa;
+  DSA_REQUIRE(ms && max_stages > 0, "dsa_stage_times: null output");
+  DSA_REQUIRE(back >= 0 && back < kStageRing && back < g_stage_calls,
+              "dsa_stage_times: no timed call %d back (timed calls so far: %lld, ring %d)", back, g_stage_calls,
+              kStageRing);
+  const StageRecord &r = g_stage_ring[(g_stage_calls - 1 - back) % kStageRing];
+  DSA_REQUIRE(r.n >= 2, "dsa_stage_times: record holds %d marks", r.n);
+  hipError_t e = hipEventSynchronize(r.ev[r.n - 1]);
+  if (e != hipSuccess) return set_error(DSA_ERR_HIP, "dsa_stage_times: %s", hipGetErrorString(e));
+  const int n = r.n - 1 < max_stages ? r.n - 1 : max_stages;
+  for (int i = 0; i < n; ++i) {
+    e = hipEventElapsedTime(&ms[i], r.ev[i], r.ev[i + 1]);
+    if (e != hipSuccess) return set_error(DSA_ERR_HIP, "dsa_stage_times: %s", hipGetErrorString(e));
+  }
+  return n;
+}

@@ -181,6 +181,9 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t nblocks) {
 namespace dsa {
 int set_error(int code, const char *fmt, ...);
 int check_launch(const char *what);
+// Stage timing of multi-kernel entry points (no-ops unless dsa_stage_timing(1)).
+void stage_begin(hipStream_t st);
+void stage_mark(hipStream_t st);
 }  // namespace dsa
 
 #define DSA_REQUIRE(cond, ...)                                   \

@@ -515,8 +515,10 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
   cp.CT = L.CT;
   cp.NC = L.NC;
   cp.NQ = L.NQ;
+  stage_begin(st);
   int rc = launch_csr(cp, B, st);
   if (rc) return rc;
+  stage_mark(st);
 
   BwdParams p;
   p.q = static_cast<const unsigned char *>(q);
@@ -546,9 +548,13 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
   else if (D_qk == 192 && D_v == 128) rc = f8 ? launch_bwd_main_p<192, 128, true>(p, f32p, st) : launch_bwd_main_p<192, 128, false>(p, f32p, st);
   else rc = launch_bwd_main_p<64, 32, false>(p, f32p, st);
   if (rc) return rc;
+  stage_mark(st);
 
   uint16_t *dkv16 = static_cast<uint16_t *>(dkv);
-  if (D_qk == 128) return launch_reduce<128>(cp, p.partials, p.partial_exp, dkv16, rows, ntiles, f32p, st);
-  if (D_qk == 192) return launch_reduce<192>(cp, p.partials, p.partial_exp, dkv16, rows, ntiles, f32p, st);
-  return launch_reduce<64>(cp, p.partials, p.partial_exp, dkv16, rows, ntiles, f32p, st);
+  if (D_qk == 128) rc = launch_reduce<128>(cp, p.partials, p.partial_exp, dkv16, rows, ntiles, f32p, st);
+  else if (D_qk == 192) rc = launch_reduce<192>(cp, p.partials, p.partial_exp, dkv16, rows, ntiles, f32p, st);
+  else rc = launch_reduce<64>(cp, p.partials, p.partial_exp, dkv16, rows, ntiles, f32p, st);
+  if (rc) return rc;
+  stage_mark(st);
+  return DSA_OK;
 }

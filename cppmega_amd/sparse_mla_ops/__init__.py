@@ -7,6 +7,7 @@ imports on hosts without a GPU and fails loudly on first call there.
 from .sparse_mla import (
     SparseMLA,
     SparseMLA_FP8,
+    apply_sparse_mla_patch,
     fused_sparse_mla_absorbed_fp8,
     sparse_mla_as_unfused_dsa,
     sparse_mla_fp8_as_unfused_dsa,
@@ -19,6 +20,7 @@ from .sparse_mla_fwd_fp8 import per_token_cast_to_fp8, sparse_mla_fwd_fp8_interf
 __all__ = [
     "SparseMLA",
     "SparseMLA_FP8",
+    "apply_sparse_mla_patch",
     "fused_sparse_mla_absorbed_fp8",
     "per_token_cast_to_fp8",
     "sparse_mla_as_unfused_dsa",

@@ -206,3 +206,35 @@ def fused_sparse_mla_absorbed_fp8(query, key, topk_indices, softmax_scale, v_cha
     if not outs:
         return None
     return torch.stack(outs, dim=1).contiguous()
+
+
+_PATCH_FLAG = "__cppmega_sparse_dsa_patched__"
+
+
+def apply_sparse_mla_patch(fp8: bool | None = None, dsa_module=None) -> bool:
+    """Route Megatron DSA sparse attention through these kernels.
+
+    The reference does this inline in its launch shims
+    (scripts/remote_smoke_h200_dsa_9_4_m.sh:346-373,
+    scripts/cppmega_fp8_shim.py:3079-3085): ``dsa.unfused_dsa_fn`` becomes the
+    bf16 or FP8 adapter (chosen by CPPMEGA_DSA_FP8_ATTENTION=1 unless ``fp8``
+    is given) and ``dsa.SparseMLA`` becomes SparseMLA (or SparseMLA_FP8), which
+    Megatron's ``_fused_sparse_mla_absorbed`` calls once per batch element.
+    Returns False when the module has no ``unfused_dsa_fn`` to replace.
+    """
+    import os
+
+    if dsa_module is None:
+        from megatron.core.transformer.experimental_attention_variant import dsa as dsa_module
+    if fp8 is None:
+        fp8 = os.environ.get("CPPMEGA_DSA_FP8_ATTENTION", "0") == "1"
+    existing = getattr(dsa_module, "unfused_dsa_fn", None)
+    if existing is None:
+        return False
+    if not getattr(existing, _PATCH_FLAG, False):
+        fn = sparse_mla_fp8_as_unfused_dsa if fp8 else sparse_mla_as_unfused_dsa
+        setattr(fn, _PATCH_FLAG, True)
+        dsa_module.unfused_dsa_fn = fn
+    dsa_module.SparseMLA = SparseMLA_FP8 if fp8 else SparseMLA
+    log.info("SparseMLA %s installed into %s", "FP8" if fp8 else "BF16", getattr(dsa_module, "__name__", "dsa"))
+    return True

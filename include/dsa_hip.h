@@ -169,6 +169,20 @@ int dsa_fp8_tensorwise_quantize(const void *x, int64_t n, int in_dtype,
                                 void *workspace, size_t workspace_bytes,
                                 void *stream);
 
+/*
+ * Stage timing (measurement aid; no counterpart in the reference, which
+ * times whole calls with CUDA events in its benchmark scripts).  With
+ * dsa_stage_timing(1) on a thread, every later dsa_sparse_mla_bwd call on
+ * that thread records HIP events on its stream at its stage boundaries:
+ * stage 0 = inverse index (CSR), 1 = main kernel (dQ + dKV partial rows),
+ * 2 = dKV reduction.  Nothing synchronises until dsa_stage_times(back, ...)
+ * reads the record of the call `back` calls ago (0 = most recent, up to 255)
+ * and writes the elapsed milliseconds of its stages; it returns the number
+ * of stages written (or a negative status).
+ */
+int dsa_stage_timing(int enable);
+int dsa_stage_times(int back, float *ms, int max_stages);
+
 #ifdef __cplusplus
 }
 #endif

@@ -219,3 +219,15 @@ def test_cfg2_full_scale(dev):
                                  inp["indices"][b:b + 1, ref_tok].contiguous(), lsec[b:b + 1, ref_tok].contiguous(),
                                  inp["scale"], DV)
     assert_close(dkv.cpu()[b, rows], rdkv[0, rows], what="dkv (sampled rows)")
+    # size-independent checks over every token and row: every token has at least one
+    # valid slot (index 0), so all outputs are finite; summing dKV over all rows, the
+    # rope tail (d >= d_v) is scale * sum_{t,h} q * sum_slot dS = 0 and the V part is
+    # sum_{t,h} dO because each softmax row sums to one
+    assert torch.isfinite(out).all() and torch.isfinite(lse).all() and torch.isfinite(dq).all()
+    vmax = kv[..., :DV].float().abs().amax()
+    assert float(out.float().abs().amax()) <= float(vmax) * 1.01      # convex combinations of V rows
+    col = dkv.double().sum(dim=(0, 1, 2)).cpu()
+    expect_v = do.double().sum(dim=(0, 1, 2)).cpu()
+    scale_v = float(expect_v.norm() / DV ** 0.5)
+    assert float((col[:DV] - expect_v).abs().max()) <= 2e-2 * scale_v, "sum_j dKV_j[:d_v] != sum dO"
+    assert float(col[DV:].abs().max()) <= 2e-2 * scale_v, "sum_j dKV_j[d_v:] != 0"

@@ -3,7 +3,7 @@
 Against the FP8 oracle on identical quantised inputs the bar is the bf16 one
 (2e-2 relative / 1e-2 absolute); against the bf16 oracle on the unquantised
 inputs (cfg4-style data with 1% x20 outliers) the looser stated bound is
-checked in tests/test_oracle_fp8.py on the CPU and here on the GPU.
+checked in tests/test_oracle_sparse_mla.py on the CPU and here on the GPU.
 """
 import pytest
 import torch

@@ -99,6 +99,22 @@ def test_package_exports():
     assert cppmega_amd is not None
 
 
+def test_sparse_mla_patch_rebinds_megatron_module(monkeypatch):
+    from cppmega_amd import sparse_mla_ops as smo
+
+    def orig(*a, **k):
+        return None
+
+    mod = types.SimpleNamespace(__name__="fake_dsa", unfused_dsa_fn=orig, SparseMLA=object)
+    monkeypatch.setenv("CPPMEGA_DSA_FP8_ATTENTION", "0")
+    assert smo.apply_sparse_mla_patch(dsa_module=mod)
+    assert mod.unfused_dsa_fn is smo.sparse_mla_as_unfused_dsa and mod.SparseMLA is smo.SparseMLA
+    mod2 = types.SimpleNamespace(__name__="fake_dsa2", unfused_dsa_fn=orig, SparseMLA=object)
+    assert smo.apply_sparse_mla_patch(fp8=True, dsa_module=mod2)
+    assert mod2.unfused_dsa_fn is smo.sparse_mla_fp8_as_unfused_dsa and mod2.SparseMLA is smo.SparseMLA_FP8
+    assert not smo.apply_sparse_mla_patch(dsa_module=types.SimpleNamespace())
+
+
 # ---------------------------------------------------------------------------
 # IndexCache schedule
 # ---------------------------------------------------------------------------

@@ -202,6 +202,29 @@ def test_fp8_reduces_to_dequantised_bf16():
     assert_close(c[0], d[0], rtol=1e-6, atol=1e-6, what="out with scales")
 
 
+@pytest.mark.parametrize("outliers,bound", [(False, 0.05), (True, 0.15)])
+def test_fp8_vs_bf16_stated_bound(outliers, bound):
+    """The stated FP8 bound: relative L2 of the e4m3-tensorwise output against the
+    bf16 result on the same (unquantised) inputs."""
+    from cppmega_amd import synthetic
+    from oracle import fp8 as of8
+    B, S, H, D, DV, K = 1, 64, 16, 128, 64, 32
+    if outliers:
+        q = synthetic.outlier_values((B, S, H, D), 31).to(torch.bfloat16)
+        kv = synthetic.outlier_values((B, S, 1, D), 32).to(torch.bfloat16)
+    else:
+        g = torch.Generator().manual_seed(31)
+        q = (torch.randn((B, S, H, D), generator=g) * 0.5).to(torch.bfloat16)
+        kv = (torch.randn((B, S, 1, D), generator=g) * 0.5).to(torch.bfloat16)
+    idx = synthetic.causal_indices(B, S, K, seed=33)
+    ref, _ = osm.sparse_mla_fwd(q, kv, idx, d_v=DV)
+    q8, qsi = of8.tensorwise_quantize(q)
+    kv8, ksi = of8.tensorwise_quantize(kv)
+    out8, _ = osm.sparse_mla_fwd(q8, kv8, idx, d_v=DV, q_scale=qsi.expand(B, S), kv_scale=ksi.expand(B, S))
+    rel = float((out8 - ref).norm() / ref.norm())
+    assert rel <= bound, rel
+
+
 def test_flop_conventions():
     # cfg2 figures quoted by the reference's benchmark scripts
     assert osm.flops_fwd(2, 4096, 32, 256, 128, 64) == 25_769_803_776
