@@ -165,6 +165,16 @@ __device__ __forceinline__ i32x2 ld_global_8(const void *p) {
   return *reinterpret_cast<const i32x2 *>(p);
 }
 
+// Raw buffer access: a resource covering `num_bytes` from `base`; loads at byte
+// offsets outside it return 0 instead of touching memory (gfx9-family
+// descriptor word 3 = 0x00020000).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buffer_rsrc(const void *base, uint32_t num_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)num_bytes, 0x00020000);
+}
+__device__ __forceinline__ float buffer_load_f32(__amdgpu_buffer_rsrc_t r, int voffset, int soffset) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voffset, soffset, 0));
+}
+
 // Remap a linear block id so that consecutive logical blocks land on the
 // same XCD (blocks are dispatched round-robin over the 8 XCDs of MI355X).
 __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t nblocks) {

@@ -1,9 +1,9 @@
-// Deterministic per-row top-k on gfx950: radix select in LDS.
+// Deterministic per-row top-k on gfx950: adaptive radix select in LDS.
 //
 // Reference: the top-k of Megatron's fused_qk_topk_naive
 // (`index_scores.topk(min(topk, seqlen), dim=-1)[1]`, restated in
 // scripts/modal_dsa_indexer_bench.py:188-194) and the radix idea of
-// tilelang_sparse_mla/topk_selector.py:30-186 (histogram of key bytes, then
+// tilelang_sparse_mla/topk_selector.py:30-186 (histogram of key bits, then
 // refinement).  Unlike both, the result here is fully determined by the
 // scores: candidates are the columns [start, end) of a row, the
 // min(topk, end - start) largest are taken, equal scores prefer the lower
@@ -11,13 +11,18 @@
 // written in ascending order, padded with -1.
 //
 // One workgroup per row.  Each thread holds a contiguous chunk of the row as
-// order-preserving 32-bit keys in registers.  Up to four 8-bit radix passes
-// (LDS histogram + block suffix scan) find the key prefix of the k-th largest
-// element and how many elements equal to it are still needed; a pass stops
-// early once the selected bucket is taken whole.  Selection is then a rank
-// among equal keys by column (block prefix sum) and the chosen columns are
-// compacted in column order with a second prefix sum, which yields the
-// ascending output directly.
+// order-preserving 32-bit keys in registers.  Each round takes the key range
+// [kmin, kmax] of the elements still undecided ("members") and histograms the
+// 11 bits just below the highest bit in which kmin and kmax differ, so the
+// 2048 LDS bins split whatever range the data occupies (a fixed top byte would
+// put most real scores, which share sign and exponent, into a handful of
+// bins and serialise the LDS atomics).  A suffix scan over the bins finds the
+// bucket holding the k-th largest member: higher buckets are taken, lower
+// ones dropped.  The span shrinks by 2^11 per round, so at most three rounds
+// run before the remaining members are either few (<= kCand: ranked exactly
+// by (key desc, column asc)) or all equal (the lowest columns are taken).
+// Taken columns are compacted in column order by a block prefix sum, which
+// yields the ascending output directly.
 #include "dsa_common.hpp"
 
 namespace dsa {
@@ -64,11 +69,45 @@ __device__ __forceinline__ int block_excl_scan(int v, int *excl, int *wtot) {
   return total;
 }
 
+// Block-wide min and max of one key per thread (result in every thread).
+template <int THREADS>
+__device__ __forceinline__ void block_minmax(uint32_t &lo, uint32_t &hi, uint32_t *rmin, uint32_t *rmax) {
+  constexpr int NW = THREADS / 64;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint32_t a = (uint32_t)__shfl_xor((int)lo, off, 64);
+    const uint32_t b = (uint32_t)__shfl_xor((int)hi, off, 64);
+    lo = a < lo ? a : lo;
+    hi = b > hi ? b : hi;
+  }
+  __syncthreads();
+  if (lane_id() == 0) {
+    rmin[wave_id()] = lo;
+    rmax[wave_id()] = hi;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    lo = rmin[i] < lo ? rmin[i] : lo;
+    hi = rmax[i] > hi ? rmax[i] : hi;
+  }
+}
+
+constexpr int kBins = 2048;   // histogram bins per round (11 bits)
+constexpr int kCand = 256;    // members ranked exactly once at most this many remain
+
 template <int THREADS, int ITEMS>
 __global__ void __launch_bounds__(THREADS) topk_select_kernel(const TopkParams p) {
-  __shared__ int hist[256];
+  static_assert(ITEMS <= 32, "membership masks are 32-bit");
+  static_assert(kBins % THREADS == 0, "bins are split evenly over the threads");
+  constexpr int BPT = kBins / THREADS;
+  __shared__ int hist[kBins];
   __shared__ int wtot[THREADS / 64];
-  __shared__ int sel_digit, sel_above;
+  __shared__ uint32_t rmin[THREADS / 64], rmax[THREADS / 64];
+  __shared__ int s_bsel, s_above;
+  __shared__ uint32_t cand_key[kCand];
+  __shared__ int cand_pos[kCand];
+  __shared__ uint32_t selmask[THREADS];
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   int64_t st, en;
@@ -113,78 +152,540 @@ __global__ void __launch_bounds__(THREADS) topk_select_kernel(const TopkParams p
   int nvalid = n - c0;
   nvalid = nvalid < 0 ? 0 : (nvalid > ITEMS ? ITEMS : nvalid);
 
-  // ---- radix select: find prefix of the k-th largest key ----
-  uint32_t prefix = 0;
-  int plen = 0;  // number of determined high bits
-  int krem = p.topk;
+  uint32_t member = nvalid >= 32 ? 0xffffffffu : ((1u << nvalid) - 1u);  // undecided elements
+  uint32_t taken = 0;                                                     // selected elements
+  int r = p.topk;  // members still to take
+  int m = n;       // members left (block-uniform)
+
+  // Four rounds always suffice: three histogram rounds shrink a 32-bit span below
+  // 2^11, the next round sees single-key buckets; the exits below end it sooner.
 #pragma unroll 1
-  for (int pass = 0; pass < 4; ++pass) {
-    const int shift = 24 - 8 * pass;
-    if (tid < 256) hist[tid] = 0;
-    __syncthreads();
+  for (int round = 0; round < 5 && r > 0; ++round) {
+    uint32_t lo = 0xffffffffu, hi = 0u;
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
-      const bool match = plen == 0 || (key[i] >> (32 - plen)) == prefix;
-      if (i < nvalid && match) atomicAdd(&hist[(key[i] >> shift) & 255u], 1);
+      if ((member >> i) & 1u) {
+        lo = key[i] < lo ? key[i] : lo;
+        hi = key[i] > hi ? key[i] : hi;
+      }
     }
+    block_minmax<THREADS>(lo, hi, rmin, rmax);
+    if (lo == hi || m <= kCand || round == 4) break;  // tie or exact ranking below
+
+    const uint32_t span = hi - lo;
+    const int shift = (32 - __clz((int)span)) > 11 ? (32 - __clz((int)span)) - 11 : 0;
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) hist[tid * BPT + j] = 0;
     __syncthreads();
-    // suffix counts: thread tid (< 256) takes digit 255 - tid
-    int hv = 0;
-    if (tid < 256) hv = hist[255 - tid];
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+      if ((member >> i) & 1u) atomicAdd(&hist[(key[i] - lo) >> shift], 1);
+    __syncthreads();
+    // suffix scan: thread tid owns bins kBins-1-tid*BPT down to kBins-BPT-tid*BPT
+    int cnt[BPT];
+    int local = 0;
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+      cnt[j] = hist[kBins - 1 - (tid * BPT + j)];
+      local += cnt[j];
+    }
     int excl;
-    block_excl_scan<THREADS>(hv, &excl, wtot);
-    if (tid < 256) {
-      const int incl = excl + hv;  // keys with digit >= 255 - tid
-      if (incl >= krem && excl < krem) {
-        sel_digit = 255 - tid;
-        sel_above = excl;
+    block_excl_scan<THREADS>(local, &excl, wtot);
+    if (excl < r && excl + local >= r) {
+      int acc = excl;
+#pragma unroll
+      for (int j = 0; j < BPT; ++j) {
+        if (acc < r && acc + cnt[j] >= r) {
+          s_bsel = kBins - 1 - (tid * BPT + j);
+          s_above = acc;
+        }
+        acc += cnt[j];
       }
     }
     __syncthreads();
-    const int d = sel_digit;
-    krem -= sel_above;
-    prefix = (prefix << 8) | (uint32_t)d;
-    plen += 8;
-    const int cnt = hist[d];
-    __syncthreads();
-    if (cnt == krem) break;  // the whole bucket is selected
+    const uint32_t bsel = (uint32_t)s_bsel;
+    const int above = s_above;
+    const int inb = hist[bsel];
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      if ((member >> i) & 1u) {
+        const uint32_t b = (key[i] - lo) >> shift;
+        if (b > bsel) taken |= 1u << i;
+        if (b != bsel) member &= ~(1u << i);
+      }
+    }
+    r -= above;
+    m = inb;
+    if (r == m) {  // the whole bucket is taken
+      taken |= member;
+      member = 0;
+      r = 0;
+    }
+    __syncthreads();  // hist and s_bsel are rewritten by the next round
   }
 
-  // ---- selection: keys above the prefix, plus the first krem equal ones by column ----
-  const int sh = 32 - plen;
-  const uint32_t P = prefix;
-  int neq = 0;
+  if (r > 0) {
+    int nm = __popc(member);
+    int before;
+    block_excl_scan<THREADS>(nm, &before, wtot);
+    bool ranked = false;
+    if (m <= kCand) {
+      // exact ranking of the <= kCand members by (key desc, column asc); candidates
+      // are stored in column order, so a lower slot means a lower column
+      int slot = before;
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i)
-    if (i < nvalid && (key[i] >> sh) == P) ++neq;
-  int eq_before;
-  block_excl_scan<THREADS>(neq, &eq_before, wtot);
-  bool take[ITEMS];
-  int nsel = 0;
-  int er = eq_before;
+      for (int i = 0; i < ITEMS; ++i) {
+        if ((member >> i) & 1u) {
+          cand_key[slot] = key[i];
+          cand_pos[slot] = c0 + i;
+          ++slot;
+        }
+      }
+      selmask[tid] = 0u;
+      __syncthreads();
+      for (int c = tid; c < m; c += THREADS) {
+        const uint32_t kc = cand_key[c];
+        int rank = 0;
+        for (int j = 0; j < m; ++j) {
+          const uint32_t kj = cand_key[j];
+          rank += (kj > kc || (kj == kc && j < c)) ? 1 : 0;
+        }
+        if (rank < r) {
+          const int pos = cand_pos[c];
+          atomicOr(&selmask[pos / ITEMS], 1u << (pos % ITEMS));
+        }
+      }
+      __syncthreads();
+      taken |= selmask[tid];
+      ranked = true;
+    }
+    if (!ranked) {
+      // all members share one key: the lowest columns win
+      int k = before;
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) {
-    bool t = false;
-    if (i < nvalid) {
-      const uint32_t hi = key[i] >> sh;
-      if (hi > P) t = true;
-      else if (hi == P) {
-        t = er < krem;
-        ++er;
+      for (int i = 0; i < ITEMS; ++i) {
+        if ((member >> i) & 1u) {
+          if (k < r) taken |= 1u << i;
+          ++k;
+        }
       }
     }
-    take[i] = t;
-    nsel += t ? 1 : 0;
   }
+
+  // ---- compaction in column order ----
+  const int nsel = __popc(taken);
   int pos;
   block_excl_scan<THREADS>(nsel, &pos, wtot);
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
-    if (take[i]) {
+    if (((taken >> i) & 1u) && pos < p.topk) {  // exactly topk are taken; the bound is a guard
       orow[pos] = (int32_t)(st + c0 + i);
       ++pos;
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Wave-per-row variant for rows of at most 64 * IPL columns (no block barriers).
+// ---------------------------------------------------------------------------
+// Lane l holds columns 256c + 4l + j (c < IPL/4, j < 4) as order-preserving
+// keys: every load instruction reads 1 KiB contiguously.  The undecided
+// elements are always the keys in an interval [A, B], so no masks are kept.
+//  * Round 0 buckets the finite scores linearly in value over [min, max]
+//    (1024 LDS bins); +inf / NaN and -inf are counted apart.  Real score rows
+//    spread evenly this way, so the bucket holding the k-th largest usually has
+//    a handful of members.
+//  * Further rounds, if more than 64 members remain, histogram the 10 key bits
+//    below the highest bit in which the members' min and max keys differ (the
+//    span shrinks by 2^10 per round, so they end).
+//  * At most 64 members are ranked exactly (each lane holds one, the others are
+//    read with v_readlane), giving the k-th largest key K* and how many
+//    K*-equal elements are taken.
+// All keys > K* and the lowest-column K*-equal ones are taken; the output is
+// compacted in column order through two LDS bitmaps read back lane-blocked.
+// Wave-wide reductions and scans use DPP row operations and readlane.
+namespace wv {
+
+template <int CTRL, int ROW_MASK = 0xf, bool BOUND_ZERO = false>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, BOUND_ZERO);
+}
+__device__ __forceinline__ uint32_t readlane(uint32_t v, int l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
+}
+// every lane of each 16-lane row gets op over the row
+template <class Op>
+__device__ __forceinline__ uint32_t row_reduce(uint32_t x, Op op) {
+  x = op(x, dpp<0xB1>(x));   // quad_perm [1,0,3,2]
+  x = op(x, dpp<0x4E>(x));   // quad_perm [2,3,0,1]
+  x = op(x, dpp<0x141>(x));  // row_half_mirror
+  x = op(x, dpp<0x140>(x));  // row_mirror
+  return x;
+}
+template <class Op>
+__device__ __forceinline__ uint32_t wave_reduce(uint32_t x, Op op) {
+  x = row_reduce(x, op);
+  return op(op(readlane(x, 0), readlane(x, 16)), op(readlane(x, 32), readlane(x, 48)));
+}
+struct MinU { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a < b ? a : b; } };
+struct MaxU { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; } };
+struct AddU { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a + b; } };
+struct OrU { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a | b; } };
+struct MinF {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const {
+    return __float_as_uint(fminf(__uint_as_float(a), __uint_as_float(b)));
+  }
+};
+struct MaxF {
+  __device__ uint32_t operator()(uint32_t a, uint32_t b) const {
+    return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+  }
+};
+// inclusive prefix sum over the wave
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+  x += dpp<0x111, 0xf, true>(x);  // row_shr:1
+  x += dpp<0x112, 0xf, true>(x);  // row_shr:2
+  x += dpp<0x114, 0xf, true>(x);  // row_shr:4
+  x += dpp<0x118, 0xf, true>(x);  // row_shr:8
+  x += dpp<0x142, 0xa>(x);        // row_bcast:15 into rows 1, 3
+  x += dpp<0x143, 0xc>(x);        // row_bcast:31 into rows 2, 3
+  return x;
+}
+}  // namespace wv
+
+constexpr int kWaveBins = 1024;
+constexpr int kNoLimit = 0x7fffffff;
+constexpr int kGroup = 16;  // items per group: passes skip whole groups past the window
+
+// Score normalised for ranking: NaN -> +inf, -0 -> +0 (x + 0 is +0 for x = -0).
+// Float comparisons of normalised scores order them exactly as the keys do.
+__device__ __forceinline__ float rank_value(float f) { return (f != f ? INFINITY : f) + 0.0f; }
+
+// Make the compiler treat the row values as freshly defined, so predicates of
+// one pass are recomputed in the next instead of being kept alive as 64-bit
+// lane masks across the whole kernel (which exhausts the scalar registers).
+template <int IPL>
+__device__ __forceinline__ void fence_values(float (&x)[IPL], int &ng) {
+#pragma unroll
+  for (int i = 0; i < IPL; ++i) asm volatile("" : "+v"(x[i]));
+  asm volatile("" : "+s"(ng));
+}
+
+__device__ __forceinline__ int lane_rank(uint64_t mask) {  // set lanes below this one
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// Suffix scan of a wave's 1024-bin histogram: the bin holding the r-th largest
+// element and the count above it.
+__device__ __forceinline__ void find_bucket(const int *hist, int r, int &bsel, int &above) {
+  constexpr int BPL = kWaveBins / 64;
+  const int lane = lane_id();
+  int cnt[BPL];
+  uint32_t local = 0u;
+#pragma unroll
+  for (int q = 0; q < BPL; ++q) {
+    cnt[q] = hist[kWaveBins - 1 - (lane * BPL + q)];
+    local += (uint32_t)cnt[q];
+  }
+  const int excl = (int)(wv::wave_incl_scan(local) - local);
+  const bool cross = excl < r && excl + (int)local >= r;
+  int bsel_l = 0, above_l = 0;
+  if (cross) {
+    int acc = excl;
+#pragma unroll
+    for (int q = 0; q < BPL; ++q) {
+      if (acc < r && acc + cnt[q] >= r) {
+        bsel_l = kWaveBins - 1 - (lane * BPL + q);
+        above_l = acc;
+      }
+      acc += cnt[q];
+    }
+  }
+  const int cl = __ffsll((unsigned long long)__ballot(cross)) - 1;  // exactly one lane crosses
+  bsel = (int)wv::readlane((uint32_t)bsel_l, cl < 0 ? 0 : cl);
+  above = (int)wv::readlane((uint32_t)above_l, cl < 0 ? 0 : cl);
+}
+
+// Exact rank among <= 64 values held one per lane (lanes >= mm hold padding):
+// the r-th largest value K and how many K-equal values are taken (kNoLimit: all).
+__device__ __forceinline__ void rank_list(float v, int mm, int r, float &K, int &c_eq) {
+  const int lane = lane_id();
+  int g = 0, e = 0;
+  for (int j = 0; j < mm; ++j) {
+    const float vj = __uint_as_float(wv::readlane(__float_as_uint(v), j));
+    g += vj > v ? 1 : 0;
+    e += vj == v ? 1 : 0;
+  }
+  const bool found = lane < mm && g < r && r <= g + e;
+  const int fl = __ffsll((unsigned long long)__ballot(found)) - 1;
+  const int src = fl < 0 ? 0 : fl;
+  K = __uint_as_float(wv::readlane(__float_as_uint(v), src));
+  const int gk = (int)wv::readlane((uint32_t)g, src);
+  const int ek = (int)wv::readlane((uint32_t)e, src);
+  c_eq = (r - gk >= ek) ? kNoLimit : r - gk;
+}
+
+template <int IPL>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(IPL <= 64 ? 4 : 2)))
+topk_wave_kernel(const TopkParams p) {
+  static_assert(IPL % kGroup == 0, "items come in whole groups");
+  constexpr int NG = IPL / kGroup;
+  constexpr int BPL = kWaveBins / 64;
+  __shared__ int s_hist[4][kWaveBins];
+  __shared__ float s_list[4][64];
+  // the wave index is uniform: make the row and everything derived from it scalar
+  const int w = __builtin_amdgcn_readfirstlane(wave_id()), lane = lane_id();
+  const int64_t row = (int64_t)blockIdx.x * 4 + w;
+  if (row >= p.rows) return;
+  int *hist = s_hist[w];
+  float *list = s_list[w];
+  int64_t st, en;
+  if (p.starts) {
+    st = p.starts[row];
+    en = p.ends[row];
+  } else if (p.causal) {
+    st = 0;
+    en = (int64_t)((uint64_t)row % (uint64_t)p.seq_q) + 1 + p.causal_offset;
+  } else {
+    st = 0;
+    en = p.row_len;
+  }
+  if (st < 0) st = 0;
+  if (en > p.row_len) en = p.row_len;
+  const int n = __builtin_amdgcn_readfirstlane(en > st ? (int)(en - st) : 0);
+  int32_t *orow = p.out + row * p.topk;
+  if (n <= p.topk) {
+    for (int i = lane; i < p.topk; i += 64) orow[i] = i < n ? (int32_t)(st + i) : -1;
+    return;
+  }
+
+  // ---- load: lane l holds columns 64i + l; NaN pads columns past the window ----
+  // Buffer loads bounded to the window (out-of-range reads return 0 without
+  // touching memory); all loads of the row are in flight together.
+  const float *src = p.scores + row * p.row_stride + st;
+  const __amdgpu_buffer_rsrc_t rsrc = make_buffer_rsrc(src, (uint32_t)n * 4u);
+  int ng = (n + 64 * kGroup - 1) / (64 * kGroup);  // groups holding window columns
+  const int npad = 64 * kGroup * ng - n;          // padded elements in those groups
+  const float kPad = __uint_as_float(0x7fc00000u);
+  float x[IPL];
+#pragma unroll
+  for (int i = 0; i < IPL; ++i) x[i] = buffer_load_f32(rsrc, 4 * lane, 256 * i);
+#pragma unroll
+  for (int i = 0; i < IPL; ++i) x[i] = (64 * i + lane < n) ? rank_value(x[i]) : kPad;
+
+  int r = p.topk;  // elements still to take
+  float K = 0.0f;  // result: take x > K and the first c_eq (column order) of x == K
+  int c_eq = kNoLimit;
+  bool decided = false;
+  float vA, vB;    // member interval for the key rounds
+  int m = n;
+
+  // ---- round 0: min / max (IEEE min / max skip the NaN pads) ----
+  fence_values(x, ng);
+  float lo = INFINITY, hi = -INFINITY;
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    if (g < ng) {
+#pragma unroll
+      for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
+        lo = fminf(lo, x[i]);
+        hi = fmaxf(hi, x[i]);
+      }
+    }
+  }
+  lo = __uint_as_float(wv::wave_reduce(__float_as_uint(lo), wv::MinF()));
+  hi = __uint_as_float(wv::wave_reduce(__float_as_uint(hi), wv::MaxF()));
+  vA = lo;
+  vB = hi;
+  if (lo == hi) {
+    K = lo;
+    c_eq = r;
+    decided = true;
+  } else if (__builtin_isfinite(lo) && __builtin_isfinite(hi)) {
+    // value-linear buckets; |x| * scale < 2^20 keeps fma rounding far below a bin
+    const float scale = 1023.5f / (hi - lo);
+    const float bias = -lo * scale;
+    if (isfinite(scale) && fmaxf(fabsf(lo), fabsf(hi)) * scale < 1048576.0f) {
+#pragma unroll
+      for (int q = 0; q < BPL; ++q) hist[lane * BPL + q] = 0;
+      wave_lds_sync();
+      fence_values(x, ng);
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        if (g < ng) {
+#pragma unroll
+          for (int i = g * kGroup; i < (g + 1) * kGroup; ++i)
+            atomicAdd(&hist[(int)fmaf(x[i], scale, bias)], 1);  // NaN pads convert to bin 0
+        }
+      }
+      wave_lds_sync();
+      if (lane == 0) hist[0] -= npad;
+      wave_lds_sync();
+      int bsel, above;
+      find_bucket(hist, r, bsel, above);
+      m = hist[bsel];
+      r -= above;
+      wave_lds_sync();  // histogram reads finish before it is reused
+      fence_values(x, ng);
+      if (m <= 64) {
+        // the bucket's members to LDS (any order), then an exact rank
+        int base = 0;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          if (g < ng) {
+#pragma unroll
+            for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
+              const bool mem = x[i] == x[i] && (int)fmaf(x[i], scale, bias) == bsel;
+              const uint64_t bm = __ballot(mem);
+              if (mem) list[base + lane_rank(bm)] = x[i];
+              base += __popcll(bm);
+            }
+          }
+        }
+        wave_lds_sync();
+        rank_list(lane < m ? list[lane] : kPad, m, r, K, c_eq);
+        decided = true;
+        wave_lds_sync();
+      } else {
+        float mlo = INFINITY, mhi = -INFINITY;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          if (g < ng) {
+#pragma unroll
+            for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
+              const bool mem = x[i] == x[i] && (int)fmaf(x[i], scale, bias) == bsel;
+              mlo = mem ? fminf(mlo, x[i]) : mlo;
+              mhi = mem ? fmaxf(mhi, x[i]) : mhi;
+            }
+          }
+        }
+        vA = __uint_as_float(wv::wave_reduce(__float_as_uint(mlo), wv::MinF()));
+        vB = __uint_as_float(wv::wave_reduce(__float_as_uint(mhi), wv::MaxF()));
+        if (r == m) {  // the whole bucket is taken
+          K = vA;
+          c_eq = kNoLimit;
+          decided = true;
+        }
+      }
+    }
+  }
+
+  // ---- key rounds (infinities, extreme ranges, crowded buckets) ----
+  // members are the scores in [vA, vB]; each round histograms the 10 key bits
+  // below the highest bit in which the members' extreme keys differ, so the
+  // interval shrinks by 2^10 per round and at most four rounds run
+#pragma unroll 1
+  for (int round = 0; round < 6 && !decided; ++round) {
+    const uint32_t A = score_key(vA), B = score_key(vB);
+    if (A == B) {
+      K = vA;
+      c_eq = r;
+      decided = true;
+      break;
+    }
+    const int bl = 32 - __clz((int)(B - A));
+    const int shift = bl > 10 ? bl - 10 : 0;
+#pragma unroll
+    for (int q = 0; q < BPL; ++q) hist[lane * BPL + q] = 0;
+    wave_lds_sync();
+    fence_values(x, ng);
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if (g < ng) {
+#pragma unroll
+        for (int i = g * kGroup; i < (g + 1) * kGroup; ++i)
+          if (x[i] >= vA && x[i] <= vB) atomicAdd(&hist[(score_key(x[i]) - A) >> shift], 1);
+      }
+    }
+    wave_lds_sync();
+    int bsel, above;
+    find_bucket(hist, r, bsel, above);
+    m = hist[bsel];
+    wave_lds_sync();
+    r -= above;
+    fence_values(x, ng);
+    float mlo = INFINITY, mhi = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if (g < ng) {
+#pragma unroll
+        for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
+          const bool mem = x[i] >= vA && x[i] <= vB && ((score_key(x[i]) - A) >> shift) == (uint32_t)bsel;
+          mlo = mem ? fminf(mlo, x[i]) : mlo;
+          mhi = mem ? fmaxf(mhi, x[i]) : mhi;
+        }
+      }
+    }
+    vA = __uint_as_float(wv::wave_reduce(__float_as_uint(mlo), wv::MinF()));
+    vB = __uint_as_float(wv::wave_reduce(__float_as_uint(mhi), wv::MaxF()));
+    if (r == m) {
+      K = vA;
+      c_eq = kNoLimit;
+      decided = true;
+    } else if (m <= 64) {
+      fence_values(x, ng);
+      int base = 0;
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        if (g < ng) {
+#pragma unroll
+          for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
+            const bool mem = x[i] >= vA && x[i] <= vB;
+            const uint64_t bm = __ballot(mem);
+            if (mem) list[base + lane_rank(bm)] = x[i];
+            base += __popcll(bm);
+          }
+        }
+      }
+      wave_lds_sync();
+      rank_list(lane < m ? list[lane] : kPad, m, r, K, c_eq);
+      decided = true;
+      wave_lds_sync();
+    }
+  }
+
+  // ---- output in column order: x > K, and the first c_eq of x == K ----
+  fence_values(x, ng);
+  int pos = 0;
+  if (c_eq == kNoLimit) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if (g < ng) {
+#pragma unroll
+        for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
+          const bool t = x[i] >= K;
+          const uint64_t tm = __ballot(t);
+          const int at = pos + lane_rank(tm);
+          if (t && at < p.topk) orow[at] = (int32_t)(st + 64 * i + lane);  // exactly topk; guard
+          pos += __popcll(tm);
+        }
+      }
+    }
+  } else {
+    int eq_before = 0;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if (g < ng) {
+#pragma unroll
+        for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
+          const bool eqv = x[i] == K;
+          const uint64_t em = __ballot(eqv);
+          const bool t = x[i] > K || (eqv && eq_before + lane_rank(em) < c_eq);
+          const uint64_t tm = __ballot(t);
+          const int at = pos + lane_rank(tm);
+          if (t && at < p.topk) orow[at] = (int32_t)(st + 64 * i + lane);
+          pos += __popcll(tm);
+          eq_before += __popcll(em);
+        }
+      }
+    }
+  }
+}
+
+template <int IPL>
+static int launch_topk_wave(const TopkParams &p, hipStream_t st) {
+  hipLaunchKernelGGL((topk_wave_kernel<IPL>), dim3((unsigned)((p.rows + 3) / 4)), dim3(256), 0, st, p);
+  return check_launch("topk_select(wave)");
 }
 
 template <int THREADS, int ITEMS>
@@ -222,9 +723,9 @@ extern "C" int dsa_topk(const float *scores, int64_t rows, int64_t row_len, int6
   p.topk = (int)topk;
   p.out = out_idx;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (row_len <= 1024) return launch_topk<256, 4>(p, st);
-  if (row_len <= 4096) return launch_topk<256, 16>(p, st);
-  if (row_len <= 8192) return launch_topk<512, 16>(p, st);
+  if (row_len <= 2048) return launch_topk_wave<32>(p, st);
+  if (row_len <= 4096) return launch_topk_wave<64>(p, st);
+  if (row_len <= 8192) return launch_topk_wave<128>(p, st);
   if (row_len <= 16384) return launch_topk<1024, 16>(p, st);
   if (row_len <= 32768) return launch_topk<1024, 32>(p, st);
   return set_error(DSA_ERR_UNSUPPORTED, "dsa_topk: rows longer than 32768 columns are not supported (got %lld)",

@@ -101,6 +101,39 @@ def test_topk_bit_exact(dev, rows, n, topk, causal):
     np.testing.assert_array_equal(got.numpy(), ref)
 
 
+def _adversarial_scores(rows, n, seed):
+    """Rows that stress the adaptive radix rounds: near-equal values a few ulps
+    apart, one huge outlier squeezing the range, mostly -inf, sign-mixed tiny
+    values, many exact ties right at the k-th value."""
+    g = np.random.default_rng(seed)
+    s = g.standard_normal((rows, n)).astype(np.float32)
+    one = np.float32(1.0).view(np.int32)
+    for r in range(rows):
+        kind = r % 6
+        if kind == 0:
+            s[r] = (one + g.integers(0, 300, n)).astype(np.int32).view(np.float32)
+        elif kind == 1:
+            s[r, g.integers(0, n)] = 1e30
+        elif kind == 2:
+            s[r] = -np.inf
+            s[r, g.integers(0, n, 40)] = g.standard_normal(40)
+        elif kind == 3:
+            s[r] = (g.standard_normal(n) * 1e-38).astype(np.float32)
+        elif kind == 4:
+            s[r] = np.round(s[r] * 4) / 4
+        else:
+            s[r, : n // 2] = 7.0
+    return s
+
+
+@pytest.mark.parametrize("rows,n,topk", [(36, 4096, 256), (24, 1000, 300), (12, 20000, 2048), (18, 600, 100)])
+def test_topk_adversarial_rows(dev, rows, n, topk):
+    s = _adversarial_scores(rows, n, seed=rows * 7 + n)
+    got = topk_indices(torch.from_numpy(s).to(dev), topk, causal=False).cpu()
+    ref = otk.topk_ascending(s, topk)
+    np.testing.assert_array_equal(got.numpy(), ref)
+
+
 def test_topk_windows_and_all_equal(dev):
     rows, n, topk = 50, 700, 32
     s = np.zeros((rows, n), dtype=np.float32)          # all equal: lowest columns win
