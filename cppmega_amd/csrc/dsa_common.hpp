@@ -68,6 +68,10 @@ __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
+// 2^x by the hardware exp (v_exp_f32, ~1 ulp); results below the normal range
+// flush to zero, which softmax weights in [0, 1] rounded to bf16 do not notice.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // 2^s as a float for |s| <= 127 (exact).
 __device__ __forceinline__ float exp2i(int s) { return ldexpf(1.0f, s); }
 

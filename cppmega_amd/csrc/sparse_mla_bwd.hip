@@ -52,79 +52,88 @@ struct BwdParams {
   uint16_t *dq;
   const float *q_scale;
   const float *kv_scale;
+  const int32_t *pos_of;  // CSR position of each entry (-1: masked slot)
   unsigned char *partials;
-  int8_t *partial_exp;  // fp16 rows: power-of-two scale exponent per (entry, tile)
+  int8_t *partial_exp;  // fp16 rows: power-of-two scale exponent per (position, tile)
   int64_t B, S, S_kv, H, G, topk;
   int hpg, ntiles;
   float sl2;    // sm_scale * log2(e)
   float scale;  // sm_scale
 };
 
+// LDS of one workgroup (one (token, kv group, 32-head tile) item, WPT waves):
+//   shared  QL [head][d] bf16 (e4m3: dequantised), DOL [head][d] bf16,
+//           LD [64] = LSE (heads 0..31) and Delta * sm_scale (32..63)
+//   per wave  Kl [slot][d] raw K rows, Kd (e4m3: dequantised rows),
+//             DS [slot][head] bf16, Ksc (e4m3: row scales)
+// After the block loop the whole allocation is reused to combine the waves'
+// dQ partial sums.
 template <int D_QK, int D_V, bool FP8, bool F32P>
 struct BwdCfg {
   using Gat = GatherCfg<D_QK, D_V, FP8>;
-  static constexpr int PSZ = F32P ? 4 : 2;              // bytes per partial element
-  static constexpr int KL_BYTES = 32 * Gat::KL_STRIDE;  // raw K rows
-  static constexpr int KD_STRIDE = D_QK * 2 + 16;       // e4m3: dequantised rows (bf16)
-  static constexpr int KD_BYTES = FP8 ? 32 * KD_STRIDE : 0;
-  static constexpr int DS_STRIDE = 32 * 2 + 16;         // dS[slot][head] bf16
-  static constexpr int DS_BYTES = 32 * DS_STRIDE;
-  static constexpr int CS_STRIDE = D_QK * PSZ + 16;     // staged c rows [slot][d]
-  static constexpr int CS_BYTES = 32 * CS_STRIDE;
-  static constexpr int OFF_KD = KL_BYTES;
-  static constexpr int OFF_DS = OFF_KD + KD_BYTES;
-  static constexpr int REG_A = (OFF_DS + DS_BYTES > CS_BYTES ? OFF_DS + DS_BYTES : CS_BYTES);
-  static constexpr int QL_STRIDE = D_QK * 2 + 16;       // Q[head][d] bf16 (e4m3 dequantised)
-  static constexpr int DOL_STRIDE = D_V * 2 + 16;       // dO[head][d] bf16
-  static constexpr int OFF_QL = (REG_A + 15) / 16 * 16;
+  static constexpr int WPT = 2;                          // waves per item
+  static constexpr int PSZ = F32P ? 4 : 2;               // bytes per partial element
+  static constexpr int QL_STRIDE = D_QK * 2 + 32;        // 32-byte pads: conflict-free transposed reads
+  static constexpr int DOL_STRIDE = D_V * 2 + 32;
+  static constexpr int OFF_QL = 0;
   static constexpr int OFF_DOL = OFF_QL + 32 * QL_STRIDE;
-  static constexpr int OFF_SC = OFF_DOL + 32 * DOL_STRIDE;
-  static constexpr int OFF_LD = OFF_SC + (FP8 ? 32 * 4 : 0);
-  static constexpr int WAVE_BYTES = (OFF_LD + 64 * 4 + 15) / 16 * 16;
-  static constexpr int WAVES = 4 * WAVE_BYTES <= 160 * 1024 ? 4 : (2 * WAVE_BYTES <= 160 * 1024 ? 2 : 1);
+  static constexpr int OFF_LD = OFF_DOL + 32 * DOL_STRIDE;
+  static constexpr int SHARED_BYTES = (OFF_LD + 64 * 4 + 15) / 16 * 16;
+  static constexpr int KL_BYTES = 32 * Gat::KL_STRIDE;
+  static constexpr int KD_STRIDE = D_QK * 2 + 32;        // e4m3: dequantised rows (bf16)
+  static constexpr int KD_BYTES = FP8 ? 32 * KD_STRIDE : 0;
+  static constexpr int DS_STRIDE = 32 * 2 + 32;          // dS[slot][head] bf16
+  static constexpr int DS_BYTES = 32 * DS_STRIDE;
+  static constexpr int CS_STRIDE = D_QK * 2 + 32;        // staged fp16 partial rows (over Kl, Kd)
+  static constexpr int ROW_CHUNKS = D_QK * 2 / 16;       // 16-byte chunks per fp16 partial row
+  static_assert((32 * ROW_CHUNKS) % 64 == 0, "whole store rounds");
+  static constexpr int W_KD = KL_BYTES;
+  static constexpr int W_DS = W_KD + KD_BYTES;
+  static_assert(32 * CS_STRIDE <= W_DS, "staged rows fit the K tiles");
+  static constexpr int W_SC = W_DS + DS_BYTES;
+  static constexpr int WAVE_BYTES = (W_SC + (FP8 ? 32 * 4 : 0) + 15) / 16 * 16;
+  static constexpr int DQ_PART_BYTES = 32 * D_QK * 4;    // one wave's fp32 dQ tile
+  static constexpr int LOOP_BYTES = SHARED_BYTES + WPT * WAVE_BYTES;
+  static constexpr int COMBINE_BYTES = (WPT - 1) * DQ_PART_BYTES;
+  static constexpr int LDS_BYTES = LOOP_BYTES > COMBINE_BYTES ? LOOP_BYTES : COMBINE_BYTES;
   static constexpr int DQT = D_QK / 32;
   static constexpr int DVT = D_V / 32;
   static constexpr int KSTEPS = D_QK / 16;
   static constexpr int VSTEPS = D_V / 16;
-  static constexpr int ROW_CHUNKS = D_QK * PSZ / 16;    // 16-byte chunks per partial row
   // bf16 source of K / V rows for the dP / dQ GEMMs
   static constexpr int K_STRIDE = FP8 ? KD_STRIDE : Gat::KL_STRIDE;
   static_assert(D_V % 32 == 0 && D_QK % 32 == 0 && D_V <= D_QK, "unsupported head dims");
 };
 
 template <int D_QK, int D_V, bool FP8, bool F32P>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(D_QK <= 128 ? 2 : 1)))
 sparse_mla_bwd_main_kernel(const BwdParams p) {
   using C = BwdCfg<D_QK, D_V, FP8, F32P>;
+  static_assert(C::WPT == 2, "launch bounds assume two waves per workgroup");
   using Gat = typename C::Gat;
-  typedef typename std::conditional<FP8, long, bf16x8>::type qop_t;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
-  const int lane = lane_id(), w = wave_id();
+  const int lane = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
   const int g32 = lane >> 5, l32 = lane & 31;
-  const int64_t nitems = p.B * p.S * p.G * p.ntiles;
-  const int64_t item = xcd_remap(blockIdx.x, gridDim.x) * C::WAVES + w;
-  if (item >= nitems) return;  // waves are independent
+  const int64_t item = xcd_remap(blockIdx.x, gridDim.x);
   const int tile = (int)(item % p.ntiles);
   int64_t rest = item / p.ntiles;
   const int64_t g = rest % p.G;
   const int64_t tok = rest / p.G;
   const int64_t b = tok / p.S;
 
-  unsigned char *wsm = smem + w * C::WAVE_BYTES;
+  unsigned char *QL = smem + C::OFF_QL;
+  unsigned char *DOL = smem + C::OFF_DOL;
+  float *LD = reinterpret_cast<float *>(smem + C::OFF_LD);
+  unsigned char *wsm = smem + C::SHARED_BYTES + w * C::WAVE_BYTES;
   unsigned char *Kl = wsm;
-  unsigned char *Kd = wsm + C::OFF_KD;
-  unsigned char *DS = wsm + C::OFF_DS;
-  unsigned char *Cs = wsm;  // aliases Kl / Kd / DS once a block's GEMMs are done
-  unsigned char *QL = wsm + C::OFF_QL;
-  unsigned char *DOL = wsm + C::OFF_DOL;
-  float *Ksc = reinterpret_cast<float *>(wsm + C::OFF_SC);
-  float *LD = reinterpret_cast<float *>(wsm + C::OFF_LD);
+  unsigned char *Kd = wsm + C::W_KD;
+  unsigned char *DS = wsm + C::W_DS;
+  float *Ksc = reinterpret_cast<float *>(wsm + C::W_SC);
   const unsigned char *Ksrc = FP8 ? Kd : Kl;
 
-  const int h_local = tile * 32 + l32;  // head of this lane in the A-operand role
-  const bool head_ok = h_local < p.hpg;
-  const int64_t qrow = tok * p.H + g * p.hpg + h_local;
+  const int64_t head0 = tok * p.H + g * p.hpg + tile * 32;  // q row of head 0 of this tile
+  const int nheads = p.hpg - tile * 32 < 32 ? p.hpg - tile * 32 : 32;
   const int64_t entry0 = (tok * p.G + g) * p.topk;  // entry (CSR key) of slot 0
   const int32_t *idx_row = p.idx + entry0;
   const unsigned char *kv_b = p.kv + ((b * p.S_kv) * p.G + g) * Gat::ROWB;
@@ -132,74 +141,94 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
   const uint32_t row_pitch = (uint32_t)(p.G * Gat::ROWB);
   const int nblk = (int)((p.topk + 31) / 32);
 
-  int idx_cur = load_slot_index(idx_row, 0, l32, p.topk, p.S_kv);
-  int idx_nxt = load_slot_index(idx_row, 1, l32, p.topk, p.S_kv);
+  // this wave's blocks: w, w + WPT, ...; start the first gather before the prologue
+  int blk = w;
+  int idx_cur = load_slot_index(idx_row, blk, l32, p.topk, p.S_kv);
+  int idx_nxt = load_slot_index(idx_row, blk + C::WPT, l32, p.topk, p.S_kv);
   typename Gat::Regs rg;
-  gather_issue<Gat>(rg, kv_b, kv_scale_b, idx_cur, row_pitch);
+  if (blk < nblk) gather_issue<Gat>(rg, kv_b, kv_scale_b, idx_cur, row_pitch);
 
-  float qsc = 1.0f;
-  if constexpr (FP8) qsc = p.q_scale[tok];
-
-  // ---------------- prologue: Q, dO (A operands), Delta, LSE, row-major Q / dO tiles ----------------
-  qop_t qA[C::KSTEPS];
-  bf16x8 doA[C::VSTEPS];
-  float delta_part = 0.0f;
+  // ---------------- prologue (all waves): Q, dO tiles, Delta, LSE ----------------
+  {
+    const int t = threadIdx.x;
+    constexpr int NT = 64 * C::WPT;
+    float qsc = 1.0f;
+    if constexpr (FP8) qsc = p.q_scale[tok];
+    // Q rows: 32 heads x D_QK / 8 chunks of 8 elements
+    constexpr int QCH = D_QK / 8;
+    for (int u = t; u < 32 * QCH; u += NT) {
+      const int h = u / QCH, c = u % QCH;
+      i32x4 v = {0, 0, 0, 0};
+      if (h < nheads) {
+        if constexpr (FP8) {
+          const long raw = *reinterpret_cast<const long *>(p.q + (head0 + h) * D_QK + 8 * c);
+          uint32_t wq[4];
 #pragma unroll
-  for (int k = 0; k < C::KSTEPS; ++k) {
-    if constexpr (FP8) {
-      const long v = head_ok ? *reinterpret_cast<const long *>(p.q + qrow * D_QK + 16 * k + 8 * g32) : 0l;
-      qA[k] = v;
-      uint32_t wq[4];
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t c0 = (uint32_t)((unsigned long)raw >> (16 * e)) & 0xffu;
+            const uint32_t c1 = (uint32_t)((unsigned long)raw >> (16 * e + 8)) & 0xffu;
+            wq[e] = pack_bf16x2(e4m3_to_f32(c0) * qsc, e4m3_to_f32(c1) * qsc);
+          }
+          v = i32x4{(int)wq[0], (int)wq[1], (int)wq[2], (int)wq[3]};
+        } else {
+          v = ld_global_16(p.q + ((head0 + h) * D_QK + 8 * c) * 2);
+        }
+      }
+      *reinterpret_cast<i32x4 *>(QL + h * C::QL_STRIDE + c * 16) = v;
+    }
+    // dO rows and Delta = sum_d O dO (8 consecutive threads share a head)
+    constexpr int VCH = D_V / 8;
+    static_assert(VCH <= 16 && (VCH & (VCH - 1)) == 0, "d_v chunks per head: power of two <= 16");
+    for (int u0 = 0; u0 < 32 * VCH; u0 += NT) {
+      const int u = u0 + t;
+      const int h = u / VCH, c = u % VCH;
+      i32x4 dv = {0, 0, 0, 0}, ov = {0, 0, 0, 0};
+      if (u < 32 * VCH && h < nheads) {
+        dv = ld_global_16(p.dO + (head0 + h) * D_V + 8 * c);
+        ov = ld_global_16(p.o + (head0 + h) * D_V + 8 * c);
+      }
+      if (u < 32 * VCH) *reinterpret_cast<i32x4 *>(DOL + h * C::DOL_STRIDE + c * 16) = dv;
+      float part = 0.0f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t c0 = (uint32_t)((unsigned long)v >> (16 * e)) & 0xffu;
-        const uint32_t c1 = (uint32_t)((unsigned long)v >> (16 * e + 8)) & 0xffu;
-        wq[e] = pack_bf16x2(e4m3_to_f32(c0) * qsc, e4m3_to_f32(c1) * qsc);
+        const uint32_t du = (uint32_t)dv[e], ou = (uint32_t)ov[e];
+        part += bf16_bits_to_f32(ou & 0xffffu) * bf16_bits_to_f32(du & 0xffffu);
+        part += bf16_bits_to_f32(ou >> 16) * bf16_bits_to_f32(du >> 16);
       }
-      *reinterpret_cast<i32x4 *>(QL + l32 * C::QL_STRIDE + (16 * k + 8 * g32) * 2) =
-          i32x4{(int)wq[0], (int)wq[1], (int)wq[2], (int)wq[3]};
-    } else {
-      i32x4 v = {0, 0, 0, 0};
-      if (head_ok) v = ld_global_16(p.q + (qrow * D_QK + 16 * k + 8 * g32) * 2);
-      qA[k] = as_bf16x8(v);
-      *reinterpret_cast<i32x4 *>(QL + l32 * C::QL_STRIDE + (16 * k + 8 * g32) * 2) = v;
-    }
-  }
 #pragma unroll
-  for (int k = 0; k < C::VSTEPS; ++k) {
-    i32x4 dv = {0, 0, 0, 0}, ov = {0, 0, 0, 0};
-    if (head_ok) {
-      dv = ld_global_16(p.dO + qrow * D_V + 16 * k + 8 * g32);
-      ov = ld_global_16(p.o + qrow * D_V + 16 * k + 8 * g32);
+      for (int off = 1; off < VCH; off <<= 1) part += __shfl_xor(part, off, 64);
+      if (u < 32 * VCH && c == 0) {
+        float dl = part;
+        if (p.delta != nullptr && h < nheads) dl = p.delta[head0 + h];
+        LD[32 + h] = dl * p.scale;
+      }
     }
-    doA[k] = as_bf16x8(dv);
-    *reinterpret_cast<i32x4 *>(DOL + l32 * C::DOL_STRIDE + (16 * k + 8 * g32) * 2) = dv;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t du = (uint32_t)dv[e], ou = (uint32_t)ov[e];
-      delta_part += bf16_bits_to_f32(ou & 0xffffu) * bf16_bits_to_f32(du & 0xffffu);
-      delta_part += bf16_bits_to_f32(ou >> 16) * bf16_bits_to_f32(du >> 16);
+    if (t < 32) {
+      float lse_h = INFINITY;  // padded heads: P = exp2(x - inf) = 0
+      if (t < nheads) {
+        const float l = p.lse[head0 + t];
+        lse_h = (l == -INFINITY) ? INFINITY : l;  // all-masked row: zero gradient
+      }
+      LD[t] = lse_h;
     }
   }
-  float delta_h = delta_part + xor32(delta_part);
-  if (p.delta != nullptr && head_ok) delta_h = p.delta[qrow];
-  float lse_h = INFINITY;  // padded heads: P = exp2(x - inf) = 0
-  if (head_ok) {
-    const float l = p.lse[qrow];
-    lse_h = (l == -INFINITY) ? INFINITY : l;  // all-masked row: zero gradient
-  }
-  if (g32 == 0) {
-    LD[l32] = lse_h;
-    LD[32 + l32] = delta_h;
-  }
+  __syncthreads();
 
+  float qsc = 1.0f;
+  long qA8[FP8 ? C::KSTEPS : 1];  // e4m3: raw Q codes as the S A operand (head l32)
+  if constexpr (FP8) {
+    qsc = p.q_scale[tok];
+#pragma unroll
+    for (int k = 0; k < C::KSTEPS; ++k)
+      qA8[k] = l32 < nheads ? *reinterpret_cast<const long *>(p.q + (head0 + l32) * D_QK + 16 * k + 8 * g32) : 0l;
+  }
   f32x16 dqacc[C::DQT];
 #pragma unroll
   for (int t = 0; t < C::DQT; ++t)
 #pragma unroll
     for (int a = 0; a < 16; ++a) dqacc[t][a] = 0.0f;
 
-  for (int blk = 0; blk < nblk; ++blk) {
+  for (; blk < nblk; blk += C::WPT) {
     const int slot0 = blk * 32;
     // ---- stage block: K rows (+ e4m3: dequantised rows, scales) ----
     gather_store_k<Gat>(rg, Kl);
@@ -208,12 +237,14 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
       gather_store_scale<Gat>(rg, Ksc);
     }
     const bool valid = idx_cur >= 0;  // slot slot0 + l32
-    const uint64_t vmask = __ballot(valid);
+    int32_t pos = -1;
+    if (valid) pos = p.pos_of[entry0 + slot0 + l32];
+    const bool wr = valid && pos >= 0;  // (pos is always set for a valid slot; the test is a guard)
     wave_lds_sync();
-    const int idx_nn = load_slot_index(idx_row, blk + 2, l32, p.topk, p.S_kv);
-    if (blk + 1 < nblk) gather_issue<Gat>(rg, kv_b, kv_scale_b, idx_nxt, row_pitch);
+    const int idx_nn = load_slot_index(idx_row, blk + 2 * C::WPT, l32, p.topk, p.S_kv);
+    if (blk + C::WPT < nblk) gather_issue<Gat>(rg, kv_b, kv_scale_b, idx_nxt, row_pitch);
 
-    // ---- S = Q K^T and dP = dO V^T  (M = head, N = slot) ----
+    // ---- S = Q K^T and dP = dO V^T  (M = head, N = slot; Q / dO rows from LDS) ----
     f32x16 sacc, dpacc;
 #pragma unroll
     for (int a = 0; a < 16; ++a) {
@@ -224,16 +255,18 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
     for (int k = 0; k < C::KSTEPS; ++k) {
       if constexpr (FP8) {
         const long kb = *reinterpret_cast<const long *>(Kl + l32 * Gat::KL_STRIDE + 16 * k + 8 * g32);
-        sacc = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(qA[k], kb, sacc, 0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(qA8[k], kb, sacc, 0, 0, 0);
       } else {
+        const i32x4 qa = *reinterpret_cast<const i32x4 *>(QL + l32 * C::QL_STRIDE + (16 * k + 8 * g32) * 2);
         const i32x4 kb = *reinterpret_cast<const i32x4 *>(Kl + l32 * Gat::KL_STRIDE + (16 * k + 8 * g32) * 2);
-        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qA[k], as_bf16x8(kb), sacc, 0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(qa), as_bf16x8(kb), sacc, 0, 0, 0);
       }
     }
 #pragma unroll
     for (int k = 0; k < C::VSTEPS; ++k) {
+      const i32x4 da = *reinterpret_cast<const i32x4 *>(DOL + l32 * C::DOL_STRIDE + (16 * k + 8 * g32) * 2);
       const i32x4 vb = *reinterpret_cast<const i32x4 *>(Ksrc + l32 * C::K_STRIDE + (16 * k + 8 * g32) * 2);
-      dpacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(doA[k], as_bf16x8(vb), dpacc, 0, 0, 0);
+      dpacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(da), as_bf16x8(vb), dpacc, 0, 0, 0);
     }
 
     // ---- P, dS  (lane = slot slot0 + l32, heads 8i + 4*g32 + j) ----
@@ -250,9 +283,9 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int a = 4 * i + j;
-          const float pv = valid ? exp2f(sacc[a] * xs - l4[j]) : 0.0f;
+          const float pv = valid ? exp2_fast(sacc[a] * xs - l4[j]) : 0.0f;
           P[j] = pv;
-          dS[j] = pv * (dpacc[a] - d4[j]) * p.scale;
+          dS[j] = pv * fmaf(dpacc[a], p.scale, -d4[j]);  // P (dP - Delta) scale
         }
         dsw[2 * i] = pack_bf16x2(dS[0], dS[1]);
         dsw[2 * i + 1] = pack_bf16x2(dS[2], dS[3]);
@@ -300,82 +333,99 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
         }
       }
     }
-    // Row scale for the fp16 form: the slot's row max |c| (this lane and its
-    // cross-half partner hold the whole row) sets a power of two that maps it
-    // into [2^13, 2^14); scaling by a power of two is exact.
-    float rscale = 1.0f;
-    int pexp = 0;
-    if constexpr (!F32P) {
+
+    // ---- the slot's partial row, written at its CSR position ----
+    // lane: slot l32, d = dt*32 + 8i + 4*g32 + j.
+    if constexpr (F32P) {
+      // fp32 rows: the two lanes of a slot store adjacent 16-byte pieces
+      unsigned char *dst = p.partials + ((int64_t)(wr ? pos : 0) * p.ntiles + tile) * (int64_t)(D_QK * 4);
+#pragma unroll
+      for (int dt = 0; dt < C::DQT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d0 = dt * 32 + 8 * i + 4 * g32;
+          if (wr)
+            *reinterpret_cast<f32x4 *>(dst + d0 * 4) =
+                f32x4{cacc[dt][4 * i], cacc[dt][4 * i + 1], cacc[dt][4 * i + 2], cacc[dt][4 * i + 3]};
+        }
+    } else {
+      // fp16 rows scaled by a power of two mapping the row max into [2^13, 2^14)
+      // (exact to undo), staged in LDS (over the consumed K tile) and written
+      // as whole rows: 16 lanes store one row's 256 contiguous bytes
       float amax = 0.0f;
 #pragma unroll
       for (int dt = 0; dt < C::DQT; ++dt)
 #pragma unroll
         for (int a = 0; a < 16; ++a) amax = fmaxf(amax, fabsf(cacc[dt][a]));
       amax = fmaxf(amax, xor32(amax));
-      pexp = partial_row_exponent(amax);
-      rscale = exp2i(pexp);
-    }
-    wave_lds_sync();  // K / dS tiles are consumed: Cs may overwrite them
-    // lane: slot l32, d = dt*32 + 8i + 4*g32 + j  ->  Cs[slot][d]
-    {
-      unsigned char *crow = Cs + l32 * C::CS_STRIDE;
+      const int pexp = partial_row_exponent(amax);
+      const float rscale = exp2i(pexp);
+      wave_lds_sync();  // the dQ GEMM's reads of the K / dS tiles are complete
+      unsigned char *Cs = Kl;  // spans Kl (and Kd for e4m3)
+      int *Lpos = reinterpret_cast<int *>(DS);
 #pragma unroll
       for (int dt = 0; dt < C::DQT; ++dt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int d0 = dt * 32 + 8 * i + 4 * g32;
-          if constexpr (F32P) {
-            *reinterpret_cast<f32x4 *>(crow + d0 * 4) =
-                f32x4{cacc[dt][4 * i], cacc[dt][4 * i + 1], cacc[dt][4 * i + 2], cacc[dt][4 * i + 3]};
-          } else {
-            *reinterpret_cast<i32x2 *>(crow + d0 * 2) =
-                i32x2{(int)pack_f16x2(cacc[dt][4 * i] * rscale, cacc[dt][4 * i + 1] * rscale),
-                      (int)pack_f16x2(cacc[dt][4 * i + 2] * rscale, cacc[dt][4 * i + 3] * rscale)};
-          }
+          *reinterpret_cast<i32x2 *>(Cs + l32 * C::CS_STRIDE + d0 * 2) =
+              i32x2{(int)pack_f16x2(cacc[dt][4 * i] * rscale, cacc[dt][4 * i + 1] * rscale),
+                    (int)pack_f16x2(cacc[dt][4 * i + 2] * rscale, cacc[dt][4 * i + 3] * rscale)};
         }
-    }
-    if constexpr (!F32P) {
-      if (g32 == 0 && valid) p.partial_exp[(entry0 + slot0 + l32) * p.ntiles + tile] = (int8_t)pexp;
-    }
-    wave_lds_sync();
-    // ---- coalesced partial rows: partials[(entry * ntiles + tile)][d] ----
-    constexpr int TOTAL = 32 * C::ROW_CHUNKS;
-    unsigned char *pbase = p.partials + ((entry0 + slot0) * p.ntiles + tile) * (int64_t)(D_QK * C::PSZ);
-    const int64_t prow_pitch = (int64_t)p.ntiles * D_QK * C::PSZ;
+      if (g32 == 0) Lpos[l32] = wr ? pos : -1;
+      if (g32 == 0 && wr) p.partial_exp[(int64_t)pos * p.ntiles + tile] = (int8_t)pexp;
+      wave_lds_sync();
 #pragma unroll
-    for (int it = 0; it < (TOTAL + 63) / 64; ++it) {
-      const int u = it * 64 + lane;
-      if (u < TOTAL) {
+      for (int it = 0; it < 32 * C::ROW_CHUNKS / 64; ++it) {
+        const int u = it * 64 + lane;
         const int row = u / C::ROW_CHUNKS, ch = u % C::ROW_CHUNKS;
-        if ((vmask >> row) & 1ull) {
-          const i32x4 v = *reinterpret_cast<const i32x4 *>(Cs + row * C::CS_STRIDE + ch * 16);
-          *reinterpret_cast<i32x4 *>(pbase + row * prow_pitch + ch * 16) = v;
-        }
+        const int ps = Lpos[row];
+        const i32x4 v = *reinterpret_cast<const i32x4 *>(Cs + row * C::CS_STRIDE + ch * 16);
+        if (ps >= 0)
+          *reinterpret_cast<i32x4 *>(p.partials + ((int64_t)ps * p.ntiles + tile) * (D_QK * 2) + ch * 16) = v;
       }
     }
-    wave_lds_sync();  // Cs is overwritten by the next block's gather
+    wave_lds_sync();  // K / dS tiles are consumed before the next block's gather lands
     idx_cur = idx_nxt;
     idx_nxt = idx_nn;
   }
 
-  // ---- dQ: lane = head l32, d = dt*32 + 8i + 4*g32 + j ----
-  if (head_ok) {
-    uint16_t *drow = p.dq + qrow * D_QK;
+  // ---- combine the waves' dQ partial sums in wave order, then write dQ ----
+  __syncthreads();  // every wave is done with the loop's LDS
+  float *dqp = reinterpret_cast<float *>(smem);
+  if (w > 0) {
 #pragma unroll
     for (int dt = 0; dt < C::DQT; ++dt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const i32x2 pk = {(int)pack_bf16x2(dqacc[dt][4 * i], dqacc[dt][4 * i + 1]),
-                          (int)pack_bf16x2(dqacc[dt][4 * i + 2], dqacc[dt][4 * i + 3])};
-        *reinterpret_cast<i32x2 *>(drow + dt * 32 + 8 * i + 4 * g32) = pk;
-      }
+      for (int a = 0; a < 16; ++a) dqp[((w - 1) * C::DQT * 16 + dt * 16 + a) * 64 + lane] = dqacc[dt][a];
+  }
+  __syncthreads();
+  if (w == 0) {
+#pragma unroll 1
+    for (int v = 1; v < C::WPT; ++v)
+#pragma unroll
+      for (int dt = 0; dt < C::DQT; ++dt)
+#pragma unroll
+        for (int a = 0; a < 16; ++a) dqacc[dt][a] += dqp[((v - 1) * C::DQT * 16 + dt * 16 + a) * 64 + lane];
+    // lane = head l32, d = dt*32 + 8i + 4*g32 + j
+    if (l32 < nheads) {
+      uint16_t *drow = p.dq + (head0 + l32) * D_QK;
+#pragma unroll
+      for (int dt = 0; dt < C::DQT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const i32x2 pk = {(int)pack_bf16x2(dqacc[dt][4 * i], dqacc[dt][4 * i + 1]),
+                            (int)pack_bf16x2(dqacc[dt][4 * i + 2], dqacc[dt][4 * i + 3])};
+          *reinterpret_cast<i32x2 *>(drow + dt * 32 + 8 * i + 4 * g32) = pk;
+        }
+    }
   }
 }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct BwdWorkspace {
-  size_t partials, pexp, hist, gsum, tot, rowptr, refs, total;
+  size_t partials, pexp, hist, gsum, tot, rowptr, pos_of, total;
   int CT, NC, NQ;
 };
 
@@ -401,7 +451,7 @@ static BwdWorkspace bwd_layout(int64_t B, int64_t S, int64_t S_kv, int64_t H, in
   off += align256((size_t)B * R * 4);
   L.rowptr = off;
   off += align256(((size_t)B * R + 1) * 4);
-  L.refs = off;
+  L.pos_of = off;
   off += align256(entries * 4);
   L.total = off;
   return L;
@@ -410,17 +460,17 @@ static BwdWorkspace bwd_layout(int64_t B, int64_t S, int64_t S_kv, int64_t H, in
 template <int D_QK, int D_V, bool FP8, bool F32P>
 static int launch_bwd_main(const BwdParams &p, hipStream_t st) {
   using C = BwdCfg<D_QK, D_V, FP8, F32P>;
-  const size_t lds = C::WAVES * (size_t)C::WAVE_BYTES;
+  const size_t lds = C::LDS_BYTES;
+  if (lds > 160 * 1024) return set_error(DSA_ERR_UNSUPPORTED, "sparse_mla_bwd: needs %zu bytes of LDS", lds);
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute((const void *)sparse_mla_bwd_main_kernel<D_QK, D_V, FP8, F32P>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return set_error(DSA_ERR_HIP, "sparse_mla_bwd: LDS attribute: %s", hipGetErrorString(e));
   }
-  const int64_t nitems = p.B * p.S * p.G * p.ntiles;
-  const int64_t nblocks = (nitems + C::WAVES - 1) / C::WAVES;
-  if (nblocks >= (1ll << 31)) return set_error(DSA_ERR_INVALID_ARG, "sparse_mla_bwd: grid too large");
-  hipLaunchKernelGGL((sparse_mla_bwd_main_kernel<D_QK, D_V, FP8, F32P>), dim3((unsigned)nblocks),
-                     dim3(64 * C::WAVES), lds, st, p);
+  const int64_t nitems = p.B * p.S * p.G * p.ntiles;  // one workgroup per item
+  if (nitems >= (1ll << 31)) return set_error(DSA_ERR_INVALID_ARG, "sparse_mla_bwd: grid too large");
+  hipLaunchKernelGGL((sparse_mla_bwd_main_kernel<D_QK, D_V, FP8, F32P>), dim3((unsigned)nitems),
+                     dim3(64 * C::WPT), lds, st, p);
   return check_launch("sparse_mla_bwd_main");
 }
 
@@ -434,11 +484,11 @@ static int launch_reduce(const CsrParams &cp, const unsigned char *partials, con
                          int64_t rows, int ntiles, bool f32p, hipStream_t st) {
   const unsigned grid = (unsigned)rows;  // one workgroup per kv row
   if (f32p)
-    hipLaunchKernelGGL((dkv_reduce_kernel<D_QK, true>), dim3(grid), dim3(256), 0, st, cp.rowptr, cp.refs, partials,
-                       pexp, dkv, rows, ntiles);
+    hipLaunchKernelGGL((dkv_reduce_kernel<D_QK, true>), dim3(grid), dim3(256), 0, st, cp.rowptr, partials, pexp,
+                       dkv, rows, ntiles);
   else
-    hipLaunchKernelGGL((dkv_reduce_kernel<D_QK, false>), dim3(grid), dim3(256), 0, st, cp.rowptr, cp.refs, partials,
-                       pexp, dkv, rows, ntiles);
+    hipLaunchKernelGGL((dkv_reduce_kernel<D_QK, false>), dim3(grid), dim3(256), 0, st, cp.rowptr, partials, pexp,
+                       dkv, rows, ntiles);
   return check_launch("sparse_mla_bwd(reduce)");
 }
 
@@ -505,7 +555,7 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
   cp.hist = reinterpret_cast<int32_t *>(ws + L.hist);
   cp.tot = reinterpret_cast<int32_t *>(ws + L.tot);
   cp.rowptr = reinterpret_cast<int32_t *>(ws + L.rowptr);
-  cp.refs = reinterpret_cast<int32_t *>(ws + L.refs);
+  cp.pos_of = reinterpret_cast<int32_t *>(ws + L.pos_of);
   cp.S = S;
   cp.S_kv = S_kv;
   cp.G = G;
@@ -531,6 +581,7 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
   p.dq = static_cast<uint16_t *>(dq);
   p.q_scale = q_scale;
   p.kv_scale = kv_scale;
+  p.pos_of = cp.pos_of;
   p.partials = ws + L.partials;
   p.partial_exp = reinterpret_cast<int8_t *>(ws + L.pexp);
   p.B = B;

@@ -17,7 +17,7 @@ namespace dsa {
 //   csr_rows     tot[b*R + r]   = row total; gsum -> exclusive prefix over groups
 //   csr_scan     rowptr         = exclusive prefix of tot
 //   csr_bases    hist[b][c][r] <- rowptr + entries of row r in earlier chunks
-//   csr_scatter  refs[...]      = entries placed token by token (stable)
+//   csr_scatter  pos_of[e]      = CSR position of entry e, tokens in order (stable)
 // Every thread touches at most CG chunks, so no kernel walks a long serial
 // chain of global loads.
 
@@ -29,7 +29,7 @@ struct CsrParams {
   int32_t *gsum;    // [B][NQ][R]
   int32_t *tot;     // [B*R]
   int32_t *rowptr;  // [B*R + 1]
-  int32_t *refs;    // [entries]
+  int32_t *pos_of;  // [entries]: CSR position of each entry, -1 for a masked slot
   int64_t S, S_kv, G, topk;
   int64_t R;        // rows per batch = S_kv * G
   int CT, NC, NQ;   // tokens per chunk, chunks per batch, chunk groups per batch
@@ -210,33 +210,33 @@ __global__ void __launch_bounds__(256) csr_scatter_kernel(const CsrParams p) {
     if (!unordered) {
       for (int64_t s = tid; s < p.topk; s += 256) {
         const int32_t j = cur_idx[s];
-        if (j >= 0 && j < p.S_kv) {
-          const int32_t pos = atomicAdd(&cur[j * p.G + g], 1);
-          p.refs[pos] = (int32_t)(e0 + s);
-        }
+        int32_t pos = -1;
+        if (j >= 0 && j < p.S_kv) pos = atomicAdd(&cur[j * p.G + g], 1);
+        p.pos_of[e0 + s] = pos;
       }
     } else if (tid == 0) {
       for (int64_t s = 0; s < p.topk; ++s) {
         const int32_t j = cur_idx[s];
-        if (j >= 0 && j < p.S_kv) p.refs[cur[j * p.G + g]++] = (int32_t)(e0 + s);
+        p.pos_of[e0 + s] = (j >= 0 && j < p.S_kv) ? cur[j * p.G + g]++ : -1;
       }
     }
   }
 }
 
-// One workgroup per kv row.  The row's work items are its (entry, head tile)
-// partial rows in CSR order, item k = entry k / ntiles, tile k % ntiles; they
-// are split into four contiguous quarters, one per wave.  A partial row is
-// read as 16-byte chunks by a group of LPE lanes, so one load instruction
-// covers EPI = 64 / LPE items and every lane keeps U loads in flight.  Lane
-// group g of a wave sums items g, g + EPI, ... of its quarter in order (fp32);
-// the groups are combined by a fixed xor tree and the four waves as
-// ((w0 + w1) + w2) + w3.  The association depends on the item count alone,
-// so the result is bitwise reproducible.
+// One workgroup per kv row.  The main kernel wrote each entry's partial rows
+// at its CSR position, so the row's items are the contiguous partial rows
+// [rowptr[r] * ntiles, rowptr[r + 1] * ntiles) in CSR order; they are split
+// into four contiguous quarters, one per wave.  A partial row is read as
+// 16-byte chunks by a group of LPE lanes, so one load instruction covers
+// EPI = 64 / LPE items and every lane keeps U loads in flight.  Lane group g
+// of a wave sums items g, g + EPI, ... of its quarter in order (fp32); the
+// groups are combined by a fixed xor tree and the four waves as
+// ((w0 + w1) + w2) + w3.  The association depends on the item count alone, so
+// the result is bitwise reproducible.
 template <int D_QK, bool F32P>
 __global__ void __launch_bounds__(256)
-dkv_reduce_kernel(const int32_t *rowptr, const int32_t *refs, const unsigned char *partials,
-                  const int8_t *partial_exp, uint16_t *dkv, int64_t nrows, int ntiles) {
+dkv_reduce_kernel(const int32_t *rowptr, const unsigned char *partials, const int8_t *partial_exp,
+                  uint16_t *dkv, int64_t nrows, int ntiles) {
   constexpr int ROWB = D_QK * (F32P ? 4 : 2);  // bytes per partial row
   constexpr int NCR = ROWB / 16;                // 16-byte chunks per partial row
   constexpr int LPE = NCR <= 8 ? 8 : (NCR <= 16 ? 16 : (NCR <= 32 ? 32 : 64));  // lanes per item
@@ -250,35 +250,22 @@ dkv_reduce_kernel(const int32_t *rowptr, const int32_t *refs, const unsigned cha
   const bool active = c < NCR;
   const int64_t r = blockIdx.x;
   if (r >= nrows) return;
-  const int32_t base = rowptr[r], n = rowptr[r + 1] - base;
-  const int64_t k0 = (int64_t)n * w / 4 * ntiles, k1 = (int64_t)n * (w + 1) / 4 * ntiles;
-  // partial row of item k (relative to this row's first entry), -1 past the quarter
-  auto item_row = [&](int64_t k) -> int64_t {
-    if (k >= k1) return -1;
-    const int64_t ent = k / ntiles;
-    return (int64_t)refs[base + ent] * ntiles + (k - ent * ntiles);
-  };
+  const int64_t base = rowptr[r], n = (int64_t)(rowptr[r + 1] - rowptr[r]) * ntiles;
+  const int64_t k0 = base * ntiles + n * w / 4, k1 = base * ntiles + n * (w + 1) / 4;
   float acc[EPC];
 #pragma unroll
   for (int x = 0; x < EPC; ++x) acc[x] = 0.0f;
-  int64_t pr_next[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) pr_next[u] = item_row(k0 + EPI * u + grp);
   for (int64_t kb = k0; kb < k1; kb += EPI * U) {
-    int64_t pr[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) pr[u] = pr_next[u];
-#pragma unroll
-    for (int u = 0; u < U; ++u) pr_next[u] = item_row(kb + EPI * (U + u) + grp);
     i32x4 v[U];
     float sc[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      const int64_t k = kb + EPI * u + grp;
       v[u] = i32x4{0, 0, 0, 0};
       sc[u] = 0.0f;
-      if (pr[u] >= 0 && active) {
-        v[u] = ld_global_16(partials + pr[u] * ROWB + c * 16);
-        if constexpr (!F32P) sc[u] = exp2i(-(int)partial_exp[pr[u]]);
+      if (k < k1 && active) {
+        v[u] = ld_global_16(partials + k * ROWB + c * 16);
+        if constexpr (!F32P) sc[u] = exp2i(-(int)partial_exp[k]);
       }
     }
 #pragma unroll

@@ -47,7 +47,7 @@ template <int D_QK, int D_V, bool FP8>
 struct FwdCfg {
   using Gat = GatherCfg<D_QK, D_V, FP8>;
   static constexpr int KL_BYTES = 32 * Gat::KL_STRIDE;
-  static constexpr int KD_STRIDE = D_V * 2 + 16;          // e4m3: dequantised V rows (bf16)
+  static constexpr int KD_STRIDE = D_V * 2 + 32;          // e4m3: dequantised V rows (bf16)
   static constexpr int KD_BYTES = FP8 ? 32 * KD_STRIDE : 0;
   static constexpr int SC_BYTES = FP8 ? 32 * 4 : 0;
   static constexpr int WAVE_BYTES = (KL_BYTES + KD_BYTES + SC_BYTES + 15) / 16 * 16;
@@ -169,11 +169,11 @@ sparse_mla_fwd_kernel(const FwdParams p) {
     }
     mloc = fmaxf(mloc, xor32(mloc));
     const float m_new = fmaxf(m_run, mloc);
-    const float alpha = exp2f(m_run - m_new);
+    const float alpha = exp2_fast(m_run - m_new);
     float lsum = 0.0f;
 #pragma unroll
     for (int a = 0; a < 16; ++a) {
-      t[a] = exp2f(t[a] - m_new);
+      t[a] = exp2_fast(t[a] - m_new);
       lsum += t[a];
     }
     lsum += xor32(lsum);

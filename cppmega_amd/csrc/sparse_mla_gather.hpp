@@ -28,7 +28,8 @@ struct GatherCfg {
   static constexpr int NCH_V = D_V / CH;           // chunks of the V prefix
   static constexpr int UNITS = 8 * NCH;            // (4 rows x 1 chunk) units per block
   static constexpr int UPL = (UNITS + 63) / 64;    // units per lane
-  static constexpr int KL_STRIDE = ROWB + 16;      // LDS row stride of the raw tile
+  static constexpr int KL_STRIDE = ROWB + 32;      // LDS row stride: a 32-byte pad puts the 4 rows of a
+                                                   // transposed read in distinct banks
   static_assert(NCH * CH == D_QK && NCH_V * CH == D_V, "head dims must be whole 16-byte chunks");
   struct Regs {
     i32x4 v[UPL][4];
