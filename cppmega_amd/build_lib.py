@@ -29,6 +29,14 @@ HIP_FLAGS = [
 ]
 
 
+# Per-file additions.  The indexer's epilogue is one max + one fma per score
+# element; with IEEE mode off and NaN inputs declared undefined, fmaxf is a
+# single v_max_f32 instead of a canonicalise + max pair.
+FILE_FLAGS = {
+    "indexer_score.hip": ["-fno-honor-nans", "-mno-amdgpu-ieee"],
+}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and os.path.exists(cand):
@@ -42,7 +50,8 @@ def sources():
 
 def _compile(src: str, verbose: bool) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src)[:-4] + ".o")
-    cmd = [hipcc(), *HIP_FLAGS, f"-I{INCLUDE_DIR}", "-c", src, "-o", obj]
+    cmd = [hipcc(), *HIP_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), f"-I{INCLUDE_DIR}", "-c", src, "-o",
+           obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -121,6 +121,15 @@ __device__ __forceinline__ int wave_id() { return (int)(threadIdx.x >> 6); }
 
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
 
+// x(lane) + x(lane ^ 32) in every lane, by one v_permlane32_swap (the swap
+// leaves lanes 0-31 of the first result holding the low half and lanes 0-31 of
+// the second holding the high half, mirrored for lanes 32-63); the sum is
+// low + high in both halves, so both get the same bits.
+__device__ __forceinline__ float sum_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Make this wave's LDS writes visible to its own other lanes.
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

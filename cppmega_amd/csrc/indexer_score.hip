@@ -10,10 +10,17 @@
 // accumulator registers (in-lane adds plus one cross-half exchange) before a
 // single fp32 store per (token, key).
 //
-// Tile: one workgroup = 256 (token, head) rows x 128 keys; each wave owns 64
-// rows (2 M-subtiles, A operands in registers) and reads the key tile (B
-// operands) from LDS.  Causal: tiles whose first key lies beyond their last
-// token do no MFMA work (mode 1 fills -inf, mode 2 skips them).
+// Tiling: a wave keeps the q rows of 2 x 32 (token, head) rows as A operands
+// in registers (4 tokens at h = 16) and streams keys through them; a workgroup
+// (4 waves, 4 * 64 / h tokens) walks a 512-key chunk in 64-key tiles that are
+// double-buffered in LDS and shared by its waves.  Per 32 keys a wave runs
+// 2 * d / 16 MFMAs, then ReLU * w and the in-lane head sum on the
+// accumulators, one permlane32 swap for the other half of the heads, and one
+// coalesced fp32 store per (token, 32 keys).  Causal: chunks wholly above a
+// token block do no work (mode 1 writes their -inf), and a wave skips the key
+// tiles above its last token.  Late (longer) token blocks are scheduled first.
+// This file is compiled with IEEE mode off and NaN inputs left undefined, so
+// the ReLU is a single v_max_f32 per element.
 #include <type_traits>
 
 #include "dsa_common.hpp"
@@ -36,60 +43,76 @@ struct IdxParams {
 template <int H, int D, bool FP8>
 struct IdxCfg {
   static constexpr int ELT = FP8 ? 1 : 2;
-  static constexpr int ROWS = 256;
-  static constexpr int TT = ROWS / H;       // tokens per workgroup
-  static constexpr int TPW = 64 / H;        // tokens per wave
-  static constexpr int TN = 128;            // keys per workgroup
+  static constexpr int MT = 2;                  // 32-row M tiles per wave
+  static constexpr int TPW = MT * 32 / H;       // tokens per wave
+  static constexpr int WAVES = 4;
+  static constexpr int TT = TPW * WAVES;        // tokens per workgroup
+  static constexpr int KT = 64;                 // keys per LDS tile
+  static constexpr int NKT = 8;                 // tiles per workgroup chunk
+  static constexpr int CHUNK = KT * NKT;        // keys per workgroup
   static constexpr int KS_STRIDE = D * ELT + 16;
   static constexpr int KSTEPS = D / 16;
+  static constexpr int CPR = D * ELT / 16;      // 16-byte chunks per key row
+  static constexpr int LOADS = KT * CPR / 256;  // 16-byte loads per thread per tile
   static_assert(H == 16 || H == 32 || H == 64, "index heads must be 16, 32 or 64");
-  static_assert(D % 16 == 0 && D * ELT % 16 == 0, "index head dim");
+  static_assert(D % 16 == 0 && LOADS >= 1 && KT * CPR % 256 == 0, "index head dim");
 };
 
-template <int H, int D, bool FP8>
-__global__ void __launch_bounds__(256) indexer_score_kernel(const IdxParams p) {
+template <int H, int D, bool FP8, bool RELU>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+indexer_score_kernel(const IdxParams p) {
   using C = IdxCfg<H, D, FP8>;
-  __shared__ __attribute__((aligned(16))) unsigned char KS[C::TN * C::KS_STRIDE];
-  const int tid = threadIdx.x, lane = lane_id(), w = wave_id();
+  __shared__ __attribute__((aligned(16))) unsigned char KS[2][C::KT * C::KS_STRIDE];
+  const int tid = threadIdx.x, lane = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
   const int g32 = lane >> 5, l32 = lane & 31;
   const int64_t b = blockIdx.z;
-  const int64_t t0 = (int64_t)blockIdx.y * C::TT;
-  const int64_t s0 = (int64_t)blockIdx.x * C::TN;
+  const int64_t t0 = (int64_t)(gridDim.y - 1 - blockIdx.y) * C::TT;
+  const int64_t k0 = (int64_t)blockIdx.x * C::CHUNK;
   const int64_t t_last = (t0 + C::TT < p.Sq ? t0 + C::TT : p.Sq) - 1;
   float *out_b = p.out + b * p.Sq * p.Sk;
+  const int64_t chunk_end = k0 + C::CHUNK < p.Sk ? k0 + C::CHUNK : p.Sk;
 
-  if (p.causal && s0 > t_last) {
+  if (p.causal && k0 > t_last) {
     if (p.causal == 1) {
-      for (int i = tid; i < C::TT * C::TN; i += 256) {
-        const int64_t t = t0 + i / C::TN, s = s0 + i % C::TN;
-        if (t < p.Sq && s < p.Sk) out_b[t * p.Sk + s] = -INFINITY;
-      }
+      const int64_t nk = chunk_end - k0;
+      for (int64_t i = tid; i < (t_last - t0 + 1) * nk; i += 256) out_b[(t0 + i / nk) * p.Sk + k0 + i % nk] = -INFINITY;
     }
     return;
   }
+  // keys computed: the chunk, cut at the block's last token in lower-triangle mode
+  const int64_t k_end = (p.causal == 2 && t_last + 1 < chunk_end) ? t_last + 1 : chunk_end;
+  const int ntile = (int)((k_end - k0 + C::KT - 1) / C::KT);
 
-  // ---- stage the key tile: KS[key][d] ----
-  constexpr int CPR = D * C::ELT / 16;  // 16-byte chunks per key row
-  for (int i = tid; i < C::TN * CPR; i += 256) {
-    const int key = i / CPR, c = i % CPR;
-    const int64_t s = s0 + key;
-    i32x4 v = {0, 0, 0, 0};
-    if (s < p.Sk) v = ld_global_16(p.k + ((s * p.B + b) * D) * C::ELT + c * 16);
-    *reinterpret_cast<i32x4 *>(KS + key * C::KS_STRIDE + c * 16) = v;
-  }
+  // ---- key tile loads (thread: LOADS 16-byte chunks of the 64-key tile) ----
+  auto load_tile = [&](int it, i32x4 (&r)[C::LOADS]) {
+#pragma unroll
+    for (int l = 0; l < C::LOADS; ++l) {
+      const int u = tid + 256 * l, key = u / C::CPR, c = u % C::CPR;
+      const int64_t sk = k0 + (int64_t)it * C::KT + key;
+      r[l] = i32x4{0, 0, 0, 0};
+      if (sk < p.Sk) r[l] = ld_global_16(p.k + ((sk * p.B + b) * D) * C::ELT + c * 16);
+    }
+  };
+  auto store_tile = [&](int buf, const i32x4 (&r)[C::LOADS]) {
+#pragma unroll
+    for (int l = 0; l < C::LOADS; ++l) {
+      const int u = tid + 256 * l, key = u / C::CPR, c = u % C::CPR;
+      *reinterpret_cast<i32x4 *>(&KS[buf][key * C::KS_STRIDE + c * 16]) = r[l];
+    }
+  };
+  i32x4 kreg[C::LOADS];
+  load_tile(0, kreg);
 
-  // ---- A operands (q rows) and per-row weights ----
+  // ---- A operands (q rows) and weights of this wave's 64 (token, head) rows ----
   typedef typename std::conditional<FP8, long, bf16x8>::type aop_t;
-  aop_t A[2][C::KSTEPS];
-  float wv[2][16];
+  aop_t A[C::MT][C::KSTEPS];
   const int64_t wave_tok0 = t0 + w * C::TPW;
 #pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    const int r = m * 32 + l32;  // A-operand row of this lane
+  for (int m = 0; m < C::MT; ++m) {
+    const int r = m * 32 + l32;
     const int64_t t = wave_tok0 + r / H;
-    const int h = r % H;
     const bool ok = t < p.Sq;
-    const int64_t qrow = (t * p.B + b) * H + h;
+    const int64_t qrow = (t * p.B + b) * H + r % H;
 #pragma unroll
     for (int k = 0; k < C::KSTEPS; ++k) {
       if constexpr (FP8) {
@@ -100,80 +123,79 @@ __global__ void __launch_bounds__(256) indexer_score_kernel(const IdxParams p) {
         A[m][k] = as_bf16x8(v);
       }
     }
-#pragma unroll
-    for (int a = 0; a < 16; ++a) {
-      const int rr = m * 32 + 8 * (a >> 2) + 4 * g32 + (a & 3);  // accumulator row
-      const int64_t tt = wave_tok0 + rr / H;
-      const int hh = rr % H;
-      float wval = 0.0f;
-      if (tt < p.Sq) {
-        const int64_t wi = (tt * p.B + b) * H + hh;
-        wval = p.w_f32 ? static_cast<const float *>(p.w)[wi]
-                       : bf16_bits_to_f32(static_cast<const uint16_t *>(p.w)[wi]);
-      }
-      wv[m][a] = wval;
-    }
   }
-  float qk = 1.0f;
-  if constexpr (FP8) qk = p.q_scale[0] * p.k_scale[0];
-  __syncthreads();
+  // w of row `lane` (token lane / H, head lane % H); e4m3: times q_scale * k_scale,
+  // which commutes with the ReLU because the scales are positive
+  float wl = 0.0f;
+  {
+    const int64_t t = wave_tok0 + lane / H;
+    if (t < p.Sq) {
+      const int64_t wi = (t * p.B + b) * H + lane % H;
+      wl = p.w_f32 ? static_cast<const float *>(p.w)[wi] : bf16_bits_to_f32(static_cast<const uint16_t *>(p.w)[wi]);
+    }
+    if constexpr (FP8) wl *= p.q_scale[0] * p.k_scale[0];
+  }
+  float wv[C::MT][16];  // weight of each accumulator row
+#pragma unroll
+  for (int m = 0; m < C::MT; ++m)
+#pragma unroll
+    for (int a = 0; a < 16; ++a) wv[m][a] = __shfl(wl, m * 32 + 8 * (a >> 2) + 4 * g32 + (a & 3), 64);
 
+  store_tile(0, kreg);
+  __syncthreads();
   const int64_t wave_tok_last = wave_tok0 + C::TPW - 1;
-#pragma unroll 1
-  for (int n = 0; n < C::TN / 32; ++n) {
-    const int64_t sn = s0 + n * 32;
-    if (sn >= p.Sk) break;
-    const int64_t s = sn + l32;
-    if (p.causal && sn > wave_tok_last) {
-      if (p.causal == 1) {
+  for (int it = 0; it < ntile; ++it) {
+    if (it + 1 < ntile) load_tile(it + 1, kreg);
+    const unsigned char *ks = KS[it & 1];
 #pragma unroll
-        for (int tl = 0; tl < C::TPW; ++tl) {
-          const int64_t t = wave_tok0 + tl;
-          if ((tl & 1) == g32 && t < p.Sq && s < p.Sk) out_b[t * p.Sk + s] = -INFINITY;
+    for (int sub = 0; sub < C::KT / 32; ++sub) {
+      const int64_t sn = k0 + (int64_t)it * C::KT + sub * 32;
+      if (sn >= k_end) break;
+      if (p.causal == 2 && sn > wave_tok_last) break;  // wholly above this wave's diagonal
+      float part[C::TPW];
+#pragma unroll
+      for (int tl = 0; tl < C::TPW; ++tl) part[tl] = 0.0f;
+#pragma unroll
+      for (int m = 0; m < C::MT; ++m) {
+        f32x16 acc;
+#pragma unroll
+        for (int a = 0; a < 16; ++a) acc[a] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < C::KSTEPS; ++k) {
+          const unsigned char *brow = ks + (sub * 32 + l32) * C::KS_STRIDE;
+          if constexpr (FP8) {
+            const long bv = *reinterpret_cast<const long *>(brow + 16 * k + 8 * g32);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(A[m][k], bv, acc, 0, 0, 0);
+          } else {
+            const i32x4 bv = *reinterpret_cast<const i32x4 *>(brow + (16 * k + 8 * g32) * 2);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[m][k], as_bf16x8(bv), acc, 0, 0, 0);
+          }
+        }
+#pragma unroll
+        for (int a = 0; a < 16; ++a) {
+          const int tl = (m * 32 + 8 * (a >> 2)) / H;
+          const float x = RELU ? fmaxf(acc[a], 0.0f) : acc[a];  // one v_max_f32 (IEEE mode off)
+          part[tl] = fmaf(x, wv[m][a], part[tl]);
         }
       }
-      continue;
+      const int64_t s = sn + l32;
+#pragma unroll
+      for (int tl = 0; tl < C::TPW; ++tl) {
+        const float v = sum_halves(part[tl]);
+        const bool mine = C::TPW == 1 ? (g32 == 0) : ((tl & 1) == g32);
+        const int64_t t = wave_tok0 + tl;
+        if (mine && t < p.Sq && s < p.Sk) {
+          if (p.causal && s > t) {
+            if (p.causal == 1) out_b[t * p.Sk + s] = -INFINITY;
+          } else {
+            out_b[t * p.Sk + s] = v;
+          }
+        }
+      }
     }
-    float part[C::TPW];
-#pragma unroll
-    for (int tl = 0; tl < C::TPW; ++tl) part[tl] = 0.0f;
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      f32x16 acc;
-#pragma unroll
-      for (int a = 0; a < 16; ++a) acc[a] = 0.0f;
-#pragma unroll
-      for (int k = 0; k < C::KSTEPS; ++k) {
-        if constexpr (FP8) {
-          const long bv = *reinterpret_cast<const long *>(KS + (n * 32 + l32) * C::KS_STRIDE + 16 * k + 8 * g32);
-          acc = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(A[m][k], bv, acc, 0, 0, 0);
-        } else {
-          const i32x4 bv = *reinterpret_cast<const i32x4 *>(KS + (n * 32 + l32) * C::KS_STRIDE + (16 * k + 8 * g32) * 2);
-          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[m][k], as_bf16x8(bv), acc, 0, 0, 0);
-        }
-      }
-#pragma unroll
-      for (int a = 0; a < 16; ++a) {
-        const int tl = (m * 32 + 8 * (a >> 2)) / H;
-        float x = acc[a];
-        if constexpr (FP8) x *= qk;
-        if (p.relu) x = fmaxf(x, 0.0f);
-        part[tl] += x * wv[m][a];
-      }
-    }
-#pragma unroll
-    for (int tl = 0; tl < C::TPW; ++tl) part[tl] += xor32(part[tl]);
-#pragma unroll
-    for (int tl = 0; tl < C::TPW; ++tl) {
-      const bool mine = C::TPW == 1 ? (g32 == 0) : ((tl & 1) == g32);
-      const int64_t t = wave_tok0 + tl;
-      if (mine && t < p.Sq && s < p.Sk) {
-        if (p.causal && s > t) {
-          if (p.causal == 1) out_b[t * p.Sk + s] = -INFINITY;
-        } else {
-          out_b[t * p.Sk + s] = part[tl];
-        }
-      }
+    if (it + 1 < ntile) {
+      store_tile((it + 1) & 1, kreg);
+      __syncthreads();
     }
   }
 }
@@ -181,8 +203,12 @@ __global__ void __launch_bounds__(256) indexer_score_kernel(const IdxParams p) {
 template <int H, int D, bool FP8>
 static int launch_idx(const IdxParams &p, hipStream_t st) {
   using C = IdxCfg<H, D, FP8>;
-  const dim3 grid((unsigned)((p.Sk + C::TN - 1) / C::TN), (unsigned)((p.Sq + C::TT - 1) / C::TT), (unsigned)p.B);
-  hipLaunchKernelGGL((indexer_score_kernel<H, D, FP8>), grid, dim3(256), 0, st, p);
+  const dim3 grid((unsigned)((p.Sk + C::CHUNK - 1) / C::CHUNK), (unsigned)((p.Sq + C::TT - 1) / C::TT),
+                  (unsigned)p.B);
+  if (p.relu)
+    hipLaunchKernelGGL((indexer_score_kernel<H, D, FP8, true>), grid, dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((indexer_score_kernel<H, D, FP8, false>), grid, dim3(256), 0, st, p);
   return check_launch("indexer_scores");
 }
 
