@@ -373,16 +373,24 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
                     (int)pack_f16x2(cacc[dt][4 * i + 2] * rscale, cacc[dt][4 * i + 3] * rscale)};
         }
       if (g32 == 0) Lpos[l32] = wr ? pos : -1;
-      if (g32 == 0 && wr) p.partial_exp[(int64_t)pos * p.ntiles + tile] = (int8_t)pexp;
+      if (g32 == 0 && wr) p.partial_exp[(uint64_t)(uint32_t)pos * (uint32_t)p.ntiles + tile] = (int8_t)pexp;
       wave_lds_sync();
+      // all LDS reads first, then the stores, so the reads overlap
+      constexpr int ITS = 32 * C::ROW_CHUNKS / 64;
+      int ps[ITS];
+      i32x4 v[ITS];
 #pragma unroll
-      for (int it = 0; it < 32 * C::ROW_CHUNKS / 64; ++it) {
+      for (int it = 0; it < ITS; ++it) {
         const int u = it * 64 + lane;
         const int row = u / C::ROW_CHUNKS, ch = u % C::ROW_CHUNKS;
-        const int ps = Lpos[row];
-        const i32x4 v = *reinterpret_cast<const i32x4 *>(Cs + row * C::CS_STRIDE + ch * 16);
-        if (ps >= 0)
-          *reinterpret_cast<i32x4 *>(p.partials + ((int64_t)ps * p.ntiles + tile) * (D_QK * 2) + ch * 16) = v;
+        ps[it] = Lpos[row];
+        v[it] = *reinterpret_cast<const i32x4 *>(Cs + row * C::CS_STRIDE + ch * 16);
+      }
+#pragma unroll
+      for (int it = 0; it < ITS; ++it) {
+        const int ch = (it * 64 + lane) % C::ROW_CHUNKS;
+        const uint64_t prow = (uint64_t)(uint32_t)ps[it] * (uint32_t)p.ntiles + tile;
+        if (ps[it] >= 0) *reinterpret_cast<i32x4 *>(p.partials + prow * (D_QK * 2) + ch * 16) = v[it];
       }
     }
     wave_lds_sync();  // K / dS tiles are consumed before the next block's gather lands
