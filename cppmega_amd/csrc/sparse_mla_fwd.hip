@@ -148,8 +148,11 @@ sparse_mla_fwd_kernel(const FwdParams p) {
       }
     }
 
-    // ---- online softmax over this block's 32 slots (log2 domain) ----
-    float t[16];
+    // ---- online softmax over this block's 32 slots (log2 domain, lazy rescale) ----
+    // P = exp2(s * scale' - m_ref) against a reference max that only moves when
+    // a score exceeds it by more than 2^8: P stays <= 256 (exact range for
+    // bf16 / fp32) and O, l are rescaled only on those (rare, wave-uniform) steps.
+    float xs[16];
     float mloc = kNegBig;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -162,27 +165,32 @@ sparse_mla_fwd_kernel(const FwdParams p) {
       for (int j = 0; j < 4; ++j) {
         const int slot = 8 * i + 4 * g32 + j;
         const bool valid = (vmask >> slot) & 1ull;
-        const float v = sacc[4 * i + j] * tscale * ksc4[j];
-        t[4 * i + j] = valid ? v : -INFINITY;
-        mloc = fmaxf(mloc, t[4 * i + j]);
+        float v = sacc[4 * i + j];
+        if constexpr (FP8) v *= ksc4[j];
+        xs[4 * i + j] = valid ? v : -INFINITY;  // raw score, scaled inside the exp
+        mloc = fmaxf(mloc, xs[4 * i + j]);
       }
     }
-    mloc = fmaxf(mloc, xor32(mloc));
-    const float m_new = fmaxf(m_run, mloc);
-    const float alpha = exp2_fast(m_run - m_new);
+    mloc = max_halves(mloc) * tscale;
+    if (__ballot(mloc > m_run + 8.0f) != 0ull) {  // some head's max moved: rescale O, l
+      const float m_new = fmaxf(m_run, mloc);
+      const float alpha = exp2_fast(m_run - m_new);
+      l_run *= alpha;
+      m_run = m_new;
+#pragma unroll
+      for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+        for (int a = 0; a < 16; ++a) oacc[dt][a] *= alpha;
+    }
+    float t[16];
     float lsum = 0.0f;
 #pragma unroll
     for (int a = 0; a < 16; ++a) {
-      t[a] = exp2_fast(t[a] - m_new);
+      t[a] = exp2_fast(fmaf(xs[a], tscale, -m_run));  // -inf (masked slot) -> 0
       lsum += t[a];
     }
-    lsum += xor32(lsum);
-    l_run = l_run * alpha + lsum;
-    m_run = m_new;
-#pragma unroll
-    for (int dt = 0; dt < C::DT; ++dt)
-#pragma unroll
-      for (int a = 0; a < 16; ++a) oacc[dt][a] *= alpha;
+    lsum = sum_halves(lsum);
+    l_run += lsum;
 
     // ---- O^T[d][head] += V^T[d][slot] P^T[slot][head]  (K = slot, accumulator order) ----
 #pragma unroll

@@ -72,9 +72,15 @@ __device__ __forceinline__ void gather_issue(typename Gat::Regs &rg, const unsig
 }
 
 // K rows, row-major (raw bf16 / e4m3 bytes): Kl[slot][chunk]; masked slots zero.
+// Blocks without masked slots (the common case, tested wave-wide) skip the selects.
 template <class Gat>
 __device__ __forceinline__ void gather_store_k(const typename Gat::Regs &rg, unsigned char *Kl) {
   const int lane = lane_id();
+  uint32_t full = 0u;  // valid bits of this lane's units that exist
+#pragma unroll
+  for (int uu = 0; uu < Gat::UPL; ++uu)
+    if (lane + 64 * uu < Gat::UNITS) full |= 0xfu << (4 * uu);
+  const bool all_valid = __ballot(rg.valid != full) == 0ull;
 #pragma unroll
   for (int uu = 0; uu < Gat::UPL; ++uu) {
     const int u = lane + 64 * uu;
@@ -82,9 +88,12 @@ __device__ __forceinline__ void gather_store_k(const typename Gat::Regs &rg, uns
     const int c = u % Gat::NCH, quad = u / Gat::NCH;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const bool ok = (rg.valid >> (4 * uu + r)) & 1u;
-      const i32x4 z = {0, 0, 0, 0};
-      *reinterpret_cast<i32x4 *>(Kl + (quad * 4 + r) * Gat::KL_STRIDE + c * 16) = ok ? rg.v[uu][r] : z;
+      i32x4 v = rg.v[uu][r];
+      if (!all_valid) {
+        const bool ok = (rg.valid >> (4 * uu + r)) & 1u;
+        v = ok ? v : i32x4{0, 0, 0, 0};
+      }
+      *reinterpret_cast<i32x4 *>(Kl + (quad * 4 + r) * Gat::KL_STRIDE + c * 16) = v;
     }
   }
 }
