@@ -38,28 +38,10 @@
 #include "dsa_common.hpp"
 #include "sparse_mla_csr.hpp"
 #include "sparse_mla_gather.hpp"
+#include "sparse_mla_params.hpp"
+#include "sparse_mla_wide.hpp"
 
 namespace dsa {
-
-struct BwdParams {
-  const unsigned char *q;
-  const unsigned char *kv;
-  const uint16_t *o;
-  const uint16_t *dO;
-  const int32_t *idx;
-  const float *lse;
-  const float *delta;  // optional precomputed Delta [B,S,H]
-  uint16_t *dq;
-  const float *q_scale;
-  const float *kv_scale;
-  const int32_t *pos_of;  // CSR position of each entry (-1: masked slot)
-  unsigned char *partials;
-  int8_t *partial_exp;  // fp16 rows: power-of-two scale exponent per (position, tile)
-  int64_t B, S, S_kv, H, G, topk;
-  int hpg, ntiles;
-  float sl2;    // sm_scale * log2(e)
-  float scale;  // sm_scale
-};
 
 // LDS of one workgroup (one (token, kv group, 32-head tile) item, WPT waves):
 //   shared  QL [head][d] bf16 (e4m3: dequantised), DOL [head][d] bf16,
@@ -445,7 +427,8 @@ static BwdWorkspace bwd_layout(int64_t B, int64_t S, int64_t S_kv, int64_t H, in
   const int64_t R = S_kv * G;
   BwdWorkspace L;
   csr_plan(S, R, &L.CT, &L.NC, &L.NQ);
-  const size_t psz = (flags & DSA_BWD_FP32_PARTIALS) ? 4 : 2;
+  // wide heads always keep fp32 partial rows
+  const size_t psz = ((flags & DSA_BWD_FP32_PARTIALS) || D_qk > 256) ? 4 : 2;
   size_t off = 0;
   L.partials = off;
   off += align256(entries * ntiles * D_qk * psz);
@@ -541,9 +524,10 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
   if (dtype == DSA_DTYPE_E4M3)
     DSA_REQUIRE(q_scale && kv_scale, "dsa_sparse_mla_bwd: e4m3 input needs q_scale and kv_scale");
   const bool f8 = dtype == DSA_DTYPE_E4M3;
-  const bool f32p = (flags & DSA_BWD_FP32_PARTIALS) != 0;
+  const bool wide = wide_shape(D_qk, D_v) && !f8;
+  const bool f32p = (flags & DSA_BWD_FP32_PARTIALS) != 0 || wide;
   const bool shape_ok = (D_qk == 128 && D_v == 64) || (D_qk == 128 && D_v == 128) ||
-                        (D_qk == 192 && D_v == 128) || (D_qk == 64 && D_v == 32 && !f8);
+                        (D_qk == 192 && D_v == 128) || (D_qk == 64 && D_v == 32 && !f8) || wide;
   if (!shape_ok)
     return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_bwd: no kernel for d_qk=%lld d_v=%lld dtype=%d",
                      (long long)D_qk, (long long)D_v, dtype);
@@ -602,7 +586,8 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
   p.ntiles = ntiles;
   p.sl2 = sm_scale * kLog2e;
   p.scale = sm_scale;
-  if (D_qk == 128 && D_v == 64) rc = f8 ? launch_bwd_main_p<128, 64, true>(p, f32p, st) : launch_bwd_main_p<128, 64, false>(p, f32p, st);
+  if (wide) rc = launch_bwd_main_wide(p, D_qk, D_v, st);
+  else if (D_qk == 128 && D_v == 64) rc = f8 ? launch_bwd_main_p<128, 64, true>(p, f32p, st) : launch_bwd_main_p<128, 64, false>(p, f32p, st);
   else if (D_qk == 128 && D_v == 128) rc = f8 ? launch_bwd_main_p<128, 128, true>(p, f32p, st) : launch_bwd_main_p<128, 128, false>(p, f32p, st);
   else if (D_qk == 192 && D_v == 128) rc = f8 ? launch_bwd_main_p<192, 128, true>(p, f32p, st) : launch_bwd_main_p<192, 128, false>(p, f32p, st);
   else rc = launch_bwd_main_p<64, 32, false>(p, f32p, st);
@@ -612,6 +597,7 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
   uint16_t *dkv16 = static_cast<uint16_t *>(dkv);
   if (D_qk == 128) rc = launch_reduce<128>(cp, p.partials, p.partial_exp, dkv16, rows, ntiles, f32p, st);
   else if (D_qk == 192) rc = launch_reduce<192>(cp, p.partials, p.partial_exp, dkv16, rows, ntiles, f32p, st);
+  else if (D_qk == 576) rc = launch_reduce<576>(cp, p.partials, p.partial_exp, dkv16, rows, ntiles, f32p, st);
   else rc = launch_reduce<64>(cp, p.partials, p.partial_exp, dkv16, rows, ntiles, f32p, st);
   if (rc) return rc;
   stage_mark(st);

@@ -227,12 +227,12 @@ __global__ void __launch_bounds__(256) csr_scatter_kernel(const CsrParams p) {
 // at its CSR position, so the row's items are the contiguous partial rows
 // [rowptr[r] * ntiles, rowptr[r + 1] * ntiles) in CSR order; they are split
 // into four contiguous quarters, one per wave.  A partial row is read as
-// 16-byte chunks by a group of LPE lanes, so one load instruction covers
-// EPI = 64 / LPE items and every lane keeps U loads in flight.  Lane group g
-// of a wave sums items g, g + EPI, ... of its quarter in order (fp32); the
-// groups are combined by a fixed xor tree and the four waves as
-// ((w0 + w1) + w2) + w3.  The association depends on the item count alone, so
-// the result is bitwise reproducible.
+// 16-byte chunks by a group of LPE lanes (rows over 1 KiB: all 64 lanes, CPL
+// chunks each), so one load instruction covers EPI = 64 / LPE items and every
+// lane keeps about 8 loads in flight.  Lane group g of a wave sums items g,
+// g + EPI, ... of its quarter in order (fp32); the groups are combined by a
+// fixed xor tree and the four waves as ((w0 + w1) + w2) + w3.  The association
+// depends on the item count alone, so the result is bitwise reproducible.
 template <int D_QK, bool F32P>
 __global__ void __launch_bounds__(256)
 dkv_reduce_kernel(const int32_t *rowptr, const unsigned char *partials, const int8_t *partial_exp,
@@ -240,43 +240,52 @@ dkv_reduce_kernel(const int32_t *rowptr, const unsigned char *partials, const in
   constexpr int ROWB = D_QK * (F32P ? 4 : 2);  // bytes per partial row
   constexpr int NCR = ROWB / 16;                // 16-byte chunks per partial row
   constexpr int LPE = NCR <= 8 ? 8 : (NCR <= 16 ? 16 : (NCR <= 32 ? 32 : 64));  // lanes per item
+  constexpr int CPL = (NCR + 63) / 64;          // chunks per lane (rows over 1 KiB)
   constexpr int EPI = 64 / LPE;                 // items per load instruction
   constexpr int EPC = F32P ? 4 : 8;             // elements per chunk
-  constexpr int U = 8;                          // loads in flight per lane
-  static_assert(NCR * 16 == ROWB && NCR <= 64, "partial rows must be whole 16-byte chunks, at most 1 KiB");
+  constexpr int U = CPL > 1 ? (8 + CPL - 1) / CPL : 8;  // items in flight per lane
+  static_assert(NCR * 16 == ROWB, "partial rows must be whole 16-byte chunks");
   __shared__ float part[4][D_QK];
   const int lane = lane_id(), w = wave_id();
   const int grp = lane / LPE, c = lane % LPE;
-  const bool active = c < NCR;
   const int64_t r = blockIdx.x;
   if (r >= nrows) return;
   const int64_t base = rowptr[r], n = (int64_t)(rowptr[r + 1] - rowptr[r]) * ntiles;
   const int64_t k0 = base * ntiles + n * w / 4, k1 = base * ntiles + n * (w + 1) / 4;
-  float acc[EPC];
+  float acc[CPL][EPC];
 #pragma unroll
-  for (int x = 0; x < EPC; ++x) acc[x] = 0.0f;
+  for (int q = 0; q < CPL; ++q)
+#pragma unroll
+    for (int x = 0; x < EPC; ++x) acc[q][x] = 0.0f;
   for (int64_t kb = k0; kb < k1; kb += EPI * U) {
-    i32x4 v[U];
+    i32x4 v[U][CPL];
     float sc[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t k = kb + EPI * u + grp;
-      v[u] = i32x4{0, 0, 0, 0};
       sc[u] = 0.0f;
-      if (k < k1 && active) {
-        v[u] = ld_global_16(partials + k * ROWB + c * 16);
-        if constexpr (!F32P) sc[u] = exp2i(-(int)partial_exp[k]);
+      if constexpr (!F32P) {
+        if (k < k1) sc[u] = exp2i(-(int)partial_exp[k]);
+      }
+#pragma unroll
+      for (int q = 0; q < CPL; ++q) {
+        const int cc = c + 64 * q;
+        v[u][q] = i32x4{0, 0, 0, 0};
+        if (k < k1 && cc < NCR) v[u][q] = ld_global_16(partials + k * ROWB + cc * 16);
       }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
 #pragma unroll
-      for (int x = 0; x < EPC; ++x) {
-        if constexpr (F32P) {
-          acc[x] += __int_as_float(v[u][x]);
-        } else {
-          const uint32_t h = ((uint32_t)v[u][x >> 1] >> (16 * (x & 1))) & 0xffffu;
-          acc[x] += f16_bits_to_f32(h) * sc[u];  // exact: sc is a power of two
+      for (int q = 0; q < CPL; ++q) {
+#pragma unroll
+        for (int x = 0; x < EPC; ++x) {
+          if constexpr (F32P) {
+            acc[q][x] += __int_as_float(v[u][q][x]);
+          } else {
+            const uint32_t h = ((uint32_t)v[u][q][x >> 1] >> (16 * (x & 1))) & 0xffffu;
+            acc[q][x] += f16_bits_to_f32(h) * sc[u];  // exact: sc is a power of two
+          }
         }
       }
     }
@@ -284,11 +293,19 @@ dkv_reduce_kernel(const int32_t *rowptr, const unsigned char *partials, const in
 #pragma unroll
   for (int off = LPE; off < 64; off *= 2) {
 #pragma unroll
-    for (int x = 0; x < EPC; ++x) acc[x] += __shfl_xor(acc[x], off, 64);
-  }
-  if (grp == 0 && active) {
+    for (int q = 0; q < CPL; ++q)
 #pragma unroll
-    for (int x = 0; x < EPC; ++x) part[w][c * EPC + x] = acc[x];
+      for (int x = 0; x < EPC; ++x) acc[q][x] += __shfl_xor(acc[q][x], off, 64);
+  }
+  if (grp == 0) {
+#pragma unroll
+    for (int q = 0; q < CPL; ++q) {
+      const int cc = c + 64 * q;
+      if (cc < NCR) {
+#pragma unroll
+        for (int x = 0; x < EPC; ++x) part[w][cc * EPC + x] = acc[q][x];
+      }
+    }
   }
   __syncthreads();
   uint32_t *out = reinterpret_cast<uint32_t *>(dkv + r * D_QK);

@@ -26,22 +26,10 @@
 // computes.
 #include "dsa_common.hpp"
 #include "sparse_mla_gather.hpp"
+#include "sparse_mla_params.hpp"
+#include "sparse_mla_wide.hpp"
 
 namespace dsa {
-
-struct FwdParams {
-  const unsigned char *q;
-  const unsigned char *kv;
-  const int32_t *idx;
-  uint16_t *out;
-  float *lse;
-  const float *q_scale;
-  const float *kv_scale;
-  int64_t B, S, S_kv, H, G, topk;
-  int hpg;     // heads per kv group
-  int ntiles;  // ceil(hpg / 32)
-  float sl2;   // sm_scale * log2(e)
-};
 
 template <int D_QK, int D_V, bool FP8>
 struct FwdCfg {
@@ -283,6 +271,10 @@ extern "C" int dsa_sparse_mla_fwd(const void *q, const void *kv, const int32_t *
   p.sl2 = sm_scale * kLog2e;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool f8 = dtype == DSA_DTYPE_E4M3;
+  if (wide_shape(D_qk, D_v)) {
+    DSA_REQUIRE(S_kv * G * D_qk * 2 < (1ll << 32), "dsa_sparse_mla_fwd: kv rows of one batch exceed 4 GiB");
+    return launch_fwd_wide(p, D_qk, D_v, f8, st);
+  }
   if (D_qk == 128 && D_v == 64) return f8 ? launch_fwd<128, 64, true>(p, st) : launch_fwd<128, 64, false>(p, st);
   if (D_qk == 128 && D_v == 128) return f8 ? launch_fwd<128, 128, true>(p, st) : launch_fwd<128, 128, false>(p, st);
   if (D_qk == 192 && D_v == 128) return f8 ? launch_fwd<192, 128, true>(p, st) : launch_fwd<192, 128, false>(p, st);

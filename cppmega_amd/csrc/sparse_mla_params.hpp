@@ -1,0 +1,43 @@
+// Kernel parameter blocks of the SparseMLA forward and backward, shared by
+// the narrow-head kernels and the wide-head (d_qk = 576) kernels.
+#pragma once
+
+#include <stdint.h>
+
+namespace dsa {
+
+struct FwdParams {
+  const unsigned char *q;
+  const unsigned char *kv;
+  const int32_t *idx;
+  uint16_t *out;
+  float *lse;
+  const float *q_scale;
+  const float *kv_scale;
+  int64_t B, S, S_kv, H, G, topk;
+  int hpg;     // heads per kv group
+  int ntiles;  // ceil(hpg / 32)
+  float sl2;   // sm_scale * log2(e)
+};
+
+struct BwdParams {
+  const unsigned char *q;
+  const unsigned char *kv;
+  const uint16_t *o;
+  const uint16_t *dO;
+  const int32_t *idx;
+  const float *lse;
+  const float *delta;  // optional precomputed Delta [B,S,H]
+  uint16_t *dq;
+  const float *q_scale;
+  const float *kv_scale;
+  const int32_t *pos_of;  // CSR position of each entry (-1: masked slot)
+  unsigned char *partials;
+  int8_t *partial_exp;  // fp16 rows: power-of-two scale exponent per (position, tile)
+  int64_t B, S, S_kv, H, G, topk;
+  int hpg, ntiles;
+  float sl2;    // sm_scale * log2(e)
+  float scale;  // sm_scale
+};
+
+}  // namespace dsa
