@@ -524,7 +524,7 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
   if (dtype == DSA_DTYPE_E4M3)
     DSA_REQUIRE(q_scale && kv_scale, "dsa_sparse_mla_bwd: e4m3 input needs q_scale and kv_scale");
   const bool f8 = dtype == DSA_DTYPE_E4M3;
-  const bool wide = wide_shape(D_qk, D_v) && !f8;
+  const bool wide = wide_shape(D_qk, D_v);
   const bool f32p = (flags & DSA_BWD_FP32_PARTIALS) != 0 || wide;
   const bool shape_ok = (D_qk == 128 && D_v == 64) || (D_qk == 128 && D_v == 128) ||
                         (D_qk == 192 && D_v == 128) || (D_qk == 64 && D_v == 32 && !f8) || wide;
@@ -586,7 +586,7 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
   p.ntiles = ntiles;
   p.sl2 = sm_scale * kLog2e;
   p.scale = sm_scale;
-  if (wide) rc = launch_bwd_main_wide(p, D_qk, D_v, st);
+  if (wide) rc = launch_bwd_main_wide(p, D_qk, D_v, f8, st);
   else if (D_qk == 128 && D_v == 64) rc = f8 ? launch_bwd_main_p<128, 64, true>(p, f32p, st) : launch_bwd_main_p<128, 64, false>(p, f32p, st);
   else if (D_qk == 128 && D_v == 128) rc = f8 ? launch_bwd_main_p<128, 128, true>(p, f32p, st) : launch_bwd_main_p<128, 128, false>(p, f32p, st);
   else if (D_qk == 192 && D_v == 128) rc = f8 ? launch_bwd_main_p<192, 128, true>(p, f32p, st) : launch_bwd_main_p<192, 128, false>(p, f32p, st);

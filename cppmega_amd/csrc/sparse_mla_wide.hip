@@ -21,7 +21,7 @@
 //   * O^T[d][head] += V^T P^T is split over d_v: wave w accumulates every
 //     fourth 32-column tile of d_v, t = w + 4q (V^T read with transposing LDS
 //     reads in accumulator order, P straight from registers).
-// The backward splits S and dP the same way, then gives each wave every
+// The backward (bf16 and e4m3) splits S and dP the same way, then gives each wave every
 // fourth 32-column tile of d_qk for dQ^T = K^T dS^T and for the per-slot dKV
 // row c^T = Q^T dS^T + dO^T P^T, written as fp32 at the entry's CSR position
 // (the kv-major reduction sums those rows in a fixed order, as for the narrow
@@ -84,9 +84,9 @@ __device__ __forceinline__ void wide_issue(typename C::Regs &rg, const unsigned 
 }
 
 // Store the staged rows: raw bytes row-major into Kl (masked slots zero); for
-// e4m3 also the V prefix dequantised to bf16 (value * kv_scale, RNE) into Kd
-// and the per-slot scales into Ksc.
-template <class C, bool FP8>
+// e4m3 also the first NCH_D chunks dequantised to bf16 (value * kv_scale, RNE)
+// into Kd (row stride KD_STRIDE) and the per-slot scales into Ksc.
+template <class C, bool FP8, int NCH_D = C::NCH_V, int KD_STRIDE = C::KD_STRIDE>
 __device__ __forceinline__ void wide_store(const typename C::Regs &rg, unsigned char *Kl, unsigned char *Kd,
                                            float *Ksc) {
   const int t = threadIdx.x;
@@ -100,7 +100,7 @@ __device__ __forceinline__ void wide_store(const typename C::Regs &rg, unsigned 
       *reinterpret_cast<i32x4 *>(Kl + row * C::KL_STRIDE + c * 16) = v;
       if constexpr (FP8) {
         const float s = ok ? rg.sc[i] : 0.0f;
-        if (c < C::NCH_V) {
+        if (c < NCH_D) {
           uint32_t wd[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
@@ -108,7 +108,7 @@ __device__ __forceinline__ void wide_store(const typename C::Regs &rg, unsigned 
             const uint32_t sh = 16 * (e & 1);
             wd[e] = pack_bf16x2(e4m3_to_f32((word >> sh) & 0xffu) * s, e4m3_to_f32((word >> (sh + 8)) & 0xffu) * s);
           }
-          unsigned char *dst = Kd + row * C::KD_STRIDE + c * 32;
+          unsigned char *dst = Kd + row * KD_STRIDE + c * 32;
           *reinterpret_cast<i32x4 *>(dst) = i32x4{(int)wd[0], (int)wd[1], (int)wd[2], (int)wd[3]};
           *reinterpret_cast<i32x4 *>(dst + 16) = i32x4{(int)wd[4], (int)wd[5], (int)wd[6], (int)wd[7]};
         }
@@ -349,33 +349,43 @@ int launch_fwd_wide(const FwdParams &p, int64_t d_qk, int64_t d_v, bool fp8, hip
 }
 
 // ---------------------------------------------------------------------------
-// Backward main pass (bf16)
+// Backward main pass (bf16 and e4m3)
 // ---------------------------------------------------------------------------
-// LDS of one workgroup: QL [head][d] and DOL [head][d] (bf16, for the S / dP A
-// operands and the transposed Q^T / dO^T operands), LD = LSE (heads 0..31) and
-// Delta * sm_scale (32..63), Kl [slot][d] gathered rows, the four waves'
-// partial S and dP tiles, and one dS[slot][head] tile per wave.
-template <int D_QK, int D_V>
+// LDS of one workgroup: QL [head][d] and DOL [head][d] (bf16; e4m3 Q
+// dequantised, for the S / dP A operands and the transposed Q^T / dO^T
+// operands), LD = LSE (heads 0..31) and Delta * sm_scale (32..63), Kl [slot][d]
+// gathered rows (raw bytes), for e4m3 also Kd [slot][d] (rows dequantised to
+// bf16, the V and K operands of dP and dQ) and Ksc (row scales), the waves'
+// partial score tiles, and one dS[slot][head] tile per wave.  bf16 exchanges
+// the S and dP partials together (8 tiles); e4m3 has room for four and
+// exchanges them one after the other, as the reference's e4m3 kernel computes
+// QK^T on the codes and the other products on dequantised bf16.
+template <int D_QK, int D_V, bool FP8>
 struct WideBwdLds {
-  using C = WideCfg<D_QK, D_V, false>;
+  using C = WideCfg<D_QK, D_V, FP8>;
   static constexpr int QL_STRIDE = D_QK * 2 + 32;
   static constexpr int DOL_STRIDE = D_V * 2 + 32;
   static constexpr int DS_STRIDE = 32 * 2 + 32;
+  static constexpr int KDB_STRIDE = D_QK * 2 + 32;  // e4m3: whole rows dequantised
   static constexpr int OFF_QL = 0;
   static constexpr int OFF_DOL = OFF_QL + 32 * QL_STRIDE;
   static constexpr int OFF_LD = OFF_DOL + 32 * DOL_STRIDE;
   static constexpr int OFF_KL = OFF_LD + 64 * 4;
-  static constexpr int OFF_SP = OFF_KL + 32 * C::KL_STRIDE;
+  static constexpr int OFF_KD = OFF_KL + 32 * C::KL_STRIDE;
+  static constexpr int OFF_SC = OFF_KD + (FP8 ? 32 * KDB_STRIDE : 0);
+  static constexpr int OFF_SP = OFF_SC + (FP8 ? 32 * 4 : 0);
   static constexpr int SP_W = 16 * 64;  // floats per partial tile
-  static constexpr int OFF_DS = OFF_SP + 8 * SP_W * 4;
+  static constexpr int SP_TILES = FP8 ? 4 : 8;
+  static constexpr int OFF_DS = OFF_SP + SP_TILES * SP_W * 4;
   static constexpr int BYTES = OFF_DS + 4 * 32 * DS_STRIDE;
+  static_assert(BYTES <= 160 * 1024, "wide backward LDS");
 };
 
-template <int D_QK, int D_V>
+template <int D_QK, int D_V, bool FP8>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 sparse_mla_bwd_wide_kernel(const BwdParams p) {
-  using C = WideCfg<D_QK, D_V, false>;
-  using L = WideBwdLds<D_QK, D_V>;
+  using C = WideCfg<D_QK, D_V, FP8>;
+  using L = WideBwdLds<D_QK, D_V, FP8>;
   constexpr int DQT = D_QK / 32;          // 32-column tiles of d_qk
   constexpr int DQW = (DQT + 3) / 4;      // tiles per wave (tile t = w + 4 q)
   constexpr int DVT = D_V / 32;
@@ -396,7 +406,11 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
   unsigned char *DOL = smem + L::OFF_DOL;
   float *LD = reinterpret_cast<float *>(smem + L::OFF_LD);
   unsigned char *Kl = smem + L::OFF_KL;
+  unsigned char *Kd = smem + L::OFF_KD;
+  float *Ksc = reinterpret_cast<float *>(smem + L::OFF_SC);
   float *Sp = reinterpret_cast<float *>(smem + L::OFF_SP);
+  const unsigned char *Ksrc = FP8 ? Kd : Kl;  // bf16 K / V rows for dP and dQ
+  constexpr int K_STRIDE = FP8 ? L::KDB_STRIDE : C::KL_STRIDE;
   unsigned char *DS = smem + L::OFF_DS + w * 32 * L::DS_STRIDE;
 
   const int64_t head0 = tok * p.H + g * p.hpg + tile * 32;
@@ -404,14 +418,17 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
   const int64_t entry0 = (tok * p.G + g) * p.topk;
   const int32_t *idx_row = p.idx + entry0;
   const unsigned char *kv_b = p.kv + ((b * p.S_kv) * p.G + g) * C::ROWB;
+  const float *kv_scale_b = FP8 ? p.kv_scale + b * p.S_kv : nullptr;
   const uint32_t row_pitch = (uint32_t)(p.G * C::ROWB);
   const int nblk = (int)((p.topk + 31) / 32);
 
   int idx_cur = load_slot_index(idx_row, 0, l32, p.topk, p.S_kv);
   int idx_nxt = load_slot_index(idx_row, 1, l32, p.topk, p.S_kv);
   typename C::Regs rg;
-  wide_issue<C, false>(rg, kv_b, nullptr, idx_cur, row_pitch);
+  wide_issue<C, FP8>(rg, kv_b, kv_scale_b, idx_cur, row_pitch);
 
+  float qsc = 1.0f;
+  if constexpr (FP8) qsc = p.q_scale[tok];
   // ---------------- prologue: Q, dO tiles, LSE, Delta ----------------
   {
     const int t = threadIdx.x;
@@ -419,7 +436,21 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
     for (int u = t; u < 32 * QCH; u += 256) {
       const int h = u / QCH, c = u % QCH;
       i32x4 v = {0, 0, 0, 0};
-      if (h < nheads) v = ld_global_16(p.q + ((head0 + h) * D_QK + 8 * c) * 2);
+      if (h < nheads) {
+        if constexpr (FP8) {
+          const long raw = *reinterpret_cast<const long *>(p.q + (head0 + h) * D_QK + 8 * c);
+          uint32_t wq[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t c0 = (uint32_t)((unsigned long)raw >> (16 * e)) & 0xffu;
+            const uint32_t c1 = (uint32_t)((unsigned long)raw >> (16 * e + 8)) & 0xffu;
+            wq[e] = pack_bf16x2(e4m3_to_f32(c0) * qsc, e4m3_to_f32(c1) * qsc);
+          }
+          v = i32x4{(int)wq[0], (int)wq[1], (int)wq[2], (int)wq[3]};
+        } else {
+          v = ld_global_16(p.q + ((head0 + h) * D_QK + 8 * c) * 2);
+        }
+      }
       *reinterpret_cast<i32x4 *>(QL + h * L::QL_STRIDE + c * 16) = v;
     }
     // dO rows and Delta = sum_d O dO: one wave per head, lane = 8-element chunk
@@ -458,6 +489,14 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
     }
   }
 
+  // e4m3: this wave's quarter of the raw Q codes, the A operand of QK^T (head l32)
+  long qA8[FP8 ? C::KQ : 1];
+  if constexpr (FP8) {
+#pragma unroll
+    for (int k = 0; k < C::KQ; ++k)
+      qA8[k] = l32 < nheads ? *reinterpret_cast<const long *>(p.q + (head0 + l32) * D_QK + 16 * (w * C::KQ + k) + 8 * g32)
+                            : 0l;
+  }
   f32x16 dqacc[DQW];
 #pragma unroll
   for (int q = 0; q < DQW; ++q)
@@ -467,14 +506,14 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
   const int k0 = w * C::KQ, v0 = w * VQ;
   for (int blk = 0; blk < nblk; ++blk) {
     const int slot0 = blk * 32;
-    wide_store<C, false>(rg, Kl, nullptr, nullptr);
+    wide_store<C, FP8, C::NCH, L::KDB_STRIDE>(rg, Kl, Kd, Ksc);
     const bool valid = idx_cur >= 0;  // slot slot0 + l32
     int32_t pos = -1;
     if (valid) pos = p.pos_of[entry0 + slot0 + l32];
     const bool wr = valid && pos >= 0;
     __syncthreads();  // rows (and, on the first block, the prologue tiles) are in LDS
     const int idx_nn = load_slot_index(idx_row, blk + 2, l32, p.topk, p.S_kv);
-    if (blk + 1 < nblk) wide_issue<C, false>(rg, kv_b, nullptr, idx_nxt, row_pitch);
+    if (blk + 1 < nblk) wide_issue<C, FP8>(rg, kv_b, kv_scale_b, idx_nxt, row_pitch);
 
     // ---- partial S = Q K^T and dP = dO V^T (M = head, N = slot) over this wave's k-steps ----
     f32x16 sacc, dpacc;
@@ -486,25 +525,42 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
 #pragma unroll
     for (int k = 0; k < C::KQ; ++k) {
       const int d0 = 16 * (k0 + k) + 8 * g32;
-      const i32x4 qa = *reinterpret_cast<const i32x4 *>(QL + l32 * L::QL_STRIDE + d0 * 2);
-      const i32x4 kb = *reinterpret_cast<const i32x4 *>(Kl + l32 * C::KL_STRIDE + d0 * 2);
-      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(qa), as_bf16x8(kb), sacc, 0, 0, 0);
+      if constexpr (FP8) {
+        const long kb = *reinterpret_cast<const long *>(Kl + l32 * C::KL_STRIDE + d0);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(qA8[k], kb, sacc, 0, 0, 0);
+      } else {
+        const i32x4 qa = *reinterpret_cast<const i32x4 *>(QL + l32 * L::QL_STRIDE + d0 * 2);
+        const i32x4 kb = *reinterpret_cast<const i32x4 *>(Kl + l32 * C::KL_STRIDE + d0 * 2);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(qa), as_bf16x8(kb), sacc, 0, 0, 0);
+      }
     }
 #pragma unroll
     for (int k = 0; k < VQ; ++k) {
       const int d0 = 16 * (v0 + k) + 8 * g32;
       const i32x4 da = *reinterpret_cast<const i32x4 *>(DOL + l32 * L::DOL_STRIDE + d0 * 2);
-      const i32x4 vb = *reinterpret_cast<const i32x4 *>(Kl + l32 * C::KL_STRIDE + d0 * 2);
+      const i32x4 vb = *reinterpret_cast<const i32x4 *>(Ksrc + l32 * K_STRIDE + d0 * 2);
       dpacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(da), as_bf16x8(vb), dpacc, 0, 0, 0);
     }
-    put_partial(Sp + (2 * w) * L::SP_W, sacc);
-    put_partial(Sp + (2 * w + 1) * L::SP_W, dpacc);
-    __syncthreads();  // all partial tiles written
     float s[16], dp[16];
-    sum_partials(Sp, 2 * L::SP_W, s);
-    sum_partials(Sp + L::SP_W, 2 * L::SP_W, dp);
+    if constexpr (FP8) {
+      put_partial(Sp + w * L::SP_W, sacc);
+      __syncthreads();  // S partial tiles written
+      sum_partials(Sp, L::SP_W, s);
+      __syncthreads();  // read before the dP partials reuse the tiles
+      put_partial(Sp + w * L::SP_W, dpacc);
+      __syncthreads();
+      sum_partials(Sp, L::SP_W, dp);
+    } else {
+      put_partial(Sp + (2 * w) * L::SP_W, sacc);
+      put_partial(Sp + (2 * w + 1) * L::SP_W, dpacc);
+      __syncthreads();  // all partial tiles written
+      sum_partials(Sp, 2 * L::SP_W, s);
+      sum_partials(Sp + L::SP_W, 2 * L::SP_W, dp);
+    }
 
     // ---- P, dS (lane = slot slot0 + l32, heads 8i + 4*g32 + j; identical in every wave) ----
+    float xs = p.sl2;
+    if constexpr (FP8) xs *= qsc * Ksc[l32];
     bf16x8 dsB[2], pB[2];
     {
       uint32_t dsw[8], pw[8];
@@ -516,7 +572,7 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int a = 4 * i + j;
-          const float pv = valid ? exp2_fast(s[a] * p.sl2 - l4[j]) : 0.0f;
+          const float pv = valid ? exp2_fast(s[a] * xs - l4[j]) : 0.0f;
           P[j] = pv;
           dS[j] = pv * fmaf(dp[a], p.scale, -d4[j]);
         }
@@ -543,7 +599,7 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
       for (int q = 0; q < DQW; ++q) {
         const int t = w + 4 * q;
         if (t < DQT) {
-          const i32x4 av = tr_operand(Kl, C::KL_STRIDE, t * 32, 16 * kc, 4, 8);
+          const i32x4 av = tr_operand(Ksrc, K_STRIDE, t * 32, 16 * kc, 4, 8);
           dqacc[q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(av), as_bf16x8(bv), dqacc[q], 0, 0, 0);
         }
       }
@@ -603,23 +659,22 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
   }
 }
 
-template <int D_QK, int D_V>
+template <int D_QK, int D_V, bool FP8>
 static int launch_bwd_wide_t(const BwdParams &p, hipStream_t st) {
-  using L = WideBwdLds<D_QK, D_V>;
+  using L = WideBwdLds<D_QK, D_V, FP8>;
   const size_t lds = L::BYTES;
-  static_assert(L::BYTES <= 160 * 1024, "wide backward LDS");
-  hipError_t e = hipFuncSetAttribute((const void *)sparse_mla_bwd_wide_kernel<D_QK, D_V>,
+  hipError_t e = hipFuncSetAttribute((const void *)sparse_mla_bwd_wide_kernel<D_QK, D_V, FP8>,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return set_error(DSA_ERR_HIP, "sparse_mla_bwd(wide): LDS attribute: %s", hipGetErrorString(e));
   const int64_t nitems = p.B * p.S * p.G * p.ntiles;
   if (nitems >= (1ll << 31)) return set_error(DSA_ERR_INVALID_ARG, "sparse_mla_bwd(wide): grid too large");
-  hipLaunchKernelGGL((sparse_mla_bwd_wide_kernel<D_QK, D_V>), dim3((unsigned)nitems), dim3(256), lds, st, p);
+  hipLaunchKernelGGL((sparse_mla_bwd_wide_kernel<D_QK, D_V, FP8>), dim3((unsigned)nitems), dim3(256), lds, st, p);
   return check_launch("sparse_mla_bwd_main(wide)");
 }
 
-int launch_bwd_main_wide(const BwdParams &p, int64_t d_qk, int64_t d_v, hipStream_t st) {
-  if (d_qk == 576 && d_v == 512) return launch_bwd_wide_t<576, 512>(p, st);
-  if (d_qk == 576 && d_v == 576) return launch_bwd_wide_t<576, 576>(p, st);
+int launch_bwd_main_wide(const BwdParams &p, int64_t d_qk, int64_t d_v, bool fp8, hipStream_t st) {
+  if (d_qk == 576 && d_v == 512) return fp8 ? launch_bwd_wide_t<576, 512, true>(p, st) : launch_bwd_wide_t<576, 512, false>(p, st);
+  if (d_qk == 576 && d_v == 576) return fp8 ? launch_bwd_wide_t<576, 576, true>(p, st) : launch_bwd_wide_t<576, 576, false>(p, st);
   return set_error(DSA_ERR_UNSUPPORTED, "sparse_mla_bwd(wide): no kernel for d_qk=%lld d_v=%lld", (long long)d_qk,
                    (long long)d_v);
 }

@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from cppmega_amd import synthetic
-from cppmega_amd.sparse_mla_ops import (SparseMLA, sparse_mla_as_unfused_dsa, sparse_mla_bwd,
+from cppmega_amd.sparse_mla_ops import (SparseMLA, sparse_mla_as_unfused_dsa, sparse_mla_bwd, sparse_mla_bwd_fp8,
                                         sparse_mla_fwd_fp8_interface, sparse_mla_fwd_interface)
 from oracle import fp8 as ofp8
 from oracle import sparse_mla as orc
@@ -152,8 +152,8 @@ def test_wide_edge_indices(dev):
 
 
 @pytest.mark.parametrize("outliers", [False, True])
-def test_wide_fp8_fwd_matches_fp8_oracle(dev, outliers):
-    """e4m3 wide forward vs the FP8 oracle on identical quantised inputs.  With
+def test_wide_fp8_fwd_bwd_match_fp8_oracle(dev, outliers):
+    """e4m3 wide forward and backward vs the FP8 oracle on identical quantised inputs.  With
     1% x20 outliers a one-ulp bf16 rounding flip of a P weight (from fp32
     reassociation of a 576-term score) is multiplied by a ~20-sigma V entry, so
     out is held to the mostly-close bar there; LSE keeps the plain bar."""
@@ -171,8 +171,18 @@ def test_wide_fp8_fwd_matches_fp8_oracle(dev, outliers):
     out, lse = sparse_mla_fwd_fp8_interface(q8.to(dev), k8.to(dev), idx.to(dev), q_scale=qsv.to(dev),
                                             kv_scale=ksv.to(dev), sm_scale=D ** -0.5, d_v=DV)
     ro, rl = orc.sparse_mla_fwd(q8, k8, idx, D ** -0.5, DV, q_scale=qsv, kv_scale=ksv)
-    (assert_mostly_close if outliers else assert_close)(out, ro, what="fp8 out")
+    check = assert_mostly_close if outliers else assert_close
+    check(out, ro, what="fp8 out")
     assert_close(lse, rl, what="fp8 lse2")
+    do = torch.randn((B, S, H, DV), generator=torch.Generator().manual_seed(80)).to(torch.bfloat16)
+    dq, dkv = sparse_mla_bwd_fp8(q8.to(dev), k8.to(dev), qsv.to(dev), ksv.to(dev), out, do.to(dev), idx.to(dev),
+                                 lse, sm_scale=D ** -0.5)
+    rdq, rdkv = orc.sparse_mla_bwd(q8, k8, out.cpu(), do, idx, lse.cpu(), D ** -0.5, DV, q_scale=qsv, kv_scale=ksv)
+    check(dq, rdq, what="fp8 dq")
+    check(dkv, rdkv, what="fp8 dkv")
+    dq2, dkv2 = sparse_mla_bwd_fp8(q8.to(dev), k8.to(dev), qsv.to(dev), ksv.to(dev), out, do.to(dev), idx.to(dev),
+                                   lse, sm_scale=D ** -0.5)
+    assert torch.equal(dq, dq2) and torch.equal(dkv, dkv2)
 
 
 def test_cfg5_fwd_full_scale(dev):
