@@ -16,9 +16,14 @@ for the single kernel with the longest median duration; its `traffic` field is
 read from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed under
 profiles/ (null when that kernel has no such summary).
 
+After the timed steps the cfg5 long-context kernels (SparseMLA forward at
+h=128, d_qk=576, d_v=512, topk=2048; e4m3 indexer at h=64, d=128; top-2048
+over s=16384) are timed on device-generated inputs and reported under "cfg5"
+(not part of `value`).
+
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
-                       [--calib-copy-mib N]   (one N MiB device copy before timing,
-                                               the calibration kernel of PMC runs)
+                       [--no-cfg5] [--calib-copy-mib N]   (one N MiB device copy
+                       before timing, the calibration kernel of PMC runs)
 """
 from __future__ import annotations
 
@@ -45,6 +50,89 @@ H_IDX, D_IDX = 16, 64
 ENTRIES = B * S * TOPK                 # (token, slot) pairs of the backward (one kv group)
 KV_ROWS = B * S                        # dKV rows
 CSR_CHUNKS = (S + 15) // 16            # inverse-index chunks per batch (16 tokens each)
+
+
+# cfg5: DeepSeek-V3.2-shaped long context (forward + indexer), reported beside the headline
+C5_S, C5_H, C5_DQK, C5_DV, C5_TOPK = 16384, 128, 576, 512, 2048
+C5_HIDX, C5_DIDX = 64, 128
+
+
+def cfg5_work():
+    """Algorithmic work of the cfg5 kernels: (flops, bytes, peak kind)."""
+    s = C5_S
+    return {
+        "fwd": (2 * s * C5_H * C5_TOPK * (C5_DQK + C5_DV), 0, "bf16"),
+        "indexer_fp8": (2 * C5_HIDX * C5_DIDX * s * (s + 1) // 2, 0, "fp8"),
+        "topk": (0, 4 * s * (s + 1) // 2 + 4 * s * C5_TOPK, None),
+    }
+
+
+def measure_cfg5(dev, reps=3):
+    """Median kernel times of the cfg5 forward (h=128, d_qk=576, d_v=512,
+    topk=2048, bf16), the e4m3 indexer (h=64, d=128, causal) and the top-2048
+    selection over s=16384, on inputs generated on the device with a fixed
+    seed.  Each figure is the median of `reps` event-timed launches."""
+    import torch
+
+    from cppmega_amd.dsa_indexer_fused_patch import CAUSAL_LOWER, index_scores
+    from cppmega_amd.dsa_topk import topk_indices
+    from cppmega_amd.sparse_mla_ops import sparse_mla_fwd_interface, tensorwise_quantize
+
+    gen = torch.Generator(device=dev).manual_seed(5)
+    S5 = C5_S
+    q = (torch.randn((1, S5, C5_H, C5_DQK), generator=gen, device=dev) * 0.5).to(torch.bfloat16)
+    kv = (torch.randn((1, S5, 1, C5_DQK), generator=gen, device=dev) * 0.5).to(torch.bfloat16)
+    idx = torch.full((1, S5, 1, C5_TOPK), -1, dtype=torch.int32, device=dev)
+    cols = torch.arange(S5, device=dev)
+    for t0 in range(0, S5, 2048):
+        t = torch.arange(t0, t0 + 2048, device=dev)[:, None]
+        keys = torch.rand((2048, S5), generator=gen, device=dev)
+        keys = torch.where(cols[None, :] <= t, keys, torch.full_like(keys, -1.0))
+        val, ix = keys.topk(C5_TOPK, dim=-1)
+        ix = torch.where(val >= 0, ix, torch.full_like(ix, S5 + 1)).sort(dim=-1).values
+        idx[0, t0:t0 + 2048, 0] = torch.where(ix > S5, torch.full_like(ix, -1), ix).to(torch.int32)
+        del keys, val, ix
+    iq = torch.randn((S5, 1, C5_HIDX, C5_DIDX), generator=gen, device=dev).to(torch.bfloat16)
+    ik = torch.randn((S5, 1, C5_DIDX), generator=gen, device=dev).to(torch.bfloat16)
+    iw = torch.randn((S5, 1, C5_HIDX), generator=gen, device=dev) / C5_HIDX ** 0.5
+    iq8, iqs = tensorwise_quantize(iq)
+    ik8, iks = tensorwise_quantize(ik)
+    del iq, ik
+    scores = torch.empty((1, S5, S5), dtype=torch.float32, device=dev)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            a, b_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b_.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b_))
+        return sorted(ts)[len(ts) // 2] / 1e3
+
+    t = {
+        "fwd": timed(lambda: sparse_mla_fwd_interface(q, kv, idx, sm_scale=C5_DQK ** -0.5, d_v=C5_DV)),
+        "indexer_fp8": timed(lambda: index_scores(iq8, iw, ik8, use_relu=True, causal=CAUSAL_LOWER,
+                                                  q_scale=iqs, k_scale=iks, out=scores)),
+        "topk": timed(lambda: topk_indices(scores, C5_TOPK, causal=True)),
+    }
+    res = {}
+    for k, (fl, by, kind) in cfg5_work().items():
+        e = {"ms": round(t[k] * 1e3, 3)}
+        if fl:
+            peak = PEAK_FP8_TFLOPS if kind == "fp8" else PEAK_BF16_TFLOPS
+            tf = fl / t[k] / 1e12
+            e.update({"bound": "mfma", "tflops": round(tf, 1), "peak": peak, "frac": round(tf / peak, 4)})
+        else:
+            gbs = by / t[k] / 1e9
+            e.update({"bound": "hbm", "gbs": round(gbs, 1), "peak": PEAK_HBM_GBS, "frac": round(gbs / PEAK_HBM_GBS, 4)})
+        res[k] = e
+    del q, kv, idx, iq8, ik8, iw, scores
+    torch.cuda.empty_cache()
+    return res
 
 
 def algorithmic_work():
@@ -134,6 +222,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=4096)
     ap.add_argument("--calib-copy-mib", type=int, default=0)
+    ap.add_argument("--no-cfg5", action="store_true", help="skip the cfg5 (long-context) kernel timings")
     args = ap.parse_args()
     if args.steps > 256:
         print("--steps must be at most 256 (the stage-timing ring holds 256 calls)", file=sys.stderr)
@@ -228,6 +317,8 @@ def main():
     t_att = kernels["fwd"]["ms"] + kernels["bwd"]["ms"]
     amortised = 9 * tokens / ((3 * t_idx + 9 * t_att) / 1e3)
 
+    cfg5 = None if args.no_cfg5 else measure_cfg5(dev)
+
     cpu = None
     if not args.no_cpu_baseline:
         from oracle.cpu_baseline import time_cpu_baseline
@@ -257,6 +348,9 @@ def main():
         "cpu_baseline": cpu,
         "kernels": kernels,
         "indexcache_amortised_tokens_per_s": round(amortised, 1),
+        "cfg5": ({"workload": f"s={C5_S} h={C5_H} d_qk={C5_DQK} d_v={C5_DV} topk={C5_TOPK} SparseMLA fwd (bf16), "
+                              f"indexer h={C5_HIDX} d={C5_DIDX} e4m3 causal, top-{C5_TOPK}",
+                  "kernels": cfg5} if cfg5 is not None else None),
     }
     print(json.dumps(line), flush=True)
 
