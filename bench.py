@@ -191,7 +191,7 @@ def roofline_entry(w, seconds):
 # rocprofv3 kernel-name prefix of each timed kernel (for the traffic summary)
 KERNEL_NAMES = {
     "indexer": "indexer_score_kernel",
-    "topk": "topk_select_kernel",
+    "topk": "topk_wave_kernel",
     "fwd": "sparse_mla_fwd_kernel",
     "bwd_main": "sparse_mla_bwd_main_kernel",
     "bwd_reduce": "dkv_reduce_kernel",
