@@ -32,8 +32,17 @@ HIP_FLAGS = [
 # Per-file additions.  The indexer's epilogue is one max + one fma per score
 # element; with IEEE mode off and NaN inputs declared undefined, fmaxf is a
 # single v_max_f32 instead of a canonicalise + max pair.
+#
+# The SparseMLA kernels keep loop-carried MFMA accumulators (O, dQ) that the
+# online softmax also touches with VALU ops; LLVM's default AGPR form for MFMA
+# results then copies them between AGPRs and VGPRs on every block.  The VGPR
+# form keeps them in VGPRs (gfx950 MFMAs read and write either file).
+_MFMA_VGPR = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
 FILE_FLAGS = {
     "indexer_score.hip": ["-fno-honor-nans", "-mno-amdgpu-ieee"],
+    "sparse_mla_fwd.hip": _MFMA_VGPR,
+    "sparse_mla_bwd.hip": _MFMA_VGPR,
+    "sparse_mla_wide.hip": _MFMA_VGPR,
 }
 
 
