@@ -176,6 +176,21 @@ __device__ __forceinline__ i32x4 tr_operand(const unsigned char *T, int stride, 
   return i32x4{r0[0], r0[1], r1[0], r1[1]};
 }
 
+// tr_operand with (h_step, g_step) = (8, 4) and the four 4-column groups of
+// each 16-column half permuted, so that accumulator row m = 8i + 4g + j of the
+// product maps to column col0 + 16(i >> 1) + 8g + 4(i & 1) + j: a lane's 16
+// accumulator values then cover two runs of 8 consecutive columns (16-byte
+// stores), and the two lane halves' runs are adjacent.
+__device__ __forceinline__ i32x4 tr_operand_perm(const unsigned char *T, int stride, int col0, int rows_base) {
+  const int lane = lane_id();
+  const int k = lane & 15, j = k >> 2, q = k & 3, cb = (lane >> 4) & 1, gg = lane >> 5;
+  const unsigned char *base =
+      T + (col0 + cb * 16 + 8 * (q & 1) + 4 * (q >> 1)) * 2 + (rows_base + gg * 4 + j) * stride;
+  const i32x2 r0 = ds_read_tr16(base);
+  const i32x2 r1 = ds_read_tr16(base + 8 * stride);
+  return i32x4{r0[0], r0[1], r1[0], r1[1]};
+}
+
 __device__ __forceinline__ i32x4 ld_global_16(const void *p) {
   return *reinterpret_cast<const i32x4 *>(p);
 }

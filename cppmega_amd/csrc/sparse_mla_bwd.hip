@@ -31,8 +31,9 @@
 //   c^T[d][slot] = Q^T dS^T + dO^T P^T
 //                                 M = d, N = slot, K = head: dS / P straight
 //                                 from the accumulator registers, Q^T / dO^T
-//                                 transposed-read from row-major Q / dO tiles;
-//                                 each lane gets 4 consecutive d of one slot;
+//                                 transposed-read from row-major Q / dO tiles
+//                                 with permuted column groups, so each lane
+//                                 gets runs of 8 consecutive d of one slot;
 //   dQ^T[d][head] = K^T dS^T      M = d, N = head, K = slot: both operands
 //                                 transposed-read (K tile, dS[slot][head] tile).
 #include "dsa_common.hpp"
@@ -66,7 +67,8 @@ struct BwdCfg {
   static constexpr int KD_BYTES = FP8 ? 32 * KD_STRIDE : 0;
   static constexpr int DS_STRIDE = 32 * 2 + 32;          // dS[slot][head] bf16
   static constexpr int DS_BYTES = 32 * DS_STRIDE;
-  static constexpr int CS_STRIDE = D_QK * 2 + 32;        // staged fp16 partial rows (over Kl, Kd)
+  static constexpr int CS_STRIDE = D_QK * 2 + 16;        // staged fp16 partial rows (over Kl, Kd): 16-byte
+                                                         // writes of 32 rows land in distinct banks
   static constexpr int ROW_CHUNKS = D_QK * 2 / 16;       // 16-byte chunks per fp16 partial row
   static_assert((32 * ROW_CHUNKS) % 64 == 0, "whole store rounds");
   static constexpr int W_KD = KL_BYTES;
@@ -304,20 +306,20 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
       for (int a = 0; a < 16; ++a) cacc[dt][a] = 0.0f;
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc) {
-        const i32x4 av = tr_operand(QL, C::QL_STRIDE, dt * 32, 16 * kc, 8, 4);
+        const i32x4 av = tr_operand_perm(QL, C::QL_STRIDE, dt * 32, 16 * kc);
         cacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(av), dsB[kc], cacc[dt], 0, 0, 0);
       }
       if (dt < C::DVT) {
 #pragma unroll
         for (int kc = 0; kc < 2; ++kc) {
-          const i32x4 av = tr_operand(DOL, C::DOL_STRIDE, dt * 32, 16 * kc, 8, 4);
+          const i32x4 av = tr_operand_perm(DOL, C::DOL_STRIDE, dt * 32, 16 * kc);
           cacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(av), pB[kc], cacc[dt], 0, 0, 0);
         }
       }
     }
 
     // ---- the slot's partial row, written at its CSR position ----
-    // lane: slot l32, d = dt*32 + 8i + 4*g32 + j.
+    // lane: slot l32, d = dt*32 + 16(i>>1) + 8*g32 + 4(i&1) + j (the permuted Q^T / dO^T columns).
     if constexpr (F32P) {
       // fp32 rows: the two lanes of a slot store adjacent 16-byte pieces
       unsigned char *dst = p.partials + ((int64_t)(wr ? pos : 0) * p.ntiles + tile) * (int64_t)(D_QK * 4);
@@ -325,7 +327,7 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
       for (int dt = 0; dt < C::DQT; ++dt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int d0 = dt * 32 + 8 * i + 4 * g32;
+          const int d0 = dt * 32 + 16 * (i >> 1) + 8 * g32 + 4 * (i & 1);
           if (wr)
             *reinterpret_cast<f32x4 *>(dst + d0 * 4) =
                 f32x4{cacc[dt][4 * i], cacc[dt][4 * i + 1], cacc[dt][4 * i + 2], cacc[dt][4 * i + 3]};
@@ -339,7 +341,7 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
       for (int dt = 0; dt < C::DQT; ++dt)
 #pragma unroll
         for (int a = 0; a < 16; ++a) amax = fmaxf(amax, fabsf(cacc[dt][a]));
-      amax = fmaxf(amax, xor32(amax));
+      amax = max_halves(amax);
       const int pexp = partial_row_exponent(amax);
       const float rscale = exp2i(pexp);
       wave_lds_sync();  // the dQ GEMM's reads of the K / dS tiles are complete
@@ -348,11 +350,13 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
 #pragma unroll
       for (int dt = 0; dt < C::DQT; ++dt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int d0 = dt * 32 + 8 * i + 4 * g32;
-          *reinterpret_cast<i32x2 *>(Cs + l32 * C::CS_STRIDE + d0 * 2) =
-              i32x2{(int)pack_f16x2(cacc[dt][4 * i] * rscale, cacc[dt][4 * i + 1] * rscale),
-                    (int)pack_f16x2(cacc[dt][4 * i + 2] * rscale, cacc[dt][4 * i + 3] * rscale)};
+        for (int s = 0; s < 2; ++s) {  // d = dt*32 + 16s + 8*g32 + (0..7): cacc[dt][8s .. 8s+7]
+          const int d0 = dt * 32 + 16 * s + 8 * g32;
+          *reinterpret_cast<i32x4 *>(Cs + l32 * C::CS_STRIDE + d0 * 2) =
+              i32x4{(int)pack_f16x2(cacc[dt][8 * s] * rscale, cacc[dt][8 * s + 1] * rscale),
+                    (int)pack_f16x2(cacc[dt][8 * s + 2] * rscale, cacc[dt][8 * s + 3] * rscale),
+                    (int)pack_f16x2(cacc[dt][8 * s + 4] * rscale, cacc[dt][8 * s + 5] * rscale),
+                    (int)pack_f16x2(cacc[dt][8 * s + 6] * rscale, cacc[dt][8 * s + 7] * rscale)};
         }
       if (g32 == 0) Lpos[l32] = wr ? pos : -1;
       if (g32 == 0 && wr) p.partial_exp[(uint64_t)(uint32_t)pos * (uint32_t)p.ntiles + tile] = (int8_t)pexp;
