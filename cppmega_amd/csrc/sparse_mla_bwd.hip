@@ -119,6 +119,7 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
   const int64_t head0 = tok * p.H + g * p.hpg + tile * 32;  // q row of head 0 of this tile
   const int nheads = p.hpg - tile * 32 < 32 ? p.hpg - tile * 32 : 32;
   const int64_t entry0 = (tok * p.G + g) * p.topk;  // entry (CSR key) of slot 0
+  const int64_t n_entries = p.B * p.S * p.G * p.topk;
   const int32_t *idx_row = p.idx + entry0;
   const unsigned char *kv_b = p.kv + ((b * p.S_kv) * p.G + g) * Gat::ROWB;
   const float *kv_scale_b = FP8 ? p.kv_scale + b * p.S_kv : nullptr;
@@ -223,7 +224,7 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
     const bool valid = idx_cur >= 0;  // slot slot0 + l32
     int32_t pos = -1;
     if (valid) pos = p.pos_of[entry0 + slot0 + l32];
-    const bool wr = valid && pos >= 0;  // (pos is always set for a valid slot; the test is a guard)
+    const bool wr = valid && pos >= 0 && pos < n_entries;  // (always true for a valid slot; a guard)
     wave_lds_sync();
     const int idx_nn = load_slot_index(idx_row, blk + 2 * C::WPT, l32, p.topk, p.S_kv);
     if (blk + C::WPT < nblk) gather_issue<Gat>(rg, kv_b, kv_scale_b, idx_nxt, row_pitch);
@@ -419,8 +420,8 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct BwdWorkspace {
-  size_t partials, pexp, hist, gsum, tot, rowptr, pos_of, total;
-  int CT, NC, NQ;
+  size_t partials, pexp, mask, base, dup, gsum, tot, rowptr, pos_of, total;
+  int NC, NQ;
 };
 
 static BwdWorkspace bwd_layout(int64_t B, int64_t S, int64_t S_kv, int64_t H, int64_t G, int64_t D_qk,
@@ -430,7 +431,7 @@ static BwdWorkspace bwd_layout(int64_t B, int64_t S, int64_t S_kv, int64_t H, in
   const size_t entries = (size_t)B * S * G * topk;
   const int64_t R = S_kv * G;
   BwdWorkspace L;
-  csr_plan(S, R, &L.CT, &L.NC, &L.NQ);
+  csr_plan(S, &L.NC, &L.NQ);
   // wide heads always keep fp32 partial rows
   const size_t psz = ((flags & DSA_BWD_FP32_PARTIALS) || D_qk > 256) ? 4 : 2;
   size_t off = 0;
@@ -438,8 +439,12 @@ static BwdWorkspace bwd_layout(int64_t B, int64_t S, int64_t S_kv, int64_t H, in
   off += align256(entries * ntiles * D_qk * psz);
   L.pexp = off;
   off += align256(entries * ntiles);
-  L.hist = off;
+  L.mask = off;
   off += align256((size_t)B * L.NC * R * 4);
+  L.base = off;
+  off += align256((size_t)B * L.NC * R * 4);
+  L.dup = off;
+  off += align256((size_t)B * L.NC * 4);
   L.gsum = off;
   off += align256((size_t)B * L.NQ * R * 4);
   L.tot = off;
@@ -548,7 +553,9 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
 
   CsrParams cp;
   cp.idx = indices;
-  cp.hist = reinterpret_cast<int32_t *>(ws + L.hist);
+  cp.mask = reinterpret_cast<uint32_t *>(ws + L.mask);
+  cp.base = reinterpret_cast<int32_t *>(ws + L.base);
+  cp.dup = reinterpret_cast<int32_t *>(ws + L.dup);
   cp.tot = reinterpret_cast<int32_t *>(ws + L.tot);
   cp.rowptr = reinterpret_cast<int32_t *>(ws + L.rowptr);
   cp.pos_of = reinterpret_cast<int32_t *>(ws + L.pos_of);
@@ -558,7 +565,6 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
   cp.topk = topk;
   cp.R = R;
   cp.gsum = reinterpret_cast<int32_t *>(ws + L.gsum);
-  cp.CT = L.CT;
   cp.NC = L.NC;
   cp.NQ = L.NQ;
   stage_begin(st);

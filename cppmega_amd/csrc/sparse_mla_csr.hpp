@@ -10,29 +10,41 @@ namespace dsa {
 // Inverse index: stable counting sort of entries by kv row
 // ---------------------------------------------------------------------------
 // Entry e = ((b*S + t)*G + g)*topk + slot; its row (within batch b) is
-// r = j*G + g for a valid index j.  Tokens are grouped into chunks of CT
+// r = j*G + g for a valid index j.  Tokens are grouped into chunks of 32
 // within one batch (NC chunks per batch); chunks form groups of CG = 16.
-//   csr_hist     hist[b][c][r]  = entries of chunk c in row r
-//   csr_gsum     gsum[b][q][r]  = sum of hist over the chunks of group q
+//   csr_mask     mask[b][c][r]  = bit tl set when token 32c + tl references
+//                                 row r; dup[b][c] = some (token, group)
+//                                 references one row twice, and then the exact
+//                                 counts go to base[b][c][r] (a bit cannot
+//                                 count repeats); count(c, r) below is that
+//                                 count or popcount(mask)
+//   csr_gsum     gsum[b][q][r]  = entries of row r in the chunks of group q
 //   csr_rows     tot[b*R + r]   = row total; gsum -> exclusive prefix over groups
 //   csr_scan     rowptr         = exclusive prefix of tot
-//   csr_bases    hist[b][c][r] <- rowptr + entries of row r in earlier chunks
-//   csr_scatter  pos_of[e]      = CSR position of entry e, tokens in order (stable)
-// Every thread touches at most CG chunks, so no kernel walks a long serial
-// chain of global loads.
+//   csr_bases    base[b][c][r]  = rowptr + entries of row r in earlier chunks
+//   csr_scatter  pos_of[e]      = base + popcount of the earlier tokens' bits:
+//                                 entries of a row in ascending entry order
+// Without repeats a row's entries inside a chunk are ordered by token alone,
+// so every entry's position is computed independently; a chunk with a repeat
+// is placed by one thread in entry order instead (the same positions the
+// stable sort defines).  Every thread touches at most CG chunks, so no kernel
+// walks a long serial chain of global loads.
 
 constexpr int kChunkGroup = 16;
+constexpr int kChunkTokens = 32;  // tokens per chunk: one bit each in a 32-bit mask
 
 struct CsrParams {
   const int32_t *idx;
-  int32_t *hist;    // [B][NC][R]
+  uint32_t *mask;   // [B][NC][R]
+  int32_t *base;    // [B][NC][R]
+  int32_t *dup;     // [B][NC]
   int32_t *gsum;    // [B][NQ][R]
   int32_t *tot;     // [B*R]
   int32_t *rowptr;  // [B*R + 1]
   int32_t *pos_of;  // [entries]: CSR position of each entry, -1 for a masked slot
   int64_t S, S_kv, G, topk;
   int64_t R;        // rows per batch = S_kv * G
-  int CT, NC, NQ;   // tokens per chunk, chunks per batch, chunk groups per batch
+  int NC, NQ;       // chunks per batch, chunk groups per batch
 };
 
 __global__ void fill_i32_kernel(int32_t *p, int64_t n, int32_t v) {
@@ -40,39 +52,84 @@ __global__ void fill_i32_kernel(int32_t *p, int64_t n, int32_t v) {
     p[i] = v;
 }
 
-// grid (NC, B), 256 threads, dynamic LDS = R ints
-__global__ void __launch_bounds__(256) csr_hist_kernel(const CsrParams p) {
-  extern __shared__ int32_t cnt[];
+// grid (NC, B), 256 threads, dynamic LDS = R words
+__global__ void __launch_bounds__(256) csr_mask_kernel(const CsrParams p) {
+  extern __shared__ uint32_t mk[];
+  __shared__ int dflag;
   const int c = blockIdx.x;
   const int64_t b = blockIdx.y;
-  for (int64_t r = threadIdx.x; r < p.R; r += 256) cnt[r] = 0;
+  const int tid = threadIdx.x;
+  for (int64_t r = tid; r < p.R; r += 256) mk[r] = 0u;
+  if (tid == 0) dflag = 0;
   __syncthreads();
-  const int64_t t0 = (int64_t)c * p.CT;
-  const int64_t t1 = t0 + p.CT < p.S ? t0 + p.CT : p.S;
-  const int64_t e0 = ((b * p.S + t0) * p.G) * p.topk;
-  const int64_t e1 = ((b * p.S + t1) * p.G) * p.topk;
-  for (int64_t e = e0 + threadIdx.x; e < e1; e += 256) {
-    const int32_t j = p.idx[e];
-    if (j >= 0 && j < p.S_kv) {
-      const int64_t g = (e / p.topk) % p.G;
-      atomicAdd(&cnt[j * p.G + g], 1);
+  const int64_t t0 = (int64_t)c * kChunkTokens;
+  const int64_t t1 = t0 + kChunkTokens < p.S ? t0 + kChunkTokens : p.S;
+  const int64_t nseg = (t1 - t0) * p.G;
+  const int32_t *seg_idx = p.idx + ((b * p.S + t0) * p.G) * p.topk;
+  // work item w = (segment w / spt, slots 256 (w % spt) + tid): block-uniform,
+  // eight loads in flight
+  const int spt = (int)((p.topk + 255) / 256);
+  const int nw = (int)nseg * spt;
+  const int G = (int)p.G;
+  int dup = 0;
+  for (int w0 = 0; w0 < nw; w0 += 8) {
+    int32_t j[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int w = w0 + u, sg = spt == 1 ? w : w / spt, s = (spt == 1 ? 0 : w % spt) * 256 + tid;
+      j[u] = (w < nw && s < p.topk) ? seg_idx[(int64_t)sg * p.topk + s] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int w = w0 + u, sg = spt == 1 ? w : w / spt;
+      if (j[u] >= 0 && j[u] < p.S_kv) {
+        const uint32_t bit = 1u << (G == 1 ? sg : sg / G);
+        const uint32_t old = atomicOr(&mk[(int64_t)j[u] * G + (G == 1 ? 0 : sg % G)], bit);
+        dup |= (old & bit) != 0u;
+      }
     }
   }
+  if (dup) dflag = 1;  // benign race: every writer stores 1
   __syncthreads();
-  int32_t *h = p.hist + (b * p.NC + c) * p.R;
-  for (int64_t r = threadIdx.x; r < p.R; r += 256) h[r] = cnt[r];
+  uint32_t *m = p.mask + (b * p.NC + c) * p.R;
+  for (int64_t r = tid; r < p.R; r += 256) m[r] = mk[r];
+  if (tid == 0) p.dup[b * p.NC + c] = dflag;
+  if (dflag) {  // block-uniform: exact per-row counts of this chunk
+    __syncthreads();
+    int32_t *cnt = reinterpret_cast<int32_t *>(mk);
+    for (int64_t r = tid; r < p.R; r += 256) cnt[r] = 0;
+    __syncthreads();
+    for (int64_t sg = 0; sg < nseg; ++sg) {
+      const int64_t g = sg % p.G;
+      for (int64_t s = tid; s < p.topk; s += 256) {
+        const int32_t j = seg_idx[sg * p.topk + s];
+        if (j >= 0 && j < p.S_kv) atomicAdd(&cnt[j * p.G + g], 1);
+      }
+    }
+    __syncthreads();
+    int32_t *dst = p.base + (b * p.NC + c) * p.R;
+    for (int64_t r = tid; r < p.R; r += 256) dst[r] = cnt[r];
+  }
 }
 
-// one thread per (b, q, r): sum of hist over the chunks of group q
+// Entries of row r in chunk c of batch b (mask popcount, or the exact count
+// the mask kernel left in base[] for a chunk with repeats).
+__device__ __forceinline__ int32_t chunk_count(const CsrParams &p, int64_t b, int c, int64_t r) {
+  const int64_t cell = (b * p.NC + c) * p.R + r;
+  return p.dup[b * p.NC + c] ? p.base[cell] : (int32_t)__popc(p.mask[cell]);
+}
+
+// grid (ceil(R / 256), B * NQ): one thread per (b, q, r): entries of row r in
+// the chunks of group q ((b, q) is uniform per workgroup)
 __global__ void csr_gsum_kernel(const CsrParams p, int64_t B) {
-  const int64_t x = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (x >= B * p.NQ * p.R) return;
-  const int64_t r = x % p.R, bq = x / p.R, q = bq % p.NQ, b = bq / p.NQ;
+  const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (r >= p.R) return;
+  const int64_t bq = blockIdx.y, q = bq % p.NQ, b = bq / p.NQ;
+  const int64_t x = bq * p.R + r;
   const int c0 = (int)q * kChunkGroup;
-  const int32_t *h = p.hist + (b * p.NC + c0) * p.R + r;
   int32_t v[kChunkGroup];
 #pragma unroll
-  for (int k = 0; k < kChunkGroup; ++k) v[k] = (c0 + k < p.NC) ? h[(int64_t)k * p.R] : 0;
+  for (int k = 0; k < kChunkGroup; ++k) v[k] = (c0 + k < p.NC) ? chunk_count(p, b, c0 + k, r) : 0;
   int32_t s = 0;
 #pragma unroll
   for (int k = 0; k < kChunkGroup; ++k) s += v[k];
@@ -94,130 +151,147 @@ __global__ void csr_rows_kernel(const CsrParams p, int64_t B) {
   p.tot[x] = run;
 }
 
-// Exclusive scan of cnt[0..n) into rowptr[0..n] with one 1024-thread workgroup.
+// Exclusive scan of cnt[0..n) into rowptr[0..n] with one 1024-thread
+// workgroup: tiles of 1024 x 8 elements, each thread scanning 8 contiguous
+// elements in registers (two 16-byte loads when aligned), a wave scan and a
+// cross-wave scan per tile, the running total carried across tiles.
 __global__ void __launch_bounds__(1024) csr_scan_kernel(const int32_t *cnt, int32_t *rowptr, int64_t n) {
   __shared__ int32_t wsum[16];
-  const int tid = threadIdx.x;
-  const int64_t per = (n + 1023) / 1024;
-  const int64_t lo = tid * per, hi = lo + per < n ? lo + per : n;
-  int32_t s = 0;
-  for (int64_t i = lo; i < hi; ++i) s += cnt[i];
-  int32_t v = s;
-  const int lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  int32_t carry = 0;
+  for (int64_t t0 = 0; t0 < n; t0 += 1024 * 8) {
+    const int64_t lo = t0 + (int64_t)tid * 8;
+    int32_t v[8];
+    if (lo + 8 <= n) {
+      const i32x4 a = *reinterpret_cast<const i32x4 *>(cnt + lo);
+      const i32x4 c = *reinterpret_cast<const i32x4 *>(cnt + lo + 4);
+      v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
+      v[4] = c[0]; v[5] = c[1]; v[6] = c[2]; v[7] = c[3];
+    } else {
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int32_t o = __shfl_up(v, off, 64);
-    if (lane >= off) v += o;
-  }
-  if (lane == 63) wsum[tid >> 6] = v;
-  __syncthreads();
-  if (tid < 16) {
-    int32_t x = wsum[tid];
-    for (int off = 1; off < 16; off <<= 1) {
-      const int32_t o = __shfl_up(x, off, 16);
-      if ((tid & 15) >= off) x += o;
+      for (int k = 0; k < 8; ++k) v[k] = lo + k < n ? cnt[lo + k] : 0;
     }
-    wsum[tid] = x;
+    int32_t s = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s += v[k];
+    int32_t x = s;  // inclusive wave scan
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int32_t o = __shfl_up(x, off, 64);
+      if (lane >= off) x += o;
+    }
+    if (lane == 63) wsum[wv] = x;
+    __syncthreads();
+    if (tid < 16) {
+      int32_t y = wsum[tid];
+      for (int off = 1; off < 16; off <<= 1) {
+        const int32_t o = __shfl_up(y, off, 16);
+        if ((tid & 15) >= off) y += o;
+      }
+      wsum[tid] = y;
+    }
+    __syncthreads();
+    int32_t run = carry + (wv > 0 ? wsum[wv - 1] : 0) + x - s;
+    const int32_t tile_total = wsum[15];
+    int32_t o[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      o[k] = run;
+      run += v[k];
+    }
+    if (lo + 8 <= n) {
+      *reinterpret_cast<i32x4 *>(rowptr + lo) = i32x4{o[0], o[1], o[2], o[3]};
+      *reinterpret_cast<i32x4 *>(rowptr + lo + 4) = i32x4{o[4], o[5], o[6], o[7]};
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (lo + k < n) rowptr[lo + k] = o[k];
+    }
+    carry += tile_total;
+    __syncthreads();  // wsum is reused by the next tile
   }
-  __syncthreads();
-  const int wv = tid >> 6;
-  int32_t run = (wv > 0 ? wsum[wv - 1] : 0) + v - s;
-  for (int64_t i = lo; i < hi; ++i) {
-    rowptr[i] = run;
-    run += cnt[i];
-  }
-  if (tid == 1023) rowptr[n] = wsum[15];
+  if (tid == 0) rowptr[n] = carry;
 }
 
-// one thread per (b, q, r): hist[b][c][r] <- absolute start of chunk c's entries of row r
+// grid (ceil(R / 256), B * NQ): one thread per (b, q, r): base[b][c][r] =
+// absolute start of chunk c's entries of row r
 __global__ void csr_bases_kernel(const CsrParams p, int64_t B) {
-  const int64_t x = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (x >= B * p.NQ * p.R) return;
-  const int64_t r = x % p.R, bq = x / p.R, q = bq % p.NQ, b = bq / p.NQ;
+  const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (r >= p.R) return;
+  const int64_t bq = blockIdx.y, q = bq % p.NQ, b = bq / p.NQ;
+  const int64_t x = bq * p.R + r;
   const int c0 = (int)q * kChunkGroup;
-  int32_t *h = p.hist + (b * p.NC + c0) * p.R + r;
-  int32_t v[kChunkGroup];
+  int32_t *bs = p.base + (b * p.NC + c0) * p.R + r;
+  int32_t v[kChunkGroup];  // all counts are read before any base overwrites one
 #pragma unroll
-  for (int k = 0; k < kChunkGroup; ++k) v[k] = (c0 + k < p.NC) ? h[(int64_t)k * p.R] : 0;
+  for (int k = 0; k < kChunkGroup; ++k) v[k] = (c0 + k < p.NC) ? chunk_count(p, b, c0 + k, r) : 0;
   int32_t run = p.rowptr[b * p.R + r] + p.gsum[x];
 #pragma unroll
   for (int k = 0; k < kChunkGroup; ++k) {
-    if (c0 + k < p.NC) h[(int64_t)k * p.R] = run;
+    if (c0 + k < p.NC) bs[(int64_t)k * p.R] = run;
     run += v[k];
   }
 }
 
-// grid (NC, B), 256 threads, dynamic LDS = R ints + 2 * topk ints.  Tokens of
-// the chunk are placed one after another (their indices are staged in LDS one
-// token ahead); within a token the slots take LDS cursors concurrently, which
-// is order-independent as long as no row repeats inside the token.  A token
-// whose valid indices are not strictly increasing (so a row could repeat) is
-// placed by one thread in slot order instead.
+// grid (NC, B), 256 threads; dynamic LDS = R ints (cursors of the serial path).
 __global__ void __launch_bounds__(256) csr_scatter_kernel(const CsrParams p) {
-  extern __shared__ int32_t lds_i32[];
-  int32_t *cur = lds_i32;                 // [R]
-  int32_t *tidx = lds_i32 + p.R;          // [2][topk]
-  __shared__ int32_t wmax[4];
-  __shared__ int32_t unordered;
+  extern __shared__ int32_t cur[];
   const int c = blockIdx.x;
   const int64_t b = blockIdx.y;
-  const int tid = threadIdx.x, lane = lane_id(), w = wave_id();
-  const int32_t *h = p.hist + (b * p.NC + c) * p.R;
-  for (int64_t r = tid; r < p.R; r += 256) cur[r] = h[r];
-  const int64_t t0 = (int64_t)c * p.CT;
-  const int64_t t1 = t0 + p.CT < p.S ? t0 + p.CT : p.S;
-  const int64_t nseg = (t1 - t0) * p.G;  // (token, group) segments of topk entries
+  const int tid = threadIdx.x;
+  const int64_t t0 = (int64_t)c * kChunkTokens;
+  const int64_t t1 = t0 + kChunkTokens < p.S ? t0 + kChunkTokens : p.S;
+  const int64_t nseg = (t1 - t0) * p.G;
   const int64_t e_first = ((b * p.S + t0) * p.G) * p.topk;
-  // stage segment 0
-  for (int64_t s = tid; s < p.topk; s += 256) tidx[s] = p.idx[e_first + s];
-  for (int64_t sg = 0; sg < nseg; ++sg) {
-    const int64_t e0 = e_first + sg * p.topk;
-    const int64_t g = sg % p.G;
-    int32_t *cur_idx = tidx + (sg & 1) * p.topk;
-    int32_t *nxt_idx = tidx + ((sg + 1) & 1) * p.topk;
-    __syncthreads();  // segment sg staged; every thread is done with segment sg - 1
-    // (the first barrier of the check loop below orders this reset before
-    // any thread sets the flag)
-    if (tid == 0) unordered = 0;
-    // prefetch the next segment while this one is placed
-    if (sg + 1 < nseg)
-      for (int64_t s = tid; s < p.topk; s += 256) nxt_idx[s] = p.idx[e0 + p.topk + s];
-    // strictly-increasing check over valid slots, in chunks of 256 slots
-    int32_t carry = -1;
-    for (int64_t s0 = 0; s0 < p.topk; s0 += 256) {
-      const int64_t s = s0 + tid;
-      int32_t j = -1;
-      if (s < p.topk) {
-        j = cur_idx[s];
-        if (j < 0 || j >= p.S_kv) j = -1;
-      }
-      int32_t m = j;  // inclusive max-scan within the wave
+  const uint32_t *m = p.mask + (b * p.NC + c) * p.R;
+  const int32_t *bs = p.base + (b * p.NC + c) * p.R;
+  if (p.dup[b * p.NC + c] == 0) {
+    // row r of (token t0 + tl, group g): position = base + earlier tokens of the chunk in r;
+    // work items as in the mask kernel, eight in flight
+    const int spt = (int)((p.topk + 255) / 256);
+    const int nw = (int)nseg * spt;
+    const int G = (int)p.G;
+    for (int w0 = 0; w0 < nw; w0 += 8) {
+      int32_t j[8];
+      int64_t e[8];
 #pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const int32_t o = __shfl_up(m, off, 64);
-        if (lane >= off) m = max(m, o);
+      for (int u = 0; u < 8; ++u) {
+        const int w = w0 + u, sg = spt == 1 ? w : w / spt, s = (spt == 1 ? 0 : w % spt) * 256 + tid;
+        e[u] = (w < nw && s < p.topk) ? e_first + (int64_t)sg * p.topk + s : -1;
+        j[u] = e[u] >= 0 ? p.idx[e[u]] : -1;
       }
-      const int32_t m_prev_lane = __shfl_up(m, 1, 64);
-      if (lane == 63) wmax[w] = m;
-      __syncthreads();
-      int32_t before = carry;
-      for (int i = 0; i < w; ++i) before = max(before, wmax[i]);
-      const int32_t prev = lane > 0 ? max(before, m_prev_lane) : before;
-      if (j >= 0 && prev >= j) unordered = 1;
-      carry = max(carry, max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3])));
-      __syncthreads();
+      int32_t bv[8];
+      uint32_t mv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int w = w0 + u, sg = spt == 1 ? w : w / spt;
+        const bool ok = j[u] >= 0 && j[u] < p.S_kv;
+        const int64_t r = ok ? (int64_t)j[u] * G + (G == 1 ? 0 : sg % G) : 0;
+        bv[u] = ok ? bs[r] : -1;
+        mv[u] = ok ? m[r] : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int w = w0 + u, sg = spt == 1 ? w : w / spt;
+        if (e[u] >= 0) {
+          const bool ok = j[u] >= 0 && j[u] < p.S_kv;
+          const uint32_t below = (1u << (G == 1 ? sg : sg / G)) - 1u;
+          p.pos_of[e[u]] = ok ? bv[u] + __popc(mv[u] & below) : -1;
+        }
+      }
     }
-    if (!unordered) {
-      for (int64_t s = tid; s < p.topk; s += 256) {
-        const int32_t j = cur_idx[s];
-        int32_t pos = -1;
-        if (j >= 0 && j < p.S_kv) pos = atomicAdd(&cur[j * p.G + g], 1);
-        p.pos_of[e0 + s] = pos;
-      }
-    } else if (tid == 0) {
-      for (int64_t s = 0; s < p.topk; ++s) {
-        const int32_t j = cur_idx[s];
-        p.pos_of[e0 + s] = (j >= 0 && j < p.S_kv) ? cur[j * p.G + g]++ : -1;
+  } else {
+    // a row repeats inside a (token, group): one thread walks the entries in order
+    for (int64_t r = tid; r < p.R; r += 256) cur[r] = bs[r];
+    __syncthreads();
+    if (tid == 0) {
+      for (int64_t sg = 0; sg < nseg; ++sg) {
+        const int64_t g = sg % p.G;
+        for (int64_t s = 0; s < p.topk; ++s) {
+          const int64_t e = e_first + sg * p.topk + s;
+          const int32_t j = p.idx[e];
+          p.pos_of[e] = (j >= 0 && j < p.S_kv) ? cur[j * p.G + g]++ : -1;
+        }
       }
     }
   }
@@ -316,41 +390,33 @@ dkv_reduce_kernel(const int32_t *rowptr, const unsigned char *partials, const in
   }
 }
 
-// Chunking of the inverse index: 16 tokens per chunk unless the chunk
-// histogram (NC * R counters per batch) would exceed 2^24 entries.
-static void csr_plan(int64_t S, int64_t R, int *CT, int *NC, int *NQ) {
-  int ct = 16;
-  while ((int64_t)((S + ct - 1) / ct) * R > (1ll << 24) && ct < (1 << 20)) ct *= 2;
-  *CT = ct;
-  *NC = (int)((S + ct - 1) / ct);
+// Chunking of the inverse index: 32-token chunks (one mask bit per token).
+static void csr_plan(int64_t S, int *NC, int *NQ) {
+  *NC = (int)((S + kChunkTokens - 1) / kChunkTokens);
   *NQ = (*NC + kChunkGroup - 1) / kChunkGroup;
 }
 
-// Host side: build the inverse index (six stream-ordered kernels, no atomics
-// on global memory, no memset).
 static int launch_csr(const CsrParams &cp, int64_t B, hipStream_t st) {
-  const size_t hist_lds = (size_t)cp.R * 4;
-  const size_t scat_lds = hist_lds + 2 * (size_t)cp.topk * 4;
-  if (scat_lds > 160 * 1024)
-    return set_error(DSA_ERR_UNSUPPORTED, "sparse_mla_bwd: inverse index needs %zu bytes of LDS", scat_lds);
-  if (hist_lds > 64 * 1024 &&
-      hipFuncSetAttribute((const void *)csr_hist_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)hist_lds) != hipSuccess)
-    return set_error(DSA_ERR_HIP, "sparse_mla_bwd: csr LDS attribute failed");
-  if (scat_lds > 64 * 1024 &&
-      hipFuncSetAttribute((const void *)csr_scatter_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)scat_lds) != hipSuccess)
-    return set_error(DSA_ERR_HIP, "sparse_mla_bwd: csr LDS attribute failed");
+  const size_t lds = (size_t)cp.R * 4;
+  if (lds > 160 * 1024)
+    return set_error(DSA_ERR_UNSUPPORTED, "sparse_mla_bwd: inverse index needs %zu bytes of LDS", lds);
+  if (lds > 64 * 1024) {
+    if (hipFuncSetAttribute((const void *)csr_mask_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+            hipSuccess ||
+        hipFuncSetAttribute((const void *)csr_scatter_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess)
+      return set_error(DSA_ERR_HIP, "sparse_mla_bwd: csr LDS attribute failed");
+  }
   const int64_t rows = B * cp.R;
   const dim3 cgrid((unsigned)cp.NC, (unsigned)B);
   const unsigned rgrid = (unsigned)((rows + 255) / 256);
-  const unsigned qgrid = (unsigned)((B * cp.NQ * cp.R + 255) / 256);
-  hipLaunchKernelGGL(csr_hist_kernel, cgrid, dim3(256), hist_lds, st, cp);
-  hipLaunchKernelGGL(csr_gsum_kernel, dim3(qgrid), dim3(256), 0, st, cp, B);
+  const dim3 qgrid((unsigned)((cp.R + 255) / 256), (unsigned)(B * cp.NQ));
+  hipLaunchKernelGGL(csr_mask_kernel, cgrid, dim3(256), lds, st, cp);
+  hipLaunchKernelGGL(csr_gsum_kernel, qgrid, dim3(256), 0, st, cp, B);
   hipLaunchKernelGGL(csr_rows_kernel, dim3(rgrid), dim3(256), 0, st, cp, B);
   hipLaunchKernelGGL(csr_scan_kernel, dim3(1), dim3(1024), 0, st, cp.tot, cp.rowptr, rows);
-  hipLaunchKernelGGL(csr_bases_kernel, dim3(qgrid), dim3(256), 0, st, cp, B);
-  hipLaunchKernelGGL(csr_scatter_kernel, cgrid, dim3(256), scat_lds, st, cp);
+  hipLaunchKernelGGL(csr_bases_kernel, qgrid, dim3(256), 0, st, cp, B);
+  hipLaunchKernelGGL(csr_scatter_kernel, cgrid, dim3(256), lds, st, cp);
   return check_launch("sparse_mla_bwd(csr)");
 }
 

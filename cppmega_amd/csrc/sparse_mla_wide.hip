@@ -416,6 +416,7 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
   const int64_t head0 = tok * p.H + g * p.hpg + tile * 32;
   const int nheads = p.hpg - tile * 32 < 32 ? p.hpg - tile * 32 : 32;
   const int64_t entry0 = (tok * p.G + g) * p.topk;
+  const int64_t n_entries = p.B * p.S * p.G * p.topk;
   const int32_t *idx_row = p.idx + entry0;
   const unsigned char *kv_b = p.kv + ((b * p.S_kv) * p.G + g) * C::ROWB;
   const float *kv_scale_b = FP8 ? p.kv_scale + b * p.S_kv : nullptr;
@@ -510,7 +511,7 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
     const bool valid = idx_cur >= 0;  // slot slot0 + l32
     int32_t pos = -1;
     if (valid) pos = p.pos_of[entry0 + slot0 + l32];
-    const bool wr = valid && pos >= 0;
+    const bool wr = valid && pos >= 0 && pos < n_entries;  // (always true for a valid slot; a guard)
     __syncthreads();  // rows (and, on the first block, the prologue tiles) are in LDS
     const int idx_nn = load_slot_index(idx_row, blk + 2, l32, p.topk, p.S_kv);
     if (blk + 1 < nblk) wide_issue<C, FP8>(rg, kv_b, kv_scale_b, idx_nxt, row_pitch);
