@@ -191,6 +191,20 @@ __device__ __forceinline__ i32x4 tr_operand_perm(const unsigned char *T, int str
   return i32x4{r0[0], r0[1], r1[0], r1[1]};
 }
 
+// Streaming (non-temporal) 16-byte global store / load: for data written once
+// and read once much later (the backward's partial dKV rows), so it neither
+// lingers as dirty lines in the caches nor evicts the working set of the
+// kernels in between.
+__device__ __forceinline__ void st_stream_16(void *p, i32x4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<i32x4 *>(p));
+}
+__device__ __forceinline__ void st_stream_16(void *p, f32x4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<f32x4 *>(p));
+}
+__device__ __forceinline__ i32x4 ld_stream_16(const void *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(p));
+}
+
 __device__ __forceinline__ i32x4 ld_global_16(const void *p) {
   return *reinterpret_cast<const i32x4 *>(p);
 }

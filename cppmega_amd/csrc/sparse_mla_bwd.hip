@@ -330,8 +330,8 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
         for (int i = 0; i < 4; ++i) {
           const int d0 = dt * 32 + 16 * (i >> 1) + 8 * g32 + 4 * (i & 1);
           if (wr)
-            *reinterpret_cast<f32x4 *>(dst + d0 * 4) =
-                f32x4{cacc[dt][4 * i], cacc[dt][4 * i + 1], cacc[dt][4 * i + 2], cacc[dt][4 * i + 3]};
+            st_stream_16(dst + d0 * 4, f32x4{cacc[dt][4 * i], cacc[dt][4 * i + 1], cacc[dt][4 * i + 2],
+                                             cacc[dt][4 * i + 3]});
         }
     } else {
       // fp16 rows scaled by a power of two mapping the row max into [2^13, 2^14)
@@ -377,7 +377,7 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
       for (int it = 0; it < ITS; ++it) {
         const int ch = (it * 64 + lane) % C::ROW_CHUNKS;
         const uint64_t prow = (uint64_t)(uint32_t)ps[it] * (uint32_t)p.ntiles + tile;
-        if (ps[it] >= 0) *reinterpret_cast<i32x4 *>(p.partials + prow * (D_QK * 2) + ch * 16) = v[it];
+        if (ps[it] >= 0) st_stream_16(p.partials + prow * (D_QK * 2) + ch * 16, v[it]);
       }
     }
     wave_lds_sync();  // K / dS tiles are consumed before the next block's gather lands

@@ -345,7 +345,7 @@ dkv_reduce_kernel(const int32_t *rowptr, const unsigned char *partials, const in
       for (int q = 0; q < CPL; ++q) {
         const int cc = c + 64 * q;
         v[u][q] = i32x4{0, 0, 0, 0};
-        if (k < k1 && cc < NCR) v[u][q] = ld_global_16(partials + k * ROWB + cc * 16);
+        if (k < k1 && cc < NCR) v[u][q] = ld_stream_16(partials + k * ROWB + cc * 16);
       }
     }
 #pragma unroll

@@ -631,8 +631,7 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int d0 = t * 32 + 8 * i + 4 * g32;
-            *reinterpret_cast<f32x4 *>(dst + d0 * 4) =
-                f32x4{cacc[4 * i], cacc[4 * i + 1], cacc[4 * i + 2], cacc[4 * i + 3]};
+            st_stream_16(dst + d0 * 4, f32x4{cacc[4 * i], cacc[4 * i + 1], cacc[4 * i + 2], cacc[4 * i + 3]});
           }
         }
       }
