@@ -127,11 +127,20 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
   const int nblk = (int)((p.topk + 31) / 32);
 
   // this wave's blocks: w, w + WPT, ...; start the first gather before the prologue
+  // Indices, CSR positions and rows of a wave's next block are loaded one block
+  // (indices two) ahead with unconditional loads, and the partial-row stores
+  // below are unconditional too (masked lanes write a trash row past the
+  // entries), so the compiler's memory waits count exactly: waiting for the
+  // next block's rows never waits for this block's stores.
   int blk = w;
-  int idx_cur = load_slot_index(idx_row, blk, l32, p.topk, p.S_kv);
-  int idx_nxt = load_slot_index(idx_row, blk + C::WPT, l32, p.topk, p.S_kv);
+  const auto idx_rs = slot_rsrc(idx_row, p.topk);
+  const auto pos_rs = slot_rsrc(p.pos_of + entry0, p.topk);
+  int idx_cur = slot_index(load_slot_raw(idx_rs, blk, l32), blk, l32, p.topk, p.S_kv);
+  int raw_nxt = load_slot_raw(idx_rs, blk + C::WPT, l32);
+  int pos_cur = load_slot_raw(pos_rs, blk, l32);
   typename Gat::Regs rg;
-  if (blk < nblk) gather_issue<Gat>(rg, kv_b, kv_scale_b, idx_cur, row_pitch);
+  gather_issue<Gat>(rg, kv_b, kv_scale_b, idx_cur, row_pitch);
+  const uint64_t trash = (uint64_t)n_entries * (uint64_t)p.ntiles;  // partial row no entry owns
 
   // ---------------- prologue (all waves): Q, dO tiles, Delta, LSE ----------------
   {
@@ -222,12 +231,14 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
       gather_store_scale<Gat>(rg, Ksc);
     }
     const bool valid = idx_cur >= 0;  // slot slot0 + l32
-    int32_t pos = -1;
-    if (valid) pos = p.pos_of[entry0 + slot0 + l32];
+    const int32_t pos = pos_cur;
     const bool wr = valid && pos >= 0 && pos < n_entries;  // (always true for a valid slot; a guard)
+    const uint64_t prow_me = wr ? (uint64_t)(uint32_t)pos * (uint32_t)p.ntiles + tile : trash;
     wave_lds_sync();
-    const int idx_nn = load_slot_index(idx_row, blk + 2 * C::WPT, l32, p.topk, p.S_kv);
-    if (blk + C::WPT < nblk) gather_issue<Gat>(rg, kv_b, kv_scale_b, idx_nxt, row_pitch);
+    const int raw_nn = load_slot_raw(idx_rs, blk + 2 * C::WPT, l32);
+    const int pos_nxt = load_slot_raw(pos_rs, blk + C::WPT, l32);
+    const int idx_nxt = slot_index(raw_nxt, blk + C::WPT, l32, p.topk, p.S_kv);
+    gather_issue<Gat>(rg, kv_b, kv_scale_b, idx_nxt, row_pitch);
 
     // ---- S = Q K^T and dP = dO V^T  (M = head, N = slot; Q / dO rows from LDS) ----
     f32x16 sacc, dpacc;
@@ -323,15 +334,14 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
     // lane: slot l32, d = dt*32 + 16(i>>1) + 8*g32 + 4(i&1) + j (the permuted Q^T / dO^T columns).
     if constexpr (F32P) {
       // fp32 rows: the two lanes of a slot store adjacent 16-byte pieces
-      unsigned char *dst = p.partials + ((int64_t)(wr ? pos : 0) * p.ntiles + tile) * (int64_t)(D_QK * 4);
+      unsigned char *dst = p.partials + prow_me * (uint64_t)(D_QK * 4);
 #pragma unroll
       for (int dt = 0; dt < C::DQT; ++dt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int d0 = dt * 32 + 16 * (i >> 1) + 8 * g32 + 4 * (i & 1);
-          if (wr)
-            st_stream_16(dst + d0 * 4, f32x4{cacc[dt][4 * i], cacc[dt][4 * i + 1], cacc[dt][4 * i + 2],
-                                             cacc[dt][4 * i + 3]});
+          st_stream_16(dst + d0 * 4, f32x4{cacc[dt][4 * i], cacc[dt][4 * i + 1], cacc[dt][4 * i + 2],
+                                           cacc[dt][4 * i + 3]});
         }
     } else {
       // fp16 rows scaled by a power of two mapping the row max into [2^13, 2^14)
@@ -360,7 +370,7 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
                     (int)pack_f16x2(cacc[dt][8 * s + 6] * rscale, cacc[dt][8 * s + 7] * rscale)};
         }
       if (g32 == 0) Lpos[l32] = wr ? pos : -1;
-      if (g32 == 0 && wr) p.partial_exp[(uint64_t)(uint32_t)pos * (uint32_t)p.ntiles + tile] = (int8_t)pexp;
+      p.partial_exp[prow_me] = (int8_t)pexp;  // both lane halves store the same byte
       wave_lds_sync();
       // all LDS reads first, then the stores, so the reads overlap
       constexpr int ITS = 32 * C::ROW_CHUNKS / 64;
@@ -376,13 +386,14 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
 #pragma unroll
       for (int it = 0; it < ITS; ++it) {
         const int ch = (it * 64 + lane) % C::ROW_CHUNKS;
-        const uint64_t prow = (uint64_t)(uint32_t)ps[it] * (uint32_t)p.ntiles + tile;
-        if (ps[it] >= 0) st_stream_16(p.partials + prow * (D_QK * 2) + ch * 16, v[it]);
+        const uint64_t prow = ps[it] >= 0 ? (uint64_t)(uint32_t)ps[it] * (uint32_t)p.ntiles + tile : trash;
+        st_stream_16(p.partials + prow * (D_QK * 2) + ch * 16, v[it]);
       }
     }
     wave_lds_sync();  // K / dS tiles are consumed before the next block's gather lands
     idx_cur = idx_nxt;
-    idx_nxt = idx_nn;
+    raw_nxt = raw_nn;
+    pos_cur = pos_nxt;
   }
 
   // ---- combine the waves' dQ partial sums in wave order, then write dQ ----
@@ -436,9 +447,9 @@ static BwdWorkspace bwd_layout(int64_t B, int64_t S, int64_t S_kv, int64_t H, in
   const size_t psz = ((flags & DSA_BWD_FP32_PARTIALS) || D_qk > 256) ? 4 : 2;
   size_t off = 0;
   L.partials = off;
-  off += align256(entries * ntiles * D_qk * psz);
+  off += align256((entries * ntiles + 1) * D_qk * psz);  // + one trash row for masked slots
   L.pexp = off;
-  off += align256(entries * ntiles);
+  off += align256(entries * ntiles + 1);
   L.mask = off;
   off += align256((size_t)B * L.NC * R * 4);
   L.base = off;

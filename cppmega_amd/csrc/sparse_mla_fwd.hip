@@ -80,8 +80,9 @@ sparse_mla_fwd_kernel(const FwdParams p) {
   const int nblk = (int)((p.topk + 31) / 32);
 
   // Indices of blocks 0 and 1, then the rows of block 0, go out before the Q loads.
-  int idx_cur = load_slot_index(idx_row, 0, l32, p.topk, p.S_kv);
-  int idx_nxt = load_slot_index(idx_row, 1, l32, p.topk, p.S_kv);
+  const auto idx_rs = slot_rsrc(idx_row, p.topk);
+  int idx_cur = slot_index(load_slot_raw(idx_rs, 0, l32), 0, l32, p.topk, p.S_kv);
+  int raw_nxt = load_slot_raw(idx_rs, 1, l32);
   typename Gat::Regs rg;
   gather_issue<Gat>(rg, kv_b, kv_scale_b, idx_cur, row_pitch);
 
@@ -118,8 +119,10 @@ sparse_mla_fwd_kernel(const FwdParams p) {
     const uint64_t vmask = __ballot(idx_cur >= 0);
     wave_lds_sync();
     // ---- prefetch: rows of block blk+1, indices of block blk+2 ----
-    const int idx_nn = load_slot_index(idx_row, blk + 2, l32, p.topk, p.S_kv);
-    if (blk + 1 < nblk) gather_issue<Gat>(rg, kv_b, kv_scale_b, idx_nxt, row_pitch);
+    // (issued unconditionally, past the last block too, so every wait is counted exactly)
+    const int raw_nn = load_slot_raw(idx_rs, blk + 2, l32);
+    const int idx_nxt = slot_index(raw_nxt, blk + 1, l32, p.topk, p.S_kv);
+    gather_issue<Gat>(rg, kv_b, kv_scale_b, idx_nxt, row_pitch);
 
     // ---- S^T = K Q^T  (M = slot, N = head, K = d) ----
     f32x16 sacc;
@@ -195,7 +198,7 @@ sparse_mla_fwd_kernel(const FwdParams p) {
     }
     wave_lds_sync();
     idx_cur = idx_nxt;
-    idx_nxt = idx_nn;
+    raw_nxt = raw_nn;
   }
 
   // ---- normalise and write: lane = head l32, d = dt*32 + 8i + 4*g32 + j ----

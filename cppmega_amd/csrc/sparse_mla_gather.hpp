@@ -38,6 +38,22 @@ struct GatherCfg {
   };
 };
 
+// Raw index of slot blk*32 + l32 through a buffer resource covering the row's
+// topk indices (0 past the end): an unconditional load, so the wait for it is
+// counted exactly and never has to drain other outstanding memory operations
+// (stores in particular).  slot_index() applies the mask when it is used.
+__device__ __forceinline__ int load_slot_raw(__amdgpu_buffer_rsrc_t idx_rs, int blk, int l32) {
+  return (int)__builtin_amdgcn_raw_buffer_load_b32(idx_rs, (blk * 32 + l32) * 4, 0, 0);
+}
+__device__ __forceinline__ int slot_index(int raw, int blk, int l32, int64_t topk, int64_t s_kv) {
+  const int64_t sl = (int64_t)blk * 32 + l32;
+  return (sl < topk && raw >= 0 && raw < s_kv) ? raw : -1;
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slot_rsrc(const int32_t *row, int64_t topk) {
+  const int64_t nb = topk * 4;
+  return make_buffer_rsrc(row, nb < 0x7fffffff ? (uint32_t)nb : 0x7fffffffu);
+}
+
 // Index of slot blk*32 + l32 of this row, or -1 when masked / past topk.
 __device__ __forceinline__ int load_slot_index(const int32_t *idx_row, int blk, int l32, int64_t topk,
                                                int64_t s_kv) {
