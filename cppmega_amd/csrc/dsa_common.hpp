@@ -117,7 +117,9 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
 // Wave helpers
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63u); }
-__device__ __forceinline__ int wave_id() { return (int)(threadIdx.x >> 6); }
+// Wave index within the workgroup, made explicitly wave-uniform (an SGPR), so
+// that addresses and branches derived from it stay scalar.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
 
