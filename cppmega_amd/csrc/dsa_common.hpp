@@ -217,8 +217,15 @@ __device__ __forceinline__ i32x2 ld_global_8(const void *p) {
 // Raw buffer access: a resource covering `num_bytes` from `base`; loads at byte
 // offsets outside it return 0 instead of touching memory (gfx9-family
 // descriptor word 3 = 0x00020000).
+// The base and size are wave-uniform by contract; they are read from the
+// first lane so the descriptor lives in SGPRs even where the compiler cannot
+// prove uniformity (otherwise every access becomes a waterfall loop).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buffer_rsrc(const void *base, uint32_t num_bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)num_bytes, 0x00020000);
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  void *pb = reinterpret_cast<void *>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(pb, (short)0, (int)__builtin_amdgcn_readfirstlane(num_bytes), 0x00020000);
 }
 __device__ __forceinline__ float buffer_load_f32(__amdgpu_buffer_rsrc_t r, int voffset, int soffset) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voffset, soffset, 0));

@@ -83,14 +83,23 @@ indexer_score_kernel(const IdxParams p) {
   const int64_t k_end = (p.causal == 2 && t_last + 1 < chunk_end) ? t_last + 1 : chunk_end;
   const int ntile = (int)((k_end - k0 + C::KT - 1) / C::KT);
 
+  // Memory operations of the tile loop are unconditional bounded buffer
+  // accesses (loads past the end return 0, stores past the end are dropped),
+  // so the compiler's memory waits are counted exactly: refilling the key tile
+  // never has to wait for the score stores to reach memory.
+  // keys of batch b: key sk at byte sk * B * D * ELT from k_rs's base
+  const auto k_rs = make_buffer_rsrc(p.k + (int64_t)b * D * C::ELT, (uint32_t)(((p.Sk - 1) * p.B + 1) * D * C::ELT));
+  // this block's score rows [t0, t_last]
+  const auto out_rs = make_buffer_rsrc(out_b + t0 * p.Sk, (uint32_t)((t_last - t0 + 1) * p.Sk * 4));
+
   // ---- key tile loads (thread: LOADS 16-byte chunks of the 64-key tile) ----
   auto load_tile = [&](int it, i32x4 (&r)[C::LOADS]) {
 #pragma unroll
     for (int l = 0; l < C::LOADS; ++l) {
       const int u = tid + 256 * l, key = u / C::CPR, c = u % C::CPR;
       const int64_t sk = k0 + (int64_t)it * C::KT + key;
-      r[l] = i32x4{0, 0, 0, 0};
-      if (sk < p.Sk) r[l] = ld_global_16(p.k + ((sk * p.B + b) * D) * C::ELT + c * 16);
+      const uint32_t off = sk < p.Sk ? (uint32_t)(sk * p.B * D * C::ELT + c * 16) : 0xffffffffu;
+      r[l] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(k_rs, (int)off, 0, 0));
     }
   };
   auto store_tile = [&](int buf, const i32x4 (&r)[C::LOADS]) {
@@ -145,52 +154,54 @@ indexer_score_kernel(const IdxParams p) {
   __syncthreads();
   const int64_t wave_tok_last = wave_tok0 + C::TPW - 1;
   for (int it = 0; it < ntile; ++it) {
-    if (it + 1 < ntile) load_tile(it + 1, kreg);
+    load_tile(it + 1, kreg);  // past the last tile: keys beyond Sk read 0, unused
     const unsigned char *ks = KS[it & 1];
 #pragma unroll
     for (int sub = 0; sub < C::KT / 32; ++sub) {
       const int64_t sn = k0 + (int64_t)it * C::KT + sub * 32;
-      if (sn >= k_end) break;
-      if (p.causal == 2 && sn > wave_tok_last) break;  // wholly above this wave's diagonal
+      // wave-uniform: the sub-tile exists and is not wholly above this wave's diagonal
+      const bool active = sn < k_end && !(p.causal == 2 && sn > wave_tok_last);
       float part[C::TPW];
 #pragma unroll
       for (int tl = 0; tl < C::TPW; ++tl) part[tl] = 0.0f;
+      if (active) {
 #pragma unroll
-      for (int m = 0; m < C::MT; ++m) {
-        f32x16 acc;
+        for (int m = 0; m < C::MT; ++m) {
+          f32x16 acc;
 #pragma unroll
-        for (int a = 0; a < 16; ++a) acc[a] = 0.0f;
+          for (int a = 0; a < 16; ++a) acc[a] = 0.0f;
 #pragma unroll
-        for (int k = 0; k < C::KSTEPS; ++k) {
-          const unsigned char *brow = ks + (sub * 32 + l32) * C::KS_STRIDE;
-          if constexpr (FP8) {
-            const long bv = *reinterpret_cast<const long *>(brow + 16 * k + 8 * g32);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(A[m][k], bv, acc, 0, 0, 0);
-          } else {
-            const i32x4 bv = *reinterpret_cast<const i32x4 *>(brow + (16 * k + 8 * g32) * 2);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[m][k], as_bf16x8(bv), acc, 0, 0, 0);
+          for (int k = 0; k < C::KSTEPS; ++k) {
+            const unsigned char *brow = ks + (sub * 32 + l32) * C::KS_STRIDE;
+            if constexpr (FP8) {
+              const long bv = *reinterpret_cast<const long *>(brow + 16 * k + 8 * g32);
+              acc = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(A[m][k], bv, acc, 0, 0, 0);
+            } else {
+              const i32x4 bv = *reinterpret_cast<const i32x4 *>(brow + (16 * k + 8 * g32) * 2);
+              acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[m][k], as_bf16x8(bv), acc, 0, 0, 0);
+            }
+          }
+#pragma unroll
+          for (int a = 0; a < 16; ++a) {
+            const int tl = (m * 32 + 8 * (a >> 2)) / H;
+            const float x = RELU ? fmaxf(acc[a], 0.0f) : acc[a];  // one v_max_f32 (IEEE mode off)
+            part[tl] = fmaf(x, wv[m][a], part[tl]);
           }
         }
-#pragma unroll
-        for (int a = 0; a < 16; ++a) {
-          const int tl = (m * 32 + 8 * (a >> 2)) / H;
-          const float x = RELU ? fmaxf(acc[a], 0.0f) : acc[a];  // one v_max_f32 (IEEE mode off)
-          part[tl] = fmaf(x, wv[m][a], part[tl]);
-        }
       }
+      // the stores are issued on every path (inactive ones land past the
+      // resource and are dropped), which keeps the memory wait counts exact
       const int64_t s = sn + l32;
 #pragma unroll
       for (int tl = 0; tl < C::TPW; ++tl) {
-        const float v = sum_halves(part[tl]);
+        float v = sum_halves(part[tl]);
         const bool mine = C::TPW == 1 ? (g32 == 0) : ((tl & 1) == g32);
         const int64_t t = wave_tok0 + tl;
-        if (mine && t < p.Sq && s < p.Sk) {
-          if (p.causal && s > t) {
-            if (p.causal == 1) out_b[t * p.Sk + s] = -INFINITY;
-          } else {
-            out_b[t * p.Sk + s] = v;
-          }
-        }
+        const bool above = p.causal && s > t;
+        if (above) v = -INFINITY;  // causal mode 1 writes it, mode 2 skips the store
+        const bool st = active && mine && t < p.Sq && s < p.Sk && !(above && p.causal == 2);
+        const uint32_t off = st ? (uint32_t)(((t - t0) * p.Sk + s) * 4) : 0xffffffffu;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), out_rs, (int)off, 0, 0);
       }
     }
     if (it + 1 < ntile) {
@@ -227,6 +238,9 @@ extern "C" int dsa_indexer_scores(const void *q, const void *w, const void *k, f
   if (B == 0 || Sq == 0 || Sk == 0) return DSA_OK;
   DSA_REQUIRE(q && w && k && scores, "dsa_indexer_scores: null tensor pointer");
   DSA_REQUIRE(Sk < (1ll << 31) && (Sq + 255) / 16 < 65536 && B < 65536, "dsa_indexer_scores: grid too large");
+  DSA_REQUIRE(Sk * B * D < (1ll << 31) && Sk < (1ll << 25),
+              "dsa_indexer_scores: k (%lld x %lld x %lld) or score rows too large for 32-bit offsets",
+              (long long)Sk, (long long)B, (long long)D);
   const bool f8 = dtype == DSA_DTYPE_E4M3;
   if (f8) DSA_REQUIRE(q_scale && k_scale, "dsa_indexer_scores: e4m3 input needs q_scale and k_scale");
   IdxParams p;
