@@ -21,9 +21,14 @@ h=128, d_qk=576, d_v=512, topk=2048; e4m3 indexer at h=64, d=128; top-2048
 over s=16384) are timed on device-generated inputs and reported under "cfg5"
 (not part of `value`).
 
+`value` and `ms_per_step` come from replays of the layer step captured in a
+HIP graph (launch gaps removed; every replay runs all 13 kernels, and three
+replays are first checked bit for bit against the eager step); the per-kernel
+breakdown and `eager_tokens_per_s` come from the eager timed steps before it.
+
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
-                       [--no-cfg5] [--calib-copy-mib N]   (one N MiB device copy
-                       before timing, the calibration kernel of PMC runs)
+                       [--no-cfg5] [--no-graph] [--calib-copy-mib N]   (one N MiB
+                       device copy before timing, the calibration kernel of PMC runs)
 """
 from __future__ import annotations
 
@@ -135,6 +140,42 @@ def measure_cfg5(dev, reps=3):
     return res
 
 
+def time_graph(step, steps, warmup):
+    """Capture one layer step (all 13 kernels, outputs allocated from the
+    graph's pool) in a HIP graph and time `steps` replays.  Before timing,
+    three replays, each separated by an eager step, are checked bit for bit
+    against the eager step's outputs (the kernels are deterministic)."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step(False)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _, gout = step(False)
+    checked = 0
+    for _ in range(3):
+        _, eager = step(False)
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(gout, eager):
+            if not torch.equal(a, b):
+                raise RuntimeError("graph replay differs from the eager step")
+        checked += 1
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    return {"wall_s": time.perf_counter() - t0, "checked": checked}
+
+
 def algorithmic_work():
     """Per-launch algorithmic work of each kernel at cfg2 / cfg3.
 
@@ -223,6 +264,8 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=4096)
     ap.add_argument("--calib-copy-mib", type=int, default=0)
     ap.add_argument("--no-cfg5", action="store_true", help="skip the cfg5 (long-context) kernel timings")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="time eager launches only (default: the step is also captured in a HIP graph)")
     args = ap.parse_args()
     if args.steps > 256:
         print("--steps must be at most 256 (the stage-timing ring holds 256 calls)", file=sys.stderr)
@@ -301,6 +344,13 @@ def main():
     tokens = B * S
     value = tokens * args.steps / wall
 
+    eager_tokens_per_s = value
+    graph_info = None
+    if not args.no_graph:
+        graph_info = time_graph(step, args.steps, args.warmup)
+        value = tokens * args.steps / graph_info["wall_s"]
+        ms_per_step = graph_info["wall_s"] / args.steps * 1e3
+
     work = algorithmic_work()
     kernels = {}
     for k, w in work.items():
@@ -348,6 +398,9 @@ def main():
         "cpu_baseline": cpu,
         "kernels": kernels,
         "indexcache_amortised_tokens_per_s": round(amortised, 1),
+        "launch": ("hip_graph" if graph_info is not None else "eager"),
+        "eager_tokens_per_s": round(eager_tokens_per_s, 1),
+        "graph_replays_checked": (graph_info["checked"] if graph_info is not None else 0),
         "cfg5": ({"workload": f"s={C5_S} h={C5_H} d_qk={C5_DQK} d_v={C5_DV} topk={C5_TOPK} SparseMLA fwd (bf16), "
                               f"indexer h={C5_HIDX} d={C5_DIDX} e4m3 causal, top-{C5_TOPK}",
                   "kernels": cfg5} if cfg5 is not None else None),
