@@ -143,6 +143,10 @@ sparse_mla_fwd_kernel(const FwdParams p) {
     // P = exp2(s * scale' - m_ref) against a reference max that only moves when
     // a score exceeds it by more than 2^8: P stays <= 256 (exact range for
     // bf16 / fp32) and O, l are rescaled only on those (rare, wave-uniform) steps.
+    // this lane's slots are 8i + 4*g32 + j: their valid bits sit at 8i + j of lmask;
+    // a block without masked slots (the common case, wave-uniform) skips the tests
+    const bool all_valid = (uint32_t)vmask == 0xffffffffu;
+    const uint32_t lmask = (uint32_t)vmask >> (4 * g32);
     float xs[16];
     float mloc = kNegBig;
 #pragma unroll
@@ -154,14 +158,18 @@ sparse_mla_fwd_kernel(const FwdParams p) {
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int slot = 8 * i + 4 * g32 + j;
-        const bool valid = (vmask >> slot) & 1ull;
         float v = sacc[4 * i + j];
         if constexpr (FP8) v *= ksc4[j];
-        xs[4 * i + j] = valid ? v : -INFINITY;  // raw score, scaled inside the exp
-        mloc = fmaxf(mloc, xs[4 * i + j]);
+        xs[4 * i + j] = v;  // raw score, scaled inside the exp
       }
     }
+    if (!all_valid) {
+#pragma unroll
+      for (int a = 0; a < 16; ++a)
+        if (!((lmask >> (8 * (a >> 2) + (a & 3))) & 1u)) xs[a] = -INFINITY;
+    }
+#pragma unroll
+    for (int a = 0; a < 16; a += 2) mloc = fmaxf(mloc, fmaxf(xs[a], xs[a + 1]));
     mloc = max_halves(mloc) * tscale;
     if (__ballot(mloc > m_run + 8.0f) != 0ull) {  // some head's max moved: rescale O, l
       const float m_new = fmaxf(m_run, mloc);
