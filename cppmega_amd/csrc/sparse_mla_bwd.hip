@@ -138,8 +138,10 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
   int idx_cur = slot_index(load_slot_raw(idx_rs, blk, l32), blk, l32, p.topk, p.S_kv);
   int raw_nxt = load_slot_raw(idx_rs, blk + C::WPT, l32);
   int pos_cur = load_slot_raw(pos_rs, blk, l32);
+  const auto kv_rs = make_buffer_rsrc(kv_b, (uint32_t)(p.S_kv * (int64_t)row_pitch));
+  const auto sc_rs = make_buffer_rsrc(kv_scale_b, FP8 ? (uint32_t)(p.S_kv * 4) : 0u);
   typename Gat::Regs rg;
-  gather_issue<Gat>(rg, kv_b, kv_scale_b, idx_cur, row_pitch);
+  gather_issue<Gat>(rg, kv_rs, sc_rs, idx_cur, row_pitch);
   const uint64_t trash = (uint64_t)n_entries * (uint64_t)p.ntiles;  // partial row no entry owns
 
   // ---------------- prologue (all waves): Q, dO tiles, Delta, LSE ----------------
@@ -238,7 +240,7 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
     const int raw_nn = load_slot_raw(idx_rs, blk + 2 * C::WPT, l32);
     const int pos_nxt = load_slot_raw(pos_rs, blk + C::WPT, l32);
     const int idx_nxt = slot_index(raw_nxt, blk + C::WPT, l32, p.topk, p.S_kv);
-    gather_issue<Gat>(rg, kv_b, kv_scale_b, idx_nxt, row_pitch);
+    gather_issue<Gat>(rg, kv_rs, sc_rs, idx_nxt, row_pitch);
 
     // ---- S = Q K^T and dP = dO V^T  (M = head, N = slot; Q / dO rows from LDS) ----
     f32x16 sacc, dpacc;

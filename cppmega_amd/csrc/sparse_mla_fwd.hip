@@ -83,8 +83,10 @@ sparse_mla_fwd_kernel(const FwdParams p) {
   const auto idx_rs = slot_rsrc(idx_row, p.topk);
   int idx_cur = slot_index(load_slot_raw(idx_rs, 0, l32), 0, l32, p.topk, p.S_kv);
   int raw_nxt = load_slot_raw(idx_rs, 1, l32);
+  const auto kv_rs = make_buffer_rsrc(kv_b, (uint32_t)(p.S_kv * (int64_t)row_pitch));
+  const auto sc_rs = make_buffer_rsrc(kv_scale_b, FP8 ? (uint32_t)(p.S_kv * 4) : 0u);
   typename Gat::Regs rg;
-  gather_issue<Gat>(rg, kv_b, kv_scale_b, idx_cur, row_pitch);
+  gather_issue<Gat>(rg, kv_rs, sc_rs, idx_cur, row_pitch);
 
   // Q as the B operand: lane = head, 8 consecutive d per k-step.
   qop_t qreg[C::KSTEPS];
@@ -122,7 +124,7 @@ sparse_mla_fwd_kernel(const FwdParams p) {
     // (issued unconditionally, past the last block too, so every wait is counted exactly)
     const int raw_nn = load_slot_raw(idx_rs, blk + 2, l32);
     const int idx_nxt = slot_index(raw_nxt, blk + 1, l32, p.topk, p.S_kv);
-    gather_issue<Gat>(rg, kv_b, kv_scale_b, idx_nxt, row_pitch);
+    gather_issue<Gat>(rg, kv_rs, sc_rs, idx_nxt, row_pitch);
 
     // ---- S^T = K Q^T  (M = slot, N = head, K = d) ----
     f32x16 sacc;
@@ -282,10 +284,8 @@ extern "C" int dsa_sparse_mla_fwd(const void *q, const void *kv, const int32_t *
   p.sl2 = sm_scale * kLog2e;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool f8 = dtype == DSA_DTYPE_E4M3;
-  if (wide_shape(D_qk, D_v)) {
-    DSA_REQUIRE(S_kv * G * D_qk * 2 < (1ll << 32), "dsa_sparse_mla_fwd: kv rows of one batch exceed 4 GiB");
-    return launch_fwd_wide(p, D_qk, D_v, f8, st);
-  }
+  DSA_REQUIRE(S_kv * G * D_qk * 2 < (1ll << 32), "dsa_sparse_mla_fwd: kv rows of one batch exceed 4 GiB");
+  if (wide_shape(D_qk, D_v)) return launch_fwd_wide(p, D_qk, D_v, f8, st);
   if (D_qk == 128 && D_v == 64) return f8 ? launch_fwd<128, 64, true>(p, st) : launch_fwd<128, 64, false>(p, st);
   if (D_qk == 128 && D_v == 128) return f8 ? launch_fwd<128, 128, true>(p, st) : launch_fwd<128, 128, false>(p, st);
   if (D_qk == 192 && D_v == 128) return f8 ? launch_fwd<192, 128, true>(p, st) : launch_fwd<192, 128, false>(p, st);

@@ -4,7 +4,7 @@
 // work is split into units of (4 consecutive slots x one 16-byte chunk); lane
 // u handles chunk u % NCH of slots 4*(u / NCH) .. +3, so 16 consecutive lanes
 // read one 256-byte row contiguously.  gather_issue() only issues the loads
-// (masked slots read row 0 and are zeroed at store time, so the loads carry no
+// (bounded buffer loads: masked slots read zeros, and the loads carry no
 // branches); the stores to LDS happen later, so a block's loads overlap the
 // previous block's compute.  Every tile is stored row-major: MFMA operands
 // that need a transposed view read it with ds_read_b64_tr_b16 (tr_operand).
@@ -34,7 +34,6 @@ struct GatherCfg {
   struct Regs {
     i32x4 v[UPL][4];
     float sc[UPL][4];
-    uint32_t valid;  // bit 4*uu + r: row r of unit uu is a real (unmasked) slot
   };
 };
 
@@ -63,12 +62,15 @@ __device__ __forceinline__ int load_slot_index(const int32_t *idx_row, int blk, 
   return (v >= 0 && v < s_kv) ? v : -1;
 }
 
-// kv_b points at row 0 of this (batch, kv group); row_pitch = G * ROWB bytes.
+// Rows are read through buffer resources: kv_rs covers the kv rows of this
+// (batch, kv group) (row r at byte r * row_pitch, row_pitch = G * ROWB), sc_rs
+// their e4m3 scales.  A masked slot reads at an offset past the resource, which
+// the hardware answers with zeros, so masked rows (and their scales) arrive as
+// zeros without selects, and every load is issued on every path.
 template <class Gat>
-__device__ __forceinline__ void gather_issue(typename Gat::Regs &rg, const unsigned char *kv_b,
-                                             const float *kv_scale_b, int my_idx, uint32_t row_pitch) {
+__device__ __forceinline__ void gather_issue(typename Gat::Regs &rg, __amdgpu_buffer_rsrc_t kv_rs,
+                                             __amdgpu_buffer_rsrc_t sc_rs, int my_idx, uint32_t row_pitch) {
   const int lane = lane_id();
-  uint32_t valid = 0;
 #pragma unroll
   for (int uu = 0; uu < Gat::UPL; ++uu) {
     const int u = lane + 64 * uu;
@@ -78,39 +80,27 @@ __device__ __forceinline__ void gather_issue(typename Gat::Regs &rg, const unsig
     for (int r = 0; r < 4; ++r) {
       const int ri = __shfl(my_idx, quad * 4 + r, 64);
       const bool ok = ri >= 0 && u < Gat::UNITS;
-      const uint32_t row = ok ? (uint32_t)ri : 0u;
-      rg.v[uu][r] = ld_global_16(kv_b + row * row_pitch + c * 16);
-      if constexpr (Gat::kFp8) rg.sc[uu][r] = kv_scale_b[row];
-      valid |= (ok ? 1u : 0u) << (4 * uu + r);
+      const uint32_t off = ok ? (uint32_t)ri * row_pitch + (uint32_t)c * 16u : 0xffffffffu;
+      rg.v[uu][r] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(kv_rs, (int)off, 0, 0));
+      if constexpr (Gat::kFp8)
+        rg.sc[uu][r] = buffer_load_f32(sc_rs, ok ? (int)((uint32_t)ri * 4u) : (int)0xffffffffu, 0);
     }
   }
-  rg.valid = valid;
 }
 
-// K rows, row-major (raw bf16 / e4m3 bytes): Kl[slot][chunk]; masked slots zero.
-// Blocks without masked slots (the common case, tested wave-wide) skip the selects.
+// K rows, row-major (raw bf16 / e4m3 bytes): Kl[slot][chunk]; masked slots
+// arrive as zeros from gather_issue.
 template <class Gat>
 __device__ __forceinline__ void gather_store_k(const typename Gat::Regs &rg, unsigned char *Kl) {
   const int lane = lane_id();
-  uint32_t full = 0u;  // valid bits of this lane's units that exist
-#pragma unroll
-  for (int uu = 0; uu < Gat::UPL; ++uu)
-    if (lane + 64 * uu < Gat::UNITS) full |= 0xfu << (4 * uu);
-  const bool all_valid = __ballot(rg.valid != full) == 0ull;
 #pragma unroll
   for (int uu = 0; uu < Gat::UPL; ++uu) {
     const int u = lane + 64 * uu;
     if (u >= Gat::UNITS) break;
     const int c = u % Gat::NCH, quad = u / Gat::NCH;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      i32x4 v = rg.v[uu][r];
-      if (!all_valid) {
-        const bool ok = (rg.valid >> (4 * uu + r)) & 1u;
-        v = ok ? v : i32x4{0, 0, 0, 0};
-      }
-      *reinterpret_cast<i32x4 *>(Kl + (quad * 4 + r) * Gat::KL_STRIDE + c * 16) = v;
-    }
+    for (int r = 0; r < 4; ++r)
+      *reinterpret_cast<i32x4 *>(Kl + (quad * 4 + r) * Gat::KL_STRIDE + c * 16) = rg.v[uu][r];
   }
 }
 
@@ -128,8 +118,7 @@ __device__ __forceinline__ void gather_store_dequant(const typename Gat::Regs &r
     if (c < NCH_D) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const bool ok = (rg.valid >> (4 * uu + r)) & 1u;
-        const float s = ok ? rg.sc[uu][r] : 0.0f;
+        const float s = rg.sc[uu][r];  // 0 for a masked slot
         uint32_t w[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -156,10 +145,7 @@ __device__ __forceinline__ void gather_store_scale(const typename Gat::Regs &rg,
     const int c = u % Gat::NCH, quad = u / Gat::NCH;
     if (c == 0) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const bool ok = (rg.valid >> (4 * uu + r)) & 1u;
-        Ksc[quad * 4 + r] = ok ? rg.sc[uu][r] : 0.0f;
-      }
+      for (int r = 0; r < 4; ++r) Ksc[quad * 4 + r] = rg.sc[uu][r];
     }
   }
 }
