@@ -54,7 +54,7 @@ H_IDX, D_IDX = 16, 64
 
 ENTRIES = B * S * TOPK                 # (token, slot) pairs of the backward (one kv group)
 KV_ROWS = B * S                        # dKV rows
-CSR_CHUNKS = (S + 15) // 16            # inverse-index chunks per batch (16 tokens each)
+CSR_CHUNKS = (S + 31) // 32            # inverse-index chunks per batch (32 tokens each)
 
 
 # cfg5: DeepSeek-V3.2-shaped long context (forward + indexer), reported beside the headline
@@ -200,7 +200,9 @@ def algorithmic_work():
         "bwd": {"flops": bwd_flops, "bytes": None},
         # inverse index: indices read twice (histogram, scatter), refs written once,
         # 16-token chunk histogram written once and read three times
-        "bwd_csr": {"flops": 0, "bytes": 3 * 4 * ENTRIES + 4 * 4 * B * CSR_CHUNKS * S},
+        # indices read twice, positions written once; per (chunk, row) a mask word written
+        # and read three times and a base word written and read once
+        "bwd_csr": {"flops": 0, "bytes": 3 * 4 * ENTRIES + 6 * 4 * B * CSR_CHUNKS * S},
         # every backward FLOP; reads q, kv, o, dO, indices, lse; writes dq and one fp16
         # partial dKV row (+ int8 exponent) per (token, slot)
         "bwd_main": {"flops": bwd_flops,
