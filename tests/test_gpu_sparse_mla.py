@@ -231,3 +231,30 @@ def test_cfg2_full_scale(dev):
     scale_v = float(expect_v.norm() / DV ** 0.5)
     assert float((col[:DV] - expect_v).abs().max()) <= 2e-2 * scale_v, "sum_j dKV_j[:d_v] != sum dO"
     assert float(col[DV:].abs().max()) <= 2e-2 * scale_v, "sum_j dKV_j[d_v:] != 0"
+
+
+@pytest.mark.parametrize("B,S,H,G,D,DV,topk,dup", [
+    (1, 100, 32, 2, 128, 128, 300, False),   # > 256 slots per segment, partial last token chunk, 2 groups
+    (2, 70, 32, 2, 128, 128, 40, True),      # a row repeated inside (token, group): serial chunk path
+    (1, 33, 16, 1, 128, 64, 520, True),      # topk > S_kv: many masked slots plus repeats
+])
+def test_bwd_inverse_index_paths(dev, B, S, H, G, D, DV, topk, dup):
+    """The inverse index's chunk paths: several 256-slot parts per (token, group),
+    a token chunk cut short by S, kv groups, and repeated rows (exact counts and
+    serial placement), all against the oracle and bitwise repeatable."""
+    inp = _inputs(B, S, H, D, DV, topk, G=G, seed=S + topk)
+    idx = inp["indices"].clone()
+    if dup:
+        g = torch.Generator().manual_seed(S)
+        t = torch.randint(0, S, (5,), generator=g)
+        for tt in t.tolist():
+            n = min(tt + 1, topk)
+            idx[0, tt, G - 1, : min(4, n)] = idx[0, tt, G - 1, 0]   # same row several times
+    q, kv, idxd, do = inp["q"].to(dev), inp["kv"].to(dev), idx.contiguous().to(dev), inp["do"].to(dev)
+    out, lse = sparse_mla_fwd_interface(q, kv, idxd, sm_scale=inp["scale"], d_v=DV)
+    dq, dkv = sparse_mla_bwd(q, kv, out, do, idxd, lse, sm_scale=inp["scale"])
+    rdq, rdkv = orc.sparse_mla_bwd(inp["q"], inp["kv"], out.cpu(), inp["do"], idx, lse.cpu(), inp["scale"], DV)
+    assert_close(dq, rdq, what="dq")
+    assert_close(dkv, rdkv, what="dkv")
+    dq2, dkv2 = sparse_mla_bwd(q, kv, out, do, idxd, lse, sm_scale=inp["scale"])
+    assert torch.equal(dq, dq2) and torch.equal(dkv, dkv2)
