@@ -47,65 +47,69 @@ struct IdxCfg {
   static constexpr int TPW = MT * 32 / H;       // tokens per wave
   static constexpr int WAVES = 4;
   static constexpr int TT = TPW * WAVES;        // tokens per workgroup
-  static constexpr int KT = 64;                 // keys per LDS tile
-  static constexpr int NKT = 8;                 // tiles per workgroup chunk
-  static constexpr int CHUNK = KT * NKT;        // keys per workgroup
-  static constexpr int KS_STRIDE = D * ELT + 16;
+  static constexpr int ROWB = D * ELT;          // bytes per key row
+  static constexpr int KT = 16384 / ROWB;       // keys per LDS tile (16 KiB of key rows)
+  static constexpr int SUBS = KT / 32;          // 32-key sub-tiles per tile
+  static constexpr int CHUNK = 2048;            // keys per workgroup
+  static constexpr int NKT = CHUNK / KT;        // tiles per workgroup chunk
+  static constexpr int KS_STRIDE = ROWB + 16;
   static constexpr int KSTEPS = D / 16;
-  static constexpr int CPR = D * ELT / 16;      // 16-byte chunks per key row
-  static constexpr int LOADS = KT * CPR / 256;  // 16-byte loads per thread per tile
+  static constexpr int CPR = ROWB / 16;         // 16-byte chunks per key row
+  static constexpr int NT = 64 * WAVES;         // threads per workgroup
+  static constexpr int LOADS = KT * CPR / NT;   // 16-byte loads per thread per tile
   static_assert(H == 16 || H == 32 || H == 64, "index heads must be 16, 32 or 64");
-  static_assert(D % 16 == 0 && LOADS >= 1 && KT * CPR % 256 == 0, "index head dim");
+  static_assert(D % 16 == 0 && LOADS >= 1 && KT * CPR % NT == 0 && CHUNK % KT == 0, "index head dim");
 };
 
+// Scores of token block [t0, t0 + TT) against keys [k0, k_end) of batch b
+// (the keys of one work segment), written to the rows of that token block.
 template <int H, int D, bool FP8, bool RELU>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
-indexer_score_kernel(const IdxParams p) {
+__device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&KS)[2][IdxCfg<H, D, FP8>::KT * IdxCfg<H, D, FP8>::KS_STRIDE],
+                                            int64_t b, int64_t t0_in, int64_t k0_in, int64_t k_end_in) {
   using C = IdxCfg<H, D, FP8>;
-  __shared__ __attribute__((aligned(16))) unsigned char KS[2][C::KT * C::KS_STRIDE];
+  // segment bounds are wave-uniform: keep them (and everything derived) scalar
+  const int64_t t0 = __builtin_amdgcn_readfirstlane((int)t0_in);
+  const int64_t k0 = __builtin_amdgcn_readfirstlane((int)k0_in);
+  const int64_t k_end = __builtin_amdgcn_readfirstlane((int)k_end_in);
   const int tid = threadIdx.x, lane = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
   const int g32 = lane >> 5, l32 = lane & 31;
-  const int64_t b = blockIdx.z;
-  const int64_t t0 = (int64_t)(gridDim.y - 1 - blockIdx.y) * C::TT;
-  const int64_t k0 = (int64_t)blockIdx.x * C::CHUNK;
   const int64_t t_last = (t0 + C::TT < p.Sq ? t0 + C::TT : p.Sq) - 1;
   float *out_b = p.out + b * p.Sq * p.Sk;
-  const int64_t chunk_end = k0 + C::CHUNK < p.Sk ? k0 + C::CHUNK : p.Sk;
-
-  if (p.causal && k0 > t_last) {
-    if (p.causal == 1) {
-      const int64_t nk = chunk_end - k0;
-      for (int64_t i = tid; i < (t_last - t0 + 1) * nk; i += 256) out_b[(t0 + i / nk) * p.Sk + k0 + i % nk] = -INFINITY;
-    }
-    return;
-  }
-  // keys computed: the chunk, cut at the block's last token in lower-triangle mode
-  const int64_t k_end = (p.causal == 2 && t_last + 1 < chunk_end) ? t_last + 1 : chunk_end;
   const int ntile = (int)((k_end - k0 + C::KT - 1) / C::KT);
+  __syncthreads();  // the previous segment's waves are done with the key tiles
 
   // Memory operations of the tile loop are unconditional bounded buffer
   // accesses (loads past the end return 0, stores past the end are dropped),
   // so the compiler's memory waits are counted exactly: refilling the key tile
   // never has to wait for the score stores to reach memory.
-  // keys of batch b: key sk at byte sk * B * D * ELT from k_rs's base
-  const auto k_rs = make_buffer_rsrc(p.k + (int64_t)b * D * C::ELT, (uint32_t)(((p.Sk - 1) * p.B + 1) * D * C::ELT));
+  // Key sk of batch b sits at byte sk * row_pitch from the batch's first key.
+  const uint32_t row_pitch = (uint32_t)(p.B * C::ROWB);
+  const unsigned char *k_b = p.k + b * C::ROWB;
   // this block's score rows [t0, t_last]
   const auto out_rs = make_buffer_rsrc(out_b + t0 * p.Sk, (uint32_t)((t_last - t0 + 1) * p.Sk * 4));
 
-  // ---- key tile loads (thread: LOADS 16-byte chunks of the 64-key tile) ----
-  auto load_tile = [&](int it, i32x4 (&r)[C::LOADS]) {
+  // ---- key tile loads (thread: LOADS 16-byte chunks of the KT-key tile) ----
+  // The resource of tile `it` starts at its first key and ends at the last key
+  // row (Sk - 1), so keys past the end read zeros without per-lane checks.
+  uint32_t loff[C::LOADS];
 #pragma unroll
-    for (int l = 0; l < C::LOADS; ++l) {
-      const int u = tid + 256 * l, key = u / C::CPR, c = u % C::CPR;
-      const int64_t sk = k0 + (int64_t)it * C::KT + key;
-      const uint32_t off = sk < p.Sk ? (uint32_t)(sk * p.B * D * C::ELT + c * 16) : 0xffffffffu;
-      r[l] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(k_rs, (int)off, 0, 0));
-    }
+  for (int l = 0; l < C::LOADS; ++l) {
+    const int u = tid + C::NT * l;
+    loff[l] = (uint32_t)(u / C::CPR) * row_pitch + (uint32_t)(u % C::CPR) * 16u;
+  }
+  auto load_tile = [&](int it, i32x4 (&r)[C::LOADS]) {
+    const int64_t first = k0 + (int64_t)it * C::KT;
+    const int64_t nkeys = p.Sk - first;
+    const uint32_t nb = nkeys > 0 ? (uint32_t)((nkeys - 1) * row_pitch + C::ROWB) : 0u;
+    const auto rs = make_buffer_rsrc(k_b + (nkeys > 0 ? first : 0) * row_pitch, nb);
+#pragma unroll
+    for (int l = 0; l < C::LOADS; ++l)
+      r[l] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)loff[l], 0, 0));
   };
   auto store_tile = [&](int buf, const i32x4 (&r)[C::LOADS]) {
 #pragma unroll
     for (int l = 0; l < C::LOADS; ++l) {
-      const int u = tid + 256 * l, key = u / C::CPR, c = u % C::CPR;
+      const int u = tid + C::NT * l, key = u / C::CPR, c = u % C::CPR;
       *reinterpret_cast<i32x4 *>(&KS[buf][key * C::KS_STRIDE + c * 16]) = r[l];
     }
   };
@@ -150,58 +154,105 @@ indexer_score_kernel(const IdxParams p) {
 #pragma unroll
     for (int a = 0; a < 16; ++a) wv[m][a] = __shfl(wl, m * 32 + 8 * (a >> 2) + 4 * g32 + (a & 3), 64);
 
+  // Scores of one 32-key sub-tile: part[tl] = sum over the wave's heads of token
+  // tl held in this lane's accumulator rows (the other half-wave holds the rest).
+  auto subtile = [&](const unsigned char *ks, int sub, float (&part)[C::TPW]) {
+#pragma unroll
+    for (int tl = 0; tl < C::TPW; ++tl) part[tl] = 0.0f;
+#pragma unroll
+    for (int m = 0; m < C::MT; ++m) {
+      f32x16 acc;
+#pragma unroll
+      for (int a = 0; a < 16; ++a) acc[a] = 0.0f;
+#pragma unroll
+      for (int k = 0; k < C::KSTEPS; ++k) {
+        const unsigned char *brow = ks + (sub * 32 + l32) * C::KS_STRIDE;
+        if constexpr (FP8) {
+          const long bv = *reinterpret_cast<const long *>(brow + 16 * k + 8 * g32);
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(A[m][k], bv, acc, 0, 0, 0);
+        } else {
+          const i32x4 bv = *reinterpret_cast<const i32x4 *>(brow + (16 * k + 8 * g32) * 2);
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[m][k], as_bf16x8(bv), acc, 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int a = 0; a < 16; ++a) {
+        const int tl = (m * 32 + 8 * (a >> 2)) / H;
+        const float x = RELU ? fmaxf(acc[a], 0.0f) : acc[a];  // one v_max_f32 (IEEE mode off)
+        part[tl] = fmaf(x, wv[m][a], part[tl]);
+      }
+    }
+  };
+
+  // Interior sub-tiles (every key below or on the wave's first token, inside
+  // Sk, all tokens inside Sq) store without checks: tokens are paired so one
+  // permlane32 swap and one add leave token 2j's total in lanes 0-31 and token
+  // 2j+1's in lanes 32-63 (each the low half plus the high half), and one
+  // full-wave store writes both rows; the sub-tile's key offset rides in the
+  // store's scalar offset.
+  constexpr int NPAIR = C::TPW >= 2 ? C::TPW / 2 : 1;
+  uint32_t soff_lane[NPAIR];
+#pragma unroll
+  for (int j = 0; j < NPAIR; ++j) {
+    const int tl = C::TPW >= 2 ? 2 * j + g32 : 0;
+    soff_lane[j] = (uint32_t)(((wave_tok0 + tl - t0) * p.Sk + k0 + l32) * 4);
+  }
+  const bool wave_in_sq = wave_tok0 + C::TPW - 1 < p.Sq;
+
   store_tile(0, kreg);
   __syncthreads();
   const int64_t wave_tok_last = wave_tok0 + C::TPW - 1;
   for (int it = 0; it < ntile; ++it) {
     load_tile(it + 1, kreg);  // past the last tile: keys beyond Sk read 0, unused
     const unsigned char *ks = KS[it & 1];
+    const int64_t tk = k0 + (int64_t)it * C::KT;
+    const bool interior = wave_in_sq && tk + C::KT <= k_end && (!p.causal || tk + C::KT - 1 <= wave_tok0);
+    if (interior) {
 #pragma unroll
-    for (int sub = 0; sub < C::KT / 32; ++sub) {
-      const int64_t sn = k0 + (int64_t)it * C::KT + sub * 32;
-      // wave-uniform: the sub-tile exists and is not wholly above this wave's diagonal
-      const bool active = sn < k_end && !(p.causal == 2 && sn > wave_tok_last);
-      float part[C::TPW];
+      for (int sub = 0; sub < C::SUBS; ++sub) {
+        float part[C::TPW];
+        subtile(ks, sub, part);
+        const int soff = (int)((uint32_t)(it * C::KT + sub * 32) * 4u);
+        if constexpr (C::TPW >= 2) {
 #pragma unroll
-      for (int tl = 0; tl < C::TPW; ++tl) part[tl] = 0.0f;
-      if (active) {
-#pragma unroll
-        for (int m = 0; m < C::MT; ++m) {
-          f32x16 acc;
-#pragma unroll
-          for (int a = 0; a < 16; ++a) acc[a] = 0.0f;
-#pragma unroll
-          for (int k = 0; k < C::KSTEPS; ++k) {
-            const unsigned char *brow = ks + (sub * 32 + l32) * C::KS_STRIDE;
-            if constexpr (FP8) {
-              const long bv = *reinterpret_cast<const long *>(brow + 16 * k + 8 * g32);
-              acc = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(A[m][k], bv, acc, 0, 0, 0);
-            } else {
-              const i32x4 bv = *reinterpret_cast<const i32x4 *>(brow + (16 * k + 8 * g32) * 2);
-              acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[m][k], as_bf16x8(bv), acc, 0, 0, 0);
-            }
+          for (int j = 0; j < NPAIR; ++j) {
+            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(part[2 * j]),
+                                                            __float_as_uint(part[2 * j + 1]), false, false);
+            const float v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), out_rs, (int)soff_lane[0 + j], soff, 0);
           }
-#pragma unroll
-          for (int a = 0; a < 16; ++a) {
-            const int tl = (m * 32 + 8 * (a >> 2)) / H;
-            const float x = RELU ? fmaxf(acc[a], 0.0f) : acc[a];  // one v_max_f32 (IEEE mode off)
-            part[tl] = fmaf(x, wv[m][a], part[tl]);
-          }
+        } else {
+          const float v = sum_halves(part[0]);
+          if (g32 == 0) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), out_rs, (int)soff_lane[0], soff, 0);
         }
       }
-      // the stores are issued on every path (inactive ones land past the
-      // resource and are dropped), which keeps the memory wait counts exact
-      const int64_t s = sn + l32;
+    } else {
 #pragma unroll
-      for (int tl = 0; tl < C::TPW; ++tl) {
-        float v = sum_halves(part[tl]);
-        const bool mine = C::TPW == 1 ? (g32 == 0) : ((tl & 1) == g32);
-        const int64_t t = wave_tok0 + tl;
-        const bool above = p.causal && s > t;
-        if (above) v = -INFINITY;  // causal mode 1 writes it, mode 2 skips the store
-        const bool st = active && mine && t < p.Sq && s < p.Sk && !(above && p.causal == 2);
-        const uint32_t off = st ? (uint32_t)(((t - t0) * p.Sk + s) * 4) : 0xffffffffu;
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), out_rs, (int)off, 0, 0);
+      for (int sub = 0; sub < C::SUBS; ++sub) {
+        const int64_t sn = tk + sub * 32;
+        // wave-uniform: the sub-tile exists and is not wholly above this wave's diagonal
+        const bool active = sn < k_end && !(p.causal == 2 && sn > wave_tok_last);
+        float part[C::TPW];
+        if (active) {
+          subtile(ks, sub, part);
+        } else {
+#pragma unroll
+          for (int tl = 0; tl < C::TPW; ++tl) part[tl] = 0.0f;
+        }
+        // the stores are issued on every path (inactive ones land past the
+        // resource and are dropped), which keeps the memory wait counts exact
+        const int64_t s = sn + l32;
+#pragma unroll
+        for (int tl = 0; tl < C::TPW; ++tl) {
+          float v = sum_halves(part[tl]);
+          const bool mine = C::TPW == 1 ? (g32 == 0) : ((tl & 1) == g32);
+          const int64_t t = wave_tok0 + tl;
+          const bool above = p.causal && s > t;
+          if (above) v = -INFINITY;  // causal mode 1 writes it, mode 2 skips the store
+          const bool st = active && mine && t < p.Sq && s < p.Sk && !(above && p.causal == 2);
+          const uint32_t off = st ? (uint32_t)(((t - t0) * p.Sk + s) * 4) : 0xffffffffu;
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), out_rs, (int)off, 0, 0);
+        }
       }
     }
     if (it + 1 < ntile) {
@@ -211,16 +262,111 @@ indexer_score_kernel(const IdxParams p) {
   }
 }
 
+// Rows of token blocks have different lengths in lower-triangle mode (block tb
+// computes keys [0, last token]), so a grid of fixed key chunks leaves some
+// compute units with 64 times the work of others.  Lower-triangle mode pairs
+// the long block NTB-1-j with the short block j instead: the pair's combined
+// row length is the same for every j, and splitting it into `pieces` equal
+// ranges of 32-key sub-tiles gives every workgroup the same work.  A piece is
+// at most two segments (the end of the long row, the start of the short one).
+// Other modes keep fixed chunks of CHUNK keys (all rows as long as Sk).
+template <int H, int D, bool FP8, bool RELU>
+__global__ void __launch_bounds__((IdxCfg<H, D, FP8>::NT)) __attribute__((amdgpu_waves_per_eu(FP8 || D <= 64 ? 3 : 2)))
+indexer_score_kernel(const IdxParams p) {
+  using C = IdxCfg<H, D, FP8>;
+  __shared__ __attribute__((aligned(16))) unsigned char KS[2][C::KT * C::KS_STRIDE];
+  const int64_t b = blockIdx.z;
+  if (p.causal == 2) {
+    const int64_t ntb = (p.Sq + C::TT - 1) / C::TT;
+    const int64_t tb_long = ntb - 1 - (int64_t)blockIdx.y, tb_short = blockIdx.y;
+    // a block's row: keys [0, min(last token + 1, Sk)), in 32-key sub-tiles
+    auto row_keys = [&](int64_t tb) {
+      const int64_t t_last = (tb * C::TT + C::TT < p.Sq ? tb * C::TT + C::TT : p.Sq) - 1;
+      return t_last + 1 < p.Sk ? t_last + 1 : p.Sk;
+    };
+    const int64_t keys_long = row_keys(tb_long), keys_short = tb_short < tb_long ? row_keys(tb_short) : 0;
+    const int64_t n_long = (keys_long + 31) / 32, n = n_long + (keys_short + 31) / 32;
+    const int64_t pieces = gridDim.x;
+    const int64_t lo = (int64_t)blockIdx.x * n / pieces, hi = ((int64_t)blockIdx.x + 1) * n / pieces;
+#pragma unroll 1
+    for (int sg = 0; sg < 2; ++sg) {
+      const int64_t a = sg == 0 ? lo : (lo > n_long ? lo : n_long) - n_long;  // first sub-tile
+      const int64_t e = sg == 0 ? (hi < n_long ? hi : n_long) : hi - n_long;  // end sub-tile
+      const int64_t keys = sg == 0 ? keys_long : keys_short;
+      if (e > a) idx_segment<H, D, FP8, RELU>(p, KS, b, (sg == 0 ? tb_long : tb_short) * C::TT, a * 32,
+                                             e * 32 < keys ? e * 32 : keys);
+    }
+    return;
+  }
+  const int64_t t0 = (int64_t)(gridDim.y - 1 - blockIdx.y) * C::TT;
+  const int64_t k0 = (int64_t)blockIdx.x * C::CHUNK;
+  const int64_t t_last = (t0 + C::TT < p.Sq ? t0 + C::TT : p.Sq) - 1;
+  const int64_t chunk_end = k0 + C::CHUNK < p.Sk ? k0 + C::CHUNK : p.Sk;
+  if (p.causal == 1 && k0 > t_last) {
+    // chunk wholly above the block's diagonal: -inf only
+    float *out_b = p.out + b * p.Sq * p.Sk;
+    const int64_t nk = chunk_end - k0;
+    for (int64_t i = threadIdx.x; i < (t_last - t0 + 1) * nk; i += C::NT)
+      out_b[(t0 + i / nk) * p.Sk + k0 + i % nk] = -INFINITY;
+    return;
+  }
+  idx_segment<H, D, FP8, RELU>(p, KS, b, t0, k0, chunk_end);
+}
+
+// Workgroups of `kernel` resident at once on the current device (cached per device).
+template <class K>
+static int64_t resident_groups(K kernel, int threads) {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess)
+      return 0;
+    cache[dev] = cus * (per_cu > 0 ? per_cu : 1);
+  }
+  return cache[dev];
+}
+
+// Pieces per block pair: the smallest count (1..8) whose grid fills the
+// resident workgroup slots within 2% of the best whole-round efficiency.
+static int pick_pieces(int64_t groups_per_piece, int64_t slots) {
+  if (slots <= 0 || groups_per_piece <= 0) return 1;
+  int best_p = 1;
+  double best = -1.0;
+  for (int pc = 1; pc <= 8; ++pc) {
+    const int64_t g = groups_per_piece * pc;
+    const double eff = (double)g / (double)(((g + slots - 1) / slots) * slots);
+    if (eff > best + 0.02) {
+      best = eff;
+      best_p = pc;
+    }
+  }
+  return best_p;
+}
+
+template <int H, int D, bool FP8, bool RELU>
+static int launch_idx_act(const IdxParams &p, hipStream_t st) {
+  using C = IdxCfg<H, D, FP8>;
+  const int64_t ntb = (p.Sq + C::TT - 1) / C::TT;
+  DSA_REQUIRE(ntb < 65536, "dsa_indexer_scores: %lld query tokens exceed the grid (%d per workgroup)",
+              (long long)p.Sq, C::TT);
+  dim3 grid;
+  if (p.causal == 2) {
+    const int64_t npairs = (ntb + 1) / 2;
+    const int pieces = pick_pieces(npairs * p.B, resident_groups(indexer_score_kernel<H, D, FP8, RELU>, C::NT));
+    grid = dim3((unsigned)pieces, (unsigned)npairs, (unsigned)p.B);
+  } else {
+    grid = dim3((unsigned)((p.Sk + C::CHUNK - 1) / C::CHUNK), (unsigned)ntb, (unsigned)p.B);
+  }
+  hipLaunchKernelGGL((indexer_score_kernel<H, D, FP8, RELU>), grid, dim3(C::NT), 0, st, p);
+  return check_launch("indexer_scores");
+}
+
 template <int H, int D, bool FP8>
 static int launch_idx(const IdxParams &p, hipStream_t st) {
-  using C = IdxCfg<H, D, FP8>;
-  const dim3 grid((unsigned)((p.Sk + C::CHUNK - 1) / C::CHUNK), (unsigned)((p.Sq + C::TT - 1) / C::TT),
-                  (unsigned)p.B);
-  if (p.relu)
-    hipLaunchKernelGGL((indexer_score_kernel<H, D, FP8, true>), grid, dim3(256), 0, st, p);
-  else
-    hipLaunchKernelGGL((indexer_score_kernel<H, D, FP8, false>), grid, dim3(256), 0, st, p);
-  return check_launch("indexer_scores");
+  return p.relu ? launch_idx_act<H, D, FP8, true>(p, st) : launch_idx_act<H, D, FP8, false>(p, st);
 }
 
 }  // namespace dsa
@@ -237,7 +383,7 @@ extern "C" int dsa_indexer_scores(const void *q, const void *w, const void *k, f
   DSA_REQUIRE(causal >= 0 && causal <= 2, "dsa_indexer_scores: causal must be 0, 1 or 2");
   if (B == 0 || Sq == 0 || Sk == 0) return DSA_OK;
   DSA_REQUIRE(q && w && k && scores, "dsa_indexer_scores: null tensor pointer");
-  DSA_REQUIRE(Sk < (1ll << 31) && (Sq + 255) / 16 < 65536 && B < 65536, "dsa_indexer_scores: grid too large");
+  DSA_REQUIRE(Sk < (1ll << 31) && B < 65536, "dsa_indexer_scores: grid too large");
   DSA_REQUIRE(Sk * B * D < (1ll << 31) && Sk < (1ll << 25),
               "dsa_indexer_scores: k (%lld x %lld x %lld) or score rows too large for 32-bit offsets",
               (long long)Sk, (long long)B, (long long)D);

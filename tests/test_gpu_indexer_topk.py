@@ -61,6 +61,39 @@ def test_indexer_causal_modes(dev):
     assert (low[:, ~tri] == 7.0).all()
 
 
+@pytest.mark.parametrize("Sq,Sk,B,H,D,fp8", [
+    (33, 33, 1, 16, 64, False),       # one token block pair, partial sub-tiles
+    (517, 517, 2, 32, 64, False),     # odd block count: the middle block has no partner
+    (1000, 1040, 1, 64, 128, True),   # keys past the last query are never visible
+    (700, 660, 1, 16, 128, False),    # rows below Sk see every key
+    (2064, 2064, 1, 16, 64, False),   # long rows: interior and diagonal tiles, several pieces
+])
+def test_indexer_lower_triangle_shapes(dev, Sq, Sk, B, H, D, fp8):
+    """Lower-triangle mode splits paired token blocks (long row + short row)
+    into equal pieces; every computed score must match the oracle and every
+    score above the diagonal must be left untouched."""
+    g = torch.Generator().manual_seed(Sq * 7 + Sk)
+    q = torch.randn((Sq, B, H, D), generator=g).to(torch.bfloat16)
+    k = torch.randn((Sk, B, D), generator=g).to(torch.bfloat16)
+    w = torch.randn((Sq, B, H), generator=g) / H ** 0.5
+    kw = {}
+    if fp8:
+        q, qs = ofp8.tensorwise_quantize(q)
+        k, ks = ofp8.tensorwise_quantize(k)
+        kw = dict(q_scale=qs.to(dev), k_scale=ks.to(dev))
+        ref = oix.compute_index_scores(q.float(), w, k.float(), q_scale=qs, k_scale=ks)
+    else:
+        ref = oix.compute_index_scores(q, w, k)
+    sentinel = torch.full((B, Sq, Sk), 7.0, device=dev)
+    low = index_scores(q.to(dev), w.to(dev), k.to(dev), causal=2, out=sentinel, **kw).cpu()
+    tri = torch.ones(Sq, Sk, dtype=torch.bool).tril()
+    assert _rel_err(low[:, tri], ref[:, tri]) < 1e-3
+    assert (low[:, ~tri] == 7.0).all()
+    neg = index_scores(q.to(dev), w.to(dev), k.to(dev), causal=1, **kw).cpu()
+    assert _rel_err(neg[:, tri], ref[:, tri]) < 1e-3
+    assert torch.isneginf(neg[:, ~tri]).all()
+
+
 def test_indexer_fp8(dev):
     S, B, H, D = 128, 1, 64, 128
     inp = synthetic.indexer_inputs(B, S, H, D, seed=9)
