@@ -78,7 +78,7 @@ struct BwdCfg {
   static constexpr int WAVE_BYTES = (W_SC + (FP8 ? 32 * 4 : 0) + 15) / 16 * 16;
   static constexpr int DQ_PART_BYTES = 32 * D_QK * 4;    // one wave's fp32 dQ tile
   static constexpr int LOOP_BYTES = SHARED_BYTES + WPT * WAVE_BYTES;
-  static constexpr int COMBINE_BYTES = (WPT - 1) * DQ_PART_BYTES;
+  static constexpr int COMBINE_BYTES = DQ_PART_BYTES;        // each wave hands over half its tiles
   static constexpr int LDS_BYTES = LOOP_BYTES > COMBINE_BYTES ? LOOP_BYTES : COMBINE_BYTES;
   static constexpr int DQT = D_QK / 32;
   static constexpr int DVT = D_V / 32;
@@ -99,12 +99,15 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
 
   const int lane = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
   const int g32 = lane >> 5, l32 = lane & 31;
-  const int64_t item = xcd_remap(blockIdx.x, gridDim.x);
-  const int tile = (int)(item % p.ntiles);
-  int64_t rest = item / p.ntiles;
-  const int64_t g = rest % p.G;
-  const int64_t tok = rest / p.G;
-  const int64_t b = tok / p.S;
+  // item = (tok * G + g) * ntiles + tile, tok = b * S + s; every factor is
+  // below 2^31 (checked on the host), so 32-bit divisions suffice
+  const uint32_t item = (uint32_t)xcd_remap(blockIdx.x, gridDim.x);
+  const uint32_t ntl = (uint32_t)p.ntiles, ng = (uint32_t)p.G;
+  const uint32_t rest = ntl == 1 ? item : item / ntl;
+  const int tile = (int)(item - rest * ntl);
+  const int64_t tok = ng == 1 ? rest : rest / ng;
+  const int64_t g = (int64_t)rest - tok * (int64_t)ng;
+  const int64_t b = (int64_t)((uint32_t)tok / (uint32_t)p.S);
 
   unsigned char *QL = smem + C::OFF_QL;
   unsigned char *DOL = smem + C::OFF_DOL;
@@ -126,7 +129,7 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
   const uint32_t row_pitch = (uint32_t)(p.G * Gat::ROWB);
   const int nblk = (int)((p.topk + 31) / 32);
 
-  // this wave's blocks: w, w + WPT, ...; start the first gather before the prologue
+  // this wave's blocks: w, w + WPT, ...
   // Indices, CSR positions and rows of a wave's next block are loaded one block
   // (indices two) ahead with unconditional loads, and the partial-row stores
   // below are unconditional too (masked lanes write a trash row past the
@@ -135,65 +138,92 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
   int blk = w;
   const auto idx_rs = slot_rsrc(idx_row, p.topk);
   const auto pos_rs = slot_rsrc(p.pos_of + entry0, p.topk);
-  int idx_cur = slot_index(load_slot_raw(idx_rs, blk, l32), blk, l32, p.topk, p.S_kv);
+  const int raw0 = load_slot_raw(idx_rs, blk, l32);
   int raw_nxt = load_slot_raw(idx_rs, blk + C::WPT, l32);
   int pos_cur = load_slot_raw(pos_rs, blk, l32);
   const auto kv_rs = make_buffer_rsrc(kv_b, (uint32_t)(p.S_kv * (int64_t)row_pitch));
   const auto sc_rs = make_buffer_rsrc(kv_scale_b, FP8 ? (uint32_t)(p.S_kv * 4) : 0u);
-  typename Gat::Regs rg;
-  gather_issue<Gat>(rg, kv_rs, sc_rs, idx_cur, row_pitch);
   const uint64_t trash = (uint64_t)n_entries * (uint64_t)p.ntiles;  // partial row no entry owns
 
   // ---------------- prologue (all waves): Q, dO tiles, Delta, LSE ----------------
+  // Every load of the prologue is issued at once, through resources that end
+  // at the item's last head (padded heads read zeros), before the first
+  // block's gather: one memory round trip instead of one per loop step.
+  constexpr int NT = 64 * C::WPT;
+  constexpr int QCH = D_QK / 8;   // 8-element chunks per q row
+  constexpr int VCH = D_V / 8;    // 8-element chunks per dO / O row
+  constexpr int QIT = (32 * QCH + NT - 1) / NT;
+  constexpr int VIT = (32 * VCH + NT - 1) / NT;
+  static_assert(VCH <= 16 && (VCH & (VCH - 1)) == 0, "d_v chunks per head: power of two <= 16");
+  const int t = threadIdx.x;
+  const auto q_rs = make_buffer_rsrc(p.q + head0 * D_QK * (FP8 ? 1 : 2), (uint32_t)(nheads * D_QK * (FP8 ? 1 : 2)));
+  const auto do_rs = make_buffer_rsrc(p.dO + head0 * D_V, (uint32_t)(nheads * D_V * 2));
+  const auto o_rs = make_buffer_rsrc(p.o + head0 * D_V, (uint32_t)(nheads * D_V * 2));
+  const auto lse_rs = make_buffer_rsrc(p.lse + head0, (uint32_t)(nheads * 4));
+  i32x4 qv[QIT], dv[VIT], ov[VIT];
+#pragma unroll
+  for (int it = 0; it < QIT; ++it) {
+    const int u = t + NT * it;  // (head u / QCH, chunk u % QCH); u past 32 rows lands past the resource
+    if constexpr (FP8) {
+      const auto r = __builtin_amdgcn_raw_buffer_load_b64(q_rs, u * 8, 0, 0);
+      qv[it] = i32x4{(int)r[0], (int)r[1], 0, 0};
+    } else {
+      qv[it] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(q_rs, u * 16, 0, 0));
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < VIT; ++it) {
+    const int u = t + NT * it;
+    dv[it] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(do_rs, u * 16, 0, 0));
+    ov[it] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(o_rs, u * 16, 0, 0));
+  }
+  const float lse_raw = buffer_load_f32(lse_rs, (t & 31) * 4, 0);
+  float qsc = 1.0f;
+  if constexpr (FP8) qsc = p.q_scale[tok];
+
+  int idx_cur = slot_index(raw0, blk, l32, p.topk, p.S_kv);
+  typename Gat::Regs rg;
+  gather_issue<Gat>(rg, kv_rs, sc_rs, idx_cur, row_pitch);
+
   {
-    const int t = threadIdx.x;
-    constexpr int NT = 64 * C::WPT;
-    float qsc = 1.0f;
-    if constexpr (FP8) qsc = p.q_scale[tok];
-    // Q rows: 32 heads x D_QK / 8 chunks of 8 elements
-    constexpr int QCH = D_QK / 8;
-    for (int u = t; u < 32 * QCH; u += NT) {
-      const int h = u / QCH, c = u % QCH;
-      i32x4 v = {0, 0, 0, 0};
-      if (h < nheads) {
+    // Q rows: 32 heads x QCH chunks of 8 elements (e4m3: dequantised to bf16)
+#pragma unroll
+    for (int it = 0; it < QIT; ++it) {
+      const int u = t + NT * it;
+      if ((32 * QCH) % NT == 0 || u < 32 * QCH) {
+        const int h = u / QCH, c = u % QCH;
+        i32x4 v = qv[it];
         if constexpr (FP8) {
-          const long raw = *reinterpret_cast<const long *>(p.q + (head0 + h) * D_QK + 8 * c);
+          const unsigned long raw = (unsigned long)(uint32_t)qv[it][0] | ((unsigned long)(uint32_t)qv[it][1] << 32);
           uint32_t wq[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const uint32_t c0 = (uint32_t)((unsigned long)raw >> (16 * e)) & 0xffu;
-            const uint32_t c1 = (uint32_t)((unsigned long)raw >> (16 * e + 8)) & 0xffu;
+            const uint32_t c0 = (uint32_t)(raw >> (16 * e)) & 0xffu;
+            const uint32_t c1 = (uint32_t)(raw >> (16 * e + 8)) & 0xffu;
             wq[e] = pack_bf16x2(e4m3_to_f32(c0) * qsc, e4m3_to_f32(c1) * qsc);
           }
           v = i32x4{(int)wq[0], (int)wq[1], (int)wq[2], (int)wq[3]};
-        } else {
-          v = ld_global_16(p.q + ((head0 + h) * D_QK + 8 * c) * 2);
         }
+        *reinterpret_cast<i32x4 *>(QL + h * C::QL_STRIDE + c * 16) = v;
       }
-      *reinterpret_cast<i32x4 *>(QL + h * C::QL_STRIDE + c * 16) = v;
     }
-    // dO rows and Delta = sum_d O dO (8 consecutive threads share a head)
-    constexpr int VCH = D_V / 8;
-    static_assert(VCH <= 16 && (VCH & (VCH - 1)) == 0, "d_v chunks per head: power of two <= 16");
-    for (int u0 = 0; u0 < 32 * VCH; u0 += NT) {
-      const int u = u0 + t;
+    // dO rows and Delta = sum_d O dO (VCH consecutive threads share a head)
+#pragma unroll
+    for (int it = 0; it < VIT; ++it) {
+      const int u = t + NT * it;
       const int h = u / VCH, c = u % VCH;
-      i32x4 dv = {0, 0, 0, 0}, ov = {0, 0, 0, 0};
-      if (u < 32 * VCH && h < nheads) {
-        dv = ld_global_16(p.dO + (head0 + h) * D_V + 8 * c);
-        ov = ld_global_16(p.o + (head0 + h) * D_V + 8 * c);
-      }
-      if (u < 32 * VCH) *reinterpret_cast<i32x4 *>(DOL + h * C::DOL_STRIDE + c * 16) = dv;
+      const bool in_tile = (32 * VCH) % NT == 0 || u < 32 * VCH;
+      if (in_tile) *reinterpret_cast<i32x4 *>(DOL + h * C::DOL_STRIDE + c * 16) = dv[it];
       float part = 0.0f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t du = (uint32_t)dv[e], ou = (uint32_t)ov[e];
+        const uint32_t du = (uint32_t)dv[it][e], ou = (uint32_t)ov[it][e];
         part += bf16_bits_to_f32(ou & 0xffffu) * bf16_bits_to_f32(du & 0xffffu);
         part += bf16_bits_to_f32(ou >> 16) * bf16_bits_to_f32(du >> 16);
       }
 #pragma unroll
       for (int off = 1; off < VCH; off <<= 1) part += __shfl_xor(part, off, 64);
-      if (u < 32 * VCH && c == 0) {
+      if (in_tile && c == 0) {
         float dl = part;
         if (p.delta != nullptr && h < nheads) dl = p.delta[head0 + h];
         LD[32 + h] = dl * p.scale;
@@ -201,19 +231,14 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
     }
     if (t < 32) {
       float lse_h = INFINITY;  // padded heads: P = exp2(x - inf) = 0
-      if (t < nheads) {
-        const float l = p.lse[head0 + t];
-        lse_h = (l == -INFINITY) ? INFINITY : l;  // all-masked row: zero gradient
-      }
+      if (t < nheads) lse_h = (lse_raw == -INFINITY) ? INFINITY : lse_raw;  // all-masked row: zero gradient
       LD[t] = lse_h;
     }
   }
   __syncthreads();
 
-  float qsc = 1.0f;
   long qA8[FP8 ? C::KSTEPS : 1];  // e4m3: raw Q codes as the S A operand (head l32)
   if constexpr (FP8) {
-    qsc = p.q_scale[tok];
 #pragma unroll
     for (int k = 0; k < C::KSTEPS; ++k)
       qA8[k] = l32 < nheads ? *reinterpret_cast<const long *>(p.q + (head0 + l32) * D_QK + 16 * k + 8 * g32) : 0l;
@@ -398,36 +423,44 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
     pos_cur = pos_nxt;
   }
 
-  // ---- combine the waves' dQ partial sums in wave order, then write dQ ----
+  // ---- combine the two waves' dQ partial sums, then write dQ ----
+  // Wave w keeps d-tiles [w * HT, w * HT + HT) and hands the other half to its
+  // partner through LDS; both add in wave order (wave 0's sum + wave 1's), so
+  // the result does not depend on which wave writes a tile.
+  constexpr int HT = C::DQT / 2;
+  static_assert(C::DQT % 2 == 0, "d-tiles split evenly between the two waves");
   __syncthreads();  // every wave is done with the loop's LDS
-  float *dqp = reinterpret_cast<float *>(smem);
-  if (w > 0) {
+  float *dqp = reinterpret_cast<float *>(smem);  // [exporter][tile][16][64]
+  auto export_tiles = [&](int first) {
 #pragma unroll
-    for (int dt = 0; dt < C::DQT; ++dt)
+    for (int tt = 0; tt < HT; ++tt)
 #pragma unroll
-      for (int a = 0; a < 16; ++a) dqp[((w - 1) * C::DQT * 16 + dt * 16 + a) * 64 + lane] = dqacc[dt][a];
-  }
-  __syncthreads();
-  if (w == 0) {
-#pragma unroll 1
-    for (int v = 1; v < C::WPT; ++v)
+      for (int a = 0; a < 16; ++a) dqp[((w * HT + tt) * 16 + a) * 64 + lane] = dqacc[first + tt][a];
+  };
+  auto finish_tiles = [&](int first) {
 #pragma unroll
-      for (int dt = 0; dt < C::DQT; ++dt)
+    for (int tt = 0; tt < HT; ++tt) {
+      const int dt = first + tt;
 #pragma unroll
-        for (int a = 0; a < 16; ++a) dqacc[dt][a] += dqp[((v - 1) * C::DQT * 16 + dt * 16 + a) * 64 + lane];
-    // lane = head l32, d = dt*32 + 8i + 4*g32 + j
-    if (l32 < nheads) {
-      uint16_t *drow = p.dq + (head0 + l32) * D_QK;
-#pragma unroll
-      for (int dt = 0; dt < C::DQT; ++dt)
+      for (int a = 0; a < 16; ++a) {
+        const float other = dqp[(((1 - w) * HT + tt) * 16 + a) * 64 + lane];
+        dqacc[dt][a] = w == 0 ? dqacc[dt][a] + other : other + dqacc[dt][a];
+      }
+      // lane = head l32, d = dt*32 + 8i + 4*g32 + j
+      if (l32 < nheads) {
+        uint16_t *drow = p.dq + (head0 + l32) * D_QK;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const i32x2 pk = {(int)pack_bf16x2(dqacc[dt][4 * i], dqacc[dt][4 * i + 1]),
                             (int)pack_bf16x2(dqacc[dt][4 * i + 2], dqacc[dt][4 * i + 3])};
           *reinterpret_cast<i32x2 *>(drow + dt * 32 + 8 * i + 4 * g32) = pk;
         }
+      }
     }
-  }
+  };
+  if (w == 0) export_tiles(HT); else export_tiles(0);
+  __syncthreads();
+  if (w == 0) finish_tiles(0); else finish_tiles(HT);
 }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
