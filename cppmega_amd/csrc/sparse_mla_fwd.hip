@@ -56,14 +56,17 @@ sparse_mla_fwd_kernel(const FwdParams p) {
 
   const int lane = lane_id(), w = wave_id();
   const int g32 = lane >> 5, l32 = lane & 31;
-  const int64_t nitems = p.B * p.S * p.G * p.ntiles;
-  const int64_t item = xcd_remap(blockIdx.x, gridDim.x) * 4 + w;
+  // item = (tok * G + g) * ntiles + tile, tok = b * S + s; every factor is
+  // below 2^31 (checked on the host), so 32-bit divisions suffice
+  const uint32_t nitems = (uint32_t)(p.B * p.S * p.G * p.ntiles);
+  const uint32_t item = (uint32_t)xcd_remap(blockIdx.x, gridDim.x) * 4u + (uint32_t)w;
   if (item >= nitems) return;  // waves are independent: no workgroup barrier below
-  const int tile = (int)(item % p.ntiles);
-  int64_t rest = item / p.ntiles;
-  const int64_t g = rest % p.G;
-  const int64_t tok = rest / p.G;
-  const int64_t b = tok / p.S;
+  const uint32_t ntl = (uint32_t)p.ntiles, ng = (uint32_t)p.G;
+  const uint32_t rest = ntl == 1 ? item : item / ntl;
+  const int tile = (int)(item - rest * ntl);
+  const int64_t tok = ng == 1 ? rest : rest / ng;
+  const int64_t g = (int64_t)rest - tok * (int64_t)ng;
+  const int64_t b = (int64_t)((uint32_t)tok / (uint32_t)p.S);
 
   unsigned char *Kl = smem + w * C::WAVE_BYTES;
   unsigned char *Kd = Kl + C::KL_BYTES;
@@ -88,16 +91,21 @@ sparse_mla_fwd_kernel(const FwdParams p) {
   typename Gat::Regs rg;
   gather_issue<Gat>(rg, kv_rs, sc_rs, idx_cur, row_pitch);
 
-  // Q as the B operand: lane = head, 8 consecutive d per k-step.
+  // Q as the B operand: lane = head, 8 consecutive d per k-step, through a
+  // resource that ends at the tile's last head (padded heads read zeros), so
+  // the loads carry no branches.
+  const int64_t qrow0 = tok * p.H + g * p.hpg + tile * 32;
+  const int nh = p.hpg - tile * 32 < 32 ? p.hpg - tile * 32 : 32;
+  const auto q_rs = make_buffer_rsrc(p.q + qrow0 * D_QK * (FP8 ? 1 : 2), (uint32_t)(nh * D_QK * (FP8 ? 1 : 2)));
   qop_t qreg[C::KSTEPS];
 #pragma unroll
   for (int k = 0; k < C::KSTEPS; ++k) {
     if constexpr (FP8) {
-      qreg[k] = head_ok ? *reinterpret_cast<const long *>(p.q + qrow * D_QK + 16 * k + 8 * g32) : 0l;
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(q_rs, l32 * D_QK + 16 * k + 8 * g32, 0, 0);
+      qreg[k] = __builtin_bit_cast(long, v);
     } else {
-      i32x4 v = {0, 0, 0, 0};
-      if (head_ok) v = ld_global_16(p.q + (qrow * D_QK + 16 * k + 8 * g32) * 2);
-      qreg[k] = as_bf16x8(v);
+      qreg[k] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                               q_rs, (l32 * D_QK + 16 * k + 8 * g32) * 2, 0, 0));
     }
   }
   float qsc = 1.0f;
@@ -239,7 +247,7 @@ static int launch_fwd(const FwdParams &p, hipStream_t st) {
   }
   const int64_t nitems = p.B * p.S * p.G * p.ntiles;
   const int64_t nblocks = (nitems + 3) / 4;
-  if (nblocks >= (1ll << 31)) return set_error(DSA_ERR_INVALID_ARG, "sparse_mla_fwd: grid too large");
+  if (nitems >= (1ll << 31)) return set_error(DSA_ERR_INVALID_ARG, "sparse_mla_fwd: grid too large");
   hipLaunchKernelGGL((sparse_mla_fwd_kernel<D_QK, D_V, FP8>), dim3((unsigned)nblocks), dim3(256), lds, st, p);
   return check_launch("sparse_mla_fwd");
 }
