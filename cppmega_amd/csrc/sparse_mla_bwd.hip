@@ -137,10 +137,34 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
   // next block's rows never waits for this block's stores.
   int blk = w;
   const auto idx_rs = slot_rsrc(idx_row, p.topk);
-  const auto pos_rs = slot_rsrc(p.pos_of + entry0, p.topk);
   const int raw0 = load_slot_raw(idx_rs, blk, l32);
   int raw_nxt = load_slot_raw(idx_rs, blk + C::WPT, l32);
-  int pos_cur = load_slot_raw(pos_rs, blk, l32);
+  // CSR position of an entry: its kv row's start for this token chunk
+  // (base[b][chunk][row]) plus the chunk's earlier tokens that picked the row
+  // (the bits below this token in mask[b][chunk][row]).  A chunk in which a
+  // token repeats a row has no such closed form: its positions were placed
+  // by the inverse-index scatter and are read from pos_of instead (that
+  // resource is empty for every other chunk, so the load reads nothing).
+  const int64_t s_in_b = tok - b * p.S;
+  const int chunk = (int)(s_in_b / kChunkTokens), tl = (int)(s_in_b % kChunkTokens);
+  const uint32_t below = (1u << tl) - 1u;
+  const int64_t plane = (b * p.NC + chunk) * p.R;
+  const bool dupc = p.dup[b * p.NC + chunk] != 0;
+  const auto mask_rs = make_buffer_rsrc(p.mask + plane, (uint32_t)(p.R * 4));
+  const auto base_rs = make_buffer_rsrc(p.base + plane, (uint32_t)(p.R * 4));
+  const auto pos_rs = slot_rsrc(p.pos_of + entry0, dupc ? p.topk : 0);
+  struct PosParts { int m, b, p; };
+  auto load_pos_parts = [&](int idxv, int bk) {
+    const uint32_t off = idxv >= 0 ? (uint32_t)(idxv * p.G + g) * 4u : 0xffffffffu;
+    PosParts r;
+    r.m = (int)__builtin_amdgcn_raw_buffer_load_b32(mask_rs, (int)off, 0, 0);
+    r.b = (int)__builtin_amdgcn_raw_buffer_load_b32(base_rs, (int)off, 0, 0);
+    r.p = load_slot_raw(pos_rs, bk, l32);
+    return r;
+  };
+  auto csr_pos = [&](const PosParts &r) {
+    return dupc ? r.p : r.b + (int)__popc((uint32_t)r.m & below);
+  };
   const auto kv_rs = make_buffer_rsrc(kv_b, (uint32_t)(p.S_kv * (int64_t)row_pitch));
   const auto sc_rs = make_buffer_rsrc(kv_scale_b, FP8 ? (uint32_t)(p.S_kv * 4) : 0u);
   const uint64_t trash = (uint64_t)n_entries * (uint64_t)p.ntiles;  // partial row no entry owns
@@ -184,6 +208,7 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
   int idx_cur = slot_index(raw0, blk, l32, p.topk, p.S_kv);
   typename Gat::Regs rg;
   gather_issue<Gat>(rg, kv_rs, sc_rs, idx_cur, row_pitch);
+  PosParts pp_cur = load_pos_parts(idx_cur, blk);
 
   {
     // Q rows: 32 heads x QCH chunks of 8 elements (e4m3: dequantised to bf16)
@@ -258,14 +283,14 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
       gather_store_scale<Gat>(rg, Ksc);
     }
     const bool valid = idx_cur >= 0;  // slot slot0 + l32
-    const int32_t pos = pos_cur;
+    const int32_t pos = csr_pos(pp_cur);
     const bool wr = valid && pos >= 0 && pos < n_entries;  // (always true for a valid slot; a guard)
     const uint64_t prow_me = wr ? (uint64_t)(uint32_t)pos * (uint32_t)p.ntiles + tile : trash;
     wave_lds_sync();
     const int raw_nn = load_slot_raw(idx_rs, blk + 2 * C::WPT, l32);
-    const int pos_nxt = load_slot_raw(pos_rs, blk + C::WPT, l32);
     const int idx_nxt = slot_index(raw_nxt, blk + C::WPT, l32, p.topk, p.S_kv);
     gather_issue<Gat>(rg, kv_rs, sc_rs, idx_nxt, row_pitch);
+    const PosParts pp_nxt = load_pos_parts(idx_nxt, blk + C::WPT);
 
     // ---- S = Q K^T and dP = dO V^T  (M = head, N = slot; Q / dO rows from LDS) ----
     f32x16 sacc, dpacc;
@@ -420,7 +445,7 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
     wave_lds_sync();  // K / dS tiles are consumed before the next block's gather lands
     idx_cur = idx_nxt;
     raw_nxt = raw_nn;
-    pos_cur = pos_nxt;
+    pp_cur = pp_nxt;
   }
 
   // ---- combine the two waves' dQ partial sums, then write dQ ----
@@ -613,6 +638,7 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
   cp.gsum = reinterpret_cast<int32_t *>(ws + L.gsum);
   cp.NC = L.NC;
   cp.NQ = L.NQ;
+  cp.dup_only = wide ? 0 : 1;  // the narrow main kernel derives the positions of chunks without repeats
   stage_begin(st);
   int rc = launch_csr(cp, B, st);
   if (rc) return rc;
@@ -630,6 +656,11 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
   p.q_scale = q_scale;
   p.kv_scale = kv_scale;
   p.pos_of = cp.pos_of;
+  p.mask = cp.mask;
+  p.base = cp.base;
+  p.dup = cp.dup;
+  p.R = cp.R;
+  p.NC = cp.NC;
   p.partials = ws + L.partials;
   p.partial_exp = reinterpret_cast<int8_t *>(ws + L.pexp);
   p.B = B;

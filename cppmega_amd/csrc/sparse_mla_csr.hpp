@@ -45,6 +45,7 @@ struct CsrParams {
   int64_t S, S_kv, G, topk;
   int64_t R;        // rows per batch = S_kv * G
   int NC, NQ;       // chunks per batch, chunk groups per batch
+  int dup_only;     // scatter only the chunks with repeats (the main kernel places the rest)
 };
 
 __global__ void fill_i32_kernel(int32_t *p, int64_t n, int32_t v) {
@@ -246,6 +247,7 @@ __global__ void __launch_bounds__(256) csr_scatter_kernel(const CsrParams p) {
   const uint32_t *m = p.mask + (b * p.NC + c) * p.R;
   const int32_t *bs = p.base + (b * p.NC + c) * p.R;
   if (p.dup[b * p.NC + c] == 0) {
+    if (p.dup_only) return;  // block-uniform
     // row r of (token t0 + tl, group g): position = base + earlier tokens of the chunk in r;
     // work items as in the mask kernel, eight in flight
     const int spt = (int)((p.topk + 255) / 256);

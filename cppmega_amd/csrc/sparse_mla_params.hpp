@@ -31,7 +31,12 @@ struct BwdParams {
   uint16_t *dq;
   const float *q_scale;
   const float *kv_scale;
-  const int32_t *pos_of;  // CSR position of each entry (-1: masked slot)
+  const int32_t *pos_of;  // CSR position of each entry (-1: masked slot); chunks with repeats only
+  const uint32_t *mask;   // inverse index: [B][NC][R] token bits per (chunk, kv row)
+  const int32_t *base;    // [B][NC][R] first CSR position of a (chunk, kv row)
+  const int32_t *dup;     // [B][NC] chunk has a token repeating a row
+  int64_t R;              // kv rows per batch (S_kv * G)
+  int NC;                 // token chunks per batch
   unsigned char *partials;
   int8_t *partial_exp;  // fp16 rows: power-of-two scale exponent per (position, tile)
   int64_t B, S, S_kv, H, G, topk;
