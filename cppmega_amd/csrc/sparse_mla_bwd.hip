@@ -139,9 +139,10 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
   const auto idx_rs = slot_rsrc(idx_row, p.topk);
   const int raw0 = load_slot_raw(idx_rs, blk, l32);
   int raw_nxt = load_slot_raw(idx_rs, blk + C::WPT, l32);
-  // CSR position of an entry: its kv row's start for this token chunk
-  // (base[b][chunk][row]) plus the chunk's earlier tokens that picked the row
-  // (the bits below this token in mask[b][chunk][row]).  A chunk in which a
+  // CSR position of an entry: its kv row's start (rowptr), plus the row's
+  // entries in earlier token chunks (base[b][chunk][row]), plus the chunk's
+  // earlier tokens that picked the row (the bits below this token in
+  // mask[b][chunk][row]).  A chunk in which a
   // token repeats a row has no such closed form: its positions were placed
   // by the inverse-index scatter and are read from pos_of instead (that
   // resource is empty for every other chunk, so the load reads nothing).
@@ -152,18 +153,20 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
   const bool dupc = p.dup[b * p.NC + chunk] != 0;
   const auto mask_rs = make_buffer_rsrc(p.mask + plane, (uint32_t)(p.R * 4));
   const auto base_rs = make_buffer_rsrc(p.base + plane, (uint32_t)(p.R * 4));
+  const auto rptr_rs = make_buffer_rsrc(p.rowptr + b * p.R, (uint32_t)(p.R * 4));
   const auto pos_rs = slot_rsrc(p.pos_of + entry0, dupc ? p.topk : 0);
-  struct PosParts { int m, b, p; };
+  struct PosParts { int m, b, s, p; };
   auto load_pos_parts = [&](int idxv, int bk) {
     const uint32_t off = idxv >= 0 ? (uint32_t)(idxv * p.G + g) * 4u : 0xffffffffu;
     PosParts r;
     r.m = (int)__builtin_amdgcn_raw_buffer_load_b32(mask_rs, (int)off, 0, 0);
     r.b = (int)__builtin_amdgcn_raw_buffer_load_b32(base_rs, (int)off, 0, 0);
+    r.s = (int)__builtin_amdgcn_raw_buffer_load_b32(rptr_rs, (int)off, 0, 0);
     r.p = load_slot_raw(pos_rs, bk, l32);
     return r;
   };
   auto csr_pos = [&](const PosParts &r) {
-    return dupc ? r.p : r.b + (int)__popc((uint32_t)r.m & below);
+    return dupc ? r.p : r.s + r.b + (int)__popc((uint32_t)r.m & below);
   };
   const auto kv_rs = make_buffer_rsrc(kv_b, (uint32_t)(p.S_kv * (int64_t)row_pitch));
   const auto sc_rs = make_buffer_rsrc(kv_scale_b, FP8 ? (uint32_t)(p.S_kv * 4) : 0u);
@@ -491,8 +494,8 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct BwdWorkspace {
-  size_t partials, pexp, mask, base, dup, gsum, tot, rowptr, pos_of, total;
-  int NC, NQ;
+  size_t partials, pexp, mask, base, dup, tot, rowptr, pos_of, total;
+  int NC;
 };
 
 static BwdWorkspace bwd_layout(int64_t B, int64_t S, int64_t S_kv, int64_t H, int64_t G, int64_t D_qk,
@@ -502,7 +505,7 @@ static BwdWorkspace bwd_layout(int64_t B, int64_t S, int64_t S_kv, int64_t H, in
   const size_t entries = (size_t)B * S * G * topk;
   const int64_t R = S_kv * G;
   BwdWorkspace L;
-  csr_plan(S, &L.NC, &L.NQ);
+  L.NC = csr_chunks(S);
   // wide heads always keep fp32 partial rows
   const size_t psz = ((flags & DSA_BWD_FP32_PARTIALS) || D_qk > 256) ? 4 : 2;
   size_t off = 0;
@@ -516,8 +519,6 @@ static BwdWorkspace bwd_layout(int64_t B, int64_t S, int64_t S_kv, int64_t H, in
   off += align256((size_t)B * L.NC * R * 4);
   L.dup = off;
   off += align256((size_t)B * L.NC * 4);
-  L.gsum = off;
-  off += align256((size_t)B * L.NQ * R * 4);
   L.tot = off;
   off += align256((size_t)B * R * 4);
   L.rowptr = off;
@@ -635,9 +636,7 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
   cp.G = G;
   cp.topk = topk;
   cp.R = R;
-  cp.gsum = reinterpret_cast<int32_t *>(ws + L.gsum);
   cp.NC = L.NC;
-  cp.NQ = L.NQ;
   cp.dup_only = wide ? 0 : 1;  // the narrow main kernel derives the positions of chunks without repeats
   stage_begin(st);
   int rc = launch_csr(cp, B, st);
@@ -660,6 +659,7 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
   p.base = cp.base;
   p.dup = cp.dup;
   p.R = cp.R;
+  p.rowptr = cp.rowptr;
   p.NC = cp.NC;
   p.partials = ws + L.partials;
   p.partial_exp = reinterpret_cast<int8_t *>(ws + L.pexp);

@@ -11,26 +11,25 @@ namespace dsa {
 // ---------------------------------------------------------------------------
 // Entry e = ((b*S + t)*G + g)*topk + slot; its row (within batch b) is
 // r = j*G + g for a valid index j.  Tokens are grouped into chunks of 32
-// within one batch (NC chunks per batch); chunks form groups of CG = 16.
+// within one batch (NC chunks per batch).
 //   csr_mask     mask[b][c][r]  = bit tl set when token 32c + tl references
 //                                 row r; dup[b][c] = some (token, group)
 //                                 references one row twice, and then the exact
 //                                 counts go to base[b][c][r] (a bit cannot
 //                                 count repeats); count(c, r) below is that
 //                                 count or popcount(mask)
-//   csr_gsum     gsum[b][q][r]  = entries of row r in the chunks of group q
-//   csr_rows     tot[b*R + r]   = row total; gsum -> exclusive prefix over groups
+//   csr_colscan  base[b][c][r]  = entries of row r in the chunks before c
+//                                 (exclusive prefix over chunks), tot = row total
 //   csr_scan     rowptr         = exclusive prefix of tot
-//   csr_bases    base[b][c][r]  = rowptr + entries of row r in earlier chunks
-//   csr_scatter  pos_of[e]      = base + popcount of the earlier tokens' bits:
-//                                 entries of a row in ascending entry order
+//   csr_scatter  pos_of[e]      = rowptr + base + popcount of the earlier
+//                                 tokens' bits: entries of a row in ascending
+//                                 entry order
 // Without repeats a row's entries inside a chunk are ordered by token alone,
-// so every entry's position is computed independently; a chunk with a repeat
-// is placed by one thread in entry order instead (the same positions the
-// stable sort defines).  Every thread touches at most CG chunks, so no kernel
-// walks a long serial chain of global loads.
+// so every entry's position is computed independently (the SparseMLA
+// backward's main kernel computes it itself and the scatter only handles
+// chunks with repeats); a chunk with a repeat is placed by one thread in
+// entry order instead (the same positions the stable sort defines).
 
-constexpr int kChunkGroup = 16;
 constexpr int kChunkTokens = 32;  // tokens per chunk: one bit each in a 32-bit mask
 
 struct CsrParams {
@@ -38,13 +37,12 @@ struct CsrParams {
   uint32_t *mask;   // [B][NC][R]
   int32_t *base;    // [B][NC][R]
   int32_t *dup;     // [B][NC]
-  int32_t *gsum;    // [B][NQ][R]
   int32_t *tot;     // [B*R]
   int32_t *rowptr;  // [B*R + 1]
   int32_t *pos_of;  // [entries]: CSR position of each entry, -1 for a masked slot
   int64_t S, S_kv, G, topk;
   int64_t R;        // rows per batch = S_kv * G
-  int NC, NQ;       // chunks per batch, chunk groups per batch
+  int NC;           // chunks per batch
   int dup_only;     // scatter only the chunks with repeats (the main kernel places the rest)
 };
 
@@ -120,36 +118,47 @@ __device__ __forceinline__ int32_t chunk_count(const CsrParams &p, int64_t b, in
   return p.dup[b * p.NC + c] ? p.base[cell] : (int32_t)__popc(p.mask[cell]);
 }
 
-// grid (ceil(R / 256), B * NQ): one thread per (b, q, r): entries of row r in
-// the chunks of group q ((b, q) is uniform per workgroup)
-__global__ void csr_gsum_kernel(const CsrParams p, int64_t B) {
-  const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (r >= p.R) return;
-  const int64_t bq = blockIdx.y, q = bq % p.NQ, b = bq / p.NQ;
-  const int64_t x = bq * p.R + r;
-  const int c0 = (int)q * kChunkGroup;
-  int32_t v[kChunkGroup];
-#pragma unroll
-  for (int k = 0; k < kChunkGroup; ++k) v[k] = (c0 + k < p.NC) ? chunk_count(p, b, c0 + k, r) : 0;
+// grid (ceil(R / 64), B), 8 waves: lane = row, wave w = a contiguous eighth of
+// the chunks.  Pass 1 totals each wave's chunks per row; pass 2 re-reads the
+// counts and writes the exclusive prefix over chunks into base[b][c][r] (a
+// chunk's exact count, kept in base for chunks with repeats, is read before
+// the same lane overwrites it).
+__global__ void __launch_bounds__(512) csr_colscan_kernel(const CsrParams p) {
+  constexpr int TILE = 16;
+  __shared__ int32_t wtot[8][64];
+  const int lane = lane_id(), w = wave_id();
+  const int64_t b = blockIdx.y;
+  const int64_t r = (int64_t)blockIdx.x * 64 + lane;
+  const bool rok = r < p.R;
+  const int c_lo = (int)((int64_t)p.NC * w / 8), c_hi = (int)((int64_t)p.NC * (w + 1) / 8);
   int32_t s = 0;
+  for (int c0 = c_lo; c0 < c_hi; c0 += TILE) {
+    int32_t v[TILE];
 #pragma unroll
-  for (int k = 0; k < kChunkGroup; ++k) s += v[k];
-  p.gsum[x] = s;
-}
-
-// one thread per (b, r): row total, and gsum -> exclusive prefix over groups
-__global__ void csr_rows_kernel(const CsrParams p, int64_t B) {
-  const int64_t x = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (x >= B * p.R) return;
-  const int64_t b = x / p.R, r = x % p.R;
-  int32_t *gs = p.gsum + b * p.NQ * p.R + r;
-  int32_t run = 0;
-  for (int q = 0; q < p.NQ; ++q) {
-    const int32_t t = gs[(int64_t)q * p.R];
-    gs[(int64_t)q * p.R] = run;
-    run += t;
+    for (int u = 0; u < TILE; ++u) v[u] = (c0 + u < c_hi && rok) ? chunk_count(p, b, c0 + u, r) : 0;
+#pragma unroll
+    for (int u = 0; u < TILE; ++u) s += v[u];
   }
-  p.tot[x] = run;
+  wtot[w][lane] = s;
+  __syncthreads();
+  int32_t run = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int32_t t = wtot[i][lane];
+    run += i < w ? t : 0;
+    tot += t;
+  }
+  for (int c0 = c_lo; c0 < c_hi; c0 += TILE) {
+    int32_t v[TILE];
+#pragma unroll
+    for (int u = 0; u < TILE; ++u) v[u] = (c0 + u < c_hi && rok) ? chunk_count(p, b, c0 + u, r) : 0;
+#pragma unroll
+    for (int u = 0; u < TILE; ++u) {
+      if (c0 + u < c_hi && rok) p.base[(b * p.NC + c0 + u) * p.R + r] = run;
+      run += v[u];
+    }
+  }
+  if (w == 0 && rok) p.tot[b * p.R + r] = tot;
 }
 
 // Exclusive scan of cnt[0..n) into rowptr[0..n] with one 1024-thread
@@ -214,26 +223,6 @@ __global__ void __launch_bounds__(1024) csr_scan_kernel(const int32_t *cnt, int3
   if (tid == 0) rowptr[n] = carry;
 }
 
-// grid (ceil(R / 256), B * NQ): one thread per (b, q, r): base[b][c][r] =
-// absolute start of chunk c's entries of row r
-__global__ void csr_bases_kernel(const CsrParams p, int64_t B) {
-  const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (r >= p.R) return;
-  const int64_t bq = blockIdx.y, q = bq % p.NQ, b = bq / p.NQ;
-  const int64_t x = bq * p.R + r;
-  const int c0 = (int)q * kChunkGroup;
-  int32_t *bs = p.base + (b * p.NC + c0) * p.R + r;
-  int32_t v[kChunkGroup];  // all counts are read before any base overwrites one
-#pragma unroll
-  for (int k = 0; k < kChunkGroup; ++k) v[k] = (c0 + k < p.NC) ? chunk_count(p, b, c0 + k, r) : 0;
-  int32_t run = p.rowptr[b * p.R + r] + p.gsum[x];
-#pragma unroll
-  for (int k = 0; k < kChunkGroup; ++k) {
-    if (c0 + k < p.NC) bs[(int64_t)k * p.R] = run;
-    run += v[k];
-  }
-}
-
 // grid (NC, B), 256 threads; dynamic LDS = R ints (cursors of the serial path).
 __global__ void __launch_bounds__(256) csr_scatter_kernel(const CsrParams p) {
   extern __shared__ int32_t cur[];
@@ -246,6 +235,7 @@ __global__ void __launch_bounds__(256) csr_scatter_kernel(const CsrParams p) {
   const int64_t e_first = ((b * p.S + t0) * p.G) * p.topk;
   const uint32_t *m = p.mask + (b * p.NC + c) * p.R;
   const int32_t *bs = p.base + (b * p.NC + c) * p.R;
+  const int32_t *rp = p.rowptr + b * p.R;
   if (p.dup[b * p.NC + c] == 0) {
     if (p.dup_only) return;  // block-uniform
     // row r of (token t0 + tl, group g): position = base + earlier tokens of the chunk in r;
@@ -269,7 +259,7 @@ __global__ void __launch_bounds__(256) csr_scatter_kernel(const CsrParams p) {
         const int w = w0 + u, sg = spt == 1 ? w : w / spt;
         const bool ok = j[u] >= 0 && j[u] < p.S_kv;
         const int64_t r = ok ? (int64_t)j[u] * G + (G == 1 ? 0 : sg % G) : 0;
-        bv[u] = ok ? bs[r] : -1;
+        bv[u] = ok ? rp[r] + bs[r] : -1;
         mv[u] = ok ? m[r] : 0u;
       }
 #pragma unroll
@@ -284,7 +274,7 @@ __global__ void __launch_bounds__(256) csr_scatter_kernel(const CsrParams p) {
     }
   } else {
     // a row repeats inside a (token, group): one thread walks the entries in order
-    for (int64_t r = tid; r < p.R; r += 256) cur[r] = bs[r];
+    for (int64_t r = tid; r < p.R; r += 256) cur[r] = rp[r] + bs[r];
     __syncthreads();
     if (tid == 0) {
       for (int64_t sg = 0; sg < nseg; ++sg) {
@@ -393,10 +383,7 @@ dkv_reduce_kernel(const int32_t *rowptr, const unsigned char *partials, const in
 }
 
 // Chunking of the inverse index: 32-token chunks (one mask bit per token).
-static void csr_plan(int64_t S, int *NC, int *NQ) {
-  *NC = (int)((S + kChunkTokens - 1) / kChunkTokens);
-  *NQ = (*NC + kChunkGroup - 1) / kChunkGroup;
-}
+static int csr_chunks(int64_t S) { return (int)((S + kChunkTokens - 1) / kChunkTokens); }
 
 static int launch_csr(const CsrParams &cp, int64_t B, hipStream_t st) {
   const size_t lds = (size_t)cp.R * 4;
@@ -411,13 +398,10 @@ static int launch_csr(const CsrParams &cp, int64_t B, hipStream_t st) {
   }
   const int64_t rows = B * cp.R;
   const dim3 cgrid((unsigned)cp.NC, (unsigned)B);
-  const unsigned rgrid = (unsigned)((rows + 255) / 256);
-  const dim3 qgrid((unsigned)((cp.R + 255) / 256), (unsigned)(B * cp.NQ));
+  const dim3 sgrid((unsigned)((cp.R + 63) / 64), (unsigned)B);
   hipLaunchKernelGGL(csr_mask_kernel, cgrid, dim3(256), lds, st, cp);
-  hipLaunchKernelGGL(csr_gsum_kernel, qgrid, dim3(256), 0, st, cp, B);
-  hipLaunchKernelGGL(csr_rows_kernel, dim3(rgrid), dim3(256), 0, st, cp, B);
+  hipLaunchKernelGGL(csr_colscan_kernel, sgrid, dim3(512), 0, st, cp);
   hipLaunchKernelGGL(csr_scan_kernel, dim3(1), dim3(1024), 0, st, cp.tot, cp.rowptr, rows);
-  hipLaunchKernelGGL(csr_bases_kernel, qgrid, dim3(256), 0, st, cp, B);
   hipLaunchKernelGGL(csr_scatter_kernel, cgrid, dim3(256), lds, st, cp);
   return check_launch("sparse_mla_bwd(csr)");
 }

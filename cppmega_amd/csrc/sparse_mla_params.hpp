@@ -35,6 +35,7 @@ struct BwdParams {
   const uint32_t *mask;   // inverse index: [B][NC][R] token bits per (chunk, kv row)
   const int32_t *base;    // [B][NC][R] first CSR position of a (chunk, kv row)
   const int32_t *dup;     // [B][NC] chunk has a token repeating a row
+  const int32_t *rowptr;  // [B*R + 1] first CSR position of each kv row
   int64_t R;              // kv rows per batch (S_kv * G)
   int NC;                 // token chunks per batch
   unsigned char *partials;
