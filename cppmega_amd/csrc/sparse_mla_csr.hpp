@@ -71,15 +71,22 @@ __global__ void __launch_bounds__(256) csr_mask_kernel(const CsrParams p) {
   const int nw = (int)nseg * spt;
   const int G = (int)p.G;
   int dup = 0;
-  for (int w0 = 0; w0 < nw; w0 += 8) {
-    int32_t j[8];
+  // all of a 32-token chunk's index loads (at topk <= 256) go out together:
+  // unconditional bounded loads, invalid work items land past the resource
+  constexpr int U = 32;
+  const auto seg_rs = make_buffer_rsrc(seg_idx, (uint32_t)(nseg * p.topk * 4));
+  for (int w0 = 0; w0 < nw; w0 += U) {
+    int32_t j[U];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int w = w0 + u, sg = spt == 1 ? w : w / spt, s = (spt == 1 ? 0 : w % spt) * 256 + tid;
-      j[u] = (w < nw && s < p.topk) ? seg_idx[(int64_t)sg * p.topk + s] : -1;
+      const bool ok = w < nw && s < p.topk;
+      const uint32_t off = ok ? (uint32_t)((sg * p.topk + s) * 4) : 0xffffffffu;
+      const int32_t v = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(seg_rs, (int)off, 0, 0);
+      j[u] = ok ? v : -1;
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int w = w0 + u, sg = spt == 1 ? w : w / spt;
       if (j[u] >= 0 && j[u] < p.S_kv) {
         const uint32_t bit = 1u << (G == 1 ? sg : sg / G);
