@@ -125,22 +125,25 @@ __device__ __forceinline__ int32_t chunk_count(const CsrParams &p, int64_t b, in
   return p.dup[b * p.NC + c] ? p.base[cell] : (int32_t)__popc(p.mask[cell]);
 }
 
-// grid (ceil(R / 64), B), 8 waves: lane = row, wave w = a contiguous eighth of
-// the chunks.  Pass 1 totals each wave's chunks per row; pass 2 re-reads the
-// counts and writes the exclusive prefix over chunks into base[b][c][r] (a
-// chunk's exact count, kept in base for chunks with repeats, is read before
-// the same lane overwrites it).
-__global__ void __launch_bounds__(512) csr_colscan_kernel(const CsrParams p) {
+// grid (ceil(R / 64), B), 16 waves: lane = row, wave w = a contiguous
+// sixteenth of the chunks.  Each wave totals its chunks per row, the waves'
+// totals are combined in LDS, and each wave then writes the exclusive prefix
+// over chunks into base[b][c][r] (a chunk's exact count, kept in base for
+// chunks with repeats, is read before the same lane overwrites it).  A wave
+// with at most TILE chunks (every wave while NC <= 16 * TILE) keeps its counts
+// in registers between the two steps; longer ranges re-read them.
+constexpr int kScanWaves = 16;
+__global__ void __launch_bounds__(64 * kScanWaves) csr_colscan_kernel(const CsrParams p) {
   constexpr int TILE = 16;
-  __shared__ int32_t wtot[8][64];
+  __shared__ int32_t wtot[kScanWaves][64];
   const int lane = lane_id(), w = wave_id();
   const int64_t b = blockIdx.y;
   const int64_t r = (int64_t)blockIdx.x * 64 + lane;
   const bool rok = r < p.R;
-  const int c_lo = (int)((int64_t)p.NC * w / 8), c_hi = (int)((int64_t)p.NC * (w + 1) / 8);
+  const int c_lo = (int)((int64_t)p.NC * w / kScanWaves), c_hi = (int)((int64_t)p.NC * (w + 1) / kScanWaves);
+  int32_t v[TILE];
   int32_t s = 0;
   for (int c0 = c_lo; c0 < c_hi; c0 += TILE) {
-    int32_t v[TILE];
 #pragma unroll
     for (int u = 0; u < TILE; ++u) v[u] = (c0 + u < c_hi && rok) ? chunk_count(p, b, c0 + u, r) : 0;
 #pragma unroll
@@ -150,15 +153,17 @@ __global__ void __launch_bounds__(512) csr_colscan_kernel(const CsrParams p) {
   __syncthreads();
   int32_t run = 0, tot = 0;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < kScanWaves; ++i) {
     const int32_t t = wtot[i][lane];
     run += i < w ? t : 0;
     tot += t;
   }
+  const bool one_tile = c_hi - c_lo <= TILE;  // wave-uniform
   for (int c0 = c_lo; c0 < c_hi; c0 += TILE) {
-    int32_t v[TILE];
+    if (!one_tile) {
 #pragma unroll
-    for (int u = 0; u < TILE; ++u) v[u] = (c0 + u < c_hi && rok) ? chunk_count(p, b, c0 + u, r) : 0;
+      for (int u = 0; u < TILE; ++u) v[u] = (c0 + u < c_hi && rok) ? chunk_count(p, b, c0 + u, r) : 0;
+    }
 #pragma unroll
     for (int u = 0; u < TILE; ++u) {
       if (c0 + u < c_hi && rok) p.base[(b * p.NC + c0 + u) * p.R + r] = run;
@@ -407,7 +412,7 @@ static int launch_csr(const CsrParams &cp, int64_t B, hipStream_t st) {
   const dim3 cgrid((unsigned)cp.NC, (unsigned)B);
   const dim3 sgrid((unsigned)((cp.R + 63) / 64), (unsigned)B);
   hipLaunchKernelGGL(csr_mask_kernel, cgrid, dim3(256), lds, st, cp);
-  hipLaunchKernelGGL(csr_colscan_kernel, sgrid, dim3(512), 0, st, cp);
+  hipLaunchKernelGGL(csr_colscan_kernel, sgrid, dim3(64 * kScanWaves), 0, st, cp);
   hipLaunchKernelGGL(csr_scan_kernel, dim3(1), dim3(1024), 0, st, cp.tot, cp.rowptr, rows);
   hipLaunchKernelGGL(csr_scatter_kernel, cgrid, dim3(256), lds, st, cp);
   return check_launch("sparse_mla_bwd(csr)");
