@@ -335,25 +335,38 @@ dkv_reduce_kernel(const int32_t *rowptr, const unsigned char *partials, const in
   for (int q = 0; q < CPL; ++q)
 #pragma unroll
     for (int x = 0; x < EPC; ++x) acc[q][x] = 0.0f;
-  for (int64_t kb = k0; kb < k1; kb += EPI * U) {
-    i32x4 v[U][CPL];
-    float sc[U];
+  // Batches of EPI * U items: batch j+1 is loaded (unconditional streaming
+  // buffer loads through a resource that ends at the wave's last item, so
+  // items past it read zeros) while batch j is summed.
+  constexpr int STEP = EPI * U;
+  const int64_t nk = k1 - k0;
+  auto issue = [&](int64_t off, i32x4 (&v)[U][CPL], int (&e)[U]) {
+    const int64_t left = nk - off;
+    const int64_t cnt = left <= 0 ? 0 : (left < STEP ? left : STEP);
+    const int64_t first = left <= 0 ? k0 : k0 + off;
+    const auto rs = make_buffer_rsrc(partials + first * ROWB, (uint32_t)(cnt * ROWB));
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t k = kb + EPI * u + grp;
-      sc[u] = 0.0f;
-      if constexpr (!F32P) {
-        if (k < k1) sc[u] = exp2i(-(int)partial_exp[k]);
-      }
+      const int item = EPI * u + grp;
 #pragma unroll
       for (int q = 0; q < CPL; ++q) {
         const int cc = c + 64 * q;
-        v[u][q] = i32x4{0, 0, 0, 0};
-        if (k < k1 && cc < NCR) v[u][q] = ld_stream_16(partials + k * ROWB + cc * 16);
+        const uint32_t o = cc < NCR ? (uint32_t)(item * ROWB + cc * 16) : 0xffffffffu;
+        v[u][q] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)o, 0, 2));
       }
+      e[u] = 0;
     }
+    if constexpr (!F32P) {
+      const auto es = make_buffer_rsrc(partial_exp + first, (uint32_t)cnt);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        e[u] = (int)(int8_t)(uint8_t)__builtin_amdgcn_raw_buffer_load_b8(es, EPI * u + grp, 0, 0);
+    }
+  };
+  auto accumulate = [&](const i32x4 (&v)[U][CPL], const int (&e)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      const float sc = F32P ? 1.0f : exp2i(-e[u]);
 #pragma unroll
       for (int q = 0; q < CPL; ++q) {
 #pragma unroll
@@ -362,11 +375,21 @@ dkv_reduce_kernel(const int32_t *rowptr, const unsigned char *partials, const in
             acc[q][x] += __int_as_float(v[u][q][x]);
           } else {
             const uint32_t h = ((uint32_t)v[u][q][x >> 1] >> (16 * (x & 1))) & 0xffffu;
-            acc[q][x] += f16_bits_to_f32(h) * sc[u];  // exact: sc is a power of two
+            acc[q][x] += f16_bits_to_f32(h) * sc;  // exact: sc is a power of two
           }
         }
       }
     }
+  };
+  i32x4 va[U][CPL], vb[U][CPL];
+  int ea[U], eb[U];
+  issue(0, va, ea);
+  for (int64_t off = 0; off < nk; off += 2 * STEP) {
+    issue(off + STEP, vb, eb);
+    accumulate(va, ea);
+    if (off + STEP >= nk) break;  // wave-uniform
+    issue(off + 2 * STEP, va, ea);
+    accumulate(vb, eb);
   }
 #pragma unroll
   for (int off = LPE; off < 64; off *= 2) {
