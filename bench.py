@@ -198,17 +198,17 @@ def algorithmic_work():
         "fwd": {"flops": 2 * B * S * H * TOPK * (D_QK + D_V), "bytes": q_b + kv_b + idx_b + o_b + lse_b},
         # whole backward op (three stages); the stages below split its time
         "bwd": {"flops": bwd_flops, "bytes": None},
-        # inverse index: indices read twice (histogram, scatter), refs written once,
-        # 16-token chunk histogram written once and read three times
-        # indices read twice, positions written once; per (chunk, row) a mask word written
-        # and read three times and a base word written and read once
-        "bwd_csr": {"flops": 0, "bytes": 3 * 4 * ENTRIES + 6 * 4 * B * CSR_CHUNKS * S},
-        # every backward FLOP; reads q, kv, o, dO, indices, lse; writes dq and one fp16
-        # partial dKV row (+ int8 exponent) per (token, slot)
+        # inverse index: indices read once; per (32-token chunk, kv row) a mask word
+        # written and read once and a base word written once (the row scan is small)
+        "bwd_csr": {"flops": 0, "bytes": 4 * ENTRIES + 3 * 4 * B * CSR_CHUNKS * S},
+        # every backward FLOP; reads q, kv, o, dO, indices, lse and the mask / base planes
+        # an entry's CSR position comes from; writes dq and one fp16 partial dKV row
+        # (+ int8 exponent) per (token, slot)
         "bwd_main": {"flops": bwd_flops,
-                     "bytes": q_b + kv_b + 2 * o_b + idx_b + lse_b + q_b + ENTRIES * (2 * D_QK + 1)},
-        # partial rows + exponents + refs read once, bf16 dKV written once
-        "bwd_reduce": {"flops": 0, "bytes": ENTRIES * (2 * D_QK + 1 + 4) + 2 * KV_ROWS * D_QK},
+                     "bytes": q_b + kv_b + 2 * o_b + idx_b + lse_b + q_b + ENTRIES * (2 * D_QK + 1)
+                     + 2 * 4 * B * CSR_CHUNKS * S},
+        # partial rows + exponents + row starts read once, bf16 dKV written once
+        "bwd_reduce": {"flops": 0, "bytes": ENTRIES * (2 * D_QK + 1) + 4 * KV_ROWS + 2 * KV_ROWS * D_QK},
     }
 
 
