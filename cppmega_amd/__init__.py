@@ -1,12 +1,14 @@
 """cppmega_amd — MI355X (gfx950) DeepSeek Sparse Attention hot path.
 
 Host code mirrors cppmega's Python surface (``sparse_mla_ops``,
-``dsa_indexer_fused_patch``, top-k, ``index_cache_patch``) and calls the
+``dsa_indexer_fused_patch``, top-k, ``index_cache_patch``,
+``dsa_splitk_indexer_loss``) and calls the
 hand-written HIP kernels of ``_lib/libdsa_hip.so`` through the C-ABI declared
 in ``include/dsa_hip.h``.
 """
 from . import _lib
 from .dsa_indexer_fused_patch import apply_dsa_indexer_fused_patch, compute_index_scores_fused_bf16, index_scores
+from .dsa_splitk_indexer_loss import compute_dsa_indexer_loss_splitk, indexer_kl_loss
 from .dsa_topk import fused_qk_topk_naive, indexer_topk, topk_indices
 from .index_cache_patch import IndexCacheSchedule, apply_index_cache_patch
 
@@ -14,9 +16,11 @@ __all__ = [
     "IndexCacheSchedule",
     "apply_dsa_indexer_fused_patch",
     "apply_index_cache_patch",
+    "compute_dsa_indexer_loss_splitk",
     "compute_index_scores_fused_bf16",
     "fused_qk_topk_naive",
     "index_scores",
+    "indexer_kl_loss",
     "indexer_topk",
     "topk_indices",
 ]

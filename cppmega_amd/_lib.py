@@ -23,6 +23,8 @@ DSA_ERR_WORKSPACE = -4
 DTYPE_BF16 = 0
 DTYPE_E4M3 = 1
 DTYPE_F32 = 2
+DTYPE_I32 = 3
+DTYPE_I64 = 4
 
 BWD_FP32_PARTIALS = 1
 
@@ -38,6 +40,8 @@ EXPORTED_SYMBOLS = (
     "dsa_topk",
     "dsa_fp8_quantize_workspace_size",
     "dsa_fp8_tensorwise_quantize",
+    "dsa_indexer_kl_loss_workspace_size",
+    "dsa_indexer_kl_loss",
     "dsa_stage_timing",
     "dsa_stage_times",
 )
@@ -68,6 +72,10 @@ _SIGNATURES = {
     "dsa_fp8_quantize_workspace_size": (_size_t, []),
     "dsa_fp8_tensorwise_quantize": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p,
                                            _c_void_p, _size_t, _c_void_p]),
+    "dsa_indexer_kl_loss_workspace_size": (_size_t, [_i64] * 5 + [_i32]),
+    "dsa_indexer_kl_loss": (_i32, [_c_void_p, _c_void_p, _i32, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                   _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _i32,
+                                   _c_void_p, _size_t, _c_void_p]),
     "dsa_stage_timing": (_i32, [_i32]),
     "dsa_stage_times": (_i32, [_i32, ctypes.POINTER(ctypes.c_float), _i32]),
 }

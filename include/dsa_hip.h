@@ -37,7 +37,9 @@ enum dsa_status {
 enum dsa_dtype {
   DSA_DTYPE_BF16 = 0,        /* bfloat16                                     */
   DSA_DTYPE_E4M3 = 1,        /* OCP float8 e4m3fn (max 448), gfx950 native   */
-  DSA_DTYPE_F32 = 2          /* float32                                      */
+  DSA_DTYPE_F32 = 2,         /* float32                                      */
+  DSA_DTYPE_I32 = 3,         /* int32 (index tensors)                        */
+  DSA_DTYPE_I64 = 4          /* int64 (index tensors)                        */
 };
 
 /* Per-thread message for the last non-zero status returned on this thread. */
@@ -168,6 +170,42 @@ int dsa_fp8_tensorwise_quantize(const void *x, int64_t n, int in_dtype,
                                 uint8_t *out_fp8, float *scale_inv,
                                 void *workspace, size_t workspace_bytes,
                                 void *stream);
+
+/*
+ * DSA indexer KL loss (the indexer's training signal):
+ *   a_h[t, s] = softmax_scale * query[t, b, h] . key[s, b, h / (H / G)]
+ *   P[t, s]   = mean_h softmax over s <= t of a_h[t, :]      (sparse: and s in
+ *               the row's top-k set)
+ *   Q[t, s]   = softmax over all s in [0, Sk) of index_scores[b, t, :] (sparse:
+ *               over the top-k set)
+ *   row_loss[b, t] = sum_s P (ln(P + 1e-10) - ln(Q + 1e-10)),
+ *   loss = loss_coeff * mean over (b, t) of row_loss.
+ * Replaces compute_dsa_indexer_loss_splitk
+ *   (cppmega/megatron/dsa_splitk_indexer_loss.py:328-468), the Triton split-K
+ *   form of Megatron's compute_dsa_indexer_loss
+ *   (clone at tests/test_dsa_splitk_indexer_loss.py:29-83).
+ *
+ *   index_scores [B, Sq, Sk] f32
+ *   topk_indices [B, Sq, topk] int32 / int64 (topk_dtype), used when sparse != 0;
+ *                values outside [0, Sk) are ignored, duplicates count once
+ *   query [Sq, B, H, D] bf16, key [Sk, B, G, D] bf16 (G divides H; G = H is
+ *                the reference's per-head key), D in {64, 128, 192, 256}
+ *   loss [1] f32 (written), row_loss [B, Sq] f32 (written; may be NULL)
+ * A row with no admissible attention column (sparse: no top-k column <= t) or
+ * whose index softmax is undefined (all -inf, any NaN or +inf) gets a NaN row
+ * loss, as the reference's softmax does, and the mean is then NaN.
+ * Deterministic: fixed summation orders, no global atomics.
+ * Limits: B * Sq * Sk < 2^29; sparse mode Sk <= 32768.
+ */
+size_t dsa_indexer_kl_loss_workspace_size(int64_t B, int64_t Sq, int64_t Sk,
+                                          int64_t H, int64_t D, int sparse);
+int dsa_indexer_kl_loss(const float *index_scores, const void *topk_indices,
+                        int topk_dtype, int64_t topk, const void *query,
+                        const void *key, float *loss, float *row_loss,
+                        int64_t B, int64_t Sq, int64_t Sk, int64_t H,
+                        int64_t G, int64_t D, float softmax_scale,
+                        float loss_coeff, int sparse, void *workspace,
+                        size_t workspace_bytes, void *stream);
 
 /*
  * Stage timing (measurement aid; no counterpart in the reference, which

@@ -20,6 +20,12 @@ definitions, sharing no code with the oracle or the HIP path:
   fp8.npz           e4m3fn code of x * (448 / amax(|x|)) chosen by a brute-force
                     nearest search over the 254 finite codes (ties to the code
                     with an even mantissa, saturation at +-448).
+  indexer_loss_*.npz per-position KL of the DSA indexer loss from explicit loops:
+                    per head, a softmax over the columns s <= t (and, sparse, in
+                    the row's top-k set) of scale * q . k; the head mean P; the
+                    index softmax Q over all columns (sparse: the top-k set); then
+                    sum_s P (ln(P + 1e-10) - ln(Q + 1e-10)).  A row with no
+                    admissible column is NaN.
 
 Inputs are bf16-representable (stored as their uint16 bit patterns), so every
 implementation reads exactly the same numbers.
@@ -230,12 +236,91 @@ def make_fp8(name, seed, n):
                         scale_inv=np.float32(np.float32(1.0) / scale), codes=codes)
 
 
+# ---------------------------------------------------------------------------
+# DSA indexer KL loss
+# ---------------------------------------------------------------------------
+def indexer_loss_rows_expected(idx_scores, topk, q, k, scale, sparse):
+    """idx_scores [B,Sq,Sk], topk [B,Sq,K], q [Sq,B,H,D], k [Sk,B,G,D] (float64) -> [B,Sq]."""
+    Sq, B, H, D = q.shape
+    Sk, G = k.shape[0], k.shape[2]
+    rows = np.zeros((B, Sq))
+    for b in range(B):
+        for t in range(Sq):
+            chosen = set(int(j) for j in topk[b, t] if 0 <= j < Sk) if sparse else set(range(Sk))
+            att_cols = [s for s in range(Sk) if s <= t and s in chosen]
+            if not att_cols or not chosen:
+                rows[b, t] = math.nan
+                continue
+            P = [0.0] * Sk
+            for h in range(H):
+                g = h // (H // G)
+                logit = {s: scale * sum(float(q[t, b, h, d]) * float(k[s, b, g, d]) for d in range(D))
+                         for s in att_cols}
+                mx = max(logit.values())
+                z = sum(math.exp(v - mx) for v in logit.values())
+                for s in att_cols:
+                    P[s] += math.exp(logit[s] - mx) / z / H
+            idx_cols = sorted(chosen)
+            mx = max(float(idx_scores[b, t, s]) for s in idx_cols)
+            z = sum(math.exp(float(idx_scores[b, t, s]) - mx) for s in idx_cols)
+            tot = 0.0
+            for s in range(Sk):
+                if P[s] == 0.0:
+                    continue
+                Qs = math.exp(float(idx_scores[b, t, s]) - mx) / z if s in chosen else 0.0
+                tot += P[s] * (math.log(P[s] + 1e-10) - math.log(Qs + 1e-10))
+            rows[b, t] = tot
+    return rows
+
+
+def make_indexer_loss(name, seed, B, Sq, Sk, H, G, D, K):
+    rng = np.random.default_rng(seed)
+    qb = bf16_bits(rng.standard_normal((Sq, B, H, D)))
+    kb = bf16_bits(rng.standard_normal((Sk, B, G, D)))
+    idx_scores = rng.standard_normal((B, Sq, Sk)).astype(np.float32)
+    # reference-test style: K distinct columns drawn from all of [0, Sk) (rows
+    # with no column <= t exist), and a causal set with one column <= t per row
+    topk_any = np.stack([rng.permutation(Sk)[:K] for _ in range(B * Sq)]).reshape(B, Sq, K).astype(np.int64)
+    topk_causal = topk_any.copy()
+    for b in range(B):
+        for t in range(Sq):
+            if not any(0 <= j <= t for j in topk_causal[b, t]):
+                topk_causal[b, t, 0] = rng.integers(0, t + 1)
+                if len(set(topk_causal[b, t].tolist())) < K:  # keep the set distinct
+                    free = [j for j in range(Sk) if j not in set(topk_causal[b, t].tolist())]
+                    topk_causal[b, t, 1:] = np.array(free[:K - 1])
+    scale = 1.0 / math.sqrt(D)
+    q, k = bf16_value(qb), bf16_value(kb)
+    sc = idx_scores.astype(np.float64)
+    dense = indexer_loss_rows_expected(sc, topk_any, q, k, scale, False)
+    sparse_any = indexer_loss_rows_expected(sc, topk_any, q, k, scale, True)
+    sparse_causal = indexer_loss_rows_expected(sc, topk_causal, q, k, scale, True)
+    np.savez_compressed(os.path.join(HERE, name), q_bits=qb, k_bits=kb, index_scores=idx_scores,
+                        topk_any=topk_any, topk_causal=topk_causal, scale=np.float64(scale),
+                        rows_dense=dense, rows_sparse_any=sparse_any, rows_sparse_causal=sparse_causal)
+    print(f"wrote {name}")
+
+
+FIXTURES = {
+    "indexer_loss": lambda: (
+        make_indexer_loss("indexer_loss_h4.npz", 16, B=1, Sq=24, Sk=24, H=4, G=4, D=64, K=8),
+        make_indexer_loss("indexer_loss_g2.npz", 17, B=2, Sq=20, Sk=28, H=8, G=2, D=32, K=6)),
+}
+
+
 def main():
+    import sys
+    if len(sys.argv) > 1:  # regenerate only the named fixture families
+        for name in sys.argv[1:]:
+            FIXTURES[name]()
+        return
     make_sparse_mla("sparse_mla_d128.npz", 11, B=1, S=16, Skv=16, H=16, G=1, D=128, d_v=64, K=16)
     make_sparse_mla("sparse_mla_d64_g2.npz", 12, B=2, S=8, Skv=20, H=32, G=2, D=64, d_v=32, K=40)
     make_indexer("indexer.npz", 13, Sq=20, Sk=28, B=2, H=16, D=64)
     make_topk("topk.npz", 14, rows=40, n=300, k=32)
     make_fp8("fp8.npz", 15, n=4096)
+    for make in FIXTURES.values():
+        make()
 
 
 if __name__ == "__main__":
