@@ -21,13 +21,18 @@ h=128, d_qk=576, d_v=512, topk=2048; e4m3 indexer at h=64, d=128; top-2048
 over s=16384) are timed on device-generated inputs and reported under "cfg5"
 (not part of `value`).
 
+The DSA indexer KL loss (compute_dsa_indexer_loss_splitk at the NAM56R
+attention shape: query/key [4096, 2, 32, 128] bf16, index scores [2, 4096,
+4096] causal, top-256) is timed dense and sparse and reported under
+"indexer_kl_loss" (not part of `value`; --no-kl skips it).
+
 `value` and `ms_per_step` come from replays of the layer step captured in a
 HIP graph (launch gaps removed; every replay runs all 13 kernels, and three
 replays are first checked bit for bit against the eager step); the per-kernel
 breakdown and `eager_tokens_per_s` come from the eager timed steps before it.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
-                       [--no-cfg5] [--no-graph] [--calib-copy-mib N]   (one N MiB
+                       [--no-cfg5] [--no-kl] [--no-graph] [--calib-copy-mib N]   (one N MiB
                        device copy before timing, the calibration kernel of PMC runs)
 """
 from __future__ import annotations
@@ -136,6 +141,49 @@ def measure_cfg5(dev, reps=3):
             e.update({"bound": "hbm", "gbs": round(gbs, 1), "peak": PEAK_HBM_GBS, "frac": round(gbs / PEAK_HBM_GBS, 4)})
         res[k] = e
     del q, kv, idx, iq8, ik8, iw, scores
+    torch.cuda.empty_cache()
+    return res
+
+
+# DSA indexer KL loss at the NAM56R attention shape, reported beside the headline
+KL_HEADS, KL_HN = 32, 128
+
+
+def measure_indexer_kl(dev, reps=5):
+    """Median time of the KL indexer loss (dense and sparse top-256) on
+    device-generated inputs: query/key [S, B, 32, 128] bf16 ~ N(0, 0.5), index
+    scores [B, S, S] ~ N(0, 1) with -inf above the diagonal, top-256 of them.
+    Algorithmic work: two q.k passes over the causal pairs of every head."""
+    import torch
+
+    from cppmega_amd.dsa_splitk_indexer_loss import indexer_kl_loss
+    from oracle.indexer_loss import kl_flops
+
+    gen = torch.Generator(device=dev).manual_seed(9)
+    q = (torch.randn((S, B, KL_HEADS, KL_HN), generator=gen, device=dev) * 0.5).to(torch.bfloat16)
+    k = (torch.randn((S, B, KL_HEADS, KL_HN), generator=gen, device=dev) * 0.5).to(torch.bfloat16)
+    sc = torch.randn((B, S, S), generator=gen, device=dev)
+    sc.masked_fill_(torch.ones(S, S, dtype=torch.bool, device=dev).triu(1), float("-inf"))
+    tk = sc.topk(TOPK, dim=-1).indices
+    scale = KL_HN ** -0.5
+    fl = kl_flops(B, S, S, KL_HEADS, KL_HN)
+    res = {}
+    for mode, sparse in (("dense", False), ("sparse", True)):
+        indexer_kl_loss(sc, tk, q, k, scale, 1.0, sparse)
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            a, b_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            indexer_kl_loss(sc, tk, q, k, scale, 1.0, sparse)
+            b_.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b_) / 1e3)
+        t = sorted(ts)[len(ts) // 2]
+        tf = fl / t / 1e12
+        res[mode] = {"ms": round(t * 1e3, 3), "bound": "mfma", "tflops": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
+                     "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
+    del q, k, sc, tk
     torch.cuda.empty_cache()
     return res
 
@@ -266,6 +314,7 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=4096)
     ap.add_argument("--calib-copy-mib", type=int, default=0)
     ap.add_argument("--no-cfg5", action="store_true", help="skip the cfg5 (long-context) kernel timings")
+    ap.add_argument("--no-kl", action="store_true", help="skip the indexer KL loss timings")
     ap.add_argument("--no-graph", action="store_true",
                     help="time eager launches only (default: the step is also captured in a HIP graph)")
     args = ap.parse_args()
@@ -370,6 +419,7 @@ def main():
     amortised = 9 * tokens / ((3 * t_idx + 9 * t_att) / 1e3)
 
     cfg5 = None if args.no_cfg5 else measure_cfg5(dev)
+    kl = None if args.no_kl else measure_indexer_kl(dev)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -406,6 +456,9 @@ def main():
         "cfg5": ({"workload": f"s={C5_S} h={C5_H} d_qk={C5_DQK} d_v={C5_DV} topk={C5_TOPK} SparseMLA fwd (bf16), "
                               f"indexer h={C5_HIDX} d={C5_DIDX} e4m3 causal, top-{C5_TOPK}",
                   "kernels": cfg5} if cfg5 is not None else None),
+        "indexer_kl_loss": ({"workload": f"compute_dsa_indexer_loss_splitk: query/key [{S},{B},{KL_HEADS},{KL_HN}] "
+                                         f"bf16, index scores [{B},{S},{S}] causal, top-{TOPK}",
+                             "kernels": kl} if kl is not None else None),
     }
     print(json.dumps(line), flush=True)
 

@@ -19,11 +19,11 @@
 //     gamma = max + log2(sum exp2(x - max)) of x = index_scores * log2(e) over
 //     the row (sparse: over the row's top-k set, built as a bitmask in LDS and
 //     written out for the other kernels);
-//  2. kl_attn_stats_kernel   per (b, head, pair of 128-token blocks): the log2
+//  2. kl_attn_stats_kernel   per (b, head, pair of 256-token blocks): the log2
 //     normaliser beta_h[t] of c * q.k (c = scale * log2(e)) over s <= t, on
 //     MFMA 32x32x16 bf16 with S^T = K . Q^T (keys on M, tokens on N, so a lane
 //     holds 16 keys of one token and row reductions stay in-lane); key chunks
-//     are double-buffered in LDS and shared by the 4 waves; a long and a short
+//     are double-buffered in LDS and shared by the 8 waves; a long and a short
 //     token block share one workgroup so every workgroup does equal work;
 //  3. kl_pass_kernel         per (b, 128-token block, key chunk): for every head
 //     recompute c * q.k, accumulate exp2(c * q.k - beta_h) in registers (the
@@ -39,22 +39,23 @@
 namespace dsa {
 namespace kl {
 
-constexpr int kTB = 128;      // tokens per workgroup (4 waves x 32 tokens)
-constexpr int kNT = 256;      // threads per workgroup
+constexpr int kNT = 256;      // threads per workgroup of the small kernels
 constexpr int kMaxW = 1024;   // mask words per row in LDS (sparse: Sk <= 32768)
 constexpr float kLn2 = 0.69314718055994531f;
 constexpr float kEps = 1e-10f;
 
-template <int D>
+template <int D, int NW>
 struct Cfg {
+  static constexpr int NT = 64 * NW;               // threads per workgroup
+  static constexpr int TB = 32 * NW;               // tokens per workgroup (32 per wave)
   static constexpr int KC = D <= 128 ? 128 : 64;   // keys per LDS chunk
   static constexpr int ROWB = D * 2;               // bytes per bf16 key row
   static constexpr int STRIDE = ROWB + 16;         // LDS row pitch (bank spread)
   static constexpr int SUBS = KC / 32;             // 32-key sub-tiles per chunk
   static constexpr int KSTEPS = D / 16;            // MFMA k-steps per q.k
   static constexpr int CPR = ROWB / 16;            // 16-byte pieces per key row
-  static constexpr int LOADS = KC * CPR / kNT;     // 16-byte loads per thread per chunk
-  static_assert(D % 32 == 0 && D <= 256 && KC * CPR % kNT == 0, "head dim");
+  static constexpr int LOADS = KC * CPR / NT;      // 16-byte loads per thread per chunk
+  static_assert(D % 32 == 0 && D <= 256 && KC * CPR % NT == 0, "head dim");
 };
 
 struct Params {
@@ -69,6 +70,7 @@ struct Params {
   float *rows;                    // [B, Sq]      per-position KL
   float *loss;                    // [1]
   int64_t B, Sq, Sk, H, G, K, W, NC;
+  int64_t NI;                     // KL work items per batch (block, chunk pairs)
   int topk_i64;
   int sparse;
   float c;                        // softmax_scale * log2(e)
@@ -150,12 +152,12 @@ __global__ void __launch_bounds__(kNT) kl_index_stats_kernel(Params p) {
 // elements 16k + 8g .. +8 of the row at k-step k (zero past Sq).
 template <int D>
 __device__ __forceinline__ void load_q_operand(const Params &p, int64_t b, int64_t h, int64_t t,
-                                               bf16x8 (&Q)[Cfg<D>::KSTEPS]) {
+                                               bf16x8 (&Q)[Cfg<D, 4>::KSTEPS]) {
   const int g = lane_id() >> 5;
   const bool ok = t < p.Sq;
   const unsigned char *row = p.query + (((ok ? t : 0) * p.B + b) * p.H + h) * (int64_t)(D * 2);
 #pragma unroll
-  for (int k = 0; k < Cfg<D>::KSTEPS; ++k) {
+  for (int k = 0; k < Cfg<D, 4>::KSTEPS; ++k) {
     i32x4 v = {0, 0, 0, 0};
     if (ok) v = ld_global_16(row + (16 * k + 8 * g) * 2);
     Q[k] = as_bf16x8(v);
@@ -164,16 +166,16 @@ __device__ __forceinline__ void load_q_operand(const Params &p, int64_t b, int64
 
 // Cooperative loads of key chunk [k0, k0 + KC) of (b, group grp) into
 // registers; rows at or past Sk read zeros (bounded buffer resource).
-template <int D>
+template <int D, int NW>
 struct ChunkLoader {
-  using C = Cfg<D>;
+  using C = Cfg<D, NW>;
   uint32_t off[C::LOADS];
   uint32_t pitch;
   __device__ ChunkLoader(const Params &p) {
     pitch = (uint32_t)(p.B * p.G * C::ROWB);
 #pragma unroll
     for (int l = 0; l < C::LOADS; ++l) {
-      const int u = threadIdx.x + kNT * l;
+      const int u = threadIdx.x + C::NT * l;
       off[l] = (uint32_t)(u / C::CPR) * pitch + (uint32_t)(u % C::CPR) * 16u;
     }
   }
@@ -189,7 +191,7 @@ struct ChunkLoader {
   __device__ static void store(unsigned char *ks, const i32x4 (&r)[C::LOADS]) {
 #pragma unroll
     for (int l = 0; l < C::LOADS; ++l) {
-      const int u = threadIdx.x + kNT * l;
+      const int u = threadIdx.x + C::NT * l;
       *reinterpret_cast<i32x4 *>(ks + (u / C::CPR) * C::STRIDE + (u % C::CPR) * 16) = r[l];
     }
   }
@@ -198,8 +200,8 @@ struct ChunkLoader {
 // S^T of sub-tile `sub` (32 keys) of the LDS chunk against the wave's 32
 // tokens: acc[4i + j] = q(token lane & 31) . k(key 32 sub + 8i + 4g + j).
 template <int D>
-__device__ __forceinline__ f32x16 qk_subtile(const unsigned char *ks, int sub, const bf16x8 (&Q)[Cfg<D>::KSTEPS]) {
-  using C = Cfg<D>;
+__device__ __forceinline__ f32x16 qk_subtile(const unsigned char *ks, int sub, const bf16x8 (&Q)[Cfg<D, 4>::KSTEPS]) {
+  using C = Cfg<D, 4>;
   const int lane = lane_id();
   const unsigned char *arow = ks + (sub * 32 + (lane & 31)) * C::STRIDE + (lane >> 5) * 16;
   f32x16 acc;
@@ -213,36 +215,54 @@ __device__ __forceinline__ f32x16 qk_subtile(const unsigned char *ks, int sub, c
   return acc;
 }
 
+// Top-k bitmask word of token t covering keys [key0, key0 + 32) (key0 a
+// multiple of 32); all ones in dense mode.
+__device__ __forceinline__ uint32_t mask_word(const Params &p, int64_t b, int64_t t, int64_t key0) {
+  if (!p.sparse) return 0xffffffffu;
+  return t < p.Sq ? p.mask[(b * p.Sq + t) * p.W + (key0 >> 5)] : 0u;
+}
+
 // Admissible-column bits of accumulator register a = 4i + j (key
-// key0 + 8i + 4g + j) for token t: s <= t, s < Sk and, sparse, in the top-k set.
-__device__ __forceinline__ uint32_t valid_bits(const Params &p, int64_t b, int64_t t, int64_t key0) {
+// key0 + 8i + 4g + j) for token t: s <= t, s < Sk, t < Sq and, sparse, in the
+// top-k set (bit of `word`).  Word-level: clear the bits past the last
+// admissible key, then gather the lane half's four 4-bit groups.
+__device__ __forceinline__ uint32_t valid_bits(const Params &p, uint32_t word, int64_t t, int64_t key0) {
   const int g = lane_id() >> 5;
-  uint32_t word = 0xffffffffu;
-  if (p.sparse) word = t < p.Sq ? p.mask[(b * p.Sq + t) * p.W + (key0 >> 5)] : 0u;
-  uint32_t v = 0u;
-#pragma unroll
-  for (int a = 0; a < 16; ++a) {
-    const int m = 8 * (a >> 2) + 4 * g + (a & 3);
-    const int64_t s = key0 + m;
-    const bool ok = ((word >> m) & 1u) && s <= t && s < p.Sk && t < p.Sq;
-    v |= (ok ? 1u : 0u) << a;
-  }
-  return v;
+  const int64_t last = (t < p.Sk - 1 ? t : p.Sk - 1) - key0;  // last admissible m
+  const uint32_t keep = t >= p.Sq || last < 0 ? 0u : (last >= 31 ? 0xffffffffu : (2u << last) - 1u);
+  const uint32_t w = (word & keep) >> (4 * g);
+  return (w & 0xfu) | ((w >> 4) & 0xf0u) | ((w >> 8) & 0xf00u) | ((w >> 12) & 0xf000u);
+}
+
+// acc if bit a of vb is set, -inf otherwise (sign-extended bit field as a
+// select mask: one bfe + one bfi).
+__device__ __forceinline__ float keep_or_neginf(float acc, uint32_t vb, int a) {
+  const uint32_t m = (uint32_t)(((int32_t)(vb << (31 - a))) >> 31);
+  return __uint_as_float((m & __float_as_uint(acc)) | (~m & 0xff800000u));
+}
+
+// Chunks of KC keys that token block blk (TB tokens) needs: keys up to
+// min(last token of the block, Sk - 1).
+__device__ __forceinline__ int64_t block_chunks(const Params &p, int64_t blk, int64_t TB, int64_t KC) {
+  const int64_t lt = (TB * (blk + 1) < p.Sq ? TB * (blk + 1) : p.Sq) - 1;
+  return (lt < p.Sk - 1 ? lt : p.Sk - 1) / KC + 1;
 }
 
 // ---------------------------------------------------------------------------
 // 2. attention normalisers beta_h[t] (log2 units of c * q.k)
 // ---------------------------------------------------------------------------
-template <int D>
-__global__ void __launch_bounds__(kNT) kl_attn_stats_kernel(Params p) {
-  using C = Cfg<D>;
+template <int D, int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 8 ? 4 : 2)))
+kl_attn_stats_kernel(Params p) {
+  using C = Cfg<D, NW>;
+  constexpr int kTB = C::TB;
   __shared__ __attribute__((aligned(16))) unsigned char KS[2][C::KC * C::STRIDE];
   const int w = wave_id(), lane = lane_id(), g = lane >> 5;
   const int64_t NB = (p.Sq + kTB - 1) / kTB, NP = (NB + 1) / 2;
   const int64_t bid = xcd_remap(blockIdx.x, gridDim.x);
   const int64_t pair = bid % NP, bh = bid / NP, h = bh % p.H, b = bh / p.H;
   const int64_t grp = h / (p.H / p.G);
-  ChunkLoader<D> ld(p);
+  ChunkLoader<D, NW> ld(p);
 
   for (int half = 0; half < 2; ++half) {
     const int64_t blk = half == 0 ? NB - 1 - pair : pair;  // the long block first
@@ -257,10 +277,18 @@ __global__ void __launch_bounds__(kNT) kl_attn_stats_kernel(Params p) {
     i32x4 kr[C::LOADS];
     __syncthreads();  // the previous block's waves are done with the LDS chunks
     ld.load(p, b, grp, 0, kr);
-    ChunkLoader<D>::store(KS[0], kr);
+    ChunkLoader<D, NW>::store(KS[0], kr);
     __syncthreads();
+    // sparse: the chunk's top-k mask words are loaded one chunk ahead
+    uint32_t mw[C::SUBS];
+#pragma unroll
+    for (int sub = 0; sub < C::SUBS; ++sub) mw[sub] = mask_word(p, b, t, 32 * sub);
     for (int ci = 0; ci < nch; ++ci) {
       if (ci + 1 < nch) ld.load(p, b, grp, (int64_t)(ci + 1) * C::KC, kr);
+      uint32_t mwn[C::SUBS];
+#pragma unroll
+      for (int sub = 0; sub < C::SUBS; ++sub)
+        mwn[sub] = ci + 1 < nch ? mask_word(p, b, t, (int64_t)(ci + 1) * C::KC + 32 * sub) : 0u;
       const unsigned char *ks = KS[ci & 1];
 #pragma unroll
       for (int sub = 0; sub < C::SUBS; ++sub) {
@@ -268,27 +296,30 @@ __global__ void __launch_bounds__(kNT) kl_attn_stats_kernel(Params p) {
         if (key0 > wt_last || key0 >= p.Sk) continue;  // wave-uniform: wholly above the diagonal
         const f32x16 acc = qk_subtile<D>(ks, sub, Q);
         const bool need_mask = p.sparse || key0 + 31 > wt0 || key0 + 31 >= p.Sk || wt_last >= p.Sq;
+        // c > 0: max(c * acc) = c * max(acc), and exp2(c * acc - nm) is one fma
         float x[16];
         if (need_mask) {
-          const uint32_t vb = valid_bits(p, b, t, key0);
+          const uint32_t vb = valid_bits(p, mw[sub], t, key0);
 #pragma unroll
-          for (int a = 0; a < 16; ++a) x[a] = ((vb >> a) & 1u) ? acc[a] * p.c : -INFINITY;
+          for (int a = 0; a < 16; ++a) x[a] = keep_or_neginf(acc[a], vb, a);
         } else {
 #pragma unroll
-          for (int a = 0; a < 16; ++a) x[a] = acc[a] * p.c;
+          for (int a = 0; a < 16; ++a) x[a] = acc[a];
         }
         float lm = x[0];
 #pragma unroll
         for (int a = 1; a < 16; ++a) lm = fmaxf(lm, x[a]);
-        const float nm = fmaxf(m, lm);
+        const float nm = fmaxf(m, lm * p.c);
         float s = 0.0f;
 #pragma unroll
-        for (int a = 0; a < 16; ++a) s += exp2_fast(x[a] - nm);
+        for (int a = 0; a < 16; ++a) s += exp2_fast(fmaf(x[a], p.c, -nm));
         d = d * exp2_fast(m - nm) + s;
         m = nm;
       }
+#pragma unroll
+      for (int sub = 0; sub < C::SUBS; ++sub) mw[sub] = mwn[sub];
       if (ci + 1 < nch) {
-        ChunkLoader<D>::store(KS[(ci + 1) & 1], kr);
+        ChunkLoader<D, NW>::store(KS[(ci + 1) & 1], kr);
         __syncthreads();
       }
     }
@@ -303,20 +334,42 @@ __global__ void __launch_bounds__(kNT) kl_attn_stats_kernel(Params p) {
 // ---------------------------------------------------------------------------
 // 3. KL partial sums per (token, key chunk)
 // ---------------------------------------------------------------------------
-template <int D>
-__global__ void __launch_bounds__(kNT) kl_pass_kernel(Params p) {
-  using C = Cfg<D>;
+template <int D, int NW>
+__global__ void __launch_bounds__(64 * NW) kl_pass_kernel(Params p) {
+  using C = Cfg<D, NW>;
+  constexpr int kTB = C::TB;
   __shared__ __attribute__((aligned(16))) unsigned char KS[2][C::KC * C::STRIDE];
   const int w = wave_id(), lane = lane_id(), g = lane >> 5;
+  // Work items are the (b, block, chunk) pairs at or below the diagonal:
+  // first every block's full chunks, block-major, then the cheaper diagonal
+  // chunks (one per block), so a last partial round of the grid is short
+  // work.  The grid is padded to a multiple of 8 so that each XCD takes one
+  // contiguous, equal share (consecutive items share a token block's q rows
+  // in that XCD's L2).
   const int64_t NB = (p.Sq + kTB - 1) / kTB;
   const int64_t bid = xcd_remap(blockIdx.x, gridDim.x);
-  const int64_t blk = bid % NB, bc = bid / NB, ci = bc % p.NC, b = bc / p.NC;
+  if (bid >= p.B * p.NI) return;
+  const int64_t nfull = p.NI - NB;  // items per batch before the diagonal ones
+  int64_t b, blk = 0, ci;
+  if (bid < p.B * nfull) {
+    b = bid / nfull;
+    int64_t rem = bid % nfull;
+    for (;; ++blk) {  // scalar walk over the blocks' full-chunk counts (NB steps at most)
+      const int64_t n = block_chunks(p, blk, kTB, C::KC) - 1;
+      if (rem < n) break;
+      rem -= n;
+    }
+    ci = rem;
+  } else {
+    const int64_t r = bid - p.B * nfull;
+    b = r / NB;
+    blk = r % NB;
+    ci = block_chunks(p, blk, kTB, C::KC) - 1;
+  }
   const int64_t t0 = blk * kTB, k0 = ci * C::KC;
-  const int64_t t_blk_last = (t0 + kTB < p.Sq ? t0 + kTB : p.Sq) - 1;
-  if (k0 > t_blk_last || k0 >= p.Sk) return;  // chunk wholly above the block's diagonal
   const int64_t wt0 = t0 + 32 * w, t = wt0 + (lane & 31), wt_last = wt0 + 31;
   const int64_t hpg = p.H / p.G;
-  ChunkLoader<D> ld(p);
+  ChunkLoader<D, NW> ld(p);
 
   // admissible bits of this lane's 16 keys per sub-tile (same for every head)
   uint32_t vb[C::SUBS];
@@ -325,7 +378,7 @@ __global__ void __launch_bounds__(kNT) kl_pass_kernel(Params p) {
   for (int sub = 0; sub < C::SUBS; ++sub) {
     const int64_t key0 = k0 + 32 * sub;
     sub_on[sub] = key0 <= wt_last && key0 < p.Sk && wt0 < p.Sq;  // wave-uniform
-    vb[sub] = sub_on[sub] ? valid_bits(p, b, t, key0) : 0u;
+    vb[sub] = sub_on[sub] ? valid_bits(p, mask_word(p, b, t, key0), t, key0) : 0u;
   }
 
   float P[C::SUBS][16];
@@ -336,7 +389,7 @@ __global__ void __launch_bounds__(kNT) kl_pass_kernel(Params p) {
 
   i32x4 kr[C::LOADS];
   ld.load(p, b, 0, k0, kr);
-  ChunkLoader<D>::store(KS[0], kr);
+  ChunkLoader<D, NW>::store(KS[0], kr);
   __syncthreads();
   // the next head's q operand and normaliser are loaded one head ahead
   const float *beta_bt = p.beta + b * p.H * p.Sq + (t < p.Sq ? t : 0);
@@ -365,7 +418,7 @@ __global__ void __launch_bounds__(kNT) kl_pass_kernel(Params p) {
     }
     if (last_of_grp && grp + 1 < p.G) {
       // the other buffer was last read for group grp - 1, before the previous barrier
-      ChunkLoader<D>::store(KS[(grp + 1) & 1], kr);
+      ChunkLoader<D, NW>::store(KS[(grp + 1) & 1], kr);
       __syncthreads();
     }
   }
@@ -422,7 +475,7 @@ __global__ void __launch_bounds__(kNT) kl_rows_kernel(Params p) {
   if (row >= p.B * p.Sq) return;
   const int64_t b = row / p.Sq, t = row % p.Sq;
   const int64_t last_k = t < p.Sk - 1 ? t : p.Sk - 1;
-  const int64_t cmax = last_k / Cfg<D>::KC;
+  const int64_t cmax = last_k / Cfg<D, 4>::KC;
   float s = 0.0f;
   for (int64_t c = 0; c <= cmax; ++c) s += p.partial[(b * p.NC + c) * p.Sq + t];
   const bool no_target = !(p.beta[b * p.H * p.Sq + t] > -INFINITY);
@@ -468,13 +521,23 @@ static Layout layout(int64_t B, int64_t Sq, int64_t Sk, int64_t H, int64_t D, in
   return L;
 }
 
-template <int D>
+template <int D, int NWS, int NWP>
 static int launch_mfma(const Params &p, hipStream_t st) {
-  const int64_t NB = (p.Sq + kTB - 1) / kTB, NP = (NB + 1) / 2;
-  hipLaunchKernelGGL(kl_attn_stats_kernel<D>, dim3((unsigned)(p.B * p.H * NP)), dim3(kNT), 0, st, p);
+  using CS = Cfg<D, NWS>;
+  using CP = Cfg<D, NWP>;
+  const int64_t NBS = (p.Sq + CS::TB - 1) / CS::TB, NP = (NBS + 1) / 2;
+  hipLaunchKernelGGL((kl_attn_stats_kernel<D, NWS>), dim3((unsigned)(p.B * p.H * NP)), dim3(CS::NT), 0, st, p);
   int rc = check_launch("kl_attn_stats_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(kl_pass_kernel<D>, dim3((unsigned)(p.B * p.NC * NB)), dim3(kNT), 0, st, p);
+  const int64_t NBP = (p.Sq + CP::TB - 1) / CP::TB;
+  Params q = p;
+  q.NI = 0;
+  for (int64_t j = 0; j < NBP; ++j) {
+    const int64_t lt = (CP::TB * (j + 1) < p.Sq ? CP::TB * (j + 1) : p.Sq) - 1;
+    q.NI += (lt < p.Sk - 1 ? lt : p.Sk - 1) / CP::KC + 1;
+  }
+  const int64_t items = (p.B * q.NI + 7) / 8 * 8;
+  hipLaunchKernelGGL((kl_pass_kernel<D, NWP>), dim3((unsigned)items), dim3(CP::NT), 0, st, q);
   rc = check_launch("kl_pass_kernel");
   if (rc) return rc;
   hipLaunchKernelGGL(kl_rows_kernel<D>, dim3((unsigned)((p.B * p.Sq + kNT - 1) / kNT)), dim3(kNT), 0, st, p);
@@ -502,6 +565,8 @@ extern "C" int dsa_indexer_kl_loss(const float *index_scores, const void *topk_i
               (long long)B, (long long)Sq, (long long)Sk, (long long)H, (long long)G);
   DSA_REQUIRE(H % G == 0, "dsa_indexer_kl_loss: H=%lld is not a multiple of the key heads G=%lld", (long long)H,
               (long long)G);
+  DSA_REQUIRE(softmax_scale > 0.0f && softmax_scale < INFINITY, "dsa_indexer_kl_loss: softmax_scale %g must be positive",
+              (double)softmax_scale);
   DSA_REQUIRE(D == 64 || D == 128 || D == 192 || D == 256, "dsa_indexer_kl_loss: head dim %lld not in {64,128,192,256}",
               (long long)D);
   DSA_REQUIRE(B * Sq * Sk < ((int64_t)1 << 29), "dsa_indexer_kl_loss: B*Sq*Sk=%lld index scores exceed 2 GiB",
@@ -543,10 +608,10 @@ extern "C" int dsa_indexer_kl_loss(const float *index_scores, const void *topk_i
   int rc = check_launch("kl_index_stats_kernel");
   if (rc) return rc;
   switch (D) {
-    case 64: rc = launch_mfma<64>(p, st); break;
-    case 128: rc = launch_mfma<128>(p, st); break;
-    case 192: rc = launch_mfma<192>(p, st); break;
-    default: rc = launch_mfma<256>(p, st); break;
+    case 64: rc = launch_mfma<64, 8, 4>(p, st); break;
+    case 128: rc = launch_mfma<128, 8, 4>(p, st); break;
+    case 192: rc = launch_mfma<192, 8, 4>(p, st); break;
+    default: rc = launch_mfma<256, 8, 4>(p, st); break;
   }
   if (rc) return rc;
   hipLaunchKernelGGL(kl_mean_kernel, dim3(1), dim3(1024), 0, st, p);

@@ -195,7 +195,7 @@ int dsa_fp8_tensorwise_quantize(const void *x, int64_t n, int in_dtype,
  * whose index softmax is undefined (all -inf, any NaN or +inf) gets a NaN row
  * loss, as the reference's softmax does, and the mean is then NaN.
  * Deterministic: fixed summation orders, no global atomics.
- * Limits: B * Sq * Sk < 2^29; sparse mode Sk <= 32768.
+ * Limits: softmax_scale > 0, B * Sq * Sk < 2^29; sparse mode Sk <= 32768.
  */
 size_t dsa_indexer_kl_loss_workspace_size(int64_t B, int64_t Sq, int64_t Sk,
                                           int64_t H, int64_t D, int sparse);
