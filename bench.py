@@ -156,6 +156,7 @@ def measure_indexer_kl(dev, reps=5):
     Algorithmic work: two q.k passes over the causal pairs of every head."""
     import torch
 
+    from cppmega_amd.dsa_index_mask import topk_index_mask
     from cppmega_amd.dsa_splitk_indexer_loss import indexer_kl_loss
     from oracle.indexer_loss import kl_flops
 
@@ -168,22 +169,33 @@ def measure_indexer_kl(dev, reps=5):
     scale = KL_HN ** -0.5
     fl = kl_flops(B, S, S, KL_HEADS, KL_HN)
     res = {}
-    for mode, sparse in (("dense", False), ("sparse", True)):
-        indexer_kl_loss(sc, tk, q, k, scale, 1.0, sparse)
+
+    def med_time(fn):
+        fn()
         torch.cuda.synchronize()
         ts = []
         for _ in range(reps):
             a, b_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
-            indexer_kl_loss(sc, tk, q, k, scale, 1.0, sparse)
+            fn()
             b_.record()
             torch.cuda.synchronize()
             ts.append(a.elapsed_time(b_) / 1e3)
-        t = sorted(ts)[len(ts) // 2]
+        return sorted(ts)[len(ts) // 2]
+
+    for mode, sparse in (("dense", False), ("sparse", True)):
+        t = med_time(lambda: indexer_kl_loss(sc, tk, q, k, scale, 1.0, sparse))
         tf = fl / t / 1e12
         res[mode] = {"ms": round(t * 1e3, 3), "bound": "mfma", "tflops": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
                      "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
-    del q, k, sc, tk
+    # the sparse loss's dense [b, s, s] top-k mask, built in one pass (HBM: the
+    # f32 mask written once, the int64 indices read once)
+    mask = torch.empty((B, S, S), dtype=torch.float32, device=dev)
+    t = med_time(lambda: topk_index_mask(tk, S, out=mask))
+    gbs = (B * S * S * 4 + tk.numel() * 8) / t / 1e9
+    res["index_mask"] = {"ms": round(t * 1e3, 4), "bound": "hbm", "gbs": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                         "frac": round(gbs / PEAK_HBM_GBS, 4)}
+    del q, k, sc, tk, mask
     torch.cuda.empty_cache()
     return res
 
@@ -457,7 +469,8 @@ def main():
                               f"indexer h={C5_HIDX} d={C5_DIDX} e4m3 causal, top-{C5_TOPK}",
                   "kernels": cfg5} if cfg5 is not None else None),
         "indexer_kl_loss": ({"workload": f"compute_dsa_indexer_loss_splitk: query/key [{S},{B},{KL_HEADS},{KL_HN}] "
-                                         f"bf16, index scores [{B},{S},{S}] causal, top-{TOPK}",
+                                         f"bf16, index scores [{B},{S},{S}] causal, top-{TOPK}; index_mask: "
+                                         f"topk_index_mask of the top-{TOPK} into [{B},{S},{S}] f32",
                              "kernels": kl} if kl is not None else None),
     }
     print(json.dumps(line), flush=True)

@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "dsa_fp8_tensorwise_quantize",
     "dsa_indexer_kl_loss_workspace_size",
     "dsa_indexer_kl_loss",
+    "dsa_topk_index_mask",
     "dsa_stage_timing",
     "dsa_stage_times",
 )
@@ -76,6 +77,8 @@ _SIGNATURES = {
     "dsa_indexer_kl_loss": (_i32, [_c_void_p, _c_void_p, _i32, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                    _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _i32,
                                    _c_void_p, _size_t, _c_void_p]),
+    "dsa_topk_index_mask": (_i32, [_c_void_p, _i32, _i64, _c_void_p, _i64, _i64, _i64, _i64, _i64,
+                                   _f32, _f32, _i32, _c_void_p]),
     "dsa_stage_timing": (_i32, [_i32]),
     "dsa_stage_times": (_i32, [_i32, ctypes.POINTER(ctypes.c_float), _i32]),
 }

@@ -208,6 +208,27 @@ int dsa_indexer_kl_loss(const float *index_scores, const void *topk_indices,
                         size_t workspace_bytes, void *stream);
 
 /*
+ * Top-k index mask of the sparse indexer loss.
+ * Replaces Megatron's _scatter_topk_into_index_mask in the CUDA-graph-safe form
+ *   cppmega patches in (cppmega/megatron/upstream_patches/apply_dsa_cg_patches.py:267-291;
+ *   eager oracle upstream_prs/examples/01_dsa_cuda_graph_safety/reproducer.py:124-138).
+ *
+ *   topk_indices [B, rows, topk] int32 / int64 (topk_dtype): the top-k columns
+ *                of mask rows [row0, row0 + rows); values outside [0, Sk) (the
+ *                -1 sentinel) are skipped, duplicates are harmless
+ *   mask [B, Sq, Sk] f32
+ * fill_rows == 0: mask[b, row0 + r, s] = value for every listed s; nothing
+ *                 else is written (the reference's in-place scatter).
+ * fill_rows != 0: every element of rows [row0, row0 + rows) is written:
+ *                 value on listed columns, fill elsewhere (Sk <= 262144).
+ * One launch, no host synchronisation, idempotent: safe under graph capture.
+ */
+int dsa_topk_index_mask(const void *topk_indices, int topk_dtype, int64_t topk,
+                        float *mask, int64_t B, int64_t Sq, int64_t Sk,
+                        int64_t row0, int64_t rows, float value, float fill,
+                        int fill_rows, void *stream);
+
+/*
  * Stage timing (measurement aid; no counterpart in the reference, which
  * times whole calls with CUDA events in its benchmark scripts).  With
  * dsa_stage_timing(1) on a thread, every later dsa_sparse_mla_bwd call on

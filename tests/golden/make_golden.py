@@ -301,10 +301,36 @@ def make_indexer_loss(name, seed, B, Sq, Sk, H, G, D, K):
     print(f"wrote {name}")
 
 
+# ---------------------------------------------------------------------------
+# Top-k index mask
+# ---------------------------------------------------------------------------
+def make_index_mask(name, seed, b, s_q, s_kv, topk, s0, s1):
+    """The reference reproducer's fixture shape (b=2, s_q=64, s_kv=256, topk=8,
+    ~15% -1 sentinels), plus out-of-range columns; expected mask by loops."""
+    rng = np.random.default_rng(seed)
+    idx = rng.integers(0, s_kv, size=(b, s1 - s0, topk)).astype(np.int64)
+    idx[rng.random(idx.shape) < 0.15] = -1
+    idx[0, 0, :] = -1                      # a row of sentinels only
+    idx[1, 1, 0] = s_kv + 3                # past the row: skipped
+    idx[1, 2, :2] = 0                      # a real column 0 next to sentinels
+    idx[1, 2, 2] = -1
+    mask = np.full((b, s_q, s_kv), -np.inf, dtype=np.float32)
+    for bb in range(b):
+        for r in range(s1 - s0):
+            for j in range(topk):
+                c = int(idx[bb, r, j])
+                if 0 <= c < s_kv:
+                    mask[bb, s0 + r, c] = 0.0
+    np.savez_compressed(os.path.join(HERE, name), idx=idx, s0=np.int64(s0), s1=np.int64(s1),
+                        s_kv=np.int64(s_kv), mask=mask)
+    print(f"wrote {name}")
+
+
 FIXTURES = {
     "indexer_loss": lambda: (
         make_indexer_loss("indexer_loss_h4.npz", 16, B=1, Sq=24, Sk=24, H=4, G=4, D=64, K=8),
         make_indexer_loss("indexer_loss_g2.npz", 17, B=2, Sq=20, Sk=28, H=8, G=2, D=32, K=6)),
+    "index_mask": lambda: make_index_mask("index_mask.npz", 18, b=2, s_q=64, s_kv=256, topk=8, s0=8, s1=40),
 }
 
 
