@@ -16,7 +16,10 @@ for the single kernel with the longest median duration; its `traffic` field is
 read from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed under
 profiles/ (null when that kernel has no such summary).
 
-After the timed steps the cfg5 long-context kernels (SparseMLA forward at
+After the timed steps the FP8-tensorwise SparseMLA forward and backward at the
+cfg2 shapes (cfg4: e4m3 q / kv with 1% x20 outliers) are timed and reported
+under "cfg4" against the mixed fp8 + bf16 MFMA floor (--no-cfg4 skips them).
+Then the cfg5 long-context kernels (SparseMLA forward at
 h=128, d_qk=576, d_v=512, topk=2048; e4m3 indexer at h=64, d=128; top-2048
 over s=16384) are timed on device-generated inputs and reported under "cfg5"
 (not part of `value`).
@@ -32,7 +35,7 @@ replays are first checked bit for bit against the eager step); the per-kernel
 breakdown and `eager_tokens_per_s` come from the eager timed steps before it.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
-                       [--no-cfg5] [--no-kl] [--no-graph] [--calib-copy-mib N]   (one N MiB
+                       [--no-cfg4] [--no-cfg5] [--no-kl] [--no-graph] [--calib-copy-mib N]   (one N MiB
                        device copy before timing, the calibration kernel of PMC runs)
 """
 from __future__ import annotations
@@ -145,6 +148,84 @@ def measure_cfg5(dev, reps=3):
     return res
 
 
+def graph_replay_time(fn, reps=10):
+    """Seconds per call of `fn` (one or more library calls on the current
+    stream), measured as replays of a HIP graph capturing it once, so host
+    launch gaps do not enter the figure: median of `reps` event-timed replays."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    g.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        a, b_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b_.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b_) / 1e3)
+    del g
+    return sorted(ts)[len(ts) // 2]
+
+
+# cfg4: FP8-tensorwise SparseMLA fwd + bwd at the cfg2 shapes, reported beside the headline
+def cfg4_work():
+    """(fp8 FLOP, bf16 FLOP) of the FP8 forward and backward: Q K^T runs on e4m3
+    codes, every other product in bf16 (fwd: PV; bwd: dP = dO V^T, dQ, dKV)."""
+    unit = 2 * B * S * H * TOPK
+    return {"fwd": (unit * D_QK, unit * D_V),
+            "bwd": (unit * D_QK, unit * (D_V + D_QK + D_QK + D_V))}
+
+
+def measure_cfg4(dev, reps=5):
+    """Median times of the cfg4 path on inputs generated on the CPU with a
+    fixed seed: q, kv ~ N(0, 1) with 1% of entries x20, quantised to e4m3 with
+    one tensorwise scale each (our quantiser, timed too), uniform causal top-256
+    indices, dO ~ N(0, 1).  Fractions are of the mixed floor
+    fp8_FLOP / 5.0 PF + bf16_FLOP / 2.5 PF.  Times are HIP-graph replays."""
+    import torch
+
+    from cppmega_amd import synthetic
+    from cppmega_amd.sparse_mla_ops import sparse_mla_fwd_fp8_interface, tensorwise_quantize
+    from cppmega_amd.sparse_mla_ops.sparse_mla_bwd_fp8 import sparse_mla_bwd_fp8
+
+    q = synthetic.outlier_values((B, S, H, D_QK), 41).to(torch.bfloat16).to(dev)
+    kv = synthetic.outlier_values((B, S, 1, D_QK), 42).to(torch.bfloat16).to(dev)
+    idx = synthetic.causal_indices(B, S, TOPK, seed=43).to(dev)
+    do = torch.randn((B, S, H, D_V), generator=torch.Generator().manual_seed(44)).to(torch.bfloat16).to(dev)
+    scale = D_QK ** -0.5
+    q8, qs = tensorwise_quantize(q)
+    k8, ks = tensorwise_quantize(kv)
+    qsv, ksv = qs.expand(B, S).contiguous(), ks.expand(B, S).contiguous()
+    out, lse = sparse_mla_fwd_fp8_interface(q8, k8, idx, q_scale=qsv, kv_scale=ksv, sm_scale=scale, d_v=D_V)
+
+    med_time = lambda fn: graph_replay_time(fn, reps)
+
+    t = {
+        "quantize_q_kv": med_time(lambda: (tensorwise_quantize(q), tensorwise_quantize(kv))),
+        "fwd": med_time(lambda: sparse_mla_fwd_fp8_interface(q8, k8, idx, q_scale=qsv, kv_scale=ksv, sm_scale=scale,
+                                                             d_v=D_V)),
+        "bwd": med_time(lambda: sparse_mla_bwd_fp8(q8, k8, qsv, ksv, out, do, idx, lse, sm_scale=scale)),
+    }
+    res = {}
+    for k, (f8, f16) in cfg4_work().items():
+        floor = f8 / (PEAK_FP8_TFLOPS * 1e12) + f16 / (PEAK_BF16_TFLOPS * 1e12)
+        res[k] = {"ms": round(t[k] * 1e3, 4), "bound": "mfma (fp8 + bf16)", "tflops": round((f8 + f16) / t[k] / 1e12, 1),
+                  "floor_us": round(floor * 1e6, 2), "frac": round(floor / t[k], 4)}
+    qbytes = (q.numel() + kv.numel()) * (2 * 2 + 1)  # amax read + quantise read, e4m3 write
+    res["quantize_q_kv"] = {"ms": round(t["quantize_q_kv"] * 1e3, 4), "bound": "hbm",
+                            "gbs": round(qbytes / t["quantize_q_kv"] / 1e9, 1), "peak": PEAK_HBM_GBS,
+                            "frac": round(qbytes / t["quantize_q_kv"] / 1e9 / PEAK_HBM_GBS, 4)}
+    del q, kv, idx, do, q8, k8, out, lse
+    torch.cuda.empty_cache()
+    return res
+
+
 # DSA indexer KL loss at the NAM56R attention shape, reported beside the headline
 KL_HEADS, KL_HN = 32, 128
 
@@ -153,7 +234,8 @@ def measure_indexer_kl(dev, reps=5):
     """Median time of the KL indexer loss (dense and sparse top-256) on
     device-generated inputs: query/key [S, B, 32, 128] bf16 ~ N(0, 0.5), index
     scores [B, S, S] ~ N(0, 1) with -inf above the diagonal, top-256 of them.
-    Algorithmic work: two q.k passes over the causal pairs of every head."""
+    Algorithmic work: two q.k passes over the causal pairs of every head.
+    Times are HIP-graph replays."""
     import torch
 
     from cppmega_amd.dsa_index_mask import topk_index_mask
@@ -169,19 +251,7 @@ def measure_indexer_kl(dev, reps=5):
     scale = KL_HN ** -0.5
     fl = kl_flops(B, S, S, KL_HEADS, KL_HN)
     res = {}
-
-    def med_time(fn):
-        fn()
-        torch.cuda.synchronize()
-        ts = []
-        for _ in range(reps):
-            a, b_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            fn()
-            b_.record()
-            torch.cuda.synchronize()
-            ts.append(a.elapsed_time(b_) / 1e3)
-        return sorted(ts)[len(ts) // 2]
+    med_time = lambda fn: graph_replay_time(fn, reps)
 
     for mode, sparse in (("dense", False), ("sparse", True)):
         t = med_time(lambda: indexer_kl_loss(sc, tk, q, k, scale, 1.0, sparse))
@@ -327,6 +397,7 @@ def main():
     ap.add_argument("--calib-copy-mib", type=int, default=0)
     ap.add_argument("--no-cfg5", action="store_true", help="skip the cfg5 (long-context) kernel timings")
     ap.add_argument("--no-kl", action="store_true", help="skip the indexer KL loss timings")
+    ap.add_argument("--no-cfg4", action="store_true", help="skip the FP8 (cfg4) SparseMLA timings")
     ap.add_argument("--no-graph", action="store_true",
                     help="time eager launches only (default: the step is also captured in a HIP graph)")
     args = ap.parse_args()
@@ -432,6 +503,7 @@ def main():
 
     cfg5 = None if args.no_cfg5 else measure_cfg5(dev)
     kl = None if args.no_kl else measure_indexer_kl(dev)
+    cfg4 = None if args.no_cfg4 else measure_cfg4(dev)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -468,6 +540,8 @@ def main():
         "cfg5": ({"workload": f"s={C5_S} h={C5_H} d_qk={C5_DQK} d_v={C5_DV} topk={C5_TOPK} SparseMLA fwd (bf16), "
                               f"indexer h={C5_HIDX} d={C5_DIDX} e4m3 causal, top-{C5_TOPK}",
                   "kernels": cfg5} if cfg5 is not None else None),
+        "cfg4": ({"workload": f"FP8 tensorwise SparseMLA fwd+bwd at cfg2 shapes (q/kv e4m3, 1% x20 outliers, "
+                               f"QK^T on e4m3, other products bf16)", "kernels": cfg4} if cfg4 is not None else None),
         "indexer_kl_loss": ({"workload": f"compute_dsa_indexer_loss_splitk: query/key [{S},{B},{KL_HEADS},{KL_HN}] "
                                          f"bf16, index scores [{B},{S},{S}] causal, top-{TOPK}; index_mask: "
                                          f"topk_index_mask of the top-{TOPK} into [{B},{S},{S}] f32",

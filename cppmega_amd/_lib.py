@@ -40,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "dsa_topk",
     "dsa_fp8_quantize_workspace_size",
     "dsa_fp8_tensorwise_quantize",
+    "dsa_fp8_dequantize",
     "dsa_indexer_kl_loss_workspace_size",
     "dsa_indexer_kl_loss",
     "dsa_topk_index_mask",
@@ -73,6 +74,7 @@ _SIGNATURES = {
     "dsa_fp8_quantize_workspace_size": (_size_t, []),
     "dsa_fp8_tensorwise_quantize": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p,
                                            _c_void_p, _size_t, _c_void_p]),
+    "dsa_fp8_dequantize": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i32, _c_void_p]),
     "dsa_indexer_kl_loss_workspace_size": (_size_t, [_i64] * 5 + [_i32]),
     "dsa_indexer_kl_loss": (_i32, [_c_void_p, _c_void_p, _i32, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                    _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _i32,

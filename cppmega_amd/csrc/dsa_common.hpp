@@ -90,6 +90,15 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
   return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
 }
 
+// Two e4m3 codes -> two exact floats by the hardware conversion
+// (v_cvt_pk_f32_fp8, OCP e4m3fn on gfx950): bytes 0 and 1 of `word` when
+// hi == false, bytes 2 and 3 when hi == true.  Same values as e4m3_to_f32
+// (checked for all 256 codes through dsa_fp8_dequantize by the GPU tests).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ f32x2 e4m3x2_to_f32(uint32_t word, bool hi) {
+  return hi ? __builtin_amdgcn_cvt_pk_f32_fp8((int)word, true) : __builtin_amdgcn_cvt_pk_f32_fp8((int)word, false);
+}
+
 // Round-to-nearest-even, saturating at +-448; NaN -> 0x7f (sign kept).
 __device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
   const uint32_t u = __float_as_uint(f);

@@ -7,7 +7,9 @@
 // scale_inv = 1 / scale.  Three stream-ordered kernels, no atomics and no
 // memset (safe under graph capture): per-block maxima, a one-block final
 // reduction that derives scale / scale_inv, and the elementwise cast
-// (round-to-nearest-even, saturating at +-448).
+// (round-to-nearest-even, saturating at +-448).  dsa_fp8_dequantize is the
+// inverse view (code value * scale_inv, the reference's Float8Tensor
+// dequantize) through the hardware e4m3 conversion the SparseMLA kernels use.
 #include "dsa_common.hpp"
 
 namespace dsa {
@@ -18,11 +20,34 @@ __device__ __forceinline__ float load_elem(const void *x, int64_t i, int bf16) {
   return bf16 ? bf16_bits_to_f32(static_cast<const uint16_t *>(x)[i]) : static_cast<const float *>(x)[i];
 }
 
-__global__ void __launch_bounds__(256) amax_partial_kernel(const void *x, int64_t n, int bf16, float *part) {
+// Per-block max |x| (NaN ignored).  With a 16-byte aligned x every thread
+// reads 16-byte chunks (8 bf16 or 4 f32), four chunks in flight per loop trip.
+__global__ void __launch_bounds__(256) amax_partial_kernel(const void *x, int64_t n, int bf16, int vec, float *part) {
   __shared__ float red[4];
   float m = 0.0f;
-  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
-    m = fmaxf(m, fabsf(load_elem(x, i, bf16)));
+  const int64_t tid = blockIdx.x * 256ll + threadIdx.x, nth = (int64_t)gridDim.x * 256;
+  int64_t head = 0;  // elements covered by whole chunks
+  if (vec) {
+    const int per = bf16 ? 8 : 4;
+    const int64_t nch = n / per;
+    head = nch * per;
+    const i32x4 *xc = static_cast<const i32x4 *>(x);
+#pragma unroll 4
+    for (int64_t i = tid; i < nch; i += nth) {
+      const i32x4 v = xc[i];
+      if (bf16) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t w = (uint32_t)v[e];
+          m = fmaxf(m, fmaxf(fabsf(__uint_as_float(w << 16)), fabsf(__uint_as_float(w & 0xffff0000u))));
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) m = fmaxf(m, fabsf(__int_as_float(v[e])));
+      }
+    }
+  }
+  for (int64_t i = head + tid; i < n; i += nth) m = fmaxf(m, fabsf(load_elem(x, i, bf16)));
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
   if (lane_id() == 0) red[wave_id()] = m;
@@ -48,18 +73,70 @@ __global__ void __launch_bounds__(256) amax_final_kernel(const float *part, int 
   }
 }
 
-__global__ void __launch_bounds__(256) quantize_kernel(const void *x, int64_t n, int bf16, const float *ws_scale,
-                                                       uint8_t *out) {
+// Elementwise cast.  With a 16-byte aligned x (and 8-byte aligned out) every
+// thread converts chunks of 8 elements: 16 (bf16) or 32 (f32) bytes in, one
+// 8-byte store of 8 codes out.
+__global__ void __launch_bounds__(256) quantize_kernel(const void *x, int64_t n, int bf16, int vec,
+                                                       const float *ws_scale, uint8_t *out) {
   const float scale = ws_scale[0];
-  const int64_t n4 = n / 4;
-  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
-    uint32_t packed = 0;
+  const int64_t tid = blockIdx.x * 256ll + threadIdx.x, nth = (int64_t)gridDim.x * 256;
+  int64_t head = 0;
+  if (vec) {
+    const int64_t n8 = n / 8;
+    head = n8 * 8;
+#pragma unroll 2
+    for (int64_t i = tid; i < n8; i += nth) {
+      float f[8];
+      if (bf16) {
+        const i32x4 v = static_cast<const i32x4 *>(x)[i];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) packed |= f32_to_e4m3(load_elem(x, 4 * i + e, bf16) * scale) << (8 * e);
-    reinterpret_cast<uint32_t *>(out)[i] = packed;
+        for (int e = 0; e < 4; ++e) {
+          f[2 * e] = __uint_as_float((uint32_t)v[e] << 16);
+          f[2 * e + 1] = __uint_as_float((uint32_t)v[e] & 0xffff0000u);
+        }
+      } else {
+        const i32x4 v0 = static_cast<const i32x4 *>(x)[2 * i], v1 = static_cast<const i32x4 *>(x)[2 * i + 1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          f[e] = __int_as_float(v0[e]);
+          f[4 + e] = __int_as_float(v1[e]);
+        }
+      }
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        lo |= f32_to_e4m3(f[e] * scale) << (8 * e);
+        hi |= f32_to_e4m3(f[4 + e] * scale) << (8 * e);
+      }
+      reinterpret_cast<i32x2 *>(out)[i] = i32x2{(int)lo, (int)hi};
+    }
   }
-  for (int64_t i = 4 * n4 + blockIdx.x * 256ll + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
-    out[i] = (uint8_t)f32_to_e4m3(load_elem(x, i, bf16) * scale);
+  for (int64_t i = head + tid; i < n; i += nth) out[i] = (uint8_t)f32_to_e4m3(load_elem(x, i, bf16) * scale);
+}
+
+// e4m3 codes -> code value * scale_inv[0] as bf16 (RNE) or f32, four codes per
+// thread through the hardware pair conversion.
+__global__ void __launch_bounds__(256) dequantize_kernel(const uint8_t *x, int64_t n, const float *scale_inv,
+                                                         int out_bf16, void *out) {
+  const float s = scale_inv[0];
+  const int64_t tid = blockIdx.x * 256ll + threadIdx.x, nth = (int64_t)gridDim.x * 256;
+  for (int64_t i = tid; 4 * i < n; i += nth) {
+    uint32_t w = 0;
+    const int64_t rem = n - 4 * i;
+    if (rem >= 4 && (reinterpret_cast<uintptr_t>(x) & 3u) == 0) {
+      w = reinterpret_cast<const uint32_t *>(x)[i];
+    } else {
+      for (int e = 0; e < 4 && e < rem; ++e) w |= (uint32_t)x[4 * i + e] << (8 * e);
+    }
+    const f32x2 a = e4m3x2_to_f32(w, false), b = e4m3x2_to_f32(w, true);
+    const float v[4] = {a[0] * s, a[1] * s, b[0] * s, b[1] * s};
+    for (int e = 0; e < 4 && e < rem; ++e) {
+      if (out_bf16)
+        static_cast<uint16_t *>(out)[4 * i + e] = (uint16_t)f32_to_bf16_bits(v[e]);
+      else
+        static_cast<float *>(out)[4 * i + e] = v[e];
+    }
+  }
 }
 
 }  // namespace dsa
@@ -87,13 +164,29 @@ extern "C" int dsa_fp8_tensorwise_quantize(const void *x, int64_t n, int in_dtyp
   int64_t blocks = (n + 255) / 256;
   if (blocks > kQuantBlocks) blocks = kQuantBlocks;
   if (blocks < 1) blocks = 1;
-  hipLaunchKernelGGL(amax_partial_kernel, dim3((unsigned)blocks), dim3(256), 0, st, x, n, bf16, part);
+  const int vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(out_fp8) & 7u) == 0;
+  hipLaunchKernelGGL(amax_partial_kernel, dim3((unsigned)blocks), dim3(256), 0, st, x, n, bf16, vec, part);
   hipLaunchKernelGGL(amax_final_kernel, dim3(1), dim3(256), 0, st, part, (int)blocks, ws_scale, scale_inv);
   if (n > 0) {
-    int64_t qb = (n / 4 + 255) / 256;
+    int64_t qb = (n / 8 + 255) / 256;
     if (qb > 4096) qb = 4096;
     if (qb < 1) qb = 1;
-    hipLaunchKernelGGL(quantize_kernel, dim3((unsigned)qb), dim3(256), 0, st, x, n, bf16, ws_scale, out_fp8);
+    hipLaunchKernelGGL(quantize_kernel, dim3((unsigned)qb), dim3(256), 0, st, x, n, bf16, vec, ws_scale, out_fp8);
   }
   return check_launch("fp8_tensorwise_quantize");
+}
+
+extern "C" int dsa_fp8_dequantize(const uint8_t *x_fp8, int64_t n, const float *scale_inv, void *out,
+                                  int out_dtype, void *stream) {
+  DSA_REQUIRE(n >= 0, "dsa_fp8_dequantize: n < 0");
+  DSA_REQUIRE(out_dtype == DSA_DTYPE_BF16 || out_dtype == DSA_DTYPE_F32,
+              "dsa_fp8_dequantize: output dtype must be bf16 or f32 (got %d)", out_dtype);
+  if (n == 0) return DSA_OK;
+  DSA_REQUIRE(x_fp8 && scale_inv && out, "dsa_fp8_dequantize: null pointer");
+  int64_t blocks = (n / 4 + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(dequantize_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), x_fp8,
+                     n, scale_inv, out_dtype == DSA_DTYPE_BF16 ? 1 : 0, out);
+  return check_launch("fp8_dequantize");
 }

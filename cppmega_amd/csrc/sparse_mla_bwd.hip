@@ -222,13 +222,11 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
         const int h = u / QCH, c = u % QCH;
         i32x4 v = qv[it];
         if constexpr (FP8) {
-          const unsigned long raw = (unsigned long)(uint32_t)qv[it][0] | ((unsigned long)(uint32_t)qv[it][1] << 32);
           uint32_t wq[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t c0 = (uint32_t)(raw >> (16 * e)) & 0xffu;
-            const uint32_t c1 = (uint32_t)(raw >> (16 * e + 8)) & 0xffu;
-            wq[e] = pack_bf16x2(e4m3_to_f32(c0) * qsc, e4m3_to_f32(c1) * qsc);
+          for (int e = 0; e < 4; ++e) {  // codes 2e, 2e + 1 of the 8 in qv[it][0..1]
+            const f32x2 v2 = e4m3x2_to_f32((uint32_t)qv[it][e >> 1], (e & 1) != 0);
+            wq[e] = pack_bf16x2(v2[0] * qsc, v2[1] * qsc);
           }
           v = i32x4{(int)wq[0], (int)wq[1], (int)wq[2], (int)wq[3]};
         }

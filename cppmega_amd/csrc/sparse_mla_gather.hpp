@@ -122,9 +122,8 @@ __device__ __forceinline__ void gather_store_dequant(const typename Gat::Regs &r
         uint32_t w[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const uint32_t word = (uint32_t)rg.v[uu][r][e >> 1];
-          const uint32_t sh = 16 * (e & 1);
-          w[e] = pack_bf16x2(e4m3_to_f32((word >> sh) & 0xffu) * s, e4m3_to_f32((word >> (sh + 8)) & 0xffu) * s);
+          const f32x2 v2 = e4m3x2_to_f32((uint32_t)rg.v[uu][r][e >> 1], (e & 1) != 0);
+          w[e] = pack_bf16x2(v2[0] * s, v2[1] * s);
         }
         unsigned char *dst = Kd + (quad * 4 + r) * stride + c * 32;
         *reinterpret_cast<i32x4 *>(dst) = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};

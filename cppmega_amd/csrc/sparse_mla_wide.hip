@@ -104,9 +104,8 @@ __device__ __forceinline__ void wide_store(const typename C::Regs &rg, unsigned 
           uint32_t wd[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const uint32_t word = (uint32_t)v[e >> 1];
-            const uint32_t sh = 16 * (e & 1);
-            wd[e] = pack_bf16x2(e4m3_to_f32((word >> sh) & 0xffu) * s, e4m3_to_f32((word >> (sh + 8)) & 0xffu) * s);
+            const f32x2 v2 = e4m3x2_to_f32((uint32_t)v[e >> 1], (e & 1) != 0);
+            wd[e] = pack_bf16x2(v2[0] * s, v2[1] * s);
           }
           unsigned char *dst = Kd + row * KD_STRIDE + c * 32;
           *reinterpret_cast<i32x4 *>(dst) = i32x4{(int)wd[0], (int)wd[1], (int)wd[2], (int)wd[3]};
@@ -447,13 +446,12 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
       i32x4 v = {0, 0, 0, 0};
       if (h < nheads) {
         if constexpr (FP8) {
-          const long raw = *reinterpret_cast<const long *>(p.q + (head0 + h) * D_QK + 8 * c);
+          const unsigned long raw = *reinterpret_cast<const unsigned long *>(p.q + (head0 + h) * D_QK + 8 * c);
           uint32_t wq[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t c0 = (uint32_t)((unsigned long)raw >> (16 * e)) & 0xffu;
-            const uint32_t c1 = (uint32_t)((unsigned long)raw >> (16 * e + 8)) & 0xffu;
-            wq[e] = pack_bf16x2(e4m3_to_f32(c0) * qsc, e4m3_to_f32(c1) * qsc);
+          for (int e = 0; e < 4; ++e) {  // codes 2e, 2e + 1 of the 8 in raw
+            const f32x2 v2 = e4m3x2_to_f32((uint32_t)(raw >> (32 * (e >> 1))), (e & 1) != 0);
+            wq[e] = pack_bf16x2(v2[0] * qsc, v2[1] * qsc);
           }
           v = i32x4{(int)wq[0], (int)wq[1], (int)wq[2], (int)wq[3]};
         } else {

@@ -467,9 +467,18 @@ topk_wave_kernel(const TopkParams p) {
   int ng = (n + 64 * kGroup - 1) / (64 * kGroup);  // groups holding window columns
   const int npad = 64 * kGroup * ng - n;          // padded elements in those groups
   const float kPad = __uint_as_float(0x7fc00000u);
+  // groups wholly past the window (half of a causal matrix) issue no loads
   float x[IPL];
 #pragma unroll
-  for (int i = 0; i < IPL; ++i) x[i] = buffer_load_f32(rsrc, 4 * lane, 256 * i);
+  for (int g = 0; g < NG; ++g) {
+    if (g < ng) {
+#pragma unroll
+      for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) x[i] = buffer_load_f32(rsrc, 4 * lane, 256 * i);
+    } else {
+#pragma unroll
+      for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) x[i] = kPad;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < IPL; ++i) x[i] = (64 * i + lane < n) ? rank_value(x[i]) : kPad;
 

@@ -15,7 +15,7 @@ from .sparse_mla import (
 from .sparse_mla_bwd import sparse_mla_bwd
 from .sparse_mla_bwd_fp8 import sparse_mla_bwd_fp8
 from .sparse_mla_fwd import sparse_mla_fwd_interface
-from .sparse_mla_fwd_fp8 import per_token_cast_to_fp8, sparse_mla_fwd_fp8_interface, tensorwise_quantize
+from .sparse_mla_fwd_fp8 import fp8_dequantize, per_token_cast_to_fp8, sparse_mla_fwd_fp8_interface, tensorwise_quantize
 
 __all__ = [
     "SparseMLA",
@@ -28,6 +28,7 @@ __all__ = [
     "sparse_mla_bwd_fp8",
     "sparse_mla_fp8_as_unfused_dsa",
     "sparse_mla_fwd_fp8_interface",
+    "fp8_dequantize",
     "sparse_mla_fwd_interface",
     "tensorwise_quantize",
 ]

@@ -46,6 +46,21 @@ def tensorwise_quantize(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     return out, scale_inv
 
 
+def fp8_dequantize(x8: torch.Tensor, scale_inv: torch.Tensor, dtype=torch.bfloat16) -> torch.Tensor:
+    """e4m3 tensor (any shape) + one-element scale_inv -> value * scale_inv as bf16 (RNE) or f32
+    (the role of Float8Tensor.dequantize() for the tensors SparseMLA_FP8 unpacks)."""
+    assert x8.dtype == torch.float8_e4m3fn, f"expected float8_e4m3fn, got {x8.dtype}"
+    assert dtype in (torch.bfloat16, torch.float32), f"dequantised dtype must be bf16 or f32, got {dtype}"
+    x8 = x8.contiguous()
+    scale_inv = scale_inv.reshape(-1)[:1].to(device=x8.device, dtype=torch.float32).contiguous()
+    out = torch.empty(x8.shape, dtype=dtype, device=x8.device)
+    _, stream = stream_of(x8)
+    rc = _lib.load().dsa_fp8_dequantize(x8.data_ptr(), x8.numel(), scale_inv.data_ptr(), out.data_ptr(),
+                                        _lib.DTYPE_BF16 if dtype == torch.bfloat16 else _lib.DTYPE_F32, stream)
+    _lib.check(rc, "dsa_fp8_dequantize")
+    return out
+
+
 def per_token_cast_to_fp8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Tensorwise e4m3 cast; the tensor scale is broadcast to shape x.shape[:-1]
     (the historical per-token name and ABI of the reference are kept)."""

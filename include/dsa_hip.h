@@ -172,6 +172,16 @@ int dsa_fp8_tensorwise_quantize(const void *x, int64_t n, int in_dtype,
                                 void *stream);
 
 /*
+ * e4m3 dequantisation: out[i] = value(x_fp8[i]) * scale_inv[0] (bf16 RNE or f32).
+ * Replaces Float8Tensor.dequantize() (the TE tensors whose _data / _scale_inv
+ *   cppmega's SparseMLA_FP8 unpacks, cppmega/megatron/sparse_mla_ops/sparse_mla.py:310-353);
+ *   decodes with the same hardware conversion the e4m3 SparseMLA kernels use.
+ *   x_fp8 [n] OCP e4m3fn, scale_inv [1] f32 (device), out [n] (out_dtype bf16 or f32).
+ */
+int dsa_fp8_dequantize(const uint8_t *x_fp8, int64_t n, const float *scale_inv,
+                       void *out, int out_dtype, void *stream);
+
+/*
  * DSA indexer KL loss (the indexer's training signal):
  *   a_h[t, s] = softmax_scale * query[t, b, h] . key[s, b, h / (H / G)]
  *   P[t, s]   = mean_h softmax over s <= t of a_h[t, :]      (sparse: and s in

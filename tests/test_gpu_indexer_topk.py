@@ -232,3 +232,42 @@ def test_fp8_quantize_zero_and_specials(dev):
     x8, si = tensorwise_quantize(x.to(dev))
     r8, rsi = ofp8.tensorwise_quantize(x)
     assert torch.equal(x8.cpu().view(torch.uint8), r8.view(torch.uint8)) and torch.equal(si.cpu(), rsi)
+
+
+def test_fp8_quantize_unaligned_input(dev):
+    """A view starting 2 bytes into its storage takes the scalar path: same bits."""
+    x = synthetic.outlier_values((4097,), seed=5).to(torch.bfloat16)
+    xd = x.to(dev)[1:]
+    x8, si = tensorwise_quantize(xd)
+    r8, rsi = ofp8.tensorwise_quantize(x[1:])
+    assert torch.equal(x8.cpu().view(torch.uint8), r8.view(torch.uint8)) and torch.equal(si.cpu(), rsi)
+
+
+def test_fp8_dequantize_every_code(dev):
+    """The hardware e4m3 conversion the SparseMLA kernels dequantise with equals
+    the bit-field decode for all 256 codes (f32, NaN codes NaN, -0 kept), and
+    the bf16 form is the RNE rounding of value * scale_inv."""
+    from cppmega_amd.sparse_mla_ops import fp8_dequantize
+
+    codes = torch.arange(256, dtype=torch.uint8)
+    exp = torch.tensor([ofp8.e4m3_value(c) for c in range(256)], dtype=torch.float32)
+    for n in (256, 255):   # a whole and a partial last group of four codes
+        x8 = codes[:n].view(torch.float8_e4m3fn).to(dev)
+        got = fp8_dequantize(x8, torch.ones(1), dtype=torch.float32).cpu()
+        e = exp[:n]
+        assert torch.equal(torch.isnan(got), torch.isnan(e))
+        ok = ~torch.isnan(e)
+        assert torch.equal(got[ok].view(torch.int32), e[ok].view(torch.int32))
+    x8 = codes.view(torch.float8_e4m3fn).to(dev)
+    for s in (1.0, 0.0625, 3.7e-3, 1000.0):
+        si = torch.tensor([s], dtype=torch.float32)
+        got = fp8_dequantize(x8, si).cpu()
+        ref = (exp * si).to(torch.bfloat16)
+        ok = ~torch.isnan(exp)
+        assert torch.equal(got[ok].view(torch.int16), ref[ok].view(torch.int16)), s
+        assert torch.isnan(got[~ok].float()).all()
+    # round trip of the quantiser at its own scale
+    x = synthetic.outlier_values((5000,), seed=9).to(torch.bfloat16)
+    q8, qs = tensorwise_quantize(x.to(dev))
+    back = fp8_dequantize(q8, qs, dtype=torch.float32).cpu()
+    assert torch.equal(back, ofp8.dequantize(q8.cpu(), qs.cpu()))
