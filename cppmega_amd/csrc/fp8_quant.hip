@@ -73,6 +73,25 @@ __global__ void __launch_bounds__(256) amax_final_kernel(const float *part, int 
   }
 }
 
+// Four floats -> four e4m3 codes by the hardware pair conversion
+// (v_cvt_pk_fp8_f32, round to nearest even).  Inputs are clamped to +-448
+// first, which gives the saturating encoding of f32_to_e4m3; a NaN input keeps
+// that encoding's code (sign | 0x7f).
+__device__ __forceinline__ uint32_t e4m3x4_encode(float a, float b, float c, float d) {
+  const float v[4] = {a, b, c, d};
+  float cl[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) cl[e] = fminf(fmaxf(v[e], -448.0f), 448.0f);
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(cl[0], cl[1], 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(cl[2], cl[3], w, true);
+  uint32_t out = (uint32_t)w;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (v[e] != v[e])
+      out = (out & ~(0xffu << (8 * e))) | (((__float_as_uint(v[e]) >> 24) & 0x80u | 0x7fu) << (8 * e));
+  return out;
+}
+
 // Elementwise cast.  With a 16-byte aligned x (and 8-byte aligned out) every
 // thread converts chunks of 8 elements: 16 (bf16) or 32 (f32) bytes in, one
 // 8-byte store of 8 codes out.
@@ -102,12 +121,11 @@ __global__ void __launch_bounds__(256) quantize_kernel(const void *x, int64_t n,
           f[4 + e] = __int_as_float(v1[e]);
         }
       }
-      uint32_t lo = 0, hi = 0;
+      float y[8];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        lo |= f32_to_e4m3(f[e] * scale) << (8 * e);
-        hi |= f32_to_e4m3(f[4 + e] * scale) << (8 * e);
-      }
+      for (int e = 0; e < 8; ++e) y[e] = f[e] * scale;
+      const uint32_t lo = e4m3x4_encode(y[0], y[1], y[2], y[3]);
+      const uint32_t hi = e4m3x4_encode(y[4], y[5], y[6], y[7]);
       reinterpret_cast<i32x2 *>(out)[i] = i32x2{(int)lo, (int)hi};
     }
   }

@@ -271,3 +271,21 @@ def test_fp8_dequantize_every_code(dev):
     q8, qs = tensorwise_quantize(x.to(dev))
     back = fp8_dequantize(q8, qs, dtype=torch.float32).cpu()
     assert torch.equal(back, ofp8.dequantize(q8.cpu(), qs.cpu()))
+
+
+def test_fp8_quantize_every_code_and_tie(dev):
+    """amax = 448 makes the scale exactly 1: every e4m3 value and every midpoint
+    between neighbours (round-to-nearest-even ties), both signs, and NaN map to
+    the same codes as torch's float8_e4m3fn cast (x * scale never exceeds 448
+    by more than rounding in a tensorwise cast, so saturation needs no test)."""
+    vals = sorted({ofp8.e4m3_value(c) for c in range(128) if c != 0x7f})
+    mids = [(a + b) / 2 for a, b in zip(vals[:-1], vals[1:])]
+    pos = torch.tensor(vals + mids, dtype=torch.float32)
+    x = torch.cat([pos, -pos, torch.tensor([448.0, float("nan"), -float("nan")])])
+    x8, si = tensorwise_quantize(x.to(dev))
+    assert float(si) == 1.0
+    r8, _ = ofp8.tensorwise_quantize(x)
+    got, ref = x8.cpu().view(torch.uint8), r8.view(torch.uint8)
+    fin = ~torch.isnan(x)
+    assert torch.equal(got[fin], ref[fin])
+    assert torch.equal(got[~fin] & 0x7f, torch.full_like(got[~fin], 0x7f))   # NaN codes
