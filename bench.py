@@ -176,10 +176,12 @@ def graph_replay_time(fn, reps=10):
 # cfg4: FP8-tensorwise SparseMLA fwd + bwd at the cfg2 shapes, reported beside the headline
 def cfg4_work():
     """(fp8 FLOP, bf16 FLOP) of the FP8 forward and backward: Q K^T runs on e4m3
-    codes, every other product in bf16 (fwd: PV; bwd: dP = dO V^T, dQ, dKV)."""
+    codes, every other product in bf16 (fwd: PV; bwd: dP = dO V^T, dQ, dKV);
+    the MXFP8 block-scaled forward splits the same way."""
     unit = 2 * B * S * H * TOPK
     return {"fwd": (unit * D_QK, unit * D_V),
-            "bwd": (unit * D_QK, unit * (D_V + D_QK + D_QK + D_V))}
+            "bwd": (unit * D_QK, unit * (D_V + D_QK + D_QK + D_V)),
+            "mxfp8_fwd": (unit * D_QK, unit * D_V)}
 
 
 def measure_cfg4(dev, reps=5):
@@ -206,7 +208,17 @@ def measure_cfg4(dev, reps=5):
 
     med_time = lambda fn: graph_replay_time(fn, reps)
 
+    # MXFP8 block-scaled payloads of the same shapes (synthetic: the e4m3 cast of
+    # the same values over a power-of-two scale per 32 channels)
+    from cppmega_amd.sparse_mla_ops import sparse_mla_blockscaled_mxfp8_fwd_interface
+    gen = torch.Generator(device=dev).manual_seed(45)
+    qbs = torch.exp2(torch.randint(-6, 0, (B, S, H, D_QK // 32), generator=gen, device=dev).float())
+    kbs = torch.exp2(torch.randint(-6, 0, (B, S, 1, D_QK // 32), generator=gen, device=dev).float())
+    qmx = (q.float() / qbs.repeat_interleave(32, dim=-1)).clamp(-448, 448).to(torch.float8_e4m3fn)
+    kmx = (kv.float() / kbs.repeat_interleave(32, dim=-1)).clamp(-448, 448).to(torch.float8_e4m3fn)
     t = {
+        "mxfp8_fwd": med_time(lambda: sparse_mla_blockscaled_mxfp8_fwd_interface(qmx, kmx, qbs, kbs, idx, sm_scale=scale,
+                                                                                 d_v=D_V)),
         "quantize_q_kv": med_time(lambda: (tensorwise_quantize(q), tensorwise_quantize(kv))),
         "fwd": med_time(lambda: sparse_mla_fwd_fp8_interface(q8, k8, idx, q_scale=qsv, kv_scale=ksv, sm_scale=scale,
                                                              d_v=D_V)),
@@ -221,7 +233,7 @@ def measure_cfg4(dev, reps=5):
     res["quantize_q_kv"] = {"ms": round(t["quantize_q_kv"] * 1e3, 4), "bound": "hbm",
                             "gbs": round(qbytes / t["quantize_q_kv"] / 1e9, 1), "peak": PEAK_HBM_GBS,
                             "frac": round(qbytes / t["quantize_q_kv"] / 1e9 / PEAK_HBM_GBS, 4)}
-    del q, kv, idx, do, q8, k8, out, lse
+    del q, kv, idx, do, q8, k8, out, lse, qmx, kmx, qbs, kbs
     torch.cuda.empty_cache()
     return res
 
@@ -240,7 +252,6 @@ def measure_indexer_kl(dev, reps=5):
 
     from cppmega_amd.dsa_index_mask import topk_index_mask
     from cppmega_amd.dsa_splitk_indexer_loss import indexer_kl_loss
-    from oracle.indexer_loss import kl_flops
 
     gen = torch.Generator(device=dev).manual_seed(9)
     q = (torch.randn((S, B, KL_HEADS, KL_HN), generator=gen, device=dev) * 0.5).to(torch.bfloat16)
@@ -249,7 +260,7 @@ def measure_indexer_kl(dev, reps=5):
     sc.masked_fill_(torch.ones(S, S, dtype=torch.bool, device=dev).triu(1), float("-inf"))
     tk = sc.topk(TOPK, dim=-1).indices
     scale = KL_HN ** -0.5
-    fl = kl_flops(B, S, S, KL_HEADS, KL_HN)
+    fl = 2 * (2 * B * KL_HEADS * KL_HN * (S * (S + 1) // 2))  # two q.k passes over the causal pairs
     res = {}
     med_time = lambda fn: graph_replay_time(fn, reps)
 
@@ -541,7 +552,8 @@ def main():
                               f"indexer h={C5_HIDX} d={C5_DIDX} e4m3 causal, top-{C5_TOPK}",
                   "kernels": cfg5} if cfg5 is not None else None),
         "cfg4": ({"workload": f"FP8 tensorwise SparseMLA fwd+bwd at cfg2 shapes (q/kv e4m3, 1% x20 outliers, "
-                               f"QK^T on e4m3, other products bf16)", "kernels": cfg4} if cfg4 is not None else None),
+                               f"QK^T on e4m3, other products bf16); mxfp8_fwd: the block-scaled (one f32 scale "
+                               f"per 32 channels) forward on the same shapes", "kernels": cfg4} if cfg4 is not None else None),
         "indexer_kl_loss": ({"workload": f"compute_dsa_indexer_loss_splitk: query/key [{S},{B},{KL_HEADS},{KL_HN}] "
                                          f"bf16, index scores [{B},{S},{S}] causal, top-{TOPK}; index_mask: "
                                          f"topk_index_mask of the top-{TOPK} into [{B},{S},{S}] f32",

@@ -25,6 +25,7 @@ DTYPE_E4M3 = 1
 DTYPE_F32 = 2
 DTYPE_I32 = 3
 DTYPE_I64 = 4
+DTYPE_MXFP8 = 5
 
 BWD_FP32_PARTIALS = 1
 
@@ -41,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "dsa_fp8_quantize_workspace_size",
     "dsa_fp8_tensorwise_quantize",
     "dsa_fp8_dequantize",
+    "dsa_fp8_dequantize_blockwise",
     "dsa_indexer_kl_loss_workspace_size",
     "dsa_indexer_kl_loss",
     "dsa_topk_index_mask",
@@ -75,6 +77,7 @@ _SIGNATURES = {
     "dsa_fp8_tensorwise_quantize": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p,
                                            _c_void_p, _size_t, _c_void_p]),
     "dsa_fp8_dequantize": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i32, _c_void_p]),
+    "dsa_fp8_dequantize_blockwise": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i32, _c_void_p]),
     "dsa_indexer_kl_loss_workspace_size": (_size_t, [_i64] * 5 + [_i32]),
     "dsa_indexer_kl_loss": (_i32, [_c_void_p, _c_void_p, _i32, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                    _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _i32,

@@ -132,13 +132,15 @@ __global__ void __launch_bounds__(256) quantize_kernel(const void *x, int64_t n,
   for (int64_t i = head + tid; i < n; i += nth) out[i] = (uint8_t)f32_to_e4m3(load_elem(x, i, bf16) * scale);
 }
 
-// e4m3 codes -> code value * scale_inv[0] as bf16 (RNE) or f32, four codes per
-// thread through the hardware pair conversion.
+// e4m3 codes -> code value * scale as bf16 (RNE) or f32, four codes per
+// thread through the hardware pair conversion; scale = scale_inv[0]
+// (block == 0) or scale_inv[i / block] (block a multiple of 4: one scale per
+// `block` consecutive elements, e.g. 32 for MXFP8 rows).
 __global__ void __launch_bounds__(256) dequantize_kernel(const uint8_t *x, int64_t n, const float *scale_inv,
-                                                         int out_bf16, void *out) {
-  const float s = scale_inv[0];
+                                                         int64_t block, int out_bf16, void *out) {
   const int64_t tid = blockIdx.x * 256ll + threadIdx.x, nth = (int64_t)gridDim.x * 256;
   for (int64_t i = tid; 4 * i < n; i += nth) {
+    const float s = block ? scale_inv[(4 * i) / block] : scale_inv[0];
     uint32_t w = 0;
     const int64_t rem = n - 4 * i;
     if (rem >= 4 && (reinterpret_cast<uintptr_t>(x) & 3u) == 0) {
@@ -194,8 +196,8 @@ extern "C" int dsa_fp8_tensorwise_quantize(const void *x, int64_t n, int in_dtyp
   return check_launch("fp8_tensorwise_quantize");
 }
 
-extern "C" int dsa_fp8_dequantize(const uint8_t *x_fp8, int64_t n, const float *scale_inv, void *out,
-                                  int out_dtype, void *stream) {
+static int dequantize(const uint8_t *x_fp8, int64_t n, const float *scale_inv, int64_t block, void *out,
+                      int out_dtype, void *stream) {
   DSA_REQUIRE(n >= 0, "dsa_fp8_dequantize: n < 0");
   DSA_REQUIRE(out_dtype == DSA_DTYPE_BF16 || out_dtype == DSA_DTYPE_F32,
               "dsa_fp8_dequantize: output dtype must be bf16 or f32 (got %d)", out_dtype);
@@ -205,6 +207,18 @@ extern "C" int dsa_fp8_dequantize(const uint8_t *x_fp8, int64_t n, const float *
   if (blocks > 4096) blocks = 4096;
   if (blocks < 1) blocks = 1;
   hipLaunchKernelGGL(dequantize_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), x_fp8,
-                     n, scale_inv, out_dtype == DSA_DTYPE_BF16 ? 1 : 0, out);
+                     n, scale_inv, block, out_dtype == DSA_DTYPE_BF16 ? 1 : 0, out);
   return check_launch("fp8_dequantize");
+}
+
+extern "C" int dsa_fp8_dequantize(const uint8_t *x_fp8, int64_t n, const float *scale_inv, void *out,
+                                  int out_dtype, void *stream) {
+  return dequantize(x_fp8, n, scale_inv, 0, out, out_dtype, stream);
+}
+
+extern "C" int dsa_fp8_dequantize_blockwise(const uint8_t *x_fp8, int64_t n, int64_t block, const float *scales,
+                                            void *out, int out_dtype, void *stream) {
+  DSA_REQUIRE(block > 0 && block % 4 == 0, "dsa_fp8_dequantize_blockwise: block %lld is not a positive multiple of 4",
+              (long long)block);
+  return dequantize(x_fp8, n, scales, block, out, out_dtype, stream);
 }

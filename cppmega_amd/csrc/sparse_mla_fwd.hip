@@ -31,13 +31,13 @@
 
 namespace dsa {
 
-template <int D_QK, int D_V, bool FP8>
+template <int D_QK, int D_V, bool FP8, bool MX = false>
 struct FwdCfg {
-  using Gat = GatherCfg<D_QK, D_V, FP8>;
+  using Gat = GatherCfg<D_QK, D_V, FP8, MX>;
   static constexpr int KL_BYTES = 32 * Gat::KL_STRIDE;
   static constexpr int KD_STRIDE = D_V * 2 + 32;          // e4m3: dequantised V rows (bf16)
   static constexpr int KD_BYTES = FP8 ? 32 * KD_STRIDE : 0;
-  static constexpr int SC_BYTES = FP8 ? 32 * 4 : 0;
+  static constexpr int SC_BYTES = FP8 ? (MX ? Gat::NBLK : 1) * 32 * 4 : 0;
   static constexpr int WAVE_BYTES = (KL_BYTES + KD_BYTES + SC_BYTES + 15) / 16 * 16;
   // bf16 source of the V^T operand: the raw tile, or the dequantised one for e4m3
   static constexpr int V_STRIDE = FP8 ? KD_STRIDE : Gat::KL_STRIDE;
@@ -46,10 +46,10 @@ struct FwdCfg {
   static_assert(D_V % 32 == 0 && D_QK % 16 == 0 && D_V <= D_QK, "unsupported head dims");
 };
 
-template <int D_QK, int D_V, bool FP8>
+template <int D_QK, int D_V, bool FP8, bool MX = false>
 __global__ void __launch_bounds__(256)
 sparse_mla_fwd_kernel(const FwdParams p) {
-  using C = FwdCfg<D_QK, D_V, FP8>;
+  using C = FwdCfg<D_QK, D_V, FP8, MX>;
   using Gat = typename C::Gat;
   typedef typename std::conditional<FP8, long, bf16x8>::type qop_t;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -78,7 +78,10 @@ sparse_mla_fwd_kernel(const FwdParams p) {
   const int64_t qrow = tok * p.H + g * p.hpg + h_local;
   const int32_t *idx_row = p.idx + (tok * p.G + g) * p.topk;
   const unsigned char *kv_b = p.kv + ((b * p.S_kv) * p.G + g) * Gat::ROWB;
-  const float *kv_scale_b = FP8 ? p.kv_scale + b * p.S_kv : nullptr;
+  // kv scales: [B, S_kv] per row, or MX [B, S_kv, G, D_QK / 32] per (row, block)
+  const float *kv_scale_b = !FP8 ? nullptr : (MX ? p.kv_scale + ((b * p.S_kv) * p.G + g) * Gat::NBLK
+                                                 : p.kv_scale + b * p.S_kv);
+  const uint32_t sc_pitch = MX ? (uint32_t)(p.G * Gat::NBLK * 4) : 4u;
   const uint32_t row_pitch = (uint32_t)(p.G * Gat::ROWB);
   const int nblk = (int)((p.topk + 31) / 32);
 
@@ -87,9 +90,9 @@ sparse_mla_fwd_kernel(const FwdParams p) {
   int idx_cur = slot_index(load_slot_raw(idx_rs, 0, l32), 0, l32, p.topk, p.S_kv);
   int raw_nxt = load_slot_raw(idx_rs, 1, l32);
   const auto kv_rs = make_buffer_rsrc(kv_b, (uint32_t)(p.S_kv * (int64_t)row_pitch));
-  const auto sc_rs = make_buffer_rsrc(kv_scale_b, FP8 ? (uint32_t)(p.S_kv * 4) : 0u);
+  const auto sc_rs = make_buffer_rsrc(kv_scale_b, FP8 ? (uint32_t)(p.S_kv * sc_pitch) : 0u);
   typename Gat::Regs rg;
-  gather_issue<Gat>(rg, kv_rs, sc_rs, idx_cur, row_pitch);
+  gather_issue<Gat>(rg, kv_rs, sc_rs, idx_cur, row_pitch, sc_pitch);
 
   // Q as the B operand: lane = head, 8 consecutive d per k-step, through a
   // resource that ends at the tile's last head (padded heads read zeros), so
@@ -109,8 +112,14 @@ sparse_mla_fwd_kernel(const FwdParams p) {
     }
   }
   float qsc = 1.0f;
-  if constexpr (FP8) qsc = p.q_scale[tok];
+  if constexpr (FP8 && !MX) qsc = p.q_scale[tok];
   const float tscale = p.sl2 * qsc;
+  // MX: this lane's head's block scales (q_scale [B, S, H, D_QK / 32])
+  float qbs[MX ? Gat::NBLK : 1];
+  if constexpr (MX) {
+#pragma unroll
+    for (int c = 0; c < Gat::NBLK; ++c) qbs[c] = head_ok ? p.q_scale[qrow * Gat::NBLK + c] : 0.0f;
+  }
 
   float m_run = kNegBig, l_run = 0.0f;
   f32x16 oacc[C::DT];
@@ -132,14 +141,35 @@ sparse_mla_fwd_kernel(const FwdParams p) {
     // (issued unconditionally, past the last block too, so every wait is counted exactly)
     const int raw_nn = load_slot_raw(idx_rs, blk + 2, l32);
     const int idx_nxt = slot_index(raw_nxt, blk + 1, l32, p.topk, p.S_kv);
-    gather_issue<Gat>(rg, kv_rs, sc_rs, idx_nxt, row_pitch);
+    gather_issue<Gat>(rg, kv_rs, sc_rs, idx_nxt, row_pitch, sc_pitch);
 
     // ---- S^T = K Q^T  (M = slot, N = head, K = d) ----
     f32x16 sacc;
 #pragma unroll
     for (int a = 0; a < 16; ++a) sacc[a] = 0.0f;
+    if constexpr (MX) {
+      // per 32-channel block: a partial product on the codes, then
+      // S += partial * kv_scale[slot][block] * q_scale[head][block]
 #pragma unroll
-    for (int k = 0; k < C::KSTEPS; ++k) {
+      for (int c = 0; c < Gat::NBLK; ++c) {
+        f32x16 part;
+#pragma unroll
+        for (int a = 0; a < 16; ++a) part[a] = 0.0f;
+#pragma unroll
+        for (int k = 2 * c; k < 2 * c + 2; ++k) {
+          const long a = *reinterpret_cast<const long *>(Kl + l32 * Gat::KL_STRIDE + 16 * k + 8 * g32);
+          part = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(a, qreg[k], part, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const f32x4 k4 = *reinterpret_cast<const f32x4 *>(Ksc + c * 32 + 8 * i + 4 * g32);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) sacc[4 * i + j] = fmaf(part[4 * i + j], k4[j] * qbs[c], sacc[4 * i + j]);
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < (MX ? 0 : C::KSTEPS); ++k) {
       if constexpr (FP8) {
         const long a = *reinterpret_cast<const long *>(Kl + l32 * Gat::KL_STRIDE + 16 * k + 8 * g32);
         sacc = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(a, qreg[k], sacc, 0, 0, 0);
@@ -162,14 +192,14 @@ sparse_mla_fwd_kernel(const FwdParams p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float ksc4[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-      if constexpr (FP8) {
+      if constexpr (FP8 && !MX) {
         const f32x4 s4 = *reinterpret_cast<const f32x4 *>(Ksc + 8 * i + 4 * g32);
         ksc4[0] = s4[0]; ksc4[1] = s4[1]; ksc4[2] = s4[2]; ksc4[3] = s4[3];
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float v = sacc[4 * i + j];
-        if constexpr (FP8) v *= ksc4[j];
+        if constexpr (FP8 && !MX) v *= ksc4[j];
         xs[4 * i + j] = v;  // raw score, scaled inside the exp
       }
     }
@@ -236,19 +266,19 @@ sparse_mla_fwd_kernel(const FwdParams p) {
   }
 }
 
-template <int D_QK, int D_V, bool FP8>
+template <int D_QK, int D_V, bool FP8, bool MX = false>
 static int launch_fwd(const FwdParams &p, hipStream_t st) {
-  using C = FwdCfg<D_QK, D_V, FP8>;
+  using C = FwdCfg<D_QK, D_V, FP8, MX>;
   const size_t lds = 4 * (size_t)C::WAVE_BYTES;
   if (lds > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void *)sparse_mla_fwd_kernel<D_QK, D_V, FP8>,
+    hipError_t e = hipFuncSetAttribute((const void *)sparse_mla_fwd_kernel<D_QK, D_V, FP8, MX>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return set_error(DSA_ERR_HIP, "sparse_mla_fwd: LDS attribute: %s", hipGetErrorString(e));
   }
   const int64_t nitems = p.B * p.S * p.G * p.ntiles;
   const int64_t nblocks = (nitems + 3) / 4;
   if (nitems >= (1ll << 31)) return set_error(DSA_ERR_INVALID_ARG, "sparse_mla_fwd: grid too large");
-  hipLaunchKernelGGL((sparse_mla_fwd_kernel<D_QK, D_V, FP8>), dim3((unsigned)nblocks), dim3(256), lds, st, p);
+  hipLaunchKernelGGL((sparse_mla_fwd_kernel<D_QK, D_V, FP8, MX>), dim3((unsigned)nblocks), dim3(256), lds, st, p);
   return check_launch("sparse_mla_fwd");
 }
 
@@ -267,11 +297,12 @@ extern "C" int dsa_sparse_mla_fwd(const void *q, const void *kv, const int32_t *
   DSA_REQUIRE(H % G == 0, "dsa_sparse_mla_fwd: H=%lld not divisible by G=%lld", (long long)H, (long long)G);
   DSA_REQUIRE(D_v > 0 && D_v <= D_qk, "dsa_sparse_mla_fwd: need 0 < d_v <= d_qk (got %lld, %lld)",
               (long long)D_v, (long long)D_qk);
-  DSA_REQUIRE(dtype == DSA_DTYPE_BF16 || dtype == DSA_DTYPE_E4M3, "dsa_sparse_mla_fwd: dtype %d", dtype);
+  DSA_REQUIRE(dtype == DSA_DTYPE_BF16 || dtype == DSA_DTYPE_E4M3 || dtype == DSA_DTYPE_MXFP8,
+              "dsa_sparse_mla_fwd: dtype %d", dtype);
   DSA_REQUIRE(S_kv < (1ll << 31) && topk < (1ll << 31), "dsa_sparse_mla_fwd: S_kv/topk too large");
   if (B == 0 || S == 0) return DSA_OK;
   DSA_REQUIRE(q && kv && indices && out && lse2, "dsa_sparse_mla_fwd: null tensor pointer");
-  if (dtype == DSA_DTYPE_E4M3)
+  if (dtype == DSA_DTYPE_E4M3 || dtype == DSA_DTYPE_MXFP8)
     DSA_REQUIRE(q_scale && kv_scale, "dsa_sparse_mla_fwd: e4m3 input needs q_scale and kv_scale");
   FwdParams p;
   p.q = static_cast<const unsigned char *>(q);
@@ -293,6 +324,13 @@ extern "C" int dsa_sparse_mla_fwd(const void *q, const void *kv, const int32_t *
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool f8 = dtype == DSA_DTYPE_E4M3;
   DSA_REQUIRE(S_kv * G * D_qk * 2 < (1ll << 32), "dsa_sparse_mla_fwd: kv rows of one batch exceed 4 GiB");
+  if (dtype == DSA_DTYPE_MXFP8) {  // e4m3 with one scale per 32 channels of every row
+    if (D_qk == 128 && D_v == 64) return launch_fwd<128, 64, true, true>(p, st);
+    if (D_qk == 128 && D_v == 128) return launch_fwd<128, 128, true, true>(p, st);
+    if (D_qk == 192 && D_v == 128) return launch_fwd<192, 128, true, true>(p, st);
+    return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_fwd: no MXFP8 kernel for d_qk=%lld d_v=%lld",
+                     (long long)D_qk, (long long)D_v);
+  }
   if (wide_shape(D_qk, D_v)) return launch_fwd_wide(p, D_qk, D_v, f8, st);
   if (D_qk == 128 && D_v == 64) return f8 ? launch_fwd<128, 64, true>(p, st) : launch_fwd<128, 64, false>(p, st);
   if (D_qk == 128 && D_v == 128) return f8 ? launch_fwd<128, 128, true>(p, st) : launch_fwd<128, 128, false>(p, st);

@@ -16,11 +16,15 @@
 
 namespace dsa {
 
-template <int D_QK, int D_V, bool FP8>
+// MX: e4m3 rows with one f32 scale per 32 consecutive channels (MXFP8 block
+// scaling) instead of one scale per row.
+template <int D_QK, int D_V, bool FP8, bool MX = false>
 struct GatherCfg {
   static constexpr int kDqk = D_QK;
   static constexpr int kDv = D_V;
   static constexpr bool kFp8 = FP8;
+  static constexpr bool kMx = MX;
+  static constexpr int NBLK = D_QK / 32;           // MX scale blocks per row
   static constexpr int ELT = FP8 ? 1 : 2;          // bytes per element in HBM
   static constexpr int ROWB = D_QK * ELT;          // bytes per kv row
   static constexpr int CH = 16 / ELT;              // elements per 16-byte chunk
@@ -31,6 +35,7 @@ struct GatherCfg {
   static constexpr int KL_STRIDE = ROWB + 32;      // LDS row stride: a 32-byte pad puts the 4 rows of a
                                                    // transposed read in distinct banks
   static_assert(NCH * CH == D_QK && NCH_V * CH == D_V, "head dims must be whole 16-byte chunks");
+  static_assert(!MX || (FP8 && D_QK % 32 == 0), "MX block scales need e4m3 rows of whole 32-channel blocks");
   struct Regs {
     i32x4 v[UPL][4];
     float sc[UPL][4];
@@ -64,12 +69,14 @@ __device__ __forceinline__ int load_slot_index(const int32_t *idx_row, int blk, 
 
 // Rows are read through buffer resources: kv_rs covers the kv rows of this
 // (batch, kv group) (row r at byte r * row_pitch, row_pitch = G * ROWB), sc_rs
-// their e4m3 scales.  A masked slot reads at an offset past the resource, which
+// their e4m3 scales (row r at byte r * sc_pitch; MX: the scale of 16-byte
+// chunk c is block c / 2 of the row, 4 bytes apart).  A masked slot reads at an offset past the resource, which
 // the hardware answers with zeros, so masked rows (and their scales) arrive as
 // zeros without selects, and every load is issued on every path.
 template <class Gat>
 __device__ __forceinline__ void gather_issue(typename Gat::Regs &rg, __amdgpu_buffer_rsrc_t kv_rs,
-                                             __amdgpu_buffer_rsrc_t sc_rs, int my_idx, uint32_t row_pitch) {
+                                             __amdgpu_buffer_rsrc_t sc_rs, int my_idx, uint32_t row_pitch,
+                                             uint32_t sc_pitch = 4u) {
   const int lane = lane_id();
 #pragma unroll
   for (int uu = 0; uu < Gat::UPL; ++uu) {
@@ -82,8 +89,10 @@ __device__ __forceinline__ void gather_issue(typename Gat::Regs &rg, __amdgpu_bu
       const bool ok = ri >= 0 && u < Gat::UNITS;
       const uint32_t off = ok ? (uint32_t)ri * row_pitch + (uint32_t)c * 16u : 0xffffffffu;
       rg.v[uu][r] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(kv_rs, (int)off, 0, 0));
-      if constexpr (Gat::kFp8)
-        rg.sc[uu][r] = buffer_load_f32(sc_rs, ok ? (int)((uint32_t)ri * 4u) : (int)0xffffffffu, 0);
+      if constexpr (Gat::kFp8) {
+        const uint32_t so = (uint32_t)ri * sc_pitch + (Gat::kMx ? (uint32_t)(c / 2) * 4u : 0u);
+        rg.sc[uu][r] = buffer_load_f32(sc_rs, ok ? (int)so : (int)0xffffffffu, 0);
+      }
     }
   }
 }
@@ -133,7 +142,8 @@ __device__ __forceinline__ void gather_store_dequant(const typename Gat::Regs &r
   }
 }
 
-// e4m3 only: per-slot kv dequant scale (0 for masked slots).
+// e4m3 only: per-slot kv dequant scale (0 for masked slots); MX: per (block,
+// slot), block-major (Ksc[block * 32 + slot]).
 template <class Gat>
 __device__ __forceinline__ void gather_store_scale(const typename Gat::Regs &rg, float *Ksc) {
   const int lane = lane_id();
@@ -142,9 +152,10 @@ __device__ __forceinline__ void gather_store_scale(const typename Gat::Regs &rg,
     const int u = lane + 64 * uu;
     if (u >= Gat::UNITS) break;
     const int c = u % Gat::NCH, quad = u / Gat::NCH;
-    if (c == 0) {
+    if (Gat::kMx ? (c % 2 == 0) : (c == 0)) {
+      float *dst = Gat::kMx ? Ksc + (c / 2) * 32 : Ksc;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Ksc[quad * 4 + r] = rg.sc[uu][r];
+      for (int r = 0; r < 4; ++r) dst[quad * 4 + r] = rg.sc[uu][r];
     }
   }
 }

@@ -12,6 +12,12 @@ from .sparse_mla import (
     sparse_mla_as_unfused_dsa,
     sparse_mla_fp8_as_unfused_dsa,
 )
+from .sparse_mla_blockscaled import (
+    mxfp8_dequantize,
+    sparse_mla_blockscaled_mxfp8_backward,
+    sparse_mla_blockscaled_mxfp8_forward,
+    sparse_mla_blockscaled_mxfp8_fwd_interface,
+)
 from .sparse_mla_bwd import sparse_mla_bwd
 from .sparse_mla_bwd_fp8 import sparse_mla_bwd_fp8
 from .sparse_mla_fwd import sparse_mla_fwd_interface
@@ -22,8 +28,12 @@ __all__ = [
     "SparseMLA_FP8",
     "apply_sparse_mla_patch",
     "fused_sparse_mla_absorbed_fp8",
+    "mxfp8_dequantize",
     "per_token_cast_to_fp8",
     "sparse_mla_as_unfused_dsa",
+    "sparse_mla_blockscaled_mxfp8_backward",
+    "sparse_mla_blockscaled_mxfp8_forward",
+    "sparse_mla_blockscaled_mxfp8_fwd_interface",
     "sparse_mla_bwd",
     "sparse_mla_bwd_fp8",
     "sparse_mla_fp8_as_unfused_dsa",

@@ -39,7 +39,8 @@ enum dsa_dtype {
   DSA_DTYPE_E4M3 = 1,        /* OCP float8 e4m3fn (max 448), gfx950 native   */
   DSA_DTYPE_F32 = 2,         /* float32                                      */
   DSA_DTYPE_I32 = 3,         /* int32 (index tensors)                        */
-  DSA_DTYPE_I64 = 4          /* int64 (index tensors)                        */
+  DSA_DTYPE_I64 = 4,         /* int64 (index tensors)                        */
+  DSA_DTYPE_MXFP8 = 5        /* e4m3 with one f32 scale per 32 channels      */
 };
 
 /* Per-thread message for the last non-zero status returned on this thread. */
@@ -66,6 +67,14 @@ int dsa_device_check(int device);
  *   lse2    [B, S, H]            f32 (log2 units)
  *   q_scale [B, S], kv_scale [B, S_kv]  f32 dequant factors (real = fp8 * scale),
  *                                 required for e4m3, ignored (may be NULL) for bf16.
+ * dtype DSA_DTYPE_MXFP8 (block-scaled e4m3): q / kv e4m3 with
+ *   q_scale [B, S, H, D_qk / 32], kv_scale [B, S_kv, G, D_qk / 32], one f32
+ *   factor per 32 consecutive channels; each block's q.k over the codes is
+ *   multiplied by q_scale[block] * kv_scale[block] before the blocks are
+ *   summed, and V is dequantised per block to bf16.  Replaces the block-scaled
+ *   forward sparse_mla_blockscaled_mxfp8_fwd_interface
+ *   (cppmega/megatron/sparse_mla_ops/tilelang_sparse_mla_blockscaled_fused.py:248-418,694-793).
+ *   (d_qk, d_v) in {(128, 64), (128, 128), (192, 128)}.
  * Head h reads kv group h / (H / G).  sm_scale multiplies the raw q.k dot.
  */
 int dsa_sparse_mla_fwd(const void *q, const void *kv, const int32_t *indices,
@@ -180,6 +189,17 @@ int dsa_fp8_tensorwise_quantize(const void *x, int64_t n, int in_dtype,
  */
 int dsa_fp8_dequantize(const uint8_t *x_fp8, int64_t n, const float *scale_inv,
                        void *out, int out_dtype, void *stream);
+
+/*
+ * Block-scaled e4m3 dequantisation: out[i] = value(x_fp8[i]) * scales[i / block]
+ * (block a positive multiple of 4; 32 for MXFP8 rows).  Replaces
+ *   _dequantize_mxfp8_tensor (cppmega/megatron/sparse_mla_ops/tilelang_sparse_mla_blockscaled_fused.py:961-969),
+ *   which the reference's block-scaled backward runs before a bf16 backward.
+ *   x_fp8 [n] e4m3, scales [n / block] f32, out [n] bf16 (RNE) or f32.
+ */
+int dsa_fp8_dequantize_blockwise(const uint8_t *x_fp8, int64_t n, int64_t block,
+                                 const float *scales, void *out, int out_dtype,
+                                 void *stream);
 
 /*
  * DSA indexer KL loss (the indexer's training signal):

@@ -219,3 +219,85 @@ __all__ = [
     "LOG2E", "sparse_mla_fwd", "sparse_mla_bwd", "sparse_mla_autograd_f64",
     "delta_f32", "flops_fwd", "flops_bwd",
 ]
+
+
+# ---------------------------------------------------------------------------
+# MXFP8 block-scaled forward
+# ---------------------------------------------------------------------------
+MX_BLOCK = 32
+
+
+def mxfp8_quantize(x, block=MX_BLOCK):
+    """OCP Microscaling (MX v1.0) E4M3 quantisation along the last dim: per block
+    of `block` elements the shared scale is 2^(floor(log2(amax)) - 8) (8 = the
+    largest e4m3 exponent), elements are x / scale cast to e4m3fn with
+    round-to-nearest-even, saturating at +-448; an all-zero block has scale 1.
+    Returns (data e4m3fn [..., D], scale f32 [..., D / block]).  The reference
+    probe quantises with quack's to_mx (not vendored): its exact scale rule is
+    parity unpinned here; the kernels take any f32 block scales."""
+    xf = x.float()
+    shp = xf.shape
+    blocks = xf.reshape(*shp[:-1], shp[-1] // block, block)
+    amax = blocks.abs().amax(-1)
+    exp = torch.where(amax > 0, torch.floor(torch.log2(amax.clamp_min(1e-38))) - 8, torch.zeros_like(amax))
+    scale = torch.exp2(exp)
+    data = (blocks / scale[..., None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return data.reshape(shp), scale.float()
+
+
+def dequantize_blockwise(data, scale, block=MX_BLOCK, out_dtype=torch.bfloat16):
+    """value * scale[block], as _dequantize_mxfp8_tensor
+    (cppmega/megatron/sparse_mla_ops/tilelang_sparse_mla_blockscaled_fused.py:961-969)."""
+    shp = data.shape
+    v = data.float().reshape(*shp[:-1], shp[-1] // block, block) * scale.float()[..., None]
+    return v.reshape(shp).to(out_dtype)
+
+
+def sparse_mla_fwd_mxfp8(q8, kv8, q_scale, kv_scale, indices, sm_scale=None, d_v=None, chunk=256):
+    """MXFP8 block-scaled SparseMLA forward, restating the reference kernel
+    sparse_mla_blockscaled_mxfp8_fwd (tilelang_sparse_mla_blockscaled_fused.py:337-415):
+    for every 32-channel block the q.k product over the e4m3 codes is scaled by
+    q_scale[b,s,h,blk] * kv_scale[b,row,g,blk] and summed over blocks; exp2
+    softmax; V = bf16(code * kv_scale[row, d // 32]); P rounded to bf16; LSE in
+    log2 units.  q8 [B,S,H,D], kv8 [B,S_kv,G,D] e4m3fn, scales f32 [..., D/32].
+    Returns (out fp32 [B,S,H,d_v], lse2 [B,S,H])."""
+    B, S, H, D = q8.shape
+    _, Skv, G, _ = kv8.shape
+    nb = D // MX_BLOCK
+    d_v = D if d_v is None else int(d_v)
+    hpg = H // G
+    scale = _default_scale(sm_scale, D)
+    sl2 = scale * LOG2E
+    out = torch.zeros(B, S, H, d_v, dtype=torch.float32)
+    lse = torch.full((B, S, H), float("-inf"), dtype=torch.float32)
+    qf = q8.float().reshape(B, S, H, nb, MX_BLOCK)
+    for b in range(B):
+        for g in range(G):
+            kv_bg = kv8[b, :, g, :].float()                          # [Skv, D]
+            ks_bg = kv_scale[b, :, g, :].float()                     # [Skv, nb]
+            for s0 in range(0, S, chunk):
+                s1 = min(S, s0 + chunk)
+                idx = indices[b, s0:s1, g, :]
+                rows, valid = _gather_rows(kv_bg, idx, Skv)          # [T,k,D]
+                safe = torch.where(valid, idx, torch.zeros_like(idx)).long()
+                ks = ks_bg[safe]                                     # [T,k,nb]
+                qs = q_scale[b, s0:s1, g * hpg:(g + 1) * hpg, :].float()  # [T,h,nb]
+                qb = qf[b, s0:s1, g * hpg:(g + 1) * hpg]             # [T,h,nb,32]
+                rb = rows.reshape(*rows.shape[:2], nb, MX_BLOCK)     # [T,k,nb,32]
+                part = torch.einsum("thcd,tkcd->thkc", qb, rb)       # per-block partials
+                s = (part * qs[:, :, None, :] * ks[:, None, :, :]).sum(-1)   # [T,h,k]
+                vblk = rows[..., :d_v].reshape(*rows.shape[:2], d_v // MX_BLOCK, MX_BLOCK)
+                vrows = _bf16r((vblk * ks[..., : d_v // MX_BLOCK, None]).reshape(*rows.shape[:2], d_v))
+                s = s.masked_fill(~valid[:, None, :], float("-inf"))
+                m = s.amax(-1, keepdim=True)
+                m_safe = torch.where(torch.isfinite(m), m, torch.zeros_like(m))
+                p = torch.exp2((s - m_safe) * sl2)
+                sumexp = p.sum(-1)
+                o = torch.bmm(_bf16r(p), vrows)
+                nz = sumexp > 0
+                o = torch.where(nz[..., None], o / sumexp.clamp_min(1e-38)[..., None], torch.zeros_like(o))
+                l2 = torch.where(nz, torch.log2(sumexp.clamp_min(1e-38)) + m_safe[..., 0] * sl2,
+                                 torch.full_like(sumexp, float("-inf")))
+                out[b, s0:s1, g * hpg:(g + 1) * hpg] = o
+                lse[b, s0:s1, g * hpg:(g + 1) * hpg] = l2
+    return out, lse

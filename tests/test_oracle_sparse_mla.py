@@ -229,3 +229,68 @@ def test_flop_conventions():
     # cfg2 figures quoted by the reference's benchmark scripts
     assert osm.flops_fwd(2, 4096, 32, 256, 128, 64) == 25_769_803_776
     assert osm.flops_bwd(2, 4096, 32, 256, 128, 64) == 68_719_476_736
+
+
+# ---------------------------------------------------------------------------
+# MXFP8 block-scaled forward
+# ---------------------------------------------------------------------------
+def _mx_inputs(B=1, S=24, H=16, D=128, G=1, K=20, seed=5):
+    from cppmega_amd import synthetic
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn((B, S, H, D), generator=g)
+    kv = torch.randn((B, S, G, D), generator=g)
+    idx = synthetic.causal_indices(B, S, K, seed=seed + 1).expand(B, S, G, K).contiguous()
+    return q, kv, idx
+
+
+def test_mxfp8_uniform_block_scales_equal_tensorwise():
+    """Equal scales in every block reduce the block-scaled forward to the
+    tensorwise FP8 forward (pinned separately) with those scales."""
+    q, kv, idx = _mx_inputs()
+    q8 = q.clamp(-400, 400).to(torch.float8_e4m3fn)
+    kv8 = kv.clamp(-400, 400).to(torch.float8_e4m3fn)
+    B, S, H, D = q.shape
+    qs, ks = 0.37, 1.9
+    qsb = torch.full((B, S, H, D // 32), qs)
+    ksb = torch.full((B, S, 1, D // 32), ks)
+    o_mx, l_mx = osm.sparse_mla_fwd_mxfp8(q8, kv8, qsb, ksb, idx, 0.1, 64)
+    o_t, l_t = osm.sparse_mla_fwd(q8, kv8, idx, 0.1, 64, q_scale=torch.full((B, S), qs),
+                                  kv_scale=torch.full((B, S), ks))
+    assert torch.allclose(o_mx, o_t, atol=1e-6, rtol=1e-5) and torch.allclose(l_mx, l_t, atol=1e-5)
+
+
+def test_mxfp8_power_of_two_scales_equal_bf16_on_dequantised_inputs():
+    """With power-of-two (MX) scales the dequantised values are exact in bf16, so
+    the block-scaled forward equals the bf16 forward on the dequantised tensors
+    (scores up to fp32 summation order)."""
+    q, kv, idx = _mx_inputs(G=2, H=32)
+    q8, qs = osm.mxfp8_quantize(q)
+    kv8, ks = osm.mxfp8_quantize(kv)
+    o_mx, l_mx = osm.sparse_mla_fwd_mxfp8(q8, kv8, qs, ks, idx, 0.09, 64)
+    qd = osm.dequantize_blockwise(q8, qs)
+    kvd = osm.dequantize_blockwise(kv8, ks)
+    assert torch.equal(qd.float(), osm.dequantize_blockwise(q8, qs, out_dtype=torch.float32))  # exact in bf16
+    o_b, l_b = osm.sparse_mla_fwd(qd, kvd, idx, 0.09, 64)
+    assert torch.allclose(o_mx, o_b, atol=2e-6, rtol=1e-5) and torch.allclose(l_mx, l_b, atol=2e-5)
+
+
+def test_mxfp8_block_scale_placement_is_pinned():
+    """Planted mistake: scaling every block by block 0's kv scale changes the result."""
+    q, kv, idx = _mx_inputs()
+    q8, qs = osm.mxfp8_quantize(q * torch.linspace(0.1, 10, 128))
+    kv8, ks = osm.mxfp8_quantize(kv * torch.linspace(10, 0.1, 128))
+    o, _ = osm.sparse_mla_fwd_mxfp8(q8, kv8, qs, ks, idx, 0.09, 64)
+    o_bad, _ = osm.sparse_mla_fwd_mxfp8(q8, kv8, qs, ks[..., :1].expand_as(ks).contiguous(), idx, 0.09, 64)
+    assert not torch.allclose(o, o_bad, atol=1e-2)
+
+
+def test_mxfp8_quantizer_closed_form():
+    """Shared exponent floor(log2 amax) - 8: a block with amax 3.0 gets scale 2^-7;
+    values that are e4m3-representable multiples of the scale round-trip exactly."""
+    x = torch.zeros(1, 64)
+    x[0, :32] = torch.tensor([3.0, -1.5, 0.75, 2.0 ** -6] + [0.0] * 28)
+    x[0, 32:] = 0.0
+    d, s = osm.mxfp8_quantize(x)
+    assert float(s[0, 0]) == 2.0 ** -7 and float(s[0, 1]) == 1.0
+    back = osm.dequantize_blockwise(d, s, out_dtype=torch.float32)
+    assert torch.equal(back, x)
