@@ -75,6 +75,8 @@ def cfg5_work():
     s = C5_S
     return {
         "fwd": (2 * s * C5_H * C5_TOPK * (C5_DQK + C5_DV), 0, "bf16"),
+        # block-scaled forward: Q K^T on e4m3 codes, PV in bf16
+        "fwd_mxfp8": ((2 * s * C5_H * C5_TOPK * C5_DQK, 2 * s * C5_H * C5_TOPK * C5_DV), 0, "fp8+bf16"),
         "indexer_fp8": (2 * C5_HIDX * C5_DIDX * s * (s + 1) // 2, 0, "fp8"),
         "topk": (0, 4 * s * (s + 1) // 2 + 4 * s * C5_TOPK, None),
     }
@@ -82,14 +84,16 @@ def cfg5_work():
 
 def measure_cfg5(dev, reps=3):
     """Median kernel times of the cfg5 forward (h=128, d_qk=576, d_v=512,
-    topk=2048, bf16), the e4m3 indexer (h=64, d=128, causal) and the top-2048
-    selection over s=16384, on inputs generated on the device with a fixed
-    seed.  Each figure is the median of `reps` event-timed launches."""
+    topk=2048, bf16), its MXFP8 block-scaled form (e4m3 q/kv with one f32
+    scale per 32 channels), the e4m3 indexer (h=64, d=128, causal) and the
+    top-2048 selection over s=16384, on inputs generated on the device with a
+    fixed seed.  Each figure is the median of `reps` event-timed launches."""
     import torch
 
     from cppmega_amd.dsa_indexer_fused_patch import CAUSAL_LOWER, index_scores
     from cppmega_amd.dsa_topk import topk_indices
-    from cppmega_amd.sparse_mla_ops import sparse_mla_fwd_interface, tensorwise_quantize
+    from cppmega_amd.sparse_mla_ops import (sparse_mla_blockscaled_mxfp8_fwd_interface, sparse_mla_fwd_interface,
+                                            tensorwise_quantize)
 
     gen = torch.Generator(device=dev).manual_seed(5)
     S5 = C5_S
@@ -112,6 +116,14 @@ def measure_cfg5(dev, reps=3):
     ik8, iks = tensorwise_quantize(ik)
     del iq, ik
     scores = torch.empty((1, S5, S5), dtype=torch.float32, device=dev)
+    # MXFP8 payloads: the e4m3 cast of the same q / kv over a power-of-two scale per 32 channels
+    qbs = torch.exp2(torch.randint(-6, 0, (1, S5, C5_H, C5_DQK // 32), generator=gen, device=dev).float())
+    kbs = torch.exp2(torch.randint(-6, 0, (1, S5, 1, C5_DQK // 32), generator=gen, device=dev).float())
+    qmx = torch.empty(q.shape, dtype=torch.float8_e4m3fn, device=dev)
+    for t0 in range(0, S5, 2048):  # bounded f32 temporaries
+        qmx[:, t0:t0 + 2048] = (q[:, t0:t0 + 2048].float() / qbs[:, t0:t0 + 2048].repeat_interleave(32, dim=-1)
+                                ).clamp(-448, 448).to(torch.float8_e4m3fn)
+    kmx = (kv.float() / kbs.repeat_interleave(32, dim=-1)).clamp(-448, 448).to(torch.float8_e4m3fn)
 
     def timed(fn):
         fn()
@@ -128,6 +140,8 @@ def measure_cfg5(dev, reps=3):
 
     t = {
         "fwd": timed(lambda: sparse_mla_fwd_interface(q, kv, idx, sm_scale=C5_DQK ** -0.5, d_v=C5_DV)),
+        "fwd_mxfp8": timed(lambda: sparse_mla_blockscaled_mxfp8_fwd_interface(qmx, kmx, qbs, kbs, idx,
+                                                                              sm_scale=C5_DQK ** -0.5, d_v=C5_DV)),
         "indexer_fp8": timed(lambda: index_scores(iq8, iw, ik8, use_relu=True, causal=CAUSAL_LOWER,
                                                   q_scale=iqs, k_scale=iks, out=scores)),
         "topk": timed(lambda: topk_indices(scores, C5_TOPK, causal=True)),
@@ -135,7 +149,11 @@ def measure_cfg5(dev, reps=3):
     res = {}
     for k, (fl, by, kind) in cfg5_work().items():
         e = {"ms": round(t[k] * 1e3, 3)}
-        if fl:
+        if kind == "fp8+bf16":
+            floor = fl[0] / (PEAK_FP8_TFLOPS * 1e12) + fl[1] / (PEAK_BF16_TFLOPS * 1e12)
+            e.update({"bound": "mfma (fp8 + bf16)", "tflops": round(sum(fl) / t[k] / 1e12, 1),
+                      "floor_us": round(floor * 1e6, 1), "frac": round(floor / t[k], 4)})
+        elif fl:
             peak = PEAK_FP8_TFLOPS if kind == "fp8" else PEAK_BF16_TFLOPS
             tf = fl / t[k] / 1e12
             e.update({"bound": "mfma", "tflops": round(tf, 1), "peak": peak, "frac": round(tf / peak, 4)})
@@ -143,7 +161,7 @@ def measure_cfg5(dev, reps=3):
             gbs = by / t[k] / 1e9
             e.update({"bound": "hbm", "gbs": round(gbs, 1), "peak": PEAK_HBM_GBS, "frac": round(gbs / PEAK_HBM_GBS, 4)})
         res[k] = e
-    del q, kv, idx, iq8, ik8, iw, scores
+    del q, kv, idx, iq8, ik8, iw, scores, qmx, kmx, qbs, kbs
     torch.cuda.empty_cache()
     return res
 
@@ -548,8 +566,8 @@ def main():
         "launch": ("hip_graph" if graph_info is not None else "eager"),
         "eager_tokens_per_s": round(eager_tokens_per_s, 1),
         "graph_replays_checked": (graph_info["checked"] if graph_info is not None else 0),
-        "cfg5": ({"workload": f"s={C5_S} h={C5_H} d_qk={C5_DQK} d_v={C5_DV} topk={C5_TOPK} SparseMLA fwd (bf16), "
-                              f"indexer h={C5_HIDX} d={C5_DIDX} e4m3 causal, top-{C5_TOPK}",
+        "cfg5": ({"workload": f"s={C5_S} h={C5_H} d_qk={C5_DQK} d_v={C5_DV} topk={C5_TOPK} SparseMLA fwd (bf16; fwd_mxfp8: "
+                              f"MXFP8 block-scaled), indexer h={C5_HIDX} d={C5_DIDX} e4m3 causal, top-{C5_TOPK}",
                   "kernels": cfg5} if cfg5 is not None else None),
         "cfg4": ({"workload": f"FP8 tensorwise SparseMLA fwd+bwd at cfg2 shapes (q/kv e4m3, 1% x20 outliers, "
                                f"QK^T on e4m3, other products bf16); mxfp8_fwd: the block-scaled (one f32 scale "

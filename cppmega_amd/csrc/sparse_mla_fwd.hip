@@ -328,6 +328,7 @@ extern "C" int dsa_sparse_mla_fwd(const void *q, const void *kv, const int32_t *
     if (D_qk == 128 && D_v == 64) return launch_fwd<128, 64, true, true>(p, st);
     if (D_qk == 128 && D_v == 128) return launch_fwd<128, 128, true, true>(p, st);
     if (D_qk == 192 && D_v == 128) return launch_fwd<192, 128, true, true>(p, st);
+    if (wide_shape(D_qk, D_v)) return launch_fwd_wide(p, D_qk, D_v, true, st, true);
     return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_fwd: no MXFP8 kernel for d_qk=%lld d_v=%lld",
                      (long long)D_qk, (long long)D_v);
   }

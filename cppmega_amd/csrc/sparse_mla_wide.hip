@@ -61,9 +61,11 @@ struct WideCfg {
 // Issue the loads of one block's 32 rows: thread t takes units t + 256 i,
 // unit u = chunk u % NCH of row u / NCH.  my_idx is the kv row of slot
 // (lane & 31) of this wave (-1: masked).
-template <class C, bool FP8>
+// kv_scale_b holds one scale per row (sc_pitch 1) or, MX, one per 32-channel
+// block of every row (sc_pitch floats apart): a unit loads its own block's.
+template <class C, bool FP8, bool MX = false>
 __device__ __forceinline__ void wide_issue(typename C::Regs &rg, const unsigned char *kv_b, const float *kv_scale_b,
-                                           int my_idx, uint32_t row_pitch) {
+                                           int my_idx, uint32_t row_pitch, uint32_t sc_pitch = 1u) {
   const int t = threadIdx.x;
   uint32_t valid = 0;
 #pragma unroll
@@ -77,7 +79,7 @@ __device__ __forceinline__ void wide_issue(typename C::Regs &rg, const unsigned 
     const uint32_t r = ok ? (uint32_t)ri : 0u;
     rg.v[i] = i32x4{0, 0, 0, 0};
     if (exists) rg.v[i] = ld_global_16(kv_b + r * row_pitch + c * 16);
-    if constexpr (FP8) rg.sc[i] = exists ? kv_scale_b[r] : 0.0f;
+    if constexpr (FP8) rg.sc[i] = exists ? kv_scale_b[r * sc_pitch + (MX ? (uint32_t)(c >> 1) : 0u)] : 0.0f;
     valid |= (ok ? 1u : 0u) << i;
   }
   rg.valid = valid;
@@ -85,8 +87,9 @@ __device__ __forceinline__ void wide_issue(typename C::Regs &rg, const unsigned 
 
 // Store the staged rows: raw bytes row-major into Kl (masked slots zero); for
 // e4m3 also the first NCH_D chunks dequantised to bf16 (value * kv_scale, RNE)
-// into Kd (row stride KD_STRIDE) and the per-slot scales into Ksc.
-template <class C, bool FP8, int NCH_D = C::NCH_V, int KD_STRIDE = C::KD_STRIDE>
+// into Kd (row stride KD_STRIDE) and the per-slot scales into Ksc (MX: the
+// per-(slot, block) scales, block-major Ksc[block * 32 + slot]).
+template <class C, bool FP8, int NCH_D = C::NCH_V, int KD_STRIDE = C::KD_STRIDE, bool MX = false>
 __device__ __forceinline__ void wide_store(const typename C::Regs &rg, unsigned char *Kl, unsigned char *Kd,
                                            float *Ksc) {
   const int t = threadIdx.x;
@@ -111,7 +114,11 @@ __device__ __forceinline__ void wide_store(const typename C::Regs &rg, unsigned 
           *reinterpret_cast<i32x4 *>(dst) = i32x4{(int)wd[0], (int)wd[1], (int)wd[2], (int)wd[3]};
           *reinterpret_cast<i32x4 *>(dst + 16) = i32x4{(int)wd[4], (int)wd[5], (int)wd[6], (int)wd[7]};
         }
-        if (c == 0) Ksc[row] = s;
+        if constexpr (MX) {
+          if ((c & 1) == 0) Ksc[(c >> 1) * 32 + row] = s;
+        } else if (c == 0) {
+          Ksc[row] = s;
+        }
       }
     }
   }
@@ -144,22 +151,56 @@ __device__ __forceinline__ void put_partial(float *dst, const f32x16 &acc) {
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
-template <int D_QK, int D_V, bool FP8>
+template <int D_QK, int D_V, bool FP8, bool MX = false>
 struct WideFwdLds {
   using C = WideCfg<D_QK, D_V, FP8>;
+  static constexpr int NBLK = D_QK / 32;  // MX scale blocks per row
   static constexpr int OFF_KL = 0;
   static constexpr int OFF_KD = OFF_KL + 32 * C::KL_STRIDE;
   static constexpr int OFF_SC = OFF_KD + (FP8 ? 32 * C::KD_STRIDE : 0);
-  static constexpr int OFF_SP = (OFF_SC + (FP8 ? 32 * 4 : 0) + 15) / 16 * 16;
+  static constexpr int OFF_SP = (OFF_SC + (FP8 ? (MX ? NBLK : 1) * 32 * 4 : 0) + 15) / 16 * 16;
   static constexpr int SP_W = 16 * 64;  // floats per wave's partial tile
   static constexpr int BYTES = OFF_SP + 4 * SP_W * 4;
 };
 
-template <int D_QK, int D_V, bool FP8>
+// MX partial scores of one wave over its k-steps [k0, k0 + KQ) of d_qk (k0 of
+// parity PAR): every 32-channel block (two k-steps; the wave's first or last
+// block may be a half that the neighbouring wave completes) accumulates a fresh
+// partial on the e4m3 codes, scaled by kv_scale[slot][block] * q_scale[head][block]
+// before it joins sacc.  The block scaling is linear, so the four waves'
+// partials still sum to the full score.
+template <class C, int PAR>
+__device__ __forceinline__ void mx_wave_scores(f32x16 &sacc, const unsigned char *Kl, const long (&qreg)[C::KQ],
+                                               const float (&qbs)[C::KQ / 2 + 1], const float *Ksc, int k0,
+                                               int l32, int g32) {
+  const int cb0 = (k0 - PAR) >> 1;  // first block this wave touches
+  f32x16 part;
+#pragma unroll
+  for (int a = 0; a < 16; ++a) part[a] = 0.0f;
+#pragma unroll
+  for (int k = 0; k < C::KQ; ++k) {
+    const long a = *reinterpret_cast<const long *>(Kl + l32 * C::KL_STRIDE + 16 * (k0 + k) + 8 * g32);
+    part = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(a, qreg[k], part, 0, 0, 0);
+    if (((k + PAR) & 1) || k == C::KQ - 1) {  // the block of k-step k0 + k ends here (for this wave)
+      const int cl = (k + PAR) >> 1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 k4 = *reinterpret_cast<const f32x4 *>(Ksc + (cb0 + cl) * 32 + 8 * i + 4 * g32);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sacc[4 * i + j] = fmaf(part[4 * i + j], k4[j] * qbs[cl], sacc[4 * i + j]);
+      }
+#pragma unroll
+      for (int a = 0; a < 16; ++a) part[a] = 0.0f;
+    }
+  }
+}
+
+template <int D_QK, int D_V, bool FP8, bool MX = false>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D_V <= 512 ? 2 : 1)))
 sparse_mla_fwd_wide_kernel(const FwdParams p) {
+  static_assert(!MX || FP8, "MX is an e4m3 mode");
   using C = WideCfg<D_QK, D_V, FP8>;
-  using L = WideFwdLds<D_QK, D_V, FP8>;
+  using L = WideFwdLds<D_QK, D_V, FP8, MX>;
   typedef typename std::conditional<FP8, long, bf16x8>::type qop_t;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
@@ -184,14 +225,17 @@ sparse_mla_fwd_wide_kernel(const FwdParams p) {
   const int64_t qrow = tok * p.H + g * p.hpg + h_local;
   const int32_t *idx_row = p.idx + (tok * p.G + g) * p.topk;
   const unsigned char *kv_b = p.kv + ((b * p.S_kv) * p.G + g) * C::ROWB;
-  const float *kv_scale_b = FP8 ? p.kv_scale + b * p.S_kv : nullptr;
+  // kv scales: [B, S_kv] per row, or MX [B, S_kv, G, D_QK / 32] per (row, block)
+  const float *kv_scale_b = !FP8 ? nullptr : (MX ? p.kv_scale + ((b * p.S_kv) * p.G + g) * L::NBLK
+                                                 : p.kv_scale + b * p.S_kv);
+  const uint32_t sc_pitch = MX ? (uint32_t)(p.G * L::NBLK) : 1u;
   const uint32_t row_pitch = (uint32_t)(p.G * C::ROWB);
   const int nblk = (int)((p.topk + 31) / 32);
 
   int idx_cur = load_slot_index(idx_row, 0, l32, p.topk, p.S_kv);
   int idx_nxt = load_slot_index(idx_row, 1, l32, p.topk, p.S_kv);
   typename C::Regs rg;
-  wide_issue<C, FP8>(rg, kv_b, kv_scale_b, idx_cur, row_pitch);
+  wide_issue<C, FP8, MX>(rg, kv_b, kv_scale_b, idx_cur, row_pitch, sc_pitch);
 
   // this wave's quarter of Q as the B operand: lane = head, 8 consecutive d per k-step
   const int k0 = w * C::KQ;
@@ -207,8 +251,18 @@ sparse_mla_fwd_wide_kernel(const FwdParams p) {
     }
   }
   float qsc = 1.0f;
-  if constexpr (FP8) qsc = p.q_scale[tok];
+  if constexpr (FP8 && !MX) qsc = p.q_scale[tok];
   const float tscale = p.sl2 * qsc;
+  // MX: this lane's head's scales of the blocks this wave's k-steps touch
+  // (q_scale [B, S, H, D_QK / 32])
+  const int par = (k0 & 1);
+  float qbs[C::KQ / 2 + 1];
+  if constexpr (MX) {
+    const int cb0 = (k0 - par) >> 1;
+#pragma unroll
+    for (int cl = 0; cl < C::KQ / 2 + 1; ++cl)
+      qbs[cl] = (head_ok && cb0 + cl < L::NBLK) ? p.q_scale[qrow * L::NBLK + cb0 + cl] : 0.0f;
+  }
 
   float m_run = kNegBig, l_run = 0.0f;
   f32x16 oacc[C::DTW];
@@ -218,18 +272,22 @@ sparse_mla_fwd_wide_kernel(const FwdParams p) {
     for (int a = 0; a < 16; ++a) oacc[t][a] = 0.0f;
 
   for (int blk = 0; blk < nblk; ++blk) {
-    wide_store<C, FP8>(rg, Kl, Kd, Ksc);
+    wide_store<C, FP8, C::NCH_V, C::KD_STRIDE, MX>(rg, Kl, Kd, Ksc);
     const uint64_t vmask = __ballot(idx_cur >= 0);
     __syncthreads();  // the block's rows are in LDS
     const int idx_nn = load_slot_index(idx_row, blk + 2, l32, p.topk, p.S_kv);
-    if (blk + 1 < nblk) wide_issue<C, FP8>(rg, kv_b, kv_scale_b, idx_nxt, row_pitch);
+    if (blk + 1 < nblk) wide_issue<C, FP8, MX>(rg, kv_b, kv_scale_b, idx_nxt, row_pitch, sc_pitch);
 
     // ---- partial S^T = K Q^T over this wave's k-steps ----
     f32x16 sacc;
 #pragma unroll
     for (int a = 0; a < 16; ++a) sacc[a] = 0.0f;
+    if constexpr (MX) {
+      if (par) mx_wave_scores<C, 1>(sacc, Kl, qreg, qbs, Ksc, k0, l32, g32);
+      else mx_wave_scores<C, 0>(sacc, Kl, qreg, qbs, Ksc, k0, l32, g32);
+    }
 #pragma unroll
-    for (int k = 0; k < C::KQ; ++k) {
+    for (int k = 0; k < (MX ? 0 : C::KQ); ++k) {
       if constexpr (FP8) {
         const long a = *reinterpret_cast<const long *>(Kl + l32 * C::KL_STRIDE + 16 * (k0 + k) + 8 * g32);
         sacc = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(a, qreg[k], sacc, 0, 0, 0);
@@ -253,14 +311,14 @@ sparse_mla_fwd_wide_kernel(const FwdParams p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float ksc4[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-      if constexpr (FP8) {
+      if constexpr (FP8 && !MX) {
         const f32x4 s4 = *reinterpret_cast<const f32x4 *>(Ksc + 8 * i + 4 * g32);
         ksc4[0] = s4[0]; ksc4[1] = s4[1]; ksc4[2] = s4[2]; ksc4[3] = s4[3];
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float v = s[4 * i + j];
-        if constexpr (FP8) v *= ksc4[j];
+        if constexpr (FP8 && !MX) v *= ksc4[j];
         xs[4 * i + j] = v;  // raw score, scaled inside the exp
       }
     }
@@ -333,22 +391,27 @@ sparse_mla_fwd_wide_kernel(const FwdParams p) {
   }
 }
 
-template <int D_QK, int D_V, bool FP8>
+template <int D_QK, int D_V, bool FP8, bool MX = false>
 static int launch_fwd_wide_t(const FwdParams &p, hipStream_t st) {
-  using L = WideFwdLds<D_QK, D_V, FP8>;
+  using L = WideFwdLds<D_QK, D_V, FP8, MX>;
   const size_t lds = L::BYTES;
   if (lds > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void *)sparse_mla_fwd_wide_kernel<D_QK, D_V, FP8>,
+    hipError_t e = hipFuncSetAttribute((const void *)sparse_mla_fwd_wide_kernel<D_QK, D_V, FP8, MX>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return set_error(DSA_ERR_HIP, "sparse_mla_fwd(wide): LDS attribute: %s", hipGetErrorString(e));
   }
   const int64_t nitems = p.B * p.S * p.G * p.ntiles;  // one workgroup per item
   if (nitems >= (1ll << 31)) return set_error(DSA_ERR_INVALID_ARG, "sparse_mla_fwd(wide): grid too large");
-  hipLaunchKernelGGL((sparse_mla_fwd_wide_kernel<D_QK, D_V, FP8>), dim3((unsigned)nitems), dim3(256), lds, st, p);
+  hipLaunchKernelGGL((sparse_mla_fwd_wide_kernel<D_QK, D_V, FP8, MX>), dim3((unsigned)nitems), dim3(256), lds, st, p);
   return check_launch("sparse_mla_fwd(wide)");
 }
 
-int launch_fwd_wide(const FwdParams &p, int64_t d_qk, int64_t d_v, bool fp8, hipStream_t st) {
+int launch_fwd_wide(const FwdParams &p, int64_t d_qk, int64_t d_v, bool fp8, hipStream_t st, bool mx) {
+  if (mx) {
+    if (d_qk == 576 && d_v == 512) return launch_fwd_wide_t<576, 512, true, true>(p, st);
+    return set_error(DSA_ERR_UNSUPPORTED, "sparse_mla_fwd(wide): no MXFP8 kernel for d_qk=%lld d_v=%lld",
+                     (long long)d_qk, (long long)d_v);
+  }
   if (d_qk == 576 && d_v == 512) return fp8 ? launch_fwd_wide_t<576, 512, true>(p, st) : launch_fwd_wide_t<576, 512, false>(p, st);
   if (d_qk == 576 && d_v == 576) return fp8 ? launch_fwd_wide_t<576, 576, true>(p, st) : launch_fwd_wide_t<576, 576, false>(p, st);
   return set_error(DSA_ERR_UNSUPPORTED, "sparse_mla_fwd(wide): no kernel for d_qk=%lld d_v=%lld", (long long)d_qk,

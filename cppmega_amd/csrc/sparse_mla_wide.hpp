@@ -13,7 +13,7 @@ namespace dsa {
 inline bool wide_shape(int64_t d_qk, int64_t d_v) { return d_qk == 576 && (d_v == 512 || d_v == 576); }
 
 // Forward over all (token, kv group, 32-head tile) items; bf16 or e4m3.
-int launch_fwd_wide(const FwdParams &p, int64_t d_qk, int64_t d_v, bool fp8, hipStream_t st);
+int launch_fwd_wide(const FwdParams &p, int64_t d_qk, int64_t d_v, bool fp8, hipStream_t st, bool mx = false);
 // Backward main pass (P, dS, dQ, fp32 partial dKV rows at CSR positions); bf16 or e4m3.
 int launch_bwd_main_wide(const BwdParams &p, int64_t d_qk, int64_t d_v, bool fp8, hipStream_t st);
 

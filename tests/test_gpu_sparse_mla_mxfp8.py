@@ -49,6 +49,11 @@ def _inputs(B, S, H, D, G, K, seed, spread=True, pow2=True):
     (2, 96, 16, 128, 64, 1, 40, False),
     (1, 64, 64, 128, 64, 2, 48, True),
     (1, 80, 32, 192, 128, 1, 64, False),
+    # d_qk = 576 (the wide kernel: four waves split d_qk, so blocks 4 and 13
+    # are each scaled half in one wave and half in the next)
+    (1, 48, 32, 576, 512, 1, 64, True),
+    (2, 40, 16, 576, 512, 1, 40, False),
+    (1, 36, 64, 576, 512, 2, 48, False),
 ])
 def test_mxfp8_fwd_matches_oracle(dev, B, S, H, D, DV, G, K, pow2):
     q8, qs, kv8, ks, idx = _inputs(B, S, H, D, G, K, seed=S + D, pow2=pow2)
@@ -74,8 +79,9 @@ def test_mxfp8_dequantize_bit_exact(dev):
                            ref.view(torch.int16 if dt == torch.bfloat16 else torch.int32))
 
 
-def test_mxfp8_public_wrappers_and_backward(dev, monkeypatch):
-    B, S, H, D, DV, K = 1, 96, 32, 128, 64, 48
+@pytest.mark.parametrize("S,D,DV", [(96, 128, 64), (40, 576, 512)])
+def test_mxfp8_public_wrappers_and_backward(dev, monkeypatch, S, D, DV):
+    B, H, K = 1, 32, 48
     # unspread values, arbitrary block scales: the gradients of the bf16
     # backward scale their dS / P rounding with |q| and |dO|, so the bar is
     # stated for the N(0, 0.5)-sized tensors it is stated for elsewhere
