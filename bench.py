@@ -269,7 +269,7 @@ def measure_indexer_kl(dev, reps=5):
     import torch
 
     from cppmega_amd.dsa_index_mask import topk_index_mask
-    from cppmega_amd.dsa_splitk_indexer_loss import indexer_kl_loss
+    from cppmega_amd.dsa_splitk_indexer_loss import indexer_kl_loss, indexer_kl_loss_backward
 
     gen = torch.Generator(device=dev).manual_seed(9)
     q = (torch.randn((S, B, KL_HEADS, KL_HN), generator=gen, device=dev) * 0.5).to(torch.bfloat16)
@@ -284,6 +284,14 @@ def measure_indexer_kl(dev, reps=5):
 
     for mode, sparse in (("dense", False), ("sparse", True)):
         t = med_time(lambda: indexer_kl_loss(sc, tk, q, k, scale, 1.0, sparse))
+        tf = fl / t / 1e12
+        res[mode] = {"ms": round(t * 1e3, 3), "bound": "mfma", "tflops": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
+                     "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
+    # gradient with respect to the index scores: the same two q.k passes (the
+    # second writes the target P), then one elementwise pass over [b, s, s]
+    one = torch.ones((), dtype=torch.float32, device=dev)
+    for mode, sparse in (("grad_dense", False), ("grad_sparse", True)):
+        t = med_time(lambda: indexer_kl_loss_backward(one, sc, tk, q, k, scale, 1.0, sparse))
         tf = fl / t / 1e12
         res[mode] = {"ms": round(t * 1e3, 3), "bound": "mfma", "tflops": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
                      "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
@@ -573,7 +581,8 @@ def main():
                                f"QK^T on e4m3, other products bf16); mxfp8_fwd: the block-scaled (one f32 scale "
                                f"per 32 channels) forward on the same shapes", "kernels": cfg4} if cfg4 is not None else None),
         "indexer_kl_loss": ({"workload": f"compute_dsa_indexer_loss_splitk: query/key [{S},{B},{KL_HEADS},{KL_HN}] "
-                                         f"bf16, index scores [{B},{S},{S}] causal, top-{TOPK}; index_mask: "
+                                         f"bf16, index scores [{B},{S},{S}] causal, top-{TOPK}; grad_*: its gradient "
+                                         f"to the index scores (indexer_kl_loss_backward); index_mask: "
                                          f"topk_index_mask of the top-{TOPK} into [{B},{S},{S}] f32",
                              "kernels": kl} if kl is not None else None),
     }

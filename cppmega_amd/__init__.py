@@ -9,7 +9,7 @@ in ``include/dsa_hip.h``.
 from . import _lib
 from .dsa_indexer_fused_patch import apply_dsa_indexer_fused_patch, compute_index_scores_fused_bf16, index_scores
 from .dsa_index_mask import scatter_topk_into_index_mask, topk_index_mask
-from .dsa_splitk_indexer_loss import compute_dsa_indexer_loss_splitk, indexer_kl_loss
+from .dsa_splitk_indexer_loss import compute_dsa_indexer_loss_splitk, indexer_kl_loss, indexer_kl_loss_backward
 from .dsa_topk import fused_qk_topk_naive, indexer_topk, topk_indices
 from .index_cache_patch import IndexCacheSchedule, apply_index_cache_patch
 
@@ -22,6 +22,7 @@ __all__ = [
     "fused_qk_topk_naive",
     "index_scores",
     "indexer_kl_loss",
+    "indexer_kl_loss_backward",
     "indexer_topk",
     "scatter_topk_into_index_mask",
     "topk_index_mask",

@@ -45,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "dsa_fp8_dequantize_blockwise",
     "dsa_indexer_kl_loss_workspace_size",
     "dsa_indexer_kl_loss",
+    "dsa_indexer_kl_loss_backward",
     "dsa_topk_index_mask",
     "dsa_stage_timing",
     "dsa_stage_times",
@@ -82,6 +83,9 @@ _SIGNATURES = {
     "dsa_indexer_kl_loss": (_i32, [_c_void_p, _c_void_p, _i32, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                    _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _i32,
                                    _c_void_p, _size_t, _c_void_p]),
+    "dsa_indexer_kl_loss_backward": (_i32, [_c_void_p, _c_void_p, _i32, _i64, _c_void_p, _c_void_p, _c_void_p,
+                                            _c_void_p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _i32,
+                                            _c_void_p, _size_t, _c_void_p]),
     "dsa_topk_index_mask": (_i32, [_c_void_p, _i32, _i64, _c_void_p, _i64, _i64, _i64, _i64, _i64,
                                    _f32, _f32, _i32, _c_void_p]),
     "dsa_stage_timing": (_i32, [_i32]),

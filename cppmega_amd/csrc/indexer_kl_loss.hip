@@ -34,6 +34,19 @@
 //     normaliser, as the reference's softmax gives);
 //  5. kl_mean_kernel         one workgroup: coeff * mean of the row losses in a
 //     fixed summation order.
+//
+// Gradient with respect to index_scores (dsa_indexer_kl_loss_backward; the
+// loss's only path back to the indexer, which Megatron obtains by autograd
+// through compute_dsa_indexer_loss).  With Q = softmax(z) over the row's
+// columns and P the detached target,
+//   dL/dz_s = g * coeff / (B * Sq) * (Q_s * R - P_s * Q_s / (Q_s + 1e-10)),
+//   R       = sum_j P_j * Q_j / (Q_j + 1e-10)
+// (0 where Q_s = 0: -inf scores and, sparse, columns outside the top-k set;
+// NaN over a row whose loss is NaN).  Kernels 1-3 run as above, except that
+// the pass kernel writes P into the gradient buffer (s <= t) and one partial
+// R per key chunk instead of the KL terms; then
+//  6. kl_grad_kernel         one workgroup per row: R in chunk order, then the
+//     whole row of the gradient in place over P (16-byte loads and stores).
 #include "dsa_common.hpp"
 
 namespace dsa {
@@ -69,6 +82,9 @@ struct Params {
   float *partial;                 // [B, NC, Sq]  KL partial sums per key chunk
   float *rows;                    // [B, Sq]      per-position KL
   float *loss;                    // [1]
+  float *partial_r;               // [B, NC, Sq]  gradient: R partial sums per key chunk
+  float *grad;                    // [B, Sq, Sk]  gradient: P (pass kernel), then dL/dz
+  const float *grad_loss;         // [1]          upstream gradient of the loss
   int64_t B, Sq, Sk, H, G, K, W, NC;
   int64_t NI;                     // KL work items per batch (block, chunk pairs)
   int topk_i64;
@@ -334,7 +350,7 @@ kl_attn_stats_kernel(Params p) {
 // ---------------------------------------------------------------------------
 // 3. KL partial sums per (token, key chunk)
 // ---------------------------------------------------------------------------
-template <int D, int NW>
+template <int D, int NW, bool GRAD = false>
 __global__ void __launch_bounds__(64 * NW) kl_pass_kernel(Params p) {
   using C = Cfg<D, NW>;
   constexpr int kTB = C::TB;
@@ -430,6 +446,7 @@ __global__ void __launch_bounds__(64 * NW) kl_pass_kernel(Params p) {
   const auto irs = make_buffer_rsrc(irow, (uint32_t)(p.Sq * p.Sk * 4));
   const bool vec = (p.Sk & 3) == 0;  // rows 16-byte aligned: one b128 load per 4 keys
   float kl = 0.0f;
+  float *grow = GRAD ? p.grad + (b * p.Sq + (t < p.Sq ? t : 0)) * p.Sk : nullptr;
 #pragma unroll
   for (int sub = 0; sub < C::SUBS; ++sub) {
     if (!sub_on[sub]) continue;
@@ -451,19 +468,47 @@ __global__ void __launch_bounds__(64 * NW) kl_pass_kernel(Params p) {
           iv[j] = buffer_load_f32(irs, (int)off, 0);
         }
       }
+      if constexpr (GRAD) {
+        // P on this lane's four keys (0 off the admissible set), and R's terms
+        f32x4 pv;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int a = 4 * i + j;
-        if ((vb[sub] >> a) & 1u) {
-          const float pr = P[sub][a] * inv_h;
+        for (int j = 0; j < 4; ++j) {
+          const int a = 4 * i + j;
+          const bool on = (vb[sub] >> a) & 1u;
+          const float pr = on ? P[sub][a] * inv_h : 0.0f;
           const float q = exp2_fast(fmaf(iv[j], kLog2e, -gam));
-          kl += pr * (__builtin_amdgcn_logf(pr + kEps) - __builtin_amdgcn_logf(q + kEps));
+          pv[j] = pr;
+          if (on) kl += pr * (q / (q + kEps));
+        }
+        if (t < p.Sq && s0 < p.Sk) {
+          if (vec) {
+            *reinterpret_cast<f32x4 *>(grow + s0) = pv;
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (s0 + j < p.Sk) grow[s0 + j] = pv[j];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int a = 4 * i + j;
+          if ((vb[sub] >> a) & 1u) {
+            const float pr = P[sub][a] * inv_h;
+            const float q = exp2_fast(fmaf(iv[j], kLog2e, -gam));
+            kl += pr * (__builtin_amdgcn_logf(pr + kEps) - __builtin_amdgcn_logf(q + kEps));
+          }
         }
       }
     }
   }
-  kl = sum_halves(kl) * kLn2;
-  if (g == 0 && t < p.Sq) p.partial[(b * p.NC + ci) * p.Sq + t] = kl;
+  if constexpr (GRAD) {
+    kl = sum_halves(kl);
+    if (g == 0 && t < p.Sq) p.partial_r[(b * p.NC + ci) * p.Sq + t] = kl;
+  } else {
+    kl = sum_halves(kl) * kLn2;
+    if (g == 0 && t < p.Sq) p.partial[(b * p.NC + ci) * p.Sq + t] = kl;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -484,6 +529,52 @@ __global__ void __launch_bounds__(kNT) kl_rows_kernel(Params p) {
   p.rows[row] = s;
 }
 
+// 6. gradient row: dL/dz over P in place (one workgroup per (b, t) row)
+template <int D>
+__global__ void __launch_bounds__(kNT) kl_grad_kernel(Params p) {
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / p.Sq, t = row % p.Sq;
+  const int64_t last_k = t < p.Sk - 1 ? t : p.Sk - 1;  // P is written for s <= last_k
+  const int64_t cmax = last_k / Cfg<D, 4>::KC;
+  float R = 0.0f;
+  for (int64_t c = 0; c <= cmax; ++c) R += p.partial_r[(b * p.NC + c) * p.Sq + t];
+  const bool no_target = !(p.beta[b * p.H * p.Sq + t] > -INFINITY);
+  const float gam = p.gamma[row];
+  const bool nan_row = no_target || gam != gam;
+  const float gs = p.grad_loss[0] * p.coeff / (float)(p.B * p.Sq);
+  const float *zrow = p.index_scores + row * p.Sk;
+  float *grow = p.grad + row * p.Sk;
+  const uint32_t *mrow = p.sparse ? p.mask + row * p.W : nullptr;
+  const bool vec = (p.Sk & 3) == 0;
+  for (int64_t s0 = 4 * (int64_t)threadIdx.x; s0 < p.Sk; s0 += 4 * kNT) {
+    f32x4 z, pr, out;
+    if (vec) {
+      z = *reinterpret_cast<const f32x4 *>(zrow + s0);
+      pr = s0 <= last_k ? *reinterpret_cast<const f32x4 *>(grow + s0) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        z[j] = s0 + j < p.Sk ? zrow[s0 + j] : 0.0f;
+        pr[j] = s0 + j <= last_k ? grow[s0 + j] : 0.0f;
+      }
+    }
+    const uint32_t mw = mrow ? mrow[s0 >> 5] >> (s0 & 31) : 0xfu;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float q = ((mw >> j) & 1u) ? exp2_fast(fmaf(z[j], kLog2e, -gam)) : 0.0f;
+      const float pj = s0 + j <= last_k ? pr[j] : 0.0f;
+      out[j] = nan_row ? __builtin_nanf("") : gs * (q * R - pj * (q / (q + kEps)));
+    }
+    if (vec) {
+      *reinterpret_cast<f32x4 *>(grow + s0) = out;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (s0 + j < p.Sk) grow[s0 + j] = out[j];
+    }
+  }
+}
+
 __global__ void __launch_bounds__(1024) kl_mean_kernel(Params p) {
   __shared__ float red[1024];
   const int64_t n = p.B * p.Sq;
@@ -502,7 +593,7 @@ __global__ void __launch_bounds__(1024) kl_mean_kernel(Params p) {
 // host
 // ---------------------------------------------------------------------------
 struct Layout {
-  size_t mask, gamma, beta, partial, rows, total;
+  size_t mask, gamma, beta, partial, rows, partial_r, total;
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -517,11 +608,12 @@ static Layout layout(int64_t B, int64_t Sq, int64_t Sk, int64_t H, int64_t D, in
   L.beta = o;    o += align256((size_t)(B * H * Sq) * 4);
   L.partial = o; o += align256((size_t)(B * NC * Sq) * 4);
   L.rows = o;    o += align256((size_t)(B * Sq) * 4);
+  L.partial_r = o; o += align256((size_t)(B * NC * Sq) * 4);
   L.total = o;
   return L;
 }
 
-template <int D, int NWS, int NWP>
+template <int D, int NWS, int NWP, bool GRAD>
 static int launch_mfma(const Params &p, hipStream_t st) {
   using CS = Cfg<D, NWS>;
   using CP = Cfg<D, NWP>;
@@ -537,11 +629,76 @@ static int launch_mfma(const Params &p, hipStream_t st) {
     q.NI += (lt < p.Sk - 1 ? lt : p.Sk - 1) / CP::KC + 1;
   }
   const int64_t items = (p.B * q.NI + 7) / 8 * 8;
-  hipLaunchKernelGGL((kl_pass_kernel<D, NWP>), dim3((unsigned)items), dim3(CP::NT), 0, st, q);
+  hipLaunchKernelGGL((kl_pass_kernel<D, NWP, GRAD>), dim3((unsigned)items), dim3(CP::NT), 0, st, q);
   rc = check_launch("kl_pass_kernel");
   if (rc) return rc;
+  if constexpr (GRAD) {
+    hipLaunchKernelGGL(kl_grad_kernel<D>, dim3((unsigned)(p.B * p.Sq)), dim3(kNT), 0, st, p);
+    return check_launch("kl_grad_kernel");
+  }
   hipLaunchKernelGGL(kl_rows_kernel<D>, dim3((unsigned)((p.B * p.Sq + kNT - 1) / kNT)), dim3(kNT), 0, st, p);
   return check_launch("kl_rows_kernel");
+}
+
+// Checks and Params shared by the loss and its gradient (kernels 1-3).
+static int kl_setup(const char *fn, const float *index_scores, const void *topk_indices, int topk_dtype,
+                    int64_t topk, const void *query, const void *key, int64_t B, int64_t Sq, int64_t Sk,
+                    int64_t H, int64_t G, int64_t D, float softmax_scale, float loss_coeff, int sparse,
+                    void *workspace, size_t workspace_bytes, Params &p) {
+  DSA_REQUIRE(index_scores && query && key, "%s: null pointer", fn);
+  DSA_REQUIRE(B > 0 && Sq > 0 && Sk > 0 && H > 0 && G > 0, "%s: empty shape B=%lld Sq=%lld Sk=%lld H=%lld G=%lld",
+              fn, (long long)B, (long long)Sq, (long long)Sk, (long long)H, (long long)G);
+  DSA_REQUIRE(H % G == 0, "%s: H=%lld is not a multiple of the key heads G=%lld", fn, (long long)H, (long long)G);
+  DSA_REQUIRE(softmax_scale > 0.0f && softmax_scale < INFINITY, "%s: softmax_scale %g must be positive", fn,
+              (double)softmax_scale);
+  DSA_REQUIRE(D == 64 || D == 128 || D == 192 || D == 256, "%s: head dim %lld not in {64,128,192,256}", fn,
+              (long long)D);
+  DSA_REQUIRE(B * Sq * Sk < ((int64_t)1 << 29), "%s: B*Sq*Sk=%lld index scores exceed 2 GiB", fn,
+              (long long)(B * Sq * Sk));
+  DSA_REQUIRE(Sk * B * G * D * 2 < ((int64_t)1 << 31), "%s: key tensor exceeds 2 GiB", fn);
+  if (sparse) {
+    DSA_REQUIRE(topk_indices && topk > 0, "%s: sparse mode needs top-k indices", fn);
+    DSA_REQUIRE(topk_dtype == DSA_DTYPE_I32 || topk_dtype == DSA_DTYPE_I64, "%s: top-k dtype %d is not int32/int64",
+                fn, topk_dtype);
+    DSA_REQUIRE(Sk <= 32 * kMaxW, "%s: sparse mode supports Sk <= %d (got %lld)", fn, 32 * kMaxW, (long long)Sk);
+  }
+  const Layout L = layout(B, Sq, Sk, H, D, sparse);
+  if (!workspace || workspace_bytes < L.total)
+    return set_error(DSA_ERR_WORKSPACE, "%s: workspace %zu bytes < %zu required", fn,
+                     workspace ? workspace_bytes : (size_t)0, L.total);
+  unsigned char *ws = static_cast<unsigned char *>(workspace);
+  p = Params{};
+  p.index_scores = index_scores;
+  p.topk = topk_indices;
+  p.query = static_cast<const unsigned char *>(query);
+  p.key = static_cast<const unsigned char *>(key);
+  p.mask = reinterpret_cast<uint32_t *>(ws + L.mask);
+  p.gamma = reinterpret_cast<float *>(ws + L.gamma);
+  p.beta = reinterpret_cast<float *>(ws + L.beta);
+  p.partial = reinterpret_cast<float *>(ws + L.partial);
+  p.rows = reinterpret_cast<float *>(ws + L.rows);
+  p.partial_r = reinterpret_cast<float *>(ws + L.partial_r);
+  p.B = B; p.Sq = Sq; p.Sk = Sk; p.H = H; p.G = G; p.K = sparse ? topk : 0;
+  p.W = (Sk + 31) / 32;
+  p.NC = (Sk + (D <= 128 ? 128 : 64) - 1) / (D <= 128 ? 128 : 64);
+  p.topk_i64 = topk_dtype == DSA_DTYPE_I64;
+  p.sparse = sparse ? 1 : 0;
+  p.c = softmax_scale * kLog2e;
+  p.coeff = loss_coeff;
+  return DSA_OK;
+}
+
+template <bool GRAD>
+static int kl_launch(const Params &p, int64_t D, hipStream_t st) {
+  hipLaunchKernelGGL(kl_index_stats_kernel, dim3((unsigned)((p.B * p.Sq + 3) / 4)), dim3(kNT), 0, st, p);
+  int rc = check_launch("kl_index_stats_kernel");
+  if (rc) return rc;
+  switch (D) {
+    case 64: return launch_mfma<64, 8, 4, GRAD>(p, st);
+    case 128: return launch_mfma<128, 8, 4, GRAD>(p, st);
+    case 192: return launch_mfma<192, 8, 4, GRAD>(p, st);
+    default: return launch_mfma<256, 8, 4, GRAD>(p, st);
+  }
 }
 
 }  // namespace kl
@@ -560,60 +717,35 @@ extern "C" int dsa_indexer_kl_loss(const float *index_scores, const void *topk_i
                                    void *workspace, size_t workspace_bytes, void *stream) {
   using namespace dsa;
   using namespace dsa::kl;
-  DSA_REQUIRE(index_scores && query && key && loss, "dsa_indexer_kl_loss: null pointer");
-  DSA_REQUIRE(B > 0 && Sq > 0 && Sk > 0 && H > 0 && G > 0, "dsa_indexer_kl_loss: empty shape B=%lld Sq=%lld Sk=%lld H=%lld G=%lld",
-              (long long)B, (long long)Sq, (long long)Sk, (long long)H, (long long)G);
-  DSA_REQUIRE(H % G == 0, "dsa_indexer_kl_loss: H=%lld is not a multiple of the key heads G=%lld", (long long)H,
-              (long long)G);
-  DSA_REQUIRE(softmax_scale > 0.0f && softmax_scale < INFINITY, "dsa_indexer_kl_loss: softmax_scale %g must be positive",
-              (double)softmax_scale);
-  DSA_REQUIRE(D == 64 || D == 128 || D == 192 || D == 256, "dsa_indexer_kl_loss: head dim %lld not in {64,128,192,256}",
-              (long long)D);
-  DSA_REQUIRE(B * Sq * Sk < ((int64_t)1 << 29), "dsa_indexer_kl_loss: B*Sq*Sk=%lld index scores exceed 2 GiB",
-              (long long)(B * Sq * Sk));
-  DSA_REQUIRE(Sk * B * G * D * 2 < ((int64_t)1 << 31), "dsa_indexer_kl_loss: key tensor exceeds 2 GiB");
-  if (sparse) {
-    DSA_REQUIRE(topk_indices && topk > 0, "dsa_indexer_kl_loss: sparse mode needs top-k indices");
-    DSA_REQUIRE(topk_dtype == DSA_DTYPE_I32 || topk_dtype == DSA_DTYPE_I64,
-                "dsa_indexer_kl_loss: top-k dtype %d is not int32/int64", topk_dtype);
-    DSA_REQUIRE(Sk <= 32 * kMaxW, "dsa_indexer_kl_loss: sparse mode supports Sk <= %d (got %lld)", 32 * kMaxW,
-                (long long)Sk);
-  }
-  const Layout L = layout(B, Sq, Sk, H, D, sparse);
-  if (!workspace || workspace_bytes < L.total)
-    return set_error(DSA_ERR_WORKSPACE, "dsa_indexer_kl_loss: workspace %zu bytes < %zu required",
-                     workspace ? workspace_bytes : (size_t)0, L.total);
-  unsigned char *ws = static_cast<unsigned char *>(workspace);
-  Params p{};
-  p.index_scores = index_scores;
-  p.topk = topk_indices;
-  p.query = static_cast<const unsigned char *>(query);
-  p.key = static_cast<const unsigned char *>(key);
-  p.mask = reinterpret_cast<uint32_t *>(ws + L.mask);
-  p.gamma = reinterpret_cast<float *>(ws + L.gamma);
-  p.beta = reinterpret_cast<float *>(ws + L.beta);
-  p.partial = reinterpret_cast<float *>(ws + L.partial);
-  p.rows = row_loss ? row_loss : reinterpret_cast<float *>(ws + L.rows);
-  p.loss = loss;
-  p.B = B; p.Sq = Sq; p.Sk = Sk; p.H = H; p.G = G; p.K = sparse ? topk : 0;
-  p.W = (Sk + 31) / 32;
-  p.NC = (Sk + (D <= 128 ? 128 : 64) - 1) / (D <= 128 ? 128 : 64);
-  p.topk_i64 = topk_dtype == DSA_DTYPE_I64;
-  p.sparse = sparse ? 1 : 0;
-  p.c = softmax_scale * kLog2e;
-  p.coeff = loss_coeff;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-
-  hipLaunchKernelGGL(kl_index_stats_kernel, dim3((unsigned)((B * Sq + 3) / 4)), dim3(kNT), 0, st, p);
-  int rc = check_launch("kl_index_stats_kernel");
+  DSA_REQUIRE(loss, "dsa_indexer_kl_loss: null loss pointer");
+  Params p;
+  int rc = kl_setup("dsa_indexer_kl_loss", index_scores, topk_indices, topk_dtype, topk, query, key, B, Sq, Sk, H, G,
+                    D, softmax_scale, loss_coeff, sparse, workspace, workspace_bytes, p);
   if (rc) return rc;
-  switch (D) {
-    case 64: rc = launch_mfma<64, 8, 4>(p, st); break;
-    case 128: rc = launch_mfma<128, 8, 4>(p, st); break;
-    case 192: rc = launch_mfma<192, 8, 4>(p, st); break;
-    default: rc = launch_mfma<256, 8, 4>(p, st); break;
-  }
+  if (row_loss) p.rows = row_loss;
+  p.loss = loss;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  rc = kl_launch<false>(p, D, st);
   if (rc) return rc;
   hipLaunchKernelGGL(kl_mean_kernel, dim3(1), dim3(1024), 0, st, p);
   return check_launch("kl_mean_kernel");
+}
+
+extern "C" int dsa_indexer_kl_loss_backward(const float *index_scores, const void *topk_indices, int topk_dtype,
+                                            int64_t topk, const void *query, const void *key,
+                                            const float *grad_loss, float *grad_index_scores, int64_t B, int64_t Sq,
+                                            int64_t Sk, int64_t H, int64_t G, int64_t D, float softmax_scale,
+                                            float loss_coeff, int sparse, void *workspace, size_t workspace_bytes,
+                                            void *stream) {
+  using namespace dsa;
+  using namespace dsa::kl;
+  DSA_REQUIRE(grad_loss && grad_index_scores, "dsa_indexer_kl_loss_backward: null gradient pointer");
+  DSA_REQUIRE(grad_index_scores != index_scores, "dsa_indexer_kl_loss_backward: the gradient may not overwrite the scores");
+  Params p;
+  int rc = kl_setup("dsa_indexer_kl_loss_backward", index_scores, topk_indices, topk_dtype, topk, query, key, B, Sq,
+                    Sk, H, G, D, softmax_scale, loss_coeff, sparse, workspace, workspace_bytes, p);
+  if (rc) return rc;
+  p.grad = grad_index_scores;
+  p.grad_loss = grad_loss;
+  return kl_launch<true>(p, D, static_cast<hipStream_t>(stream));
 }

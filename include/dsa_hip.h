@@ -238,6 +238,31 @@ int dsa_indexer_kl_loss(const float *index_scores, const void *topk_indices,
                         size_t workspace_bytes, void *stream);
 
 /*
+ * Gradient of dsa_indexer_kl_loss's scalar with respect to index_scores:
+ *   grad_index_scores[b, t, s] = grad_loss[0] * loss_coeff / (B * Sq)
+ *                                * (Q_s * R - P_s * Q_s / (Q_s + 1e-10)),
+ *   R = sum_j P_j * Q_j / (Q_j + 1e-10)
+ * (P the detached head-mean attention target, Q the index softmax; 0 where
+ * Q_s = 0, NaN over a row whose loss is NaN).  Replaces the autograd path
+ * through Megatron's compute_dsa_indexer_loss that the reference's split-K
+ * loss (cppmega/megatron/dsa_splitk_indexer_loss.py:328-468) does not provide,
+ * and the gradient the lemyx fused indexer loss returns to the index scores
+ * (cppmega/megatron/lemyx_dsa_warmup.py:78-178).  grad_loss is a device
+ * pointer (no host synchronisation).  Same arguments, limits and workspace
+ * size as dsa_indexer_kl_loss; grad_index_scores [B, Sq, Sk] f32 must not
+ * alias index_scores.
+ */
+int dsa_indexer_kl_loss_backward(const float *index_scores,
+                                 const void *topk_indices, int topk_dtype,
+                                 int64_t topk, const void *query,
+                                 const void *key, const float *grad_loss,
+                                 float *grad_index_scores, int64_t B,
+                                 int64_t Sq, int64_t Sk, int64_t H, int64_t G,
+                                 int64_t D, float softmax_scale,
+                                 float loss_coeff, int sparse, void *workspace,
+                                 size_t workspace_bytes, void *stream);
+
+/*
  * Top-k index mask of the sparse indexer loss.
  * Replaces Megatron's _scatter_topk_into_index_mask in the CUDA-graph-safe form
  *   cppmega patches in (cppmega/megatron/upstream_patches/apply_dsa_cg_patches.py:267-291;

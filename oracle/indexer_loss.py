@@ -94,6 +94,19 @@ def compute_dsa_indexer_loss(index_scores, topk_indices, query, key, softmax_sca
     return rows.mean() * loss_coeff
 
 
+def indexer_kl_grad(index_scores, topk_indices, query, key, softmax_scale, loss_coeff, sparse_loss,
+                    grad_loss=1.0, dtype=torch.float64):
+    """d(loss) / d(index_scores) [b, sq, sk] by autograd of compute_dsa_indexer_loss
+    in float64 (query / key are the detached target's inputs, as in Megatron,
+    whose indexer gradient is autograd through this same loss).  Pinned by
+    torch.autograd.gradcheck against finite differences and by the invariants
+    of a softmax gradient (every row sums to zero; zero wherever Q = 0)."""
+    z = index_scores.detach().to(dtype).requires_grad_(True)
+    loss = compute_dsa_indexer_loss(z, topk_indices, query, key, softmax_scale, loss_coeff, sparse_loss, dtype)
+    (g,) = torch.autograd.grad(loss, z, grad_outputs=torch.as_tensor(grad_loss, dtype=dtype))
+    return g
+
+
 def kl_flops(b, sq, sk, np_, hn):
     """Algorithmic MFMA work of the causal attention target: two q.k passes
     (softmax statistics, then the recomputed KL), 2 * hn FLOP per (head, t, s <= t)."""

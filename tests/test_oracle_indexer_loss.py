@@ -144,3 +144,54 @@ def test_rows_at_matches_full_form():
         full = okl.indexer_kl_rows(sc, topk, q, k, scale, sparse)
         at = okl.indexer_kl_rows_at(sc, topk, q, k, scale, sparse, pos)
         _same(at.numpy(), full.flatten().numpy())
+
+
+# ---- gradient with respect to the index scores ----
+
+def _grad_case(seed, sq=6, sk=6, b=1, np_=2, hn=4, topk=3):
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn(sq, b, np_, hn, generator=gen).to(torch.bfloat16)
+    k = torch.randn(sk, b, np_, hn, generator=gen).to(torch.bfloat16)
+    z = torch.randn(b, sq, sk, generator=gen, dtype=torch.float64)
+    # causal top-k (every row keeps column 0, so no row is empty)
+    ti = torch.stack([torch.cat([torch.zeros(1, dtype=torch.long),
+                                 torch.randint(0, t + 1, (topk - 1,), generator=gen)]) for t in range(sq)] * b)
+    return q, k, z, ti.reshape(b, sq, topk)
+
+
+@pytest.mark.parametrize("sparse", [False, True], ids=["dense", "sparse"])
+def test_grad_matches_finite_differences(sparse):
+    q, k, z, ti = _grad_case(5)
+    f = lambda zz: okl.compute_dsa_indexer_loss(zz, ti, q, k, 0.5, 0.7, sparse)
+    assert torch.autograd.gradcheck(f, (z.clone().requires_grad_(True),), eps=1e-6, atol=1e-8)
+    g = okl.indexer_kl_grad(z, ti, q, k, 0.5, 0.7, sparse, grad_loss=1.0)
+    gd = torch.zeros_like(z)
+    for idx in np.ndindex(*z.shape):  # central differences of the loss itself
+        e = torch.zeros_like(z)
+        e[idx] = 1e-6
+        gd[idx] = (f(z + e) - f(z - e)) / 2e-6
+    assert torch.allclose(g, gd, atol=1e-8, rtol=1e-5)
+
+
+@pytest.mark.parametrize("sparse", [False, True], ids=["dense", "sparse"])
+def test_grad_invariants(sparse):
+    q, k, z, ti = _grad_case(9, sq=12, sk=12, np_=3, topk=4)
+    z[0, 3, 7] = float("-inf")  # a masked score: Q = 0 there
+    g = okl.indexer_kl_grad(z, ti, q, k, 0.3, 1.0, sparse, grad_loss=2.0)
+    # a softmax gradient sums to zero over every row
+    assert g.sum(-1).abs().max() < 1e-15
+    # zero wherever Q = 0
+    assert g[0, 3, 7] == 0.0
+    if sparse:
+        keep = torch.isfinite(okl.sparse_mask(ti, 12))
+        assert (g[~keep] == 0).all()
+    # linear in the upstream gradient and in loss_coeff
+    g1 = okl.indexer_kl_grad(z, ti, q, k, 0.3, 0.5, sparse, grad_loss=1.0)
+    assert torch.allclose(g, 4.0 * g1, rtol=1e-12, atol=0)
+
+
+def test_grad_nan_rows():
+    q, k, z, _ = _grad_case(2, sq=5, sk=5)
+    ti = torch.full((1, 5, 2), 4, dtype=torch.long)  # only column 4: rows t < 4 have no admissible column
+    g = okl.indexer_kl_grad(z, ti, q, k, 0.5, 1.0, True)
+    assert torch.isnan(g[0, :4]).all() and torch.isfinite(g[0, 4]).all()
