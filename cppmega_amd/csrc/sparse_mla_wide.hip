@@ -35,14 +35,15 @@
 
 namespace dsa {
 
-template <int D_QK, int D_V, bool FP8>
+template <int D_QK, int D_V, bool FP8, int NTHR_ = 256>
 struct WideCfg {
+  static constexpr int NTHR = NTHR_;               // threads that gather a block
   static constexpr int ELT = FP8 ? 1 : 2;          // bytes per element in HBM
   static constexpr int ROWB = D_QK * ELT;          // bytes per kv row
   static constexpr int NCH = ROWB / 16;            // 16-byte chunks per row
   static constexpr int NCH_V = D_V * ELT / 16;     // chunks of the V prefix
   static constexpr int UNITS = 32 * NCH;           // (row, chunk) units per block
-  static constexpr int UPT = (UNITS + 255) / 256;  // units per thread
+  static constexpr int UPT = (UNITS + NTHR - 1) / NTHR;  // units per thread
   static constexpr int KL_STRIDE = ROWB + 32;      // padded LDS row (conflict-free transposed reads)
   static constexpr int KD_STRIDE = D_V * 2 + 32;   // e4m3: dequantised V rows (bf16)
   static constexpr int KSTEPS = D_QK / 16;         // 32x32x16 k-steps over d_qk
@@ -58,7 +59,7 @@ struct WideCfg {
   };
 };
 
-// Issue the loads of one block's 32 rows: thread t takes units t + 256 i,
+// Issue the loads of one block's 32 rows: thread t takes units t + NTHR i,
 // unit u = chunk u % NCH of row u / NCH.  my_idx is the kv row of slot
 // (lane & 31) of this wave (-1: masked).
 // kv_scale_b holds one scale per row (sc_pitch 1) or, MX, one per 32-channel
@@ -70,7 +71,7 @@ __device__ __forceinline__ void wide_issue(typename C::Regs &rg, const unsigned 
   uint32_t valid = 0;
 #pragma unroll
   for (int i = 0; i < C::UPT; ++i) {
-    const int u = t + 256 * i;
+    const int u = t + C::NTHR * i;
     const int row = (u / C::NCH) & 31;
     const int c = u % C::NCH;
     const int ri = __shfl(my_idx, row, 64);
@@ -95,7 +96,7 @@ __device__ __forceinline__ void wide_store(const typename C::Regs &rg, unsigned 
   const int t = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < C::UPT; ++i) {
-    const int u = t + 256 * i;
+    const int u = t + C::NTHR * i;
     if ((i + 1 < C::UPT) || u < C::UNITS) {
       const int row = u / C::NCH, c = u % C::NCH;
       const bool ok = (rg.valid >> i) & 1u;
@@ -151,16 +152,16 @@ __device__ __forceinline__ void put_partial(float *dst, const f32x16 &acc) {
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
-template <int D_QK, int D_V, bool FP8, bool MX = false>
+template <int D_QK, int D_V, bool FP8, bool MX = false, int NT = 1>
 struct WideFwdLds {
-  using C = WideCfg<D_QK, D_V, FP8>;
+  using C = WideCfg<D_QK, D_V, FP8, 256 * NT>;
   static constexpr int NBLK = D_QK / 32;  // MX scale blocks per row
   static constexpr int OFF_KL = 0;
   static constexpr int OFF_KD = OFF_KL + 32 * C::KL_STRIDE;
   static constexpr int OFF_SC = OFF_KD + (FP8 ? 32 * C::KD_STRIDE : 0);
   static constexpr int OFF_SP = (OFF_SC + (FP8 ? (MX ? NBLK : 1) * 32 * 4 : 0) + 15) / 16 * 16;
   static constexpr int SP_W = 16 * 64;  // floats per wave's partial tile
-  static constexpr int BYTES = OFF_SP + 4 * SP_W * 4;
+  static constexpr int BYTES = OFF_SP + 4 * NT * SP_W * 4;  // a partial tile per wave
 };
 
 // MX partial scores of one wave over its k-steps [k0, k0 + KQ) of d_qk (k0 of
@@ -195,20 +196,25 @@ __device__ __forceinline__ void mx_wave_scores(f32x16 &sacc, const unsigned char
   }
 }
 
-template <int D_QK, int D_V, bool FP8, bool MX = false>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D_V <= 512 ? 2 : 1)))
+// NT head tiles per workgroup: waves 4 ht .. 4 ht + 3 own 32-head tile ht of
+// the item and split its head dims as described above; all 4 NT waves gather
+// (and, e4m3, dequantise) the block's kv rows once for the NT tiles.
+template <int D_QK, int D_V, bool FP8, bool MX = false, int NT = 1>
+__global__ void __launch_bounds__(256 * NT) __attribute__((amdgpu_waves_per_eu(D_V <= 512 ? 2 : 1)))
 sparse_mla_fwd_wide_kernel(const FwdParams p) {
   static_assert(!MX || FP8, "MX is an e4m3 mode");
-  using C = WideCfg<D_QK, D_V, FP8>;
-  using L = WideFwdLds<D_QK, D_V, FP8, MX>;
+  using C = WideCfg<D_QK, D_V, FP8, 256 * NT>;
+  using L = WideFwdLds<D_QK, D_V, FP8, MX, NT>;
   typedef typename std::conditional<FP8, long, bf16x8>::type qop_t;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
-  const int lane = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
+  const int lane = lane_id(), wv = __builtin_amdgcn_readfirstlane(wave_id());
+  const int ht = wv >> 2, w = wv & 3;  // head tile within the item, wave within the tile
   const int g32 = lane >> 5, l32 = lane & 31;
   const int64_t item = xcd_remap(blockIdx.x, gridDim.x);
-  const int tile = (int)(item % p.ntiles);
-  const int64_t rest = item / p.ntiles;
+  const int ntg = (p.ntiles + NT - 1) / NT;  // items per (token, kv group)
+  const int tile = (int)(item % ntg) * NT + ht;
+  const int64_t rest = item / ntg;
   const int64_t g = rest % p.G;
   const int64_t tok = rest / p.G;
   const int64_t b = tok / p.S;
@@ -296,10 +302,10 @@ sparse_mla_fwd_wide_kernel(const FwdParams p) {
         sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), qreg[k], sacc, 0, 0, 0);
       }
     }
-    put_partial(Sp + w * L::SP_W, sacc);
+    put_partial(Sp + wv * L::SP_W, sacc);
     __syncthreads();  // all partial tiles written
     float s[16];
-    sum_partials(Sp, L::SP_W, s);
+    sum_partials(Sp + 4 * ht * L::SP_W, L::SP_W, s);
 
     // ---- online softmax (log2 domain, lazy rescale; identical in every wave) ----
     // this lane's slots are 8i + 4*g32 + j: their valid bits sit at 8i + j of lmask;
@@ -391,19 +397,27 @@ sparse_mla_fwd_wide_kernel(const FwdParams p) {
   }
 }
 
-template <int D_QK, int D_V, bool FP8, bool MX = false>
-static int launch_fwd_wide_t(const FwdParams &p, hipStream_t st) {
-  using L = WideFwdLds<D_QK, D_V, FP8, MX>;
+template <int D_QK, int D_V, bool FP8, bool MX, int NT>
+static int launch_fwd_wide_nt(const FwdParams &p, hipStream_t st) {
+  using L = WideFwdLds<D_QK, D_V, FP8, MX, NT>;
   const size_t lds = L::BYTES;
   if (lds > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void *)sparse_mla_fwd_wide_kernel<D_QK, D_V, FP8, MX>,
+    hipError_t e = hipFuncSetAttribute((const void *)sparse_mla_fwd_wide_kernel<D_QK, D_V, FP8, MX, NT>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return set_error(DSA_ERR_HIP, "sparse_mla_fwd(wide): LDS attribute: %s", hipGetErrorString(e));
   }
-  const int64_t nitems = p.B * p.S * p.G * p.ntiles;  // one workgroup per item
+  const int64_t nitems = p.B * p.S * p.G * ((p.ntiles + NT - 1) / NT);  // one workgroup per item
   if (nitems >= (1ll << 31)) return set_error(DSA_ERR_INVALID_ARG, "sparse_mla_fwd(wide): grid too large");
-  hipLaunchKernelGGL((sparse_mla_fwd_wide_kernel<D_QK, D_V, FP8, MX>), dim3((unsigned)nitems), dim3(256), lds, st, p);
+  hipLaunchKernelGGL((sparse_mla_fwd_wide_kernel<D_QK, D_V, FP8, MX, NT>), dim3((unsigned)nitems), dim3(256 * NT), lds,
+                     st, p);
   return check_launch("sparse_mla_fwd(wide)");
+}
+
+// Two head tiles per workgroup when a kv group has at least 64 heads (the
+// gather and dequantisation of a block serve both), else one.
+template <int D_QK, int D_V, bool FP8, bool MX = false>
+static int launch_fwd_wide_t(const FwdParams &p, hipStream_t st) {
+  return p.ntiles >= 2 ? launch_fwd_wide_nt<D_QK, D_V, FP8, MX, 2>(p, st) : launch_fwd_wide_nt<D_QK, D_V, FP8, MX, 1>(p, st);
 }
 
 int launch_fwd_wide(const FwdParams &p, int64_t d_qk, int64_t d_v, bool fp8, hipStream_t st, bool mx) {

@@ -54,6 +54,7 @@ def _inputs(B, S, H, D, G, K, seed, spread=True, pow2=True):
     (1, 48, 32, 576, 512, 1, 64, True),
     (2, 40, 16, 576, 512, 1, 40, False),
     (1, 36, 64, 576, 512, 2, 48, False),
+    (1, 24, 96, 576, 512, 1, 40, False),   # two head tiles per workgroup, one empty
 ])
 def test_mxfp8_fwd_matches_oracle(dev, B, S, H, D, DV, G, K, pow2):
     q8, qs, kv8, ks, idx = _inputs(B, S, H, D, G, K, seed=S + D, pow2=pow2)

@@ -111,7 +111,8 @@ def test_wide_autograd_direct_with_sentinels(dev):
     assert_close(kv.grad, rdkv, what="dkv")
 
 
-@pytest.mark.parametrize("B,S,H,topk", [(1, 64, 128, 96), (1, 72, 40, 64), (2, 48, 32, 33)])
+# H >= 64: two head tiles per workgroup (H = 96: the last workgroup's second tile is empty)
+@pytest.mark.parametrize("B,S,H,topk", [(1, 64, 128, 96), (1, 72, 40, 64), (2, 48, 32, 33), (1, 40, 96, 64)])
 def test_wide_head_tiles(dev, B, S, H, topk):
     """Several 32-head tiles per token, a ragged last tile, a ragged last slot block."""
     inp = synthetic.sparse_mla_inputs(B, S, H, D, DV, topk, std=0.5, seed=B * 100 + H)
@@ -151,13 +152,13 @@ def test_wide_edge_indices(dev):
     assert torch.all(dq[0, 5] == 0)
 
 
-@pytest.mark.parametrize("outliers", [False, True])
-def test_wide_fp8_fwd_bwd_match_fp8_oracle(dev, outliers):
+@pytest.mark.parametrize("outliers,H", [(False, 32), (True, 32), (False, 96)])
+def test_wide_fp8_fwd_bwd_match_fp8_oracle(dev, outliers, H):
     """e4m3 wide forward and backward vs the FP8 oracle on identical quantised inputs.  With
     1% x20 outliers a one-ulp bf16 rounding flip of a P weight (from fp32
     reassociation of a 576-term score) is multiplied by a ~20-sigma V entry, so
     out is held to the mostly-close bar there; LSE keeps the plain bar."""
-    B, S, H, topk = 1, 96, 32, 64
+    B, S, topk = 1, 96, 64
     if outliers:
         q = synthetic.outlier_values((B, S, H, D), 77).to(torch.bfloat16)
         kv = synthetic.outlier_values((B, S, 1, D), 78).to(torch.bfloat16)
