@@ -30,7 +30,7 @@ attention shape: query/key [4096, 2, 32, 128] bf16, index scores [2, 4096,
 "indexer_kl_loss" (not part of `value`; --no-kl skips it).
 
 `value` and `ms_per_step` come from replays of the layer step captured in a
-HIP graph (launch gaps removed; every replay runs all 13 kernels, and three
+HIP graph (launch gaps removed; every replay runs every kernel of the step, and three
 replays are first checked bit for bit against the eager step); the per-kernel
 breakdown and `eager_tokens_per_s` come from the eager timed steps before it.
 
@@ -308,7 +308,7 @@ def measure_indexer_kl(dev, reps=5):
 
 
 def time_graph(step, steps, warmup):
-    """Capture one layer step (all 13 kernels, outputs allocated from the
+    """Capture one layer step (every kernel, outputs allocated from the
     graph's pool) in a HIP graph and time `steps` replays.  Before timing,
     three replays, each separated by an eager step, are checked bit for bit
     against the eager step's outputs (the kernels are deterministic)."""
@@ -344,57 +344,77 @@ def time_graph(step, steps, warmup):
 
 
 def algorithmic_work():
-    """Per-launch algorithmic work of each kernel at cfg2 / cfg3.
+    """Per-launch algorithmic work of each kernel at cfg2 / cfg3, and its bound.
 
-    `flops` follow the reference's FLOP conventions (0 for pure data-movement
-    kernels); `bytes` are the HBM bytes the kernel must move by design (every
-    input read once, every output written once).  The roofline bound of a
-    kernel is the resource with the longer floor at MI355X peak."""
-    MiB = 1 << 20
+    The bound and the work follow the survey's measurement table: the indexer,
+    SparseMLA forward and backward are priced as MFMA work by the reference's
+    FLOP conventions (the forward also against its 112 MB of unique HBM
+    traffic, whichever floor is longer), top-k as the HBM bytes it must read
+    and write.  `io_bytes` are the bytes of the op's own inputs and outputs
+    (every input read once, every output written once); `design_bytes` add
+    what this build's kernels move beyond them (the backward's partial dKV
+    rows and inverse-index planes), reported beside the roofline, never as
+    its denominator."""
     bwd_flops = 2 * B * S * H * TOPK * (3 * D_QK + 2 * D_V)
     q_b, kv_b, idx_b = B * S * H * D_QK * 2, B * S * D_QK * 2, ENTRIES * 4
     o_b, lse_b = B * S * H * D_V * 2, B * S * H * 4
+    csr_planes = 3 * 4 * B * CSR_CHUNKS * S      # mask word written + read, base word written
+    partial_rows = ENTRIES * (2 * D_QK + 1)      # fp16 partial dKV row + int8 exponent per entry
+    bwd_io = q_b + kv_b + 2 * o_b + idx_b + lse_b + q_b + kv_b   # q kv o dO idx lse in; dq dkv out
     return {
         # q, k, w read; lower-triangle fp32 scores written
-        "indexer": {"flops": 2 * B * H_IDX * D_IDX * S * (S + 1) // 2,
-                    "bytes": B * S * H_IDX * D_IDX * 2 + B * S * D_IDX * 2 + B * S * H_IDX * 4
+        "indexer": {"bound": "mfma", "flops": 2 * B * H_IDX * D_IDX * S * (S + 1) // 2,
+                    "io_bytes": B * S * H_IDX * D_IDX * 2 + B * S * D_IDX * 2 + B * S * H_IDX * 4
                     + 4 * B * S * (S + 1) // 2},
         # causal scores read, int32 indices written
-        "topk": {"flops": 0, "bytes": 4 * B * S * (S + 1) // 2 + 4 * B * S * TOPK},
+        "topk": {"bound": "hbm", "flops": 0, "io_bytes": 4 * B * S * (S + 1) // 2 + 4 * B * S * TOPK},
         # q, kv, indices read; out, lse written (the kv gather itself hits L2)
-        "fwd": {"flops": 2 * B * S * H * TOPK * (D_QK + D_V), "bytes": q_b + kv_b + idx_b + o_b + lse_b},
-        # whole backward op (three stages); the stages below split its time
-        "bwd": {"flops": bwd_flops, "bytes": None},
+        "fwd": {"bound": "max", "flops": 2 * B * S * H * TOPK * (D_QK + D_V),
+                "io_bytes": q_b + kv_b + idx_b + o_b + lse_b},
+        # whole backward op (all stages); the stages below split its time
+        "bwd": {"bound": "mfma", "flops": bwd_flops, "io_bytes": bwd_io,
+                "design_bytes": bwd_io + csr_planes + 2 * partial_rows},
         # inverse index: indices read once; per (32-token chunk, kv row) a mask word
         # written and read once and a base word written once (the row scan is small)
-        "bwd_csr": {"flops": 0, "bytes": 4 * ENTRIES + 3 * 4 * B * CSR_CHUNKS * S},
-        # every backward FLOP; reads q, kv, o, dO, indices, lse and the mask / base planes
-        # an entry's CSR position comes from; writes dq and one fp16 partial dKV row
-        # (+ int8 exponent) per (token, slot)
-        "bwd_main": {"flops": bwd_flops,
-                     "bytes": q_b + kv_b + 2 * o_b + idx_b + lse_b + q_b + ENTRIES * (2 * D_QK + 1)
+        "bwd_csr": {"bound": "hbm", "flops": 0, "io_bytes": 4 * ENTRIES + csr_planes},
+        # every backward FLOP; reads q, kv, o, dO, indices, lse (and the mask / base
+        # planes an entry's CSR position comes from), writes dq and one fp16
+        # partial dKV row (+ int8 exponent) per (token, slot)
+        "bwd_main": {"bound": "mfma", "flops": bwd_flops,
+                     "io_bytes": q_b + kv_b + 2 * o_b + idx_b + lse_b + q_b,
+                     "design_bytes": q_b + kv_b + 2 * o_b + idx_b + lse_b + q_b + partial_rows
                      + 2 * 4 * B * CSR_CHUNKS * S},
         # partial rows + exponents + row starts read once, bf16 dKV written once
-        "bwd_reduce": {"flops": 0, "bytes": ENTRIES * (2 * D_QK + 1) + 4 * KV_ROWS + 2 * KV_ROWS * D_QK},
+        "bwd_reduce": {"bound": "hbm", "flops": 0,
+                       "io_bytes": partial_rows + 4 * KV_ROWS + 2 * KV_ROWS * D_QK},
     }
 
 
 def roofline_entry(w, seconds):
-    """Achieved rate against the binding peak (MFMA bf16 or HBM) for one kernel."""
+    """Achieved rate against the kernel's bound (MFMA bf16 or HBM) for one kernel.
+
+    bound "max" prices the kernel against whichever floor (MFMA at the bf16
+    peak, or its io_bytes at the HBM peak) is longer."""
     t_mfma = w["flops"] / (PEAK_BF16_TFLOPS * 1e12)
-    t_hbm = (w["bytes"] or 0) / (PEAK_HBM_GBS * 1e9)
-    if t_mfma >= t_hbm:
+    t_hbm = (w["io_bytes"] or 0) / (PEAK_HBM_GBS * 1e9)
+    bound = w["bound"]
+    if bound == "max":
+        bound = "mfma" if t_mfma >= t_hbm else "hbm"
+    if bound == "mfma":
         ach = w["flops"] / seconds / 1e12
         e = {"bound": "mfma", "achieved": ach, "unit": "TFLOP/s", "peak": PEAK_BF16_TFLOPS}
     else:
-        ach = w["bytes"] / seconds / 1e9
+        ach = w["io_bytes"] / seconds / 1e9
         e = {"bound": "hbm", "achieved": ach, "unit": "GB/s", "peak": PEAK_HBM_GBS}
     e["frac"] = e["achieved"] / e["peak"]
     e["floor_us"] = {"mfma": round(t_mfma * 1e6, 2), "hbm": round(t_hbm * 1e6, 2)}
     if w["flops"]:
         e["tflops"] = round(w["flops"] / seconds / 1e12, 2)
-    if w["bytes"]:
-        e["gbs"] = round(w["bytes"] / seconds / 1e9, 1)
+    if w.get("io_bytes"):
+        e["io_gbs"] = round(w["io_bytes"] / seconds / 1e9, 1)
+    if w.get("design_bytes"):
+        e["design_bytes"] = int(w["design_bytes"])
+        e["design_gbs"] = round(w["design_bytes"] / seconds / 1e9, 1)
     return e
 
 
@@ -532,8 +552,11 @@ def main():
     singles = [k for k in kernels if k != "bwd"]          # "bwd" spans three kernels
     dom = max(singles, key=lambda k: kernels[k]["ms"])
     roof = dict(kernels[dom])
+    traffic = measured_traffic(dom)
     roof_obj = {"kernel": KERNEL_NAMES.get(dom, dom), "bound": roof["bound"], "achieved": roof["achieved"],
-                "peak": roof["peak"], "unit": roof["unit"], "frac": roof["frac"], "traffic": measured_traffic(dom)}
+                "peak": roof["peak"], "unit": roof["unit"], "frac": roof["frac"], "traffic": traffic,
+                "io_bytes": work[dom]["io_bytes"],
+                "traffic_over_io": (round(traffic / work[dom]["io_bytes"], 3) if traffic else None)}
     t_idx = kernels["indexer"]["ms"] + kernels["topk"]["ms"]
     t_att = kernels["fwd"]["ms"] + kernels["bwd"]["ms"]
     amortised = 9 * tokens / ((3 * t_idx + 9 * t_att) / 1e3)

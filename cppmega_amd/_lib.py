@@ -38,6 +38,7 @@ EXPORTED_SYMBOLS = (
     "dsa_sparse_mla_bwd_workspace_size",
     "dsa_sparse_mla_bwd",
     "dsa_indexer_scores",
+    "dsa_indexer_scores_masked",
     "dsa_topk",
     "dsa_fp8_quantize_workspace_size",
     "dsa_fp8_tensorwise_quantize",
@@ -72,6 +73,10 @@ _SIGNATURES = {
     "dsa_indexer_scores": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                   _i64, _i64, _i64, _i64, _i64, _i32, _i32,
                                   _c_void_p, _c_void_p, _i32, _i32, _c_void_p]),
+    "dsa_indexer_scores_masked": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                         _i64, _i64, _i64, _i64, _i64, _i32, _i32,
+                                         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
+                                         _i32, _c_void_p]),
     "dsa_topk": (_i32, [_c_void_p, _i64, _i64, _i64, _i64, _i32, _i64,
                         _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p]),
     "dsa_fp8_quantize_workspace_size": (_size_t, []),

@@ -34,11 +34,20 @@ struct IdxParams {
   float *out;
   const float *q_scale;
   const float *k_scale;
+  // window mode (causal == 3): row t of batch b keeps columns [starts, ends) of
+  // its [B, Sq] windows, plus the additive mask (batch stride mask_bstride
+  // elements, 0 = one mask for every batch; NULL = no mask); -inf elsewhere
+  const int32_t *starts;
+  const int32_t *ends;
+  const float *mask;
+  int64_t mask_bstride;
   int64_t B, Sq, Sk;
   int w_f32;
   int causal;
   int relu;
 };
+
+constexpr int kCausalWindow = 3;
 
 template <int H, int D, bool FP8>
 struct IdxCfg {
@@ -199,6 +208,28 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
   }
   const bool wave_in_sq = wave_tok0 + C::TPW - 1 < p.Sq;
 
+  // window mode: this wave's token windows (wave-uniform scalar loads) and
+  // their union; sub-tiles outside the union are not computed
+  const bool win = p.causal == kCausalWindow;
+  int wst[C::TPW], wen[C::TPW];
+  int64_t wmin = 0, wmax = 0;
+  if (win) {
+    wmin = p.Sk;
+#pragma unroll
+    for (int tl = 0; tl < C::TPW; ++tl) {
+      const int64_t t = wave_tok0 + tl;
+      wst[tl] = t < p.Sq ? p.starts[b * p.Sq + t] : 0;
+      wen[tl] = t < p.Sq ? p.ends[b * p.Sq + t] : 0;
+      if (wen[tl] > wst[tl]) {
+        wmin = wst[tl] < wmin ? wst[tl] : wmin;
+        wmax = wen[tl] > wmax ? wen[tl] : wmax;
+      }
+    }
+  }
+  // additive mask rows of this token block (an empty resource without a mask: loads read 0)
+  const float *mask_b = (win && p.mask) ? p.mask + b * p.mask_bstride + t0 * p.Sk : nullptr;
+  const auto mask_rs = make_buffer_rsrc(mask_b, mask_b ? (uint32_t)((t_last - t0 + 1) * p.Sk * 4) : 0u);
+
   store_tile(0, kreg);
   __syncthreads();
   const int64_t wave_tok_last = wave_tok0 + C::TPW - 1;
@@ -206,7 +237,7 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
     load_tile(it + 1, kreg);  // past the last tile: keys beyond Sk read 0, unused
     const unsigned char *ks = KS[it & 1];
     const int64_t tk = k0 + (int64_t)it * C::KT;
-    const bool interior = wave_in_sq && tk + C::KT <= k_end && (!p.causal || tk + C::KT - 1 <= wave_tok0);
+    const bool interior = !win && wave_in_sq && tk + C::KT <= k_end && (!p.causal || tk + C::KT - 1 <= wave_tok0);
     if (interior) {
 #pragma unroll
       for (int sub = 0; sub < C::SUBS; ++sub) {
@@ -230,8 +261,18 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
 #pragma unroll
       for (int sub = 0; sub < C::SUBS; ++sub) {
         const int64_t sn = tk + sub * 32;
-        // wave-uniform: the sub-tile exists and is not wholly above this wave's diagonal
-        const bool active = sn < k_end && !(p.causal == 2 && sn > wave_tok_last);
+        // wave-uniform: the sub-tile exists and is not wholly above this wave's
+        // diagonal (lower-triangle mode) or outside its windows (window mode)
+        const bool active = sn < k_end && !(p.causal == 2 && sn > wave_tok_last) &&
+                            !(win && (sn + 32 <= wmin || sn >= wmax));
+        const int64_t s = sn + l32;
+        float mv[C::TPW];  // window mode: the additive mask, loaded ahead of the MFMAs
+#pragma unroll
+        for (int tl = 0; tl < C::TPW; ++tl) {
+          const int64_t t = wave_tok0 + tl;
+          const bool ld = win && active && t < p.Sq && s < p.Sk;
+          mv[tl] = buffer_load_f32(mask_rs, ld ? (int)(((t - t0) * p.Sk + s) * 4) : (int)0xffffffffu, 0);
+        }
         float part[C::TPW];
         if (active) {
           subtile(ks, sub, part);
@@ -241,15 +282,18 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
         }
         // the stores are issued on every path (inactive ones land past the
         // resource and are dropped), which keeps the memory wait counts exact
-        const int64_t s = sn + l32;
 #pragma unroll
         for (int tl = 0; tl < C::TPW; ++tl) {
           float v = sum_halves(part[tl]);
           const bool mine = C::TPW == 1 ? (g32 == 0) : ((tl & 1) == g32);
           const int64_t t = wave_tok0 + tl;
-          const bool above = p.causal && s > t;
-          if (above) v = -INFINITY;  // causal mode 1 writes it, mode 2 skips the store
-          const bool st = active && mine && t < p.Sq && s < p.Sk && !(above && p.causal == 2);
+          bool above = (p.causal == 1 || p.causal == 2) && s > t;
+          if (win) {
+            above = s < wst[tl] || s >= wen[tl];
+            v += mv[tl];
+          }
+          if (above) v = -INFINITY;  // modes 1 and 3 write it, mode 2 skips the store
+          const bool st = (active || (win && sn < k_end)) && mine && t < p.Sq && s < p.Sk && !(above && p.causal == 2);
           const uint32_t off = st ? (uint32_t)(((t - t0) * p.Sk + s) * 4) : 0xffffffffu;
           __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), out_rs, (int)off, 0, 0);
         }
@@ -302,8 +346,27 @@ indexer_score_kernel(const IdxParams p) {
   const int64_t k0 = (int64_t)blockIdx.x * C::CHUNK;
   const int64_t t_last = (t0 + C::TT < p.Sq ? t0 + C::TT : p.Sq) - 1;
   const int64_t chunk_end = k0 + C::CHUNK < p.Sk ? k0 + C::CHUNK : p.Sk;
-  if (p.causal == 1 && k0 > t_last) {
-    // chunk wholly above the block's diagonal: -inf only
+  bool outside = p.causal == 1 && k0 > t_last;
+  if (p.causal == kCausalWindow) {
+    // union of the block's token windows (TT <= 64 tokens: one per lane of wave 0)
+    __shared__ int blk_win[2];
+    if (threadIdx.x < 64) {
+      const int64_t t = t0 + threadIdx.x;
+      const bool ok = threadIdx.x < C::TT && t < p.Sq;
+      int st = ok ? p.starts[b * p.Sq + t] : 0, en = ok ? p.ends[b * p.Sq + t] : 0;
+      if (en <= st) { st = 0x7fffffff; en = 0; }
+      for (int off = 32; off >= 1; off >>= 1) {
+        const int so = __shfl_xor(st, off, 64), eo = __shfl_xor(en, off, 64);
+        st = so < st ? so : st;
+        en = eo > en ? eo : en;
+      }
+      if (threadIdx.x == 0) { blk_win[0] = st; blk_win[1] = en; }
+    }
+    __syncthreads();
+    outside = chunk_end <= blk_win[0] || k0 >= blk_win[1];
+  }
+  if (outside) {
+    // chunk wholly above the block's diagonal (mode 1) or outside every window (mode 3): -inf only
     float *out_b = p.out + b * p.Sq * p.Sk;
     const int64_t nk = chunk_end - k0;
     for (int64_t i = threadIdx.x; i < (t_last - t0 + 1) * nk; i += C::NT)
@@ -373,22 +436,22 @@ static int launch_idx(const IdxParams &p, hipStream_t st) {
 
 using namespace dsa;
 
-extern "C" int dsa_indexer_scores(const void *q, const void *w, const void *k, float *scores, int64_t B,
-                                  int64_t Sq, int64_t Sk, int64_t H, int64_t D, int dtype, int w_dtype,
-                                  const float *q_scale, const float *k_scale, int causal, int use_relu,
-                                  void *stream) {
-  DSA_REQUIRE(B >= 0 && Sq >= 0 && Sk >= 0 && H > 0 && D > 0, "dsa_indexer_scores: bad dims");
-  DSA_REQUIRE(dtype == DSA_DTYPE_BF16 || dtype == DSA_DTYPE_E4M3, "dsa_indexer_scores: dtype %d", dtype);
-  DSA_REQUIRE(w_dtype == DSA_DTYPE_BF16 || w_dtype == DSA_DTYPE_F32, "dsa_indexer_scores: w dtype %d", w_dtype);
-  DSA_REQUIRE(causal >= 0 && causal <= 2, "dsa_indexer_scores: causal must be 0, 1 or 2");
+static int indexer_scores_impl(const void *q, const void *w, const void *k, float *scores, int64_t B, int64_t Sq,
+                               int64_t Sk, int64_t H, int64_t D, int dtype, int w_dtype, const float *q_scale,
+                               const float *k_scale, int causal, const int32_t *starts, const int32_t *ends,
+                               const float *mask, int64_t mask_bstride, int use_relu, hipStream_t st,
+                               const char *fn) {
+  DSA_REQUIRE(B >= 0 && Sq >= 0 && Sk >= 0 && H > 0 && D > 0, "%s: bad dims", fn);
+  DSA_REQUIRE(dtype == DSA_DTYPE_BF16 || dtype == DSA_DTYPE_E4M3, "%s: dtype %d", fn, dtype);
+  DSA_REQUIRE(w_dtype == DSA_DTYPE_BF16 || w_dtype == DSA_DTYPE_F32, "%s: w dtype %d", fn, w_dtype);
   if (B == 0 || Sq == 0 || Sk == 0) return DSA_OK;
-  DSA_REQUIRE(q && w && k && scores, "dsa_indexer_scores: null tensor pointer");
-  DSA_REQUIRE(Sk < (1ll << 31) && B < 65536, "dsa_indexer_scores: grid too large");
+  DSA_REQUIRE(q && w && k && scores, "%s: null tensor pointer", fn);
+  DSA_REQUIRE(Sk < (1ll << 31) && B < 65536, "%s: grid too large", fn);
   DSA_REQUIRE(Sk * B * D < (1ll << 31) && Sk < (1ll << 25),
-              "dsa_indexer_scores: k (%lld x %lld x %lld) or score rows too large for 32-bit offsets",
-              (long long)Sk, (long long)B, (long long)D);
+              "%s: k (%lld x %lld x %lld) or score rows too large for 32-bit offsets", fn, (long long)Sk,
+              (long long)B, (long long)D);
   const bool f8 = dtype == DSA_DTYPE_E4M3;
-  if (f8) DSA_REQUIRE(q_scale && k_scale, "dsa_indexer_scores: e4m3 input needs q_scale and k_scale");
+  if (f8) DSA_REQUIRE(q_scale && k_scale, "%s: e4m3 input needs q_scale and k_scale", fn);
   IdxParams p;
   p.q = static_cast<const unsigned char *>(q);
   p.w = w;
@@ -396,13 +459,16 @@ extern "C" int dsa_indexer_scores(const void *q, const void *w, const void *k, f
   p.out = scores;
   p.q_scale = q_scale;
   p.k_scale = k_scale;
+  p.starts = starts;
+  p.ends = ends;
+  p.mask = mask;
+  p.mask_bstride = mask_bstride;
   p.B = B;
   p.Sq = Sq;
   p.Sk = Sk;
   p.w_f32 = w_dtype == DSA_DTYPE_F32;
   p.causal = causal;
   p.relu = use_relu != 0;
-  hipStream_t st = static_cast<hipStream_t>(stream);
 #define DSA_IDX_CASE(HH, DD)                                                              \
   if (H == HH && D == DD) return f8 ? launch_idx<HH, DD, true>(p, st) : launch_idx<HH, DD, false>(p, st);
   DSA_IDX_CASE(16, 64)
@@ -412,6 +478,26 @@ extern "C" int dsa_indexer_scores(const void *q, const void *w, const void *k, f
   DSA_IDX_CASE(32, 128)
   DSA_IDX_CASE(64, 128)
 #undef DSA_IDX_CASE
-  return set_error(DSA_ERR_UNSUPPORTED, "dsa_indexer_scores: no kernel for h=%lld d=%lld", (long long)H,
-                   (long long)D);
+  return set_error(DSA_ERR_UNSUPPORTED, "%s: no kernel for h=%lld d=%lld", fn, (long long)H, (long long)D);
+}
+
+extern "C" int dsa_indexer_scores(const void *q, const void *w, const void *k, float *scores, int64_t B,
+                                  int64_t Sq, int64_t Sk, int64_t H, int64_t D, int dtype, int w_dtype,
+                                  const float *q_scale, const float *k_scale, int causal, int use_relu,
+                                  void *stream) {
+  DSA_REQUIRE(causal >= 0 && causal <= 2, "dsa_indexer_scores: causal must be 0, 1 or 2");
+  return indexer_scores_impl(q, w, k, scores, B, Sq, Sk, H, D, dtype, w_dtype, q_scale, k_scale, causal, nullptr,
+                             nullptr, nullptr, 0, use_relu, static_cast<hipStream_t>(stream), "dsa_indexer_scores");
+}
+
+extern "C" int dsa_indexer_scores_masked(const void *q, const void *w, const void *k, float *scores, int64_t B,
+                                         int64_t Sq, int64_t Sk, int64_t H, int64_t D, int dtype, int w_dtype,
+                                         const float *q_scale, const float *k_scale, const int32_t *starts,
+                                         const int32_t *ends, const float *mask, int64_t mask_bstride,
+                                         int use_relu, void *stream) {
+  DSA_REQUIRE(starts && ends, "dsa_indexer_scores_masked: null window arrays");
+  DSA_REQUIRE(mask_bstride >= 0, "dsa_indexer_scores_masked: negative mask batch stride");
+  return indexer_scores_impl(q, w, k, scores, B, Sq, Sk, H, D, dtype, w_dtype, q_scale, k_scale, kCausalWindow,
+                             starts, ends, mask, mask_bstride, use_relu, static_cast<hipStream_t>(stream),
+                             "dsa_indexer_scores_masked");
 }

@@ -29,13 +29,18 @@ _PATCH_MARKER = "__cppmega_amd_dsa_indexer_fused_patched__"
 CAUSAL_NONE = 0       # every (t, s)
 CAUSAL_NEG_INF = 1    # s > t written as -inf
 CAUSAL_LOWER = 2      # only s <= t written
+CAUSAL_WINDOW = 3     # per-row [start, end) windows plus an additive mask, -inf elsewhere
 
 
-def index_scores(q, weights, k, use_relu=True, causal=CAUSAL_NONE, q_scale=None, k_scale=None, out=None):
+def index_scores(q, weights, k, use_relu=True, causal=CAUSAL_NONE, q_scale=None, k_scale=None, out=None,
+                 starts=None, ends=None, mask=None):
     """q [sq,b,h,d] (bf16 or e4m3), weights [sq,b,h] (f32 or bf16), k [sk,b,d] -> [b,sq,sk] f32.
 
     For e4m3 q / k, q_scale and k_scale are one-element f32 tensors (per-tensor
-    dequant factors, real = fp8 * scale).
+    dequant factors, real = fp8 * scale).  causal=CAUSAL_WINDOW keeps, for row t
+    of batch b, the columns [starts[b, t], ends[b, t]) (int32 device tensors
+    broadcastable to [b, sq]) and adds ``mask`` there (f32, broadcastable to
+    [b, sq, sk], or None); every other element is -inf.
     """
     assert q.dim() == 4, f"q must be [sq,b,h,d], got {tuple(q.shape)}"
     assert k.dim() == 3, f"k must be [sk,b,d], got {tuple(k.shape)}"
@@ -61,6 +66,26 @@ def index_scores(q, weights, k, use_relu=True, causal=CAUSAL_NONE, q_scale=None,
     else:
         assert out.shape == (b, sq, sk) and out.dtype == torch.float32 and out.is_contiguous()
     dev = _lib.ensure_device(q)
+    if causal == CAUSAL_WINDOW:
+        assert starts is not None and ends is not None, "window mode needs starts and ends"
+        starts = starts.to(device=q.device, dtype=torch.int32).expand(b, sq).contiguous()
+        ends = ends.to(device=q.device, dtype=torch.int32).expand(b, sq).contiguous()
+        bstride = 0
+        if mask is not None:
+            mask = mask.to(device=q.device, dtype=torch.float32)
+            mask = mask.reshape(-1, *mask.shape[-2:]) if mask.dim() >= 3 else mask.reshape(1, *mask.shape)
+            assert mask.shape[-2:] == (sq, sk) and mask.shape[0] in (1, b), \
+                f"mask {tuple(mask.shape)} does not broadcast to {(b, sq, sk)}"
+            mask = mask.contiguous()
+            bstride = 0 if mask.shape[0] == 1 else sq * sk
+        rc = _lib.load().dsa_indexer_scores_masked(
+            q.data_ptr(), weights.data_ptr(), k.data_ptr(), out.data_ptr(), b, sq, sk, h, d,
+            _lib.DTYPE_E4M3 if fp8 else _lib.DTYPE_BF16,
+            _lib.DTYPE_F32 if weights.dtype == torch.float32 else _lib.DTYPE_BF16,
+            _lib.ptr(q_scale), _lib.ptr(k_scale), starts.data_ptr(), ends.data_ptr(), _lib.ptr(mask), bstride,
+            1 if use_relu else 0, _lib.stream_ptr(dev))
+        _lib.check(rc, "dsa_indexer_scores_masked")
+        return out
     rc = _lib.load().dsa_indexer_scores(
         q.data_ptr(), weights.data_ptr(), k.data_ptr(), out.data_ptr(), b, sq, sk, h, d,
         _lib.DTYPE_E4M3 if fp8 else _lib.DTYPE_BF16,

@@ -14,7 +14,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .dsa_indexer_fused_patch import CAUSAL_LOWER, CAUSAL_NEG_INF, CAUSAL_NONE, index_scores
+from .dsa_indexer_fused_patch import CAUSAL_LOWER, CAUSAL_NEG_INF, CAUSAL_NONE, CAUSAL_WINDOW, index_scores
 
 
 def topk_indices(scores, topk, causal=True, starts=None, ends=None, causal_offset=0, seq_q=None):
@@ -59,39 +59,133 @@ def indexer_topk(q, k, weights, index_topk, use_relu=True, causal=True, q_scale=
     return (scores, idx) if return_scores else idx
 
 
+def _row_windows(x, b, sq, what):
+    """A per-row int tensor ([sq], [b, sq] or [b * sq]) as int32 [b, sq]."""
+    x = x.to(torch.int32)
+    if x.numel() == sq:
+        return x.reshape(1, sq).expand(b, sq)
+    if x.numel() == b * sq:
+        return x.reshape(b, sq)
+    raise ValueError(f"{what} has {x.numel()} entries; expected {sq} or {b * sq} (one per query row)")
+
+
+def mask_windows(mask, b, sq, sk):
+    """[first, last + 1) span of the finite entries of each row of an additive
+    mask broadcastable to [b, sq, sk], as int32 [b, sq] tensors ((0, 0) for a
+    row without a finite entry).  Device ops only: no host synchronisation."""
+    m = mask.reshape(-1, sq, sk)
+    fin = torch.isfinite(m)
+    fin8 = fin.to(torch.uint8)
+    has = fin.any(-1)
+    first = fin8.argmax(-1)                      # first maximum: the first finite column
+    end = sk - fin8.flip(-1).argmax(-1)          # one past the last finite column
+    zero = torch.zeros_like(first)
+    starts = torch.where(has, first, zero).to(torch.int32)
+    ends = torch.where(has, end, zero).to(torch.int32)
+    return starts.expand(b, sq), ends.expand(b, sq)
+
+
+def drop_masked_picks(scores, idx):
+    """Picks whose score is -inf (an interior hole of a masked row that the
+    window held fewer finite columns than topk around) become -1, and the
+    remaining columns stay ascending with the -1 padding at the end."""
+    sel = scores.gather(-1, idx.clamp(min=0).to(torch.int64))
+    big = torch.iinfo(torch.int32).max
+    key = torch.where((idx < 0) | torch.isneginf(sel), torch.full_like(idx, big), idx)
+    key = key.sort(dim=-1).values
+    return torch.where(key == big, torch.full_like(key, -1), key)
+
+
 def fused_qk_topk_naive(q, k, weights, index_topk, mask=None, varlen_starts=None, varlen_ends=None,
                         key_positions=None, use_relu=True):
-    """Megatron-compatible (scores [b,sq,sk] f32, topk_indices [b,sq,topk] int64).
+    """Megatron ``fused_qk_topk_naive`` on gfx950 -> (scores [b,sq,sk] f32, indices [b,sq,k] int64).
 
-    mask=None scores every key (no causal window), as Megatron does; a float
-    additive mask [sq, sk] (0 / -inf) restricts each row to its finite entries,
-    which must form one contiguous window per row (causal or sliding); varlen
-    starts / ends give the windows directly.  Rows with fewer candidates than
-    topk are padded with -1.
+    k = min(index_topk, sq), the reference's ``min(index_topk, seqlen)`` with
+    seqlen = q.size(0) (scripts/modal_dsa_indexer_bench.py:188-194); the call
+    shapes are Megatron's (cppmega/megatron/lemyx_dsa_warmup.py:169-176,
+    index_cache_patch.py:148-153).
+
+    * mask=None, no varlen: every key is a candidate; scores are the unmasked
+      indexer scores.
+    * mask: an additive float mask broadcastable to [b, sq, sk] (0 / -inf, or
+      any finite bias): the scores returned are ``index_scores + mask``; the
+      candidates of a row are its finite-mask columns.
+    * varlen_starts / varlen_ends (one per query row): the candidates of row t
+      are the keys whose position lies in [start_t, end_t); a key's position
+      is its column, or key_positions[s] (shape [sk] or [b, sk]) when given.
+      Scores outside are -inf.
+
+    Selection is deterministic (ties to the lower column), the chosen columns
+    ascend, and a row with fewer candidates than k is padded with -1.  Key
+    tiles outside every row window of a query block are not computed, so a
+    causal mask costs the lower-triangle work.  Everything runs on the device:
+    no host synchronisation, so the call can be captured in a graph.
+    Parity unpinned against Megatron's own masking (not vendored): the
+    candidate sets above are this build's contract.
     """
-    if key_positions is not None:
-        raise NotImplementedError("key_positions remapping is not supported by the gfx950 top-k")
-    scores = index_scores(q, weights, k, use_relu=use_relu, causal=CAUSAL_NONE)
-    b, sq, sk = scores.shape
-    if varlen_starts is not None or varlen_ends is not None:
-        starts = varlen_starts.to(torch.int32).expand(b, sq).contiguous()
-        ends = varlen_ends.to(torch.int32).expand(b, sq).contiguous()
-        idx = topk_indices(scores, index_topk, causal=False, starts=starts, ends=ends)
-    elif mask is not None:
-        finite = torch.isfinite(mask.float()).reshape(-1, sq, sk)
-        cols = torch.arange(sk, device=scores.device)
-        has = finite.any(-1)
-        first = torch.where(has, torch.where(finite, cols, sk).amin(-1), torch.zeros_like(cols[:1]))
-        last = torch.where(has, torch.where(finite, cols, -1).amax(-1) + 1, torch.zeros_like(cols[:1]))
-        span_ok = (finite.sum(-1) == (last - first)).all()
-        if not bool(span_ok):
-            raise ValueError("mask rows must be contiguous windows of finite entries")
-        idx = topk_indices(scores, index_topk, causal=False,
-                           starts=first.expand(b, sq).contiguous(), ends=last.expand(b, sq).contiguous())
+    sq, b = int(q.shape[0]), int(q.shape[1])
+    sk = int(k.shape[0])
+    topk_k = min(int(index_topk), sq)
+    varlen = varlen_starts is not None or varlen_ends is not None
+    if mask is None and not varlen:
+        scores = index_scores(q, weights, k, use_relu=use_relu, causal=CAUSAL_NONE)
+        return scores, topk_indices(scores, topk_k, causal=False).to(torch.int64)
+    dev = q.device
+    add = None if mask is None else mask.to(device=dev, dtype=torch.float32)
+    if varlen:
+        assert varlen_starts is not None and varlen_ends is not None, "give both varlen_starts and varlen_ends"
+        vs = _row_windows(varlen_starts.to(dev), b, sq, "varlen_starts")
+        ve = _row_windows(varlen_ends.to(dev), b, sq, "varlen_ends")
+    if add is not None:
+        add = add.reshape(-1, sq, sk)                                                # [1 or b, sq, sk]
+    if varlen and key_positions is not None:
+        # a key's position need not be its column: the windows become an additive mask
+        kp = key_positions.to(device=dev, dtype=torch.int64).reshape(-1, 1, sk)    # [1 or b, 1, sk]
+        ok = (kp >= vs.unsqueeze(-1)) & (kp < ve.unsqueeze(-1))                    # [b, sq, sk]
+        kmask = torch.zeros(ok.shape, dtype=torch.float32, device=dev).masked_fill_(~ok, float("-inf"))
+        add = kmask if add is None else add + kmask
+        starts, ends = mask_windows(add, b, sq, sk)
+    elif add is not None:
+        starts, ends = mask_windows(add, b, sq, sk)
+        if varlen:
+            starts, ends = torch.maximum(starts, vs), torch.minimum(ends, ve)
     else:
-        idx = topk_indices(scores, index_topk, causal=False)
+        starts, ends = vs, ve
+    starts, ends = starts.contiguous(), ends.contiguous()
+    scores = index_scores(q, weights, k, use_relu=use_relu, causal=CAUSAL_WINDOW, starts=starts, ends=ends,
+                          mask=add)
+    idx = topk_indices(scores, topk_k, causal=False, starts=starts, ends=ends)
+    if add is not None:
+        idx = drop_masked_picks(scores, idx)
     return scores, idx.to(torch.int64)
 
 
-__all__ = ["CAUSAL_LOWER", "CAUSAL_NEG_INF", "CAUSAL_NONE", "fused_qk_topk_naive", "indexer_topk",
-           "topk_indices"]
+_TOPK_MARKER = "__cppmega_amd_dsa_topk_patched__"
+
+
+def apply_dsa_topk_patch(*, force: bool = False, dsa_module=None) -> bool:
+    """Install this module's ``fused_qk_topk_naive`` as Megatron's
+    ``dsa.fused_qk_topk_naive`` (what DSAttention, the fused indexer loss and
+    IndexCache call: cppmega/megatron/lemyx_dsa_warmup.py:169-176,
+    index_cache_patch.py:148-153).  Idempotent; raises when the attribute is
+    absent (Megatron version mismatch)."""
+    if dsa_module is None:
+        from megatron.core.transformer.experimental_attention_variant import dsa as dsa_module
+    existing = getattr(dsa_module, "fused_qk_topk_naive", None)
+    if existing is None:
+        raise RuntimeError("dsa.fused_qk_topk_naive not found - Megatron version mismatch?")
+    if getattr(existing, _TOPK_MARKER, False) and not force:
+        return True
+
+    def _fused_qk_topk_gfx950(q, k, weights, index_topk, mask=None, varlen_starts=None, varlen_ends=None,
+                              key_positions=None, use_relu=True, **kwargs):
+        return fused_qk_topk_naive(q, k, weights, index_topk, mask=mask, varlen_starts=varlen_starts,
+                                   varlen_ends=varlen_ends, key_positions=key_positions, use_relu=use_relu)
+
+    setattr(_fused_qk_topk_gfx950, _TOPK_MARKER, True)
+    dsa_module.fused_qk_topk_naive = _fused_qk_topk_gfx950
+    return True
+
+
+__all__ = ["CAUSAL_LOWER", "CAUSAL_NEG_INF", "CAUSAL_NONE", "CAUSAL_WINDOW", "apply_dsa_topk_patch",
+           "drop_masked_picks", "fused_qk_topk_naive", "indexer_topk", "mask_windows", "topk_indices"]

@@ -10,10 +10,16 @@ The cache is cleared when the lowest Full rank runs, i.e. once per
 micro-batch (:115-117).
 
 The schedule itself lives in ``IndexCacheSchedule`` (no Megatron needed);
-``apply_index_cache_patch`` wires it into Megatron's ``DSAttention`` as the
-reference does, re-deriving Full-layer indices with this package's
-deterministic gfx950 indexer + top-k (``fused_qk_topk_naive``) instead of
-Megatron's torch one.  Context-parallel gathers go through Megatron's
+``apply_index_cache_patch`` wires it into Megatron's ``DSAttention``.  The
+reference runs a Full layer's original forward and then derives the indices a
+second time (``forward_before_topk`` + an unmasked ``fused_qk_topk_naive``,
+:136-154), because the forward does not expose the ones it computed.  Here the
+Full layer computes them once: while its original forward runs, the dsa
+module's ``fused_qk_topk_naive`` is wrapped so the indices the layer itself
+selected (with its own mask, on its own inputs) are captured and cached.  Only
+when the forward never calls it does the layer fall back to the reference's
+re-derivation, done with this package's deterministic gfx950 indexer + top-k.
+Context-parallel gathers go through Megatron's
 ``gather_from_sequence_parallel_region`` exactly where the reference calls it.
 """
 from __future__ import annotations
@@ -48,6 +54,8 @@ class IndexCacheSchedule:
         self.cache: dict[int, torch.Tensor] = {}
         self.step = -1
         self.promoted: set[int] = set()
+        self.captured = 0    # Full-layer forwards whose own top-k indices were cached
+        self.rederived = 0   # Full-layer forwards that fell back to a second indexer + top-k pass
 
     def set_full_ranks(self, ranks) -> None:
         self.full_ranks = set(ranks)
@@ -154,7 +162,26 @@ def apply_index_cache_patch(force: bool = False, dsa_module=None) -> bool:
                 sched.promote(rank)
                 log.info("IndexCache: DSA rank %d auto-promoted to FULL (no preceding Full rank)", rank)
         if cached is None:
-            result = orig_forward(self, query, key, value, attention_mask, x, qr, **kw)
+            # compute once: keep what the layer's own top-k call returns
+            captured = []
+            inner = getattr(dsa_module, "fused_qk_topk_naive", None)
+            if inner is not None:
+                def _capture(*a, **k):
+                    res = inner(*a, **k)
+                    captured.append(res[1])
+                    return res
+
+                dsa_module.fused_qk_topk_naive = _capture
+            try:
+                result = orig_forward(self, query, key, value, attention_mask, x, qr, **kw)
+            finally:
+                if inner is not None:
+                    dsa_module.fused_qk_topk_naive = inner
+            if captured:
+                sched.store(rank, captured[-1].detach())
+                sched.captured += 1
+                return result
+            sched.rederived += 1
             with torch.no_grad():
                 q_idx, k_idx, w_idx = self.indexer.forward_before_topk(x.detach(), qr.detach(), packed_seq_params)
                 cp_group, cp_size, _ = _cp_info(self.indexer)

@@ -1,8 +1,6 @@
 """Shared host-side helpers of the SparseMLA entry points."""
 from __future__ import annotations
 
-import os
-
 import torch
 
 from .. import _lib
@@ -16,18 +14,6 @@ def normalize_sm_scale(sm_scale, d_qk: int) -> float:
     if isinstance(sm_scale, torch.Tensor):
         return float(sm_scale.detach().item())
     return float(sm_scale)
-
-
-def env_int(name: str, default: int) -> int:
-    """Same parsing as the reference's _env_int (tilelang_sparse_mla_fwd.py:43-51)."""
-    value = os.getenv(name)
-    if value is None:
-        return default
-    try:
-        parsed = int(value)
-    except ValueError:
-        return default
-    return parsed if parsed > 0 else default
 
 
 def unwrap_quantized(t):

@@ -145,6 +145,28 @@ int dsa_indexer_scores(const void *q, const void *w, const void *k,
                        int use_relu, void *stream);
 
 /*
+ * DSA indexer scores restricted to per-row windows, with Megatron's additive
+ * mask: the scores fused_qk_topk_naive ranks when it is given a mask or varlen
+ * windows (call shapes cppmega/megatron/lemyx_dsa_warmup.py:169-176,
+ * cppmega/megatron/index_cache_patch.py:148-153):
+ *   scores[b, t, s] = sum_h w * act(q . k) + mask[b, t, s]   for starts[b, t] <= s < ends[b, t]
+ *                   = -inf                                    elsewhere.
+ *   q, w, k, scores, dtype, w_dtype, q_scale, k_scale, use_relu as in
+ *   dsa_indexer_scores; starts, ends [B, Sq] int32 (device);
+ *   mask [Mb, Sq, Sk] f32 with batch stride mask_bstride elements (0: one mask
+ *   shared by every batch) or NULL (no additive term).
+ * Key tiles outside every window of a group of query tokens are not computed,
+ * so a causal window costs the lower-triangle work.  Every element is written.
+ */
+int dsa_indexer_scores_masked(const void *q, const void *w, const void *k,
+                              float *scores, int64_t B, int64_t Sq, int64_t Sk,
+                              int64_t H, int64_t D, int dtype, int w_dtype,
+                              const float *q_scale, const float *k_scale,
+                              const int32_t *starts, const int32_t *ends,
+                              const float *mask, int64_t mask_bstride,
+                              int use_relu, void *stream);
+
+/*
  * Per-row top-k selection over fp32 scores.
  * Replaces the top-k of Megatron `fused_qk_topk_naive`
  *   (restated in scripts/modal_dsa_indexer_bench.py:188-194) with a stricter,

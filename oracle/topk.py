@@ -24,12 +24,15 @@ def causal_windows(rows, seq_q, row_len, offset=0):
     return np.zeros(rows, dtype=np.int64), np.maximum(ends, 0)
 
 
-def topk_ascending(scores, topk, starts=None, ends=None):
+def topk_ascending(scores, topk, starts=None, ends=None, admissible=None):
     """scores [rows, n] float32 -> idx [rows, topk] int32 (ascending, -1 padded).
 
     Vectorised: one stable descending sort by score keeps the lower column first
     among equal scores; the window is enforced by a second stable sort on an
-    out-of-window flag.
+    out-of-window flag.  `admissible` ([rows, n] bool, optional) further
+    restricts the candidates to its True columns inside the window: the
+    finite-mask columns of a row that Megatron's fused_qk_topk_naive ranks
+    after adding its mask (call shape cppmega/megatron/lemyx_dsa_warmup.py:169-176).
     """
     scores = np.asarray(scores, dtype=np.float32)
     rows, n = scores.shape
@@ -41,13 +44,15 @@ def topk_ascending(scores, topk, starts=None, ends=None):
     ends = np.asarray(ends, dtype=np.int64)
     col = np.arange(n)[None, :]
     inwin = (col >= starts[:, None]) & (col < ends[:, None])
+    if admissible is not None:
+        inwin = inwin & np.asarray(admissible, dtype=bool)
     key = np.where(np.isnan(scores), np.float32(np.inf), scores).astype(np.float64)
     key = key + 0.0  # -0.0 -> +0.0
     order = np.argsort(-key, axis=1, kind="stable")
     flag = (~np.take_along_axis(inwin, order, axis=1)).astype(np.int8)
     order2 = np.argsort(flag, axis=1, kind="stable")
     order = np.take_along_axis(order, order2, axis=1)
-    nvalid = np.clip(ends - starts, 0, None)
+    nvalid = inwin.sum(axis=1)
     count = np.minimum(nvalid, topk)
     out = np.full((rows, topk), -1, dtype=np.int32)
     kk = min(topk, n)
@@ -60,8 +65,9 @@ def topk_ascending(scores, topk, starts=None, ends=None):
     return out
 
 
-def topk_bruteforce_row(row, topk, start=0, end=None):
-    """Pure-Python reference for one row (tiny rows only)."""
+def topk_bruteforce_row(row, topk, start=0, end=None, admissible=None):
+    """Pure-Python reference for one row (tiny rows only); `admissible` is an
+    optional per-column bool list restricting the candidates."""
     n = len(row)
     end = n if end is None else end
 
@@ -71,7 +77,8 @@ def topk_bruteforce_row(row, topk, start=0, end=None):
             v = float("inf")
         return (-v, i)
 
-    cand = sorted(range(start, max(start, end)), key=k)[:topk]
+    cols = [i for i in range(start, max(start, end)) if admissible is None or admissible[i]]
+    cand = sorted(cols, key=k)[:topk]
     cand.sort()
     return cand + [-1] * (topk - len(cand))
 

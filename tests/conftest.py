@@ -26,9 +26,9 @@ def dev():
     if not torch.cuda.is_available():
         pytest.skip("no GPU visible")
     from cppmega_amd import _lib
-    from cppmega_amd.build_lib import sources
+    from cppmega_amd.build_lib import deps
     lib_mtime = os.path.getmtime(_lib.LIB_PATH)
-    stale = [s for s in sources() if os.path.getmtime(s) > lib_mtime + 1]
+    stale = [s for s in deps() if os.path.getmtime(s) > lib_mtime + 1]
     assert not stale, f"libdsa_hip.so is older than {stale}: rebuild before running GPU tests"
     _lib.load()
     return torch.device("cuda", 0)

@@ -58,6 +58,7 @@ def _check_grad(got, ref, what, zeros=True):
     (200, 300, 1, 8, 8, 128, 40, 5),     # sk > sq, sk % 4 != 0 (scalar paths), partial blocks
     (160, 160, 1, 8, 2, 192, 24, 6),     # grouped key heads, 64-key chunks
     (96, 130, 1, 4, 4, 256, 8, 7),       # hn = 256
+    (300, 150, 2, 4, 1, 64, 16, 9),      # sk < sq: rows t >= sk clamp their last key to sk - 1
 ])
 def test_grad_matches_oracle(dev, sparse, sq, sk, b, np_, g, hn, topk, seed):
     query, key, sc = _inputs(sq, sk, b, np_, hn, seed, g=g)

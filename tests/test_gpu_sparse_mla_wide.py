@@ -152,12 +152,16 @@ def test_wide_edge_indices(dev):
     assert torch.all(dq[0, 5] == 0)
 
 
-@pytest.mark.parametrize("outliers,H", [(False, 32), (True, 32), (False, 96)])
-def test_wide_fp8_fwd_bwd_match_fp8_oracle(dev, outliers, H):
+@pytest.mark.parametrize("outliers,H,dv", [(False, 32, DV), (True, 32, DV), (False, 96, DV), (False, 32, D),
+                                           (False, 96, D)])
+def test_wide_fp8_fwd_bwd_match_fp8_oracle(dev, outliers, H, dv):
     """e4m3 wide forward and backward vs the FP8 oracle on identical quantised inputs.  With
     1% x20 outliers a one-ulp bf16 rounding flip of a P weight (from fp32
     reassociation of a 576-term score) is multiplied by a ~20-sigma V entry, so
-    out is held to the mostly-close bar there; LSE keeps the plain bar."""
+    out is held to the mostly-close bar there; LSE keeps the plain bar.  d_v = 576
+    (V the whole row) runs with one head tile (H = 32) and with two tiles per
+    workgroup, the second one empty (H = 96)."""
+    DV = dv
     B, S, topk = 1, 96, 64
     if outliers:
         q = synthetic.outlier_values((B, S, H, D), 77).to(torch.bfloat16)
@@ -213,9 +217,12 @@ def test_cfg5_fwd_full_scale(dev):
     assert_close(lse[:, toks], rl, what="cfg5 lse2 (sampled)")
 
 
-def test_wide_default_dv_is_whole_row(dev):
-    """d_v=None means d_v = d_qk (sparse_mla.py:386-387): V is the whole 576-dim row."""
-    B, S, H, topk = 1, 64, 16, 40
+@pytest.mark.parametrize("H", [16, 96])
+def test_wide_default_dv_is_whole_row(dev, H):
+    """d_v=None means d_v = d_qk (sparse_mla.py:386-387): V is the whole 576-dim row.
+    H = 96 takes the two-tile forward (64 heads per workgroup) with an empty
+    second tile in the last workgroup of each token."""
+    B, S, topk = 1, 64, 40
     inp = synthetic.sparse_mla_inputs(B, S, H, D, D, topk, std=0.5, seed=31)
     q = inp["q"].to(dev).requires_grad_()
     kv = inp["kv"].to(dev).requires_grad_()

@@ -195,6 +195,48 @@ def test_index_cache_patch_full_shared_promote(monkeypatch):
     assert picks and not any(picks)            # relu defaults to the config's False, as the reference
 
 
+def test_index_cache_full_layer_computes_indices_once(monkeypatch):
+    """When the Full layer's own forward calls the dsa module's
+    fused_qk_topk_naive (as Megatron's DSAttention does), IndexCache caches the
+    indices of that call: no second indexer + top-k pass, and the Shared layers
+    get exactly the Full layer's (masked) picks."""
+    monkeypatch.setenv("CPPMEGA_INDEX_CACHE_FULL_LAYERS", "0,3")
+    monkeypatch.setattr(icp, "_SCHEDULE", None)
+
+    def rederive(*a, **k):
+        raise AssertionError("the Full layer must not run a second indexer + top-k pass")
+
+    monkeypatch.setattr(icp, "fused_qk_topk_naive", rederive)
+    calls = []
+    mod = _fake_dsa_module(calls)
+    topk_calls = []
+
+    def module_topk(q, k, w, topk, mask=None, **kw):
+        topk_calls.append(int(q))
+        return None, torch.tensor([int(q), -1])
+
+    mod.fused_qk_topk_naive = module_topk
+
+    def forward(self, query, key, value, attention_mask, x, qr, **kw):
+        _, idx = mod.fused_qk_topk_naive(x, qr, None, 2, mask="causal")   # Megatron's own call
+        calls.append(("full", self._ic_dsa_rank))
+        return "full-out"
+
+    mod.DSAttention.forward = forward
+    assert icp.apply_index_cache_patch(dsa_module=mod)
+    layers = [mod.DSAttention(i) for i in range(6)]
+    q4 = torch.zeros(4, 1, 2, 8)
+    outs = [layer.forward(q4, q4, None, None, torch.tensor(10 + i), torch.tensor(0), None)
+            for i, layer in enumerate(layers)]
+    assert outs == ["full-out", "shared-out", "shared-out", "full-out", "shared-out", "shared-out"]
+    assert topk_calls == [10, 13]                       # one top-k per Full layer
+    shared = [c[1].tolist() for c in calls if c[0] == "shared"]
+    assert shared == [[10, -1], [10, -1], [13, -1], [13, -1]]
+    assert mod.fused_qk_topk_naive is module_topk        # the wrapper is removed after the forward
+    sched = icp.get_schedule()
+    assert sched.captured == 2 and sched.rederived == 0
+
+
 # ---------------------------------------------------------------------------
 # bench.py: one GPU only
 # ---------------------------------------------------------------------------

@@ -117,6 +117,48 @@ def test_topk_property_bruteforce(row, k, data):
     assert len(sel) == min(k, end - start) and all(start <= i < end for i in sel)
 
 
+@settings(max_examples=200, deadline=None)
+@given(st.lists(st.tuples(_score, st.booleans()), min_size=1, max_size=40), st.integers(1, 45), st.data())
+def test_topk_admissible_property_bruteforce(cells, k, data):
+    """Admissible-set restriction (the masked candidates of fused_qk_topk_naive)
+    against the pure-Python brute force, inside random windows."""
+    n = len(cells)
+    row = [c[0] for c in cells]
+    adm = [c[1] for c in cells]
+    start = data.draw(st.integers(0, n))
+    end = data.draw(st.integers(start, n))
+    arr = np.array([row], dtype=np.float32)
+    out = otk.topk_ascending(arr, k, np.array([start]), np.array([end]), admissible=np.array([adm]))[0]
+    assert list(out) == otk.topk_bruteforce_row(arr[0], k, start, end, admissible=adm)
+    sel = [i for i in out if i >= 0]
+    assert len(sel) == min(k, sum(adm[start:end])) and all(adm[i] for i in sel)
+
+
+def test_mask_windows_and_masked_pick_repair():
+    """Host-side pieces of the sync-free fused_qk_topk_naive: per-row spans of the
+    finite mask entries (first / last finite column, (0, 0) for an all -inf row),
+    and the repair that turns picks on -inf holes into trailing -1 padding."""
+    import torch
+    from cppmega_amd.dsa_topk import drop_masked_picks, mask_windows
+
+    ninf = float("-inf")
+    m = torch.tensor([[0, 0, ninf, ninf],          # prefix
+                      [ninf, 0, ninf, 0],          # span with a hole
+                      [ninf, ninf, ninf, ninf],    # nothing admissible
+                      [ninf, ninf, ninf, 0.5]])    # last column only, finite bias
+    st_, en_ = mask_windows(m, 2, 4, 4)
+    assert st_.shape == (2, 4) and st_.dtype == torch.int32
+    assert st_[1].tolist() == [0, 1, 0, 3] and en_[0].tolist() == [2, 4, 0, 4]
+    causal = torch.full((5, 5), ninf).triu(1)
+    cs, ce = mask_windows(causal, 1, 5, 5)
+    assert cs[0].tolist() == [0] * 5 and ce[0].tolist() == [1, 2, 3, 4, 5]
+    scores = torch.tensor([[[1.0, ninf, 3.0, ninf, 5.0]]])
+    idx = torch.tensor([[[0, 1, 2, 3]]], dtype=torch.int32)
+    assert drop_masked_picks(scores, idx).tolist() == [[[0, 2, -1, -1]]]
+    idx = torch.tensor([[[4, -1, -1]]], dtype=torch.int32)
+    assert drop_masked_picks(scores, idx).tolist() == [[[4, -1, -1]]]
+
+
 # ---------------------------------------------------------------------------
 # FP8 e4m3fn
 # ---------------------------------------------------------------------------
