@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "dsa_topk",
     "dsa_fp8_quantize_workspace_size",
     "dsa_fp8_tensorwise_quantize",
+    "dsa_fp8_tensorwise_quantize_noalloc",
     "dsa_fp8_dequantize",
     "dsa_fp8_dequantize_blockwise",
     "dsa_indexer_kl_loss_workspace_size",
@@ -82,6 +83,7 @@ _SIGNATURES = {
     "dsa_fp8_quantize_workspace_size": (_size_t, []),
     "dsa_fp8_tensorwise_quantize": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p,
                                            _c_void_p, _size_t, _c_void_p]),
+    "dsa_fp8_tensorwise_quantize_noalloc": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _c_void_p]),
     "dsa_fp8_dequantize": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _i32, _c_void_p]),
     "dsa_fp8_dequantize_blockwise": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i32, _c_void_p]),
     "dsa_indexer_kl_loss_workspace_size": (_size_t, [_i64] * 5 + [_i32]),

@@ -10,11 +10,20 @@
 // (round-to-nearest-even, saturating at +-448).  dsa_fp8_dequantize is the
 // inverse view (code value * scale_inv, the reference's Float8Tensor
 // dequantize) through the hardware e4m3 conversion the SparseMLA kernels use.
+#include <mutex>
+
 #include "dsa_common.hpp"
 
 namespace dsa {
 
 constexpr int kQuantBlocks = 1024;
+constexpr int kQuantScratchFloats = kQuantBlocks + 64;  // block maxima, then the scale
+
+// Scratch of dsa_fp8_tensorwise_quantize_noalloc: one copy per GPU, held
+// until the process ends.  Host code never uses this name as an address (it
+// is a host-side stand-in there); it uses the per-device pointer that
+// hipGetSymbolAddress returns below.
+static __device__ __align__(256) float scratch[kQuantScratchFloats];
 
 __device__ __forceinline__ float load_elem(const void *x, int64_t i, int bf16) {
   return bf16 ? bf16_bits_to_f32(static_cast<const uint16_t *>(x)[i]) : static_cast<const float *>(x)[i];
@@ -163,7 +172,7 @@ __global__ void __launch_bounds__(256) dequantize_kernel(const uint8_t *x, int64
 
 using namespace dsa;
 
-extern "C" size_t dsa_fp8_quantize_workspace_size(void) { return (kQuantBlocks + 64) * sizeof(float); }
+extern "C" size_t dsa_fp8_quantize_workspace_size(void) { return kQuantScratchFloats * sizeof(float); }
 
 extern "C" int dsa_fp8_tensorwise_quantize(const void *x, int64_t n, int in_dtype, uint8_t *out_fp8,
                                            float *scale_inv, void *workspace, size_t workspace_bytes,
@@ -194,6 +203,43 @@ extern "C" int dsa_fp8_tensorwise_quantize(const void *x, int64_t n, int in_dtyp
     hipLaunchKernelGGL(quantize_kernel, dim3((unsigned)qb), dim3(256), 0, st, x, n, bf16, vec, ws_scale, out_fp8);
   }
   return check_launch("fp8_tensorwise_quantize");
+}
+
+// Device address of `scratch` on the current device, looked up once per device.
+static int quant_scratch(float **out) {
+  static std::mutex mu;
+  static float *addr[64] = {nullptr};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(DSA_ERR_HIP, "dsa_fp8_tensorwise_quantize_noalloc: hipGetDevice: %s",
+                                        hipGetErrorString(e));
+  if (dev < 0 || dev >= 64) return set_error(DSA_ERR_UNSUPPORTED, "dsa_fp8_tensorwise_quantize_noalloc: device %d", dev);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(DSA_ERR_HIP, "dsa_fp8_tensorwise_quantize_noalloc: hipGetSymbolAddress(scratch): %s",
+                       hipGetErrorString(e));
+    addr[dev] = static_cast<float *>(p);
+  }
+  *out = addr[dev];
+  return DSA_OK;
+}
+
+extern "C" int dsa_fp8_tensorwise_quantize_noalloc(const void *x, int64_t n, int in_dtype, uint8_t *out_fp8,
+                                                   float *scale_inv, void *stream) {
+  static_assert(sizeof(scratch) >= kQuantScratchFloats * sizeof(float), "scratch holds the quantiser workspace");
+  const size_t need = dsa_fp8_quantize_workspace_size();
+  if (need > sizeof(scratch))
+    return set_error(DSA_ERR_WORKSPACE, "dsa_fp8_tensorwise_quantize_noalloc: needs %zu scratch bytes, the "
+                                        "static scratch holds %zu", need, sizeof(scratch));
+  float *ws = nullptr;
+  const int rc = quant_scratch(&ws);
+  if (rc) return rc;
+  // Every element of the scratch that a call reads is written earlier in the
+  // same call (block maxima, then the scale), so nothing needs clearing.
+  return dsa_fp8_tensorwise_quantize(x, n, in_dtype, out_fp8, scale_inv, ws, sizeof(scratch), stream);
 }
 
 static int dequantize(const uint8_t *x_fp8, int64_t n, const float *scale_inv, int64_t block, void *out,

@@ -203,6 +203,21 @@ int dsa_fp8_tensorwise_quantize(const void *x, int64_t n, int in_dtype,
                                 void *stream);
 
 /*
+ * dsa_fp8_tensorwise_quantize without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * Same arguments, result and error behaviour as dsa_fp8_tensorwise_quantize;
+ * the scratch comes from a static device array of
+ * dsa_fp8_quantize_workspace_size() bytes (4352) that each GPU holds until
+ * the process ends, so every n is accepted.  The call allocates nothing.
+ * Calls that overlap on one GPU (different streams) share that scratch and
+ * race; serialise them on one stream.
+ */
+int dsa_fp8_tensorwise_quantize_noalloc(const void *x, int64_t n, int in_dtype,
+                                        uint8_t *out_fp8, float *scale_inv,
+                                        void *stream);
+
+/*
  * e4m3 dequantisation: out[i] = value(x_fp8[i]) * scale_inv[0] (bf16 RNE or f32).
  * Replaces Float8Tensor.dequantize() (the TE tensors whose _data / _scale_inv
  *   cppmega's SparseMLA_FP8 unpacks, cppmega/megatron/sparse_mla_ops/sparse_mla.py:310-353);
