@@ -268,6 +268,7 @@ def measure_indexer_kl(dev, reps=5):
     Times are HIP-graph replays."""
     import torch
 
+    from cppmega_amd import synthetic
     from cppmega_amd.dsa_index_mask import topk_index_mask
     from cppmega_amd.dsa_splitk_indexer_loss import indexer_kl_loss, indexer_kl_loss_backward
 
@@ -295,6 +296,20 @@ def measure_indexer_kl(dev, reps=5):
         tf = fl / t / 1e12
         res[mode] = {"ms": round(t * 1e3, 3), "bound": "mfma", "tflops": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
                      "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
+    # the indexer's own backward at cfg3 (b=2, s=4096, h=16, d=64, causal): gradient of
+    # the scores -> dq, dw, dk; algorithmic work = the dq and dk products over the
+    # causal pairs (the reference's autograd reuses its saved logits; this build
+    # recomputes them in both kernels, which is not credited)
+    from cppmega_amd.dsa_indexer_fused_patch import index_scores_backward
+    ii = synthetic.indexer_inputs(B, S, H_IDX, D_IDX, seed=1235)
+    iq, ik, iw = ii["q"].to(dev), ii["k"].to(dev), (ii["w"] * (H_IDX ** 0.5) / 4.0).to(dev)
+    gsc = torch.randn((B, S, S), generator=gen, device=dev) * 1e-3
+    t = med_time(lambda: index_scores_backward(gsc, iq, iw, ik, use_relu=True, causal=True))
+    fl_bwd = 2 * (2 * B * H_IDX * D_IDX * (S * (S + 1) // 2))
+    res["indexer_scores_backward"] = {"ms": round(t * 1e3, 4), "bound": "mfma", "tflops": round(fl_bwd / t / 1e12, 1),
+                                      "peak": PEAK_BF16_TFLOPS, "frac": round(fl_bwd / t / 1e12 / PEAK_BF16_TFLOPS, 4),
+                                      "shape": f"b={B} s={S} h={H_IDX} d={D_IDX} causal"}
+    del gsc, iq, ik, iw
     # the sparse loss's dense [b, s, s] top-k mask, built in one pass (HBM: the
     # f32 mask written once, the int64 indices read once)
     mask = torch.empty((B, S, S), dtype=torch.float32, device=dev)

@@ -44,6 +44,7 @@ FILE_FLAGS = {
     "sparse_mla_bwd.hip": _MFMA_VGPR,
     "sparse_mla_wide.hip": _MFMA_VGPR,
     "indexer_kl_loss.hip": _MFMA_VGPR,
+    "indexer_bwd.hip": _MFMA_VGPR,
 }
 
 

@@ -11,6 +11,13 @@ head; here one MFMA kernel computes every head and reduces over heads in
 registers, writing each score once.  ``index_scores`` adds the causal modes the
 fused top-k path uses (entries above the diagonal written as -inf or not at
 all) and the e4m3 form with per-tensor scales.
+
+The reference's loop is plain torch, so autograd carries the indexer's
+gradient (from Megatron's KL loss) back to q, weights and k.  Here
+``compute_index_scores_fused_bf16`` returns a tensor with that history whenever
+grad mode is on and an input requires grad: ``IndexScores`` runs the forward
+kernel and, in backward, ``index_scores_backward`` (two MFMA kernels that
+recompute q.k, dsa_indexer_scores_backward).
 """
 from __future__ import annotations
 
@@ -22,7 +29,8 @@ from . import _lib
 
 log = logging.getLogger(__name__)
 
-__all__ = ["apply_dsa_indexer_fused_patch", "compute_index_scores_fused_bf16", "index_scores"]
+__all__ = ["IndexScores", "apply_dsa_indexer_fused_patch", "compute_index_scores_fused_bf16", "index_scores",
+           "index_scores_backward"]
 
 _PATCH_MARKER = "__cppmega_amd_dsa_indexer_fused_patched__"
 
@@ -95,17 +103,86 @@ def index_scores(q, weights, k, use_relu=True, causal=CAUSAL_NONE, q_scale=None,
     return out
 
 
+def index_scores_backward(grad, q, weights, k, use_relu=True, causal=False):
+    """Gradients of ``index_scores`` (bf16 q / k) for grad = d loss / d scores
+    [b, sq, sk]: returns (dq [sq,b,h,d] bf16, dweights [sq,b,h] in weights'
+    dtype, dk [sk,b,d] bf16).  causal=True ignores grad above the diagonal
+    (the entries a lower-triangle forward never wrote)."""
+    sq, b, h, d = q.shape
+    sk = k.shape[0]
+    assert q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16, \
+        f"the indexer backward takes bf16 q / k, got {q.dtype}/{k.dtype}"
+    assert tuple(grad.shape) == (b, sq, sk), f"grad {tuple(grad.shape)} != {(b, sq, sk)}"
+    if weights.dtype not in (torch.float32, torch.bfloat16):
+        weights = weights.float()
+    grad = grad.to(torch.float32).contiguous()
+    q, k, weights = q.contiguous(), k.contiguous(), weights.contiguous()
+    dq = torch.empty_like(q)
+    dw = torch.empty_like(weights)
+    dk = torch.empty_like(k)
+    dev = _lib.ensure_device(q)
+    lib = _lib.load()
+    ws_bytes = int(lib.dsa_indexer_scores_backward_workspace_size(b, sq, sk, h, d))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    rc = lib.dsa_indexer_scores_backward(
+        grad.data_ptr(), q.data_ptr(), weights.data_ptr(), k.data_ptr(), dq.data_ptr(), dw.data_ptr(),
+        dk.data_ptr(), b, sq, sk, h, d, _lib.DTYPE_BF16,
+        _lib.DTYPE_F32 if weights.dtype == torch.float32 else _lib.DTYPE_BF16,
+        1 if causal else 0, 1 if use_relu else 0, ws.data_ptr(), ws_bytes, _lib.stream_ptr(dev))
+    _lib.check(rc, "dsa_indexer_scores_backward")
+    return dq, dw, dk
+
+
+class IndexScores(torch.autograd.Function):
+    """Indexer scores with a backward to q, weights and k.
+
+    forward(q, weights, k, use_relu, causal, starts, ends, mask) -> [b, sq, sk]
+    f32 with ``index_scores``' modes (CAUSAL_NONE, CAUSAL_NEG_INF, CAUSAL_LOWER,
+    CAUSAL_WINDOW).  The lower-triangle modes write constants above the
+    diagonal, which carry no gradient (causal backward).  The window mode is
+    Megatron's ``scores + mask``: the raw scores receive the upstream gradient
+    everywhere, masked entries included, as autograd through the add gives
+    them (full backward; the raw scores are recomputed, so entries the forward
+    never computed are no obstacle).
+    """
+
+    @staticmethod
+    def forward(ctx, q, weights, k, use_relu=True, causal=CAUSAL_NONE, starts=None, ends=None, mask=None):
+        out = index_scores(q, weights, k, use_relu=use_relu, causal=causal, starts=starts, ends=ends, mask=mask)
+        ctx.save_for_backward(q, weights, k)
+        ctx.use_relu = use_relu
+        ctx.causal = causal in (CAUSAL_NEG_INF, CAUSAL_LOWER)
+        ctx.wdtype = weights.dtype
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        q, weights, k = ctx.saved_tensors
+        dq, dw, dk = index_scores_backward(grad, q, weights, k, use_relu=ctx.use_relu, causal=ctx.causal)
+        return dq, dw.to(ctx.wdtype), dk, None, None, None, None, None
+
+
+def _needs_grad(*ts):
+    return torch.is_grad_enabled() and any(t.requires_grad for t in ts)
+
+
 def compute_index_scores_fused_bf16(q, weights, k, use_relu: bool = True):
-    """Drop-in for Megatron DSA ``_compute_index_scores`` (bf16): [b, sq, sk] fp32, unmasked."""
+    """Drop-in for Megatron DSA ``_compute_index_scores`` (bf16): [b, sq, sk] fp32,
+    unmasked; differentiable with respect to q, weights and k like the
+    reference's torch loop when grad mode is on and any of them requires grad."""
+    if _needs_grad(q, weights, k):
+        return IndexScores.apply(q, weights, k, use_relu, CAUSAL_NONE)
     return index_scores(q, weights, k, use_relu=use_relu, causal=CAUSAL_NONE)
 
 
-def apply_dsa_indexer_fused_patch(*, force: bool = False) -> bool:
+def apply_dsa_indexer_fused_patch(*, force: bool = False, dsa_module=None) -> bool:
     """Install ``compute_index_scores_fused_bf16`` as Megatron's ``dsa._compute_index_scores``.
 
     Idempotent; raises if the Megatron DSA module or the attribute is absent.
     """
-    from megatron.core.transformer.experimental_attention_variant import dsa as dsa_mod
+    dsa_mod = dsa_module
+    if dsa_mod is None:
+        from megatron.core.transformer.experimental_attention_variant import dsa as dsa_mod
 
     existing = getattr(dsa_mod, "_compute_index_scores", None)
     if existing is None:

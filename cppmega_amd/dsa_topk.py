@@ -14,7 +14,16 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .dsa_indexer_fused_patch import CAUSAL_LOWER, CAUSAL_NEG_INF, CAUSAL_NONE, CAUSAL_WINDOW, index_scores
+from .dsa_indexer_fused_patch import (CAUSAL_LOWER, CAUSAL_NEG_INF, CAUSAL_NONE, CAUSAL_WINDOW, IndexScores,
+                                      index_scores)
+
+
+def _scores(q, weights, k, use_relu, causal, starts=None, ends=None, mask=None):
+    """index_scores, through the differentiable IndexScores when grad mode is on
+    and q, weights or k requires grad (the scores Megatron's loss consumes)."""
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, weights, k)):
+        return IndexScores.apply(q, weights, k, use_relu, causal, starts, ends, mask)
+    return index_scores(q, weights, k, use_relu=use_relu, causal=causal, starts=starts, ends=ends, mask=mask)
 
 
 def topk_indices(scores, topk, causal=True, starts=None, ends=None, causal_offset=0, seq_q=None):
@@ -128,8 +137,8 @@ def fused_qk_topk_naive(q, k, weights, index_topk, mask=None, varlen_starts=None
     topk_k = min(int(index_topk), sq)
     varlen = varlen_starts is not None or varlen_ends is not None
     if mask is None and not varlen:
-        scores = index_scores(q, weights, k, use_relu=use_relu, causal=CAUSAL_NONE)
-        return scores, topk_indices(scores, topk_k, causal=False).to(torch.int64)
+        scores = _scores(q, weights, k, use_relu, CAUSAL_NONE)
+        return scores, topk_indices(scores.detach(), topk_k, causal=False).to(torch.int64)
     dev = q.device
     add = None if mask is None else mask.to(device=dev, dtype=torch.float32)
     if varlen:
@@ -152,11 +161,10 @@ def fused_qk_topk_naive(q, k, weights, index_topk, mask=None, varlen_starts=None
     else:
         starts, ends = vs, ve
     starts, ends = starts.contiguous(), ends.contiguous()
-    scores = index_scores(q, weights, k, use_relu=use_relu, causal=CAUSAL_WINDOW, starts=starts, ends=ends,
-                          mask=add)
-    idx = topk_indices(scores, topk_k, causal=False, starts=starts, ends=ends)
+    scores = _scores(q, weights, k, use_relu, CAUSAL_WINDOW, starts, ends, add)
+    idx = topk_indices(scores.detach(), topk_k, causal=False, starts=starts, ends=ends)
     if add is not None:
-        idx = drop_masked_picks(scores, idx)
+        idx = drop_masked_picks(scores.detach(), idx)
     return scores, idx.to(torch.int64)
 
 

@@ -167,6 +167,35 @@ int dsa_indexer_scores_masked(const void *q, const void *w, const void *k,
                               int use_relu, void *stream);
 
 /*
+ * Backward of dsa_indexer_scores (bf16 q / k): given grad_scores G [B, Sq, Sk] f32,
+ *   dw[t, b, h]    = sum_s G[b, t, s] * act(L)
+ *   dq[t, b, h, :] = w[t, b, h] * sum_s G[b, t, s] * act'(L) * k[s, b, :]
+ *   dk[s, b, :]    = sum_{t, h} G[b, t, s] * w[t, b, h] * act'(L) * q[t, b, h, :]
+ * with L = q[t, b, h, :] . k[s, b, :] recomputed on MFMA (act = ReLU when
+ * use_relu, act' its 0/1 derivative; identity otherwise).  G * act'(L)
+ * (times w for dk) is rounded to bf16 for the MFMA; sums are fp32.
+ * Replaces the autograd backward of compute_index_scores_fused_bf16's
+ * per-head loop (cppmega/megatron/dsa_indexer_fused_patch.py:71-133), the
+ * gradient Megatron's indexer loss sends to the indexer's q, weights and k.
+ *   q [Sq, B, H, D] bf16, w [Sq, B, H] (w_dtype), k [Sk, B, D] bf16;
+ *   dq [Sq, B, H, D] bf16, dw [Sq, B, H] (w_dtype), dk [Sk, B, D] bf16 (written).
+ * causal: 0 = every (t, s); 1 = only s <= t (G above the diagonal ignored).
+ * Deterministic (fixed summation orders, no atomics).  workspace >=
+ * dsa_indexer_scores_backward_workspace_size() bytes (fp32 dk partials per
+ * token chunk).  Limits: Sq * Sk < 2^30, H in {16, 32, 64}, D in {64, 128}.
+ */
+size_t dsa_indexer_scores_backward_workspace_size(int64_t B, int64_t Sq,
+                                                  int64_t Sk, int64_t H,
+                                                  int64_t D);
+int dsa_indexer_scores_backward(const float *grad_scores, const void *q,
+                                const void *w, const void *k, void *dq,
+                                void *dw, void *dk, int64_t B, int64_t Sq,
+                                int64_t Sk, int64_t H, int64_t D, int dtype,
+                                int w_dtype, int causal, int use_relu,
+                                void *workspace, size_t workspace_bytes,
+                                void *stream);
+
+/*
  * Per-row top-k selection over fp32 scores.
  * Replaces the top-k of Megatron `fused_qk_topk_naive`
  *   (restated in scripts/modal_dsa_indexer_bench.py:188-194) with a stricter,

@@ -8,6 +8,8 @@ upcasts q and k to fp32, forms q_h . k with a batched matmul, applies ReLU,
 multiplies by the fp32 head weight and accumulates into a [b, sq, sk] fp32
 buffer.  compute_index_scores_einsum restates the upstream Megatron form
 that the reference test clones (tests/test_dsa_indexer_fused_patch.py:18-30).
+index_scores_backward gives the gradients autograd takes through that loop
+(to q, weights and k), in float64.
 The FP8 form dequantises e4m3 codes with one per-tensor scale for q and one
 for k before the same arithmetic.
 """
@@ -58,6 +60,43 @@ def compute_index_scores_f64(q, weights, k, use_relu=True):
                 logits = logits.clamp_min(0)
             out[bi] += logits * wd[:, bi, hi][:, None]
     return out
+
+
+def index_scores_diff(q, weights, k, use_relu=True):
+    """Differentiable float64 restatement of the reference's per-head loop
+    (cppmega/megatron/dsa_indexer_fused_patch.py:71-133): per head, q_h . k,
+    ReLU, times the head weight, accumulated over heads -> [b, sq, sk].
+    Inputs are used as given (float64 leaves that may require grad)."""
+    sq, b, h, d = q.shape
+    out = None
+    for hi in range(h):
+        logits = torch.einsum("sbd,tbd->bst", q[:, :, hi, :], k)   # [b, sq, sk]
+        if use_relu:
+            logits = torch.relu(logits)
+        term = logits * weights[:, :, hi].transpose(0, 1).unsqueeze(-1)
+        out = term if out is None else out + term
+    return out
+
+
+def index_scores_backward(grad, q, weights, k, use_relu=True, causal=False):
+    """Gradients (dq, dweights, dk) in float64 of the reference's score loop for
+    the upstream gradient `grad` [b, sq, sk], by autograd through
+    index_scores_diff (what autograd through the reference's torch loop
+    computes).  causal=True zeroes grad above the diagonal first (the entries
+    a lower-triangle forward never computed).  Pinned by
+    torch.autograd.gradcheck (finite differences) and a one-head, one-key
+    closed form in tests/test_oracle_indexer_topk_fp8.py."""
+    g = grad.detach().double()
+    if causal:
+        sq, sk = g.shape[-2:]
+        g = g.masked_fill(torch.ones(sq, sk, dtype=torch.bool).triu(1), 0.0)
+    with torch.enable_grad():  # also when called from inside another backward
+        qd = q.detach().double().requires_grad_(True)
+        wd = weights.detach().double().requires_grad_(True)
+        kd = k.detach().double().requires_grad_(True)
+        out = index_scores_diff(qd, wd, kd, use_relu)
+        dq, dw, dk = torch.autograd.grad(out, (qd, wd, kd), grad_outputs=g)
+    return dq, dw, dk
 
 
 def causal_mask_(scores, fill=float("-inf")):

@@ -1,0 +1,149 @@
+"""GPU parity of the indexer backward (dsa_indexer_scores_backward) and of the
+FusedDSAIndexerLoss drop-in that chains it after the KL loss.
+
+Oracle: float64 autograd of the reference's per-head score loop
+(oracle.indexer.index_scores_backward), and for the fused loss float64
+autograd through scores -> KL loss (oracle.indexer_loss).
+
+Bars.  Without ReLU every element of dq, dw, dk is within 2e-2 relative +
+1e-2 of the tensor's largest magnitude (the kernels round G * act'(L) (* w)
+to bf16 before the MFMA; sums are fp32).  With ReLU the same elementwise band
+must hold for all but 0.1% of the elements and the relative L2 error must stay
+below 5e-3: a logit within fp32 rounding of 0 can take the other side of the
+ReLU than in float64, which moves that gradient by one whole term.
+"""
+import numpy as np
+import pytest
+import torch
+
+from cppmega_amd import synthetic
+from cppmega_amd.dsa_fused_indexer_loss import FusedDSAIndexerLoss
+from cppmega_amd.dsa_indexer_fused_patch import (CAUSAL_LOWER, CAUSAL_NONE, IndexScores,
+                                                  compute_index_scores_fused_bf16, index_scores_backward)
+from cppmega_amd.dsa_topk import fused_qk_topk_naive
+from oracle import indexer as oix
+from oracle import indexer_loss as okl
+from oracle import topk as otk
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(got, ref, relu, what):
+    a = got.detach().double().cpu()
+    e = ref.detach().double().cpu()
+    assert a.shape == e.shape, f"{what}: shape {tuple(a.shape)} != {tuple(e.shape)}"
+    scale = float(e.abs().max())
+    bad = (a - e).abs() > 2e-2 * e.abs() + 1e-2 * scale
+    frac = float(bad.double().mean())
+    rel = float((a - e).norm() / e.norm().clamp_min(1e-300))
+    if relu:
+        assert frac <= 1e-3 and rel <= 5e-3, f"{what}: {int(bad.sum())} outside the band (frac {frac:.2e}), rel L2 {rel:.2e}"
+    else:
+        assert not bad.any(), f"{what}: {int(bad.sum())}/{bad.numel()} outside the band, rel L2 {rel:.2e}"
+
+
+def _inputs(S, Sk, B, H, D, wdt, seed):
+    inp = synthetic.indexer_inputs(B, S, H, D, seed=seed, w_dtype=wdt)
+    g = torch.Generator().manual_seed(seed + 1)
+    k = torch.randn((Sk, B, D), generator=g).to(torch.bfloat16) if Sk != S else inp["k"]
+    grad = torch.randn((B, S, Sk), generator=g)
+    return inp["q"], inp["w"], k, grad
+
+
+@pytest.mark.parametrize("S,Sk,B,H,D,wdt,relu,causal", [
+    (128, 128, 2, 16, 64, torch.float32, True, False),
+    (200, 200, 1, 16, 64, torch.float32, True, True),     # partial token blocks and chunks
+    (130, 257, 1, 32, 64, torch.bfloat16, True, False),  # Sk % 4 != 0 (scalar G loads), Sk > Sq
+    (96, 96, 1, 64, 128, torch.float32, False, False),   # d = 128, one tile per wave
+    (160, 100, 2, 32, 128, torch.float32, True, True),   # Sk < Sq
+    (64, 64, 1, 64, 64, torch.bfloat16, False, True),    # h = 64: one token per wave
+    (300, 300, 1, 16, 64, torch.float32, False, True),   # several token chunks of the dk kernel
+])
+def test_indexer_backward_matches_oracle(dev, S, Sk, B, H, D, wdt, relu, causal):
+    q, w, k, grad = _inputs(S, Sk, B, H, D, wdt, seed=S + H + D)
+    dq, dw, dk = index_scores_backward(grad.to(dev), q.to(dev), w.to(dev), k.to(dev), use_relu=relu, causal=causal)
+    assert dq.dtype == torch.bfloat16 and dk.dtype == torch.bfloat16 and dw.dtype == wdt
+    rq, rw, rk = oix.index_scores_backward(grad, q, w, k, use_relu=relu, causal=causal)
+    _check(dq, rq, relu, "dq")
+    _check(dw, rw, relu, "dw")
+    _check(dk, rk, relu, "dk")
+    dq2, dw2, dk2 = index_scores_backward(grad.to(dev), q.to(dev), w.to(dev), k.to(dev), use_relu=relu,
+                                          causal=causal)
+    assert torch.equal(dq, dq2) and torch.equal(dw, dw2) and torch.equal(dk, dk2), "not bitwise reproducible"
+
+
+def test_autograd_through_compute_index_scores(dev):
+    """The Megatron drop-in keeps autograd: grads of a loss over the scores
+    reach q, weights and k and equal the direct backward call."""
+    S, B, H, D = 96, 2, 16, 64
+    q, w, k, grad = _inputs(S, S, B, H, D, torch.float32, seed=5)
+    qd, wd, kd = (t.to(dev).requires_grad_() for t in (q, w, k))
+    out = compute_index_scores_fused_bf16(qd, wd, kd)
+    assert out.grad_fn is not None
+    out.backward(grad.to(dev))
+    dq, dw, dk = index_scores_backward(grad.to(dev), q.to(dev), w.to(dev), k.to(dev))
+    assert torch.equal(qd.grad, dq) and torch.equal(wd.grad, dw) and torch.equal(kd.grad, dk)
+    # the lower-triangle mode's backward is the causal one
+    qd.grad = wd.grad = kd.grad = None
+    low = IndexScores.apply(qd, wd, kd, True, CAUSAL_LOWER)
+    tri = torch.ones(S, S, dtype=torch.bool, device=dev).tril()
+    (low * tri).backward(grad.to(dev))
+    dqc, dwc, dkc = index_scores_backward(grad.to(dev), q.to(dev), w.to(dev), k.to(dev), causal=True)
+    assert torch.equal(qd.grad, dqc) and torch.equal(kd.grad, dkc)
+
+
+def test_cfg3_backward_full_scale(dev):
+    """cfg3 shapes (b=2, s=4096, h=16, d=64, causal): dq / dw of 24 sampled
+    tokens and dk of 12 sampled keys vs the oracle, every output finite."""
+    S, B, H, D = 4096, 2, 16, 64
+    inp = synthetic.indexer_inputs(B, S, H, D, seed=1235)
+    q, w, k = inp["q"], inp["w"] * (H ** 0.5) / 4.0, inp["k"]
+    grad = torch.randn((B, S, S), generator=torch.Generator(device=dev).manual_seed(3), device=dev) * 1e-3
+    dq, dw, dk = index_scores_backward(grad, q.to(dev), w.to(dev), k.to(dev), causal=True)
+    assert torch.isfinite(dq).all() and torch.isfinite(dw).all() and torch.isfinite(dk).all()
+    gc = grad.cpu()
+    toks = torch.tensor([0, 1, 31, 500, 1023, 2047, 2048, 3000, 3333, 4000, 4094, 4095,
+                         7, 15, 16, 255, 256, 777, 1500, 2500, 3071, 3584, 3968, 4064])
+    g_rows = gc[:, toks].masked_fill(torch.arange(S)[None, None, :] > toks[None, :, None], 0.0)
+    rq, rw, _ = oix.index_scores_backward(g_rows, q[toks], w[toks], k, causal=False)
+    _check(dq[toks], rq, True, "dq (sampled tokens)")
+    _check(dw[toks], rw, True, "dw (sampled tokens)")
+    keys = torch.tensor([0, 1, 100, 1024, 2047, 2048, 3000, 4000, 4095, 63, 64, 255])
+    g_cols = gc[:, :, keys].masked_fill(keys[None, None, :] > torch.arange(S)[None, :, None], 0.0)
+    _, _, rk = oix.index_scores_backward(g_cols, q, w, k[keys], causal=False)
+    _check(dk[keys], rk, True, "dk (sampled keys)")
+
+
+@pytest.mark.parametrize("sparse", [False, True], ids=["dense", "sparse"])
+def test_fused_indexer_loss_matches_oracle(dev, sparse):
+    """FusedDSAIndexerLoss.apply with a causal mask: top-k bit-exact with the
+    deterministic top-k of its own scores, the loss against the float64 KL of
+    the float64 scores, and the gradients of q, weights and k against float64
+    autograd through scores -> loss (same top-k set on both sides)."""
+    S, B, H, D, NP, HN, TOPK = 192, 2, 16, 64, 8, 64, 48
+    q, w, k, _ = _inputs(S, S, B, H, D, torch.float32, seed=77)
+    g = torch.Generator().manual_seed(78)
+    query = (torch.randn((S, B, NP, HN), generator=g) * 0.5).to(torch.bfloat16)
+    key = (torch.randn((S, B, NP, HN), generator=g) * 0.5).to(torch.bfloat16)
+    mask = torch.full((S, S), float("-inf")).triu(1)
+    scale, coeff = HN ** -0.5, 0.3
+    qd, wd, kd = (t.to(dev).requires_grad_() for t in (q, w, k))
+    idx, loss = FusedDSAIndexerLoss.apply(qd, wd, kd, query.to(dev), key.to(dev), scale, TOPK, coeff, mask.to(dev),
+                                          sparse, None)
+    assert idx.dtype == torch.int64 and idx.shape == (B, S, TOPK) and loss.dim() == 0
+    loss.backward()
+    sc, ref_idx = fused_qk_topk_naive(q.to(dev), k.to(dev), w.to(dev), TOPK, mask=mask.to(dev))
+    assert torch.equal(idx, ref_idx)
+    adm = torch.isfinite(mask)[None].expand(B, S, S)
+    ref = otk.topk_ascending(sc.cpu().numpy().reshape(B * S, S), TOPK, admissible=adm.reshape(B * S, S).numpy())
+    np.testing.assert_array_equal(idx.cpu().numpy().reshape(B * S, TOPK), ref)
+    # float64 chain: scores (+ mask) -> KL loss -> grads of q, w, k
+    q64, w64, k64 = (t.double().requires_grad_() for t in (q, w, k))
+    s64 = oix.index_scores_diff(q64, w64, k64, True) + mask.double()
+    l64 = okl.compute_dsa_indexer_loss(s64, idx.cpu(), query, key, scale, coeff, sparse)
+    l64.backward()
+    lv, rv = float(loss.detach()), float(l64.detach())
+    assert abs(lv - rv) <= 1e-3 * abs(rv) + 1e-5, (lv, rv)
+    _check(qd.grad, q64.grad, True, "dq through the loss")
+    _check(wd.grad, w64.grad, True, "dw through the loss")
+    _check(kd.grad, k64.grad, True, "dk through the loss")

@@ -237,6 +237,64 @@ def test_index_cache_full_layer_computes_indices_once(monkeypatch):
     assert sched.captured == 2 and sched.rederived == 0
 
 
+def test_index_scores_patch_keeps_autograd(monkeypatch):
+    """compute_index_scores_fused_bf16 (what the Megatron patch installs) returns
+    a tensor with autograd history whenever grad mode is on and q, weights or k
+    requires grad, and its backward runs the indexer backward; without grad it
+    returns a plain tensor.  The HIP launches are replaced by CPU stand-ins
+    (this checks the wiring; the GPU tests check the kernels)."""
+    from cppmega_amd import dsa_indexer_fused_patch as dip
+    from oracle import indexer as oix
+
+    seen = []
+
+    def fake_scores(q, weights, k, use_relu=True, causal=0, **kw):
+        return oix.compute_index_scores(q, weights, k, use_relu)
+
+    def fake_backward(grad, q, weights, k, use_relu=True, causal=False):
+        seen.append((use_relu, causal))
+        dq, dw, dk = oix.index_scores_backward(grad, q, weights, k, use_relu, causal)
+        return dq.to(q.dtype), dw.to(weights.dtype), dk.to(k.dtype)
+
+    monkeypatch.setattr(dip, "index_scores", fake_scores)
+    monkeypatch.setattr(dip, "index_scores_backward", fake_backward)
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(6, 1, 16, 64, generator=g).to(torch.bfloat16).requires_grad_()
+    w = torch.randn(6, 1, 16, generator=g).requires_grad_()
+    k = torch.randn(7, 1, 64, generator=g).to(torch.bfloat16).requires_grad_()
+    out = dip.compute_index_scores_fused_bf16(q, w, k)
+    assert out.requires_grad and out.grad_fn is not None, "the patch must not return a detached tensor"
+    out.sum().backward()
+    assert seen == [(True, False)]
+    assert q.grad is not None and w.grad is not None and k.grad is not None
+    assert q.grad.dtype == torch.bfloat16 and w.grad.dtype == torch.float32
+    with torch.no_grad():
+        plain = dip.compute_index_scores_fused_bf16(q, w, k)
+    assert not plain.requires_grad
+    mod = types.SimpleNamespace(_compute_index_scores=lambda *a, **kw: None)
+    assert dip.apply_dsa_indexer_fused_patch(dsa_module=mod)
+    r = mod._compute_index_scores(q, w, k, use_relu=True)
+    assert r.requires_grad
+
+
+def test_fused_indexer_loss_patch_rebinds_the_module():
+    from cppmega_amd import dsa_fused_indexer_loss as fil
+
+    class Megatrons:
+        @staticmethod
+        def apply(*a, **kw):
+            raise AssertionError("replaced")
+
+    mod = types.SimpleNamespace(FusedDSAIndexerLoss=Megatrons)
+    assert fil.apply_fused_indexer_loss_patch(dsa_module=mod)
+    assert mod.FusedDSAIndexerLoss is fil.FusedDSAIndexerLoss
+    assert fil.apply_fused_indexer_loss_patch(dsa_module=mod)
+    with pytest.raises(RuntimeError):
+        fil.apply_fused_indexer_loss_patch(dsa_module=types.SimpleNamespace())
+    with pytest.raises(NotImplementedError):
+        fil.fused_dsa_indexer_loss(None, None, None, None, None, 0.1, 4, 1.0, query_valid_rows=torch.ones(1))
+
+
 # ---------------------------------------------------------------------------
 # bench.py: one GPU only
 # ---------------------------------------------------------------------------

@@ -54,6 +54,53 @@ def test_indexer_fp8_scales_dequantise():
     assert_close(a, b, rtol=1e-5, atol=1e-4, what="fp8 indexer")
 
 
+@pytest.mark.parametrize("relu", [True, False])
+def test_indexer_backward_oracle_gradcheck(relu):
+    """The float64 score loop is differentiable the way finite differences say
+    (gradcheck), and its autograd gradients match the loop's value at a
+    perturbed point to first order."""
+    g = torch.Generator().manual_seed(7)
+    q = torch.randn(5, 2, 3, 4, generator=g, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(5, 2, 3, generator=g, dtype=torch.float64, requires_grad=True)
+    k = torch.randn(6, 2, 4, generator=g, dtype=torch.float64, requires_grad=True)
+    assert torch.autograd.gradcheck(lambda a, b_, c: oidx.index_scores_diff(a, b_, c, relu), (q, w, k))
+    grad = torch.randn(2, 5, 6, generator=g, dtype=torch.float64)
+    dq, dw, dk = oidx.index_scores_backward(grad, q, w, k, use_relu=relu)
+    assert dq.shape == q.shape and dw.shape == w.shape and dk.shape == k.shape
+    # the float64 loop equals the fp32 oracle restatement's values
+    assert torch.allclose(oidx.index_scores_diff(q, w, k, relu).float(),
+                          oidx.compute_index_scores(q.float(), w.float(), k.float(), relu), atol=1e-5)
+
+
+def test_indexer_backward_closed_form_and_causal():
+    """One head, one query, one key: dq = G w [L > 0] k, dw = G ReLU(L),
+    dk = G w [L > 0] q; a negative logit gives zero dq / dk / dw under ReLU;
+    causal=True drops the gradient above the diagonal."""
+    q = torch.tensor([[[[1.0, 2.0]]]], dtype=torch.float64)          # [1, 1, 1, 2]
+    k = torch.tensor([[[0.5, -0.25]]], dtype=torch.float64)          # [1, 1, 2]
+    w = torch.tensor([[[3.0]]], dtype=torch.float64)
+    G = torch.tensor([[[2.0]]], dtype=torch.float64)
+    L = float((q[0, 0, 0] * k[0, 0]).sum())                        # 0.5 - 0.5 = 0: ReLU' is 0 at 0
+    assert L == 0.0
+    k = torch.tensor([[[0.5, 0.25]]], dtype=torch.float64)
+    L = float((q[0, 0, 0] * k[0, 0]).sum())                        # 1.0
+    dq, dw, dk = oidx.index_scores_backward(G, q, w, k)
+    assert torch.allclose(dq[0, 0, 0], 2.0 * 3.0 * k[0, 0]) and float(dw) == 2.0 * L
+    assert torch.allclose(dk[0, 0], 2.0 * 3.0 * q[0, 0, 0])
+    dq, dw, dk = oidx.index_scores_backward(G, q, w, -k)              # L < 0: ReLU blocks everything
+    assert float(dq.abs().sum() + dw.abs().sum() + dk.abs().sum()) == 0.0
+    gen = torch.Generator().manual_seed(3)
+    q2 = torch.randn(3, 1, 2, 4, dtype=torch.float64, generator=gen)
+    k2 = torch.randn(3, 1, 4, dtype=torch.float64, generator=gen)
+    w2 = torch.randn(3, 1, 2, dtype=torch.float64, generator=gen)
+    G2 = torch.zeros(1, 3, 3, dtype=torch.float64)
+    G2[0, 0, 2] = 1.0                                                 # above the diagonal only
+    dq, dw, dk = oidx.index_scores_backward(G2, q2, w2, k2, use_relu=False, causal=True)
+    assert float(dq.abs().sum() + dw.abs().sum() + dk.abs().sum()) == 0.0
+    dq, dw, dk = oidx.index_scores_backward(G2, q2, w2, k2, use_relu=False, causal=False)
+    assert float(dk[2].abs().sum()) > 0 and float(dk[:2].abs().sum()) == 0.0
+
+
 def test_causal_mask_and_flops():
     s = torch.zeros(2, 4, 4)
     oidx.causal_mask_(s)
