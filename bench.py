@@ -138,7 +138,10 @@ def measure_cfg5(dev, reps=3):
             ts.append(a.elapsed_time(b_))
         return sorted(ts)[len(ts) // 2] / 1e3
 
+    from cppmega_amd.dsa_topk import indexer_topk_streaming
     t = {
+        "indexer_topk_streaming": timed(lambda: indexer_topk_streaming(iq8, ik8, iw, C5_TOPK, q_scale=iqs, k_scale=iks,
+                                                                       max_scratch_bytes=64 << 20)),
         "fwd": timed(lambda: sparse_mla_fwd_interface(q, kv, idx, sm_scale=C5_DQK ** -0.5, d_v=C5_DV)),
         "fwd_mxfp8": timed(lambda: sparse_mla_blockscaled_mxfp8_fwd_interface(qmx, kmx, qbs, kbs, idx,
                                                                               sm_scale=C5_DQK ** -0.5, d_v=C5_DV)),
@@ -146,7 +149,9 @@ def measure_cfg5(dev, reps=3):
                                                   q_scale=iqs, k_scale=iks, out=scores)),
         "topk": timed(lambda: topk_indices(scores, C5_TOPK, causal=True)),
     }
-    res = {}
+    res = {"indexer_topk_streaming": {"ms": round(t["indexer_topk_streaming"] * 1e3, 3),
+                                      "scratch_mib": 64, "note": "e4m3 indexer + top-2048 in 1024-row chunks, "
+                                      "no [1, 16384, 16384] score matrix (dense path: indexer_fp8 + topk)"}}
     for k, (fl, by, kind) in cfg5_work().items():
         e = {"ms": round(t[k] * 1e3, 3)}
         if kind == "fp8+bf16":
@@ -576,6 +581,11 @@ def main():
     t_att = kernels["fwd"]["ms"] + kernels["bwd"]["ms"]
     amortised = 9 * tokens / ((3 * t_idx + 9 * t_att) / 1e3)
 
+    from cppmega_amd.dsa_topk import indexer_topk_streaming
+    t_stream = graph_replay_time(lambda: indexer_topk_streaming(iq, ik, iw, TOPK, max_scratch_bytes=16 << 20))
+    streaming = {"ms": round(t_stream * 1e3, 4), "scratch_mib": 16,
+                 "note": "cfg3 indexer + top-256 in 512-row chunks (no [2, 4096, 4096] score matrix); "
+                         "HIP-graph replays; dense path = kernels.indexer + kernels.topk"}
     cfg5 = None if args.no_cfg5 else measure_cfg5(dev)
     kl = None if args.no_kl else measure_indexer_kl(dev)
     cfg4 = None if args.no_cfg4 else measure_cfg4(dev)
@@ -609,6 +619,7 @@ def main():
         "cpu_baseline": cpu,
         "kernels": kernels,
         "indexcache_amortised_tokens_per_s": round(amortised, 1),
+        "indexer_topk_streaming": streaming,
         "launch": ("hip_graph" if graph_info is not None else "eager"),
         "eager_tokens_per_s": round(eager_tokens_per_s, 1),
         "graph_replays_checked": (graph_info["checked"] if graph_info is not None else 0),

@@ -12,7 +12,7 @@ from .dsa_indexer_fused_patch import (IndexScores, apply_dsa_indexer_fused_patch
                                       index_scores, index_scores_backward)
 from .dsa_index_mask import scatter_topk_into_index_mask, topk_index_mask
 from .dsa_splitk_indexer_loss import compute_dsa_indexer_loss_splitk, indexer_kl_loss, indexer_kl_loss_backward
-from .dsa_topk import apply_dsa_topk_patch, fused_qk_topk_naive, indexer_topk, topk_indices
+from .dsa_topk import apply_dsa_topk_patch, fused_qk_topk_naive, indexer_topk, indexer_topk_streaming, topk_indices
 from .index_cache_patch import IndexCacheSchedule, apply_index_cache_patch
 
 __all__ = [
@@ -32,6 +32,7 @@ __all__ = [
     "indexer_kl_loss",
     "indexer_kl_loss_backward",
     "indexer_topk",
+    "indexer_topk_streaming",
     "scatter_topk_into_index_mask",
     "topk_index_mask",
     "topk_indices",

@@ -41,6 +41,8 @@ EXPORTED_SYMBOLS = (
     "dsa_indexer_scores_masked",
     "dsa_indexer_scores_backward_workspace_size",
     "dsa_indexer_scores_backward",
+    "dsa_indexer_topk_streaming_workspace_size",
+    "dsa_indexer_topk_streaming",
     "dsa_topk",
     "dsa_fp8_quantize_workspace_size",
     "dsa_fp8_tensorwise_quantize",
@@ -82,6 +84,9 @@ _SIGNATURES = {
                                          _i32, _c_void_p]),
     "dsa_indexer_scores_backward_workspace_size": (_size_t, [_i64] * 5),
     "dsa_indexer_scores_backward": (_i32, [_c_void_p] * 7 + [_i64] * 5 + [_i32] * 4 + [_c_void_p, _size_t, _c_void_p]),
+    "dsa_indexer_topk_streaming_workspace_size": (_size_t, [_i64] * 4),
+    "dsa_indexer_topk_streaming": (_i32, [_c_void_p] * 5 + [_i64] * 5 + [_i32, _i32, _c_void_p, _c_void_p, _i64,
+                                                                         _i32, _i32, _c_void_p, _size_t, _c_void_p]),
     "dsa_topk": (_i32, [_c_void_p, _i64, _i64, _i64, _i64, _i32, _i64,
                         _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p]),
     "dsa_fp8_quantize_workspace_size": (_size_t, []),

@@ -42,6 +42,7 @@ struct IdxParams {
   const float *mask;
   int64_t mask_bstride;
   int64_t B, Sq, Sk;
+  int64_t coff;  // causal modes 1 / 2: row t keeps keys s <= t + coff (q starts coff tokens into the sequence)
   int w_f32;
   int causal;
   int relu;
@@ -237,7 +238,7 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
     load_tile(it + 1, kreg);  // past the last tile: keys beyond Sk read 0, unused
     const unsigned char *ks = KS[it & 1];
     const int64_t tk = k0 + (int64_t)it * C::KT;
-    const bool interior = !win && wave_in_sq && tk + C::KT <= k_end && (!p.causal || tk + C::KT - 1 <= wave_tok0);
+    const bool interior = !win && wave_in_sq && tk + C::KT <= k_end && (!p.causal || tk + C::KT - 1 <= wave_tok0 + p.coff);
     if (interior) {
 #pragma unroll
       for (int sub = 0; sub < C::SUBS; ++sub) {
@@ -263,7 +264,7 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
         const int64_t sn = tk + sub * 32;
         // wave-uniform: the sub-tile exists and is not wholly above this wave's
         // diagonal (lower-triangle mode) or outside its windows (window mode)
-        const bool active = sn < k_end && !(p.causal == 2 && sn > wave_tok_last) &&
+        const bool active = sn < k_end && !(p.causal == 2 && sn > wave_tok_last + p.coff) &&
                             !(win && (sn + 32 <= wmin || sn >= wmax));
         const int64_t s = sn + l32;
         float mv[C::TPW];  // window mode: the additive mask, loaded ahead of the MFMAs
@@ -287,7 +288,7 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
           float v = sum_halves(part[tl]);
           const bool mine = C::TPW == 1 ? (g32 == 0) : ((tl & 1) == g32);
           const int64_t t = wave_tok0 + tl;
-          bool above = (p.causal == 1 || p.causal == 2) && s > t;
+          bool above = (p.causal == 1 || p.causal == 2) && s > t + p.coff;
           if (win) {
             above = s < wst[tl] || s >= wen[tl];
             v += mv[tl];
@@ -326,7 +327,7 @@ indexer_score_kernel(const IdxParams p) {
     // a block's row: keys [0, min(last token + 1, Sk)), in 32-key sub-tiles
     auto row_keys = [&](int64_t tb) {
       const int64_t t_last = (tb * C::TT + C::TT < p.Sq ? tb * C::TT + C::TT : p.Sq) - 1;
-      return t_last + 1 < p.Sk ? t_last + 1 : p.Sk;
+      return t_last + 1 + p.coff < p.Sk ? t_last + 1 + p.coff : p.Sk;
     };
     const int64_t keys_long = row_keys(tb_long), keys_short = tb_short < tb_long ? row_keys(tb_short) : 0;
     const int64_t n_long = (keys_long + 31) / 32, n = n_long + (keys_short + 31) / 32;
@@ -346,7 +347,7 @@ indexer_score_kernel(const IdxParams p) {
   const int64_t k0 = (int64_t)blockIdx.x * C::CHUNK;
   const int64_t t_last = (t0 + C::TT < p.Sq ? t0 + C::TT : p.Sq) - 1;
   const int64_t chunk_end = k0 + C::CHUNK < p.Sk ? k0 + C::CHUNK : p.Sk;
-  bool outside = p.causal == 1 && k0 > t_last;
+  bool outside = p.causal == 1 && k0 > t_last + p.coff;
   if (p.causal == kCausalWindow) {
     // union of the block's token windows (TT <= 64 tokens: one per lane of wave 0)
     __shared__ int blk_win[2];
@@ -440,7 +441,7 @@ static int indexer_scores_impl(const void *q, const void *w, const void *k, floa
                                int64_t Sk, int64_t H, int64_t D, int dtype, int w_dtype, const float *q_scale,
                                const float *k_scale, int causal, const int32_t *starts, const int32_t *ends,
                                const float *mask, int64_t mask_bstride, int use_relu, hipStream_t st,
-                               const char *fn) {
+                               const char *fn, int64_t coff = 0) {
   DSA_REQUIRE(B >= 0 && Sq >= 0 && Sk >= 0 && H > 0 && D > 0, "%s: bad dims", fn);
   DSA_REQUIRE(dtype == DSA_DTYPE_BF16 || dtype == DSA_DTYPE_E4M3, "%s: dtype %d", fn, dtype);
   DSA_REQUIRE(w_dtype == DSA_DTYPE_BF16 || w_dtype == DSA_DTYPE_F32, "%s: w dtype %d", fn, w_dtype);
@@ -466,6 +467,7 @@ static int indexer_scores_impl(const void *q, const void *w, const void *k, floa
   p.B = B;
   p.Sq = Sq;
   p.Sk = Sk;
+  p.coff = coff;
   p.w_f32 = w_dtype == DSA_DTYPE_F32;
   p.causal = causal;
   p.relu = use_relu != 0;
@@ -500,4 +502,80 @@ extern "C" int dsa_indexer_scores_masked(const void *q, const void *w, const voi
   return indexer_scores_impl(q, w, k, scores, B, Sq, Sk, H, D, dtype, w_dtype, q_scale, k_scale, kCausalWindow,
                              starts, ends, mask, mask_bstride, use_relu, static_cast<hipStream_t>(stream),
                              "dsa_indexer_scores_masked");
+}
+
+// ---------------------------------------------------------------------------
+// Streaming indexer + top-k: query rows in chunks through a bounded scratch
+// ---------------------------------------------------------------------------
+namespace dsa {
+
+// out_scores[b, r0 + t, j] = scratch[b][t][idx] for the chunk's picks (-inf for -1 padding)
+__global__ void __launch_bounds__(256) gather_topk_scores_kernel(const float *scratch, const int32_t *idx,
+                                                                 float *out, int64_t B, int64_t Sq, int64_t rows,
+                                                                 int64_t r0, int64_t Sk, int64_t topk) {
+  const int64_t e = blockIdx.x * 256ll + threadIdx.x;
+  if (e >= B * rows * topk) return;
+  const int64_t j = e % topk, t = (e / topk) % rows, b = e / (topk * rows);
+  const int64_t o = (b * Sq + r0 + t) * topk + j;
+  const int32_t c = idx[o];
+  out[o] = (c >= 0 && c < Sk) ? scratch[(b * rows + t) * Sk + c] : -INFINITY;
+}
+
+static int64_t stream_chunk_rows(int64_t B, int64_t Sq, int64_t Sk, size_t workspace_bytes) {
+  const int64_t per_row = B * Sk * 4;
+  int64_t cr = per_row > 0 ? (int64_t)(workspace_bytes / (size_t)per_row) : 0;
+  if (cr > Sq) cr = Sq;
+  return cr;
+}
+
+}  // namespace dsa
+
+extern "C" size_t dsa_indexer_topk_streaming_workspace_size(int64_t B, int64_t Sq, int64_t Sk, int64_t chunk_rows) {
+  if (B <= 0 || Sq <= 0 || Sk <= 0 || chunk_rows <= 0) return 0;
+  const int64_t cr = chunk_rows < Sq ? chunk_rows : Sq;
+  return (size_t)B * cr * Sk * 4;
+}
+
+extern "C" int dsa_indexer_topk_streaming(const void *q, const void *w, const void *k, int32_t *out_idx,
+                                          float *out_scores, int64_t B, int64_t Sq, int64_t Sk, int64_t H, int64_t D,
+                                          int dtype, int w_dtype, const float *q_scale, const float *k_scale,
+                                          int64_t topk, int causal, int use_relu, void *workspace,
+                                          size_t workspace_bytes, void *stream) {
+  DSA_REQUIRE(B >= 0 && Sq >= 0 && Sk >= 0 && H > 0 && D > 0 && topk > 0,
+              "dsa_indexer_topk_streaming: bad dims");
+  DSA_REQUIRE(causal == 0 || causal == 1, "dsa_indexer_topk_streaming: causal must be 0 or 1");
+  if (B == 0 || Sq == 0) return DSA_OK;
+  DSA_REQUIRE(out_idx, "dsa_indexer_topk_streaming: null out_idx");
+  const int64_t cr = stream_chunk_rows(B, Sq, Sk, workspace_bytes);
+  if (!workspace || cr < 1)
+    return set_error(DSA_ERR_WORKSPACE,
+                     "dsa_indexer_topk_streaming: workspace %zu bytes holds no score row (need >= %lld per query row)",
+                     workspace_bytes, (long long)(B * Sk * 4));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float *scratch = static_cast<float *>(workspace);
+  const int64_t elt = dtype == DSA_DTYPE_E4M3 ? 1 : 2;
+  const int64_t welt = w_dtype == DSA_DTYPE_F32 ? 4 : 2;
+  for (int64_t r0 = 0; r0 < Sq; r0 += cr) {
+    const int64_t rows = Sq - r0 < cr ? Sq - r0 : cr;
+    // query rows [r0, r0 + rows): q / w start r0 tokens in; causal keys s <= r0 + t
+    const unsigned char *qc = static_cast<const unsigned char *>(q) + r0 * B * H * D * elt;
+    const unsigned char *wc = static_cast<const unsigned char *>(w) + r0 * B * H * welt;
+    int rc = indexer_scores_impl(qc, wc, k, scratch, B, rows, Sk, H, D, dtype, w_dtype, q_scale, k_scale,
+                                 causal ? 2 : 0, nullptr, nullptr, nullptr, 0, use_relu, st,
+                                 "dsa_indexer_topk_streaming", causal ? r0 : 0);
+    if (rc) return rc;
+    for (int64_t b = 0; b < B; ++b) {
+      rc = dsa_topk(scratch + b * rows * Sk, rows, Sk, Sk, rows, causal, causal ? r0 : 0, nullptr, nullptr, topk,
+                    out_idx + (b * Sq + r0) * topk, stream);
+      if (rc) return rc;
+    }
+    if (out_scores) {
+      const int64_t n = B * rows * topk;
+      hipLaunchKernelGGL(gather_topk_scores_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, scratch,
+                         out_idx, out_scores, B, Sq, rows, r0, Sk, topk);
+      rc = check_launch("indexer_topk_streaming(gather)");
+      if (rc) return rc;
+    }
+  }
+  return DSA_OK;
 }

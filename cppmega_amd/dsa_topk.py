@@ -105,6 +105,48 @@ def drop_masked_picks(scores, idx):
     return torch.where(key == big, torch.full_like(key, -1), key)
 
 
+def indexer_topk_streaming(q, k, weights, index_topk, use_relu=True, causal=True, q_scale=None, k_scale=None,
+                           return_scores=False, max_scratch_bytes=64 << 20, chunk_rows=None):
+    """Indexer scores + deterministic top-k without the [b, sq, sk] score matrix:
+    q [sq,b,h,d] (bf16 or e4m3), k [sk,b,d], weights [sq,b,h] -> indices
+    [b, sq, index_topk] int32 (ascending, -1 padded), and with
+    ``return_scores`` also the selected scores [b, sq, index_topk] f32 (-inf
+    on padding).  Query rows go through a scratch of at most
+    ``max_scratch_bytes`` (or ``chunk_rows`` rows) in chunks; the indices are
+    bit-identical to ``topk_indices`` over the full scores.  The reference's
+    stated target for its indexer (docs/status/cppmega_architecture_status.md:340-362)."""
+    assert q.dim() == 4 and k.dim() == 3 and weights.dim() == 3
+    sq, b, h, d = q.shape
+    sk = k.shape[0]
+    fp8 = q.dtype == torch.float8_e4m3fn
+    if fp8:
+        assert k.dtype == torch.float8_e4m3fn and q_scale is not None and k_scale is not None, \
+            "e4m3 indexer inputs need q_scale and k_scale"
+        q_scale = q_scale.reshape(-1)[:1].to(torch.float32).contiguous()
+        k_scale = k_scale.reshape(-1)[:1].to(torch.float32).contiguous()
+    elif q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
+        raise TypeError(f"indexer q/k must be bf16 or float8_e4m3fn, got {q.dtype}/{k.dtype}")
+    if weights.dtype not in (torch.float32, torch.bfloat16):
+        weights = weights.float()
+    q, k, weights = q.contiguous(), k.contiguous(), weights.contiguous()
+    if chunk_rows is None:
+        chunk_rows = max(1, int(max_scratch_bytes) // max(1, b * sk * 4))
+    lib = _lib.load()
+    ws_bytes = int(lib.dsa_indexer_topk_streaming_workspace_size(b, sq, sk, int(chunk_rows)))
+    dev = _lib.ensure_device(q)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    idx = torch.empty((b, sq, int(index_topk)), dtype=torch.int32, device=q.device)
+    vals = torch.empty((b, sq, int(index_topk)), dtype=torch.float32, device=q.device) if return_scores else None
+    rc = lib.dsa_indexer_topk_streaming(
+        q.data_ptr(), weights.data_ptr(), k.data_ptr(), idx.data_ptr(), _lib.ptr(vals), b, sq, sk, h, d,
+        _lib.DTYPE_E4M3 if fp8 else _lib.DTYPE_BF16,
+        _lib.DTYPE_F32 if weights.dtype == torch.float32 else _lib.DTYPE_BF16,
+        _lib.ptr(q_scale), _lib.ptr(k_scale), int(index_topk), 1 if causal else 0, 1 if use_relu else 0,
+        ws.data_ptr(), ws_bytes, _lib.stream_ptr(dev))
+    _lib.check(rc, "dsa_indexer_topk_streaming")
+    return (idx, vals) if return_scores else idx
+
+
 def fused_qk_topk_naive(q, k, weights, index_topk, mask=None, varlen_starts=None, varlen_ends=None,
                         key_positions=None, use_relu=True):
     """Megatron ``fused_qk_topk_naive`` on gfx950 -> (scores [b,sq,sk] f32, indices [b,sq,k] int64).
@@ -196,4 +238,5 @@ def apply_dsa_topk_patch(*, force: bool = False, dsa_module=None) -> bool:
 
 
 __all__ = ["CAUSAL_LOWER", "CAUSAL_NEG_INF", "CAUSAL_NONE", "CAUSAL_WINDOW", "apply_dsa_topk_patch",
-           "drop_masked_picks", "fused_qk_topk_naive", "indexer_topk", "mask_windows", "topk_indices"]
+           "drop_masked_picks", "fused_qk_topk_naive", "indexer_topk", "indexer_topk_streaming", "mask_windows",
+           "topk_indices"]

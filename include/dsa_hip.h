@@ -217,6 +217,32 @@ int dsa_topk(const float *scores, int64_t rows, int64_t row_len,
              void *stream);
 
 /*
+ * Streaming indexer + top-k: the top-k of the indexer scores of every query
+ * row without the [B, Sq, Sk] score matrix, the target the reference states
+ * for its indexer ("emit only [b, sq, topk] indices and optional top-k
+ * scores", docs/status/cppmega_architecture_status.md:340-362).  Query rows
+ * go through the workspace in chunks of as many rows as it holds
+ * (workspace_bytes / (B * Sk * 4)): per chunk the indexer kernel writes the
+ * chunk's scores (causal: only s <= t) and the top-k kernel selects from them,
+ * so the indices equal dsa_topk's on the same fp32 scores, bit for bit.
+ *   q, w, k, dtype, w_dtype, q_scale, k_scale, use_relu as in dsa_indexer_scores;
+ *   out_idx [B, Sq, topk] int32 (ascending, -1 padded; candidates s <= t when
+ *   causal, every key otherwise); out_scores [B, Sq, topk] f32 (the selected
+ *   scores, -inf for padding) or NULL.
+ * workspace: >= dsa_indexer_topk_streaming_workspace_size(B, Sq, Sk, rows)
+ * bytes for chunks of `rows` query rows (at least one row).
+ */
+size_t dsa_indexer_topk_streaming_workspace_size(int64_t B, int64_t Sq, int64_t Sk,
+                                                 int64_t chunk_rows);
+int dsa_indexer_topk_streaming(const void *q, const void *w, const void *k,
+                               int32_t *out_idx, float *out_scores, int64_t B,
+                               int64_t Sq, int64_t Sk, int64_t H, int64_t D,
+                               int dtype, int w_dtype, const float *q_scale,
+                               const float *k_scale, int64_t topk, int causal,
+                               int use_relu, void *workspace,
+                               size_t workspace_bytes, void *stream);
+
+/*
  * Tensorwise (current-scaling) quantisation to OCP e4m3:
  *   amax = max|x|, scale = 448 / amax (1 when amax == 0),
  *   out = e4m3(RNE(x * scale)) saturated to +-448, scale_inv = 1 / scale.
