@@ -61,6 +61,19 @@ __device__ __forceinline__ int partial_row_exponent(float amax) {
   s = s > 127 ? 127 : (s < -114 ? -114 : s);
   return s;
 }
+// The same exponent from an upper bound bnd of the row's magnitudes, known
+// before the row is computed: bnd * 2^s lies in [2^15, 2^16).  Callers pass
+// bnd with a relative margin of at least 2^-6 over every rounding in the row's
+// computation, so each element scales below 2^16 / (1 + 2^-6) < 64528, inside
+// fp16's finite range (65504).
+__device__ __forceinline__ int partial_row_exponent_bound(float bnd) {
+  if (!(bnd > 0.0f) || !(bnd <= 3.402823466e38f)) return 0;
+  int ex;
+  (void)frexpf(bnd, &ex);
+  int s = 16 - ex;
+  s = s > 127 ? 127 : (s < -114 ? -114 : s);
+  return s;
+}
 __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
   const _Float16 h = (_Float16)f;  // round to nearest even
   return (uint32_t)__builtin_bit_cast(uint16_t, h);

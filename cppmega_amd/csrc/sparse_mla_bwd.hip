@@ -61,7 +61,16 @@ struct BwdCfg {
   static constexpr int OFF_QL = 0;
   static constexpr int OFF_DOL = OFF_QL + 32 * QL_STRIDE;
   static constexpr int OFF_LD = OFF_DOL + 32 * DOL_STRIDE;
-  static constexpr int SHARED_BYTES = (OFF_LD + 64 * 4 + 15) / 16 * 16;
+  // LD: 64 floats (LSE, Delta * scale), then 4 (per-wave max|Q| and max|dO| of the item)
+  static constexpr int SHARED_BYTES = (OFF_LD + 68 * 4 + 15) / 16 * 16;
+  static constexpr int KSTEPS = D_QK / 16;
+  static constexpr int VSTEPS = D_V / 16;
+  // bf16 input with fp16 partial rows: each partial row's power-of-two scale is
+  // taken from a bound before its products
+  static constexpr bool BEXP = !FP8 && !F32P;
+  // bf16 input: the Q / dO operands of S and dP stay in registers where they
+  // fit beside the accumulators (2 waves per SIMD up to d_qk = 128, 1 above)
+  static constexpr bool REGQ = !FP8 && (KSTEPS + VSTEPS <= 12 || D_QK > 128);
   static constexpr int KL_BYTES = 32 * Gat::KL_STRIDE;
   static constexpr int KD_STRIDE = D_QK * 2 + 32;        // e4m3: dequantised rows (bf16)
   static constexpr int KD_BYTES = FP8 ? 32 * KD_STRIDE : 0;
@@ -82,8 +91,6 @@ struct BwdCfg {
   static constexpr int LDS_BYTES = LOOP_BYTES > COMBINE_BYTES ? LOOP_BYTES : COMBINE_BYTES;
   static constexpr int DQT = D_QK / 32;
   static constexpr int DVT = D_V / 32;
-  static constexpr int KSTEPS = D_QK / 16;
-  static constexpr int VSTEPS = D_V / 16;
   // bf16 source of K / V rows for the dP / dQ GEMMs
   static constexpr int K_STRIDE = FP8 ? KD_STRIDE : Gat::KL_STRIDE;
   static_assert(D_V % 32 == 0 && D_QK % 32 == 0 && D_V <= D_QK, "unsupported head dims");
@@ -260,8 +267,52 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
       if (t < nheads) lse_h = (lse_raw == -INFINITY) ? INFINITY : lse_raw;  // all-masked row: zero gradient
       LD[t] = lse_h;
     }
+    if constexpr (C::BEXP) {
+      // max |Q| and max |dO| over the item (padded heads read zeros): the bound
+      // of every partial row's magnitude below
+      float mq = 0.0f, md = 0.0f;
+#pragma unroll
+      for (int it = 0; it < QIT; ++it)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t u = (uint32_t)qv[it][e];
+          mq = fmaxf(mq, fmaxf(__uint_as_float((u << 16) & 0x7fff0000u), __uint_as_float(u & 0x7fff0000u)));
+        }
+#pragma unroll
+      for (int it = 0; it < VIT; ++it)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t u = (uint32_t)dv[it][e];
+          md = fmaxf(md, fmaxf(__uint_as_float((u << 16) & 0x7fff0000u), __uint_as_float(u & 0x7fff0000u)));
+        }
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        mq = fmaxf(mq, __shfl_xor(mq, off, 64));
+        md = fmaxf(md, __shfl_xor(md, off, 64));
+      }
+      if (lane == 0) {
+        LD[64 + 2 * w] = mq;
+        LD[65 + 2 * w] = md;
+      }
+    }
   }
   __syncthreads();
+
+  // bf16 path: the S / dP A operands (head l32, d = 16k + 8 g32 + e) stay in registers
+  i32x4 qA[C::REGQ ? C::KSTEPS : 1], doA[C::REGQ ? C::VSTEPS : 1];
+  float maxq = 0.0f, maxdo = 0.0f;
+  if constexpr (C::REGQ) {
+#pragma unroll
+    for (int k = 0; k < C::KSTEPS; ++k)
+      qA[k] = *reinterpret_cast<const i32x4 *>(QL + l32 * C::QL_STRIDE + (16 * k + 8 * g32) * 2);
+#pragma unroll
+    for (int k = 0; k < C::VSTEPS; ++k)
+      doA[k] = *reinterpret_cast<const i32x4 *>(DOL + l32 * C::DOL_STRIDE + (16 * k + 8 * g32) * 2);
+  }
+  if constexpr (C::BEXP) {
+    maxq = fmaxf(LD[64], LD[66]);
+    maxdo = fmaxf(LD[65], LD[67]);
+  }
 
   long qA8[FP8 ? C::KSTEPS : 1];  // e4m3: raw Q codes as the S A operand (head l32)
   if constexpr (FP8) {
@@ -306,43 +357,75 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
         const long kb = *reinterpret_cast<const long *>(Kl + l32 * Gat::KL_STRIDE + 16 * k + 8 * g32);
         sacc = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(qA8[k], kb, sacc, 0, 0, 0);
       } else {
-        const i32x4 qa = *reinterpret_cast<const i32x4 *>(QL + l32 * C::QL_STRIDE + (16 * k + 8 * g32) * 2);
+        // V is the leading D_V columns of K: one K read feeds S and dP
         const i32x4 kb = *reinterpret_cast<const i32x4 *>(Kl + l32 * Gat::KL_STRIDE + (16 * k + 8 * g32) * 2);
+        const i32x4 qa =
+            C::REGQ ? qA[C::REGQ ? k : 0]
+                    : *reinterpret_cast<const i32x4 *>(QL + l32 * C::QL_STRIDE + (16 * k + 8 * g32) * 2);
         sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(qa), as_bf16x8(kb), sacc, 0, 0, 0);
+        if (k < C::VSTEPS) {
+          const i32x4 da =
+              C::REGQ ? doA[C::REGQ ? k : 0]
+                      : *reinterpret_cast<const i32x4 *>(DOL + l32 * C::DOL_STRIDE + (16 * k + 8 * g32) * 2);
+          dpacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(da), as_bf16x8(kb), dpacc, 0, 0, 0);
+        }
       }
     }
+    if constexpr (FP8) {  // dP on the dequantised rows
 #pragma unroll
-    for (int k = 0; k < C::VSTEPS; ++k) {
-      const i32x4 da = *reinterpret_cast<const i32x4 *>(DOL + l32 * C::DOL_STRIDE + (16 * k + 8 * g32) * 2);
-      const i32x4 vb = *reinterpret_cast<const i32x4 *>(Ksrc + l32 * C::K_STRIDE + (16 * k + 8 * g32) * 2);
-      dpacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(da), as_bf16x8(vb), dpacc, 0, 0, 0);
+      for (int k = 0; k < C::VSTEPS; ++k) {
+        const i32x4 da = *reinterpret_cast<const i32x4 *>(DOL + l32 * C::DOL_STRIDE + (16 * k + 8 * g32) * 2);
+        const i32x4 vb = *reinterpret_cast<const i32x4 *>(Ksrc + l32 * C::K_STRIDE + (16 * k + 8 * g32) * 2);
+        dpacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(da), as_bf16x8(vb), dpacc, 0, 0, 0);
+      }
     }
 
     // ---- P, dS  (lane = slot slot0 + l32, heads 8i + 4*g32 + j) ----
     float xs = p.sl2;
     if constexpr (FP8) xs *= qsc * Ksc[l32];
     bf16x8 dsB[2], pB[2];
+    int pexp = 0;  // bf16 path: the partial row's scale exponent, fixed before its products
     {
       uint32_t dsw[8], pw[8];
+      float P[16], dS[16];
+      float sabs = 0.0f, psum = 0.0f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const f32x4 l4 = *reinterpret_cast<const f32x4 *>(LD + 8 * i + 4 * g32);
         const f32x4 d4 = *reinterpret_cast<const f32x4 *>(LD + 32 + 8 * i + 4 * g32);
-        float P[4], dS[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int a = 4 * i + j;
           const float pv = valid ? exp2_fast(sacc[a] * xs - l4[j]) : 0.0f;
-          P[j] = pv;
-          dS[j] = pv * fmaf(dpacc[a], p.scale, -d4[j]);  // P (dP - Delta) scale
+          P[a] = pv;
+          dS[a] = pv * fmaf(dpacc[a], p.scale, -d4[j]);  // P (dP - Delta) scale
+          sabs += fabsf(dS[a]);
+          psum += pv;
         }
-        dsw[2 * i] = pack_bf16x2(dS[0], dS[1]);
-        dsw[2 * i + 1] = pack_bf16x2(dS[2], dS[3]);
-        pw[2 * i] = pack_bf16x2(P[0], P[1]);
-        pw[2 * i + 1] = pack_bf16x2(P[2], P[3]);
+        dsw[2 * i] = pack_bf16x2(dS[4 * i], dS[4 * i + 1]);
+        dsw[2 * i + 1] = pack_bf16x2(dS[4 * i + 2], dS[4 * i + 3]);
         // dS[slot][heads 8i + 4*g32 .. +3] row-major for the dQ GEMM
         *reinterpret_cast<i32x2 *>(DS + l32 * C::DS_STRIDE + (8 * i + 4 * g32) * 2) =
             i32x2{(int)dsw[2 * i], (int)dsw[2 * i + 1]};
+      }
+      float rs = 1.0f;
+      if constexpr (C::BEXP) {
+        // |c[d]| <= max|Q| sum_h |dS_h| + max|dO| sum_h P_h over the slot's 32
+        // heads; the margin 2^-6 covers the bf16 rounding of dS / P (2^-8) and
+        // the fp32 sums (< 2^-17)
+        const float bnd = sum_halves(fmaf(maxq, sabs, maxdo * psum)) * 1.015625f;
+        pexp = partial_row_exponent_bound(bnd);
+        rs = exp2i(pexp);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {  // bf16(x 2^s) = bf16(x) 2^s: the scaled rows are exact
+          dsw[2 * i] = pack_bf16x2(dS[4 * i] * rs, dS[4 * i + 1] * rs);
+          dsw[2 * i + 1] = pack_bf16x2(dS[4 * i + 2] * rs, dS[4 * i + 3] * rs);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pw[2 * i] = pack_bf16x2(P[4 * i] * rs, P[4 * i + 1] * rs);
+        pw[2 * i + 1] = pack_bf16x2(P[4 * i + 2] * rs, P[4 * i + 3] * rs);
       }
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc) {
@@ -400,14 +483,17 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
       // fp16 rows scaled by a power of two mapping the row max into [2^13, 2^14)
       // (exact to undo), staged in LDS (over the consumed K tile) and written
       // as whole rows: 16 lanes store one row's 256 contiguous bytes
-      float amax = 0.0f;
+      float rscale = 1.0f;  // bf16 path: c already carries 2^pexp
+      if constexpr (!C::BEXP) {
+        float amax = 0.0f;
 #pragma unroll
-      for (int dt = 0; dt < C::DQT; ++dt)
+        for (int dt = 0; dt < C::DQT; ++dt)
 #pragma unroll
-        for (int a = 0; a < 16; ++a) amax = fmaxf(amax, fabsf(cacc[dt][a]));
-      amax = max_halves(amax);
-      const int pexp = partial_row_exponent(amax);
-      const float rscale = exp2i(pexp);
+          for (int a = 0; a < 16; ++a) amax = fmaxf(amax, fabsf(cacc[dt][a]));
+        amax = max_halves(amax);
+        pexp = partial_row_exponent(amax);
+        rscale = exp2i(pexp);
+      }
       wave_lds_sync();  // the dQ GEMM's reads of the K / dS tiles are complete
       unsigned char *Cs = Kl;  // spans Kl (and Kd for e4m3)
       int *Lpos = reinterpret_cast<int *>(DS);
