@@ -36,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "dsa_device_check",
     "dsa_sparse_mla_fwd",
     "dsa_sparse_mla_bwd_workspace_size",
+    "dsa_sparse_mla_bwd_pass_bytes",
     "dsa_sparse_mla_bwd",
     "dsa_indexer_scores",
     "dsa_indexer_scores_masked",
@@ -71,6 +72,7 @@ _SIGNATURES = {
                                   _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                   _f32, _i32, _c_void_p, _c_void_p, _c_void_p]),
     "dsa_sparse_mla_bwd_workspace_size": (_size_t, [_i64] * 8 + [_i32]),
+    "dsa_sparse_mla_bwd_pass_bytes": (_i32, [ctypes.c_uint64]),
     "dsa_sparse_mla_bwd": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                   _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _size_t,
                                   _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,

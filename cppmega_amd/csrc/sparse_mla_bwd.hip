@@ -36,6 +36,8 @@
 //                                 gets runs of 8 consecutive d of one slot;
 //   dQ^T[d][head] = K^T dS^T      M = d, N = head, K = slot: both operands
 //                                 transposed-read (K tile, dS[slot][head] tile).
+#include <atomic>
+
 #include "dsa_common.hpp"
 #include "sparse_mla_csr.hpp"
 #include "sparse_mla_gather.hpp"
@@ -577,38 +579,83 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Passes of the backward.  A pass is a contiguous range of the flattened
+// [B * S] tokens: whole batches while their partial rows fit the per-pass cap,
+// else a slice of one batch (a multiple of 32 tokens).  Each pass builds its
+// own inverse index, runs the main kernel on its tokens and reduces its
+// partial rows; when a batch spans several passes the kv rows' sums are
+// carried between them in fp32 (first pass stores, later passes add, the
+// last casts to bf16), in pass order, so the result stays deterministic.
+constexpr uint64_t kBwdPassBytes = 2ull << 30;  // default: partial rows (+ exponents) per pass
+static std::atomic<uint64_t> g_pass_bytes{kBwdPassBytes};
+
+struct BwdPlan {
+  int64_t nb;   // batches per pass
+  int64_t ct;   // tokens of one batch per pass (S unless a batch is split)
+  int64_t npb;  // passes per batch (1 unless split)
+  int NC;       // 32-token chunks per batch within a pass
+};
+
+// bytes per partial element: fp32 with DSA_BWD_FP32_PARTIALS and for wide heads, else fp16
+static int64_t partial_elem_bytes(int flags, int64_t D_qk) {
+  return ((flags & DSA_BWD_FP32_PARTIALS) || D_qk > 256) ? 4 : 2;
+}
+
+static BwdPlan bwd_plan(int64_t B, int64_t S, int64_t H, int64_t G, int64_t D_qk, int64_t topk, int flags) {
+  const int64_t hpg = H / (G > 0 ? G : 1);
+  const int64_t ntiles = (hpg + 31) / 32;
+  const uint64_t per_token = (uint64_t)(G * topk * ntiles) * (uint64_t)(D_qk * partial_elem_bytes(flags, D_qk) + 1);
+  BwdPlan pl;
+  const uint64_t cap = g_pass_bytes.load();
+  if ((uint64_t)S * per_token <= cap) {
+    pl.ct = S;
+    pl.npb = 1;
+    const int64_t fit = (int64_t)(cap / ((uint64_t)S * per_token));
+    pl.nb = fit < 1 ? 1 : (fit < B ? fit : B);
+  } else {
+    int64_t ct = (int64_t)(cap / per_token) / kChunkTokens * kChunkTokens;
+    pl.ct = ct < kChunkTokens ? kChunkTokens : ct;
+    pl.npb = (S + pl.ct - 1) / pl.ct;
+    pl.nb = 1;
+  }
+  pl.NC = csr_chunks(pl.ct);
+  return pl;
+}
+
 struct BwdWorkspace {
-  size_t partials, pexp, mask, base, dup, tot, rowptr, pos_of, total;
-  int NC;
+  size_t partials, pexp, mask, base, dup, tot, rowptr, pos_of, carry, total;
+  BwdPlan plan;
 };
 
 static BwdWorkspace bwd_layout(int64_t B, int64_t S, int64_t S_kv, int64_t H, int64_t G, int64_t D_qk,
                                int64_t topk, int flags) {
   const int64_t hpg = H / (G > 0 ? G : 1);
   const int ntiles = (int)((hpg + 31) / 32);
-  const size_t entries = (size_t)B * S * G * topk;
-  const int64_t R = S_kv * G;
   BwdWorkspace L;
-  L.NC = csr_chunks(S);
-  // wide heads always keep fp32 partial rows
-  const size_t psz = ((flags & DSA_BWD_FP32_PARTIALS) || D_qk > 256) ? 4 : 2;
+  L.plan = bwd_plan(B, S, H, G, D_qk, topk, flags);
+  const BwdPlan &pl = L.plan;
+  const size_t entries = (size_t)pl.nb * pl.ct * G * topk;  // of one pass
+  const int64_t R = S_kv * G;
+  const size_t psz = (size_t)partial_elem_bytes(flags, D_qk);
   size_t off = 0;
   L.partials = off;
   off += align256((entries * ntiles + 1) * D_qk * psz);  // + one trash row for masked slots
   L.pexp = off;
   off += align256(entries * ntiles + 1);
   L.mask = off;
-  off += align256((size_t)B * L.NC * R * 4);
+  off += align256((size_t)pl.nb * pl.NC * R * 4);
   L.base = off;
-  off += align256((size_t)B * L.NC * R * 4);
+  off += align256((size_t)pl.nb * pl.NC * R * 4);
   L.dup = off;
-  off += align256((size_t)B * L.NC * 4);
+  off += align256((size_t)pl.nb * pl.NC * 4);
   L.tot = off;
-  off += align256((size_t)B * R * 4);
+  off += align256((size_t)pl.nb * R * 4);
   L.rowptr = off;
-  off += align256(((size_t)B * R + 1) * 4);
+  off += align256(((size_t)pl.nb * R + 1) * 4);
   L.pos_of = off;
   off += align256(entries * 4);
+  L.carry = off;  // fp32 sums of one batch's kv rows, carried across its passes
+  off += pl.npb > 1 ? align256((size_t)R * D_qk * 4) : 0;
   L.total = off;
   return L;
 }
@@ -637,20 +684,25 @@ static int launch_bwd_main_p(const BwdParams &p, bool f32p, hipStream_t st) {
 
 template <int D_QK>
 static int launch_reduce(const CsrParams &cp, const unsigned char *partials, const int8_t *pexp, uint16_t *dkv,
-                         int64_t rows, int ntiles, bool f32p, hipStream_t st) {
+                         float *carry, int mode, int64_t rows, int ntiles, bool f32p, hipStream_t st) {
   const unsigned grid = (unsigned)rows;  // one workgroup per kv row
   if (f32p)
     hipLaunchKernelGGL((dkv_reduce_kernel<D_QK, true>), dim3(grid), dim3(256), 0, st, cp.rowptr, partials, pexp,
-                       dkv, rows, ntiles);
+                       dkv, carry, mode, rows, ntiles);
   else
     hipLaunchKernelGGL((dkv_reduce_kernel<D_QK, false>), dim3(grid), dim3(256), 0, st, cp.rowptr, partials, pexp,
-                       dkv, rows, ntiles);
+                       dkv, carry, mode, rows, ntiles);
   return check_launch("sparse_mla_bwd(reduce)");
 }
 
 }  // namespace dsa
 
 using namespace dsa;
+
+extern "C" int dsa_sparse_mla_bwd_pass_bytes(uint64_t bytes) {
+  g_pass_bytes.store(bytes == 0 ? kBwdPassBytes : bytes);
+  return DSA_OK;
+}
 
 extern "C" size_t dsa_sparse_mla_bwd_workspace_size(int64_t B, int64_t S, int64_t S_kv, int64_t H, int64_t G,
                                                     int64_t D_qk, int64_t D_v, int64_t topk, int flags) {
@@ -706,71 +758,87 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
                        (rows * D_qk) / 2, 0);
     return check_launch("sparse_mla_bwd(fill)");
   }
-
-  CsrParams cp;
-  cp.idx = indices;
-  cp.mask = reinterpret_cast<uint32_t *>(ws + L.mask);
-  cp.base = reinterpret_cast<int32_t *>(ws + L.base);
-  cp.dup = reinterpret_cast<int32_t *>(ws + L.dup);
-  cp.tot = reinterpret_cast<int32_t *>(ws + L.tot);
-  cp.rowptr = reinterpret_cast<int32_t *>(ws + L.rowptr);
-  cp.pos_of = reinterpret_cast<int32_t *>(ws + L.pos_of);
-  cp.S = S;
-  cp.S_kv = S_kv;
-  cp.G = G;
-  cp.topk = topk;
-  cp.R = R;
-  cp.NC = L.NC;
-  cp.dup_only = wide ? 0 : 1;  // the narrow main kernel derives the positions of chunks without repeats
-  stage_begin(st);
-  int rc = launch_csr(cp, B, st);
-  if (rc) return rc;
-  stage_mark(st);
-
-  BwdParams p;
-  p.q = static_cast<const unsigned char *>(q);
-  p.kv = static_cast<const unsigned char *>(kv);
-  p.o = static_cast<const uint16_t *>(o);
-  p.dO = static_cast<const uint16_t *>(dO);
-  p.idx = indices;
-  p.lse = lse2;
-  p.delta = delta;
-  p.dq = static_cast<uint16_t *>(dq);
-  p.q_scale = q_scale;
-  p.kv_scale = kv_scale;
-  p.pos_of = cp.pos_of;
-  p.mask = cp.mask;
-  p.base = cp.base;
-  p.dup = cp.dup;
-  p.R = cp.R;
-  p.rowptr = cp.rowptr;
-  p.NC = cp.NC;
-  p.partials = ws + L.partials;
-  p.partial_exp = reinterpret_cast<int8_t *>(ws + L.pexp);
-  p.B = B;
-  p.S = S;
-  p.S_kv = S_kv;
-  p.H = H;
-  p.G = G;
-  p.topk = topk;
-  p.hpg = (int)hpg;
-  p.ntiles = ntiles;
-  p.sl2 = sm_scale * kLog2e;
-  p.scale = sm_scale;
-  if (wide) rc = launch_bwd_main_wide(p, D_qk, D_v, f8, st);
-  else if (D_qk == 128 && D_v == 64) rc = f8 ? launch_bwd_main_p<128, 64, true>(p, f32p, st) : launch_bwd_main_p<128, 64, false>(p, f32p, st);
-  else if (D_qk == 128 && D_v == 128) rc = f8 ? launch_bwd_main_p<128, 128, true>(p, f32p, st) : launch_bwd_main_p<128, 128, false>(p, f32p, st);
-  else if (D_qk == 192 && D_v == 128) rc = f8 ? launch_bwd_main_p<192, 128, true>(p, f32p, st) : launch_bwd_main_p<192, 128, false>(p, f32p, st);
-  else rc = launch_bwd_main_p<64, 32, false>(p, f32p, st);
-  if (rc) return rc;
-  stage_mark(st);
-
+  const BwdPlan &pl = L.plan;
+  const int64_t npass = pl.npb > 1 ? B * pl.npb : (B + pl.nb - 1) / pl.nb;
+  const size_t qel = dtype == DSA_DTYPE_E4M3 ? 1 : 2;  // bytes per q / kv element
   uint16_t *dkv16 = static_cast<uint16_t *>(dkv);
-  if (D_qk == 128) rc = launch_reduce<128>(cp, p.partials, p.partial_exp, dkv16, rows, ntiles, f32p, st);
-  else if (D_qk == 192) rc = launch_reduce<192>(cp, p.partials, p.partial_exp, dkv16, rows, ntiles, f32p, st);
-  else if (D_qk == 576) rc = launch_reduce<576>(cp, p.partials, p.partial_exp, dkv16, rows, ntiles, f32p, st);
-  else rc = launch_reduce<64>(cp, p.partials, p.partial_exp, dkv16, rows, ntiles, f32p, st);
-  if (rc) return rc;
-  stage_mark(st);
+  float *carry = reinterpret_cast<float *>(ws + L.carry);
+  stage_begin(st);
+  for (int64_t ps = 0; ps < npass; ++ps) {
+    // this pass: batches [b0, b0 + nbp), tokens [t0, t0 + ctp) of each
+    const int64_t b0 = pl.npb > 1 ? ps / pl.npb : ps * pl.nb;
+    const int64_t nbp = pl.npb > 1 ? 1 : (B - b0 < pl.nb ? B - b0 : pl.nb);
+    const int64_t t0 = pl.npb > 1 ? (ps % pl.npb) * pl.ct : 0;
+    const int64_t ctp = pl.npb > 1 ? (S - t0 < pl.ct ? S - t0 : pl.ct) : S;
+    const int64_t T0 = b0 * S + t0;  // first flattened token
+    const int mode = pl.npb == 1 ? 0 : (ps % pl.npb == 0 ? 1 : (ps % pl.npb == pl.npb - 1 ? 3 : 2));
+    const bool timed = npass == 1;
+
+    CsrParams cp;
+    cp.idx = indices + T0 * G * topk;
+    cp.mask = reinterpret_cast<uint32_t *>(ws + L.mask);
+    cp.base = reinterpret_cast<int32_t *>(ws + L.base);
+    cp.dup = reinterpret_cast<int32_t *>(ws + L.dup);
+    cp.tot = reinterpret_cast<int32_t *>(ws + L.tot);
+    cp.rowptr = reinterpret_cast<int32_t *>(ws + L.rowptr);
+    cp.pos_of = reinterpret_cast<int32_t *>(ws + L.pos_of);
+    cp.S = ctp;
+    cp.S_kv = S_kv;
+    cp.G = G;
+    cp.topk = topk;
+    cp.R = R;
+    cp.NC = csr_chunks(ctp);
+    cp.dup_only = wide ? 0 : 1;  // the narrow main kernel derives the positions of chunks without repeats
+    int rc = launch_csr(cp, nbp, st);
+    if (rc) return rc;
+    if (timed) stage_mark(st);
+
+    BwdParams p;
+    p.q = static_cast<const unsigned char *>(q) + (size_t)T0 * H * D_qk * qel;
+    p.kv = static_cast<const unsigned char *>(kv) + (size_t)b0 * S_kv * G * D_qk * qel;
+    p.o = static_cast<const uint16_t *>(o) + T0 * H * D_v;
+    p.dO = static_cast<const uint16_t *>(dO) + T0 * H * D_v;
+    p.idx = cp.idx;
+    p.lse = lse2 + T0 * H;
+    p.delta = delta ? delta + T0 * H : nullptr;
+    p.dq = static_cast<uint16_t *>(dq) + T0 * H * D_qk;
+    p.q_scale = q_scale ? q_scale + T0 : nullptr;
+    p.kv_scale = kv_scale ? kv_scale + b0 * S_kv : nullptr;
+    p.pos_of = cp.pos_of;
+    p.mask = cp.mask;
+    p.base = cp.base;
+    p.dup = cp.dup;
+    p.R = cp.R;
+    p.rowptr = cp.rowptr;
+    p.NC = cp.NC;
+    p.partials = ws + L.partials;
+    p.partial_exp = reinterpret_cast<int8_t *>(ws + L.pexp);
+    p.B = nbp;
+    p.S = ctp;
+    p.S_kv = S_kv;
+    p.H = H;
+    p.G = G;
+    p.topk = topk;
+    p.hpg = (int)hpg;
+    p.ntiles = ntiles;
+    p.sl2 = sm_scale * kLog2e;
+    p.scale = sm_scale;
+    if (wide) rc = launch_bwd_main_wide(p, D_qk, D_v, f8, st);
+    else if (D_qk == 128 && D_v == 64) rc = f8 ? launch_bwd_main_p<128, 64, true>(p, f32p, st) : launch_bwd_main_p<128, 64, false>(p, f32p, st);
+    else if (D_qk == 128 && D_v == 128) rc = f8 ? launch_bwd_main_p<128, 128, true>(p, f32p, st) : launch_bwd_main_p<128, 128, false>(p, f32p, st);
+    else if (D_qk == 192 && D_v == 128) rc = f8 ? launch_bwd_main_p<192, 128, true>(p, f32p, st) : launch_bwd_main_p<192, 128, false>(p, f32p, st);
+    else rc = launch_bwd_main_p<64, 32, false>(p, f32p, st);
+    if (rc) return rc;
+    if (timed) stage_mark(st);
+
+    uint16_t *dkv_p = dkv16 + b0 * R * D_qk;
+    const int64_t prow = nbp * R;
+    if (D_qk == 128) rc = launch_reduce<128>(cp, p.partials, p.partial_exp, dkv_p, carry, mode, prow, ntiles, f32p, st);
+    else if (D_qk == 192) rc = launch_reduce<192>(cp, p.partials, p.partial_exp, dkv_p, carry, mode, prow, ntiles, f32p, st);
+    else if (D_qk == 576) rc = launch_reduce<576>(cp, p.partials, p.partial_exp, dkv_p, carry, mode, prow, ntiles, f32p, st);
+    else rc = launch_reduce<64>(cp, p.partials, p.partial_exp, dkv_p, carry, mode, prow, ntiles, f32p, st);
+    if (rc) return rc;
+  }
+  stage_mark(st);  // several passes: one stage for the whole call
   return DSA_OK;
 }

@@ -311,10 +311,14 @@ __global__ void __launch_bounds__(256) csr_scatter_kernel(const CsrParams p) {
 // g + EPI, ... of its quarter in order (fp32); the groups are combined by a
 // fixed xor tree and the four waves as ((w0 + w1) + w2) + w3.  The association
 // depends on the item count alone, so the result is bitwise reproducible.
+// When one batch's tokens span several passes of the backward, the rows'
+// sums are carried in an fp32 accumulator: mode 1 (first pass) stores the
+// pass's sum there, mode 2 adds it to the carried sum, mode 3 (last pass)
+// writes bf16(carried + pass sum); mode 0 (one pass) writes bf16(pass sum).
 template <int D_QK, bool F32P>
 __global__ void __launch_bounds__(256)
 dkv_reduce_kernel(const int32_t *rowptr, const unsigned char *partials, const int8_t *partial_exp,
-                  uint16_t *dkv, int64_t nrows, int ntiles) {
+                  uint16_t *dkv, float *carry, int mode, int64_t nrows, int ntiles) {
   constexpr int ROWB = D_QK * (F32P ? 4 : 2);  // bytes per partial row
   constexpr int NCR = ROWB / 16;                // 16-byte chunks per partial row
   constexpr int LPE = NCR <= 8 ? 8 : (NCR <= 16 ? 16 : (NCR <= 32 ? 32 : 64));  // lanes per item
@@ -410,10 +414,20 @@ dkv_reduce_kernel(const int32_t *rowptr, const unsigned char *partials, const in
   }
   __syncthreads();
   uint32_t *out = reinterpret_cast<uint32_t *>(dkv + r * D_QK);
+  float *cr = carry + (mode != 0 ? r * D_QK : 0);
   for (int pi = threadIdx.x; pi < D_QK / 2; pi += 256) {
-    const float x0 = ((part[0][2 * pi] + part[1][2 * pi]) + part[2][2 * pi]) + part[3][2 * pi];
-    const float x1 = ((part[0][2 * pi + 1] + part[1][2 * pi + 1]) + part[2][2 * pi + 1]) + part[3][2 * pi + 1];
-    out[pi] = pack_bf16x2(x0, x1);
+    float x0 = ((part[0][2 * pi] + part[1][2 * pi]) + part[2][2 * pi]) + part[3][2 * pi];
+    float x1 = ((part[0][2 * pi + 1] + part[1][2 * pi + 1]) + part[2][2 * pi + 1]) + part[3][2 * pi + 1];
+    if (mode >= 2) {  // earlier passes' sum first
+      x0 = cr[2 * pi] + x0;
+      x1 = cr[2 * pi + 1] + x1;
+    }
+    if (mode == 0 || mode == 3) {
+      out[pi] = pack_bf16x2(x0, x1);
+    } else {
+      cr[2 * pi] = x0;
+      cr[2 * pi + 1] = x1;
+    }
   }
 }
 

@@ -91,6 +91,17 @@ enum dsa_bwd_flags {
   DSA_BWD_FP32_PARTIALS = 1
 };
 
+/*
+ * Per-pass cap on the backward's partial dKV rows (bytes; 0 restores the
+ * default of 2 GiB).  dsa_sparse_mla_bwd runs in passes over contiguous token
+ * ranges sized to this cap, so its workspace stays bounded at any sequence
+ * length; a batch split over passes carries its kv rows' sums in fp32 between
+ * them.  Process-wide; set it before dsa_sparse_mla_bwd_workspace_size and
+ * keep it until the matching dsa_sparse_mla_bwd call.  No counterpart in the
+ * reference (whose backward scatters into one fp32 dKV buffer with atomics).
+ */
+int dsa_sparse_mla_bwd_pass_bytes(uint64_t bytes);
+
 /* Bytes of workspace dsa_sparse_mla_bwd needs for these dimensions and flags. */
 size_t dsa_sparse_mla_bwd_workspace_size(int64_t B, int64_t S, int64_t S_kv,
                                          int64_t H, int64_t G, int64_t D_qk,
@@ -113,7 +124,10 @@ size_t dsa_sparse_mla_bwd_workspace_size(int64_t B, int64_t S, int64_t S_kv,
  * significant bits relative to the row max; fp32 with DSA_BWD_FP32_PARTIALS) in
  * ascending (token, kv group, slot) order in fp32, so repeated calls are
  * bitwise identical.  Gradients are with respect to the dequantised values
- * for e4m3 inputs.  Limits: S_kv * G <= 32768, B * S * G * topk < 2^31.
+ * for e4m3 inputs.  The work runs in passes over token ranges whose partial
+ * rows fit the per-pass cap (dsa_sparse_mla_bwd_pass_bytes), so the workspace
+ * is bounded; results are deterministic for a given cap.
+ * Limits: S_kv * G <= 32768, B * S * G * topk < 2^31.
  */
 int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o,
                        const void *dO, const int32_t *indices,
