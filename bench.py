@@ -19,7 +19,7 @@ profiles/ (null when that kernel has no such summary).
 After the timed steps the FP8-tensorwise SparseMLA forward and backward at the
 cfg2 shapes (cfg4: e4m3 q / kv with 1% x20 outliers) are timed and reported
 under "cfg4" against the mixed fp8 + bf16 MFMA floor (--no-cfg4 skips them).
-Then the cfg5 long-context kernels (SparseMLA forward at
+Then the cfg5 long-context kernels (SparseMLA forward and backward at
 h=128, d_qk=576, d_v=512, topk=2048; e4m3 indexer at h=64, d=128; top-2048
 over s=16384) are timed on device-generated inputs and reported under "cfg5"
 (not part of `value`).
@@ -75,6 +75,8 @@ def cfg5_work():
     s = C5_S
     return {
         "fwd": (2 * s * C5_H * C5_TOPK * (C5_DQK + C5_DV), 0, "bf16"),
+        # backward (recompute P, dP, dS, dQ, dKV): 23,639,499,997,184 FLOP
+        "bwd": (2 * s * C5_H * C5_TOPK * (3 * C5_DQK + 2 * C5_DV), 0, "bf16"),
         # block-scaled forward: Q K^T on e4m3 codes, PV in bf16
         "fwd_mxfp8": ((2 * s * C5_H * C5_TOPK * C5_DQK, 2 * s * C5_H * C5_TOPK * C5_DV), 0, "fp8+bf16"),
         "indexer_fp8": (2 * C5_HIDX * C5_DIDX * s * (s + 1) // 2, 0, "fp8"),
@@ -83,8 +85,8 @@ def cfg5_work():
 
 
 def measure_cfg5(dev, reps=3):
-    """Median kernel times of the cfg5 forward (h=128, d_qk=576, d_v=512,
-    topk=2048, bf16), its MXFP8 block-scaled form (e4m3 q/kv with one f32
+    """Median kernel times of the cfg5 forward and backward (h=128, d_qk=576,
+    d_v=512, topk=2048, bf16), the forward's MXFP8 block-scaled form (e4m3 q/kv with one f32
     scale per 32 channels), the e4m3 indexer (h=64, d=128, causal) and the
     top-2048 selection over s=16384, on inputs generated on the device with a
     fixed seed.  Each figure is the median of `reps` event-timed launches."""
@@ -92,8 +94,8 @@ def measure_cfg5(dev, reps=3):
 
     from cppmega_amd.dsa_indexer_fused_patch import CAUSAL_LOWER, index_scores
     from cppmega_amd.dsa_topk import topk_indices
-    from cppmega_amd.sparse_mla_ops import (sparse_mla_blockscaled_mxfp8_fwd_interface, sparse_mla_fwd_interface,
-                                            tensorwise_quantize)
+    from cppmega_amd.sparse_mla_ops import (sparse_mla_blockscaled_mxfp8_fwd_interface, sparse_mla_bwd,
+                                            sparse_mla_fwd_interface, tensorwise_quantize)
 
     gen = torch.Generator(device=dev).manual_seed(5)
     S5 = C5_S
@@ -139,7 +141,10 @@ def measure_cfg5(dev, reps=3):
         return sorted(ts)[len(ts) // 2] / 1e3
 
     from cppmega_amd.dsa_topk import indexer_topk_streaming
+    out, lse = sparse_mla_fwd_interface(q, kv, idx, sm_scale=C5_DQK ** -0.5, d_v=C5_DV)
+    do = torch.randn(out.shape, generator=gen, device=dev).to(torch.bfloat16)
     t = {
+        "bwd": timed(lambda: sparse_mla_bwd(q, kv, out, do, idx, lse, sm_scale=C5_DQK ** -0.5)),
         "indexer_topk_streaming": timed(lambda: indexer_topk_streaming(iq8, ik8, iw, C5_TOPK, q_scale=iqs, k_scale=iks,
                                                                        max_scratch_bytes=64 << 20)),
         "fwd": timed(lambda: sparse_mla_fwd_interface(q, kv, idx, sm_scale=C5_DQK ** -0.5, d_v=C5_DV)),
@@ -166,7 +171,9 @@ def measure_cfg5(dev, reps=3):
             gbs = by / t[k] / 1e9
             e.update({"bound": "hbm", "gbs": round(gbs, 1), "peak": PEAK_HBM_GBS, "frac": round(gbs / PEAK_HBM_GBS, 4)})
         res[k] = e
-    del q, kv, idx, iq8, ik8, iw, scores, qmx, kmx, qbs, kbs
+    res["bwd"]["note"] = ("in passes of <= 2 GiB of fp32 partial dKV rows (one pass would hold ~309 GB); "
+                          "dKV reduced deterministically")
+    del q, kv, idx, iq8, ik8, iw, scores, qmx, kmx, qbs, kbs, out, lse, do
     torch.cuda.empty_cache()
     return res
 
@@ -623,7 +630,7 @@ def main():
         "launch": ("hip_graph" if graph_info is not None else "eager"),
         "eager_tokens_per_s": round(eager_tokens_per_s, 1),
         "graph_replays_checked": (graph_info["checked"] if graph_info is not None else 0),
-        "cfg5": ({"workload": f"s={C5_S} h={C5_H} d_qk={C5_DQK} d_v={C5_DV} topk={C5_TOPK} SparseMLA fwd (bf16; fwd_mxfp8: "
+        "cfg5": ({"workload": f"s={C5_S} h={C5_H} d_qk={C5_DQK} d_v={C5_DV} topk={C5_TOPK} SparseMLA fwd + bwd (bf16; fwd_mxfp8: "
                               f"MXFP8 block-scaled), indexer h={C5_HIDX} d={C5_DIDX} e4m3 causal, top-{C5_TOPK}",
                   "kernels": cfg5} if cfg5 is not None else None),
         "cfg4": ({"workload": f"FP8 tensorwise SparseMLA fwd+bwd at cfg2 shapes (q/kv e4m3, 1% x20 outliers, "

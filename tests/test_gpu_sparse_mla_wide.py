@@ -190,9 +190,9 @@ def test_wide_fp8_fwd_bwd_match_fp8_oracle(dev, outliers, H, dv):
     assert torch.equal(dq, dq2) and torch.equal(dkv, dkv2)
 
 
-def test_cfg5_fwd_full_scale(dev):
-    """cfg5 forward at full size (b=1, s=16384, h=128, topk=2048): sampled
-    tokens vs the oracle; every output finite and inside the convex hull bound."""
+def _cfg5_inputs(dev):
+    """cfg5 shapes (b=1, s=16384, h=128, d_qk=576, topk=2048) on the device:
+    q, kv ~ N(0, 0.5) bf16, uniform distinct causal indices, ascending, -1 padded."""
     B, S, H, topk = 1, 16384, 128, 2048
     gen = torch.Generator(device=dev).manual_seed(2048)
     q = (torch.randn((B, S, H, D), generator=gen, device=dev) * 0.5).to(torch.bfloat16)
@@ -206,6 +206,13 @@ def test_cfg5_fwd_full_scale(dev):
         val, ix = keys.topk(topk, dim=-1)
         ix = torch.where(val >= 0, ix, torch.full_like(ix, S + 1)).sort(dim=-1).values
         idx[0, t0:t0 + 2048, 0] = torch.where(ix > S, torch.full_like(ix, -1), ix).to(torch.int32)
+    return q, kv, idx, gen
+
+
+def test_cfg5_fwd_full_scale(dev):
+    """cfg5 forward at full size (b=1, s=16384, h=128, topk=2048): sampled
+    tokens vs the oracle; every output finite and inside the convex hull bound."""
+    q, kv, idx, _ = _cfg5_inputs(dev)
     out, lse = sparse_mla_fwd_interface(q, kv, idx, sm_scale=D ** -0.5, d_v=DV)
     torch.cuda.synchronize()
     assert torch.isfinite(out).all() and torch.isfinite(lse).all()
@@ -215,6 +222,32 @@ def test_cfg5_fwd_full_scale(dev):
     ro, rl = orc.sparse_mla_fwd(qs, kv.cpu(), ids, D ** -0.5, DV)
     assert_close(out[:, toks], ro, what="cfg5 out (sampled)")
     assert_close(lse[:, toks], rl, what="cfg5 lse2 (sampled)")
+
+
+def test_cfg5_bwd_full_scale(dev):
+    """cfg5 backward at full size (one pass would hold ~309 GB of partial rows;
+    it runs in passes under the default cap): dq of sampled tokens vs the
+    oracle, every output finite, bitwise repeatable, and the dKV column sums:
+    summed over all kv rows the V part is sum_{t,h} dO (each softmax row sums
+    to one) and the rope tail is 0 (sum over slots of dS is 0)."""
+    q, kv, idx, gen = _cfg5_inputs(dev)
+    do = torch.randn(q.shape[:3] + (DV,), generator=gen, device=dev).to(torch.bfloat16)
+    out, lse = sparse_mla_fwd_interface(q, kv, idx, sm_scale=D ** -0.5, d_v=DV)
+    dq, dkv = sparse_mla_bwd(q, kv, out, do, idx, lse, sm_scale=D ** -0.5)
+    dq2, dkv2 = sparse_mla_bwd(q, kv, out, do, idx, lse, sm_scale=D ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(dq, dq2) and torch.equal(dkv, dkv2), "not bitwise repeatable"
+    del dq2, dkv2
+    assert torch.isfinite(dq).all() and torch.isfinite(dkv).all()
+    toks = torch.tensor([0, 1, 2047, 9000, 16383], device=dev)
+    sub = lambda x: x[:, toks].cpu()
+    rdq, _ = orc.sparse_mla_bwd(sub(q), kv.cpu(), sub(out), sub(do), sub(idx), sub(lse), D ** -0.5, DV)
+    assert_close(dq[:, toks], rdq, what="cfg5 dq (sampled)")
+    col = dkv.double().sum(dim=(0, 1, 2)).cpu()
+    expect_v = do.double().sum(dim=(0, 1, 2)).cpu()
+    scale_v = float(expect_v.norm() / DV ** 0.5)
+    assert float((col[:DV] - expect_v).abs().max()) <= 2e-2 * scale_v, "sum_j dKV_j[:d_v] != sum dO"
+    assert float(col[DV:].abs().max()) <= 2e-2 * scale_v, "sum_j dKV_j[d_v:] != 0"
 
 
 @pytest.mark.parametrize("H", [16, 96])
