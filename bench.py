@@ -171,7 +171,7 @@ def measure_cfg5(dev, reps=3):
             gbs = by / t[k] / 1e9
             e.update({"bound": "hbm", "gbs": round(gbs, 1), "peak": PEAK_HBM_GBS, "frac": round(gbs / PEAK_HBM_GBS, 4)})
         res[k] = e
-    res["bwd"]["note"] = ("in passes of <= 2 GiB of fp32 partial dKV rows (one pass would hold ~309 GB); "
+    res["bwd"]["note"] = ("in passes of <= 4 GiB of fp16 partial dKV rows (one pass would hold ~155 GB); "
                           "dKV reduced deterministically")
     del q, kv, idx, iq8, ik8, iw, scores, qmx, kmx, qbs, kbs, out, lse, do
     torch.cuda.empty_cache()

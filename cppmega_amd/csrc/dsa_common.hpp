@@ -74,6 +74,16 @@ __device__ __forceinline__ int partial_row_exponent_bound(float bnd) {
   s = s > 127 ? 127 : (s < -114 ? -114 : s);
   return s;
 }
+// max |x| over the 8 bf16 values of v (NaNs ignored, as fmaxf does).
+__device__ __forceinline__ float bf16x8_absmax(i32x4 v) {
+  float m = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t u = (uint32_t)v[e];
+    m = fmaxf(m, fmaxf(__uint_as_float((u << 16) & 0x7fff0000u), __uint_as_float(u & 0x7fff0000u)));
+  }
+  return m;
+}
 __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
   const _Float16 h = (_Float16)f;  // round to nearest even
   return (uint32_t)__builtin_bit_cast(uint16_t, h);

@@ -586,7 +586,7 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // partial rows; when a batch spans several passes the kv rows' sums are
 // carried between them in fp32 (first pass stores, later passes add, the
 // last casts to bf16), in pass order, so the result stays deterministic.
-constexpr uint64_t kBwdPassBytes = 2ull << 30;  // default: partial rows (+ exponents) per pass
+constexpr uint64_t kBwdPassBytes = 4ull << 30;  // default: partial rows (+ exponents) per pass
 static std::atomic<uint64_t> g_pass_bytes{kBwdPassBytes};
 
 struct BwdPlan {
@@ -596,9 +596,10 @@ struct BwdPlan {
   int NC;       // 32-token chunks per batch within a pass
 };
 
-// bytes per partial element: fp32 with DSA_BWD_FP32_PARTIALS and for wide heads, else fp16
+// bytes per partial element: fp32 with DSA_BWD_FP32_PARTIALS, else fp16
 static int64_t partial_elem_bytes(int flags, int64_t D_qk) {
-  return ((flags & DSA_BWD_FP32_PARTIALS) || D_qk > 256) ? 4 : 2;
+  (void)D_qk;
+  return (flags & DSA_BWD_FP32_PARTIALS) ? 4 : 2;
 }
 
 static BwdPlan bwd_plan(int64_t B, int64_t S, int64_t H, int64_t G, int64_t D_qk, int64_t topk, int flags) {
@@ -742,7 +743,7 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
     DSA_REQUIRE(q_scale && kv_scale, "dsa_sparse_mla_bwd: e4m3 input needs q_scale and kv_scale");
   const bool f8 = dtype == DSA_DTYPE_E4M3;
   const bool wide = wide_shape(D_qk, D_v);
-  const bool f32p = (flags & DSA_BWD_FP32_PARTIALS) != 0 || wide;
+  const bool f32p = (flags & DSA_BWD_FP32_PARTIALS) != 0;
   const bool shape_ok = (D_qk == 128 && D_v == 64) || (D_qk == 128 && D_v == 128) ||
                         (D_qk == 192 && D_v == 128) || (D_qk == 64 && D_v == 32 && !f8) || wide;
   if (!shape_ok)
@@ -823,7 +824,7 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
     p.ntiles = ntiles;
     p.sl2 = sm_scale * kLog2e;
     p.scale = sm_scale;
-    if (wide) rc = launch_bwd_main_wide(p, D_qk, D_v, f8, st);
+    if (wide) rc = launch_bwd_main_wide(p, D_qk, D_v, f8, f32p, st);
     else if (D_qk == 128 && D_v == 64) rc = f8 ? launch_bwd_main_p<128, 64, true>(p, f32p, st) : launch_bwd_main_p<128, 64, false>(p, f32p, st);
     else if (D_qk == 128 && D_v == 128) rc = f8 ? launch_bwd_main_p<128, 128, true>(p, f32p, st) : launch_bwd_main_p<128, 128, false>(p, f32p, st);
     else if (D_qk == 192 && D_v == 128) rc = f8 ? launch_bwd_main_p<192, 128, true>(p, f32p, st) : launch_bwd_main_p<192, 128, false>(p, f32p, st);

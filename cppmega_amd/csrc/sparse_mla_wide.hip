@@ -23,9 +23,10 @@
 //     reads in accumulator order, P straight from registers).
 // The backward (bf16 and e4m3) splits S and dP the same way, then gives each wave every
 // fourth 32-column tile of d_qk for dQ^T = K^T dS^T and for the per-slot dKV
-// row c^T = Q^T dS^T + dO^T P^T, written as fp32 at the entry's CSR position
-// (the kv-major reduction sums those rows in a fixed order, as for the narrow
-// kernels).
+// row c^T = Q^T dS^T + dO^T P^T, written at the entry's CSR position as fp16
+// scaled by a per-row power of two fixed from a bound before the products (as
+// in the narrow kernels), or as fp32 with DSA_BWD_FP32_PARTIALS; the kv-major
+// reduction sums those rows in a fixed order.
 #include <type_traits>
 
 #include "dsa_common.hpp"
@@ -446,6 +447,7 @@ int launch_fwd_wide(const FwdParams &p, int64_t d_qk, int64_t d_v, bool fp8, hip
 // QK^T on the codes and the other products on dequantised bf16.
 template <int D_QK, int D_V, bool FP8>
 struct WideBwdLds {
+  // (after DS) MX: per-wave max |Q| (0..3) and max |dO| (4..7) of the item
   using C = WideCfg<D_QK, D_V, FP8>;
   static constexpr int QL_STRIDE = D_QK * 2 + 32;
   static constexpr int DOL_STRIDE = D_V * 2 + 32;
@@ -461,11 +463,12 @@ struct WideBwdLds {
   static constexpr int SP_W = 16 * 64;  // floats per partial tile
   static constexpr int SP_TILES = FP8 ? 4 : 8;
   static constexpr int OFF_DS = OFF_SP + SP_TILES * SP_W * 4;
-  static constexpr int BYTES = OFF_DS + 4 * 32 * DS_STRIDE;
+  static constexpr int OFF_MX = OFF_DS + 4 * 32 * DS_STRIDE;
+  static constexpr int BYTES = OFF_MX + 8 * 4;
   static_assert(BYTES <= 160 * 1024, "wide backward LDS");
 };
 
-template <int D_QK, int D_V, bool FP8>
+template <int D_QK, int D_V, bool FP8, bool F32P>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 sparse_mla_bwd_wide_kernel(const BwdParams p) {
   using C = WideCfg<D_QK, D_V, FP8>;
@@ -496,6 +499,7 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
   const unsigned char *Ksrc = FP8 ? Kd : Kl;  // bf16 K / V rows for dP and dQ
   constexpr int K_STRIDE = FP8 ? L::KDB_STRIDE : C::KL_STRIDE;
   unsigned char *DS = smem + L::OFF_DS + w * 32 * L::DS_STRIDE;
+  float *MX = reinterpret_cast<float *>(smem + L::OFF_MX);
 
   const int64_t head0 = tok * p.H + g * p.hpg + tile * 32;
   const int nheads = p.hpg - tile * 32 < 32 ? p.hpg - tile * 32 : 32;
@@ -518,6 +522,7 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
   {
     const int t = threadIdx.x;
     constexpr int QCH = D_QK / 8;
+    float mq = 0.0f, md = 0.0f;  // max |Q|, |dO| seen by this thread (fp16 rows only)
     for (int u = t; u < 32 * QCH; u += 256) {
       const int h = u / QCH, c = u % QCH;
       i32x4 v = {0, 0, 0, 0};
@@ -536,6 +541,7 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
         }
       }
       *reinterpret_cast<i32x4 *>(QL + h * L::QL_STRIDE + c * 16) = v;
+      if constexpr (!F32P) mq = fmaxf(mq, bf16x8_absmax(v));
     }
     // dO rows and Delta = sum_d O dO: one wave per head, lane = 8-element chunk
     constexpr int VCH = D_V / 8;
@@ -548,6 +554,7 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
           ov = ld_global_16(p.o + (head0 + h) * D_V + 8 * c);
         }
         *reinterpret_cast<i32x4 *>(DOL + h * L::DOL_STRIDE + c * 16) = dv;
+        if constexpr (!F32P) md = fmaxf(md, bf16x8_absmax(dv));
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const uint32_t du = (uint32_t)dv[e], ou = (uint32_t)ov[e];
@@ -570,6 +577,17 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
         lse_h = (l == -INFINITY) ? INFINITY : l;  // all-masked row: zero gradient
       }
       LD[t] = lse_h;
+    }
+    if constexpr (!F32P) {
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        mq = fmaxf(mq, __shfl_xor(mq, off, 64));
+        md = fmaxf(md, __shfl_xor(md, off, 64));
+      }
+      if (lane == 0) {
+        MX[w] = mq;
+        MX[4 + w] = md;
+      }
     }
   }
 
@@ -646,26 +664,49 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
     float xs = p.sl2;
     if constexpr (FP8) xs *= qsc * Ksc[l32];
     bf16x8 dsB[2], pB[2];
+    int pexp = 0;  // fp16 rows: the slot's partial-row scale exponent (identical in every wave)
     {
       uint32_t dsw[8], pw[8];
+      float P[16], dS[16];
+      float sabs = 0.0f, psum = 0.0f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const f32x4 l4 = *reinterpret_cast<const f32x4 *>(LD + 8 * i + 4 * g32);
         const f32x4 d4 = *reinterpret_cast<const f32x4 *>(LD + 32 + 8 * i + 4 * g32);
-        float P[4], dS[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int a = 4 * i + j;
           const float pv = valid ? exp2_fast(s[a] * xs - l4[j]) : 0.0f;
-          P[j] = pv;
-          dS[j] = pv * fmaf(dp[a], p.scale, -d4[j]);
+          P[a] = pv;
+          dS[a] = pv * fmaf(dp[a], p.scale, -d4[j]);
+          sabs += fabsf(dS[a]);
+          psum += pv;
         }
-        dsw[2 * i] = pack_bf16x2(dS[0], dS[1]);
-        dsw[2 * i + 1] = pack_bf16x2(dS[2], dS[3]);
-        pw[2 * i] = pack_bf16x2(P[0], P[1]);
-        pw[2 * i + 1] = pack_bf16x2(P[2], P[3]);
+        dsw[2 * i] = pack_bf16x2(dS[4 * i], dS[4 * i + 1]);
+        dsw[2 * i + 1] = pack_bf16x2(dS[4 * i + 2], dS[4 * i + 3]);
         *reinterpret_cast<i32x2 *>(DS + l32 * L::DS_STRIDE + (8 * i + 4 * g32) * 2) =
             i32x2{(int)dsw[2 * i], (int)dsw[2 * i + 1]};
+      }
+      float rs = 1.0f;
+      if constexpr (!F32P) {
+        // |c[d]| <= max|Q| sum_h |dS_h| + max|dO| sum_h P_h over the slot's 32
+        // heads; the margin 2^-6 covers the bf16 rounding of dS / P (2^-8) and
+        // the fp32 sums.  c is computed from dS 2^s and P 2^s (exact scalings).
+        const float maxq = fmaxf(fmaxf(MX[0], MX[1]), fmaxf(MX[2], MX[3]));
+        const float maxdo = fmaxf(fmaxf(MX[4], MX[5]), fmaxf(MX[6], MX[7]));
+        const float bnd = sum_halves(fmaf(maxq, sabs, maxdo * psum)) * 1.015625f;
+        pexp = partial_row_exponent_bound(bnd);
+        rs = exp2i(pexp);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          dsw[2 * i] = pack_bf16x2(dS[4 * i] * rs, dS[4 * i + 1] * rs);
+          dsw[2 * i + 1] = pack_bf16x2(dS[4 * i + 2] * rs, dS[4 * i + 3] * rs);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pw[2 * i] = pack_bf16x2(P[4 * i] * rs, P[4 * i + 1] * rs);
+        pw[2 * i + 1] = pack_bf16x2(P[4 * i + 2] * rs, P[4 * i + 3] * rs);
       }
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc) {
@@ -689,8 +730,12 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
       }
     }
 
-    // ---- c^T[d][slot] = Q^T dS^T + dO^T P^T on tiles t = w + 4q, stored as fp32 ----
-    unsigned char *dst = p.partials + ((int64_t)(wr ? pos : 0) * p.ntiles + tile) * (int64_t)(D_QK * 4);
+    // ---- c^T[d][slot] = Q^T dS^T + dO^T P^T on tiles t = w + 4q (fp16 rows: times 2^pexp) ----
+    const int64_t prow = (int64_t)(wr ? pos : 0) * p.ntiles + tile;
+    unsigned char *dst = p.partials + prow * (int64_t)(D_QK * (F32P ? 4 : 2));
+    if constexpr (!F32P) {
+      if (wr && w == 0 && g32 == 0) p.partial_exp[prow] = (int8_t)pexp;
+    }
 #pragma unroll
     for (int q = 0; q < DQW; ++q) {
       const int t = w + 4 * q;
@@ -714,7 +759,15 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int d0 = t * 32 + 8 * i + 4 * g32;
-            st_stream_16(dst + d0 * 4, f32x4{cacc[4 * i], cacc[4 * i + 1], cacc[4 * i + 2], cacc[4 * i + 3]});
+            // plain (write-back) stores: a row's pieces come from four waves and
+            // several instructions, and L2 merges them into whole lines
+            if constexpr (F32P) {
+              *reinterpret_cast<f32x4 *>(dst + d0 * 4) = f32x4{cacc[4 * i], cacc[4 * i + 1], cacc[4 * i + 2],
+                                                               cacc[4 * i + 3]};
+            } else {
+              *reinterpret_cast<i32x2 *>(dst + d0 * 2) =
+                  i32x2{(int)pack_f16x2(cacc[4 * i], cacc[4 * i + 1]), (int)pack_f16x2(cacc[4 * i + 2], cacc[4 * i + 3])};
+            }
           }
         }
       }
@@ -742,22 +795,29 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
   }
 }
 
-template <int D_QK, int D_V, bool FP8>
+template <int D_QK, int D_V, bool FP8, bool F32P>
 static int launch_bwd_wide_t(const BwdParams &p, hipStream_t st) {
   using L = WideBwdLds<D_QK, D_V, FP8>;
   const size_t lds = L::BYTES;
-  hipError_t e = hipFuncSetAttribute((const void *)sparse_mla_bwd_wide_kernel<D_QK, D_V, FP8>,
+  hipError_t e = hipFuncSetAttribute((const void *)sparse_mla_bwd_wide_kernel<D_QK, D_V, FP8, F32P>,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return set_error(DSA_ERR_HIP, "sparse_mla_bwd(wide): LDS attribute: %s", hipGetErrorString(e));
   const int64_t nitems = p.B * p.S * p.G * p.ntiles;
   if (nitems >= (1ll << 31)) return set_error(DSA_ERR_INVALID_ARG, "sparse_mla_bwd(wide): grid too large");
-  hipLaunchKernelGGL((sparse_mla_bwd_wide_kernel<D_QK, D_V, FP8>), dim3((unsigned)nitems), dim3(256), lds, st, p);
+  hipLaunchKernelGGL((sparse_mla_bwd_wide_kernel<D_QK, D_V, FP8, F32P>), dim3((unsigned)nitems), dim3(256), lds, st,
+                     p);
   return check_launch("sparse_mla_bwd_main(wide)");
 }
 
-int launch_bwd_main_wide(const BwdParams &p, int64_t d_qk, int64_t d_v, bool fp8, hipStream_t st) {
-  if (d_qk == 576 && d_v == 512) return fp8 ? launch_bwd_wide_t<576, 512, true>(p, st) : launch_bwd_wide_t<576, 512, false>(p, st);
-  if (d_qk == 576 && d_v == 576) return fp8 ? launch_bwd_wide_t<576, 576, true>(p, st) : launch_bwd_wide_t<576, 576, false>(p, st);
+template <int D_QK, int D_V>
+static int launch_bwd_wide_f(const BwdParams &p, bool fp8, bool f32p, hipStream_t st) {
+  if (fp8) return f32p ? launch_bwd_wide_t<D_QK, D_V, true, true>(p, st) : launch_bwd_wide_t<D_QK, D_V, true, false>(p, st);
+  return f32p ? launch_bwd_wide_t<D_QK, D_V, false, true>(p, st) : launch_bwd_wide_t<D_QK, D_V, false, false>(p, st);
+}
+
+int launch_bwd_main_wide(const BwdParams &p, int64_t d_qk, int64_t d_v, bool fp8, bool f32p, hipStream_t st) {
+  if (d_qk == 576 && d_v == 512) return launch_bwd_wide_f<576, 512>(p, fp8, f32p, st);
+  if (d_qk == 576 && d_v == 576) return launch_bwd_wide_f<576, 576>(p, fp8, f32p, st);
   return set_error(DSA_ERR_UNSUPPORTED, "sparse_mla_bwd(wide): no kernel for d_qk=%lld d_v=%lld", (long long)d_qk,
                    (long long)d_v);
 }

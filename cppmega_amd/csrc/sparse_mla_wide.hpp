@@ -15,6 +15,6 @@ inline bool wide_shape(int64_t d_qk, int64_t d_v) { return d_qk == 576 && (d_v =
 // Forward over all (token, kv group, 32-head tile) items; bf16 or e4m3.
 int launch_fwd_wide(const FwdParams &p, int64_t d_qk, int64_t d_v, bool fp8, hipStream_t st, bool mx = false);
 // Backward main pass (P, dS, dQ, fp32 partial dKV rows at CSR positions); bf16 or e4m3.
-int launch_bwd_main_wide(const BwdParams &p, int64_t d_qk, int64_t d_v, bool fp8, hipStream_t st);
+int launch_bwd_main_wide(const BwdParams &p, int64_t d_qk, int64_t d_v, bool fp8, bool f32p, hipStream_t st);
 
 }  // namespace dsa

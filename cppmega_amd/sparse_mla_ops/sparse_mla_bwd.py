@@ -21,9 +21,9 @@ from ._common import check_same_device, normalize_sm_scale, stream_of, unwrap_qu
 def fp32_partials_default() -> bool:
     """CPPMEGA_AMD_BWD_FP32_PARTIALS=1 keeps the per-(token, slot) dKV rows in fp32
     (exact fp32 accumulation, 2x the workspace traffic); the default stores
-    each row as fp16 scaled by a per-row power of two (11 significant bits
-    relative to the row's largest element) before the deterministic fp32
-    reduction."""
+    each row as fp16 scaled by a per-row power of two (11 significant bits,
+    placed from a bound on the row's magnitudes: max|Q| sum|dS| + max|dO| sum P)
+    before the deterministic fp32 reduction."""
     return os.getenv("CPPMEGA_AMD_BWD_FP32_PARTIALS", "0").strip().lower() in {"1", "true", "yes", "on"}
 
 

@@ -93,7 +93,7 @@ enum dsa_bwd_flags {
 
 /*
  * Per-pass cap on the backward's partial dKV rows (bytes; 0 restores the
- * default of 2 GiB).  dsa_sparse_mla_bwd runs in passes over contiguous token
+ * default of 4 GiB).  dsa_sparse_mla_bwd runs in passes over contiguous token
  * ranges sized to this cap, so its workspace stays bounded at any sequence
  * length; a batch split over passes carries its kv rows' sums in fp32 between
  * them.  Process-wide; set it before dsa_sparse_mla_bwd_workspace_size and
@@ -120,8 +120,8 @@ size_t dsa_sparse_mla_bwd_workspace_size(int64_t B, int64_t S, int64_t S_kv,
  *   delta [B, S, H] f32 = sum_d o * dO, or NULL to compute it from o and dO
  *   dq  [B, S, H, D_qk] bf16 (written), dkv [B, S_kv, G, D_qk] bf16 (written)
  * dKV is reduced deterministically: every kv row sums its per-(token, slot)
- * contribution rows (fp16 with a per-row power-of-two scale, i.e. 11
- * significant bits relative to the row max; fp32 with DSA_BWD_FP32_PARTIALS) in
+ * contribution rows (fp16 with a per-row power-of-two scale taken from a bound
+ * on the row, max|Q| sum|dS| + max|dO| sum P; fp32 with DSA_BWD_FP32_PARTIALS) in
  * ascending (token, kv group, slot) order in fp32, so repeated calls are
  * bitwise identical.  Gradients are with respect to the dequantised values
  * for e4m3 inputs.  The work runs in passes over token ranges whose partial

@@ -1,7 +1,7 @@
 """GPU parity of the SparseMLA backward when it runs in several passes.
 
 dsa_sparse_mla_bwd works through contiguous token ranges sized so that each
-pass's partial dKV rows fit a cap (2 GiB by default, set small here with
+pass's partial dKV rows fit a cap (4 GiB by default, set small here with
 dsa_sparse_mla_bwd_pass_bytes): whole batches per pass, or one batch split
 into 32-token multiples whose kv-row sums are carried in fp32 between passes.
 Each case checks dq / dkv against the oracle at the usual bar, dq bitwise
@@ -30,7 +30,7 @@ def pass_bytes():
 
 def _per_token_bytes(H, D, topk, fp32_rows=False):
     ntiles = (H + 31) // 32
-    return topk * ntiles * (D * (4 if fp32_rows or D > 256 else 2) + 1)
+    return topk * ntiles * (D * (4 if fp32_rows else 2) + 1)
 
 
 def _close_to_one_pass(a, b, what):
@@ -81,16 +81,18 @@ def test_bwd_passes_repeated_rows(dev, pass_bytes):
     assert_close(dkv, rdkv, what="dkv")
 
 
+@pytest.mark.parametrize("fp32_rows", [False, True], ids=["fp16_rows", "fp32_rows"])
 @pytest.mark.parametrize("B,S,H,topk,tokens_per_pass", [(1, 72, 64, 48, 32), (2, 40, 32, 33, 40)])
-def test_bwd_passes_wide(dev, pass_bytes, B, S, H, topk, tokens_per_pass):
-    """d_qk = 576 / d_v = 512 (fp32 partial rows): a split batch, and whole batches per pass."""
+def test_bwd_passes_wide(dev, pass_bytes, B, S, H, topk, tokens_per_pass, fp32_rows):
+    """d_qk = 576 / d_v = 512: a split batch, and whole batches per pass, with
+    fp16 (default) and fp32 partial rows."""
     D, DV = 576, 512
     inp = synthetic.sparse_mla_inputs(B, S, H, D, DV, topk, std=0.5, seed=H + topk)
     q, kv, idx, do = (inp[k].to(dev) for k in ("q", "kv", "indices", "do"))
     out, lse = sparse_mla_fwd_interface(q, kv, idx, sm_scale=inp["scale"], d_v=DV)
-    dq1, dkv1 = sparse_mla_bwd(q, kv, out, do, idx, lse, sm_scale=inp["scale"])
-    pass_bytes(tokens_per_pass * _per_token_bytes(H, D, topk))
-    dq, dkv = sparse_mla_bwd(q, kv, out, do, idx, lse, sm_scale=inp["scale"])
+    dq1, dkv1 = sparse_mla_bwd(q, kv, out, do, idx, lse, sm_scale=inp["scale"], fp32_partials=fp32_rows)
+    pass_bytes(tokens_per_pass * _per_token_bytes(H, D, topk, fp32_rows))
+    dq, dkv = sparse_mla_bwd(q, kv, out, do, idx, lse, sm_scale=inp["scale"], fp32_partials=fp32_rows)
     rdq, rdkv = orc.sparse_mla_bwd(inp["q"], inp["kv"], out.cpu(), inp["do"], inp["indices"], lse.cpu(),
                                    inp["scale"], DV)
     assert_close(dq, rdq, what="dq")
