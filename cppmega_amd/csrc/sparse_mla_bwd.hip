@@ -471,15 +471,16 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
     // ---- the slot's partial row, written at its CSR position ----
     // lane: slot l32, d = dt*32 + 16(i>>1) + 8*g32 + 4(i&1) + j (the permuted Q^T / dO^T columns).
     if constexpr (F32P) {
-      // fp32 rows: the two lanes of a slot store adjacent 16-byte pieces
+      // fp32 rows: the two lanes of a slot store adjacent 16-byte pieces, with
+      // plain (write-back) stores so that L2 merges a row's pieces into lines
       unsigned char *dst = p.partials + prow_me * (uint64_t)(D_QK * 4);
 #pragma unroll
       for (int dt = 0; dt < C::DQT; ++dt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int d0 = dt * 32 + 16 * (i >> 1) + 8 * g32 + 4 * (i & 1);
-          st_stream_16(dst + d0 * 4, f32x4{cacc[dt][4 * i], cacc[dt][4 * i + 1], cacc[dt][4 * i + 2],
-                                           cacc[dt][4 * i + 3]});
+          *reinterpret_cast<f32x4 *>(dst + d0 * 4) = f32x4{cacc[dt][4 * i], cacc[dt][4 * i + 1],
+                                                           cacc[dt][4 * i + 2], cacc[dt][4 * i + 3]};
         }
     } else {
       // fp16 rows scaled by a power of two mapping the row max into [2^13, 2^14)
