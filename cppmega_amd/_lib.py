@@ -35,6 +35,8 @@ EXPORTED_SYMBOLS = (
     "dsa_abi_version",
     "dsa_device_check",
     "dsa_sparse_mla_fwd",
+    "dsa_sparse_mla_fwd_workspace_size",
+    "dsa_sparse_mla_fwd_ws",
     "dsa_sparse_mla_bwd_workspace_size",
     "dsa_sparse_mla_bwd_pass_bytes",
     "dsa_sparse_mla_bwd",
@@ -71,6 +73,10 @@ _SIGNATURES = {
     "dsa_sparse_mla_fwd": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                   _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                   _f32, _i32, _c_void_p, _c_void_p, _c_void_p]),
+    "dsa_sparse_mla_fwd_workspace_size": (_size_t, [_i64] * 5 + [_i32]),
+    "dsa_sparse_mla_fwd_ws": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                     _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                     _f32, _i32, _c_void_p, _c_void_p, _c_void_p, _size_t, _c_void_p]),
     "dsa_sparse_mla_bwd_workspace_size": (_size_t, [_i64] * 8 + [_i32]),
     "dsa_sparse_mla_bwd_pass_bytes": (_i32, [ctypes.c_uint64]),
     "dsa_sparse_mla_bwd": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,

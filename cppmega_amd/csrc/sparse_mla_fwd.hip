@@ -31,9 +31,13 @@
 
 namespace dsa {
 
-template <int D_QK, int D_V, bool FP8, bool MX = false>
+template <int D_QK, int D_V, bool FP8, bool MX = false, bool VPRE = false>
 struct FwdCfg {
   using Gat = GatherCfg<D_QK, D_V, FP8, MX>;
+  // e4m3 with V dequantised once per call: the V rows are gathered as bf16
+  // straight into the V tile (a bf16 gather over d_v columns), not converted
+  using VGat = GatherCfg<D_V, D_V, false>;
+  static_assert(!VPRE || FP8, "pre-dequantised V exists for e4m3 input only");
   static constexpr int KL_BYTES = 32 * Gat::KL_STRIDE;
   static constexpr int KD_STRIDE = D_V * 2 + 32;          // e4m3: dequantised V rows (bf16)
   static constexpr int KD_BYTES = FP8 ? 32 * KD_STRIDE : 0;
@@ -46,11 +50,13 @@ struct FwdCfg {
   static_assert(D_V % 32 == 0 && D_QK % 16 == 0 && D_V <= D_QK, "unsupported head dims");
 };
 
-template <int D_QK, int D_V, bool FP8, bool MX = false>
+template <int D_QK, int D_V, bool FP8, bool MX = false, bool VPRE = false>
 __global__ void __launch_bounds__(256)
 sparse_mla_fwd_kernel(const FwdParams p) {
-  using C = FwdCfg<D_QK, D_V, FP8, MX>;
+  using C = FwdCfg<D_QK, D_V, FP8, MX, VPRE>;
   using Gat = typename C::Gat;
+  using VGat = typename C::VGat;
+  static_assert(VGat::KL_STRIDE == C::KD_STRIDE, "bf16 V rows land in the V tile's layout");
   typedef typename std::conditional<FP8, long, bf16x8>::type qop_t;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
@@ -93,6 +99,12 @@ sparse_mla_fwd_kernel(const FwdParams p) {
   const auto sc_rs = make_buffer_rsrc(kv_scale_b, FP8 ? (uint32_t)(p.S_kv * sc_pitch) : 0u);
   typename Gat::Regs rg;
   gather_issue<Gat>(rg, kv_rs, sc_rs, idx_cur, row_pitch, sc_pitch);
+  // pre-dequantised V rows [B, S_kv, G, D_V] bf16 of this (batch, group)
+  const uint32_t v_pitch = (uint32_t)(p.G * D_V * 2);
+  const auto v_rs = make_buffer_rsrc(VPRE ? p.v16 + ((b * p.S_kv) * p.G + g) * D_V : nullptr,
+                                     VPRE ? (uint32_t)(p.S_kv * (int64_t)v_pitch) : 0u);
+  typename VGat::Regs rgv;
+  if constexpr (VPRE) gather_issue<VGat>(rgv, v_rs, v_rs, idx_cur, v_pitch);
 
   // Q as the B operand: lane = head, 8 consecutive d per k-step, through a
   // resource that ends at the tile's last head (padded heads read zeros), so
@@ -132,7 +144,10 @@ sparse_mla_fwd_kernel(const FwdParams p) {
     // ---- stage block blk: K row-major, V transposed (bf16, dequantised for e4m3) ----
     gather_store_k<Gat>(rg, Kl);
     if constexpr (FP8) {
-      gather_store_dequant<Gat, Gat::NCH_V>(rg, Kd, C::KD_STRIDE);
+      if constexpr (VPRE)
+        gather_store_k<VGat>(rgv, Kd);
+      else
+        gather_store_dequant<Gat, Gat::NCH_V>(rg, Kd, C::KD_STRIDE);
       gather_store_scale<Gat>(rg, Ksc);
     }
     const uint64_t vmask = __ballot(idx_cur >= 0);
@@ -142,6 +157,7 @@ sparse_mla_fwd_kernel(const FwdParams p) {
     const int raw_nn = load_slot_raw(idx_rs, blk + 2, l32);
     const int idx_nxt = slot_index(raw_nxt, blk + 1, l32, p.topk, p.S_kv);
     gather_issue<Gat>(rg, kv_rs, sc_rs, idx_nxt, row_pitch, sc_pitch);
+    if constexpr (VPRE) gather_issue<VGat>(rgv, v_rs, v_rs, idx_nxt, v_pitch);
 
     // ---- S^T = K Q^T  (M = slot, N = head, K = d) ----
     f32x16 sacc;
@@ -266,31 +282,70 @@ sparse_mla_fwd_kernel(const FwdParams p) {
   }
 }
 
-template <int D_QK, int D_V, bool FP8, bool MX = false>
-static int launch_fwd(const FwdParams &p, hipStream_t st) {
-  using C = FwdCfg<D_QK, D_V, FP8, MX>;
+template <int D_QK, int D_V, bool FP8, bool MX, bool VPRE>
+static int launch_fwd_t(const FwdParams &p, hipStream_t st) {
+  using C = FwdCfg<D_QK, D_V, FP8, MX, VPRE>;
   const size_t lds = 4 * (size_t)C::WAVE_BYTES;
   if (lds > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void *)sparse_mla_fwd_kernel<D_QK, D_V, FP8, MX>,
+    hipError_t e = hipFuncSetAttribute((const void *)sparse_mla_fwd_kernel<D_QK, D_V, FP8, MX, VPRE>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return set_error(DSA_ERR_HIP, "sparse_mla_fwd: LDS attribute: %s", hipGetErrorString(e));
   }
   const int64_t nitems = p.B * p.S * p.G * p.ntiles;
   const int64_t nblocks = (nitems + 3) / 4;
   if (nitems >= (1ll << 31)) return set_error(DSA_ERR_INVALID_ARG, "sparse_mla_fwd: grid too large");
-  hipLaunchKernelGGL((sparse_mla_fwd_kernel<D_QK, D_V, FP8, MX>), dim3((unsigned)nblocks), dim3(256), lds, st, p);
+  hipLaunchKernelGGL((sparse_mla_fwd_kernel<D_QK, D_V, FP8, MX, VPRE>), dim3((unsigned)nblocks), dim3(256), lds, st,
+                     p);
   return check_launch("sparse_mla_fwd");
+}
+
+// e4m3: the kernel reads pre-dequantised V rows when p.v16 is set
+template <int D_QK, int D_V, bool FP8, bool MX = false>
+static int launch_fwd(const FwdParams &p, hipStream_t st) {
+  if constexpr (FP8) {
+    if (p.v16) return launch_fwd_t<D_QK, D_V, true, MX, true>(p, st);
+  }
+  return launch_fwd_t<D_QK, D_V, FP8, MX, false>(p, st);
+}
+
+// V rows of e4m3 kv dequantised to bf16 once per call, with the arithmetic of
+// the kernels' in-LDS dequantisation (hardware e4m3 pair decode, times the
+// row's or the 32-channel block's scale, round to nearest even), so the values
+// are bit-identical.  One thread per 8 consecutive V columns of a row; rows
+// are (b, s_kv, g), kv_scale [B, S_kv] per (b, s_kv), or MX [B, S_kv, G, D_qk / 32].
+template <bool MX>
+__global__ void __launch_bounds__(256)
+dequant_v_kernel(const unsigned char *kv, const float *kv_scale, uint16_t *v16, int64_t rows, int G, int D_qk,
+                 int D_v) {
+  const int per_row = D_v / 8;
+  const int64_t n = rows * per_row;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / per_row;
+    const int c8 = (int)(i - row * per_row);
+    const uint2 raw = *reinterpret_cast<const uint2 *>(kv + row * D_qk + 8 * c8);
+    const float s = MX ? kv_scale[row * (D_qk / 32) + (8 * c8) / 32] : kv_scale[row / G];
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const f32x2 v2 = e4m3x2_to_f32(e < 2 ? raw.x : raw.y, (e & 1) != 0);
+      w[e] = pack_bf16x2(v2[0] * s, v2[1] * s);
+    }
+    *reinterpret_cast<i32x4 *>(v16 + row * D_v + 8 * c8) = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+  }
 }
 
 }  // namespace dsa
 
 using namespace dsa;
 
-extern "C" int dsa_sparse_mla_fwd(const void *q, const void *kv, const int32_t *indices, void *out,
-                                  float *lse2, int64_t B, int64_t S, int64_t S_kv, int64_t H,
-                                  int64_t G, int64_t D_qk, int64_t D_v, int64_t topk, float sm_scale,
-                                  int dtype, const float *q_scale, const float *kv_scale,
-                                  void *stream) {
+static size_t v16_bytes(int64_t B, int64_t S_kv, int64_t G, int64_t D_v) {
+  return ((size_t)B * S_kv * G * D_v * 2 + 255) & ~(size_t)255;
+}
+
+static int sparse_mla_fwd_impl(const void *q, const void *kv, const int32_t *indices, void *out, float *lse2,
+                               int64_t B, int64_t S, int64_t S_kv, int64_t H, int64_t G, int64_t D_qk, int64_t D_v,
+                               int64_t topk, float sm_scale, int dtype, const float *q_scale, const float *kv_scale,
+                               void *workspace, size_t workspace_bytes, void *stream) {
   DSA_REQUIRE(B >= 0 && S >= 0 && S_kv > 0 && H > 0 && G > 0 && topk > 0,
               "dsa_sparse_mla_fwd: bad dims B=%lld S=%lld S_kv=%lld H=%lld G=%lld topk=%lld",
               (long long)B, (long long)S, (long long)S_kv, (long long)H, (long long)G, (long long)topk);
@@ -312,6 +367,7 @@ extern "C" int dsa_sparse_mla_fwd(const void *q, const void *kv, const int32_t *
   p.lse = lse2;
   p.q_scale = q_scale;
   p.kv_scale = kv_scale;
+  p.v16 = nullptr;
   p.B = B;
   p.S = S;
   p.S_kv = S_kv;
@@ -324,6 +380,24 @@ extern "C" int dsa_sparse_mla_fwd(const void *q, const void *kv, const int32_t *
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool f8 = dtype == DSA_DTYPE_E4M3;
   DSA_REQUIRE(S_kv * G * D_qk * 2 < (1ll << 32), "dsa_sparse_mla_fwd: kv rows of one batch exceed 4 GiB");
+  if (workspace != nullptr && dtype != DSA_DTYPE_BF16 && !wide_shape(D_qk, D_v)) {
+    // e4m3 / MX: dequantise the V rows once instead of once per gather
+    DSA_REQUIRE(workspace_bytes >= v16_bytes(B, S_kv, G, D_v), "dsa_sparse_mla_fwd: workspace %zu < required %zu",
+                workspace_bytes, v16_bytes(B, S_kv, G, D_v));
+    uint16_t *v16 = static_cast<uint16_t *>(workspace);
+    const int64_t rows = B * S_kv * G;
+    const int64_t n = rows * (D_v / 8);
+    const unsigned grid = (unsigned)((n + 255) / 256 < 8192 ? (n + 255) / 256 : 8192);
+    if (dtype == DSA_DTYPE_MXFP8)
+      hipLaunchKernelGGL(dequant_v_kernel<true>, dim3(grid), dim3(256), 0, st, p.kv, kv_scale, v16, rows, (int)G,
+                         (int)D_qk, (int)D_v);
+    else
+      hipLaunchKernelGGL(dequant_v_kernel<false>, dim3(grid), dim3(256), 0, st, p.kv, kv_scale, v16, rows, (int)G,
+                         (int)D_qk, (int)D_v);
+    const int rc = check_launch("sparse_mla_fwd(dequant V)");
+    if (rc) return rc;
+    p.v16 = v16;
+  }
   if (dtype == DSA_DTYPE_MXFP8) {  // e4m3 with one scale per 32 channels of every row
     if (D_qk == 128 && D_v == 64) return launch_fwd<128, 64, true, true>(p, st);
     if (D_qk == 128 && D_v == 128) return launch_fwd<128, 128, true, true>(p, st);
@@ -339,4 +413,32 @@ extern "C" int dsa_sparse_mla_fwd(const void *q, const void *kv, const int32_t *
   if (D_qk == 64 && D_v == 32 && !f8) return launch_fwd<64, 32, false>(p, st);
   return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_fwd: no kernel for d_qk=%lld d_v=%lld dtype=%d",
                    (long long)D_qk, (long long)D_v, dtype);
+}
+
+extern "C" int dsa_sparse_mla_fwd(const void *q, const void *kv, const int32_t *indices, void *out,
+                                  float *lse2, int64_t B, int64_t S, int64_t S_kv, int64_t H,
+                                  int64_t G, int64_t D_qk, int64_t D_v, int64_t topk, float sm_scale,
+                                  int dtype, const float *q_scale, const float *kv_scale,
+                                  void *stream) {
+  return sparse_mla_fwd_impl(q, kv, indices, out, lse2, B, S, S_kv, H, G, D_qk, D_v, topk, sm_scale, dtype, q_scale,
+                             kv_scale, nullptr, 0, stream);
+}
+
+extern "C" size_t dsa_sparse_mla_fwd_workspace_size(int64_t B, int64_t S_kv, int64_t G, int64_t D_qk,
+                                                    int64_t D_v, int dtype) {
+  // the wide (d_qk = 576) kernels keep converting V in LDS: at cfg5 reading bf16
+  // V rows (1 KiB each, beside 576 B of codes) was no faster than converting them
+  if (B <= 0 || S_kv <= 0 || G <= 0 || D_v <= 0 || dtype == DSA_DTYPE_BF16 || wide_shape(D_qk, D_v)) return 0;
+  return v16_bytes(B, S_kv, G, D_v);
+}
+
+extern "C" int dsa_sparse_mla_fwd_ws(const void *q, const void *kv, const int32_t *indices, void *out,
+                                     float *lse2, int64_t B, int64_t S, int64_t S_kv, int64_t H, int64_t G,
+                                     int64_t D_qk, int64_t D_v, int64_t topk, float sm_scale, int dtype,
+                                     const float *q_scale, const float *kv_scale, void *workspace,
+                                     size_t workspace_bytes, void *stream) {
+  const size_t need = dsa_sparse_mla_fwd_workspace_size(B, S_kv, G, D_qk, D_v, dtype);
+  DSA_REQUIRE(need == 0 || workspace, "dsa_sparse_mla_fwd_ws: null workspace (%zu bytes required)", need);
+  return sparse_mla_fwd_impl(q, kv, indices, out, lse2, B, S, S_kv, H, G, D_qk, D_v, topk, sm_scale, dtype, q_scale,
+                             kv_scale, need ? workspace : nullptr, workspace_bytes, stream);
 }

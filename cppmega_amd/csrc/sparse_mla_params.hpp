@@ -14,6 +14,7 @@ struct FwdParams {
   float *lse;
   const float *q_scale;
   const float *kv_scale;
+  const uint16_t *v16;  // e4m3 / MX: V rows dequantised once to bf16 [B, S_kv, G, D_v], or null
   int64_t B, S, S_kv, H, G, topk;
   int hpg;     // heads per kv group
   int ntiles;  // ceil(hpg / 32)

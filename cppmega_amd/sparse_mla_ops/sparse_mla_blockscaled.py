@@ -133,11 +133,16 @@ def sparse_mla_blockscaled_mxfp8_fwd_interface(q_data, kv_data, q_scale, kv_scal
     out = torch.empty((batch, seq_len, heads, d_v), dtype=torch.bfloat16, device=q_data.device)
     lse = torch.empty((batch, seq_len, heads), dtype=torch.float32, device=q_data.device)
     dev, stream = stream_of(q_data)
-    rc = _lib.load().dsa_sparse_mla_fwd(
+    L = _lib.load()
+    # the V rows are dequantised to bf16 once per call (with their block scales) into a workspace
+    ws_bytes = int(L.dsa_sparse_mla_fwd_workspace_size(batch, seq_len_kv, kv_group, dim_total, d_v,
+                                                       _lib.DTYPE_MXFP8))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q_data.device) if ws_bytes else None
+    rc = L.dsa_sparse_mla_fwd_ws(
         q_data.data_ptr(), kv_data.data_ptr(), indices.data_ptr(), out.data_ptr(), lse.data_ptr(),
         batch, seq_len, seq_len_kv, heads, kv_group, dim_total, d_v, topk, scale, _lib.DTYPE_MXFP8,
-        q_scale.data_ptr(), kv_scale.data_ptr(), stream)
-    _lib.check(rc, "dsa_sparse_mla_fwd(mxfp8)")
+        q_scale.data_ptr(), kv_scale.data_ptr(), _lib.ptr(ws), ws_bytes, stream)
+    _lib.check(rc, "dsa_sparse_mla_fwd_ws(mxfp8)")
     if squeeze_batch:
         out, lse = out.squeeze(0), lse.squeeze(0)
     return out, lse

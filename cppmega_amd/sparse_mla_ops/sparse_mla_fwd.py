@@ -25,11 +25,15 @@ def _launch_fwd(q, kv, indices, sm_scale, d_v, dtype_code, q_scale=None, kv_scal
     out = torch.empty((B, S, H, d_v), dtype=torch.bfloat16, device=q.device)
     lse = torch.empty((B, S, H), dtype=torch.float32, device=q.device)
     _, stream = stream_of(q)
-    rc = _lib.load().dsa_sparse_mla_fwd(
+    L = _lib.load()
+    # e4m3: the V rows are dequantised to bf16 once per call into a workspace
+    ws_bytes = int(L.dsa_sparse_mla_fwd_workspace_size(B, S_kv, G, D, d_v, dtype_code))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device) if ws_bytes else None
+    rc = L.dsa_sparse_mla_fwd_ws(
         q.data_ptr(), kv.data_ptr(), indices.data_ptr(), out.data_ptr(), lse.data_ptr(),
         B, S, S_kv, H, G, D, d_v, topk, float(sm_scale), dtype_code,
-        _lib.ptr(q_scale), _lib.ptr(kv_scale), stream)
-    _lib.check(rc, "dsa_sparse_mla_fwd")
+        _lib.ptr(q_scale), _lib.ptr(kv_scale), _lib.ptr(ws), ws_bytes, stream)
+    _lib.check(rc, "dsa_sparse_mla_fwd_ws")
     return out, lse
 
 

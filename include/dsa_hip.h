@@ -84,6 +84,25 @@ int dsa_sparse_mla_fwd(const void *q, const void *kv, const int32_t *indices,
                        const float *q_scale, const float *kv_scale,
                        void *stream);
 
+/*
+ * The same forward with a workspace: for e4m3 and MXFP8 input the V rows
+ * (the first D_v columns of kv) are dequantised to bf16 once per call into the
+ * workspace, bit-identical to the per-gather dequantisation of
+ * dsa_sparse_mla_fwd, and the kernel gathers those rows instead of converting
+ * every gathered row again.  dsa_sparse_mla_fwd_workspace_size returns the
+ * bytes needed (B * S_kv * G * D_v bf16; 0 for bf16 input and for the
+ * d_qk = 576 kernels, which keep converting V in LDS; then `workspace` may be
+ * NULL).  Replaces the same reference interfaces as dsa_sparse_mla_fwd.
+ */
+size_t dsa_sparse_mla_fwd_workspace_size(int64_t B, int64_t S_kv, int64_t G,
+                                         int64_t D_qk, int64_t D_v, int dtype);
+int dsa_sparse_mla_fwd_ws(const void *q, const void *kv, const int32_t *indices,
+                          void *out, float *lse2, int64_t B, int64_t S,
+                          int64_t S_kv, int64_t H, int64_t G, int64_t D_qk,
+                          int64_t D_v, int64_t topk, float sm_scale, int dtype,
+                          const float *q_scale, const float *kv_scale,
+                          void *workspace, size_t workspace_bytes, void *stream);
+
 /* dsa_sparse_mla_bwd flags */
 enum dsa_bwd_flags {
   /* Keep the per-(token, slot) dKV rows in fp32 instead of bf16 before the

@@ -98,3 +98,43 @@ def test_per_token_cast_broadcasts_scale(dev):
     r8, rs = ofp8.tensorwise_quantize(x)
     assert s.shape == (6,) and torch.all(s.cpu() == rs)
     assert torch.equal(x8.cpu().view(torch.uint8), r8.view(torch.uint8))
+
+
+@pytest.mark.parametrize("mx", [False, True], ids=["e4m3", "mxfp8"])
+@pytest.mark.parametrize("B,S,H,G,D,DV,topk", [(2, 96, 32, 1, 128, 64, 64), (1, 80, 64, 2, 128, 128, 48),
+                                               (1, 64, 32, 1, 192, 128, 40)])
+def test_fwd_with_v_dequantised_once_is_bit_identical(dev, mx, B, S, H, G, D, DV, topk):
+    """dsa_sparse_mla_fwd_ws (V rows dequantised to bf16 once per call into the
+    workspace) returns the same bits as dsa_sparse_mla_fwd (V converted per
+    gather), with per-row and per-block scales and masked slots."""
+    from cppmega_amd import _lib
+    L = _lib.load()
+    g = torch.Generator(device=dev).manual_seed(B * S + H + D)
+    q8 = torch.randn((B, S, H, D), generator=g, device=dev).to(torch.float8_e4m3fn)
+    k8 = torch.randn((B, S, G, D), generator=g, device=dev).to(torch.float8_e4m3fn)
+    idx = synthetic.causal_indices(B, S, topk, seed=S).to(dev).expand(B, S, G, topk).contiguous()
+    idx[:, 5, :, 3:9] = -1
+    if mx:
+        dtype = _lib.DTYPE_MXFP8
+        qs = torch.exp2(torch.randint(-3, 2, (B, S, H, D // 32), generator=g, device=dev).float()) * 1.37
+        ks = torch.exp2(torch.randint(-3, 2, (B, S, G, D // 32), generator=g, device=dev).float()) * 0.61
+    else:
+        dtype = _lib.DTYPE_E4M3
+        qs = torch.rand((B, S), generator=g, device=dev) + 0.25
+        ks = torch.rand((B, S), generator=g, device=dev) + 0.25
+    outs = []
+    for use_ws in (False, True):
+        out = torch.empty((B, S, H, DV), dtype=torch.bfloat16, device=dev)
+        lse = torch.empty((B, S, H), dtype=torch.float32, device=dev)
+        st = torch.cuda.current_stream().cuda_stream
+        args = (q8.data_ptr(), k8.data_ptr(), idx.data_ptr(), out.data_ptr(), lse.data_ptr(), B, S, S, H, G, D, DV,
+                topk, D ** -0.5, dtype, qs.data_ptr(), ks.data_ptr())
+        if use_ws:
+            n = int(L.dsa_sparse_mla_fwd_workspace_size(B, S, G, D, DV, dtype))
+            assert n >= B * S * G * DV * 2
+            ws = torch.empty(n, dtype=torch.uint8, device=dev)
+            _lib.check(L.dsa_sparse_mla_fwd_ws(*args, ws.data_ptr(), n, st), "dsa_sparse_mla_fwd_ws")
+        else:
+            _lib.check(L.dsa_sparse_mla_fwd(*args, st), "dsa_sparse_mla_fwd")
+        outs.append((out, lse))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
