@@ -39,6 +39,10 @@ EXPORTED_SYMBOLS = (
     "dsa_sparse_mla_fwd_ws",
     "dsa_sparse_mla_bwd_workspace_size",
     "dsa_sparse_mla_bwd_pass_bytes",
+    "dsa_sparse_mla_bwd_index_size",
+    "dsa_sparse_mla_bwd_indexed_workspace_size",
+    "dsa_sparse_mla_bwd_build_index",
+    "dsa_sparse_mla_bwd_indexed",
     "dsa_sparse_mla_bwd",
     "dsa_indexer_scores",
     "dsa_indexer_scores_masked",
@@ -79,6 +83,11 @@ _SIGNATURES = {
                                      _f32, _i32, _c_void_p, _c_void_p, _c_void_p, _size_t, _c_void_p]),
     "dsa_sparse_mla_bwd_workspace_size": (_size_t, [_i64] * 8 + [_i32]),
     "dsa_sparse_mla_bwd_pass_bytes": (_i32, [ctypes.c_uint64]),
+    "dsa_sparse_mla_bwd_index_size": (_size_t, [_i64] * 8 + [_i32]),
+    "dsa_sparse_mla_bwd_indexed_workspace_size": (_size_t, [_i64] * 8 + [_i32]),
+    "dsa_sparse_mla_bwd_build_index": (_i32, [_c_void_p] + [_i64] * 8 + [_i32, _c_void_p, _size_t, _c_void_p]),
+    "dsa_sparse_mla_bwd_indexed": (_i32, [_c_void_p] * 9 + [_c_void_p, _size_t, _c_void_p, _size_t] + [_i64] * 8
+                                   + [_f32, _i32, _c_void_p, _c_void_p, _i32, _c_void_p]),
     "dsa_sparse_mla_bwd": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                   _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _size_t,
                                   _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,

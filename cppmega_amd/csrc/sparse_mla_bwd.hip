@@ -624,8 +624,16 @@ static BwdPlan bwd_plan(int64_t B, int64_t S, int64_t H, int64_t G, int64_t D_qk
   return pl;
 }
 
+// Workspace: the partial-row section (rows, exponents, carry) and the
+// inverse-index section (per 32-token chunk and kv row a token bitmask and a
+// base word, chunk flags, row totals, rowptr, CSR positions), each sized for
+// one pass.  dsa_sparse_mla_bwd takes both in one buffer (rows first);
+// dsa_sparse_mla_bwd_indexed takes the index section as a separate buffer that
+// dsa_sparse_mla_bwd_build_index filled ahead of the call.
 struct BwdWorkspace {
-  size_t partials, pexp, mask, base, dup, tot, rowptr, pos_of, carry, total;
+  size_t partials, pexp, carry, rows_total;          // offsets in the rows section
+  size_t mask, base, dup, tot, rowptr, pos_of, index_total;  // offsets in the index section
+  size_t total;                                      // rows section + index section
   BwdPlan plan;
 };
 
@@ -644,6 +652,10 @@ static BwdWorkspace bwd_layout(int64_t B, int64_t S, int64_t S_kv, int64_t H, in
   off += align256((entries * ntiles + 1) * D_qk * psz);  // + one trash row for masked slots
   L.pexp = off;
   off += align256(entries * ntiles + 1);
+  L.carry = off;  // fp32 sums of one batch's kv rows, carried across its passes
+  off += pl.npb > 1 ? align256((size_t)R * D_qk * 4) : 0;
+  L.rows_total = off;
+  off = 0;
   L.mask = off;
   off += align256((size_t)pl.nb * pl.NC * R * 4);
   L.base = off;
@@ -656,10 +668,35 @@ static BwdWorkspace bwd_layout(int64_t B, int64_t S, int64_t S_kv, int64_t H, in
   off += align256(((size_t)pl.nb * R + 1) * 4);
   L.pos_of = off;
   off += align256(entries * 4);
-  L.carry = off;  // fp32 sums of one batch's kv rows, carried across its passes
-  off += pl.npb > 1 ? align256((size_t)R * D_qk * 4) : 0;
-  L.total = off;
+  L.index_total = off;
+  L.total = L.rows_total + L.index_total;
   return L;
+}
+
+static int64_t bwd_passes(const BwdPlan &pl, int64_t B) {
+  return pl.npb > 1 ? B * pl.npb : (B + pl.nb - 1) / pl.nb;
+}
+
+// The inverse index of one pass (tokens [T0, T0 + nbp * ctp) of the flattened
+// [B * S]) in the index section ix.
+static CsrParams bwd_csr_params(const int32_t *indices, const BwdWorkspace &L, unsigned char *ix, int64_t T0,
+                                int64_t ctp, int64_t S_kv, int64_t G, int64_t topk, bool wide) {
+  CsrParams cp;
+  cp.idx = indices + T0 * G * topk;
+  cp.mask = reinterpret_cast<uint32_t *>(ix + L.mask);
+  cp.base = reinterpret_cast<int32_t *>(ix + L.base);
+  cp.dup = reinterpret_cast<int32_t *>(ix + L.dup);
+  cp.tot = reinterpret_cast<int32_t *>(ix + L.tot);
+  cp.rowptr = reinterpret_cast<int32_t *>(ix + L.rowptr);
+  cp.pos_of = reinterpret_cast<int32_t *>(ix + L.pos_of);
+  cp.S = ctp;
+  cp.S_kv = S_kv;
+  cp.G = G;
+  cp.topk = topk;
+  cp.R = S_kv * G;
+  cp.NC = csr_chunks(ctp);
+  cp.dup_only = wide ? 0 : 1;  // the narrow main kernel derives the positions of chunks without repeats
+  return cp;
 }
 
 template <int D_QK, int D_V, bool FP8, bool F32P>
@@ -713,56 +750,46 @@ extern "C" size_t dsa_sparse_mla_bwd_workspace_size(int64_t B, int64_t S, int64_
   return bwd_layout(B, S, S_kv, H, G, D_qk, topk, flags).total;
 }
 
-extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, const void *dO,
-                                  const int32_t *indices, const float *lse2, const float *delta, void *dq,
-                                  void *dkv, void *workspace, size_t workspace_bytes, int64_t B, int64_t S,
-                                  int64_t S_kv, int64_t H, int64_t G, int64_t D_qk, int64_t D_v, int64_t topk,
-                                  float sm_scale, int dtype, const float *q_scale, const float *kv_scale,
-                                  int flags, void *stream) {
+static int bwd_check(const char *fn, int64_t B, int64_t S, int64_t S_kv, int64_t H, int64_t G, int64_t D_qk,
+                     int64_t D_v, int64_t topk, int dtype, int flags) {
   DSA_REQUIRE(B >= 0 && S >= 0 && S_kv > 0 && H > 0 && G > 0 && topk > 0,
-              "dsa_sparse_mla_bwd: bad dims B=%lld S=%lld S_kv=%lld H=%lld G=%lld topk=%lld",
-              (long long)B, (long long)S, (long long)S_kv, (long long)H, (long long)G, (long long)topk);
-  DSA_REQUIRE(H % G == 0, "dsa_sparse_mla_bwd: H=%lld not divisible by G=%lld", (long long)H, (long long)G);
-  DSA_REQUIRE(D_v > 0 && D_v <= D_qk, "dsa_sparse_mla_bwd: need 0 < d_v <= d_qk");
-  DSA_REQUIRE(dtype == DSA_DTYPE_BF16 || dtype == DSA_DTYPE_E4M3, "dsa_sparse_mla_bwd: dtype %d", dtype);
-  DSA_REQUIRE((flags & ~DSA_BWD_FP32_PARTIALS) == 0, "dsa_sparse_mla_bwd: unknown flags 0x%x", flags);
-  hipStream_t st = static_cast<hipStream_t>(stream);
+              "%s: bad dims B=%lld S=%lld S_kv=%lld H=%lld G=%lld topk=%lld", fn, (long long)B, (long long)S,
+              (long long)S_kv, (long long)H, (long long)G, (long long)topk);
+  DSA_REQUIRE(H % G == 0, "%s: H=%lld not divisible by G=%lld", fn, (long long)H, (long long)G);
+  DSA_REQUIRE(D_v > 0 && D_v <= D_qk, "%s: need 0 < d_v <= d_qk", fn);
+  DSA_REQUIRE(dtype == DSA_DTYPE_BF16 || dtype == DSA_DTYPE_E4M3, "%s: dtype %d", fn, dtype);
+  DSA_REQUIRE((flags & ~DSA_BWD_FP32_PARTIALS) == 0, "%s: unknown flags 0x%x", fn, flags);
   const int64_t R = S_kv * G;
-  const int64_t rows = B * R;
-  if (B == 0) return DSA_OK;
-  DSA_REQUIRE(dkv, "dsa_sparse_mla_bwd: null dkv");
   const int64_t entries = B * S * G * topk;
+  const int64_t ntiles = (H / G + 31) / 32;
+  DSA_REQUIRE(entries < (1ll << 31) && B * R < (1ll << 31) && entries * ntiles < (1ll << 40),
+              "%s: too many entries for int32 CSR keys", fn);
+  DSA_REQUIRE(R <= 32768, "%s: S_kv * G = %lld exceeds the 32768 rows one LDS histogram holds", fn, (long long)R);
+  DSA_REQUIRE(S_kv * G * D_qk * 2 < (1ll << 32), "%s: kv rows of one batch exceed 4 GiB", fn);
+  const bool f8 = dtype == DSA_DTYPE_E4M3;
+  const bool shape_ok = (D_qk == 128 && D_v == 64) || (D_qk == 128 && D_v == 128) || (D_qk == 192 && D_v == 128) ||
+                        (D_qk == 64 && D_v == 32 && !f8) || wide_shape(D_qk, D_v);
+  if (!shape_ok)
+    return set_error(DSA_ERR_UNSUPPORTED, "%s: no kernel for d_qk=%lld d_v=%lld dtype=%d", fn, (long long)D_qk,
+                     (long long)D_v, dtype);
+  return DSA_OK;
+}
+
+// Main kernel, reduction (and, unless index_ready, the inverse index) of every pass.
+static int bwd_run(const void *q, const void *kv, const void *o, const void *dO, const int32_t *indices,
+                   const float *lse2, const float *delta, void *dq, void *dkv, unsigned char *ws, unsigned char *ix,
+                   bool index_ready, int64_t B, int64_t S, int64_t S_kv, int64_t H, int64_t G, int64_t D_qk,
+                   int64_t D_v, int64_t topk, float sm_scale, int dtype, const float *q_scale, const float *kv_scale,
+                   int flags, const BwdWorkspace &L, hipStream_t st) {
+  const int64_t R = S_kv * G;
   const int64_t hpg = H / G;
   const int ntiles = (int)((hpg + 31) / 32);
-  DSA_REQUIRE(entries < (1ll << 31) && rows < (1ll << 31) && entries * ntiles < (1ll << 40),
-              "dsa_sparse_mla_bwd: too many entries for int32 CSR keys");
-  DSA_REQUIRE(R <= 32768, "dsa_sparse_mla_bwd: S_kv * G = %lld exceeds the 32768 rows one LDS histogram holds",
-              (long long)R);
-  DSA_REQUIRE(S_kv * G * D_qk * 2 < (1ll << 32), "dsa_sparse_mla_bwd: kv rows of one batch exceed 4 GiB");
-  DSA_REQUIRE(q && kv && o && dO && indices && lse2 && dq, "dsa_sparse_mla_bwd: null tensor pointer");
-  if (dtype == DSA_DTYPE_E4M3)
-    DSA_REQUIRE(q_scale && kv_scale, "dsa_sparse_mla_bwd: e4m3 input needs q_scale and kv_scale");
   const bool f8 = dtype == DSA_DTYPE_E4M3;
   const bool wide = wide_shape(D_qk, D_v);
   const bool f32p = (flags & DSA_BWD_FP32_PARTIALS) != 0;
-  const bool shape_ok = (D_qk == 128 && D_v == 64) || (D_qk == 128 && D_v == 128) ||
-                        (D_qk == 192 && D_v == 128) || (D_qk == 64 && D_v == 32 && !f8) || wide;
-  if (!shape_ok)
-    return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_bwd: no kernel for d_qk=%lld d_v=%lld dtype=%d",
-                     (long long)D_qk, (long long)D_v, dtype);
-  const BwdWorkspace L = bwd_layout(B, S, S_kv, H, G, D_qk, topk, flags);
-  if (!workspace || workspace_bytes < L.total)
-    return set_error(DSA_ERR_WORKSPACE, "dsa_sparse_mla_bwd: workspace %zu < required %zu", workspace_bytes,
-                     L.total);
-  unsigned char *ws = static_cast<unsigned char *>(workspace);
-  if (S == 0) {  // no queries: dKV is zero
-    hipLaunchKernelGGL(fill_i32_kernel, dim3(256), dim3(256), 0, st, reinterpret_cast<int32_t *>(dkv),
-                       (rows * D_qk) / 2, 0);
-    return check_launch("sparse_mla_bwd(fill)");
-  }
   const BwdPlan &pl = L.plan;
-  const int64_t npass = pl.npb > 1 ? B * pl.npb : (B + pl.nb - 1) / pl.nb;
-  const size_t qel = dtype == DSA_DTYPE_E4M3 ? 1 : 2;  // bytes per q / kv element
+  const int64_t npass = bwd_passes(pl, B);
+  const size_t qel = f8 ? 1 : 2;  // bytes per q / kv element
   uint16_t *dkv16 = static_cast<uint16_t *>(dkv);
   float *carry = reinterpret_cast<float *>(ws + L.carry);
   stage_begin(st);
@@ -776,24 +803,13 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
     const int mode = pl.npb == 1 ? 0 : (ps % pl.npb == 0 ? 1 : (ps % pl.npb == pl.npb - 1 ? 3 : 2));
     const bool timed = npass == 1;
 
-    CsrParams cp;
-    cp.idx = indices + T0 * G * topk;
-    cp.mask = reinterpret_cast<uint32_t *>(ws + L.mask);
-    cp.base = reinterpret_cast<int32_t *>(ws + L.base);
-    cp.dup = reinterpret_cast<int32_t *>(ws + L.dup);
-    cp.tot = reinterpret_cast<int32_t *>(ws + L.tot);
-    cp.rowptr = reinterpret_cast<int32_t *>(ws + L.rowptr);
-    cp.pos_of = reinterpret_cast<int32_t *>(ws + L.pos_of);
-    cp.S = ctp;
-    cp.S_kv = S_kv;
-    cp.G = G;
-    cp.topk = topk;
-    cp.R = R;
-    cp.NC = csr_chunks(ctp);
-    cp.dup_only = wide ? 0 : 1;  // the narrow main kernel derives the positions of chunks without repeats
-    int rc = launch_csr(cp, nbp, st);
-    if (rc) return rc;
-    if (timed) stage_mark(st);
+    const CsrParams cp = bwd_csr_params(indices, L, ix, T0, ctp, S_kv, G, topk, wide);
+    int rc = DSA_OK;
+    if (!index_ready) {
+      rc = launch_csr(cp, nbp, st);
+      if (rc) return rc;
+    }
+    if (timed) stage_mark(st);  // (a prebuilt index makes this stage empty)
 
     BwdParams p;
     p.q = static_cast<const unsigned char *>(q) + (size_t)T0 * H * D_qk * qel;
@@ -843,4 +859,98 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
   }
   stage_mark(st);  // several passes: one stage for the whole call
   return DSA_OK;
+}
+
+static int bwd_zero_dkv(void *dkv, int64_t rows, int64_t D_qk, hipStream_t st) {
+  hipLaunchKernelGGL(fill_i32_kernel, dim3(256), dim3(256), 0, st, reinterpret_cast<int32_t *>(dkv),
+                     (rows * D_qk) / 2, 0);
+  return check_launch("sparse_mla_bwd(fill)");
+}
+
+extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, const void *dO,
+                                  const int32_t *indices, const float *lse2, const float *delta, void *dq,
+                                  void *dkv, void *workspace, size_t workspace_bytes, int64_t B, int64_t S,
+                                  int64_t S_kv, int64_t H, int64_t G, int64_t D_qk, int64_t D_v, int64_t topk,
+                                  float sm_scale, int dtype, const float *q_scale, const float *kv_scale,
+                                  int flags, void *stream) {
+  int rc = bwd_check("dsa_sparse_mla_bwd", B, S, S_kv, H, G, D_qk, D_v, topk, dtype, flags);
+  if (rc) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (B == 0) return DSA_OK;
+  DSA_REQUIRE(dkv, "dsa_sparse_mla_bwd: null dkv");
+  DSA_REQUIRE(q && kv && o && dO && indices && lse2 && dq, "dsa_sparse_mla_bwd: null tensor pointer");
+  if (dtype == DSA_DTYPE_E4M3)
+    DSA_REQUIRE(q_scale && kv_scale, "dsa_sparse_mla_bwd: e4m3 input needs q_scale and kv_scale");
+  const BwdWorkspace L = bwd_layout(B, S, S_kv, H, G, D_qk, topk, flags);
+  if (!workspace || workspace_bytes < L.total)
+    return set_error(DSA_ERR_WORKSPACE, "dsa_sparse_mla_bwd: workspace %zu < required %zu", workspace_bytes,
+                     L.total);
+  if (S == 0) return bwd_zero_dkv(dkv, B * S_kv * G, D_qk, st);  // no queries: dKV is zero
+  unsigned char *ws = static_cast<unsigned char *>(workspace);
+  return bwd_run(q, kv, o, dO, indices, lse2, delta, dq, dkv, ws, ws + L.rows_total, false, B, S, S_kv, H, G, D_qk,
+                 D_v, topk, sm_scale, dtype, q_scale, kv_scale, flags, L, st);
+}
+
+extern "C" size_t dsa_sparse_mla_bwd_index_size(int64_t B, int64_t S, int64_t S_kv, int64_t H, int64_t G,
+                                                int64_t D_qk, int64_t D_v, int64_t topk, int flags) {
+  (void)D_v;
+  if (B <= 0 || S <= 0 || S_kv <= 0 || H <= 0 || G <= 0 || topk <= 0 || D_qk <= 0) return 0;
+  const BwdWorkspace L = bwd_layout(B, S, S_kv, H, G, D_qk, topk, flags);
+  return bwd_passes(L.plan, B) == 1 ? L.index_total : 0;  // several passes rebuild it per pass
+}
+
+extern "C" size_t dsa_sparse_mla_bwd_indexed_workspace_size(int64_t B, int64_t S, int64_t S_kv, int64_t H,
+                                                            int64_t G, int64_t D_qk, int64_t D_v, int64_t topk,
+                                                            int flags) {
+  (void)D_v;
+  if (B <= 0 || S <= 0 || S_kv <= 0 || H <= 0 || G <= 0 || topk <= 0 || D_qk <= 0) return 0;
+  return bwd_layout(B, S, S_kv, H, G, D_qk, topk, flags).rows_total;
+}
+
+extern "C" int dsa_sparse_mla_bwd_build_index(const int32_t *indices, int64_t B, int64_t S, int64_t S_kv, int64_t H,
+                                              int64_t G, int64_t D_qk, int64_t D_v, int64_t topk, int flags,
+                                              void *index, size_t index_bytes, void *stream) {
+  int rc = bwd_check("dsa_sparse_mla_bwd_build_index", B, S, S_kv, H, G, D_qk, D_v, topk, DSA_DTYPE_BF16, flags);
+  if (rc) return rc;
+  if (B == 0 || S == 0) return DSA_OK;
+  const BwdWorkspace L = bwd_layout(B, S, S_kv, H, G, D_qk, topk, flags);
+  DSA_REQUIRE(bwd_passes(L.plan, B) == 1,
+              "dsa_sparse_mla_bwd_build_index: this backward runs in several passes (no prebuilt index)");
+  DSA_REQUIRE(indices, "dsa_sparse_mla_bwd_build_index: null indices");
+  if (!index || index_bytes < L.index_total)
+    return set_error(DSA_ERR_WORKSPACE, "dsa_sparse_mla_bwd_build_index: index buffer %zu < required %zu",
+                     index_bytes, L.index_total);
+  const CsrParams cp = bwd_csr_params(indices, L, static_cast<unsigned char *>(index), 0, S, S_kv, G, topk,
+                                      wide_shape(D_qk, D_v));
+  return launch_csr(cp, B, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int dsa_sparse_mla_bwd_indexed(const void *q, const void *kv, const void *o, const void *dO,
+                                          const int32_t *indices, const float *lse2, const float *delta, void *dq,
+                                          void *dkv, const void *index, size_t index_bytes, void *workspace,
+                                          size_t workspace_bytes, int64_t B, int64_t S, int64_t S_kv, int64_t H,
+                                          int64_t G, int64_t D_qk, int64_t D_v, int64_t topk, float sm_scale,
+                                          int dtype, const float *q_scale, const float *kv_scale, int flags,
+                                          void *stream) {
+  int rc = bwd_check("dsa_sparse_mla_bwd_indexed", B, S, S_kv, H, G, D_qk, D_v, topk, dtype, flags);
+  if (rc) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (B == 0) return DSA_OK;
+  DSA_REQUIRE(dkv, "dsa_sparse_mla_bwd_indexed: null dkv");
+  DSA_REQUIRE(q && kv && o && dO && indices && lse2 && dq, "dsa_sparse_mla_bwd_indexed: null tensor pointer");
+  if (dtype == DSA_DTYPE_E4M3)
+    DSA_REQUIRE(q_scale && kv_scale, "dsa_sparse_mla_bwd_indexed: e4m3 input needs q_scale and kv_scale");
+  const BwdWorkspace L = bwd_layout(B, S, S_kv, H, G, D_qk, topk, flags);
+  if (S == 0) return bwd_zero_dkv(dkv, B * S_kv * G, D_qk, st);
+  DSA_REQUIRE(bwd_passes(L.plan, B) == 1,
+              "dsa_sparse_mla_bwd_indexed: this backward runs in several passes (use dsa_sparse_mla_bwd)");
+  if (!index || index_bytes < L.index_total)
+    return set_error(DSA_ERR_WORKSPACE, "dsa_sparse_mla_bwd_indexed: index buffer %zu < required %zu", index_bytes,
+                     L.index_total);
+  if (!workspace || workspace_bytes < L.rows_total)
+    return set_error(DSA_ERR_WORKSPACE, "dsa_sparse_mla_bwd_indexed: workspace %zu < required %zu", workspace_bytes,
+                     L.rows_total);
+  return bwd_run(q, kv, o, dO, indices, lse2, delta, dq, dkv, static_cast<unsigned char *>(workspace),
+                 const_cast<unsigned char *>(static_cast<const unsigned char *>(index)), true, B, S, S_kv, H, G, D_qk,
+                 D_v, topk, sm_scale, dtype, q_scale, kv_scale, flags, L, st);
 }

@@ -18,7 +18,7 @@ from .sparse_mla_blockscaled import (
     sparse_mla_blockscaled_mxfp8_forward,
     sparse_mla_blockscaled_mxfp8_fwd_interface,
 )
-from .sparse_mla_bwd import sparse_mla_bwd
+from .sparse_mla_bwd import InverseIndex, build_inverse_index, side_stream, sparse_mla_bwd
 from .sparse_mla_bwd_fp8 import sparse_mla_bwd_fp8
 from .sparse_mla_fwd import sparse_mla_fwd_interface
 from .sparse_mla_fwd_fp8 import fp8_dequantize, per_token_cast_to_fp8, sparse_mla_fwd_fp8_interface, tensorwise_quantize
@@ -35,6 +35,9 @@ __all__ = [
     "sparse_mla_blockscaled_mxfp8_forward",
     "sparse_mla_blockscaled_mxfp8_fwd_interface",
     "sparse_mla_bwd",
+    "InverseIndex",
+    "build_inverse_index",
+    "side_stream",
     "sparse_mla_bwd_fp8",
     "sparse_mla_fp8_as_unfused_dsa",
     "sparse_mla_fwd_fp8_interface",

@@ -23,7 +23,7 @@ import logging
 import torch
 
 from ._common import unwrap_quantized
-from .sparse_mla_bwd import sparse_mla_bwd
+from .sparse_mla_bwd import build_inverse_index, side_stream, sparse_mla_bwd
 from .sparse_mla_bwd_fp8 import sparse_mla_bwd_fp8
 from .sparse_mla_fwd import sparse_mla_fwd_interface
 from .sparse_mla_fwd_fp8 import _enforce_te_tensorwise_quant_backend, per_token_cast_to_fp8, \
@@ -66,6 +66,10 @@ class SparseMLA(torch.autograd.Function):
         ctx.scaling = scaling
         if d_v is None:
             d_v = q.shape[-1]
+        # the backward's inverse index depends on the indices alone: build it on a
+        # second stream while the forward kernel runs
+        ctx.inverse_index = (build_inverse_index(q, kv, indices, d_v, stream=side_stream(q.device))
+                             if ctx.needs_input_grad[0] or ctx.needs_input_grad[1] else None)
         out, lse = sparse_mla_fwd_interface(q, kv, indices, sm_scale=scaling, d_v=d_v)
         ctx.d_v = d_v
         ctx.save_for_backward(q, kv, indices, out, lse)
@@ -74,7 +78,9 @@ class SparseMLA(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_output, grad_lse):
         q, kv, indices, out, lse = ctx.saved_tensors
-        dq, dkv = sparse_mla_bwd(q, kv, out, grad_output.contiguous(), indices, lse, sm_scale=ctx.scaling)
+        dq, dkv = sparse_mla_bwd(q, kv, out, grad_output.contiguous(), indices, lse, sm_scale=ctx.scaling,
+                                 inverse_index=ctx.inverse_index)
+        ctx.inverse_index = None
         return dq, dkv, None, None, None
 
 
@@ -124,6 +130,8 @@ class SparseMLA_FP8(torch.autograd.Function):
             k8 = k8_flat.reshape(kv.shape)
             kv_scale = ks_flat.reshape(kv.shape[:-2])
 
+        ctx.inverse_index = (build_inverse_index(q8, k8, indices, d_v, stream=side_stream(q8.device))
+                             if ctx.needs_input_grad[0] or ctx.needs_input_grad[1] else None)
         out, lse = sparse_mla_fwd_fp8_interface(q8, k8, indices, q_scale=q_scale, kv_scale=kv_scale,
                                                 sm_scale=scaling, d_v=d_v)
         ctx.d_v = d_v
@@ -134,7 +142,8 @@ class SparseMLA_FP8(torch.autograd.Function):
     def backward(ctx, grad_output, grad_lse):
         q8, k8, q_scale, kv_scale, indices, out, lse = ctx.saved_tensors
         dq, dkv = sparse_mla_bwd_fp8(q8, k8, q_scale, kv_scale, out, grad_output.contiguous(), indices, lse,
-                                     sm_scale=ctx.scaling)
+                                     sm_scale=ctx.scaling, inverse_index=ctx.inverse_index)
+        ctx.inverse_index = None
         return dq, dkv, None, None, None
 
 

@@ -27,21 +27,105 @@ def fp32_partials_default() -> bool:
     return os.getenv("CPPMEGA_AMD_BWD_FP32_PARTIALS", "0").strip().lower() in {"1", "true", "yes", "on"}
 
 
+class InverseIndex:
+    """The backward's inverse index (kv row -> entries in order), built from the
+    indices alone by ``build_inverse_index`` ahead of the backward -- e.g. on a
+    second stream while the forward runs -- and consumed by ``sparse_mla_bwd``
+    / ``sparse_mla_bwd_fp8`` (``inverse_index=``), which then run only the main
+    kernel and the dKV reduction.  Holds the index buffer, the event that ends
+    its build (None when built on the caller's stream) and the call shape it
+    was built for; the indices must not change in between."""
+
+    __slots__ = ("buf", "event", "key")
+
+    def __init__(self, buf, event, key):
+        self.buf, self.event, self.key = buf, event, key
+
+
+_SIDE_STREAMS: dict = {}
+
+
+def side_stream(device) -> torch.cuda.Stream:
+    """A second stream of ``device`` (default priority) for work that overlaps the
+    current stream, e.g. ``build_inverse_index`` during the forward."""
+    idx = torch.device(device).index
+    idx = torch.cuda.current_device() if idx is None else idx
+    s = _SIDE_STREAMS.get(idx)
+    if s is None:
+        s = _SIDE_STREAMS[idx] = torch.cuda.Stream(device=idx)
+    return s
+
+
+def _bwd_flags(fp32_partials):
+    if fp32_partials is None:
+        fp32_partials = fp32_partials_default()
+    return _lib.BWD_FP32_PARTIALS if fp32_partials else 0
+
+
+def build_inverse_index(q, kv, indices, d_v, *, fp32_partials=None, stream=None):
+    """Build the backward's inverse index for q [B,S,H,D] (or 3-D), kv
+    [B,S_kv,G,D] and indices [B,S,G,topk] int32; returns an ``InverseIndex``,
+    or None when the backward runs in several passes (it then builds its index
+    per pass).  With ``stream`` (e.g. ``side_stream(q.device)``) the build runs
+    there after the work already queued on the current stream, and the
+    backward waits for it through an event."""
+    if q.ndim == 3:
+        q, kv, indices = q.unsqueeze(0), kv.unsqueeze(0), indices.unsqueeze(0)
+    assert indices.is_contiguous() and indices.dtype == torch.int32
+    B, S, H, D = q.shape
+    _, S_kv, G, _ = kv.shape
+    topk = indices.shape[-1]
+    flags = _bwd_flags(fp32_partials)
+    L = _lib.load()
+    n = int(L.dsa_sparse_mla_bwd_index_size(B, S, S_kv, H, G, D, int(d_v), topk, flags))
+    if n == 0:
+        return None
+    cur = torch.cuda.current_stream(q.device)
+    side = stream if stream is not None else cur
+    buf = torch.empty(n, dtype=torch.uint8, device=q.device)
+    if side != cur:
+        side.wait_stream(cur)
+    rc = L.dsa_sparse_mla_bwd_build_index(indices.data_ptr(), B, S, S_kv, H, G, D, int(d_v), topk, flags,
+                                          buf.data_ptr(), n, side.cuda_stream)
+    _lib.check(rc, "dsa_sparse_mla_bwd_build_index")
+    event = None
+    if side != cur:
+        if not torch.cuda.is_current_stream_capturing():  # a capture keeps its pool alive itself
+            buf.record_stream(side)
+            indices.record_stream(side)
+        event = torch.cuda.Event()
+        event.record(side)
+    return InverseIndex(buf, event, (B, S, S_kv, H, G, D, int(d_v), topk, flags, indices.data_ptr()))
+
+
 def _launch_bwd(q, kv, o, do, indices, lse, delta, sm_scale, dtype_code, q_scale=None, kv_scale=None,
-                fp32_partials=None):
+                fp32_partials=None, inverse_index=None):
     B, S, H, D = q.shape
     _, S_kv, G, _ = kv.shape
     d_v = o.shape[-1]
     topk = indices.shape[-1]
-    if fp32_partials is None:
-        fp32_partials = fp32_partials_default()
-    flags = _lib.BWD_FP32_PARTIALS if fp32_partials else 0
+    flags = _bwd_flags(fp32_partials)
     L = _lib.load()
-    ws_bytes = int(L.dsa_sparse_mla_bwd_workspace_size(B, S, S_kv, H, G, D, d_v, topk, flags))
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     dq = torch.empty((B, S, H, D), dtype=torch.bfloat16, device=q.device)
     dkv = torch.empty((B, S_kv, G, D), dtype=torch.bfloat16, device=q.device)
     _, stream = stream_of(q)
+    if inverse_index is not None:
+        key = (B, S, S_kv, H, G, D, d_v, topk, flags, indices.data_ptr())
+        assert inverse_index.key == key, "inverse_index was built for another call"
+        if inverse_index.event is not None:
+            torch.cuda.current_stream(q.device).wait_event(inverse_index.event)
+        ws_bytes = int(L.dsa_sparse_mla_bwd_indexed_workspace_size(B, S, S_kv, H, G, D, d_v, topk, flags))
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+        ix = inverse_index.buf
+        rc = L.dsa_sparse_mla_bwd_indexed(
+            q.data_ptr(), kv.data_ptr(), o.data_ptr(), do.data_ptr(), indices.data_ptr(),
+            lse.data_ptr(), _lib.ptr(delta), dq.data_ptr(), dkv.data_ptr(), ix.data_ptr(), ix.numel(),
+            ws.data_ptr(), ws_bytes, B, S, S_kv, H, G, D, d_v, topk, float(sm_scale), dtype_code,
+            _lib.ptr(q_scale), _lib.ptr(kv_scale), flags, stream)
+        _lib.check(rc, "dsa_sparse_mla_bwd_indexed")
+        return dq, dkv
+    ws_bytes = int(L.dsa_sparse_mla_bwd_workspace_size(B, S, S_kv, H, G, D, d_v, topk, flags))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     rc = L.dsa_sparse_mla_bwd(
         q.data_ptr(), kv.data_ptr(), o.data_ptr(), do.data_ptr(), indices.data_ptr(),
         lse.data_ptr(), _lib.ptr(delta), dq.data_ptr(), dkv.data_ptr(), ws.data_ptr(), ws_bytes,
@@ -61,13 +145,15 @@ def _prep_delta(delta, B, S, H):
 
 
 def sparse_mla_bwd(q, kv, o, do, indices, lse, sm_scale=None, d_v=None, is_casual=True,
-                   return_kernel=False, delta=None, *, fp32_partials=None):
+                   return_kernel=False, delta=None, *, fp32_partials=None, inverse_index=None):
     """Run the sparse-MLA backward and return (dq, dkv), both bf16.
 
     Accepts 3-D [seq, heads, dim] or 4-D [batch, seq, heads, dim] tensors;
     ``lse`` is the forward's log2-unit LSE.  grad of lse is not an input (the
     reference ignores it too).  ``fp32_partials`` (keyword only; default from
     CPPMEGA_AMD_BWD_FP32_PARTIALS) keeps the dKV contribution rows in fp32.
+    ``inverse_index`` (keyword only): an ``InverseIndex`` from
+    ``build_inverse_index`` for these indices, built ahead of the call.
     """
     q = unwrap_quantized(q)
     kv = unwrap_quantized(kv)
@@ -104,7 +190,7 @@ def sparse_mla_bwd(q, kv, o, do, indices, lse, sm_scale=None, d_v=None, is_casua
 
     scale = normalize_sm_scale(sm_scale, dim_plus_tail_dim)
     dq, dkv = _launch_bwd(q, kv, o, do, indices, lse, delta, scale, _lib.DTYPE_BF16,
-                          fp32_partials=fp32_partials)
+                          fp32_partials=fp32_partials, inverse_index=inverse_index)
     if squeeze_batch:
         dq, dkv = dq.squeeze(0), dkv.squeeze(0)
     return dq, dkv

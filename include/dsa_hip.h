@@ -159,6 +159,43 @@ int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o,
                        int flags, void *stream);
 
 /*
+ * The backward's inverse index (kv row -> entries) depends on the indices
+ * alone, so a caller may build it ahead of the backward, e.g. on a second
+ * stream while the forward runs, and pass it to dsa_sparse_mla_bwd_indexed,
+ * which then runs only the main kernel and the dKV reduction (same results,
+ * bit for bit, as dsa_sparse_mla_bwd).  Available when the backward runs in one
+ * pass: dsa_sparse_mla_bwd_index_size returns 0 otherwise (then use
+ * dsa_sparse_mla_bwd).  The index buffer must stay untouched between the two
+ * calls and the build must be ordered before the backward (same stream, or an
+ * event).  dsa_sparse_mla_bwd_indexed_workspace_size is the partial-row
+ * workspace it needs besides the index.  No counterpart in the reference
+ * (its backward has no inverse index).
+ */
+size_t dsa_sparse_mla_bwd_index_size(int64_t B, int64_t S, int64_t S_kv,
+                                     int64_t H, int64_t G, int64_t D_qk,
+                                     int64_t D_v, int64_t topk, int flags);
+size_t dsa_sparse_mla_bwd_indexed_workspace_size(int64_t B, int64_t S,
+                                                 int64_t S_kv, int64_t H,
+                                                 int64_t G, int64_t D_qk,
+                                                 int64_t D_v, int64_t topk,
+                                                 int flags);
+int dsa_sparse_mla_bwd_build_index(const int32_t *indices, int64_t B, int64_t S,
+                                   int64_t S_kv, int64_t H, int64_t G,
+                                   int64_t D_qk, int64_t D_v, int64_t topk,
+                                   int flags, void *index, size_t index_bytes,
+                                   void *stream);
+int dsa_sparse_mla_bwd_indexed(const void *q, const void *kv, const void *o,
+                               const void *dO, const int32_t *indices,
+                               const float *lse2, const float *delta, void *dq,
+                               void *dkv, const void *index, size_t index_bytes,
+                               void *workspace, size_t workspace_bytes,
+                               int64_t B, int64_t S, int64_t S_kv, int64_t H,
+                               int64_t G, int64_t D_qk, int64_t D_v,
+                               int64_t topk, float sm_scale, int dtype,
+                               const float *q_scale, const float *kv_scale,
+                               int flags, void *stream);
+
+/*
  * DSA indexer scores: score[b, t, s] = sum_h w[t, b, h] * act(q[t, b, h, :] . k[s, b, :])
  * with act = ReLU when use_relu != 0, identity otherwise; fp32 accumulate.
  * Replaces Megatron `_compute_index_scores` as patched by
