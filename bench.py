@@ -19,7 +19,9 @@ for the single kernel with the longest median duration; its `traffic` field is
 read from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed under
 profiles/ (null when that kernel has no such summary).
 
-After the timed steps the FP8-tensorwise SparseMLA forward and backward at the
+After the timed steps the same step chained (SparseMLA fed the top-k's own
+indices) is timed as HIP-graph replays and reported under "chained_step".
+Then the FP8-tensorwise SparseMLA forward and backward at the
 cfg2 shapes (cfg4: e4m3 q / kv with 1% x20 outliers) are timed and reported
 under "cfg4" against the mixed fp8 + bf16 MFMA floor (--no-cfg4 skips them).
 Then the cfg5 long-context kernels (SparseMLA forward and backward at
@@ -605,6 +607,19 @@ def main():
     t_att = kernels["fwd"]["ms"] + kernels["bwd"]["ms"]
     amortised = 9 * tokens / ((3 * t_idx + 9 * t_att) / 1e3)
 
+    def chained_step():
+        # the same layer step with SparseMLA consuming the top-k's own indices
+        sc = index_scores(iq, iw, ik, use_relu=True, causal=CAUSAL_LOWER)
+        sel_c = topk_indices(sc, TOPK, causal=True).view(B, S, 1, TOPK)
+        inv_c = build_inverse_index(q, kv, sel_c, D_V, stream=side)
+        out_c, lse_c = sparse_mla_fwd_interface(q, kv, sel_c, sm_scale=scale, d_v=D_V)
+        return sparse_mla_bwd(q, kv, out_c, do, sel_c, lse_c, sm_scale=scale, inverse_index=inv_c)
+
+    t_chain = graph_replay_time(chained_step)
+    chained = {"tokens_per_s": round(tokens / t_chain, 1), "ms_per_step": round(t_chain * 1e3, 4),
+               "note": "HIP-graph replays of the step with SparseMLA fed the top-256 the indexer just chose "
+                       "(cfg3 scores) instead of cfg2's uniform indices; same work per token"}
+
     from cppmega_amd.dsa_topk import indexer_topk_streaming
     t_stream = graph_replay_time(lambda: indexer_topk_streaming(iq, ik, iw, TOPK, max_scratch_bytes=16 << 20))
     streaming = {"ms": round(t_stream * 1e3, 4), "scratch_mib": 16,
@@ -644,6 +659,7 @@ def main():
         "kernels": kernels,
         "indexcache_amortised_tokens_per_s": round(amortised, 1),
         "indexer_topk_streaming": streaming,
+        "chained_step": chained,
         "launch": ("hip_graph" if graph_info is not None else "eager"),
         "eager_tokens_per_s": round(eager_tokens_per_s, 1),
         "graph_replays_checked": (graph_info["checked"] if graph_info is not None else 0),
