@@ -288,13 +288,15 @@ __global__ void __launch_bounds__(THREADS) topk_select_kernel(const TopkParams p
 // ---------------------------------------------------------------------------
 // Wave-per-row variant for rows of at most 64 * IPL columns (no block barriers).
 // ---------------------------------------------------------------------------
-// Lane l holds columns 256c + 4l + j (c < IPL/4, j < 4) as order-preserving
-// keys: every load instruction reads 1 KiB contiguously.  The undecided
-// elements are always the keys in an interval [A, B], so no masks are kept.
-//  * Round 0 buckets the finite scores linearly in value over [min, max]
-//    (1024 LDS bins); +inf / NaN and -inf are counted apart.  Real score rows
-//    spread evenly this way, so the bucket holding the k-th largest usually has
-//    a handful of members.
+// Lane l holds columns 64i + l (i < IPL) as normalised scores: every load
+// instruction reads 256 B contiguously.  The undecided elements are always the
+// scores in an interval [A, B], so no masks are kept.
+//  * Round 0 finds the maximum and a lower bound L of the k-th largest score
+//    (the least of 4 interleaved per-lane subset maxima), then buckets the
+//    finite scores >= L linearly in value over [L, max] (1024 LDS bins).  Real
+//    score rows spread evenly this way, so the bucket holding the k-th largest
+//    usually has a handful of members, and only the scores >= L (the upper
+//    tail) take part in the LDS atomics.
 //  * Further rounds, if more than 64 members remain, histogram the 10 key bits
 //    below the highest bit in which the members' min and max keys differ (the
 //    span shrinks by 2^10 per round, so they end).
@@ -310,6 +312,8 @@ template <int CTRL, int ROW_MASK = 0xf, bool BOUND_ZERO = false>
 __device__ __forceinline__ uint32_t dpp(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, BOUND_ZERO);
 }
+// lanes whose predicate holds (the compare result itself, no 0/1 round trip)
+__device__ __forceinline__ uint64_t ballot(bool b) { return __builtin_amdgcn_ballot_w64(b); }
 __device__ __forceinline__ uint32_t readlane(uint32_t v, int l) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
 }
@@ -357,9 +361,18 @@ constexpr int kWaveBins = 1024;
 constexpr int kNoLimit = 0x7fffffff;
 constexpr int kGroup = 16;  // items per group: passes skip whole groups past the window
 
-// Score normalised for ranking: NaN -> +inf, -0 -> +0 (x + 0 is +0 for x = -0).
-// Float comparisons of normalised scores order them exactly as the keys do.
-__device__ __forceinline__ float rank_value(float f) { return (f != f ? INFINITY : f) + 0.0f; }
+// Score normalised for ranking: NaN -> +inf.  -0 stays: every float
+// comparison (and the linear buckets) treats it as +0, and score_key maps it
+// to the key of +0, so normalised scores order exactly as the keys do.
+__device__ __forceinline__ float rank_value(float f) { return f != f ? INFINITY : f; }
+
+// Linear bucket of x >= L (see the round-0 comment in topk_wave_kernel):
+// fma(x, scale, cbin) lies in [1.5 * 2^23, 1.5 * 2^23 + 1024), so its bit
+// pattern less kBinBits is the bin.
+constexpr uint32_t kBinBits = 0x4B400000u;
+__device__ __forceinline__ uint32_t lin_bits(float x, float scale, float cbin) {
+  return __float_as_uint(fmaf(x, scale, cbin));
+}
 
 // Make the compiler treat the row values as freshly defined, so predicates of
 // one pass are recomputed in the next instead of being kept alive as 64-bit
@@ -401,7 +414,7 @@ __device__ __forceinline__ void find_bucket(const int *hist, int r, int &bsel, i
       acc += cnt[q];
     }
   }
-  const int cl = __ffsll((unsigned long long)__ballot(cross)) - 1;  // exactly one lane crosses
+  const int cl = __ffsll((unsigned long long)wv::ballot(cross)) - 1;  // exactly one lane crosses
   bsel = (int)wv::readlane((uint32_t)bsel_l, cl < 0 ? 0 : cl);
   above = (int)wv::readlane((uint32_t)above_l, cl < 0 ? 0 : cl);
 }
@@ -417,7 +430,7 @@ __device__ __forceinline__ void rank_list(float v, int mm, int r, float &K, int 
     e += vj == v ? 1 : 0;
   }
   const bool found = lane < mm && g < r && r <= g + e;
-  const int fl = __ffsll((unsigned long long)__ballot(found)) - 1;
+  const int fl = __ffsll((unsigned long long)wv::ballot(found)) - 1;
   const int src = fl < 0 ? 0 : fl;
   K = __uint_as_float(wv::readlane(__float_as_uint(v), src));
   const int gk = (int)wv::readlane((uint32_t)g, src);
@@ -465,7 +478,6 @@ topk_wave_kernel(const TopkParams p) {
   const float *src = p.scores + row * p.row_stride + st;
   const __amdgpu_buffer_rsrc_t rsrc = make_buffer_rsrc(src, (uint32_t)n * 4u);
   int ng = (n + 64 * kGroup - 1) / (64 * kGroup);  // groups holding window columns
-  const int npad = 64 * kGroup * ng - n;          // padded elements in those groups
   const float kPad = __uint_as_float(0x7fc00000u);
   // groups wholly past the window (half of a causal matrix) issue no loads
   float x[IPL];
@@ -480,7 +492,19 @@ topk_wave_kernel(const TopkParams p) {
     }
   }
 #pragma unroll
-  for (int i = 0; i < IPL; ++i) x[i] = (64 * i + lane < n) ? rank_value(x[i]) : kPad;
+  for (int q = 0; q < BPL; ++q) hist[lane * BPL + q] = 0;
+  // only the last loaded group reaches past the window
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    if (g < ng) {
+      const bool last = g == ng - 1;
+#pragma unroll
+      for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
+        x[i] = rank_value(x[i]);
+        if (last) x[i] = (64 * i + lane < n) ? x[i] : kPad;
+      }
+    }
+  }
 
   int r = p.topk;  // elements still to take
   float K = 0.0f;  // result: take x > K and the first c_eq (column order) of x == K
@@ -489,65 +513,98 @@ topk_wave_kernel(const TopkParams p) {
   float vA, vB;    // member interval for the key rounds
   int m = n;
 
-  // ---- round 0: min / max (IEEE min / max skip the NaN pads) ----
+  // ---- round 0: maximum and a lower bound L of the r-th largest score ----
+  // Item i of each lane feeds the running maximum of subset i % kSub.  The
+  // 64 * kSub subset maxima are distinct elements, so when r <= 64 * kSub at
+  // least r scores are >= L = their minimum: scores below L are never taken
+  // and stay out of every later pass (IEEE min / max skip the NaN pads, which
+  // also fail every x >= L test).  A subset without scores makes L = -inf;
+  // then, or for larger r, L is the row minimum.
+  constexpr int kSub = 4;
   fence_values(x, ng);
-  float lo = INFINITY, hi = -INFINITY;
+  float smax[kSub];
+#pragma unroll
+  for (int j = 0; j < kSub; ++j) smax[j] = -INFINITY;
 #pragma unroll
   for (int g = 0; g < NG; ++g) {
     if (g < ng) {
 #pragma unroll
-      for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
-        lo = fminf(lo, x[i]);
-        hi = fmaxf(hi, x[i]);
-      }
+      for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) smax[i % kSub] = fmaxf(smax[i % kSub], x[i]);
     }
   }
-  lo = __uint_as_float(wv::wave_reduce(__float_as_uint(lo), wv::MinF()));
+  float L = smax[0], hi = smax[0];
+#pragma unroll
+  for (int j = 1; j < kSub; ++j) {
+    L = fminf(L, smax[j]);
+    hi = fmaxf(hi, smax[j]);
+  }
+  L = __uint_as_float(wv::wave_reduce(__float_as_uint(L), wv::MinF()));
   hi = __uint_as_float(wv::wave_reduce(__float_as_uint(hi), wv::MaxF()));
-  vA = lo;
+  if (r > 64 * kSub || L == -INFINITY) {
+    fence_values(x, ng);
+    float lo = INFINITY;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if (g < ng) {
+#pragma unroll
+        for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) lo = fminf(lo, x[i]);
+      }
+    }
+    L = __uint_as_float(wv::wave_reduce(__float_as_uint(lo), wv::MinF()));
+  }
+  vA = L;
   vB = hi;
-  if (lo == hi) {
-    K = lo;
+  if (L == hi) {  // the r largest all equal the maximum
+    K = hi;
     c_eq = r;
     decided = true;
-  } else if (__builtin_isfinite(lo) && __builtin_isfinite(hi)) {
-    // value-linear buckets; |x| * scale < 2^20 keeps fma rounding far below a bin
-    const float scale = 1023.5f / (hi - lo);
-    const float bias = -lo * scale;
-    if (isfinite(scale) && fmaxf(fabsf(lo), fabsf(hi)) * scale < 1048576.0f) {
-#pragma unroll
-      for (int q = 0; q < BPL; ++q) hist[lane * BPL + q] = 0;
-      wave_lds_sync();
+  } else if (__builtin_isfinite(L) && __builtin_isfinite(hi)) {
+    // Value-linear buckets over [L, hi]: the bin of x >= L is the integer that
+    // fma(x, scale, cbin) rounds to in the binade [2^23, 2^24) (unit spacing),
+    // less 1.5 * 2^23, i.e. round((x - L) * scale + 1 + d) with |d| <= 0.5625
+    // (0.5 from rounding cbin, 1/16 from rounding -L * scale while
+    // |x| * scale < 2^20), so bins run over [0, 1023] and rise with x.
+    const float scale = 1021.0f / (hi - L);
+    const float cbin = -L * scale + 12582913.0f;   // 1.5 * 2^23 + 1
+    if (isfinite(scale) && fmaxf(fabsf(L), fabsf(hi)) * scale < 1048576.0f) {
+      wave_lds_sync();  // the zeroed histogram (cleared while the row loaded)
       fence_values(x, ng);
+      // bins addressed from the raw fma bits: one shift-add per element
+      int *const hist_b = hist - kBinBits;
+      int one = 1;
+      asm volatile("" : "+v"(one));
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
         if (g < ng) {
 #pragma unroll
           for (int i = g * kGroup; i < (g + 1) * kGroup; ++i)
-            atomicAdd(&hist[(int)fmaf(x[i], scale, bias)], 1);  // NaN pads convert to bin 0
+            if (x[i] >= L) atomicAdd(&hist_b[lin_bits(x[i], scale, cbin)], one);
         }
       }
-      wave_lds_sync();
-      if (lane == 0) hist[0] -= npad;
       wave_lds_sync();
       int bsel, above;
       find_bucket(hist, r, bsel, above);
       m = hist[bsel];
       r -= above;
+      const uint32_t bsel_bits = kBinBits + (uint32_t)bsel;
       wave_lds_sync();  // histogram reads finish before it is reused
       fence_values(x, ng);
       if (m <= 64) {
-        // the bucket's members to LDS (any order), then an exact rank
+        // the bucket's members to LDS (any order), then an exact rank; most
+        // items hold no member in any lane and skip the placement
         int base = 0;
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
           if (g < ng) {
 #pragma unroll
             for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
-              const bool mem = x[i] == x[i] && (int)fmaf(x[i], scale, bias) == bsel;
-              const uint64_t bm = __ballot(mem);
-              if (mem) list[base + lane_rank(bm)] = x[i];
-              base += __popcll(bm);
+              // two ballots of plain compares, combined on the scalar unit
+              const uint64_t bm =
+                  wv::ballot(x[i] >= L) & wv::ballot(lin_bits(x[i], scale, cbin) == bsel_bits);
+              if (bm) {
+                if ((bm >> lane) & 1u) list[base + lane_rank(bm)] = x[i];
+                base += __popcll(bm);
+              }
             }
           }
         }
@@ -562,7 +619,7 @@ topk_wave_kernel(const TopkParams p) {
           if (g < ng) {
 #pragma unroll
             for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
-              const bool mem = x[i] == x[i] && (int)fmaf(x[i], scale, bias) == bsel;
+              const bool mem = x[i] >= L && lin_bits(x[i], scale, cbin) == bsel_bits;
               mlo = mem ? fminf(mlo, x[i]) : mlo;
               mhi = mem ? fmaxf(mhi, x[i]) : mhi;
             }
@@ -640,7 +697,7 @@ topk_wave_kernel(const TopkParams p) {
 #pragma unroll
           for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
             const bool mem = x[i] >= vA && x[i] <= vB;
-            const uint64_t bm = __ballot(mem);
+            const uint64_t bm = wv::ballot(mem);
             if (mem) list[base + lane_rank(bm)] = x[i];
             base += __popcll(bm);
           }
@@ -654,6 +711,11 @@ topk_wave_kernel(const TopkParams p) {
   }
 
   // ---- output in column order: x > K, and the first c_eq of x == K ----
+  // Stores go through a resource of exactly topk entries; lanes that take
+  // nothing (and any position past topk) store past it and are dropped, so
+  // the pass runs without branches.
+  const __amdgpu_buffer_rsrc_t orsrc = make_buffer_rsrc(orow, (uint32_t)p.topk * 4u);
+  constexpr int kDrop = 0x7ffffffc;
   fence_values(x, ng);
   int pos = 0;
   if (c_eq == kNoLimit) {
@@ -663,9 +725,9 @@ topk_wave_kernel(const TopkParams p) {
 #pragma unroll
         for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
           const bool t = x[i] >= K;
-          const uint64_t tm = __ballot(t);
+          const uint64_t tm = wv::ballot(t);
           const int at = pos + lane_rank(tm);
-          if (t && at < p.topk) orow[at] = (int32_t)(st + 64 * i + lane);  // exactly topk; guard
+          __builtin_amdgcn_raw_buffer_store_b32((uint32_t)(st + 64 * i + lane), orsrc, t ? 4 * at : kDrop, 0, 0);
           pos += __popcll(tm);
         }
       }
@@ -678,11 +740,11 @@ topk_wave_kernel(const TopkParams p) {
 #pragma unroll
         for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
           const bool eqv = x[i] == K;
-          const uint64_t em = __ballot(eqv);
+          const uint64_t em = wv::ballot(eqv);
           const bool t = x[i] > K || (eqv && eq_before + lane_rank(em) < c_eq);
-          const uint64_t tm = __ballot(t);
+          const uint64_t tm = wv::ballot(t);
           const int at = pos + lane_rank(tm);
-          if (t && at < p.topk) orow[at] = (int32_t)(st + 64 * i + lane);
+          __builtin_amdgcn_raw_buffer_store_b32((uint32_t)(st + 64 * i + lane), orsrc, t ? 4 * at : kDrop, 0, 0);
           pos += __popcll(tm);
           eq_before += __popcll(em);
         }
