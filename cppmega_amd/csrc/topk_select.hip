@@ -292,8 +292,9 @@ __global__ void __launch_bounds__(THREADS) topk_select_kernel(const TopkParams p
 // instruction reads 256 B contiguously.  The undecided elements are always the
 // scores in an interval [A, B], so no masks are kept.
 //  * Round 0 finds the maximum and a lower bound L of the k-th largest score
-//    (the least of 4 interleaved per-lane subset maxima), then buckets the
-//    finite scores >= L linearly in value over [L, max] (1024 LDS bins).  Real
+//    (the least of 4 interleaved per-lane subset maxima, see subset_bound),
+//    then buckets the finite scores >= L linearly in value over [L, max]
+//    (1024 LDS bins).  Real
 //    score rows spread evenly this way, so the bucket holding the k-th largest
 //    usually has a handful of members, and only the scores >= L (the upper
 //    tail) take part in the LDS atomics.
@@ -374,6 +375,28 @@ __device__ __forceinline__ uint32_t lin_bits(float x, float scale, float cbin) {
   return __float_as_uint(fmaf(x, scale, cbin));
 }
 
+// Lower bound of the r-th largest score.  Item i of each lane feeds the
+// running maximum of subset i % KSUB (sm).  Subsets are disjoint, so if c of
+// them hold a score above -inf (pads past the window and -inf scores hold
+// none), at least c scores are >= the least of their maxima, which bounds the
+// r-th largest from below whenever c >= r.  Returns the wave's least non-empty
+// subset maximum and its count of non-empty subsets; also the wave maximum.
+template <int KSUB>
+__device__ __forceinline__ float subset_bound(const float (&sm)[KSUB], int &count, float &hi) {
+  float L = INFINITY, h = -INFINITY;
+  int c = 0;
+#pragma unroll
+  for (int j = 0; j < KSUB; ++j) {
+    const bool has = sm[j] > -INFINITY;
+    L = has ? fminf(L, sm[j]) : L;
+    h = fmaxf(h, sm[j]);
+    c += __popcll(wv::ballot(has));
+  }
+  count = c;
+  hi = __uint_as_float(wv::wave_reduce(__float_as_uint(h), wv::MaxF()));
+  return __uint_as_float(wv::wave_reduce(__float_as_uint(L), wv::MinF()));
+}
+
 // Make the compiler treat the row values as freshly defined, so predicates of
 // one pass are recomputed in the next instead of being kept alive as 64-bit
 // lane masks across the whole kernel (which exhausts the scalar registers).
@@ -390,14 +413,15 @@ __device__ __forceinline__ int lane_rank(uint64_t mask) {  // set lanes below th
 
 // Suffix scan of a wave's 1024-bin histogram: the bin holding the r-th largest
 // element and the count above it.
+template <int NBINS = kWaveBins>
 __device__ __forceinline__ void find_bucket(const int *hist, int r, int &bsel, int &above) {
-  constexpr int BPL = kWaveBins / 64;
+  constexpr int BPL = NBINS / 64;
   const int lane = lane_id();
   int cnt[BPL];
   uint32_t local = 0u;
 #pragma unroll
   for (int q = 0; q < BPL; ++q) {
-    cnt[q] = hist[kWaveBins - 1 - (lane * BPL + q)];
+    cnt[q] = hist[NBINS - 1 - (lane * BPL + q)];
     local += (uint32_t)cnt[q];
   }
   const int excl = (int)(wv::wave_incl_scan(local) - local);
@@ -408,7 +432,7 @@ __device__ __forceinline__ void find_bucket(const int *hist, int r, int &bsel, i
 #pragma unroll
     for (int q = 0; q < BPL; ++q) {
       if (acc < r && acc + cnt[q] >= r) {
-        bsel_l = kWaveBins - 1 - (lane * BPL + q);
+        bsel_l = NBINS - 1 - (lane * BPL + q);
         above_l = acc;
       }
       acc += cnt[q];
@@ -514,12 +538,10 @@ topk_wave_kernel(const TopkParams p) {
   int m = n;
 
   // ---- round 0: maximum and a lower bound L of the r-th largest score ----
-  // Item i of each lane feeds the running maximum of subset i % kSub.  The
-  // 64 * kSub subset maxima are distinct elements, so when r <= 64 * kSub at
-  // least r scores are >= L = their minimum: scores below L are never taken
-  // and stay out of every later pass (IEEE min / max skip the NaN pads, which
-  // also fail every x >= L test).  A subset without scores makes L = -inf;
-  // then, or for larger r, L is the row minimum.
+  // L from 4 interleaved subset maxima per lane (subset_bound): scores below L
+  // are never taken and stay out of every later pass (IEEE min / max skip the
+  // NaN pads, which also fail every x >= L test).  With fewer than r non-empty
+  // subsets, L is the row minimum.
   constexpr int kSub = 4;
   fence_values(x, ng);
   float smax[kSub];
@@ -532,15 +554,10 @@ topk_wave_kernel(const TopkParams p) {
       for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) smax[i % kSub] = fmaxf(smax[i % kSub], x[i]);
     }
   }
-  float L = smax[0], hi = smax[0];
-#pragma unroll
-  for (int j = 1; j < kSub; ++j) {
-    L = fminf(L, smax[j]);
-    hi = fmaxf(hi, smax[j]);
-  }
-  L = __uint_as_float(wv::wave_reduce(__float_as_uint(L), wv::MinF()));
-  hi = __uint_as_float(wv::wave_reduce(__float_as_uint(hi), wv::MaxF()));
-  if (r > 64 * kSub || L == -INFINITY) {
+  int nsub;
+  float hi;
+  float L = subset_bound(smax, nsub, hi);
+  if (r > nsub) {
     fence_values(x, ng);
     float lo = INFINITY;
 #pragma unroll
@@ -753,6 +770,396 @@ topk_wave_kernel(const TopkParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Workgroup-per-row variant for rows of up to NW * 64 * IPL columns: the wave
+// kernel's passes with NW waves per row.  Wave w holds the contiguous segment
+// of 64 * IPL columns from w * 64 * IPL (lane l: columns w * 64 * IPL + 64i + l),
+// the histogram (2048 bins) is shared in LDS, and minima, maxima, counts and
+// the output positions are combined across the waves through LDS.  Every wave
+// scans the shared histogram itself, so all of them reach the same bucket
+// without a broadcast.  The lower bound L comes from 8 interleaved subset
+// maxima per lane (subset_bound), counted over the whole workgroup.
+// ---------------------------------------------------------------------------
+constexpr int kBlockBins = 2048;
+
+template <int NW>
+struct BlockLds {
+  int hist[kBlockBins];
+  float list[NW][64];   // bucket members, one region per wave
+  float redf[2 * NW];
+  int redi[2 * NW];
+};
+
+// Block-wide (min, max) of one wave-uniform pair; the leading barrier lets the
+// previous readers of the exchange slots finish.
+template <int NW>
+__device__ __forceinline__ void block_minmax_f(float &lo, float &hi, BlockLds<NW> &sm, int w) {
+  __syncthreads();
+  if (lane_id() == 0) {
+    sm.redf[w] = lo;
+    sm.redf[NW + w] = hi;
+  }
+  __syncthreads();
+  lo = sm.redf[0];
+  hi = sm.redf[NW];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) {
+    lo = fminf(lo, sm.redf[i]);
+    hi = fmaxf(hi, sm.redf[NW + i]);
+  }
+}
+
+// Members (at most 64 over the block) to lanes: wave w wrote its `c` members
+// to its own region; lane l of every wave then holds member l (in wave order).
+template <int NW>
+__device__ __forceinline__ float gather_members(BlockLds<NW> &sm, int w, int c, float pad) {
+  __syncthreads();
+  if (lane_id() == 0) sm.redi[w] = c;
+  __syncthreads();
+  const int lane = lane_id();
+  float v = pad;
+  int acc = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    const int ci = sm.redi[i];
+    if (lane >= acc && lane < acc + ci) v = sm.list[i][lane - acc];
+    acc += ci;
+  }
+  return v;
+}
+
+template <int NW, int IPL>
+__global__ void __launch_bounds__(64 * NW) topk_block_kernel(const TopkParams p) {
+  static_assert(IPL % kGroup == 0, "items come in whole groups");
+  constexpr int NG = IPL / kGroup;
+  constexpr int SEG = 64 * IPL;
+  constexpr int kSub = 8;
+  static_assert(kGroup % kSub == 0, "every group feeds every subset");
+  __shared__ BlockLds<NW> sm;
+  int *hist = sm.hist;
+  const int w = __builtin_amdgcn_readfirstlane(wave_id()), lane = lane_id();
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  int64_t st, en;
+  if (p.starts) {
+    st = p.starts[row];
+    en = p.ends[row];
+  } else if (p.causal) {
+    st = 0;
+    en = (int64_t)((uint64_t)row % (uint64_t)p.seq_q) + 1 + p.causal_offset;
+  } else {
+    st = 0;
+    en = p.row_len;
+  }
+  if (st < 0) st = 0;
+  if (en > p.row_len) en = p.row_len;
+  const int n = __builtin_amdgcn_readfirstlane(en > st ? (int)(en - st) : 0);
+  int32_t *orow = p.out + row * p.topk;
+  if (n <= p.topk) {  // block-uniform: the whole workgroup leaves together
+    for (int i = tid; i < p.topk; i += 64 * NW) orow[i] = i < n ? (int32_t)(st + i) : -1;
+    return;
+  }
+
+  // ---- load this wave's segment; groups past the window issue no loads ----
+  const float *src = p.scores + row * p.row_stride + st;
+  const __amdgpu_buffer_rsrc_t rsrc = make_buffer_rsrc(src, (uint32_t)n * 4u);
+  const int seg0 = w * SEG;
+  const int nseg = n - seg0;
+  int ng = nseg <= 0 ? 0 : (nseg + 64 * kGroup - 1) / (64 * kGroup);
+  ng = __builtin_amdgcn_readfirstlane(ng < NG ? ng : NG);
+  const float kPad = __uint_as_float(0x7fc00000u);
+  float x[IPL];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    if (g < ng) {
+#pragma unroll
+      for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) x[i] = buffer_load_f32(rsrc, 4 * lane, 4 * seg0 + 256 * i);
+    } else {
+#pragma unroll
+      for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) x[i] = kPad;
+    }
+  }
+  for (int q = tid; q < kBlockBins; q += 64 * NW) hist[q] = 0;
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    if (g < ng) {
+      const bool last = g == ng - 1;
+#pragma unroll
+      for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
+        x[i] = rank_value(x[i]);
+        if (last) x[i] = (64 * i + lane < nseg) ? x[i] : kPad;
+      }
+    }
+  }
+
+  int r = p.topk;
+  float K = 0.0f;
+  int c_eq = kNoLimit;
+  bool decided = false;  // block-uniform throughout
+  float vA, vB;
+  int m = n;
+
+  // ---- round 0: maximum and the lower bound L (see the wave kernel) ----
+  fence_values(x, ng);
+  float smax[kSub];
+#pragma unroll
+  for (int j = 0; j < kSub; ++j) smax[j] = -INFINITY;
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    if (g < ng) {
+#pragma unroll
+      for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) smax[i % kSub] = fmaxf(smax[i % kSub], x[i]);
+    }
+  }
+  int nsub;
+  float hi;
+  float L = subset_bound(smax, nsub, hi);
+  if (lane == 0) sm.redi[NW + w] = nsub;
+  block_minmax_f<NW>(L, hi, sm, w);
+  nsub = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) nsub += sm.redi[NW + i];
+  if (r > nsub) {
+    fence_values(x, ng);
+    float lo = INFINITY, unused = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if (g < ng) {
+#pragma unroll
+        for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) lo = fminf(lo, x[i]);
+      }
+    }
+    lo = __uint_as_float(wv::wave_reduce(__float_as_uint(lo), wv::MinF()));
+    block_minmax_f<NW>(lo, unused, sm, w);
+    L = lo;
+  }
+  vA = L;
+  vB = hi;
+  if (L == hi) {
+    K = hi;
+    c_eq = r;
+    decided = true;
+  } else if (__builtin_isfinite(L) && __builtin_isfinite(hi)) {
+    // linear buckets as in the wave kernel, 2048 of them: bins round((x - L) * scale + 1 + d)
+    const float scale = (float)(kBlockBins - 3) / (hi - L);
+    const float cbin = -L * scale + 12582913.0f;
+    if (isfinite(scale) && fmaxf(fabsf(L), fabsf(hi)) * scale < 1048576.0f) {
+      __syncthreads();  // the zeroed histogram
+      fence_values(x, ng);
+      int *const hist_b = hist - kBinBits;
+      int one = 1;
+      asm volatile("" : "+v"(one));
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        if (g < ng) {
+#pragma unroll
+          for (int i = g * kGroup; i < (g + 1) * kGroup; ++i)
+            if (x[i] >= L) atomicAdd(&hist_b[lin_bits(x[i], scale, cbin)], one);
+        }
+      }
+      __syncthreads();
+      int bsel, above;
+      find_bucket<kBlockBins>(hist, r, bsel, above);
+      m = hist[bsel];
+      r -= above;
+      const uint32_t bsel_bits = kBinBits + (uint32_t)bsel;
+      fence_values(x, ng);
+      if (m <= 64) {
+        int base = 0;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          if (g < ng) {
+#pragma unroll
+            for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
+              const uint64_t bm =
+                  wv::ballot(x[i] >= L) & wv::ballot(lin_bits(x[i], scale, cbin) == bsel_bits);
+              if (bm) {
+                if ((bm >> lane) & 1u) sm.list[w][base + lane_rank(bm)] = x[i];
+                base += __popcll(bm);
+              }
+            }
+          }
+        }
+        rank_list(gather_members<NW>(sm, w, base, kPad), m, r, K, c_eq);
+        decided = true;
+      } else {
+        float mlo = INFINITY, mhi = -INFINITY;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          if (g < ng) {
+#pragma unroll
+            for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
+              const bool mem = x[i] >= L && lin_bits(x[i], scale, cbin) == bsel_bits;
+              mlo = mem ? fminf(mlo, x[i]) : mlo;
+              mhi = mem ? fmaxf(mhi, x[i]) : mhi;
+            }
+          }
+        }
+        mlo = __uint_as_float(wv::wave_reduce(__float_as_uint(mlo), wv::MinF()));
+        mhi = __uint_as_float(wv::wave_reduce(__float_as_uint(mhi), wv::MaxF()));
+        block_minmax_f<NW>(mlo, mhi, sm, w);
+        vA = mlo;
+        vB = mhi;
+        if (r == m) {
+          K = vA;
+          c_eq = kNoLimit;
+          decided = true;
+        }
+      }
+    }
+  }
+
+  // ---- key rounds: 11 key bits per round over the shared histogram ----
+#pragma unroll 1
+  for (int round = 0; round < 5 && !decided; ++round) {
+    const uint32_t A = score_key(vA), B = score_key(vB);
+    if (A == B) {
+      K = vA;
+      c_eq = r;
+      decided = true;
+      break;
+    }
+    const int bl = 32 - __clz((int)(B - A));
+    const int shift = bl > 11 ? bl - 11 : 0;
+    __syncthreads();  // earlier readers of the histogram are done
+    for (int q = tid; q < kBlockBins; q += 64 * NW) hist[q] = 0;
+    __syncthreads();
+    fence_values(x, ng);
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if (g < ng) {
+#pragma unroll
+        for (int i = g * kGroup; i < (g + 1) * kGroup; ++i)
+          if (x[i] >= vA && x[i] <= vB) atomicAdd(&hist[(score_key(x[i]) - A) >> shift], 1);
+      }
+    }
+    __syncthreads();
+    int bsel, above;
+    find_bucket<kBlockBins>(hist, r, bsel, above);
+    m = hist[bsel];
+    r -= above;
+    fence_values(x, ng);
+    float mlo = INFINITY, mhi = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if (g < ng) {
+#pragma unroll
+        for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
+          const bool mem = x[i] >= vA && x[i] <= vB && ((score_key(x[i]) - A) >> shift) == (uint32_t)bsel;
+          mlo = mem ? fminf(mlo, x[i]) : mlo;
+          mhi = mem ? fmaxf(mhi, x[i]) : mhi;
+        }
+      }
+    }
+    mlo = __uint_as_float(wv::wave_reduce(__float_as_uint(mlo), wv::MinF()));
+    mhi = __uint_as_float(wv::wave_reduce(__float_as_uint(mhi), wv::MaxF()));
+    block_minmax_f<NW>(mlo, mhi, sm, w);
+    vA = mlo;
+    vB = mhi;
+    if (r == m) {
+      K = vA;
+      c_eq = kNoLimit;
+      decided = true;
+    } else if (m <= 64) {
+      fence_values(x, ng);
+      int base = 0;
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        if (g < ng) {
+#pragma unroll
+          for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
+            const uint64_t bm = wv::ballot(x[i] >= vA) & wv::ballot(x[i] <= vB);
+            if (bm) {
+              if ((bm >> lane) & 1u) sm.list[w][base + lane_rank(bm)] = x[i];
+              base += __popcll(bm);
+            }
+          }
+        }
+      }
+      rank_list(gather_members<NW>(sm, w, base, kPad), m, r, K, c_eq);
+      decided = true;
+    }
+  }
+
+  // ---- output in column order across the waves ----
+  // per-wave counts of x >= K (or of x > K and x == K), then each wave's start
+  fence_values(x, ng);
+  const bool nolimit = c_eq == kNoLimit;
+  int c1 = 0, c2 = 0;
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    if (g < ng) {
+#pragma unroll
+      for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
+        if (nolimit) {
+          c1 += __popcll(wv::ballot(x[i] >= K));
+        } else {
+          c1 += __popcll(wv::ballot(x[i] > K));
+          c2 += __popcll(wv::ballot(x[i] == K));
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (lane == 0) {
+    sm.redi[w] = c1;
+    sm.redi[NW + w] = c2;
+  }
+  __syncthreads();
+  int pos = 0, eq_before = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    if (i < w) {
+      const int ci = sm.redi[i], ei = sm.redi[NW + i];
+      const int room = c_eq - eq_before;
+      pos += nolimit ? ci : ci + (ei < room ? ei : (room > 0 ? room : 0));
+      eq_before += ei;
+    }
+  }
+  const __amdgpu_buffer_rsrc_t orsrc = make_buffer_rsrc(orow, (uint32_t)p.topk * 4u);
+  constexpr int kDrop = 0x7ffffffc;
+  const int64_t col0 = st + seg0 + lane;
+  fence_values(x, ng);
+  if (nolimit) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if (g < ng) {
+#pragma unroll
+        for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
+          const bool t = x[i] >= K;
+          const uint64_t tm = wv::ballot(t);
+          const int at = pos + lane_rank(tm);
+          __builtin_amdgcn_raw_buffer_store_b32((uint32_t)(col0 + 64 * i), orsrc, t ? 4 * at : kDrop, 0, 0);
+          pos += __popcll(tm);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if (g < ng) {
+#pragma unroll
+        for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
+          const bool eqv = x[i] == K;
+          const uint64_t em = wv::ballot(eqv);
+          const bool t = x[i] > K || (eqv && eq_before + lane_rank(em) < c_eq);
+          const uint64_t tm = wv::ballot(t);
+          const int at = pos + lane_rank(tm);
+          __builtin_amdgcn_raw_buffer_store_b32((uint32_t)(col0 + 64 * i), orsrc, t ? 4 * at : kDrop, 0, 0);
+          pos += __popcll(tm);
+          eq_before += __popcll(em);
+        }
+      }
+    }
+  }
+}
+
+template <int NW, int IPL>
+static int launch_topk_block(const TopkParams &p, hipStream_t st) {
+  hipLaunchKernelGGL((topk_block_kernel<NW, IPL>), dim3((unsigned)p.rows), dim3(64 * NW), 0, st, p);
+  return check_launch("topk_select(block)");
+}
+
 template <int IPL>
 static int launch_topk_wave(const TopkParams &p, hipStream_t st) {
   hipLaunchKernelGGL((topk_wave_kernel<IPL>), dim3((unsigned)((p.rows + 3) / 4)), dim3(256), 0, st, p);
@@ -797,8 +1204,8 @@ extern "C" int dsa_topk(const float *scores, int64_t rows, int64_t row_len, int6
   if (row_len <= 2048) return launch_topk_wave<32>(p, st);
   if (row_len <= 4096) return launch_topk_wave<64>(p, st);
   if (row_len <= 8192) return launch_topk_wave<128>(p, st);
-  if (row_len <= 16384) return launch_topk<1024, 16>(p, st);
-  if (row_len <= 32768) return launch_topk<1024, 32>(p, st);
+  if (row_len <= 16384) return launch_topk_block<4, 64>(p, st);
+  if (row_len <= 32768) return launch_topk_block<8, 64>(p, st);
   return set_error(DSA_ERR_UNSUPPORTED, "dsa_topk: rows longer than 32768 columns are not supported (got %lld)",
                    (long long)row_len);
 }

@@ -167,6 +167,57 @@ def test_topk_adversarial_rows(dev, rows, n, topk):
     np.testing.assert_array_equal(got.numpy(), ref)
 
 
+def _subset_bound_rows(rows, n, topk, seed):
+    """Rows aimed at the wave kernel's lower bound L of the k-th largest (the
+    least of 4 interleaved per-lane subset maxima; lane l holds columns 64i + l,
+    item i feeds subset i % 4): exactly one large score per (lane, subset) so
+    that only topk scores reach L, ties at L and scores one ulp below it (the
+    same linear bucket), every subset maximum equal, NaN (ranked +inf) inside
+    subsets, a subset made only of -inf (L falls back to the row minimum)."""
+    g = np.random.default_rng(seed)
+    s = (g.standard_normal((rows, n)) * 0.1).astype(np.float32)
+    cols = np.arange(n)
+    subset = (cols // 64) % 4
+    lane = cols % 64
+    for r in range(rows):
+        kind = r % 5
+        if kind in (0, 1, 2):
+            big = (100.0 + g.random(256)).astype(np.float32)
+            if kind == 1:
+                big[:] = 5.0
+            for ls in range(256):
+                pick = np.flatnonzero((lane == ls // 4) & (subset == ls % 4))
+                s[r, g.choice(pick)] = big[ls]
+            lmin = big.min()
+            if kind == 0:   # neighbours of L: equal to it, and one ulp below it
+                free = np.flatnonzero(s[r] < 50)
+                s[r, g.choice(free, 5, replace=False)] = lmin
+                s[r, g.choice(free, 7, replace=False)] = np.nextafter(lmin, np.float32(-np.inf))
+            if kind == 2:
+                s[r, g.choice(n, 9, replace=False)] = np.nan
+        elif kind == 3:
+            s[r, (lane == 5) & (subset == 2)] = -np.inf
+        else:
+            s[r] = np.round(s[r] * 40) / 40
+    return s
+
+
+@pytest.mark.parametrize("n", [2048, 4096, 8192])
+@pytest.mark.parametrize("topk", [64, 200, 256])
+def test_topk_subset_bound_edges(dev, n, topk):
+    s = _subset_bound_rows(30, n, topk, seed=n + topk)
+    got = topk_indices(torch.from_numpy(s).to(dev), topk, causal=False).cpu()
+    np.testing.assert_array_equal(got.numpy(), otk.topk_ascending(s, topk))
+    # the same rows as causal windows ending at every length up to n
+    rows = 96
+    t = np.repeat(s[:1], rows, axis=0)
+    t[1::2] = s[1]
+    got = topk_indices(torch.from_numpy(t).to(dev), topk, causal=True, seq_q=rows,
+                       causal_offset=n - rows).cpu()
+    st, en = otk.causal_windows(rows, rows, n, offset=n - rows)
+    np.testing.assert_array_equal(got.numpy(), otk.topk_ascending(t, topk, st, en))
+
+
 def test_topk_windows_and_all_equal(dev):
     rows, n, topk = 50, 700, 32
     s = np.zeros((rows, n), dtype=np.float32)          # all equal: lowest columns win
