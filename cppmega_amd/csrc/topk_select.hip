@@ -1,4 +1,4 @@
-// Deterministic per-row top-k on gfx950: adaptive radix select in LDS.
+// Deterministic per-row top-k on gfx950: adaptive bucket select in LDS.
 //
 // Reference: the top-k of Megatron's fused_qk_topk_naive
 // (`index_scores.topk(min(topk, seqlen), dim=-1)[1]`, restated in
@@ -10,19 +10,13 @@
 // column, NaN ranks as +inf, -0.0 equals +0.0, and the chosen columns are
 // written in ascending order, padded with -1.
 //
-// One workgroup per row.  Each thread holds a contiguous chunk of the row as
-// order-preserving 32-bit keys in registers.  Each round takes the key range
-// [kmin, kmax] of the elements still undecided ("members") and histograms the
-// 11 bits just below the highest bit in which kmin and kmax differ, so the
-// 2048 LDS bins split whatever range the data occupies (a fixed top byte would
-// put most real scores, which share sign and exponent, into a handful of
-// bins and serialise the LDS atomics).  A suffix scan over the bins finds the
-// bucket holding the k-th largest member: higher buckets are taken, lower
-// ones dropped.  The span shrinks by 2^11 per round, so at most three rounds
-// run before the remaining members are either few (<= kCand: ranked exactly
-// by (key desc, column asc)) or all equal (the lowest columns are taken).
-// Taken columns are compacted in column order by a block prefix sum, which
-// yields the ascending output directly.
+// Rows of up to 8192 columns run one wave per row (topk_wave_kernel), longer
+// rows one workgroup of NW waves per row (topk_block_kernel).  The row stays
+// in registers; a lower bound of the k-th largest score from per-lane subset
+// maxima keeps the lower scores out of the value-linear histogram, which
+// usually leaves a handful of members in the bucket holding the k-th largest;
+// those are ranked exactly, and the output is compacted in column order by
+// ballots.
 #include "dsa_common.hpp"
 
 namespace dsa {
@@ -44,249 +38,8 @@ __device__ __forceinline__ uint32_t score_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Block-wide exclusive prefix sum of one int per thread; returns the total.
-template <int THREADS>
-__device__ __forceinline__ int block_excl_scan(int v, int *excl, int *wtot) {
-  constexpr int NW = THREADS / 64;
-  const int lane = lane_id(), w = wave_id();
-  int incl = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int o = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += o;
-  }
-  __syncthreads();
-  if (lane == 63) wtot[w] = incl;
-  __syncthreads();
-  int before = 0, total = 0;
-#pragma unroll
-  for (int i = 0; i < NW; ++i) {
-    const int t = wtot[i];
-    before += (i < w) ? t : 0;
-    total += t;
-  }
-  *excl = before + incl - v;
-  return total;
-}
-
-// Block-wide min and max of one key per thread (result in every thread).
-template <int THREADS>
-__device__ __forceinline__ void block_minmax(uint32_t &lo, uint32_t &hi, uint32_t *rmin, uint32_t *rmax) {
-  constexpr int NW = THREADS / 64;
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const uint32_t a = (uint32_t)__shfl_xor((int)lo, off, 64);
-    const uint32_t b = (uint32_t)__shfl_xor((int)hi, off, 64);
-    lo = a < lo ? a : lo;
-    hi = b > hi ? b : hi;
-  }
-  __syncthreads();
-  if (lane_id() == 0) {
-    rmin[wave_id()] = lo;
-    rmax[wave_id()] = hi;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < NW; ++i) {
-    lo = rmin[i] < lo ? rmin[i] : lo;
-    hi = rmax[i] > hi ? rmax[i] : hi;
-  }
-}
-
-constexpr int kBins = 2048;   // histogram bins per round (11 bits)
-constexpr int kCand = 256;    // members ranked exactly once at most this many remain
-
-template <int THREADS, int ITEMS>
-__global__ void __launch_bounds__(THREADS) topk_select_kernel(const TopkParams p) {
-  static_assert(ITEMS <= 32, "membership masks are 32-bit");
-  static_assert(kBins % THREADS == 0, "bins are split evenly over the threads");
-  constexpr int BPT = kBins / THREADS;
-  __shared__ int hist[kBins];
-  __shared__ int wtot[THREADS / 64];
-  __shared__ uint32_t rmin[THREADS / 64], rmax[THREADS / 64];
-  __shared__ int s_bsel, s_above;
-  __shared__ uint32_t cand_key[kCand];
-  __shared__ int cand_pos[kCand];
-  __shared__ uint32_t selmask[THREADS];
-  const int tid = threadIdx.x;
-  const int64_t row = blockIdx.x;
-  int64_t st, en;
-  if (p.starts) {
-    st = p.starts[row];
-    en = p.ends[row];
-  } else if (p.causal) {
-    st = 0;
-    en = (row % p.seq_q) + 1 + p.causal_offset;
-  } else {
-    st = 0;
-    en = p.row_len;
-  }
-  if (st < 0) st = 0;
-  if (en > p.row_len) en = p.row_len;
-  const int n = en > st ? (int)(en - st) : 0;
-  int32_t *orow = p.out + row * p.topk;
-
-  if (n <= p.topk) {  // everything in the window is selected
-    for (int i = tid; i < p.topk; i += THREADS) orow[i] = i < n ? (int32_t)(st + i) : -1;
-    return;
-  }
-
-  // ---- load keys (blocked: thread owns columns [tid*ITEMS, tid*ITEMS + ITEMS)) ----
-  const float *src = p.scores + row * p.row_stride + st;
-  uint32_t key[ITEMS];
-  const int c0 = tid * ITEMS;
-  const bool vec = ((reinterpret_cast<uintptr_t>(src) & 15u) == 0) && (ITEMS % 4 == 0);
-  if (vec && c0 + ITEMS <= n) {
-#pragma unroll
-    for (int i = 0; i < ITEMS; i += 4) {
-      const f32x4 v = *reinterpret_cast<const f32x4 *>(src + c0 + i);
-      key[i] = score_key(v[0]);
-      key[i + 1] = score_key(v[1]);
-      key[i + 2] = score_key(v[2]);
-      key[i + 3] = score_key(v[3]);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < ITEMS; ++i) key[i] = (c0 + i < n) ? score_key(src[c0 + i]) : 0u;
-  }
-  int nvalid = n - c0;
-  nvalid = nvalid < 0 ? 0 : (nvalid > ITEMS ? ITEMS : nvalid);
-
-  uint32_t member = nvalid >= 32 ? 0xffffffffu : ((1u << nvalid) - 1u);  // undecided elements
-  uint32_t taken = 0;                                                     // selected elements
-  int r = p.topk;  // members still to take
-  int m = n;       // members left (block-uniform)
-
-  // Four rounds always suffice: three histogram rounds shrink a 32-bit span below
-  // 2^11, the next round sees single-key buckets; the exits below end it sooner.
-#pragma unroll 1
-  for (int round = 0; round < 5 && r > 0; ++round) {
-    uint32_t lo = 0xffffffffu, hi = 0u;
-#pragma unroll
-    for (int i = 0; i < ITEMS; ++i) {
-      if ((member >> i) & 1u) {
-        lo = key[i] < lo ? key[i] : lo;
-        hi = key[i] > hi ? key[i] : hi;
-      }
-    }
-    block_minmax<THREADS>(lo, hi, rmin, rmax);
-    if (lo == hi || m <= kCand || round == 4) break;  // tie or exact ranking below
-
-    const uint32_t span = hi - lo;
-    const int shift = (32 - __clz((int)span)) > 11 ? (32 - __clz((int)span)) - 11 : 0;
-#pragma unroll
-    for (int j = 0; j < BPT; ++j) hist[tid * BPT + j] = 0;
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < ITEMS; ++i)
-      if ((member >> i) & 1u) atomicAdd(&hist[(key[i] - lo) >> shift], 1);
-    __syncthreads();
-    // suffix scan: thread tid owns bins kBins-1-tid*BPT down to kBins-BPT-tid*BPT
-    int cnt[BPT];
-    int local = 0;
-#pragma unroll
-    for (int j = 0; j < BPT; ++j) {
-      cnt[j] = hist[kBins - 1 - (tid * BPT + j)];
-      local += cnt[j];
-    }
-    int excl;
-    block_excl_scan<THREADS>(local, &excl, wtot);
-    if (excl < r && excl + local >= r) {
-      int acc = excl;
-#pragma unroll
-      for (int j = 0; j < BPT; ++j) {
-        if (acc < r && acc + cnt[j] >= r) {
-          s_bsel = kBins - 1 - (tid * BPT + j);
-          s_above = acc;
-        }
-        acc += cnt[j];
-      }
-    }
-    __syncthreads();
-    const uint32_t bsel = (uint32_t)s_bsel;
-    const int above = s_above;
-    const int inb = hist[bsel];
-#pragma unroll
-    for (int i = 0; i < ITEMS; ++i) {
-      if ((member >> i) & 1u) {
-        const uint32_t b = (key[i] - lo) >> shift;
-        if (b > bsel) taken |= 1u << i;
-        if (b != bsel) member &= ~(1u << i);
-      }
-    }
-    r -= above;
-    m = inb;
-    if (r == m) {  // the whole bucket is taken
-      taken |= member;
-      member = 0;
-      r = 0;
-    }
-    __syncthreads();  // hist and s_bsel are rewritten by the next round
-  }
-
-  if (r > 0) {
-    int nm = __popc(member);
-    int before;
-    block_excl_scan<THREADS>(nm, &before, wtot);
-    bool ranked = false;
-    if (m <= kCand) {
-      // exact ranking of the <= kCand members by (key desc, column asc); candidates
-      // are stored in column order, so a lower slot means a lower column
-      int slot = before;
-#pragma unroll
-      for (int i = 0; i < ITEMS; ++i) {
-        if ((member >> i) & 1u) {
-          cand_key[slot] = key[i];
-          cand_pos[slot] = c0 + i;
-          ++slot;
-        }
-      }
-      selmask[tid] = 0u;
-      __syncthreads();
-      for (int c = tid; c < m; c += THREADS) {
-        const uint32_t kc = cand_key[c];
-        int rank = 0;
-        for (int j = 0; j < m; ++j) {
-          const uint32_t kj = cand_key[j];
-          rank += (kj > kc || (kj == kc && j < c)) ? 1 : 0;
-        }
-        if (rank < r) {
-          const int pos = cand_pos[c];
-          atomicOr(&selmask[pos / ITEMS], 1u << (pos % ITEMS));
-        }
-      }
-      __syncthreads();
-      taken |= selmask[tid];
-      ranked = true;
-    }
-    if (!ranked) {
-      // all members share one key: the lowest columns win
-      int k = before;
-#pragma unroll
-      for (int i = 0; i < ITEMS; ++i) {
-        if ((member >> i) & 1u) {
-          if (k < r) taken |= 1u << i;
-          ++k;
-        }
-      }
-    }
-  }
-
-  // ---- compaction in column order ----
-  const int nsel = __popc(taken);
-  int pos;
-  block_excl_scan<THREADS>(nsel, &pos, wtot);
-#pragma unroll
-  for (int i = 0; i < ITEMS; ++i) {
-    if (((taken >> i) & 1u) && pos < p.topk) {  // exactly topk are taken; the bound is a guard
-      orow[pos] = (int32_t)(st + c0 + i);
-      ++pos;
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------
-// Wave-per-row variant for rows of at most 64 * IPL columns (no block barriers).
+// Wave-per-row kernel for rows of at most 64 * IPL columns (no block barriers).
 // ---------------------------------------------------------------------------
 // Lane l holds columns 64i + l (i < IPL) as normalised scores: every load
 // instruction reads 256 B contiguously.  The undecided elements are always the
@@ -771,7 +524,7 @@ topk_wave_kernel(const TopkParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Workgroup-per-row variant for rows of up to NW * 64 * IPL columns: the wave
+// Workgroup-per-row kernel for rows of up to NW * 64 * IPL columns: the wave
 // kernel's passes with NW waves per row.  Wave w holds the contiguous segment
 // of 64 * IPL columns from w * 64 * IPL (lane l: columns w * 64 * IPL + 64i + l),
 // the histogram (2048 bins) is shared in LDS, and minima, maxima, counts and
@@ -1164,12 +917,6 @@ template <int IPL>
 static int launch_topk_wave(const TopkParams &p, hipStream_t st) {
   hipLaunchKernelGGL((topk_wave_kernel<IPL>), dim3((unsigned)((p.rows + 3) / 4)), dim3(256), 0, st, p);
   return check_launch("topk_select(wave)");
-}
-
-template <int THREADS, int ITEMS>
-static int launch_topk(const TopkParams &p, hipStream_t st) {
-  hipLaunchKernelGGL((topk_select_kernel<THREADS, ITEMS>), dim3((unsigned)p.rows), dim3(THREADS), 0, st, p);
-  return check_launch("topk_select");
 }
 
 }  // namespace dsa
