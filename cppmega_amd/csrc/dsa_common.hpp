@@ -122,6 +122,30 @@ __device__ __forceinline__ f32x2 e4m3x2_to_f32(uint32_t word, bool hi) {
   return hi ? __builtin_amdgcn_cvt_pk_f32_fp8((int)word, true) : __builtin_amdgcn_cvt_pk_f32_fp8((int)word, false);
 }
 
+// Eight e4m3 codes (lo: bytes 0-3, hi: bytes 4-7) times one scale, as bf16
+// (round to nearest even).  Exact when the scale is a power of two within
+// mx_scale_exact's range: a code has at most 4 significant bits.
+__device__ __forceinline__ bf16x8 e4m3x8_to_bf16_scaled(uint32_t lo, uint32_t hi, float s) {
+  uint32_t w[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const f32x2 v2 = e4m3x2_to_f32(e < 2 ? lo : hi, (e & 1) != 0);
+    w[e] = pack_bf16x2(v2[0] * s, v2[1] * s);
+  }
+  return __builtin_bit_cast(bf16x8, i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
+}
+
+// A block scale for which code * scale is exact in bf16 (and in fp32) for every
+// e4m3 code: zero, or a power of two in [2^-40, 2^40], so the scaled values,
+// their products and a d_qk-long sum of them stay normal and finite in fp32.
+// OCP MX scales (E8M0) are powers of two.
+__device__ __forceinline__ bool mx_scale_exact(float s) {
+  const uint32_t u = __float_as_uint(s) & 0x7fffffffu;
+  if (u == 0u) return true;
+  const uint32_t e = u >> 23;
+  return (u & 0x7fffffu) == 0u && e >= 87u && e <= 167u;
+}
+
 // Round-to-nearest-even, saturating at +-448; NaN -> 0x7f (sign kept).
 __device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
   const uint32_t u = __float_as_uint(f);

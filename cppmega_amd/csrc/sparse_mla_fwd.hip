@@ -50,9 +50,13 @@ struct FwdCfg {
   static_assert(D_V % 32 == 0 && D_QK % 16 == 0 && D_V <= D_QK, "unsupported head dims");
 };
 
-template <int D_QK, int D_V, bool FP8, bool MX = false, bool VPRE = false>
+// QMX: the bf16 kernel with Q given as e4m3 codes and one scale per 32
+// channels (q_scale [B, S, H, D_QK / 32]), converted to bf16 as it is loaded.
+template <int D_QK, int D_V, bool FP8, bool MX = false, bool VPRE = false, bool QMX = false>
 __global__ void __launch_bounds__(256)
 sparse_mla_fwd_kernel(const FwdParams p) {
+  static_assert(!QMX || !FP8, "QMX converts Q for the bf16 kernel");
+  if (p.gate != nullptr && *p.gate != p.gate_run) return;  // the call's other kernel computes it
   using C = FwdCfg<D_QK, D_V, FP8, MX, VPRE>;
   using Gat = typename C::Gat;
   using VGat = typename C::VGat;
@@ -99,9 +103,10 @@ sparse_mla_fwd_kernel(const FwdParams p) {
   const auto sc_rs = make_buffer_rsrc(kv_scale_b, FP8 ? (uint32_t)(p.S_kv * sc_pitch) : 0u);
   typename Gat::Regs rg;
   gather_issue<Gat>(rg, kv_rs, sc_rs, idx_cur, row_pitch, sc_pitch);
-  // pre-dequantised V rows [B, S_kv, G, D_V] bf16 of this (batch, group)
-  const uint32_t v_pitch = (uint32_t)(p.G * D_V * 2);
-  const auto v_rs = make_buffer_rsrc(VPRE ? p.v16 + ((b * p.S_kv) * p.G + g) * D_V : nullptr,
+  // pre-dequantised V rows of this (batch, group): bf16, v16_ld elements per
+  // row of [B, S_kv, G], V in the leading D_V
+  const uint32_t v_pitch = (uint32_t)(p.G * p.v16_ld * 2);
+  const auto v_rs = make_buffer_rsrc(VPRE ? p.v16 + ((b * p.S_kv) * p.G + g) * p.v16_ld : nullptr,
                                      VPRE ? (uint32_t)(p.S_kv * (int64_t)v_pitch) : 0u);
   typename VGat::Regs rgv;
   if constexpr (VPRE) gather_issue<VGat>(rgv, v_rs, v_rs, idx_cur, v_pitch);
@@ -111,13 +116,23 @@ sparse_mla_fwd_kernel(const FwdParams p) {
   // the loads carry no branches.
   const int64_t qrow0 = tok * p.H + g * p.hpg + tile * 32;
   const int nh = p.hpg - tile * 32 < 32 ? p.hpg - tile * 32 : 32;
-  const auto q_rs = make_buffer_rsrc(p.q + qrow0 * D_QK * (FP8 ? 1 : 2), (uint32_t)(nh * D_QK * (FP8 ? 1 : 2)));
+  constexpr int QB = FP8 || QMX ? 1 : 2;  // bytes per Q element
+  const auto q_rs = make_buffer_rsrc(p.q + qrow0 * D_QK * QB, (uint32_t)(nh * D_QK * QB));
   qop_t qreg[C::KSTEPS];
+  float qmxs[QMX ? D_QK / 32 : 1];  // QMX: this lane's head's block scales
+  if constexpr (QMX) {
+#pragma unroll
+    for (int c = 0; c < D_QK / 32; ++c) qmxs[c] = head_ok ? p.q_scale[qrow * (D_QK / 32) + c] : 0.0f;
+  }
 #pragma unroll
   for (int k = 0; k < C::KSTEPS; ++k) {
     if constexpr (FP8) {
       const auto v = __builtin_amdgcn_raw_buffer_load_b64(q_rs, l32 * D_QK + 16 * k + 8 * g32, 0, 0);
       qreg[k] = __builtin_bit_cast(long, v);
+    } else if constexpr (QMX) {
+      // channels 16k + 8 g32 .. + 7 all lie in block k / 2
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(q_rs, l32 * D_QK + 16 * k + 8 * g32, 0, 0);
+      qreg[k] = e4m3x8_to_bf16_scaled((uint32_t)v[0], (uint32_t)v[1], qmxs[k >> 1]);
     } else {
       qreg[k] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
                                                q_rs, (l32 * D_QK + 16 * k + 8 * g32) * 2, 0, 0));
@@ -282,20 +297,20 @@ sparse_mla_fwd_kernel(const FwdParams p) {
   }
 }
 
-template <int D_QK, int D_V, bool FP8, bool MX, bool VPRE>
+template <int D_QK, int D_V, bool FP8, bool MX, bool VPRE, bool QMX = false>
 static int launch_fwd_t(const FwdParams &p, hipStream_t st) {
   using C = FwdCfg<D_QK, D_V, FP8, MX, VPRE>;
   const size_t lds = 4 * (size_t)C::WAVE_BYTES;
   if (lds > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void *)sparse_mla_fwd_kernel<D_QK, D_V, FP8, MX, VPRE>,
+    hipError_t e = hipFuncSetAttribute((const void *)sparse_mla_fwd_kernel<D_QK, D_V, FP8, MX, VPRE, QMX>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return set_error(DSA_ERR_HIP, "sparse_mla_fwd: LDS attribute: %s", hipGetErrorString(e));
   }
   const int64_t nitems = p.B * p.S * p.G * p.ntiles;
   const int64_t nblocks = (nitems + 3) / 4;
   if (nitems >= (1ll << 31)) return set_error(DSA_ERR_INVALID_ARG, "sparse_mla_fwd: grid too large");
-  hipLaunchKernelGGL((sparse_mla_fwd_kernel<D_QK, D_V, FP8, MX, VPRE>), dim3((unsigned)nblocks), dim3(256), lds, st,
-                     p);
+  hipLaunchKernelGGL((sparse_mla_fwd_kernel<D_QK, D_V, FP8, MX, VPRE, QMX>), dim3((unsigned)nblocks), dim3(256), lds,
+                     st, p);
   return check_launch("sparse_mla_fwd");
 }
 
@@ -334,12 +349,53 @@ dequant_v_kernel(const unsigned char *kv, const float *kv_scale, uint16_t *v16, 
   }
 }
 
+// MX forward with a workspace, first of its two passes: every kv row
+// dequantised to bf16 (code times its 32-channel block scale, round to nearest
+// even: the values the block-scaled kernel forms for V) into kv16 [B, S_kv, G,
+// D_qk], and every q and kv block scale checked.  *gate (cleared by
+// mx_gate_reset_kernel) becomes 1 unless each scale passes mx_scale_exact.  If
+// all do, every dequantised value (and Q converted the same way at load) is
+// exact, and the bf16 kernel on them computes the block-scaled scores up to the
+// order of the fp32 sums; otherwise the block-scaled e4m3 kernel runs instead.
+__global__ void __launch_bounds__(256)
+mx_prepass_kernel(const unsigned char *kv, const float *kv_scale, uint16_t *kv16, int64_t rows, int D_qk,
+                  const float *q_scale, int64_t n_qscales, int *gate) {
+  const int per_row = D_qk / 8;
+  const int64_t n = rows * per_row;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  bool bad = false;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += stride) {
+    const int64_t row = i / per_row;
+    const int c8 = (int)(i - row * per_row);
+    const uint2 raw = *reinterpret_cast<const uint2 *>(kv + row * D_qk + 8 * c8);
+    const float sc = kv_scale[row * (D_qk / 32) + (8 * c8) / 32];
+    bad |= !mx_scale_exact(sc);
+    *reinterpret_cast<bf16x8 *>(kv16 + row * D_qk + 8 * c8) = e4m3x8_to_bf16_scaled(raw.x, raw.y, sc);
+  }
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n_qscales; i += stride)
+    bad |= !mx_scale_exact(q_scale[i]);
+  if (__ballot(bad) != 0ull && lane_id() == 0) atomicOr(gate, 1);
+}
+
+__global__ void mx_gate_reset_kernel(int *gate) {
+  if (threadIdx.x == 0) *gate = 0;
+}
+
 }  // namespace dsa
 
 using namespace dsa;
 
 static size_t v16_bytes(int64_t B, int64_t S_kv, int64_t G, int64_t D_v) {
   return ((size_t)B * S_kv * G * D_v * 2 + 255) & ~(size_t)255;
+}
+
+// MX shapes with the exact-dequantisation path (a bf16 kernel for d_qk / d_v)
+static bool mx_exact_shape(int64_t D_qk, int64_t D_v) {
+  return (D_qk == 128 && (D_v == 64 || D_v == 128)) || (D_qk == 192 && D_v == 128) || (D_qk == 576 && D_v == 512);
+}
+// MX workspace: whole kv rows in bf16, then the gate (256 bytes)
+static size_t mx_ws_bytes(int64_t B, int64_t S_kv, int64_t G, int64_t D_qk) {
+  return v16_bytes(B, S_kv, G, D_qk) + 256;
 }
 
 static int sparse_mla_fwd_impl(const void *q, const void *kv, const int32_t *indices, void *out, float *lse2,
@@ -368,6 +424,9 @@ static int sparse_mla_fwd_impl(const void *q, const void *kv, const int32_t *ind
   p.q_scale = q_scale;
   p.kv_scale = kv_scale;
   p.v16 = nullptr;
+  p.v16_ld = (int)D_v;
+  p.gate = nullptr;
+  p.gate_run = 0;
   p.B = B;
   p.S = S;
   p.S_kv = S_kv;
@@ -380,8 +439,41 @@ static int sparse_mla_fwd_impl(const void *q, const void *kv, const int32_t *ind
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool f8 = dtype == DSA_DTYPE_E4M3;
   DSA_REQUIRE(S_kv * G * D_qk * 2 < (1ll << 32), "dsa_sparse_mla_fwd: kv rows of one batch exceed 4 GiB");
-  if (workspace != nullptr && dtype != DSA_DTYPE_BF16 && !wide_shape(D_qk, D_v)) {
-    // e4m3 / MX: dequantise the V rows once instead of once per gather
+  if (workspace != nullptr && dtype == DSA_DTYPE_MXFP8 && mx_exact_shape(D_qk, D_v)) {
+    // MX: kv rows dequantised once (and the scales checked), then two kernels
+    // gated on the check: the bf16 kernel on the dequantised rows with Q
+    // converted at load when every scale makes the conversion exact, else the
+    // block-scaled e4m3 kernel (reading V from the dequantised rows when narrow)
+    const size_t need = mx_ws_bytes(B, S_kv, G, D_qk);
+    DSA_REQUIRE(workspace_bytes >= need, "dsa_sparse_mla_fwd: workspace %zu < required %zu", workspace_bytes, need);
+    uint16_t *kv16 = static_cast<uint16_t *>(workspace);
+    int *gate = reinterpret_cast<int *>(static_cast<unsigned char *>(workspace) + v16_bytes(B, S_kv, G, D_qk));
+    const int64_t rows = B * S_kv * G;
+    const int64_t units = rows * (D_qk / 8);
+    const unsigned grid = (unsigned)((units + 255) / 256 < 8192 ? (units + 255) / 256 : 8192);
+    hipLaunchKernelGGL(mx_gate_reset_kernel, dim3(1), dim3(64), 0, st, gate);
+    hipLaunchKernelGGL(mx_prepass_kernel, dim3(grid), dim3(256), 0, st, p.kv, kv_scale, kv16, rows, (int)D_qk, q_scale,
+                       B * S * H * (D_qk / 32), gate);
+    int rc = check_launch("sparse_mla_fwd(MX dequantise)");
+    if (rc) return rc;
+    FwdParams pe = p;
+    pe.kv = reinterpret_cast<const unsigned char *>(kv16);
+    pe.kv_scale = nullptr;
+    pe.gate = gate;
+    pe.gate_run = 0;
+    if (wide_shape(D_qk, D_v)) rc = launch_fwd_wide(pe, D_qk, D_v, false, st, false, true);
+    else if (D_qk == 128 && D_v == 64) rc = launch_fwd_t<128, 64, false, false, false, true>(pe, st);
+    else if (D_qk == 128) rc = launch_fwd_t<128, 128, false, false, false, true>(pe, st);
+    else rc = launch_fwd_t<192, 128, false, false, false, true>(pe, st);
+    if (rc) return rc;
+    p.gate = gate;
+    p.gate_run = 1;
+    if (!wide_shape(D_qk, D_v)) {
+      p.v16 = kv16;
+      p.v16_ld = (int)D_qk;
+    }
+  } else if (workspace != nullptr && dtype != DSA_DTYPE_BF16 && !wide_shape(D_qk, D_v)) {
+    // e4m3: dequantise the V rows once instead of once per gather
     DSA_REQUIRE(workspace_bytes >= v16_bytes(B, S_kv, G, D_v), "dsa_sparse_mla_fwd: workspace %zu < required %zu",
                 workspace_bytes, v16_bytes(B, S_kv, G, D_v));
     uint16_t *v16 = static_cast<uint16_t *>(workspace);
@@ -426,9 +518,11 @@ extern "C" int dsa_sparse_mla_fwd(const void *q, const void *kv, const int32_t *
 
 extern "C" size_t dsa_sparse_mla_fwd_workspace_size(int64_t B, int64_t S_kv, int64_t G, int64_t D_qk,
                                                     int64_t D_v, int dtype) {
-  // the wide (d_qk = 576) kernels keep converting V in LDS: at cfg5 reading bf16
-  // V rows (1 KiB each, beside 576 B of codes) was no faster than converting them
-  if (B <= 0 || S_kv <= 0 || G <= 0 || D_v <= 0 || dtype == DSA_DTYPE_BF16 || wide_shape(D_qk, D_v)) return 0;
+  if (B <= 0 || S_kv <= 0 || G <= 0 || D_v <= 0 || dtype == DSA_DTYPE_BF16) return 0;
+  if (dtype == DSA_DTYPE_MXFP8 && mx_exact_shape(D_qk, D_v)) return mx_ws_bytes(B, S_kv, G, D_qk);
+  // the wide (d_qk = 576) e4m3 kernel keeps converting V in LDS: at cfg5 reading
+  // bf16 V rows (1 KiB each, beside 576 B of codes) was no faster than converting them
+  if (wide_shape(D_qk, D_v)) return 0;
   return v16_bytes(B, S_kv, G, D_v);
 }
 

@@ -14,7 +14,12 @@ struct FwdParams {
   float *lse;
   const float *q_scale;
   const float *kv_scale;
-  const uint16_t *v16;  // e4m3 / MX: V rows dequantised once to bf16 [B, S_kv, G, D_v], or null
+  const uint16_t *v16;  // e4m3 / MX: V rows dequantised once to bf16 (v16_ld elements per row), or null
+  int v16_ld;           // elements per row of v16: D_v, or D_qk when it holds whole kv rows
+  // when set, the kernel computes only if *gate == gate_run (two kernels of one
+  // call, one of which does the work, chosen on the device without a host sync)
+  const int *gate;
+  int gate_run;
   int64_t B, S, S_kv, H, G, topk;
   int hpg;     // heads per kv group
   int ntiles;  // ceil(hpg / 32)

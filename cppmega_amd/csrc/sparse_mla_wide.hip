@@ -199,11 +199,15 @@ __device__ __forceinline__ void mx_wave_scores(f32x16 &sacc, const unsigned char
 
 // NT head tiles per workgroup: waves 4 ht .. 4 ht + 3 own 32-head tile ht of
 // the item and split its head dims as described above; all 4 NT waves gather
-// (and, e4m3, dequantise) the block's kv rows once for the NT tiles.
-template <int D_QK, int D_V, bool FP8, bool MX = false, int NT = 1>
+// (and, e4m3, dequantise) the block's kv rows once for the NT tiles.  QMX: the
+// bf16 kernel with Q given as e4m3 codes and one scale per 32 channels,
+// converted to bf16 as it is loaded.
+template <int D_QK, int D_V, bool FP8, bool MX = false, int NT = 1, bool QMX = false>
 __global__ void __launch_bounds__(256 * NT) __attribute__((amdgpu_waves_per_eu(D_V <= 512 ? 2 : 1)))
 sparse_mla_fwd_wide_kernel(const FwdParams p) {
   static_assert(!MX || FP8, "MX is an e4m3 mode");
+  static_assert(!QMX || !FP8, "QMX converts Q for the bf16 kernel");
+  if (p.gate != nullptr && *p.gate != p.gate_run) return;  // workgroup-uniform: the call's other kernel computes it
   using C = WideCfg<D_QK, D_V, FP8, 256 * NT>;
   using L = WideFwdLds<D_QK, D_V, FP8, MX, NT>;
   typedef typename std::conditional<FP8, long, bf16x8>::type qop_t;
@@ -251,6 +255,15 @@ sparse_mla_fwd_wide_kernel(const FwdParams p) {
   for (int k = 0; k < C::KQ; ++k) {
     if constexpr (FP8) {
       qreg[k] = head_ok ? *reinterpret_cast<const long *>(p.q + qrow * D_QK + 16 * (k0 + k) + 8 * g32) : 0l;
+    } else if constexpr (QMX) {
+      const int d0 = 16 * (k0 + k) + 8 * g32;  // 8 channels of block d0 / 32
+      uint2 c8 = {0u, 0u};
+      float sc = 0.0f;
+      if (head_ok) {
+        c8 = *reinterpret_cast<const uint2 *>(p.q + qrow * D_QK + d0);
+        sc = p.q_scale[qrow * (D_QK / 32) + (d0 >> 5)];
+      }
+      qreg[k] = e4m3x8_to_bf16_scaled(c8.x, c8.y, sc);
     } else {
       i32x4 v = {0, 0, 0, 0};
       if (head_ok) v = ld_global_16(p.q + (qrow * D_QK + 16 * (k0 + k) + 8 * g32) * 2);
@@ -398,30 +411,36 @@ sparse_mla_fwd_wide_kernel(const FwdParams p) {
   }
 }
 
-template <int D_QK, int D_V, bool FP8, bool MX, int NT>
+template <int D_QK, int D_V, bool FP8, bool MX, int NT, bool QMX = false>
 static int launch_fwd_wide_nt(const FwdParams &p, hipStream_t st) {
   using L = WideFwdLds<D_QK, D_V, FP8, MX, NT>;
   const size_t lds = L::BYTES;
   if (lds > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void *)sparse_mla_fwd_wide_kernel<D_QK, D_V, FP8, MX, NT>,
+    hipError_t e = hipFuncSetAttribute((const void *)sparse_mla_fwd_wide_kernel<D_QK, D_V, FP8, MX, NT, QMX>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return set_error(DSA_ERR_HIP, "sparse_mla_fwd(wide): LDS attribute: %s", hipGetErrorString(e));
   }
   const int64_t nitems = p.B * p.S * p.G * ((p.ntiles + NT - 1) / NT);  // one workgroup per item
   if (nitems >= (1ll << 31)) return set_error(DSA_ERR_INVALID_ARG, "sparse_mla_fwd(wide): grid too large");
-  hipLaunchKernelGGL((sparse_mla_fwd_wide_kernel<D_QK, D_V, FP8, MX, NT>), dim3((unsigned)nitems), dim3(256 * NT), lds,
-                     st, p);
+  hipLaunchKernelGGL((sparse_mla_fwd_wide_kernel<D_QK, D_V, FP8, MX, NT, QMX>), dim3((unsigned)nitems), dim3(256 * NT),
+                     lds, st, p);
   return check_launch("sparse_mla_fwd(wide)");
 }
 
 // Two head tiles per workgroup when a kv group has at least 64 heads (the
 // gather and dequantisation of a block serve both), else one.
-template <int D_QK, int D_V, bool FP8, bool MX = false>
+template <int D_QK, int D_V, bool FP8, bool MX = false, bool QMX = false>
 static int launch_fwd_wide_t(const FwdParams &p, hipStream_t st) {
-  return p.ntiles >= 2 ? launch_fwd_wide_nt<D_QK, D_V, FP8, MX, 2>(p, st) : launch_fwd_wide_nt<D_QK, D_V, FP8, MX, 1>(p, st);
+  return p.ntiles >= 2 ? launch_fwd_wide_nt<D_QK, D_V, FP8, MX, 2, QMX>(p, st)
+                       : launch_fwd_wide_nt<D_QK, D_V, FP8, MX, 1, QMX>(p, st);
 }
 
-int launch_fwd_wide(const FwdParams &p, int64_t d_qk, int64_t d_v, bool fp8, hipStream_t st, bool mx) {
+int launch_fwd_wide(const FwdParams &p, int64_t d_qk, int64_t d_v, bool fp8, hipStream_t st, bool mx, bool qmx) {
+  if (qmx) {
+    if (d_qk == 576 && d_v == 512) return launch_fwd_wide_t<576, 512, false, false, true>(p, st);
+    return set_error(DSA_ERR_UNSUPPORTED, "sparse_mla_fwd(wide): no converted-Q kernel for d_qk=%lld d_v=%lld",
+                     (long long)d_qk, (long long)d_v);
+  }
   if (mx) {
     if (d_qk == 576 && d_v == 512) return launch_fwd_wide_t<576, 512, true, true>(p, st);
     return set_error(DSA_ERR_UNSUPPORTED, "sparse_mla_fwd(wide): no MXFP8 kernel for d_qk=%lld d_v=%lld",

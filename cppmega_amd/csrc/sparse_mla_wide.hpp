@@ -13,7 +13,10 @@ namespace dsa {
 inline bool wide_shape(int64_t d_qk, int64_t d_v) { return d_qk == 576 && (d_v == 512 || d_v == 576); }
 
 // Forward over all (token, kv group, 32-head tile) items; bf16 or e4m3.
-int launch_fwd_wide(const FwdParams &p, int64_t d_qk, int64_t d_v, bool fp8, hipStream_t st, bool mx = false);
+// mx: block-scaled e4m3 kernel; qmx: bf16 kernel with Q converted from e4m3
+// codes and 32-channel block scales as it is loaded
+int launch_fwd_wide(const FwdParams &p, int64_t d_qk, int64_t d_v, bool fp8, hipStream_t st, bool mx = false,
+                    bool qmx = false);
 // Backward main pass (P, dS, dQ, fp32 partial dKV rows at CSR positions); bf16 or e4m3.
 int launch_bwd_main_wide(const BwdParams &p, int64_t d_qk, int64_t d_v, bool fp8, bool f32p, hipStream_t st);
 

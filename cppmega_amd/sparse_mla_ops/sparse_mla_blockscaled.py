@@ -134,7 +134,10 @@ def sparse_mla_blockscaled_mxfp8_fwd_interface(q_data, kv_data, q_scale, kv_scal
     lse = torch.empty((batch, seq_len, heads), dtype=torch.float32, device=q_data.device)
     dev, stream = stream_of(q_data)
     L = _lib.load()
-    # the V rows are dequantised to bf16 once per call (with their block scales) into a workspace
+    # the kv rows are dequantised to bf16 once per call (with their block scales) into a
+    # workspace; when every block scale is a power of two (so the dequantisation is
+    # exact) the bf16 kernel runs on them with q converted at load, otherwise the
+    # block-scaled e4m3 kernel runs (chosen on the device, no host sync)
     ws_bytes = int(L.dsa_sparse_mla_fwd_workspace_size(batch, seq_len_kv, kv_group, dim_total, d_v,
                                                        _lib.DTYPE_MXFP8))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q_data.device) if ws_bytes else None

@@ -85,14 +85,23 @@ int dsa_sparse_mla_fwd(const void *q, const void *kv, const int32_t *indices,
                        void *stream);
 
 /*
- * The same forward with a workspace: for e4m3 and MXFP8 input the V rows
- * (the first D_v columns of kv) are dequantised to bf16 once per call into the
- * workspace, bit-identical to the per-gather dequantisation of
- * dsa_sparse_mla_fwd, and the kernel gathers those rows instead of converting
- * every gathered row again.  dsa_sparse_mla_fwd_workspace_size returns the
- * bytes needed (B * S_kv * G * D_v bf16; 0 for bf16 input and for the
- * d_qk = 576 kernels, which keep converting V in LDS; then `workspace` may be
- * NULL).  Replaces the same reference interfaces as dsa_sparse_mla_fwd.
+ * The same forward with a workspace.  e4m3 input: the V rows (the first D_v
+ * columns of kv) are dequantised to bf16 once per call into the workspace,
+ * bit-identical to the per-gather dequantisation of dsa_sparse_mla_fwd, and
+ * the kernel gathers those rows instead of converting every gathered row
+ * again.  MXFP8 input (d_qk/d_v 128/64, 128/128, 192/128, 576/512): whole kv
+ * rows are dequantised to bf16 (code times its block scale) and every q and kv
+ * block scale is checked on the device; if each is zero or a power of two in
+ * [2^-40, 2^40] (OCP MX scales are powers of two), every dequantised value is
+ * exact and the bf16 kernel runs on those rows with q converted at load (the
+ * block-scaled scores up to the order of the fp32 sums), otherwise the
+ * block-scaled e4m3 kernel runs, with the same result as dsa_sparse_mla_fwd.
+ * The choice is made on the device (no host synchronisation; graph capture
+ * safe).  dsa_sparse_mla_fwd_workspace_size returns the bytes needed (e4m3:
+ * B * S_kv * G * D_v bf16, 0 for the d_qk = 576 kernels, which keep converting
+ * V in LDS; MXFP8: B * S_kv * G * D_qk bf16 plus 256; bf16 input: 0, and then
+ * `workspace` may be NULL).  Replaces the same reference interfaces as
+ * dsa_sparse_mla_fwd.
  */
 size_t dsa_sparse_mla_fwd_workspace_size(int64_t B, int64_t S_kv, int64_t G,
                                          int64_t D_qk, int64_t D_v, int dtype);

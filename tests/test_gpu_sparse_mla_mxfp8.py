@@ -13,7 +13,7 @@ import os
 import pytest
 import torch
 
-from cppmega_amd import synthetic
+from cppmega_amd import _lib, synthetic
 from cppmega_amd.sparse_mla_ops import (mxfp8_dequantize, sparse_mla_blockscaled_mxfp8_backward,
                                         sparse_mla_blockscaled_mxfp8_forward,
                                         sparse_mla_blockscaled_mxfp8_fwd_interface)
@@ -69,6 +69,80 @@ def test_mxfp8_fwd_matches_oracle(dev, B, S, H, D, DV, G, K, pow2):
     out2, lse2 = sparse_mla_blockscaled_mxfp8_fwd_interface(q8.to(dev), kv8.to(dev), qs.to(dev), ks.to(dev),
                                                             idx.to(dev), sm_scale=scale, d_v=DV)
     assert torch.equal(out, out2) and torch.equal(lse, lse2)
+
+
+def _mx_fwd_blockscaled_only(q8, kv8, qs, ks, idx, scale, dv):
+    """dsa_sparse_mla_fwd without a workspace: the block-scaled e4m3 kernel alone."""
+    B, S, H, D = q8.shape
+    _, Skv, G, _ = kv8.shape
+    out = torch.empty((B, S, H, dv), dtype=torch.bfloat16, device=q8.device)
+    lse = torch.empty((B, S, H), dtype=torch.float32, device=q8.device)
+    L = _lib.load()
+    _lib.check(L.dsa_sparse_mla_fwd(q8.data_ptr(), kv8.data_ptr(), idx.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                                    B, S, Skv, H, G, D, dv, idx.shape[-1], scale, _lib.DTYPE_MXFP8, qs.data_ptr(),
+                                    ks.data_ptr(), 0), "dsa_sparse_mla_fwd(mxfp8)")
+    return out, lse
+
+
+@pytest.mark.parametrize("B,S,H,D,DV,G,K", [
+    (1, 128, 32, 128, 64, 1, 64),
+    (2, 64, 64, 128, 64, 2, 48),
+    (1, 80, 32, 192, 128, 1, 64),
+    (1, 48, 96, 576, 512, 1, 64),
+])
+def test_mxfp8_exact_path_and_fallback(dev, B, S, H, D, DV, G, K):
+    """Power-of-two block scales: the call dequantises kv exactly and runs the
+    bf16 kernel (q converted at load); its output matches the block-scaled
+    kernel's up to the order of the fp32 score sums.  One scale that is not a
+    power of two sends the same call to the block-scaled kernel, whose result
+    then equals the no-workspace call's bit for bit."""
+    q8, qs, kv8, ks, idx = (t.to(dev) for t in _inputs(B, S, H, D, G, K, seed=D + H))
+    scale = D ** -0.5
+    out, lse = sparse_mla_blockscaled_mxfp8_fwd_interface(q8, kv8, qs, ks, idx, sm_scale=scale, d_v=DV)
+    ob, lb = _mx_fwd_blockscaled_only(q8, kv8, qs, ks, idx, scale, DV)
+    ref_scale = float(ob.float().abs().max())
+    assert float((out.float() - ob.float()).abs().max()) <= 2 ** -7 * ref_scale
+    assert float((lse - lb).abs().max()) <= 1e-4 * float(lb.abs().max())
+    ro, rl = orc.sparse_mla_fwd_mxfp8(q8.cpu(), kv8.cpu(), qs.cpu(), ks.cpu(), idx.cpu(), scale, DV)
+    assert_close(out, ro, what="exact-path out")
+    assert_close(lse, rl, what="exact-path lse2")
+    for which in ("kv", "q"):   # one scale off the power-of-two grid: the block-scaled kernel
+        qs2, ks2 = qs.clone(), ks.clone()
+        (ks2 if which == "kv" else qs2).view(-1)[5] *= 1.5
+        o2, l2 = sparse_mla_blockscaled_mxfp8_fwd_interface(q8, kv8, qs2, ks2, idx, sm_scale=scale, d_v=DV)
+        ob2, lb2 = _mx_fwd_blockscaled_only(q8, kv8, qs2, ks2, idx, scale, DV)
+        assert torch.equal(o2, ob2) and torch.equal(l2, lb2), which
+
+
+def test_mxfp8_path_choice_in_a_graph(dev):
+    """The path is chosen on the device at every replay: a captured call
+    follows in-place changes of the block scales between replays."""
+    B, S, H, D, DV, G, K = 1, 96, 32, 128, 64, 1, 48
+    q8, qs, kv8, ks, idx = (t.to(dev) for t in _inputs(B, S, H, D, G, K, seed=7))
+    scale = D ** -0.5
+    ks_pow2 = ks.clone()
+    ks_odd = ks.clone()
+    ks_odd.view(-1)[3] *= 1.25
+    eager = {}
+    for name, k in (("pow2", ks_pow2), ("odd", ks_odd)):
+        ks.copy_(k)
+        eager[name] = [t.clone() for t in sparse_mla_blockscaled_mxfp8_fwd_interface(q8, kv8, qs, ks, idx,
+                                                                                      sm_scale=scale, d_v=DV)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        sparse_mla_blockscaled_mxfp8_fwd_interface(q8, kv8, qs, ks, idx, sm_scale=scale, d_v=DV)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        res = sparse_mla_blockscaled_mxfp8_fwd_interface(q8, kv8, qs, ks, idx, sm_scale=scale, d_v=DV)
+    for name in ("pow2", "odd", "pow2", "odd"):
+        ks.copy_(ks_pow2 if name == "pow2" else ks_odd)
+        torch.zeros(1 << 20, device=dev).sum().item()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(res[0], eager[name][0]) and torch.equal(res[1], eager[name][1]), name
 
 
 def test_mxfp8_dequantize_bit_exact(dev):
