@@ -510,15 +510,16 @@ extern "C" int dsa_indexer_scores_masked(const void *q, const void *w, const voi
 namespace dsa {
 
 // out_scores[b, r0 + t, j] = scratch[b][t][idx] for the chunk's picks (-inf for -1 padding)
+// scratch rows are `pitch` scores wide (the chunk's key range)
 __global__ void __launch_bounds__(256) gather_topk_scores_kernel(const float *scratch, const int32_t *idx,
                                                                  float *out, int64_t B, int64_t Sq, int64_t rows,
-                                                                 int64_t r0, int64_t Sk, int64_t topk) {
+                                                                 int64_t r0, int64_t pitch, int64_t topk) {
   const int64_t e = blockIdx.x * 256ll + threadIdx.x;
   if (e >= B * rows * topk) return;
   const int64_t j = e % topk, t = (e / topk) % rows, b = e / (topk * rows);
   const int64_t o = (b * Sq + r0 + t) * topk + j;
   const int32_t c = idx[o];
-  out[o] = (c >= 0 && c < Sk) ? scratch[(b * rows + t) * Sk + c] : -INFINITY;
+  out[o] = (c >= 0 && c < pitch) ? scratch[(b * rows + t) * pitch + c] : -INFINITY;
 }
 
 static int64_t stream_chunk_rows(int64_t B, int64_t Sq, int64_t Sk, size_t workspace_bytes) {
@@ -526,6 +527,23 @@ static int64_t stream_chunk_rows(int64_t B, int64_t Sq, int64_t Sk, size_t works
   int64_t cr = per_row > 0 ? (int64_t)(workspace_bytes / (size_t)per_row) : 0;
   if (cr > Sq) cr = Sq;
   return cr;
+}
+
+// Scores of a chunk of query rows [r0, r0 + rows) need keys [0, pitch): all Sk
+// keys, or with causal rows only up to the chunk's last query position.
+static int64_t stream_pitch(int64_t r0, int64_t rows, int64_t Sk, bool causal) {
+  return causal && r0 + rows < Sk ? r0 + rows : Sk;
+}
+// Most rows from r0 whose [B, rows, pitch] scores fit the workspace (at least
+// one when a full-width row does; rows * pitch only grows with rows).
+static int64_t stream_next_rows(int64_t B, int64_t Sq, int64_t Sk, int64_t r0, bool causal, size_t bytes) {
+  int64_t lo = 1, hi = Sq - r0;
+  while (lo < hi) {
+    const int64_t mid = lo + (hi - lo + 1) / 2;
+    if ((size_t)(B * mid * stream_pitch(r0, mid, Sk, causal) * 4) <= bytes) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
 }
 
 }  // namespace dsa
@@ -555,24 +573,26 @@ extern "C" int dsa_indexer_topk_streaming(const void *q, const void *w, const vo
   float *scratch = static_cast<float *>(workspace);
   const int64_t elt = dtype == DSA_DTYPE_E4M3 ? 1 : 2;
   const int64_t welt = w_dtype == DSA_DTYPE_F32 ? 4 : 2;
-  for (int64_t r0 = 0; r0 < Sq; r0 += cr) {
-    const int64_t rows = Sq - r0 < cr ? Sq - r0 : cr;
-    // query rows [r0, r0 + rows): q / w start r0 tokens in; causal keys s <= r0 + t
+  for (int64_t r0 = 0, rows = 0; r0 < Sq; r0 += rows) {
+    // query rows [r0, r0 + rows): q / w start r0 tokens in; causal keys s <= r0 + t,
+    // so a causal chunk's scratch rows span only keys [0, r0 + rows) and early
+    // chunks take more rows
+    rows = stream_next_rows(B, Sq, Sk, r0, causal != 0, workspace_bytes);
+    const int64_t pitch = stream_pitch(r0, rows, Sk, causal != 0);
     const unsigned char *qc = static_cast<const unsigned char *>(q) + r0 * B * H * D * elt;
     const unsigned char *wc = static_cast<const unsigned char *>(w) + r0 * B * H * welt;
-    int rc = indexer_scores_impl(qc, wc, k, scratch, B, rows, Sk, H, D, dtype, w_dtype, q_scale, k_scale,
+    int rc = indexer_scores_impl(qc, wc, k, scratch, B, rows, pitch, H, D, dtype, w_dtype, q_scale, k_scale,
                                  causal ? 2 : 0, nullptr, nullptr, nullptr, 0, use_relu, st,
                                  "dsa_indexer_topk_streaming", causal ? r0 : 0);
     if (rc) return rc;
-    for (int64_t b = 0; b < B; ++b) {
-      rc = dsa_topk(scratch + b * rows * Sk, rows, Sk, Sk, rows, causal, causal ? r0 : 0, nullptr, nullptr, topk,
-                    out_idx + (b * Sq + r0) * topk, stream);
-      if (rc) return rc;
-    }
+    // every batch's rows in one top-k launch (outputs Sq * topk apart)
+    rc = topk_batched(scratch, rows, B, pitch, pitch, causal, causal ? r0 : 0, topk, out_idx + r0 * topk,
+                      Sq * topk, st);
+    if (rc) return rc;
     if (out_scores) {
       const int64_t n = B * rows * topk;
       hipLaunchKernelGGL(gather_topk_scores_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, scratch,
-                         out_idx, out_scores, B, Sq, rows, r0, Sk, topk);
+                         out_idx, out_scores, B, Sq, rows, r0, pitch, topk);
       rc = check_launch("indexer_topk_streaming(gather)");
       if (rc) return rc;
     }

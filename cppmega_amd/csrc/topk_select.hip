@@ -29,7 +29,17 @@ struct TopkParams {
   int causal;
   int topk;
   int32_t *out;
+  // 0: output rows are contiguous; else the output of row r is at
+  // out + (r / seq_q) * out_bstride + (r % seq_q) * topk (batches of seq_q rows
+  // whose outputs sit out_bstride elements apart)
+  int64_t out_bstride;
 };
+
+__device__ __forceinline__ int32_t *topk_out_row(const TopkParams &p, int64_t row) {
+  if (p.out_bstride == 0) return p.out + row * p.topk;
+  const int64_t b = row / p.seq_q;
+  return p.out + b * p.out_bstride + (row - b * p.seq_q) * p.topk;
+}
 
 __device__ __forceinline__ uint32_t score_key(float f) {
   uint32_t u = __float_as_uint(f);
@@ -243,7 +253,7 @@ topk_wave_kernel(const TopkParams p) {
   if (st < 0) st = 0;
   if (en > p.row_len) en = p.row_len;
   const int n = __builtin_amdgcn_readfirstlane(en > st ? (int)(en - st) : 0);
-  int32_t *orow = p.out + row * p.topk;
+  int32_t *orow = topk_out_row(p, row);
   if (n <= p.topk) {
     for (int i = lane; i < p.topk; i += 64) orow[i] = i < n ? (int32_t)(st + i) : -1;
     return;
@@ -607,7 +617,7 @@ __global__ void __launch_bounds__(64 * NW) topk_block_kernel(const TopkParams p)
   if (st < 0) st = 0;
   if (en > p.row_len) en = p.row_len;
   const int n = __builtin_amdgcn_readfirstlane(en > st ? (int)(en - st) : 0);
-  int32_t *orow = p.out + row * p.topk;
+  int32_t *orow = topk_out_row(p, row);
   if (n <= p.topk) {  // block-uniform: the whole workgroup leaves together
     for (int i = tid; i < p.topk; i += 64 * NW) orow[i] = i < n ? (int32_t)(st + i) : -1;
     return;
@@ -923,6 +933,43 @@ static int launch_topk_wave(const TopkParams &p, hipStream_t st) {
 
 using namespace dsa;
 
+namespace dsa {
+static int topk_run(const TopkParams &p, hipStream_t st) {
+  if (p.row_len <= 2048) return launch_topk_wave<32>(p, st);
+  if (p.row_len <= 4096) return launch_topk_wave<64>(p, st);
+  if (p.row_len <= 8192) return launch_topk_wave<128>(p, st);
+  if (p.row_len <= 16384) return launch_topk_block<4, 64>(p, st);
+  if (p.row_len <= 32768) return launch_topk_block<8, 64>(p, st);
+  return set_error(DSA_ERR_UNSUPPORTED, "dsa_topk: rows longer than 32768 columns are not supported (got %lld)",
+                   (long long)p.row_len);
+}
+
+// nbatch batches of rows_per_batch rows (scores rows consecutive, row_stride
+// apart), causal windows [0, t + 1 + causal_offset) for row t of a batch, and
+// the outputs of batch b from out + b * out_bstride: one launch for all batches.
+int topk_batched(const float *scores, int64_t rows_per_batch, int64_t nbatch, int64_t row_len, int64_t row_stride,
+                 int causal, int64_t causal_offset, int64_t topk, int32_t *out, int64_t out_bstride,
+                 hipStream_t st) {
+  DSA_REQUIRE(rows_per_batch > 0 && nbatch > 0 && row_len >= 0 && row_stride >= row_len && topk > 0 &&
+                  topk < (1ll << 30) && rows_per_batch * nbatch < (1ll << 31),
+              "topk_batched: bad dims");
+  TopkParams p;
+  p.scores = scores;
+  p.rows = rows_per_batch * nbatch;
+  p.row_len = row_len;
+  p.row_stride = row_stride;
+  p.seq_q = rows_per_batch;
+  p.causal_offset = causal_offset;
+  p.starts = nullptr;
+  p.ends = nullptr;
+  p.causal = causal;
+  p.topk = (int)topk;
+  p.out = out;
+  p.out_bstride = out_bstride;
+  return topk_run(p, st);
+}
+}  // namespace dsa
+
 extern "C" int dsa_topk(const float *scores, int64_t rows, int64_t row_len, int64_t row_stride, int64_t seq_q,
                         int causal, int64_t causal_offset, const int32_t *starts, const int32_t *ends,
                         int64_t topk, int32_t *out_idx, void *stream) {
@@ -947,12 +994,6 @@ extern "C" int dsa_topk(const float *scores, int64_t rows, int64_t row_len, int6
   p.causal = causal;
   p.topk = (int)topk;
   p.out = out_idx;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (row_len <= 2048) return launch_topk_wave<32>(p, st);
-  if (row_len <= 4096) return launch_topk_wave<64>(p, st);
-  if (row_len <= 8192) return launch_topk_wave<128>(p, st);
-  if (row_len <= 16384) return launch_topk_block<4, 64>(p, st);
-  if (row_len <= 32768) return launch_topk_block<8, 64>(p, st);
-  return set_error(DSA_ERR_UNSUPPORTED, "dsa_topk: rows longer than 32768 columns are not supported (got %lld)",
-                   (long long)row_len);
+  p.out_bstride = 0;
+  return topk_run(p, static_cast<hipStream_t>(stream));
 }
