@@ -530,7 +530,7 @@ def main():
     side = side_stream(dev)
 
     def step(record):
-        marks = [torch.cuda.Event(enable_timing=True) for _ in range(7)] if record else None
+        marks = [torch.cuda.Event(enable_timing=True) for _ in range(8)] if record else None
         if record:
             marks[0].record()
         scores = index_scores(iq, iw, ik, use_relu=True, causal=CAUSAL_LOWER)
@@ -547,6 +547,9 @@ def main():
         inv = build_inverse_index(q, kv, idx, D_V, stream=side)
         if record:
             marks[6].record(side)
+            # the forward's own start: the side-stream launches above may leave the
+            # main stream idle while the host issues them
+            marks[7].record()
         out, lse = sparse_mla_fwd_interface(q, kv, idx, sm_scale=scale, d_v=D_V)
         if record:
             marks[3].record()
@@ -568,8 +571,8 @@ def main():
     wall = time.perf_counter() - t0
     _lib.stage_timing(False)
     for m in all_marks:
-        for i, k in enumerate(("indexer", "topk", "fwd", "bwd")):
-            ev[k].append(m[i].elapsed_time(m[i + 1]) / 1e3)
+        for k, (a, b) in zip(("indexer", "topk", "fwd", "bwd"), ((0, 1), (1, 2), (7, 3), (3, 4))):
+            ev[k].append(m[a].elapsed_time(m[b]) / 1e3)
     for k in _lib.BWD_STAGES:
         ev["bwd_" + k] = []
     for back in range(args.steps):
