@@ -632,7 +632,7 @@ static BwdPlan bwd_plan(int64_t B, int64_t S, int64_t H, int64_t G, int64_t D_qk
 // dsa_sparse_mla_bwd_build_index filled ahead of the call.
 struct BwdWorkspace {
   size_t partials, pexp, carry, rows_total;          // offsets in the rows section
-  size_t mask, base, dup, tot, rowptr, pos_of, index_total;  // offsets in the index section
+  size_t mask, base, dup, dupc, tot, rowptr, pos_of, index_total;  // offsets in the index section
   size_t total;                                      // rows section + index section
   BwdPlan plan;
 };
@@ -660,7 +660,12 @@ static BwdWorkspace bwd_layout(int64_t B, int64_t S, int64_t S_kv, int64_t H, in
   off += align256((size_t)pl.nb * pl.NC * R * 4);
   L.base = off;
   off += align256((size_t)pl.nb * pl.NC * R * 4);
+  // row parts per chunk: a pass with fewer chunks takes more parts, at most
+  // max(16, R / 16384 rounded up)
+  const int64_t spl_max = (R + 16383) / 16384 > 16 ? (R + 16383) / 16384 : 16;
   L.dup = off;
+  off += align256((size_t)pl.nb * pl.NC * spl_max * 4);
+  L.dupc = off;
   off += align256((size_t)pl.nb * pl.NC * 4);
   L.tot = off;
   off += align256((size_t)pl.nb * R * 4);
@@ -680,12 +685,13 @@ static int64_t bwd_passes(const BwdPlan &pl, int64_t B) {
 // The inverse index of one pass (tokens [T0, T0 + nbp * ctp) of the flattened
 // [B * S]) in the index section ix.
 static CsrParams bwd_csr_params(const int32_t *indices, const BwdWorkspace &L, unsigned char *ix, int64_t T0,
-                                int64_t ctp, int64_t S_kv, int64_t G, int64_t topk, bool wide) {
+                                int64_t nbp, int64_t ctp, int64_t S_kv, int64_t G, int64_t topk, bool wide) {
   CsrParams cp;
   cp.idx = indices + T0 * G * topk;
   cp.mask = reinterpret_cast<uint32_t *>(ix + L.mask);
   cp.base = reinterpret_cast<int32_t *>(ix + L.base);
   cp.dup = reinterpret_cast<int32_t *>(ix + L.dup);
+  cp.dupc = reinterpret_cast<int32_t *>(ix + L.dupc);
   cp.tot = reinterpret_cast<int32_t *>(ix + L.tot);
   cp.rowptr = reinterpret_cast<int32_t *>(ix + L.rowptr);
   cp.pos_of = reinterpret_cast<int32_t *>(ix + L.pos_of);
@@ -695,6 +701,8 @@ static CsrParams bwd_csr_params(const int32_t *indices, const BwdWorkspace &L, u
   cp.topk = topk;
   cp.R = S_kv * G;
   cp.NC = csr_chunks(ctp);
+  cp.SPL = csr_split((int64_t)cp.NC * nbp, cp.R);
+  cp.RP = (cp.R + cp.SPL - 1) / cp.SPL;
   cp.dup_only = wide ? 0 : 1;  // the narrow main kernel derives the positions of chunks without repeats
   return cp;
 }
@@ -764,7 +772,6 @@ static int bwd_check(const char *fn, int64_t B, int64_t S, int64_t S_kv, int64_t
   const int64_t ntiles = (H / G + 31) / 32;
   DSA_REQUIRE(entries < (1ll << 31) && B * R < (1ll << 31) && entries * ntiles < (1ll << 40),
               "%s: too many entries for int32 CSR keys", fn);
-  DSA_REQUIRE(R <= 32768, "%s: S_kv * G = %lld exceeds the 32768 rows one LDS histogram holds", fn, (long long)R);
   DSA_REQUIRE(S_kv * G * D_qk * 2 < (1ll << 32), "%s: kv rows of one batch exceed 4 GiB", fn);
   const bool f8 = dtype == DSA_DTYPE_E4M3;
   const bool shape_ok = (D_qk == 128 && D_v == 64) || (D_qk == 128 && D_v == 128) || (D_qk == 192 && D_v == 128) ||
@@ -803,7 +810,7 @@ static int bwd_run(const void *q, const void *kv, const void *o, const void *dO,
     const int mode = pl.npb == 1 ? 0 : (ps % pl.npb == 0 ? 1 : (ps % pl.npb == pl.npb - 1 ? 3 : 2));
     const bool timed = npass == 1;
 
-    const CsrParams cp = bwd_csr_params(indices, L, ix, T0, ctp, S_kv, G, topk, wide);
+    const CsrParams cp = bwd_csr_params(indices, L, ix, T0, nbp, ctp, S_kv, G, topk, wide);
     int rc = DSA_OK;
     if (!index_ready) {
       rc = launch_csr(cp, nbp, st);
@@ -825,7 +832,7 @@ static int bwd_run(const void *q, const void *kv, const void *o, const void *dO,
     p.pos_of = cp.pos_of;
     p.mask = cp.mask;
     p.base = cp.base;
-    p.dup = cp.dup;
+    p.dup = cp.dupc;
     p.R = cp.R;
     p.rowptr = cp.rowptr;
     p.NC = cp.NC;
@@ -920,7 +927,7 @@ extern "C" int dsa_sparse_mla_bwd_build_index(const int32_t *indices, int64_t B,
   if (!index || index_bytes < L.index_total)
     return set_error(DSA_ERR_WORKSPACE, "dsa_sparse_mla_bwd_build_index: index buffer %zu < required %zu",
                      index_bytes, L.index_total);
-  const CsrParams cp = bwd_csr_params(indices, L, static_cast<unsigned char *>(index), 0, S, S_kv, G, topk,
+  const CsrParams cp = bwd_csr_params(indices, L, static_cast<unsigned char *>(index), 0, B, S, S_kv, G, topk,
                                       wide_shape(D_qk, D_v));
   return launch_csr(cp, B, static_cast<hipStream_t>(stream));
 }

@@ -11,15 +11,20 @@ namespace dsa {
 // ---------------------------------------------------------------------------
 // Entry e = ((b*S + t)*G + g)*topk + slot; its row (within batch b) is
 // r = j*G + g for a valid index j.  Tokens are grouped into chunks of 32
-// within one batch (NC chunks per batch).
+// within one batch (NC chunks per batch), and a chunk's rows into SPL parts
+// of RP consecutive rows (one workgroup each, so a chunk's LDS holds RP words
+// and short token ranges with long rows still fill the GPU).
 //   csr_mask     mask[b][c][r]  = bit tl set when token 32c + tl references
-//                                 row r; dup[b][c] = some (token, group)
-//                                 references one row twice, and then the exact
-//                                 counts go to base[b][c][r] (a bit cannot
-//                                 count repeats); count(c, r) below is that
-//                                 count or popcount(mask)
+//                                 row r; dup[b][c][part] = some (token, group)
+//                                 references one row of the part twice, and
+//                                 then the exact counts of the part's rows go
+//                                 to base[b][c][r] (a bit cannot count
+//                                 repeats); count(c, r) below is that count
+//                                 or popcount(mask)
 //   csr_colscan  base[b][c][r]  = entries of row r in the chunks before c
-//                                 (exclusive prefix over chunks), tot = row total
+//                                 (exclusive prefix over chunks), tot = row
+//                                 total; dupc[b][c] = any part of chunk c has
+//                                 a repeat
 //   csr_scan     rowptr         = exclusive prefix of tot
 //   csr_scatter  pos_of[e]      = rowptr + base + popcount of the earlier
 //                                 tokens' bits: entries of a row in ascending
@@ -36,50 +41,71 @@ struct CsrParams {
   const int32_t *idx;
   uint32_t *mask;   // [B][NC][R]
   int32_t *base;    // [B][NC][R]
-  int32_t *dup;     // [B][NC]
+  int32_t *dup;     // [B][NC][SPL]: the part's rows hold a repeat
+  int32_t *dupc;    // [B][NC]: some part of the chunk does
   int32_t *tot;     // [B*R]
   int32_t *rowptr;  // [B*R + 1]
   int32_t *pos_of;  // [entries]: CSR position of each entry, -1 for a masked slot
   int64_t S, S_kv, G, topk;
   int64_t R;        // rows per batch = S_kv * G
   int NC;           // chunks per batch
+  int SPL;          // row parts per chunk
+  int64_t RP;       // rows per part (the last part may hold fewer)
   int dup_only;     // scatter only the chunks with repeats (the main kernel places the rest)
 };
+
+// Row parts per chunk: enough that a part's rows fit 64 KiB of LDS, and up to
+// 16 when the chunks alone (nchunks over all batches) leave the GPU idle.
+static int csr_split(int64_t nchunks, int64_t R) {
+  int64_t spl = (R + 16383) / 16384;
+  int64_t want = nchunks >= 256 ? 1 : (256 + nchunks - 1) / (nchunks > 0 ? nchunks : 1);
+  want = want < 16 ? want : 16;
+  spl = spl > want ? spl : want;
+  return (int)(spl < R ? spl : (R > 0 ? R : 1));
+}
 
 __global__ void fill_i32_kernel(int32_t *p, int64_t n, int32_t v) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
     p[i] = v;
 }
 
-// grid (NC, B), 256 threads, dynamic LDS = R words
-__global__ void __launch_bounds__(256) csr_mask_kernel(const CsrParams p) {
+// grid (NC * SPL, B), kMaskThreads threads, dynamic LDS = RP words: workgroup
+// (c, part) reads every index of chunk c and records the rows [r_lo, r_hi) of
+// its part.
+constexpr int kMaskThreads = 1024;
+__global__ void __launch_bounds__(kMaskThreads) csr_mask_kernel(const CsrParams p) {
   extern __shared__ uint32_t mk[];
   __shared__ int dflag;
-  const int c = blockIdx.x;
+  const int c = blockIdx.x / p.SPL, part = blockIdx.x % p.SPL;
   const int64_t b = blockIdx.y;
   const int tid = threadIdx.x;
-  for (int64_t r = tid; r < p.R; r += 256) mk[r] = 0u;
+  // parts past the last row (RP * SPL may exceed R) hold no rows
+  const int64_t r_lo = part * p.RP, r_hi = r_lo + p.RP < p.R ? r_lo + p.RP : p.R;
+  const uint32_t nr = r_hi > r_lo ? (uint32_t)(r_hi - r_lo) : 0u;
+  for (int64_t r = tid; r < nr; r += kMaskThreads) mk[r] = 0u;
   if (tid == 0) dflag = 0;
   __syncthreads();
   const int64_t t0 = (int64_t)c * kChunkTokens;
   const int64_t t1 = t0 + kChunkTokens < p.S ? t0 + kChunkTokens : p.S;
   const int64_t nseg = (t1 - t0) * p.G;
   const int32_t *seg_idx = p.idx + ((b * p.S + t0) * p.G) * p.topk;
-  // work item w = (segment w / spt, slots 256 (w % spt) + tid): block-uniform,
-  // eight loads in flight
+  // work item w = (segment w / spt, slots 256 (w % spt) + sl), taken by the
+  // thread group ig = w % IG of 256 threads; a round issues U loads per thread
+  // (U * IG work items) before any is used
+  constexpr int IG = kMaskThreads / 256;
+  const int sl = tid & 255, ig = tid >> 8;
   const int spt = (int)((p.topk + 255) / 256);
   const int nw = (int)nseg * spt;
   const int G = (int)p.G;
   int dup = 0;
-  // all of a 32-token chunk's index loads (at topk <= 256) go out together:
-  // unconditional bounded loads, invalid work items land past the resource
-  constexpr int U = 32;
+  // unconditional bounded loads: invalid work items land past the resource
+  constexpr int U = 16;
   const auto seg_rs = make_buffer_rsrc(seg_idx, (uint32_t)(nseg * p.topk * 4));
-  for (int w0 = 0; w0 < nw; w0 += U) {
+  for (int w0 = 0; w0 < nw; w0 += U * IG) {
     int32_t j[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int w = w0 + u, sg = spt == 1 ? w : w / spt, s = (spt == 1 ? 0 : w % spt) * 256 + tid;
+      const int w = w0 + u * IG + ig, sg = spt == 1 ? w : w / spt, s = (spt == 1 ? 0 : w % spt) * 256 + sl;
       const bool ok = w < nw && s < p.topk;
       const uint32_t off = ok ? (uint32_t)((sg * p.topk + s) * 4) : 0xffffffffu;
       const int32_t v = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(seg_rs, (int)off, 0, 0);
@@ -87,42 +113,43 @@ __global__ void __launch_bounds__(256) csr_mask_kernel(const CsrParams p) {
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int w = w0 + u, sg = spt == 1 ? w : w / spt;
-      if (j[u] >= 0 && j[u] < p.S_kv) {
+      const int w = w0 + u * IG + ig, sg = spt == 1 ? w : w / spt;
+      // rows of other parts (and invalid indices) fail the unsigned range test
+      const uint32_t rr = (uint32_t)((int64_t)j[u] * G + (G == 1 ? 0 : sg % G) - r_lo);
+      if (j[u] >= 0 && j[u] < p.S_kv && rr < nr) {
         const uint32_t bit = 1u << (G == 1 ? sg : sg / G);
-        const uint32_t old = atomicOr(&mk[(int64_t)j[u] * G + (G == 1 ? 0 : sg % G)], bit);
+        const uint32_t old = atomicOr(&mk[rr], bit);
         dup |= (old & bit) != 0u;
       }
     }
   }
   if (dup) dflag = 1;  // benign race: every writer stores 1
   __syncthreads();
-  uint32_t *m = p.mask + (b * p.NC + c) * p.R;
-  for (int64_t r = tid; r < p.R; r += 256) m[r] = mk[r];
-  if (tid == 0) p.dup[b * p.NC + c] = dflag;
-  if (dflag) {  // block-uniform: exact per-row counts of this chunk
+  uint32_t *m = p.mask + (b * p.NC + c) * p.R + r_lo;
+  for (int64_t r = tid; r < nr; r += kMaskThreads) m[r] = mk[r];
+  if (tid == 0) p.dup[(b * p.NC + c) * p.SPL + part] = dflag;
+  if (dflag) {  // block-uniform: exact per-row counts of this part's rows
     __syncthreads();
     int32_t *cnt = reinterpret_cast<int32_t *>(mk);
-    for (int64_t r = tid; r < p.R; r += 256) cnt[r] = 0;
+    for (int64_t r = tid; r < nr; r += kMaskThreads) cnt[r] = 0;
     __syncthreads();
-    for (int64_t sg = 0; sg < nseg; ++sg) {
-      const int64_t g = sg % p.G;
-      for (int64_t s = tid; s < p.topk; s += 256) {
-        const int32_t j = seg_idx[sg * p.topk + s];
-        if (j >= 0 && j < p.S_kv) atomicAdd(&cnt[j * p.G + g], 1);
-      }
+    for (int64_t e = tid; e < nseg * p.topk; e += kMaskThreads) {
+      const int64_t g = (e / p.topk) % p.G;
+      const int32_t j = seg_idx[e];
+      const uint32_t rr = (uint32_t)(j * p.G + g - r_lo);
+      if (j >= 0 && j < p.S_kv && rr < nr) atomicAdd(&cnt[rr], 1);
     }
     __syncthreads();
-    int32_t *dst = p.base + (b * p.NC + c) * p.R;
-    for (int64_t r = tid; r < p.R; r += 256) dst[r] = cnt[r];
+    int32_t *dst = p.base + (b * p.NC + c) * p.R + r_lo;
+    for (int64_t r = tid; r < nr; r += kMaskThreads) dst[r] = cnt[r];
   }
 }
 
 // Entries of row r in chunk c of batch b (mask popcount, or the exact count
 // the mask kernel left in base[] for a chunk with repeats).
-__device__ __forceinline__ int32_t chunk_count(const CsrParams &p, int64_t b, int c, int64_t r) {
+__device__ __forceinline__ int32_t chunk_count(const CsrParams &p, int64_t b, int c, int64_t r, int part) {
   const int64_t cell = (b * p.NC + c) * p.R + r;
-  return p.dup[b * p.NC + c] ? p.base[cell] : (int32_t)__popc(p.mask[cell]);
+  return p.dup[(b * p.NC + c) * p.SPL + part] ? p.base[cell] : (int32_t)__popc(p.mask[cell]);
 }
 
 // grid (ceil(R / 64), B), 16 waves: lane = row, wave w = a contiguous
@@ -140,12 +167,20 @@ __global__ void __launch_bounds__(64 * kScanWaves) csr_colscan_kernel(const CsrP
   const int64_t b = blockIdx.y;
   const int64_t r = (int64_t)blockIdx.x * 64 + lane;
   const bool rok = r < p.R;
+  const int part = rok ? (int)(r / p.RP) : 0;
   const int c_lo = (int)((int64_t)p.NC * w / kScanWaves), c_hi = (int)((int64_t)p.NC * (w + 1) / kScanWaves);
+  if (blockIdx.x == 0) {  // the chunks' combined repeat flags (read by the scatter and the main kernel)
+    for (int c = threadIdx.x; c < p.NC; c += 64 * kScanWaves) {
+      int any = 0;
+      for (int q = 0; q < p.SPL; ++q) any |= p.dup[(b * p.NC + c) * p.SPL + q];
+      p.dupc[b * p.NC + c] = any;
+    }
+  }
   int32_t v[TILE];
   int32_t s = 0;
   for (int c0 = c_lo; c0 < c_hi; c0 += TILE) {
 #pragma unroll
-    for (int u = 0; u < TILE; ++u) v[u] = (c0 + u < c_hi && rok) ? chunk_count(p, b, c0 + u, r) : 0;
+    for (int u = 0; u < TILE; ++u) v[u] = (c0 + u < c_hi && rok) ? chunk_count(p, b, c0 + u, r, part) : 0;
 #pragma unroll
     for (int u = 0; u < TILE; ++u) s += v[u];
   }
@@ -162,7 +197,7 @@ __global__ void __launch_bounds__(64 * kScanWaves) csr_colscan_kernel(const CsrP
   for (int c0 = c_lo; c0 < c_hi; c0 += TILE) {
     if (!one_tile) {
 #pragma unroll
-      for (int u = 0; u < TILE; ++u) v[u] = (c0 + u < c_hi && rok) ? chunk_count(p, b, c0 + u, r) : 0;
+      for (int u = 0; u < TILE; ++u) v[u] = (c0 + u < c_hi && rok) ? chunk_count(p, b, c0 + u, r, part) : 0;
     }
 #pragma unroll
     for (int u = 0; u < TILE; ++u) {
@@ -235,10 +270,14 @@ __global__ void __launch_bounds__(1024) csr_scan_kernel(const int32_t *cnt, int3
   if (tid == 0) rowptr[n] = carry;
 }
 
-// grid (NC, B), 256 threads; dynamic LDS = R ints (cursors of the serial path).
+// grid (NC * SPL, B), 256 threads; dynamic LDS = RP ints (cursors of the
+// serial path).  Chunks without repeats: the SPL workgroups of a chunk split
+// its entries, each entry placed independently.  A chunk with a repeat: each
+// part's workgroup walks the chunk's entries in order with one thread and
+// places those whose rows lie in its part.
 __global__ void __launch_bounds__(256) csr_scatter_kernel(const CsrParams p) {
   extern __shared__ int32_t cur[];
-  const int c = blockIdx.x;
+  const int c = blockIdx.x / p.SPL, part = blockIdx.x % p.SPL;
   const int64_t b = blockIdx.y;
   const int tid = threadIdx.x;
   const int64_t t0 = (int64_t)c * kChunkTokens;
@@ -248,20 +287,21 @@ __global__ void __launch_bounds__(256) csr_scatter_kernel(const CsrParams p) {
   const uint32_t *m = p.mask + (b * p.NC + c) * p.R;
   const int32_t *bs = p.base + (b * p.NC + c) * p.R;
   const int32_t *rp = p.rowptr + b * p.R;
-  if (p.dup[b * p.NC + c] == 0) {
+  if (p.dupc[b * p.NC + c] == 0) {
     if (p.dup_only) return;  // block-uniform
     // row r of (token t0 + tl, group g): position = base + earlier tokens of the chunk in r;
-    // work items as in the mask kernel, eight in flight
+    // work items as in the mask kernel, this part's share of them, eight in flight
     const int spt = (int)((p.topk + 255) / 256);
     const int nw = (int)nseg * spt;
+    const int w_lo = (int)((int64_t)nw * part / p.SPL), w_hi = (int)((int64_t)nw * (part + 1) / p.SPL);
     const int G = (int)p.G;
-    for (int w0 = 0; w0 < nw; w0 += 8) {
+    for (int w0 = w_lo; w0 < w_hi; w0 += 8) {
       int32_t j[8];
       int64_t e[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int w = w0 + u, sg = spt == 1 ? w : w / spt, s = (spt == 1 ? 0 : w % spt) * 256 + tid;
-        e[u] = (w < nw && s < p.topk) ? e_first + (int64_t)sg * p.topk + s : -1;
+        e[u] = (w < w_hi && s < p.topk) ? e_first + (int64_t)sg * p.topk + s : -1;
         j[u] = e[u] >= 0 ? p.idx[e[u]] : -1;
       }
       int32_t bv[8];
@@ -285,8 +325,11 @@ __global__ void __launch_bounds__(256) csr_scatter_kernel(const CsrParams p) {
       }
     }
   } else {
-    // a row repeats inside a (token, group): one thread walks the entries in order
-    for (int64_t r = tid; r < p.R; r += 256) cur[r] = rp[r] + bs[r];
+    // a row repeats inside a (token, group): one thread per part walks the
+    // entries in order (the part holding row 0 also marks the masked slots)
+    const int64_t r_lo = part * p.RP, r_hi = r_lo + p.RP < p.R ? r_lo + p.RP : p.R;
+    const uint32_t nr = r_hi > r_lo ? (uint32_t)(r_hi - r_lo) : 0u;
+    for (int64_t r = tid; r < nr; r += 256) cur[r] = rp[r_lo + r] + bs[r_lo + r];
     __syncthreads();
     if (tid == 0) {
       for (int64_t sg = 0; sg < nseg; ++sg) {
@@ -294,7 +337,12 @@ __global__ void __launch_bounds__(256) csr_scatter_kernel(const CsrParams p) {
         for (int64_t s = 0; s < p.topk; ++s) {
           const int64_t e = e_first + sg * p.topk + s;
           const int32_t j = p.idx[e];
-          p.pos_of[e] = (j >= 0 && j < p.S_kv) ? cur[j * p.G + g]++ : -1;
+          if (j >= 0 && j < p.S_kv) {
+            const uint32_t rr = (uint32_t)(j * p.G + g - r_lo);
+            if (rr < nr) p.pos_of[e] = cur[rr]++;
+          } else if (part == 0) {
+            p.pos_of[e] = -1;
+          }
         }
       }
     }
@@ -435,20 +483,14 @@ dkv_reduce_kernel(const int32_t *rowptr, const unsigned char *partials, const in
 static int csr_chunks(int64_t S) { return (int)((S + kChunkTokens - 1) / kChunkTokens); }
 
 static int launch_csr(const CsrParams &cp, int64_t B, hipStream_t st) {
-  const size_t lds = (size_t)cp.R * 4;
-  if (lds > 160 * 1024)
-    return set_error(DSA_ERR_UNSUPPORTED, "sparse_mla_bwd: inverse index needs %zu bytes of LDS", lds);
-  if (lds > 64 * 1024) {
-    if (hipFuncSetAttribute((const void *)csr_mask_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
-            hipSuccess ||
-        hipFuncSetAttribute((const void *)csr_scatter_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)lds) != hipSuccess)
-      return set_error(DSA_ERR_HIP, "sparse_mla_bwd: csr LDS attribute failed");
-  }
+  const size_t lds = (size_t)cp.RP * 4;
+  if (cp.SPL < 1 || cp.RP * cp.SPL < cp.R || lds > 64 * 1024 || (int64_t)cp.NC * cp.SPL >= (1ll << 31))
+    return set_error(DSA_ERR_UNSUPPORTED, "sparse_mla_bwd: inverse index split %d x %lld rows of %lld", cp.SPL,
+                     (long long)cp.RP, (long long)cp.R);
   const int64_t rows = B * cp.R;
-  const dim3 cgrid((unsigned)cp.NC, (unsigned)B);
+  const dim3 cgrid((unsigned)(cp.NC * cp.SPL), (unsigned)B);
   const dim3 sgrid((unsigned)((cp.R + 63) / 64), (unsigned)B);
-  hipLaunchKernelGGL(csr_mask_kernel, cgrid, dim3(256), lds, st, cp);
+  hipLaunchKernelGGL(csr_mask_kernel, cgrid, dim3(kMaskThreads), lds, st, cp);
   hipLaunchKernelGGL(csr_colscan_kernel, sgrid, dim3(64 * kScanWaves), 0, st, cp);
   hipLaunchKernelGGL(csr_scan_kernel, dim3(1), dim3(1024), 0, st, cp.tot, cp.rowptr, rows);
   hipLaunchKernelGGL(csr_scatter_kernel, cgrid, dim3(256), lds, st, cp);

@@ -155,7 +155,7 @@ size_t dsa_sparse_mla_bwd_workspace_size(int64_t B, int64_t S, int64_t S_kv,
  * for e4m3 inputs.  The work runs in passes over token ranges whose partial
  * rows fit the per-pass cap (dsa_sparse_mla_bwd_pass_bytes), so the workspace
  * is bounded; results are deterministic for a given cap.
- * Limits: S_kv * G <= 32768, B * S * G * topk < 2^31.
+ * Limits: B * S_kv * G < 2^31, B * S * G * topk < 2^31.
  */
 int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o,
                        const void *dO, const int32_t *indices,

@@ -258,3 +258,31 @@ def test_bwd_inverse_index_paths(dev, B, S, H, G, D, DV, topk, dup):
     assert_close(dkv, rdkv, what="dkv")
     dq2, dkv2 = sparse_mla_bwd(q, kv, out, do, idxd, lse, sm_scale=inp["scale"])
     assert torch.equal(dq, dq2) and torch.equal(dkv, dkv2)
+
+
+@pytest.mark.parametrize("S,G,S_kv,topk,dup", [
+    (64, 1, 40000, 256, False),    # more kv rows than one LDS histogram held (32768)
+    (40, 2, 20000, 128, True),     # 40000 rows over two groups, repeats in one row part
+    (16, 1, 270000, 64, False),    # rows split by LDS size (17 parts), not only to fill the GPU
+])
+def test_bwd_long_kv_rows(dev, S, G, S_kv, topk, dup):
+    """Backward with S_kv * G well past 32768 rows: the inverse index splits every
+    32-token chunk's rows into parts (one workgroup and one LDS slice each);
+    indices spread over the whole kv range, checked against the oracle and
+    bitwise repeatable."""
+    B, H, D, DV = 1, 32, 128, 64
+    inp = _inputs(B, S, H, D, DV, topk, G=G, seed=S_kv + S, S_kv=S_kv)
+    g = torch.Generator().manual_seed(S_kv)
+    idx = torch.stack([torch.rand((S, S_kv), generator=g).topk(topk, dim=-1).indices.sort(dim=-1).values
+                       for _ in range(G)], dim=1).to(torch.int32)[None]          # [1, S, G, topk]
+    if dup:
+        idx[0, 3, G - 1, :3] = idx[0, 3, G - 1, 0]
+        idx[0, S - 1, 0, 1] = idx[0, S - 1, 0, 0]
+    q, kv, idxd, do = inp["q"].to(dev), inp["kv"].to(dev), idx.contiguous().to(dev), inp["do"].to(dev)
+    out, lse = sparse_mla_fwd_interface(q, kv, idxd, sm_scale=inp["scale"], d_v=DV)
+    dq, dkv = sparse_mla_bwd(q, kv, out, do, idxd, lse, sm_scale=inp["scale"])
+    rdq, rdkv = orc.sparse_mla_bwd(inp["q"], inp["kv"], out.cpu(), inp["do"], idx, lse.cpu(), inp["scale"], DV)
+    assert_close(dq, rdq, what="dq")
+    assert_close(dkv, rdkv, what="dkv")
+    dq2, dkv2 = sparse_mla_bwd(q, kv, out, do, idxd, lse, sm_scale=inp["scale"])
+    assert torch.equal(dq, dq2) and torch.equal(dkv, dkv2)
