@@ -51,6 +51,8 @@ EXPORTED_SYMBOLS = (
     "dsa_indexer_topk_streaming_workspace_size",
     "dsa_indexer_topk_streaming",
     "dsa_topk",
+    "dsa_topk_workspace_size",
+    "dsa_topk_ws",
     "dsa_fp8_quantize_workspace_size",
     "dsa_fp8_tensorwise_quantize",
     "dsa_fp8_tensorwise_quantize_noalloc",
@@ -106,6 +108,9 @@ _SIGNATURES = {
                                                                          _i32, _i32, _c_void_p, _size_t, _c_void_p]),
     "dsa_topk": (_i32, [_c_void_p, _i64, _i64, _i64, _i64, _i32, _i64,
                         _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p]),
+    "dsa_topk_workspace_size": (_size_t, [_i64, _i64, _i64]),
+    "dsa_topk_ws": (_i32, [_c_void_p, _i64, _i64, _i64, _i64, _i32, _i64,
+                           _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _size_t, _c_void_p]),
     "dsa_fp8_quantize_workspace_size": (_size_t, []),
     "dsa_fp8_tensorwise_quantize": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p,
                                            _c_void_p, _size_t, _c_void_p]),

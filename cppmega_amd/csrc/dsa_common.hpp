@@ -306,7 +306,7 @@ int check_launch(const char *what);
 // Top-k over nbatch batches of rows in one launch (defined in topk_select.hip).
 int topk_batched(const float *scores, int64_t rows_per_batch, int64_t nbatch, int64_t row_len, int64_t row_stride,
                  int causal, int64_t causal_offset, int64_t topk, int32_t *out, int64_t out_bstride,
-                 hipStream_t st);
+                 void *ws, size_t ws_bytes, hipStream_t st);
 // Stage timing of multi-kernel entry points (no-ops unless dsa_stage_timing(1)).
 void stage_begin(hipStream_t st);
 void stage_mark(hipStream_t st);

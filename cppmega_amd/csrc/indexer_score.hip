@@ -522,25 +522,24 @@ __global__ void __launch_bounds__(256) gather_topk_scores_kernel(const float *sc
   out[o] = (c >= 0 && c < pitch) ? scratch[(b * rows + t) * pitch + c] : -INFINITY;
 }
 
-static int64_t stream_chunk_rows(int64_t B, int64_t Sq, int64_t Sk, size_t workspace_bytes) {
-  const int64_t per_row = B * Sk * 4;
-  int64_t cr = per_row > 0 ? (int64_t)(workspace_bytes / (size_t)per_row) : 0;
-  if (cr > Sq) cr = Sq;
-  return cr;
-}
-
 // Scores of a chunk of query rows [r0, r0 + rows) need keys [0, pitch): all Sk
 // keys, or with causal rows only up to the chunk's last query position.
 static int64_t stream_pitch(int64_t r0, int64_t rows, int64_t Sk, bool causal) {
   return causal && r0 + rows < Sk ? r0 + rows : Sk;
 }
-// Most rows from r0 whose [B, rows, pitch] scores fit the workspace (at least
-// one when a full-width row does; rows * pitch only grows with rows).
-static int64_t stream_next_rows(int64_t B, int64_t Sq, int64_t Sk, int64_t r0, bool causal, size_t bytes) {
+// Workspace of a chunk: its [B, rows, pitch] scores, then (rows over 32768
+// keys) the top-k's segment passes.
+static size_t stream_chunk_bytes(int64_t B, int64_t rows, int64_t pitch, int64_t topk) {
+  return (((size_t)(B * rows * pitch * 4) + 255) & ~(size_t)255) + dsa_topk_workspace_size(B * rows, pitch, topk);
+}
+// Most rows from r0 whose chunk fits the workspace (at least one when a
+// full-width row does; the need only grows with rows).
+static int64_t stream_next_rows(int64_t B, int64_t Sq, int64_t Sk, int64_t r0, bool causal, int64_t topk,
+                                size_t bytes) {
   int64_t lo = 1, hi = Sq - r0;
   while (lo < hi) {
     const int64_t mid = lo + (hi - lo + 1) / 2;
-    if ((size_t)(B * mid * stream_pitch(r0, mid, Sk, causal) * 4) <= bytes) lo = mid;
+    if (stream_chunk_bytes(B, mid, stream_pitch(r0, mid, Sk, causal), topk) <= bytes) lo = mid;
     else hi = mid - 1;
   }
   return lo;
@@ -564,11 +563,10 @@ extern "C" int dsa_indexer_topk_streaming(const void *q, const void *w, const vo
   DSA_REQUIRE(causal == 0 || causal == 1, "dsa_indexer_topk_streaming: causal must be 0 or 1");
   if (B == 0 || Sq == 0) return DSA_OK;
   DSA_REQUIRE(out_idx, "dsa_indexer_topk_streaming: null out_idx");
-  const int64_t cr = stream_chunk_rows(B, Sq, Sk, workspace_bytes);
-  if (!workspace || cr < 1)
+  if (!workspace || stream_chunk_bytes(B, 1, Sk, topk) > workspace_bytes)
     return set_error(DSA_ERR_WORKSPACE,
-                     "dsa_indexer_topk_streaming: workspace %zu bytes holds no score row (need >= %lld per query row)",
-                     workspace_bytes, (long long)(B * Sk * 4));
+                     "dsa_indexer_topk_streaming: workspace %zu bytes holds no score row (need >= %zu per query row)",
+                     workspace_bytes, stream_chunk_bytes(B, 1, Sk, topk));
   hipStream_t st = static_cast<hipStream_t>(stream);
   float *scratch = static_cast<float *>(workspace);
   const int64_t elt = dtype == DSA_DTYPE_E4M3 ? 1 : 2;
@@ -577,8 +575,9 @@ extern "C" int dsa_indexer_topk_streaming(const void *q, const void *w, const vo
     // query rows [r0, r0 + rows): q / w start r0 tokens in; causal keys s <= r0 + t,
     // so a causal chunk's scratch rows span only keys [0, r0 + rows) and early
     // chunks take more rows
-    rows = stream_next_rows(B, Sq, Sk, r0, causal != 0, workspace_bytes);
+    rows = stream_next_rows(B, Sq, Sk, r0, causal != 0, topk, workspace_bytes);
     const int64_t pitch = stream_pitch(r0, rows, Sk, causal != 0);
+    const size_t sbytes = ((size_t)(B * rows * pitch * 4) + 255) & ~(size_t)255;
     const unsigned char *qc = static_cast<const unsigned char *>(q) + r0 * B * H * D * elt;
     const unsigned char *wc = static_cast<const unsigned char *>(w) + r0 * B * H * welt;
     int rc = indexer_scores_impl(qc, wc, k, scratch, B, rows, pitch, H, D, dtype, w_dtype, q_scale, k_scale,
@@ -587,7 +586,7 @@ extern "C" int dsa_indexer_topk_streaming(const void *q, const void *w, const vo
     if (rc) return rc;
     // every batch's rows in one top-k launch (outputs Sq * topk apart)
     rc = topk_batched(scratch, rows, B, pitch, pitch, causal, causal ? r0 : 0, topk, out_idx + r0 * topk,
-                      Sq * topk, st);
+                      Sq * topk, static_cast<unsigned char *>(workspace) + sbytes, workspace_bytes - sbytes, st);
     if (rc) return rc;
     if (out_scores) {
       const int64_t n = B * rows * topk;

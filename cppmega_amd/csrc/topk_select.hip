@@ -33,7 +33,36 @@ struct TopkParams {
   // out + (r / seq_q) * out_bstride + (r % seq_q) * topk (batches of seq_q rows
   // whose outputs sit out_bstride elements apart)
   int64_t out_bstride;
+  // segment mode (nseg > 1, rows over one pass's reach): launch row v is
+  // segment v % nseg (columns [seg * seg_len, +seg_len)) of row v / nseg, whose
+  // window is cut to the segment; rows counts launch rows, and the output of
+  // launch row v is out + v * topk
+  int64_t seg_len;
+  int nseg;
 };
+
+// Launch row v: its scores row `row` and window [st, en) (clamped to the row
+// and, in segment mode, to the segment).
+__device__ __forceinline__ void topk_window(const TopkParams &p, int64_t v, int64_t &row, int64_t &st, int64_t &en) {
+  row = p.nseg > 1 ? v / p.nseg : v;
+  if (p.starts) {
+    st = p.starts[row];
+    en = p.ends[row];
+  } else if (p.causal) {
+    st = 0;
+    en = (int64_t)((uint64_t)row % (uint64_t)p.seq_q) + 1 + p.causal_offset;
+  } else {
+    st = 0;
+    en = p.row_len;
+  }
+  if (st < 0) st = 0;
+  if (en > p.row_len) en = p.row_len;
+  if (p.nseg > 1) {
+    const int64_t c0 = (v - row * p.nseg) * p.seg_len;
+    st = st > c0 ? st : c0;
+    en = en < c0 + p.seg_len ? en : c0 + p.seg_len;
+  }
+}
 
 __device__ __forceinline__ int32_t *topk_out_row(const TopkParams &p, int64_t row) {
   if (p.out_bstride == 0) return p.out + row * p.topk;
@@ -235,25 +264,14 @@ topk_wave_kernel(const TopkParams p) {
   __shared__ float s_list[4][64];
   // the wave index is uniform: make the row and everything derived from it scalar
   const int w = __builtin_amdgcn_readfirstlane(wave_id()), lane = lane_id();
-  const int64_t row = (int64_t)blockIdx.x * 4 + w;
-  if (row >= p.rows) return;
+  const int64_t vrow = (int64_t)blockIdx.x * 4 + w;
+  if (vrow >= p.rows) return;
   int *hist = s_hist[w];
   float *list = s_list[w];
-  int64_t st, en;
-  if (p.starts) {
-    st = p.starts[row];
-    en = p.ends[row];
-  } else if (p.causal) {
-    st = 0;
-    en = (int64_t)((uint64_t)row % (uint64_t)p.seq_q) + 1 + p.causal_offset;
-  } else {
-    st = 0;
-    en = p.row_len;
-  }
-  if (st < 0) st = 0;
-  if (en > p.row_len) en = p.row_len;
+  int64_t row, st, en;
+  topk_window(p, vrow, row, st, en);
   const int n = __builtin_amdgcn_readfirstlane(en > st ? (int)(en - st) : 0);
-  int32_t *orow = topk_out_row(p, row);
+  int32_t *orow = topk_out_row(p, vrow);
   if (n <= p.topk) {
     for (int i = lane; i < p.topk; i += 64) orow[i] = i < n ? (int32_t)(st + i) : -1;
     return;
@@ -602,22 +620,11 @@ __global__ void __launch_bounds__(64 * NW) topk_block_kernel(const TopkParams p)
   int *hist = sm.hist;
   const int w = __builtin_amdgcn_readfirstlane(wave_id()), lane = lane_id();
   const int tid = threadIdx.x;
-  const int64_t row = blockIdx.x;
-  int64_t st, en;
-  if (p.starts) {
-    st = p.starts[row];
-    en = p.ends[row];
-  } else if (p.causal) {
-    st = 0;
-    en = (int64_t)((uint64_t)row % (uint64_t)p.seq_q) + 1 + p.causal_offset;
-  } else {
-    st = 0;
-    en = p.row_len;
-  }
-  if (st < 0) st = 0;
-  if (en > p.row_len) en = p.row_len;
+  const int64_t vrow = blockIdx.x;
+  int64_t row, st, en;
+  topk_window(p, vrow, row, st, en);
   const int n = __builtin_amdgcn_readfirstlane(en > st ? (int)(en - st) : 0);
-  int32_t *orow = topk_out_row(p, row);
+  int32_t *orow = topk_out_row(p, vrow);
   if (n <= p.topk) {  // block-uniform: the whole workgroup leaves together
     for (int i = tid; i < p.topk; i += 64 * NW) orow[i] = i < n ? (int32_t)(st + i) : -1;
     return;
@@ -934,22 +941,160 @@ static int launch_topk_wave(const TopkParams &p, hipStream_t st) {
 using namespace dsa;
 
 namespace dsa {
+constexpr int64_t kTopkOnePass = 32768;  // the longest row (or segment) one kernel takes
+
+// One launch over rows (segment mode: segments) of up to kTopkOnePass columns.
 static int topk_run(const TopkParams &p, hipStream_t st) {
-  if (p.row_len <= 2048) return launch_topk_wave<32>(p, st);
-  if (p.row_len <= 4096) return launch_topk_wave<64>(p, st);
-  if (p.row_len <= 8192) return launch_topk_wave<128>(p, st);
-  if (p.row_len <= 16384) return launch_topk_block<4, 64>(p, st);
-  if (p.row_len <= 32768) return launch_topk_block<8, 64>(p, st);
-  return set_error(DSA_ERR_UNSUPPORTED, "dsa_topk: rows longer than 32768 columns are not supported (got %lld)",
-                   (long long)p.row_len);
+  const int64_t len = p.nseg > 1 ? p.seg_len : p.row_len;
+  if (len <= 2048) return launch_topk_wave<32>(p, st);
+  if (len <= 4096) return launch_topk_wave<64>(p, st);
+  if (len <= 8192) return launch_topk_wave<128>(p, st);
+  if (len <= 16384) return launch_topk_block<4, 64>(p, st);
+  if (len <= kTopkOnePass) return launch_topk_block<8, 64>(p, st);
+  return set_error(DSA_ERR_UNSUPPORTED, "dsa_topk: rows longer than %lld columns need a workspace (dsa_topk_ws)",
+                   (long long)kTopkOnePass);
+}
+
+// Rows longer than kTopkOnePass: nseg segments of seg_len columns each.  The
+// chosen set under the order (value descending, NaN as +inf, ties to the lower
+// column) restricted to a segment is contained in that segment's own top-k,
+// so the union of the segments' picks holds the row's top-k:
+//   1. segment mode: every segment's top-k columns, in column order (cand);
+//   2. topk_compact_kernel: per row the segments' valid picks concatenated in
+//      segment order (so still in column order) with their scores, and the
+//      row's window [0, total) for the next pass;
+//   3. one pass over those candidate rows (ties to the lower position are ties
+//      to the lower column), positions out;
+//   4. topk_map_kernel: positions back to columns.
+struct TopkLong {
+  int64_t nseg, seg_len, crow;  // crow = nseg * topk: candidate row length
+  size_t cand, cscore, ccol, starts, ends, pos, total;  // workspace offsets
+};
+
+static TopkLong topk_long_plan(int64_t rows, int64_t row_len, int64_t topk) {
+  TopkLong t;
+  t.nseg = (row_len + kTopkOnePass - 1) / kTopkOnePass;
+  t.seg_len = (row_len + t.nseg - 1) / t.nseg;
+  t.crow = t.nseg * topk;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += (bytes + 255) & ~(size_t)255;
+    return o;
+  };
+  t.cand = take((size_t)rows * t.crow * 4);
+  t.cscore = take((size_t)rows * t.crow * 4);
+  t.ccol = take((size_t)rows * t.crow * 4);
+  t.starts = take((size_t)rows * 4);
+  t.ends = take((size_t)rows * 4);
+  t.pos = take((size_t)rows * topk * 4);
+  t.total = off;
+  return t;
+}
+
+// One workgroup per row: the segments' valid picks (a segment of n window
+// columns yields min(n, topk), the rest of its output is -1 padding) packed
+// in segment order, with their scores.
+__global__ void __launch_bounds__(256) topk_compact_kernel(const TopkParams p, const int32_t *cand, float *cscore,
+                                                           int32_t *ccol, int32_t *starts2, int32_t *ends2) {
+  const int64_t row = blockIdx.x;
+  const int64_t crow = (int64_t)p.nseg * p.topk;
+  __shared__ int off[65];
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int sg = 0; sg < p.nseg; ++sg) {
+      int64_t r, st, en;
+      topk_window(p, row * p.nseg + sg, r, st, en);
+      const int64_t n = en > st ? en - st : 0;
+      off[sg] = run;
+      run += (int)(n < p.topk ? n : p.topk);
+    }
+    off[p.nseg] = run;
+    starts2[row] = 0;
+    ends2[row] = run;
+  }
+  __syncthreads();
+  const float *srow = p.scores + row * p.row_stride;
+  for (int64_t i = threadIdx.x; i < crow; i += 256) {
+    const int sg = (int)(i / p.topk), k = (int)(i - (int64_t)sg * p.topk);
+    const int dst = off[sg] + k;
+    if (dst < off[sg + 1]) {
+      const int32_t col = cand[row * crow + i];
+      cscore[row * crow + dst] = srow[col];
+      ccol[row * crow + dst] = col;
+    }
+  }
+}
+
+__global__ void topk_map_kernel(const TopkParams p, const int32_t *pos, const int32_t *ccol, int64_t crow) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= p.rows * p.topk) return;
+  const int64_t row = i / p.topk, k = i - row * p.topk;
+  const int32_t q = pos[i];
+  topk_out_row(p, row)[k] = q >= 0 ? ccol[row * crow + q] : -1;
+}
+
+// p: rows of p.row_len > kTopkOnePass columns (nseg / seg_len unset).
+static int topk_long(const TopkParams &p, void *ws, size_t ws_bytes, hipStream_t st) {
+  const TopkLong t = topk_long_plan(p.rows, p.row_len, p.topk);
+  if (t.crow > kTopkOnePass || t.nseg > 64)
+    return set_error(DSA_ERR_UNSUPPORTED,
+                     "dsa_topk: %lld segments x topk %d exceed one candidate pass (%lld columns)", (long long)t.nseg,
+                     p.topk, (long long)kTopkOnePass);
+  if (!ws || ws_bytes < t.total)
+    return set_error(DSA_ERR_WORKSPACE, "dsa_topk: rows of %lld columns need a %zu-byte workspace (got %zu)",
+                     (long long)p.row_len, t.total, ws_bytes);
+  if (p.rows * t.nseg >= (1ll << 31) || p.rows * t.crow >= (1ll << 40))
+    return set_error(DSA_ERR_INVALID_ARG, "dsa_topk: too many rows for the segment passes");
+  unsigned char *w = static_cast<unsigned char *>(ws);
+  int32_t *cand = reinterpret_cast<int32_t *>(w + t.cand);
+  float *cscore = reinterpret_cast<float *>(w + t.cscore);
+  int32_t *ccol = reinterpret_cast<int32_t *>(w + t.ccol);
+  int32_t *starts2 = reinterpret_cast<int32_t *>(w + t.starts);
+  int32_t *ends2 = reinterpret_cast<int32_t *>(w + t.ends);
+  int32_t *pos = reinterpret_cast<int32_t *>(w + t.pos);
+  TopkParams p1 = p;  // 1. per segment
+  p1.rows = p.rows * t.nseg;
+  p1.nseg = (int)t.nseg;
+  p1.seg_len = t.seg_len;
+  p1.out = cand;
+  p1.out_bstride = 0;
+  int rc = topk_run(p1, st);
+  if (rc) return rc;
+  hipLaunchKernelGGL(topk_compact_kernel, dim3((unsigned)p.rows), dim3(256), 0, st, p1, cand, cscore, ccol,
+                     starts2, ends2);  // 2.
+  rc = check_launch("dsa_topk(compact)");
+  if (rc) return rc;
+  TopkParams p2;  // 3. over the candidates
+  p2.scores = cscore;
+  p2.rows = p.rows;
+  p2.row_len = t.crow;
+  p2.row_stride = t.crow;
+  p2.seq_q = 1;
+  p2.causal_offset = 0;
+  p2.starts = starts2;
+  p2.ends = ends2;
+  p2.causal = 0;
+  p2.topk = p.topk;
+  p2.out = pos;
+  p2.out_bstride = 0;
+  p2.seg_len = 0;
+  p2.nseg = 1;
+  rc = topk_run(p2, st);
+  if (rc) return rc;
+  const int64_t nout = p.rows * p.topk;  // 4.
+  hipLaunchKernelGGL(topk_map_kernel, dim3((unsigned)((nout + 255) / 256)), dim3(256), 0, st, p, pos, ccol,
+                     t.crow);
+  return check_launch("dsa_topk(map)");
 }
 
 // nbatch batches of rows_per_batch rows (scores rows consecutive, row_stride
 // apart), causal windows [0, t + 1 + causal_offset) for row t of a batch, and
-// the outputs of batch b from out + b * out_bstride: one launch for all batches.
+// the outputs of batch b from out + b * out_bstride: one launch for all batches
+// (rows over kTopkOnePass columns: the segment passes, in ws).
 int topk_batched(const float *scores, int64_t rows_per_batch, int64_t nbatch, int64_t row_len, int64_t row_stride,
-                 int causal, int64_t causal_offset, int64_t topk, int32_t *out, int64_t out_bstride,
-                 hipStream_t st) {
+                 int causal, int64_t causal_offset, int64_t topk, int32_t *out, int64_t out_bstride, void *ws,
+                 size_t ws_bytes, hipStream_t st) {
   DSA_REQUIRE(rows_per_batch > 0 && nbatch > 0 && row_len >= 0 && row_stride >= row_len && topk > 0 &&
                   topk < (1ll << 30) && rows_per_batch * nbatch < (1ll << 31),
               "topk_batched: bad dims");
@@ -966,13 +1111,16 @@ int topk_batched(const float *scores, int64_t rows_per_batch, int64_t nbatch, in
   p.topk = (int)topk;
   p.out = out;
   p.out_bstride = out_bstride;
+  p.seg_len = 0;
+  p.nseg = 1;
+  if (row_len > kTopkOnePass) return topk_long(p, ws, ws_bytes, st);
   return topk_run(p, st);
 }
 }  // namespace dsa
 
-extern "C" int dsa_topk(const float *scores, int64_t rows, int64_t row_len, int64_t row_stride, int64_t seq_q,
-                        int causal, int64_t causal_offset, const int32_t *starts, const int32_t *ends,
-                        int64_t topk, int32_t *out_idx, void *stream) {
+static int topk_impl(const float *scores, int64_t rows, int64_t row_len, int64_t row_stride, int64_t seq_q,
+                     int causal, int64_t causal_offset, const int32_t *starts, const int32_t *ends, int64_t topk,
+                     int32_t *out_idx, void *ws, size_t ws_bytes, hipStream_t stream) {
   DSA_REQUIRE(rows >= 0 && row_len >= 0 && topk > 0, "dsa_topk: bad dims rows=%lld row_len=%lld topk=%lld",
               (long long)rows, (long long)row_len, (long long)topk);
   DSA_REQUIRE(row_stride >= row_len, "dsa_topk: row_stride %lld < row_len %lld", (long long)row_stride,
@@ -995,5 +1143,27 @@ extern "C" int dsa_topk(const float *scores, int64_t rows, int64_t row_len, int6
   p.topk = (int)topk;
   p.out = out_idx;
   p.out_bstride = 0;
-  return topk_run(p, static_cast<hipStream_t>(stream));
+  p.seg_len = 0;
+  p.nseg = 1;
+  if (row_len > kTopkOnePass) return topk_long(p, ws, ws_bytes, stream);
+  return topk_run(p, stream);
+}
+
+extern "C" int dsa_topk(const float *scores, int64_t rows, int64_t row_len, int64_t row_stride, int64_t seq_q,
+                        int causal, int64_t causal_offset, const int32_t *starts, const int32_t *ends,
+                        int64_t topk, int32_t *out_idx, void *stream) {
+  return topk_impl(scores, rows, row_len, row_stride, seq_q, causal, causal_offset, starts, ends, topk, out_idx,
+                   nullptr, 0, static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t dsa_topk_workspace_size(int64_t rows, int64_t row_len, int64_t topk) {
+  if (rows <= 0 || topk <= 0 || row_len <= kTopkOnePass) return 0;
+  return topk_long_plan(rows, row_len, topk).total;
+}
+
+extern "C" int dsa_topk_ws(const float *scores, int64_t rows, int64_t row_len, int64_t row_stride, int64_t seq_q,
+                           int causal, int64_t causal_offset, const int32_t *starts, const int32_t *ends,
+                           int64_t topk, int32_t *out_idx, void *workspace, size_t ws_bytes, void *stream) {
+  return topk_impl(scores, rows, row_len, row_stride, seq_q, causal, causal_offset, starts, ends, topk, out_idx,
+                   workspace, ws_bytes, static_cast<hipStream_t>(stream));
 }

@@ -49,9 +49,13 @@ def topk_indices(scores, topk, causal=True, starts=None, ends=None, causal_offse
         starts = starts.to(torch.int32).reshape(rows).contiguous()
         ends = ends.to(torch.int32).reshape(rows).contiguous()
     dev = _lib.ensure_device(scores)
-    rc = _lib.load().dsa_topk(
+    lib = _lib.load()
+    # rows over 32768 columns run in segment passes through a workspace
+    ws_bytes = int(lib.dsa_topk_workspace_size(rows, sk, int(topk)))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=scores.device) if ws_bytes else None
+    rc = lib.dsa_topk_ws(
         flat.data_ptr(), rows, sk, flat.stride(0), int(seq_q or sq), 1 if causal else 0, int(causal_offset),
-        _lib.ptr(starts), _lib.ptr(ends), int(topk), out.data_ptr(), _lib.stream_ptr(dev))
+        _lib.ptr(starts), _lib.ptr(ends), int(topk), out.data_ptr(), _lib.ptr(ws), ws_bytes, _lib.stream_ptr(dev))
     _lib.check(rc, "dsa_topk")
     return out
 
@@ -133,6 +137,8 @@ def indexer_topk_streaming(q, k, weights, index_topk, use_relu=True, causal=True
         chunk_rows = max(1, int(max_scratch_bytes) // max(1, b * sk * 4))
     lib = _lib.load()
     ws_bytes = int(lib.dsa_indexer_topk_streaming_workspace_size(b, sq, sk, int(chunk_rows)))
+    # rows over 32768 keys: room for the top-k's segment passes of a chunk too
+    ws_bytes += 256 + int(lib.dsa_topk_workspace_size(b * min(int(chunk_rows), sq), sk, int(index_topk)))
     dev = _lib.ensure_device(q)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     idx = torch.empty((b, sq, int(index_topk)), dtype=torch.int32, device=q.device)

@@ -296,20 +296,42 @@ int dsa_topk(const float *scores, int64_t rows, int64_t row_len,
              void *stream);
 
 /*
+ * dsa_topk for rows of any length up to 64 x 32768 columns (with
+ * ceil(row_len / 32768) * topk <= 32768), the reach of the reference's
+ * tl_topk, which streams rows of any seq_len (topk_selector.py:30-186).
+ * dsa_topk takes rows of up to 32768 columns in one pass; longer rows run as
+ * segments of at most 32768 columns, each segment's top-k, then one top-k
+ * over the segments' picks (which hold the row's top-k), so the result
+ * follows the same contract bit for bit.  Those passes use a workspace of
+ * dsa_topk_workspace_size(rows, row_len, topk) bytes (0 for rows that fit
+ * one pass, where workspace may be NULL).
+ */
+size_t dsa_topk_workspace_size(int64_t rows, int64_t row_len, int64_t topk);
+int dsa_topk_ws(const float *scores, int64_t rows, int64_t row_len,
+                int64_t row_stride, int64_t seq_q, int causal,
+                int64_t causal_offset, const int32_t *starts,
+                const int32_t *ends, int64_t topk, int32_t *out_idx,
+                void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * Streaming indexer + top-k: the top-k of the indexer scores of every query
  * row without the [B, Sq, Sk] score matrix, the target the reference states
  * for its indexer ("emit only [b, sq, topk] indices and optional top-k
  * scores", docs/status/cppmega_architecture_status.md:340-362).  Query rows
  * go through the workspace in chunks of as many rows as it holds
- * (workspace_bytes / (B * Sk * 4)): per chunk the indexer kernel writes the
- * chunk's scores (causal: only s <= t) and the top-k kernel selects from them,
- * so the indices equal dsa_topk's on the same fp32 scores, bit for bit.
+ * (workspace_bytes / (B * Sk * 4); causal chunks hold only keys up to their
+ * last query row): per chunk the indexer kernel writes the chunk's scores
+ * (causal: only s <= t) and the top-k kernel selects from them, so the
+ * indices equal dsa_topk's on the same fp32 scores, bit for bit.  Rows over
+ * 32768 keys also keep the top-k's segment passes in the workspace
+ * (dsa_topk_workspace_size of the chunk's B * rows rows).
  *   q, w, k, dtype, w_dtype, q_scale, k_scale, use_relu as in dsa_indexer_scores;
  *   out_idx [B, Sq, topk] int32 (ascending, -1 padded; candidates s <= t when
  *   causal, every key otherwise); out_scores [B, Sq, topk] f32 (the selected
  *   scores, -inf for padding) or NULL.
  * workspace: >= dsa_indexer_topk_streaming_workspace_size(B, Sq, Sk, rows)
- * bytes for chunks of `rows` query rows (at least one row).
+ * bytes for chunks of `rows` query rows (at least one row); for Sk > 32768
+ * add 256 + dsa_topk_workspace_size(B * rows, Sk, topk).
  */
 size_t dsa_indexer_topk_streaming_workspace_size(int64_t B, int64_t Sq, int64_t Sk,
                                                  int64_t chunk_rows);

@@ -41,6 +41,25 @@ def test_streaming_equals_full(dev, causal, chunk_rows):
     assert torch.equal(vals, _gathered(sc, ref))
 
 
+def test_streaming_long_keys(dev):
+    """Keys past one top-k pass (40000 > 32768): each chunk's top-k runs its
+    segment passes in the scratch after the chunk's scores; equal to the full
+    matrix's top-k, itself checked against the oracle here."""
+    import numpy as np
+    from oracle import topk as otk
+    Sq, Sk, B, H, D, K = 40, 40000, 2, 16, 64, 512
+    inp = synthetic.indexer_inputs(B, Sk, H, D, seed=93)
+    q, k, w = inp["q"][:Sq].to(dev), inp["k"].to(dev), inp["w"][:Sq].to(dev)
+    sc, ref = _full(q.contiguous(), k, w.contiguous(), K, False)
+    np.testing.assert_array_equal(ref.cpu().reshape(B * Sq, K).numpy(),
+                                  otk.topk_ascending(sc.cpu().reshape(B * Sq, Sk).numpy(), K))
+    for chunk_rows in (7, 40):
+        idx, vals = indexer_topk_streaming(q.contiguous(), k, w.contiguous(), K, causal=False, return_scores=True,
+                                           chunk_rows=chunk_rows)
+        assert torch.equal(idx, ref)
+        assert torch.equal(vals, _gathered(sc, ref))
+
+
 def test_streaming_e4m3_wide_heads(dev):
     """cfg5's indexer form (e4m3, h = 64, d = 128) at a small length, in 3-row chunks."""
     S, B, H, D, K = 200, 1, 64, 128, 96

@@ -218,6 +218,36 @@ def test_topk_subset_bound_edges(dev, n, topk):
     np.testing.assert_array_equal(got.numpy(), otk.topk_ascending(t, topk, st, en))
 
 
+@pytest.mark.parametrize("rows,n,topk,causal", [
+    (6, 70000, 2048, False),   # 3 segments of 23334 columns
+    (40, 40000, 256, True),    # causal windows ending in either segment
+    (5, 32769, 64, False),     # one column past a single pass
+    (3, 300000, 100, False),   # 10 segments
+])
+def test_topk_long_rows(dev, rows, n, topk, causal):
+    """Rows over 32768 columns: per-segment top-k, then one top-k over the
+    segments' picks; the same contract (ties to the lower column, NaN as +inf,
+    ascending, -1 padded) as one pass, against the oracle."""
+    s = _tie_heavy_scores(rows, n, seed=rows + n)
+    s[0, ::7] = np.nan                                   # NaN ranks +inf in every segment
+    s[1 % rows] = np.float32(3.0)                         # all equal: the lowest columns win
+    if rows > 3:
+        s[3, : n // 2] = -np.inf                          # a -inf segment head
+    seq_q, off = (rows, n // 2 - rows // 2) if causal else (1, 0)      # causal ends straddle the middle
+    got = topk_indices(torch.from_numpy(s).to(dev), topk, causal=causal, seq_q=seq_q if causal else None,
+                       causal_offset=off).cpu()
+    st, en = otk.causal_windows(rows, seq_q, n, offset=off) if causal else (None, None)
+    np.testing.assert_array_equal(got.numpy(), otk.topk_ascending(s, topk, st, en))
+    # explicit windows crossing the segment boundaries, some shorter than topk
+    g = np.random.default_rng(n)
+    starts = g.integers(0, n, rows).astype(np.int32)
+    ends = np.minimum(n, starts + g.integers(0, n, rows)).astype(np.int32)
+    ends[0] = min(n, starts[0] + topk // 2)
+    got = topk_indices(torch.from_numpy(s).to(dev), topk, causal=False,
+                       starts=torch.from_numpy(starts).to(dev), ends=torch.from_numpy(ends).to(dev)).cpu()
+    np.testing.assert_array_equal(got.numpy(), otk.topk_ascending(s, topk, starts, ends))
+
+
 def test_topk_windows_and_all_equal(dev):
     rows, n, topk = 50, 700, 32
     s = np.zeros((rows, n), dtype=np.float32)          # all equal: lowest columns win
