@@ -63,12 +63,12 @@ struct IdxCfg {
   static constexpr int CHUNK = 2048;            // keys per workgroup
   static constexpr int NKT = CHUNK / KT;        // tiles per workgroup chunk
   static constexpr int KS_STRIDE = ROWB + 16;
-  static constexpr int KSTEPS = D / 16;
+  static constexpr int KSTEPS = FP8 ? D / 64 : D / 16;  // MFMA k-steps: 32x32x64 f8f6f4 or 32x32x16 bf16
   static constexpr int CPR = ROWB / 16;         // 16-byte chunks per key row
   static constexpr int NT = 64 * WAVES;         // threads per workgroup
   static constexpr int LOADS = KT * CPR / NT;   // 16-byte loads per thread per tile
   static_assert(H == 16 || H == 32 || H == 64, "index heads must be 16, 32 or 64");
-  static_assert(D % 16 == 0 && LOADS >= 1 && KT * CPR % NT == 0 && CHUNK % KT == 0, "index head dim");
+  static_assert(D % (FP8 ? 64 : 16) == 0 && LOADS >= 1 && KT * CPR % NT == 0 && CHUNK % KT == 0, "index head dim");
 };
 
 // Scores of token block [t0, t0 + TT) against keys [k0, k_end) of batch b
@@ -127,7 +127,9 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
   load_tile(0, kreg);
 
   // ---- A operands (q rows) and weights of this wave's 64 (token, head) rows ----
-  typedef typename std::conditional<FP8, long, bf16x8>::type aop_t;
+  // e4m3: operands of the 32x32x64 f8f6f4 MFMA, lane (row l32, half g32)
+  // holding channels [16 g32, +16) and [32 + 16 g32, +16) of each 64-channel chunk
+  typedef typename std::conditional<FP8, i32x8, bf16x8>::type aop_t;
   aop_t A[C::MT][C::KSTEPS];
   const int64_t wave_tok0 = t0 + w * C::TPW;
 #pragma unroll
@@ -139,7 +141,12 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
 #pragma unroll
     for (int k = 0; k < C::KSTEPS; ++k) {
       if constexpr (FP8) {
-        A[m][k] = ok ? *reinterpret_cast<const long *>(p.q + qrow * D + 16 * k + 8 * g32) : 0l;
+        i32x4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
+        if (ok) {
+          lo = ld_global_16(p.q + qrow * D + 64 * k + 16 * g32);
+          hi = ld_global_16(p.q + qrow * D + 64 * k + 32 + 16 * g32);
+        }
+        A[m][k] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       } else {
         i32x4 v = {0, 0, 0, 0};
         if (ok) v = ld_global_16(p.q + (qrow * D + 16 * k + 8 * g32) * 2);
@@ -178,8 +185,11 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
       for (int k = 0; k < C::KSTEPS; ++k) {
         const unsigned char *brow = ks + (sub * 32 + l32) * C::KS_STRIDE;
         if constexpr (FP8) {
-          const long bv = *reinterpret_cast<const long *>(brow + 16 * k + 8 * g32);
-          acc = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(A[m][k], bv, acc, 0, 0, 0);
+          const i32x4 lo = *reinterpret_cast<const i32x4 *>(brow + 64 * k + 16 * g32);
+          const i32x4 hi = *reinterpret_cast<const i32x4 *>(brow + 64 * k + 32 + 16 * g32);
+          const i32x8 bv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          // unit block scales (E8M0 127 = 2^0): a plain e4m3 product, two k-chunks of 32
+          acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A[m][k], bv, acc, 0, 0, 0, 127, 0, 127);
         } else {
           const i32x4 bv = *reinterpret_cast<const i32x4 *>(brow + (16 * k + 8 * g32) * 2);
           acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[m][k], as_bf16x8(bv), acc, 0, 0, 0);
