@@ -61,7 +61,12 @@ sparse_mla_fwd_kernel(const FwdParams p) {
   using Gat = typename C::Gat;
   using VGat = typename C::VGat;
   static_assert(VGat::KL_STRIDE == C::KD_STRIDE, "bf16 V rows land in the V tile's layout");
-  typedef typename std::conditional<FP8, long, bf16x8>::type qop_t;
+  // tensorwise e4m3: S on the 32x32x64 f8f6f4 MFMA (unit block scales), whose
+  // lane (row l32, half g32) holds channels [16 g32, +16) and [32 + 16 g32, +16)
+  // of each 64-channel chunk; MX keeps 32x32x16 (one partial per 32-channel block)
+  constexpr bool F8X = FP8 && !MX && D_QK % 64 == 0;
+  constexpr int QK = F8X ? D_QK / 64 : C::KSTEPS;  // Q operand registers (MFMA k-steps)
+  typedef typename std::conditional<F8X, i32x8, typename std::conditional<FP8, long, bf16x8>::type>::type qop_t;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
   const int lane = lane_id(), w = wave_id();
@@ -118,15 +123,19 @@ sparse_mla_fwd_kernel(const FwdParams p) {
   const int nh = p.hpg - tile * 32 < 32 ? p.hpg - tile * 32 : 32;
   constexpr int QB = FP8 || QMX ? 1 : 2;  // bytes per Q element
   const auto q_rs = make_buffer_rsrc(p.q + qrow0 * D_QK * QB, (uint32_t)(nh * D_QK * QB));
-  qop_t qreg[C::KSTEPS];
+  qop_t qreg[QK];
   float qmxs[QMX ? D_QK / 32 : 1];  // QMX: this lane's head's block scales
   if constexpr (QMX) {
 #pragma unroll
     for (int c = 0; c < D_QK / 32; ++c) qmxs[c] = head_ok ? p.q_scale[qrow * (D_QK / 32) + c] : 0.0f;
   }
 #pragma unroll
-  for (int k = 0; k < C::KSTEPS; ++k) {
-    if constexpr (FP8) {
+  for (int k = 0; k < QK; ++k) {
+    if constexpr (F8X) {
+      const auto lo = __builtin_amdgcn_raw_buffer_load_b128(q_rs, l32 * D_QK + 64 * k + 16 * g32, 0, 0);
+      const auto hi = __builtin_amdgcn_raw_buffer_load_b128(q_rs, l32 * D_QK + 64 * k + 32 + 16 * g32, 0, 0);
+      qreg[k] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    } else if constexpr (FP8) {
       const auto v = __builtin_amdgcn_raw_buffer_load_b64(q_rs, l32 * D_QK + 16 * k + 8 * g32, 0, 0);
       qreg[k] = __builtin_bit_cast(long, v);
     } else if constexpr (QMX) {
@@ -200,8 +209,14 @@ sparse_mla_fwd_kernel(const FwdParams p) {
       }
     }
 #pragma unroll
-    for (int k = 0; k < (MX ? 0 : C::KSTEPS); ++k) {
-      if constexpr (FP8) {
+    for (int k = 0; k < (MX ? 0 : QK); ++k) {
+      if constexpr (F8X) {
+        const unsigned char *kr = Kl + l32 * Gat::KL_STRIDE + 64 * k + 16 * g32;
+        const i32x4 lo = *reinterpret_cast<const i32x4 *>(kr);
+        const i32x4 hi = *reinterpret_cast<const i32x4 *>(kr + 32);
+        const i32x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        sacc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, qreg[k], sacc, 0, 0, 0, 127, 0, 127);
+      } else if constexpr (FP8) {
         const long a = *reinterpret_cast<const long *>(Kl + l32 * Gat::KL_STRIDE + 16 * k + 8 * g32);
         sacc = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(a, qreg[k], sacc, 0, 0, 0);
       } else {
