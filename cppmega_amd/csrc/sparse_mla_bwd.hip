@@ -316,11 +316,23 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
     maxdo = fmaxf(LD[65], LD[67]);
   }
 
-  long qA8[FP8 ? C::KSTEPS : 1];  // e4m3: raw Q codes as the S A operand (head l32)
+  // e4m3: raw Q codes as the A operand of S on the 32x32x64 f8f6f4 MFMA (unit
+  // block scales; lane (head l32, half g32) holds channels [16 g32, +16) and
+  // [32 + 16 g32, +16) of each 64-channel chunk)
+  constexpr int K8 = D_QK / 64;
+  static_assert(!FP8 || D_QK % 64 == 0, "e4m3 rows come in 64-channel chunks");
+  i32x8 qA8[FP8 ? K8 : 1];
   if constexpr (FP8) {
 #pragma unroll
-    for (int k = 0; k < C::KSTEPS; ++k)
-      qA8[k] = l32 < nheads ? *reinterpret_cast<const long *>(p.q + (head0 + l32) * D_QK + 16 * k + 8 * g32) : 0l;
+    for (int k = 0; k < K8; ++k) {
+      i32x4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
+      if (l32 < nheads) {
+        const unsigned char *qr = p.q + (head0 + l32) * D_QK + 64 * k + 16 * g32;
+        lo = *reinterpret_cast<const i32x4 *>(qr);
+        hi = *reinterpret_cast<const i32x4 *>(qr + 32);
+      }
+      qA8[k] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
   }
   f32x16 dqacc[C::DQT];
 #pragma unroll
@@ -354,10 +366,13 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
       dpacc[a] = 0.0f;
     }
 #pragma unroll
-    for (int k = 0; k < C::KSTEPS; ++k) {
+    for (int k = 0; k < (FP8 ? K8 : C::KSTEPS); ++k) {
       if constexpr (FP8) {
-        const long kb = *reinterpret_cast<const long *>(Kl + l32 * Gat::KL_STRIDE + 16 * k + 8 * g32);
-        sacc = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(qA8[k], kb, sacc, 0, 0, 0);
+        const unsigned char *kr = Kl + l32 * Gat::KL_STRIDE + 64 * k + 16 * g32;
+        const i32x4 lo = *reinterpret_cast<const i32x4 *>(kr);
+        const i32x4 hi = *reinterpret_cast<const i32x4 *>(kr + 32);
+        const i32x8 kb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        sacc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qA8[k], kb, sacc, 0, 0, 0, 127, 0, 127);
       } else {
         // V is the leading D_V columns of K: one K read feeds S and dP
         const i32x4 kb = *reinterpret_cast<const i32x4 *>(Kl + l32 * Gat::KL_STRIDE + (16 * k + 8 * g32) * 2);
