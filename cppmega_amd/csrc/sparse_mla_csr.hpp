@@ -152,25 +152,27 @@ __device__ __forceinline__ int32_t chunk_count(const CsrParams &p, int64_t b, in
   return p.dup[(b * p.NC + c) * p.SPL + part] ? p.base[cell] : (int32_t)__popc(p.mask[cell]);
 }
 
-// grid (ceil(R / 64), B), 16 waves: lane = row, wave w = a contiguous
-// sixteenth of the chunks.  Each wave totals its chunks per row, the waves'
-// totals are combined in LDS, and each wave then writes the exclusive prefix
-// over chunks into base[b][c][r] (a chunk's exact count, kept in base for
-// chunks with repeats, is read before the same lane overwrites it).  A wave
-// with at most TILE chunks (every wave while NC <= 16 * TILE) keeps its counts
-// in registers between the two steps; longer ranges re-read them.
-constexpr int kScanWaves = 16;
-__global__ void __launch_bounds__(64 * kScanWaves) csr_colscan_kernel(const CsrParams p) {
-  constexpr int TILE = 16;
-  __shared__ int32_t wtot[kScanWaves][64];
-  const int lane = lane_id(), w = wave_id();
+// grid (ceil(R / 16), B), 256 threads: thread t takes row 16 blockIdx.x + t % 16
+// and chunk group t / 16 (a contiguous sixteenth of the chunks).  Each thread
+// totals its chunks of its row, the groups' totals are combined in LDS, and
+// each thread then writes the exclusive prefix over chunks into base[b][c][r]
+// (a chunk's exact count, kept in base for chunks with repeats, is read before
+// the same thread overwrites it).  A group of at most TILE chunks (every group
+// while NC <= 16 * TILE) keeps its counts in registers between the two steps;
+// longer ranges re-read them.  Four-wave workgroups with few registers fit
+// beside the forward kernel, which this kernel runs next to on a second stream.
+constexpr int kScanRows = 16, kScanGroups = 16;
+__global__ void __launch_bounds__(kScanRows * kScanGroups) csr_colscan_kernel(const CsrParams p) {
+  constexpr int TILE = 4;
+  __shared__ int32_t gtot[kScanGroups][kScanRows];
+  const int tid = threadIdx.x, rl = tid % kScanRows, cg = tid / kScanRows;
   const int64_t b = blockIdx.y;
-  const int64_t r = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t r = (int64_t)blockIdx.x * kScanRows + rl;
   const bool rok = r < p.R;
   const int part = rok ? (int)(r / p.RP) : 0;
-  const int c_lo = (int)((int64_t)p.NC * w / kScanWaves), c_hi = (int)((int64_t)p.NC * (w + 1) / kScanWaves);
+  const int c_lo = (int)((int64_t)p.NC * cg / kScanGroups), c_hi = (int)((int64_t)p.NC * (cg + 1) / kScanGroups);
   if (blockIdx.x == 0) {  // the chunks' combined repeat flags (read by the scatter and the main kernel)
-    for (int c = threadIdx.x; c < p.NC; c += 64 * kScanWaves) {
+    for (int c = tid; c < p.NC; c += kScanRows * kScanGroups) {
       int any = 0;
       for (int q = 0; q < p.SPL; ++q) any |= p.dup[(b * p.NC + c) * p.SPL + q];
       p.dupc[b * p.NC + c] = any;
@@ -184,16 +186,16 @@ __global__ void __launch_bounds__(64 * kScanWaves) csr_colscan_kernel(const CsrP
 #pragma unroll
     for (int u = 0; u < TILE; ++u) s += v[u];
   }
-  wtot[w][lane] = s;
+  gtot[cg][rl] = s;
   __syncthreads();
   int32_t run = 0, tot = 0;
 #pragma unroll
-  for (int i = 0; i < kScanWaves; ++i) {
-    const int32_t t = wtot[i][lane];
-    run += i < w ? t : 0;
+  for (int i = 0; i < kScanGroups; ++i) {
+    const int32_t t = gtot[i][rl];
+    run += i < cg ? t : 0;
     tot += t;
   }
-  const bool one_tile = c_hi - c_lo <= TILE;  // wave-uniform
+  const bool one_tile = c_hi - c_lo <= TILE;  // block-uniform
   for (int c0 = c_lo; c0 < c_hi; c0 += TILE) {
     if (!one_tile) {
 #pragma unroll
@@ -205,7 +207,7 @@ __global__ void __launch_bounds__(64 * kScanWaves) csr_colscan_kernel(const CsrP
       run += v[u];
     }
   }
-  if (w == 0 && rok) p.tot[b * p.R + r] = tot;
+  if (cg == 0 && rok) p.tot[b * p.R + r] = tot;
 }
 
 // Exclusive scan of cnt[0..n) into rowptr[0..n] with one 1024-thread
@@ -489,9 +491,9 @@ static int launch_csr(const CsrParams &cp, int64_t B, hipStream_t st) {
                      (long long)cp.RP, (long long)cp.R);
   const int64_t rows = B * cp.R;
   const dim3 cgrid((unsigned)(cp.NC * cp.SPL), (unsigned)B);
-  const dim3 sgrid((unsigned)((cp.R + 63) / 64), (unsigned)B);
+  const dim3 sgrid((unsigned)((cp.R + kScanRows - 1) / kScanRows), (unsigned)B);
   hipLaunchKernelGGL(csr_mask_kernel, cgrid, dim3(kMaskThreads), lds, st, cp);
-  hipLaunchKernelGGL(csr_colscan_kernel, sgrid, dim3(64 * kScanWaves), 0, st, cp);
+  hipLaunchKernelGGL(csr_colscan_kernel, sgrid, dim3(kScanRows * kScanGroups), 0, st, cp);
   hipLaunchKernelGGL(csr_scan_kernel, dim3(1), dim3(1024), 0, st, cp.tot, cp.rowptr, rows);
   hipLaunchKernelGGL(csr_scatter_kernel, cgrid, dim3(256), lds, st, cp);
   return check_launch("sparse_mla_bwd(csr)");
