@@ -142,6 +142,31 @@ __device__ __forceinline__ void sum_partials(const float *Sp, int stride_w, floa
   }
 }
 
+// Split form of sum_partials for four waves: wave w sums quarter w (64 lanes x
+// 4 floats) of the four partial tiles in the same order and writes it to the
+// reduced tile Sr; after a barrier every wave reads the whole reduced tile
+// (get_reduced), so each reads 8 KiB of LDS instead of 16.
+__device__ __forceinline__ void reduce_quarter(const float *Sp, int stride_w, float *Sr, int w) {
+  const int lane = lane_id();
+  const f32x4 v0 = *reinterpret_cast<const f32x4 *>(Sp + 0 * stride_w + (w * 64 + lane) * 4);
+  const f32x4 v1 = *reinterpret_cast<const f32x4 *>(Sp + 1 * stride_w + (w * 64 + lane) * 4);
+  const f32x4 v2 = *reinterpret_cast<const f32x4 *>(Sp + 2 * stride_w + (w * 64 + lane) * 4);
+  const f32x4 v3 = *reinterpret_cast<const f32x4 *>(Sp + 3 * stride_w + (w * 64 + lane) * 4);
+  f32x4 r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) r[j] = ((v0[j] + v1[j]) + v2[j]) + v3[j];
+  *reinterpret_cast<f32x4 *>(Sr + (w * 64 + lane) * 4) = r;
+}
+__device__ __forceinline__ void get_reduced(const float *Sr, float (&s)[16]) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4) {
+    const f32x4 v = *reinterpret_cast<const f32x4 *>(Sr + (q4 * 64 + lane) * 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s[4 * q4 + j] = v[j];
+  }
+}
+
 __device__ __forceinline__ void put_partial(float *dst, const f32x16 &acc) {
   const int lane = lane_id();
 #pragma unroll
@@ -162,7 +187,8 @@ struct WideFwdLds {
   static constexpr int OFF_SC = OFF_KD + (FP8 ? 32 * C::KD_STRIDE : 0);
   static constexpr int OFF_SP = (OFF_SC + (FP8 ? (MX ? NBLK : 1) * 32 * 4 : 0) + 15) / 16 * 16;
   static constexpr int SP_W = 16 * 64;  // floats per wave's partial tile
-  static constexpr int BYTES = OFF_SP + 4 * NT * SP_W * 4;  // a partial tile per wave
+  static constexpr int OFF_SR = OFF_SP + 4 * NT * SP_W * 4;  // a partial tile per wave
+  static constexpr int BYTES = OFF_SR + NT * SP_W * 4;       // a reduced tile per head tile
 };
 
 // MX partial scores of one wave over its k-steps [k0, k0 + KQ) of d_qk (k0 of
@@ -228,6 +254,7 @@ sparse_mla_fwd_wide_kernel(const FwdParams p) {
   unsigned char *Kd = smem + L::OFF_KD;
   float *Ksc = reinterpret_cast<float *>(smem + L::OFF_SC);
   float *Sp = reinterpret_cast<float *>(smem + L::OFF_SP);
+  float *Sr = reinterpret_cast<float *>(smem + L::OFF_SR) + ht * L::SP_W;
   const unsigned char *Vsrc = FP8 ? Kd : Kl;
   constexpr int V_STRIDE = FP8 ? C::KD_STRIDE : C::KL_STRIDE;
 
@@ -318,8 +345,10 @@ sparse_mla_fwd_wide_kernel(const FwdParams p) {
     }
     put_partial(Sp + wv * L::SP_W, sacc);
     __syncthreads();  // all partial tiles written
+    reduce_quarter(Sp + 4 * ht * L::SP_W, L::SP_W, Sr, w);
+    __syncthreads();  // the head tile's reduced scores are whole
     float s[16];
-    sum_partials(Sp + 4 * ht * L::SP_W, L::SP_W, s);
+    get_reduced(Sr, s);
 
     // ---- online softmax (log2 domain, lazy rescale; identical in every wave) ----
     // this lane's slots are 8i + 4*g32 + j: their valid bits sit at 8i + j of lmask;
