@@ -632,6 +632,16 @@ def main():
     kl = None if args.no_kl else measure_indexer_kl(dev)
     cfg4 = None if args.no_cfg4 else measure_cfg4(dev)
 
+    def cpu_model():
+        try:
+            with open("/proc/cpuinfo") as f:
+                for ln in f:
+                    if ln.startswith("model name"):
+                        return ln.split(":", 1)[1].strip()
+        except OSError:
+            pass
+        return "unknown"
+
     cpu = None
     if not args.no_cpu_baseline:
         from oracle.cpu_baseline import time_cpu_baseline
@@ -639,7 +649,7 @@ def main():
         cpu = {"value": round(cb["tokens_per_s"], 2), "unit": "tokens/s", "cores": cb["cores"], "kind": "port",
                "sample": f"batch 0, all {cb['tokens']} query tokens of s=4096 (full keys): per-head fp32 indexer "
                          f"+ torch.topk + gather-softmax SparseMLA fwd + autograd bwd, median of 3 reps",
-               "phases_s": {k: round(v, 4) for k, v in cb["phases_s"].items()}}
+               "phases_s": {k: round(v, 4) for k, v in cb["phases_s"].items()}, "cpu_model": cpu_model()}
 
     line = {
         "metric": "SparseMLA+indexer fwd+bwd tokens/s at s=4096,topk=256 on 1 GPU",
