@@ -39,6 +39,7 @@ struct TopkParams {
   // launch row v is out + v * topk
   int64_t seg_len;
   int nseg;
+  int64_t row0;  // launch row v is row row0 + v (a launch over part of the rows)
 };
 
 // Launch row v: its scores row `row` and window [st, en) (clamped to the row
@@ -264,8 +265,9 @@ topk_wave_kernel(const TopkParams p) {
   __shared__ float s_list[4][64];
   // the wave index is uniform: make the row and everything derived from it scalar
   const int w = __builtin_amdgcn_readfirstlane(wave_id()), lane = lane_id();
-  const int64_t vrow = (int64_t)blockIdx.x * 4 + w;
-  if (vrow >= p.rows) return;
+  const int64_t lrow = (int64_t)blockIdx.x * 4 + w;
+  if (lrow >= p.rows) return;
+  const int64_t vrow = p.row0 + lrow;
   int *hist = s_hist[w];
   float *list = s_list[w];
   int64_t row, st, en;
@@ -620,7 +622,7 @@ __global__ void __launch_bounds__(64 * NW) topk_block_kernel(const TopkParams p)
   int *hist = sm.hist;
   const int w = __builtin_amdgcn_readfirstlane(wave_id()), lane = lane_id();
   const int tid = threadIdx.x;
-  const int64_t vrow = blockIdx.x;
+  const int64_t vrow = p.row0 + blockIdx.x;
   int64_t row, st, en;
   topk_window(p, vrow, row, st, en);
   const int n = __builtin_amdgcn_readfirstlane(en > st ? (int)(en - st) : 0);
@@ -946,6 +948,28 @@ constexpr int64_t kTopkOnePass = 32768;  // the longest row (or segment) one ker
 // One launch over rows (segment mode: segments) of up to kTopkOnePass columns.
 static int topk_run(const TopkParams &p, hipStream_t st) {
   const int64_t len = p.nseg > 1 ? p.seg_len : p.row_len;
+  // causal rows longer than 8192 columns: the rows whose window still fits
+  // 8192 columns (t < 8192 - causal_offset in each batch) take one wave per
+  // row instead of a workgroup whose later waves would hold no column
+  if (p.nseg <= 1 && p.causal && !p.starts && len > 8192 && len <= kTopkOnePass && p.row0 == 0 &&
+      p.rows % p.seq_q == 0) {
+    int64_t nshort = 8192 - p.causal_offset;
+    nshort = nshort < 0 ? 0 : (nshort > p.seq_q ? p.seq_q : nshort);
+    if (nshort > 0 && nshort < p.seq_q) {
+      for (int64_t b = 0; b < p.rows / p.seq_q; ++b) {
+        TopkParams q = p;
+        q.row0 = b * p.seq_q;
+        q.rows = nshort;
+        int rc = launch_topk_wave<128>(q, st);
+        if (rc) return rc;
+        q.row0 = b * p.seq_q + nshort;
+        q.rows = p.seq_q - nshort;
+        rc = len <= 16384 ? launch_topk_block<4, 64>(q, st) : launch_topk_block<8, 64>(q, st);
+        if (rc) return rc;
+      }
+      return DSA_OK;
+    }
+  }
   if (len <= 2048) return launch_topk_wave<32>(p, st);
   if (len <= 4096) return launch_topk_wave<64>(p, st);
   if (len <= 8192) return launch_topk_wave<128>(p, st);
@@ -1080,6 +1104,7 @@ static int topk_long(const TopkParams &p, void *ws, size_t ws_bytes, hipStream_t
   p2.out_bstride = 0;
   p2.seg_len = 0;
   p2.nseg = 1;
+  p2.row0 = 0;
   rc = topk_run(p2, st);
   if (rc) return rc;
   const int64_t nout = p.rows * p.topk;  // 4.
@@ -1113,6 +1138,7 @@ int topk_batched(const float *scores, int64_t rows_per_batch, int64_t nbatch, in
   p.out_bstride = out_bstride;
   p.seg_len = 0;
   p.nseg = 1;
+  p.row0 = 0;
   if (row_len > kTopkOnePass) return topk_long(p, ws, ws_bytes, st);
   return topk_run(p, st);
 }
@@ -1145,6 +1171,7 @@ static int topk_impl(const float *scores, int64_t rows, int64_t row_len, int64_t
   p.out_bstride = 0;
   p.seg_len = 0;
   p.nseg = 1;
+  p.row0 = 0;
   if (row_len > kTopkOnePass) return topk_long(p, ws, ws_bytes, stream);
   return topk_run(p, stream);
 }

@@ -248,6 +248,19 @@ def test_topk_long_rows(dev, rows, n, topk, causal):
     np.testing.assert_array_equal(got.numpy(), otk.topk_ascending(s, topk, starts, ends))
 
 
+@pytest.mark.parametrize("n,off", [(16384, 8192 - 32), (20000, 8192 - 40), (12000, 8192 - 1)])
+def test_topk_causal_rows_across_8192(dev, n, off):
+    """Causal rows on both sides of 8192 columns in one call (two batches): the
+    rows whose window fits 8192 take the wave kernel, the longer ones the
+    workgroup kernel; both against the oracle."""
+    rows, seq_q, topk = 128, 64, 512
+    s = _tie_heavy_scores(rows, n, seed=n + off)
+    got = topk_indices(torch.from_numpy(s).to(dev), topk, causal=True, seq_q=seq_q, causal_offset=off).cpu()
+    st, en = otk.causal_windows(rows, seq_q, n, offset=off)
+    assert (en <= 8192).any() and (en > 8192).any()
+    np.testing.assert_array_equal(got.numpy(), otk.topk_ascending(s, topk, st, en))
+
+
 def test_topk_windows_and_all_equal(dev):
     rows, n, topk = 50, 700, 32
     s = np.zeros((rows, n), dtype=np.float32)          # all equal: lowest columns win
