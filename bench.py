@@ -540,19 +540,20 @@ def main():
         if record:
             marks[2].record()
         # the backward's inverse index depends on the indices alone: it is built on
-        # a second stream while the forward runs (marks 5, 6 time it there)
+        # a second stream while the forward runs (marks 5, 6 time it there); the
+        # forward is queued first and the build waits only for the work before it
+        ready = torch.cuda.Event()
+        ready.record()
         if record:
-            side.wait_stream(torch.cuda.current_stream())
-            marks[5].record(side)
-        inv = build_inverse_index(q, kv, idx, D_V, stream=side)
-        if record:
-            marks[6].record(side)
-            # the forward's own start: the side-stream launches above may leave the
-            # main stream idle while the host issues them
             marks[7].record()
         out, lse = sparse_mla_fwd_interface(q, kv, idx, sm_scale=scale, d_v=D_V)
         if record:
             marks[3].record()
+            side.wait_event(ready)
+            marks[5].record(side)
+        inv = build_inverse_index(q, kv, idx, D_V, stream=side, after=ready)
+        if record:
+            marks[6].record(side)
         dq, dkv = sparse_mla_bwd(q, kv, out, do, idx, lse, sm_scale=scale, inverse_index=inv)
         if record:
             marks[4].record()
@@ -614,8 +615,10 @@ def main():
         # the same layer step with SparseMLA consuming the top-k's own indices
         sc = index_scores(iq, iw, ik, use_relu=True, causal=CAUSAL_LOWER)
         sel_c = topk_indices(sc, TOPK, causal=True).view(B, S, 1, TOPK)
-        inv_c = build_inverse_index(q, kv, sel_c, D_V, stream=side)
+        ready_c = torch.cuda.Event()
+        ready_c.record()
         out_c, lse_c = sparse_mla_fwd_interface(q, kv, sel_c, sm_scale=scale, d_v=D_V)
+        inv_c = build_inverse_index(q, kv, sel_c, D_V, stream=side, after=ready_c)
         return sparse_mla_bwd(q, kv, out_c, do, sel_c, lse_c, sm_scale=scale, inverse_index=inv_c)
 
     t_chain = graph_replay_time(chained_step)

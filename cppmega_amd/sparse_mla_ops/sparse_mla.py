@@ -67,10 +67,15 @@ class SparseMLA(torch.autograd.Function):
         if d_v is None:
             d_v = q.shape[-1]
         # the backward's inverse index depends on the indices alone: build it on a
-        # second stream while the forward kernel runs
-        ctx.inverse_index = (build_inverse_index(q, kv, indices, d_v, stream=side_stream(q.device))
-                             if ctx.needs_input_grad[0] or ctx.needs_input_grad[1] else None)
+        # second stream while the forward kernel runs (the forward is queued
+        # first; the build waits only for the work before it)
+        need_index = ctx.needs_input_grad[0] or ctx.needs_input_grad[1]
+        ready = torch.cuda.Event() if need_index else None
+        if ready is not None:
+            ready.record()
         out, lse = sparse_mla_fwd_interface(q, kv, indices, sm_scale=scaling, d_v=d_v)
+        ctx.inverse_index = (build_inverse_index(q, kv, indices, d_v, stream=side_stream(q.device), after=ready)
+                             if need_index else None)
         ctx.d_v = d_v
         ctx.save_for_backward(q, kv, indices, out, lse)
         return out, lse
@@ -130,10 +135,14 @@ class SparseMLA_FP8(torch.autograd.Function):
             k8 = k8_flat.reshape(kv.shape)
             kv_scale = ks_flat.reshape(kv.shape[:-2])
 
-        ctx.inverse_index = (build_inverse_index(q8, k8, indices, d_v, stream=side_stream(q8.device))
-                             if ctx.needs_input_grad[0] or ctx.needs_input_grad[1] else None)
+        need_index = ctx.needs_input_grad[0] or ctx.needs_input_grad[1]
+        ready = torch.cuda.Event() if need_index else None
+        if ready is not None:
+            ready.record()
         out, lse = sparse_mla_fwd_fp8_interface(q8, k8, indices, q_scale=q_scale, kv_scale=kv_scale,
                                                 sm_scale=scaling, d_v=d_v)
+        ctx.inverse_index = (build_inverse_index(q8, k8, indices, d_v, stream=side_stream(q8.device), after=ready)
+                             if need_index else None)
         ctx.d_v = d_v
         ctx.save_for_backward(q8, k8, q_scale, kv_scale, indices, out, lse)
         return out, lse

@@ -62,13 +62,15 @@ def _bwd_flags(fp32_partials):
     return _lib.BWD_FP32_PARTIALS if fp32_partials else 0
 
 
-def build_inverse_index(q, kv, indices, d_v, *, fp32_partials=None, stream=None):
+def build_inverse_index(q, kv, indices, d_v, *, fp32_partials=None, stream=None, after=None):
     """Build the backward's inverse index for q [B,S,H,D] (or 3-D), kv
     [B,S_kv,G,D] and indices [B,S,G,topk] int32; returns an ``InverseIndex``,
     or None when the backward runs in several passes (it then builds its index
     per pass).  With ``stream`` (e.g. ``side_stream(q.device)``) the build runs
-    there after the work already queued on the current stream, and the
-    backward waits for it through an event."""
+    there after the work already queued on the current stream (or, with
+    ``after``, a ``torch.cuda.Event`` recorded on it, after the work up to
+    that event: work queued since, such as the forward kernel, does not delay
+    the build), and the backward waits for it through an event."""
     if q.ndim == 3:
         q, kv, indices = q.unsqueeze(0), kv.unsqueeze(0), indices.unsqueeze(0)
     assert indices.is_contiguous() and indices.dtype == torch.int32
@@ -84,7 +86,10 @@ def build_inverse_index(q, kv, indices, d_v, *, fp32_partials=None, stream=None)
     side = stream if stream is not None else cur
     buf = torch.empty(n, dtype=torch.uint8, device=q.device)
     if side != cur:
-        side.wait_stream(cur)
+        if after is not None:
+            side.wait_event(after)
+        else:
+            side.wait_stream(cur)
     rc = L.dsa_sparse_mla_bwd_build_index(indices.data_ptr(), B, S, S_kv, H, G, D, int(d_v), topk, flags,
                                           buf.data_ptr(), n, side.cuda_stream)
     _lib.check(rc, "dsa_sparse_mla_bwd_build_index")
