@@ -340,6 +340,14 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
 #pragma unroll
     for (int a = 0; a < 16; ++a) dqacc[t][a] = 0.0f;
 
+  // The first block's rows and CSR positions have landed before the loop (its
+  // first use waits for them anyway).  With nothing in flight on entry, the
+  // compiler's memory waits inside the loop follow the loop's own order only,
+  // so waiting for the next block's rows and positions leaves this block's
+  // partial-row stores (issued after them) in flight; without it the waits at
+  // the loop head drain every store.  (s_waitcnt vmcnt(0) with expcnt and
+  // lgkmcnt left open, gfx9 encoding.)
+  __builtin_amdgcn_s_waitcnt(0x0F70);
   for (; blk < nblk; blk += C::WPT) {
     const int slot0 = blk * 32;
     // ---- stage block: K rows (+ e4m3: dequantised rows, scales) ----
