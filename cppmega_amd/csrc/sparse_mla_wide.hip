@@ -79,9 +79,10 @@ __device__ __forceinline__ void wide_issue(typename C::Regs &rg, const unsigned 
     const bool exists = (i + 1 < C::UPT) || u < C::UNITS;
     const bool ok = ri >= 0 && exists;
     const uint32_t r = ok ? (uint32_t)ri : 0u;
-    rg.v[i] = i32x4{0, 0, 0, 0};
-    if (exists) rg.v[i] = ld_global_16(kv_b + r * row_pitch + c * 16);
-    if constexpr (FP8) rg.sc[i] = exists ? kv_scale_b[r * sc_pitch + (MX ? (uint32_t)(c >> 1) : 0u)] : 0.0f;
+    // unconditional: a unit past the block (or a masked slot) reads row 0, which
+    // wide_store drops, so every wave issues the same loads on every block
+    rg.v[i] = ld_global_16(kv_b + r * row_pitch + c * 16);
+    if constexpr (FP8) rg.sc[i] = kv_scale_b[r * sc_pitch + (MX ? (uint32_t)(c >> 1) : 0u)];
     valid |= (ok ? 1u : 0u) << i;
   }
   rg.valid = valid;
@@ -559,10 +560,20 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
   const uint32_t row_pitch = (uint32_t)(p.G * C::ROWB);
   const int nblk = (int)((p.topk + 31) / 32);
 
-  int idx_cur = load_slot_index(idx_row, 0, l32, p.topk, p.S_kv);
-  int idx_nxt = load_slot_index(idx_row, 1, l32, p.topk, p.S_kv);
+  // Indices (two blocks ahead), rows and CSR positions (one block ahead) are
+  // loaded unconditionally through resources that end at the item's top-k, and
+  // every partial-row store is unconditional (masked slots write the trash row
+  // past the entries), so each wave issues the same memory operations on every
+  // block and the compiler's waits count exactly: waiting for a block's rows
+  // or positions leaves the previous block's stores in flight.
+  const auto idx_rs = slot_rsrc(idx_row, p.topk);
+  const auto pos_rs = slot_rsrc(p.pos_of + entry0, p.topk);
+  int idx_cur = slot_index(load_slot_raw(idx_rs, 0, l32), 0, l32, p.topk, p.S_kv);
+  int raw_nxt = load_slot_raw(idx_rs, 1, l32);
   typename C::Regs rg;
   wide_issue<C, FP8>(rg, kv_b, kv_scale_b, idx_cur, row_pitch);
+  int pos_cur = load_slot_raw(pos_rs, 0, l32);
+  const uint64_t trash = (uint64_t)n_entries * (uint64_t)p.ntiles;  // partial row no entry owns
 
   float qsc = 1.0f;
   if constexpr (FP8) qsc = p.q_scale[tok];
@@ -654,16 +665,21 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
     for (int a = 0; a < 16; ++a) dqacc[q][a] = 0.0f;
 
   const int k0 = w * C::KQ, v0 = w * VQ;
+  // the first block's rows and positions have landed: nothing is in flight on
+  // entry, so the loop's waits follow its own order (s_waitcnt vmcnt(0) with
+  // expcnt and lgkmcnt left open, gfx9 encoding)
+  __builtin_amdgcn_s_waitcnt(0x0F70);
   for (int blk = 0; blk < nblk; ++blk) {
     const int slot0 = blk * 32;
     wide_store<C, FP8, C::NCH, L::KDB_STRIDE>(rg, Kl, Kd, Ksc);
     const bool valid = idx_cur >= 0;  // slot slot0 + l32
-    int32_t pos = -1;
-    if (valid) pos = p.pos_of[entry0 + slot0 + l32];
+    const int32_t pos = pos_cur;
     const bool wr = valid && pos >= 0 && pos < n_entries;  // (always true for a valid slot; a guard)
     __syncthreads();  // rows (and, on the first block, the prologue tiles) are in LDS
-    const int idx_nn = load_slot_index(idx_row, blk + 2, l32, p.topk, p.S_kv);
-    if (blk + 1 < nblk) wide_issue<C, FP8>(rg, kv_b, kv_scale_b, idx_nxt, row_pitch);
+    const int raw_nn = load_slot_raw(idx_rs, blk + 2, l32);
+    const int idx_nxt = slot_index(raw_nxt, blk + 1, l32, p.topk, p.S_kv);
+    wide_issue<C, FP8>(rg, kv_b, kv_scale_b, idx_nxt, row_pitch);  // past the last block too
+    const int pos_nxt = load_slot_raw(pos_rs, blk + 1, l32);
 
     // ---- partial S = Q K^T and dP = dO V^T (M = head, N = slot) over this wave's k-steps ----
     f32x16 sacc, dpacc;
@@ -779,15 +795,16 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
     }
 
     // ---- c^T[d][slot] = Q^T dS^T + dO^T P^T on tiles t = w + 4q (fp16 rows: times 2^pexp) ----
-    const int64_t prow = (int64_t)(wr ? pos : 0) * p.ntiles + tile;
-    unsigned char *dst = p.partials + prow * (int64_t)(D_QK * (F32P ? 4 : 2));
-    if constexpr (!F32P) {
-      if (wr && w == 0 && g32 == 0) p.partial_exp[prow] = (int8_t)pexp;
-    }
+    const uint64_t prow = wr ? (uint64_t)(uint32_t)pos * (uint32_t)p.ntiles + tile : trash;
+    unsigned char *dst = p.partials + prow * (uint64_t)(D_QK * (F32P ? 4 : 2));
+    if constexpr (!F32P) p.partial_exp[prow] = (int8_t)pexp;  // every wave and lane half stores the same byte
 #pragma unroll
     for (int q = 0; q < DQW; ++q) {
-      const int t = w + 4 * q;
-      if (t < DQT) {
+      // a wave without a tile of its own on the last step redoes tile DQT - 1
+      // and stores the same bits again, so that every wave issues the same
+      // stores on every block
+      const int t = w + 4 * q < DQT ? w + 4 * q : DQT - 1;
+      {
         f32x16 cacc;
 #pragma unroll
         for (int a = 0; a < 16; ++a) cacc[a] = 0.0f;
@@ -803,7 +820,7 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
             cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(av), pB[kc], cacc, 0, 0, 0);
           }
         }
-        if (wr) {
+        {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int d0 = t * 32 + 8 * i + 4 * g32;
@@ -822,7 +839,8 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
     }
     __syncthreads();  // rows, partial tiles and dS tiles consumed before the next block
     idx_cur = idx_nxt;
-    idx_nxt = idx_nn;
+    raw_nxt = raw_nn;
+    pos_cur = pos_nxt;
   }
 
   // ---- dQ: lane = head l32, d = t*32 + 8i + 4*g32 + j ----
