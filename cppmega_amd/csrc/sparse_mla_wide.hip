@@ -65,7 +65,10 @@ struct WideCfg {
 // (lane & 31) of this wave (-1: masked).
 // kv_scale_b holds one scale per row (sc_pitch 1) or, MX, one per 32-channel
 // block of every row (sc_pitch floats apart): a unit loads its own block's.
-template <class C, bool FP8, bool MX = false>
+// UNCOND (the backward): the loads are unconditional, a unit past the block
+// (or a masked slot) reading row 0, which wide_store drops, so that every wave
+// issues the same loads on every block.
+template <class C, bool FP8, bool MX = false, bool UNCOND = false>
 __device__ __forceinline__ void wide_issue(typename C::Regs &rg, const unsigned char *kv_b, const float *kv_scale_b,
                                            int my_idx, uint32_t row_pitch, uint32_t sc_pitch = 1u) {
   const int t = threadIdx.x;
@@ -79,10 +82,14 @@ __device__ __forceinline__ void wide_issue(typename C::Regs &rg, const unsigned 
     const bool exists = (i + 1 < C::UPT) || u < C::UNITS;
     const bool ok = ri >= 0 && exists;
     const uint32_t r = ok ? (uint32_t)ri : 0u;
-    // unconditional: a unit past the block (or a masked slot) reads row 0, which
-    // wide_store drops, so every wave issues the same loads on every block
-    rg.v[i] = ld_global_16(kv_b + r * row_pitch + c * 16);
-    if constexpr (FP8) rg.sc[i] = kv_scale_b[r * sc_pitch + (MX ? (uint32_t)(c >> 1) : 0u)];
+    if constexpr (UNCOND) {
+      rg.v[i] = ld_global_16(kv_b + r * row_pitch + c * 16);
+      if constexpr (FP8) rg.sc[i] = kv_scale_b[r * sc_pitch + (MX ? (uint32_t)(c >> 1) : 0u)];
+    } else {
+      rg.v[i] = i32x4{0, 0, 0, 0};
+      if (exists) rg.v[i] = ld_global_16(kv_b + r * row_pitch + c * 16);
+      if constexpr (FP8) rg.sc[i] = exists ? kv_scale_b[r * sc_pitch + (MX ? (uint32_t)(c >> 1) : 0u)] : 0.0f;
+    }
     valid |= (ok ? 1u : 0u) << i;
   }
   rg.valid = valid;
@@ -571,7 +578,7 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
   int idx_cur = slot_index(load_slot_raw(idx_rs, 0, l32), 0, l32, p.topk, p.S_kv);
   int raw_nxt = load_slot_raw(idx_rs, 1, l32);
   typename C::Regs rg;
-  wide_issue<C, FP8>(rg, kv_b, kv_scale_b, idx_cur, row_pitch);
+  wide_issue<C, FP8, false, true>(rg, kv_b, kv_scale_b, idx_cur, row_pitch);
   int pos_cur = load_slot_raw(pos_rs, 0, l32);
   const uint64_t trash = (uint64_t)n_entries * (uint64_t)p.ntiles;  // partial row no entry owns
 
@@ -678,7 +685,7 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
     __syncthreads();  // rows (and, on the first block, the prologue tiles) are in LDS
     const int raw_nn = load_slot_raw(idx_rs, blk + 2, l32);
     const int idx_nxt = slot_index(raw_nxt, blk + 1, l32, p.topk, p.S_kv);
-    wide_issue<C, FP8>(rg, kv_b, kv_scale_b, idx_nxt, row_pitch);  // past the last block too
+    wide_issue<C, FP8, false, true>(rg, kv_b, kv_scale_b, idx_nxt, row_pitch);  // past the last block too
     const int pos_nxt = load_slot_raw(pos_rs, blk + 1, l32);
 
     // ---- partial S = Q K^T and dP = dO V^T (M = head, N = slot) over this wave's k-steps ----
