@@ -101,12 +101,15 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
   // ---- key tile loads (thread: LOADS 16-byte chunks of the KT-key tile) ----
   // The resource of tile `it` starts at its first key and ends at the last key
   // row (Sk - 1), so keys past the end read zeros without per-lane checks.
-  uint32_t loff[C::LOADS];
-#pragma unroll
-  for (int l = 0; l < C::LOADS; ++l) {
-    const int u = tid + C::NT * l;
-    loff[l] = (uint32_t)(u / C::CPR) * row_pitch + (uint32_t)(u % C::CPR) * 16u;
-  }
+  // Thread tid loads chunk tid % CPR of keys tid / CPR + l * (NT / CPR): one
+  // per-thread offset, the l steps in the scalar offset of the load and in the
+  // immediate of the LDS store, so the tile loop keeps no per-load addresses
+  // live (they had spilled to scratch, and each reload's wait drained the
+  // score stores in flight)
+  static_assert(C::NT % C::CPR == 0, "whole keys per load round");
+  constexpr int KPR = C::NT / C::CPR;  // keys per load round
+  const uint32_t loff0 = (uint32_t)(tid / C::CPR) * row_pitch + (uint32_t)(tid % C::CPR) * 16u;
+  const int soff0 = (tid / C::CPR) * C::KS_STRIDE + (tid % C::CPR) * 16;
   auto load_tile = [&](int it, i32x4 (&r)[C::LOADS]) {
     const int64_t first = k0 + (int64_t)it * C::KT;
     const int64_t nkeys = p.Sk - first;
@@ -114,14 +117,13 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
     const auto rs = make_buffer_rsrc(k_b + (nkeys > 0 ? first : 0) * row_pitch, nb);
 #pragma unroll
     for (int l = 0; l < C::LOADS; ++l)
-      r[l] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)loff[l], 0, 0));
+      r[l] = __builtin_bit_cast(
+          i32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)loff0, (int)((uint32_t)(l * KPR) * row_pitch), 0));
   };
   auto store_tile = [&](int buf, const i32x4 (&r)[C::LOADS]) {
+    unsigned char *dst = &KS[buf][soff0];
 #pragma unroll
-    for (int l = 0; l < C::LOADS; ++l) {
-      const int u = tid + C::NT * l, key = u / C::CPR, c = u % C::CPR;
-      *reinterpret_cast<i32x4 *>(&KS[buf][key * C::KS_STRIDE + c * 16]) = r[l];
-    }
+    for (int l = 0; l < C::LOADS; ++l) *reinterpret_cast<i32x4 *>(dst + l * KPR * C::KS_STRIDE) = r[l];
   };
   i32x4 kreg[C::LOADS];
   load_tile(0, kreg);
@@ -243,6 +245,12 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
 
   store_tile(0, kreg);
   __syncthreads();
+  // every load of the prologue has landed (the first tile's keys just went to
+  // LDS): with nothing in flight on entry, the compiler's waits in the loop
+  // count only the loop's own operations, and the score stores of a tile stay
+  // in flight past the next tile's key loads (s_waitcnt vmcnt(0) with expcnt
+  // and lgkmcnt left open, gfx9 encoding)
+  __builtin_amdgcn_s_waitcnt(0x0F70);
   const int64_t wave_tok_last = wave_tok0 + C::TPW - 1;
   for (int it = 0; it < ntile; ++it) {
     load_tile(it + 1, kreg);  // past the last tile: keys beyond Sk read 0, unused
