@@ -175,6 +175,9 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
 
   // Scores of one 32-key sub-tile: part[tl] = sum over the wave's heads of token
   // tl held in this lane's accumulator rows (the other half-wave holds the rest).
+  // this lane's B-operand row and column group in a key tile; the sub-tile and
+  // k-step parts of the address are immediates of the LDS reads
+  const int brow_off = l32 * C::KS_STRIDE + 16 * g32;
   auto subtile = [&](const unsigned char *ks, int sub, float (&part)[C::TPW]) {
 #pragma unroll
     for (int tl = 0; tl < C::TPW; ++tl) part[tl] = 0.0f;
@@ -185,15 +188,15 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
       for (int a = 0; a < 16; ++a) acc[a] = 0.0f;
 #pragma unroll
       for (int k = 0; k < C::KSTEPS; ++k) {
-        const unsigned char *brow = ks + (sub * 32 + l32) * C::KS_STRIDE;
+        const unsigned char *brow = ks + brow_off + sub * 32 * C::KS_STRIDE;  // + 16 g32 folded in
         if constexpr (FP8) {
-          const i32x4 lo = *reinterpret_cast<const i32x4 *>(brow + 64 * k + 16 * g32);
-          const i32x4 hi = *reinterpret_cast<const i32x4 *>(brow + 64 * k + 32 + 16 * g32);
+          const i32x4 lo = *reinterpret_cast<const i32x4 *>(brow + 64 * k);
+          const i32x4 hi = *reinterpret_cast<const i32x4 *>(brow + 64 * k + 32);
           const i32x8 bv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
           // unit block scales (E8M0 127 = 2^0): a plain e4m3 product, two k-chunks of 32
           acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A[m][k], bv, acc, 0, 0, 0, 127, 0, 127);
         } else {
-          const i32x4 bv = *reinterpret_cast<const i32x4 *>(brow + (16 * k + 8 * g32) * 2);
+          const i32x4 bv = *reinterpret_cast<const i32x4 *>(brow + 32 * k);  // (16 k + 8 g32) bf16
           acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[m][k], as_bf16x8(bv), acc, 0, 0, 0);
         }
       }
