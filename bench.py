@@ -378,8 +378,7 @@ def time_graph(step, steps, warmup):
 def algorithmic_work():
     """Per-launch algorithmic work of each kernel at cfg2 / cfg3, and its bound.
 
-    The bound and the work follow the survey's measurement table: the indexer,
-    SparseMLA forward and backward are priced as MFMA work by the reference's
+    The indexer, SparseMLA forward and backward are priced as MFMA work by the reference's
     FLOP conventions (the forward also against its 112 MB of unique HBM
     traffic, whichever floor is longer), top-k as the HBM bytes it must read
     and write.  `io_bytes` are the bytes of the op's own inputs and outputs

@@ -248,12 +248,6 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
 
   store_tile(0, kreg);
   __syncthreads();
-  // every load of the prologue has landed (the first tile's keys just went to
-  // LDS): with nothing in flight on entry, the compiler's waits in the loop
-  // count only the loop's own operations, and the score stores of a tile stay
-  // in flight past the next tile's key loads (s_waitcnt vmcnt(0) with expcnt
-  // and lgkmcnt left open, gfx9 encoding)
-  __builtin_amdgcn_s_waitcnt(0x0F70);
   const int64_t wave_tok_last = wave_tok0 + C::TPW - 1;
   for (int it = 0; it < ntile; ++it) {
     load_tile(it + 1, kreg);  // past the last tile: keys beyond Sk read 0, unused
