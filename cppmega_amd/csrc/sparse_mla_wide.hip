@@ -278,8 +278,11 @@ sparse_mla_fwd_wide_kernel(const FwdParams p) {
   const uint32_t row_pitch = (uint32_t)(p.G * C::ROWB);
   const int nblk = (int)((p.topk + 31) / 32);
 
-  int idx_cur = load_slot_index(idx_row, 0, l32, p.topk, p.S_kv);
-  int idx_nxt = load_slot_index(idx_row, 1, l32, p.topk, p.S_kv);
+  // indices two blocks ahead as raw loads, masked where they are used a block
+  // later: the block loop never waits on an index load it has just issued
+  const auto idx_rs = slot_rsrc(idx_row, p.topk);
+  int idx_cur = slot_index(load_slot_raw(idx_rs, 0, l32), 0, l32, p.topk, p.S_kv);
+  int raw_nxt = load_slot_raw(idx_rs, 1, l32);
   typename C::Regs rg;
   wide_issue<C, FP8, MX>(rg, kv_b, kv_scale_b, idx_cur, row_pitch, sc_pitch);
 
@@ -330,7 +333,8 @@ sparse_mla_fwd_wide_kernel(const FwdParams p) {
     wide_store<C, FP8, C::NCH_V, C::KD_STRIDE, MX>(rg, Kl, Kd, Ksc);
     const uint64_t vmask = __ballot(idx_cur >= 0);
     __syncthreads();  // the block's rows are in LDS
-    const int idx_nn = load_slot_index(idx_row, blk + 2, l32, p.topk, p.S_kv);
+    const int raw_nn = load_slot_raw(idx_rs, blk + 2, l32);
+    const int idx_nxt = slot_index(raw_nxt, blk + 1, l32, p.topk, p.S_kv);
     if (blk + 1 < nblk) wide_issue<C, FP8, MX>(rg, kv_b, kv_scale_b, idx_nxt, row_pitch, sc_pitch);
 
     // ---- partial S^T = K Q^T over this wave's k-steps ----
@@ -425,7 +429,7 @@ sparse_mla_fwd_wide_kernel(const FwdParams p) {
     }
     __syncthreads();  // rows and partial tiles consumed before the next block overwrites them
     idx_cur = idx_nxt;
-    idx_nxt = idx_nn;
+    raw_nxt = raw_nn;
   }
 
   // ---- normalise and write: lane = head l32, d = (w + 4*dt)*32 + 8i + 4*g32 + j ----
