@@ -28,10 +28,22 @@ from __future__ import annotations
 
 import torch
 
+from . import dsa_topk
 from .dsa_splitk_indexer_loss import indexer_kl_loss
-from .dsa_topk import fused_qk_topk_naive
 
 __all__ = ["FusedDSAIndexerLoss", "apply_fused_indexer_loss_patch", "fused_dsa_indexer_loss"]
+
+# The Megatron dsa module this drop-in was installed into.  The top-k is looked
+# up on it at call time (cppmega/megatron/lemyx_dsa_warmup.py:166-176 imports
+# ``fused_qk_topk_naive`` from the dsa module inside ``apply``), so whatever is
+# bound there at that moment runs: the gfx950 top-k patch, or IndexCache's
+# capture wrapper around it while a Full layer's forward is running.
+_DSA_MODULE = None
+
+
+def _topk_fn():
+    fn = getattr(_DSA_MODULE, "fused_qk_topk_naive", None) if _DSA_MODULE is not None else None
+    return fn if fn is not None else dsa_topk.fused_qk_topk_naive
 
 
 def fused_dsa_indexer_loss(q, weights, k, query, key, softmax_scale, topk, loss_coeff, mask=None,
@@ -42,15 +54,18 @@ def fused_dsa_indexer_loss(q, weights, k, query, key, softmax_scale, topk, loss_
 
     q [sq, b, h_idx, d] bf16, weights [sq, b, h_idx] (f32 or bf16), k [sk, b, d]
     bf16; query [sq, b, np, hn] / key [sk, b, np or a divisor, hn] bf16 (the
-    attention inputs; no gradient).  ``query_valid_rows`` (padded packed rows)
-    is not supported and raises; ``pg_collection`` is accepted and not used, as
-    in cppmega's split-K loss.
+    attention inputs; no gradient).  ``query_valid_rows`` and ``pg_collection``
+    are accepted and not used, as in the lemyx drop-in
+    (cppmega/megatron/lemyx_dsa_warmup.py:86-178, which takes
+    ``query_valid_rows`` and never reads it) and cppmega's split-K loss.
+
+    The scores and top-k come from ``fused_qk_topk_naive`` as bound on the dsa
+    module that ``apply_fused_indexer_loss_patch`` installed this into, looked
+    up at call time; without one, from this package's gfx950 implementation.
     """
-    if query_valid_rows is not None:
-        raise NotImplementedError("query_valid_rows (padded packed rows) is not supported by the gfx950 indexer loss")
-    scores, topk_indices = fused_qk_topk_naive(q, k, weights, topk, mask=mask, varlen_starts=varlen_starts,
-                                               varlen_ends=varlen_ends, key_positions=key_positions,
-                                               use_relu=use_relu)
+    del query_valid_rows, pg_collection
+    scores, topk_indices = _topk_fn()(q, k, weights, topk, mask=mask, varlen_starts=varlen_starts,
+                                      varlen_ends=varlen_ends, key_positions=key_positions, use_relu=use_relu)
     loss = indexer_kl_loss(scores, topk_indices, query.detach(), key.detach(), softmax_scale, loss_coeff,
                            sparse_loss)
     return topk_indices, loss
@@ -79,12 +94,15 @@ def apply_fused_indexer_loss_patch(*, force: bool = False, dsa_module=None) -> b
     """Install ``FusedDSAIndexerLoss`` as Megatron's ``dsa.FusedDSAIndexerLoss``
     (what cppmega's apply_lemyx_dsa_patch does for its kernel,
     cppmega/megatron/lemyx_dsa_warmup.py:188-207).  Idempotent; raises when the
-    attribute is absent (Megatron version mismatch)."""
+    attribute is absent (Megatron version mismatch).  From then on the loss
+    takes its top-k from ``dsa_module.fused_qk_topk_naive``, resolved per call."""
+    global _DSA_MODULE
     if dsa_module is None:
         from megatron.core.transformer.experimental_attention_variant import dsa as dsa_module
     existing = getattr(dsa_module, "FusedDSAIndexerLoss", None)
     if existing is None:
         raise RuntimeError("dsa.FusedDSAIndexerLoss not found - Megatron version mismatch?")
+    _DSA_MODULE = dsa_module
     if getattr(existing, _MARKER, False) and not force:
         return True
     dsa_module.FusedDSAIndexerLoss = FusedDSAIndexerLoss

@@ -15,10 +15,18 @@ reference runs a Full layer's original forward and then derives the indices a
 second time (``forward_before_topk`` + an unmasked ``fused_qk_topk_naive``,
 :136-154), because the forward does not expose the ones it computed.  Here the
 Full layer computes them once: while its original forward runs, the dsa
-module's ``fused_qk_topk_naive`` is wrapped so the indices the layer itself
-selected (with its own mask, on its own inputs) are captured and cached.  Only
-when the forward never calls it does the layer fall back to the reference's
-re-derivation, done with this package's deterministic gfx950 indexer + top-k.
+module's ``fused_qk_topk_naive`` and ``FusedDSAIndexerLoss.apply`` (the
+indexer-loss path, which returns the top-k indices beside the loss) are
+wrapped so the indices the layer itself selected (with its own mask, on its
+own inputs) are captured and cached.  Only when the forward calls neither does
+the layer fall back to the reference's re-derivation, done with this package's
+deterministic gfx950 indexer + top-k and with the layer's own attention mask
+(``_build_dsattention_forward_mask``), so both routes cache the same picks.
+
+Deviation from the reference: the cached indices are the Full layer's masked
+picks (the ones its own sparse attention used), where the reference caches an
+unmasked ``mask=None`` top-k (index_cache_patch.py:148-153) whose rows may pick
+future keys that the Shared layers' mask then discards.
 Context-parallel gathers go through Megatron's
 ``gather_from_sequence_parallel_region`` exactly where the reference calls it.
 """
@@ -142,6 +150,18 @@ def apply_index_cache_patch(force: bool = False, dsa_module=None) -> bool:
     orig_init = cls.__init__
     orig_forward = cls.forward
 
+    def _layer_mask(self, sq, skv, b, device, attention_mask, attn_mask_type, position_ids, packed_seq_params):
+        """The layer's attention mask as Megatron builds it for sparse attention:
+        (float_mask, varlen_starts, varlen_ends, key_positions)."""
+        cp_group, cp_size, cp_rank = _cp_info(self.indexer)
+        float_mask, varlen = build_mask(
+            sq=sq, skv=skv, b=b, device=device, cp_size=cp_size, cp_rank=cp_rank,
+            cp_comm_type=normalize_cp(getattr(self, "cp_comm_type", None)), cp_group=cp_group,
+            attn_mask_type=attn_mask_type, attention_mask=attention_mask, position_ids=position_ids,
+            packed_seq_params=packed_seq_params, packed_query_positions=None)
+        starts, ends, key_positions = varlen if varlen is not None else (None, None, None)
+        return float_mask, starts, ends, key_positions
+
     def _ic_init(self, *args, **kwargs):
         orig_init(self, *args, **kwargs)
         self._ic_dsa_rank = counter[0]
@@ -162,9 +182,11 @@ def apply_index_cache_patch(force: bool = False, dsa_module=None) -> bool:
                 sched.promote(rank)
                 log.info("IndexCache: DSA rank %d auto-promoted to FULL (no preceding Full rank)", rank)
         if cached is None:
-            # compute once: keep what the layer's own top-k call returns
+            # compute once: keep what the layer's own top-k call returns, through
+            # the plain top-k or through the indexer-loss path
             captured = []
             inner = getattr(dsa_module, "fused_qk_topk_naive", None)
+            inner_loss = getattr(dsa_module, "FusedDSAIndexerLoss", None)
             if inner is not None:
                 def _capture(*a, **k):
                     res = inner(*a, **k)
@@ -172,11 +194,22 @@ def apply_index_cache_patch(force: bool = False, dsa_module=None) -> bool:
                     return res
 
                 dsa_module.fused_qk_topk_naive = _capture
+            if inner_loss is not None:
+                class _CaptureLoss:
+                    @staticmethod
+                    def apply(*a, **k):
+                        res = inner_loss.apply(*a, **k)
+                        captured.append(res[0])
+                        return res
+
+                dsa_module.FusedDSAIndexerLoss = _CaptureLoss
             try:
                 result = orig_forward(self, query, key, value, attention_mask, x, qr, **kw)
             finally:
                 if inner is not None:
                     dsa_module.fused_qk_topk_naive = inner
+                if inner_loss is not None:
+                    dsa_module.FusedDSAIndexerLoss = inner_loss
             if captured:
                 sched.store(rank, captured[-1].detach())
                 sched.captured += 1
@@ -184,10 +217,21 @@ def apply_index_cache_patch(force: bool = False, dsa_module=None) -> bool:
             sched.rederived += 1
             with torch.no_grad():
                 q_idx, k_idx, w_idx = self.indexer.forward_before_topk(x.detach(), qr.detach(), packed_seq_params)
-                cp_group, cp_size, _ = _cp_info(self.indexer)
-                if cp_size > 1 and k_idx.size(0) == query.size(0) and cp_gather is not None:
-                    k_idx = cp_gather(k_idx, group=cp_group)
-                _, idx = fused_qk_topk_naive(q_idx, k_idx, w_idx, self.indexer.index_topk, mask=None,
+                cp_group, cp_size, cp_rank = _cp_info(self.indexer)
+                q_sbhd, _ = ensure_sbhd(query, "query")
+                k_sbhd, _ = ensure_sbhd(key, "key")
+                sq_local, b = q_sbhd.size(0), q_sbhd.size(1)
+                skv = k_sbhd.size(0)
+                if cp_size > 1 and cp_gather is not None:
+                    if k_idx.size(0) == sq_local:
+                        k_idx = cp_gather(k_idx, group=cp_group)
+                    if skv == sq_local:
+                        skv *= cp_size
+                float_mask, starts, ends, key_positions = _layer_mask(
+                    self, sq_local, skv, b, x.device, attention_mask, attn_mask_type, position_ids,
+                    packed_seq_params)
+                _, idx = fused_qk_topk_naive(q_idx, k_idx, w_idx, self.indexer.index_topk, mask=float_mask,
+                                             varlen_starts=starts, varlen_ends=ends, key_positions=key_positions,
                                              use_relu=getattr(self.config, "dsa_indexer_scoring_relu", False))
                 sched.store(rank, idx)
             return result
@@ -210,12 +254,8 @@ def apply_index_cache_patch(force: bool = False, dsa_module=None) -> bool:
                 key = cp_gather(key, group=cp_group)
             if value is not None and value.size(0) == sq:
                 value = cp_gather(value, group=cp_group)
-        float_mask, varlen = build_mask(
-            sq=sq, skv=key.size(0), b=b, device=x.device, cp_size=cp_size, cp_rank=cp_rank,
-            cp_comm_type=normalize_cp(getattr(self, "cp_comm_type", None)), cp_group=cp_group,
-            attn_mask_type=attn_mask_type, attention_mask=attention_mask, position_ids=position_ids,
-            packed_seq_params=packed_seq_params, packed_query_positions=None)
-        starts, ends, key_positions = varlen if varlen is not None else (None, None, None)
+        float_mask, starts, ends, key_positions = _layer_mask(
+            self, sq, key.size(0), b, x.device, attention_mask, attn_mask_type, position_ids, packed_seq_params)
         output, _ = run_sparse(absorbed_mla=absorbed, query=query, key=key, value=value, up_v_weight=up_v_weight,
                                topk_indices=cached, softmax_scale=self.softmax_scale, config=self.config,
                                mask=float_mask, varlen_starts=starts, varlen_ends=ends,

@@ -94,3 +94,63 @@ def test_index_cache_computes_once_and_shares(dev, monkeypatch):
         assert torch.equal(o, outs[0])          # same indices, same inputs: same attention output
     sched = icp.get_schedule()
     assert sched.captured == 2 and sched.rederived == 0
+
+
+def test_index_cache_with_the_indexer_loss_path(dev, monkeypatch):
+    """Megatron's training path: the Full layer takes its indices from
+    dsa.FusedDSAIndexerLoss.apply, with this package's top-k, indexer-loss and
+    IndexCache patches all installed.  Each Full layer runs one masked indexer +
+    top-k (captured, nothing re-derived), the cached picks are bit-identical
+    to the causal indexer_topk, the Shared layers' outputs equal SparseMLA on
+    those picks, and the loss's gradient reaches the indexer inputs."""
+    from cppmega_amd import dsa_fused_indexer_loss as fil
+
+    S, B, H, D, DV = 256, 2, 32, 128, 64
+    monkeypatch.setenv("CPPMEGA_INDEX_CACHE_FULL_LAYERS", "0,3")
+    monkeypatch.setattr(icp, "_SCHEDULE", None)
+    monkeypatch.setattr(fil, "_DSA_MODULE", None)
+    ii = synthetic.indexer_inputs(B, S, 16, 64, seed=63)
+    qi = ii["q"].to(dev).requires_grad_()
+    ki = ii["k"].to(dev).requires_grad_()
+    wi = ii["w"].to(dev).requires_grad_()
+    calls = []
+    mod = _module(dev, S, calls)
+    causal = mod._build_dsattention_forward_mask()[0]
+    mod.FusedDSAIndexerLoss = type("MegatronFusedDSAIndexerLoss", (), {})
+    losses = []
+
+    def forward(self, query, key, value, attention_mask, x, qr, **kw):
+        ix = self.indexer
+        idx, loss = mod.FusedDSAIndexerLoss.apply(ix.qi, ix.wi, ix.ki, query, key, self.softmax_scale,
+                                                  ix.index_topk, 1.0, causal, True, None)
+        losses.append(loss)
+        calls.append(("full", idx))
+        return sparse_mla_as_unfused_dsa(query, key, value, idx, self.softmax_scale)
+
+    mod.DSAttention.forward = forward
+    assert fil.apply_fused_indexer_loss_patch(dsa_module=mod)
+    assert icp.apply_index_cache_patch(dsa_module=mod)
+    layers = [mod.DSAttention(_Indexer(qi, ki, wi)) for _ in range(6)]
+    g = torch.Generator().manual_seed(64)
+    query = (torch.randn((S, B, H, D), generator=g) * 0.5).to(torch.bfloat16).to(dev)
+    key = (torch.randn((S, B, 1, D), generator=g) * 0.5).to(torch.bfloat16).to(dev).expand(S, B, H, D)
+    value = key[..., :DV]
+    x = torch.zeros(S, B, 8, device=dev)
+    outs = [layer.forward(query, key, value, None, x, x) for layer in layers]
+    assert [c[0] for c in calls] == ["full", "shared", "shared", "full", "shared", "shared"]
+    sched = icp.get_schedule()
+    assert sched.captured == 2 and sched.rederived == 0
+    with torch.no_grad():
+        ref = indexer_topk(qi.detach(), ki.detach(), wi.detach(), 64, causal=True).to(torch.int64)
+    full_idx = calls[0][1]
+    assert torch.equal(full_idx, ref)
+    for c in calls[1:3] + calls[4:]:
+        assert torch.equal(c[1], full_idx)
+    on_picks = sparse_mla_as_unfused_dsa(query, key, value, full_idx, 128 ** -0.5)
+    for o in outs:
+        assert torch.equal(o, on_picks)
+    assert len(losses) == 2 and all(bool(torch.isfinite(l)) for l in losses)
+    losses[0].backward()
+    for t in (qi, ki, wi):
+        assert t.grad is not None and bool(torch.isfinite(t.grad.float()).all()) and bool(t.grad.abs().sum() > 0)
+    assert mod.FusedDSAIndexerLoss is fil.FusedDSAIndexerLoss

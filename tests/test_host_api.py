@@ -277,8 +277,10 @@ def test_index_scores_patch_keeps_autograd(monkeypatch):
     assert r.requires_grad
 
 
-def test_fused_indexer_loss_patch_rebinds_the_module():
+def test_fused_indexer_loss_patch_rebinds_the_module(monkeypatch):
     from cppmega_amd import dsa_fused_indexer_loss as fil
+
+    monkeypatch.setattr(fil, "_DSA_MODULE", None)
 
     class Megatrons:
         @staticmethod
@@ -289,10 +291,173 @@ def test_fused_indexer_loss_patch_rebinds_the_module():
     assert fil.apply_fused_indexer_loss_patch(dsa_module=mod)
     assert mod.FusedDSAIndexerLoss is fil.FusedDSAIndexerLoss
     assert fil.apply_fused_indexer_loss_patch(dsa_module=mod)
+    assert fil._DSA_MODULE is mod
     with pytest.raises(RuntimeError):
         fil.apply_fused_indexer_loss_patch(dsa_module=types.SimpleNamespace())
-    with pytest.raises(NotImplementedError):
-        fil.fused_dsa_indexer_loss(None, None, None, None, None, 0.1, 4, 1.0, query_valid_rows=torch.ones(1))
+
+
+def test_fused_indexer_loss_resolves_topk_at_call_time(monkeypatch):
+    """The loss takes its scores and top-k from the dsa module's
+    fused_qk_topk_naive as bound at call time (lemyx_dsa_warmup.py:166-176
+    imports it inside apply), and accepts and ignores query_valid_rows
+    (lemyx_dsa_warmup.py:101)."""
+    from cppmega_amd import dsa_fused_indexer_loss as fil
+
+    monkeypatch.setattr(fil, "_DSA_MODULE", None)
+    seen = []
+
+    def kl(scores, idx, query, key, scale, coeff, sparse):
+        seen.append(("kl", scores, idx, sparse))
+        return torch.tensor(0.25)
+
+    monkeypatch.setattr(fil, "indexer_kl_loss", kl)
+
+    def first(q, k, w, topk, mask=None, varlen_starts=None, varlen_ends=None, key_positions=None, use_relu=True):
+        seen.append(("first", mask, use_relu))
+        return "scores-1", "idx-1"
+
+    def second(q, k, w, topk, **kw):
+        seen.append(("second", kw["mask"]))
+        return "scores-2", "idx-2"
+
+    mod = types.SimpleNamespace(FusedDSAIndexerLoss=object, fused_qk_topk_naive=first)
+    assert fil.apply_fused_indexer_loss_patch(dsa_module=mod)
+    t = torch.zeros(2, 1, 1, 1)
+    idx, loss = mod.FusedDSAIndexerLoss.apply(t, t, t, t, t, 0.1, 4, 1.0, "m", True, None,
+                                              query_valid_rows=torch.ones(2, dtype=torch.int32), use_relu=False)
+    assert (idx, float(loss)) == ("idx-1", 0.25)
+    mod.fused_qk_topk_naive = second                  # rebinding after the patch takes effect on the next call
+    idx, _ = mod.FusedDSAIndexerLoss.apply(t, t, t, t, t, 0.1, 4, 1.0, "m2", False, None)
+    assert idx == "idx-2"
+    assert seen == [("first", "m", False), ("kl", "scores-1", "idx-1", True), ("second", "m2"),
+                    ("kl", "scores-2", "idx-2", False)]
+
+
+def _loss_layer_module(calls, loss_cls_factory):
+    """A fake dsa module whose DSAttention takes its indices from
+    FusedDSAIndexerLoss.apply (Megatron's training path with the indexer loss)."""
+    mod = _fake_dsa_module(calls)
+    topk_calls = []
+
+    def module_topk(q, k, w, topk, mask=None, **kw):
+        topk_calls.append((int(q), mask))
+        return "scores", torch.tensor([int(q), -1])
+
+    mod.fused_qk_topk_naive = module_topk
+    mod.FusedDSAIndexerLoss = loss_cls_factory(mod)
+
+    def forward(self, query, key, value, attention_mask, x, qr, **kw):
+        idx, loss = mod.FusedDSAIndexerLoss.apply(x, None, qr, query, key, 0.1, 2, 1.0, "causal", True, None)
+        calls.append(("full", self._ic_dsa_rank, idx.tolist()))
+        return "full-out"
+
+    mod.DSAttention.forward = forward
+    return mod, topk_calls
+
+
+def test_index_cache_captures_indices_of_the_indexer_loss_path(monkeypatch):
+    """Both patches installed (this package's FusedDSAIndexerLoss and
+    IndexCache), the Full layers take their indices from
+    FusedDSAIndexerLoss.apply: each Full layer runs one top-k, its masked
+    picks are cached, nothing is re-derived."""
+    from cppmega_amd import dsa_fused_indexer_loss as fil
+
+    monkeypatch.setattr(fil, "_DSA_MODULE", None)
+    monkeypatch.setattr(fil, "indexer_kl_loss", lambda *a: torch.tensor(0.5))
+    monkeypatch.setenv("CPPMEGA_INDEX_CACHE_FULL_LAYERS", "0,3")
+    monkeypatch.setattr(icp, "_SCHEDULE", None)
+
+    def rederive(*a, **k):
+        raise AssertionError("the Full layer must not run a second indexer + top-k pass")
+
+    monkeypatch.setattr(icp, "fused_qk_topk_naive", rederive)
+    calls = []
+
+    def factory(mod):
+        class Megatrons:
+            @staticmethod
+            def apply(*a, **kw):
+                raise AssertionError("replaced by the gfx950 drop-in")
+        return Megatrons
+
+    mod, topk_calls = _loss_layer_module(calls, factory)
+    assert fil.apply_fused_indexer_loss_patch(dsa_module=mod)
+    assert icp.apply_index_cache_patch(dsa_module=mod)
+    layers = [mod.DSAttention(i) for i in range(6)]
+    q4 = torch.zeros(4, 1, 2, 8)
+    outs = [layer.forward(q4, q4, None, None, torch.tensor(20 + i), torch.tensor(0), None)
+            for i, layer in enumerate(layers)]
+    assert outs == ["full-out", "shared-out", "shared-out", "full-out", "shared-out", "shared-out"]
+    assert topk_calls == [(20, "causal"), (23, "causal")]        # one masked top-k per Full layer
+    shared = [c[1].tolist() for c in calls if c[0] == "shared"]
+    assert shared == [[20, -1], [20, -1], [23, -1], [23, -1]]
+    assert mod.FusedDSAIndexerLoss is fil.FusedDSAIndexerLoss   # wrappers removed after the forward
+    sched = icp.get_schedule()
+    assert sched.captured == 2 and sched.rederived == 0
+
+
+def test_index_cache_captures_a_loss_bound_at_import(monkeypatch):
+    """An indexer loss that imported its top-k at load time (so the module's
+    fused_qk_topk_naive is never called) is still captured, through the
+    FusedDSAIndexerLoss.apply wrapper."""
+    monkeypatch.setenv("CPPMEGA_INDEX_CACHE_FULL_LAYERS", "0")
+    monkeypatch.setattr(icp, "_SCHEDULE", None)
+    monkeypatch.setattr(icp, "fused_qk_topk_naive",
+                        lambda *a, **k: (_ for _ in ()).throw(AssertionError("no re-derivation")))
+    calls = []
+
+    def factory(mod):
+        class BoundAtImport:
+            @staticmethod
+            def apply(q, w, k, *rest, **kw):
+                return torch.tensor([int(q), 7]), torch.tensor(0.0)
+        return BoundAtImport
+
+    mod, topk_calls = _loss_layer_module(calls, factory)
+    assert icp.apply_index_cache_patch(dsa_module=mod)
+    layers = [mod.DSAttention(i) for i in range(3)]
+    q4 = torch.zeros(4, 1, 2, 8)
+    outs = [layer.forward(q4, q4, None, None, torch.tensor(30 + i), torch.tensor(0), None)
+            for i, layer in enumerate(layers)]
+    assert outs == ["full-out", "shared-out", "shared-out"] and topk_calls == []
+    assert [c[1].tolist() for c in calls if c[0] == "shared"] == [[30, 7], [30, 7]]
+    sched = icp.get_schedule()
+    assert sched.captured == 1 and sched.rederived == 0
+
+
+def test_index_cache_fallback_uses_the_layer_mask(monkeypatch):
+    """A Full forward that calls neither top-k entry falls back to a second
+    pass, which selects with the layer's own attention mask and varlen windows
+    (so it caches what the layer would have picked)."""
+    monkeypatch.setenv("CPPMEGA_INDEX_CACHE_FULL_LAYERS", "0")
+    monkeypatch.setattr(icp, "_SCHEDULE", None)
+    seen = []
+
+    def rederive(q, k, w, topk, mask=None, varlen_starts=None, varlen_ends=None, key_positions=None,
+                 use_relu=False):
+        seen.append((mask, varlen_starts, varlen_ends, key_positions, topk))
+        return None, "picks"
+
+    monkeypatch.setattr(icp, "fused_qk_topk_naive", rederive)
+    calls = []
+    mod = _fake_dsa_module(calls)
+    built = []
+
+    def build_mask(**kw):
+        built.append((kw["sq"], kw["skv"], kw["b"]))
+        return "layer-mask", ("st", "en", "kp")
+
+    mod._build_dsattention_forward_mask = build_mask
+    assert icp.apply_index_cache_patch(dsa_module=mod)
+    layers = [mod.DSAttention(i) for i in range(2)]
+    q = torch.zeros(5, 3, 2, 8)
+    outs = [layer.forward(q, q, None, None, torch.tensor(1), torch.tensor(0), None) for layer in layers]
+    assert outs == ["full-out", "shared-out"]
+    assert seen == [("layer-mask", "st", "en", "kp", 2)]
+    assert built[0] == (5, 5, 3)
+    assert calls[-1] == ("shared", "picks")
+    sched = icp.get_schedule()
+    assert sched.captured == 0 and sched.rederived == 1
 
 
 # ---------------------------------------------------------------------------
