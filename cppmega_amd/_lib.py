@@ -38,7 +38,6 @@ EXPORTED_SYMBOLS = (
     "dsa_sparse_mla_fwd_workspace_size",
     "dsa_sparse_mla_fwd_ws",
     "dsa_sparse_mla_bwd_workspace_size",
-    "dsa_sparse_mla_bwd_pass_bytes",
     "dsa_sparse_mla_bwd_index_size",
     "dsa_sparse_mla_bwd_indexed_workspace_size",
     "dsa_sparse_mla_bwd_build_index",
@@ -71,6 +70,7 @@ _i64 = ctypes.c_int64
 _i32 = ctypes.c_int
 _f32 = ctypes.c_float
 _size_t = ctypes.c_size_t
+_u64 = ctypes.c_uint64
 
 _SIGNATURES = {
     "dsa_last_error": (ctypes.c_char_p, []),
@@ -83,17 +83,17 @@ _SIGNATURES = {
     "dsa_sparse_mla_fwd_ws": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                      _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                      _f32, _i32, _c_void_p, _c_void_p, _c_void_p, _size_t, _c_void_p]),
-    "dsa_sparse_mla_bwd_workspace_size": (_size_t, [_i64] * 8 + [_i32]),
-    "dsa_sparse_mla_bwd_pass_bytes": (_i32, [ctypes.c_uint64]),
-    "dsa_sparse_mla_bwd_index_size": (_size_t, [_i64] * 8 + [_i32]),
-    "dsa_sparse_mla_bwd_indexed_workspace_size": (_size_t, [_i64] * 8 + [_i32]),
-    "dsa_sparse_mla_bwd_build_index": (_i32, [_c_void_p] + [_i64] * 8 + [_i32, _c_void_p, _size_t, _c_void_p]),
+    "dsa_sparse_mla_bwd_workspace_size": (_size_t, [_i64] * 8 + [_i32, _u64]),
+    "dsa_sparse_mla_bwd_index_size": (_size_t, [_i64] * 8 + [_i32, _u64]),
+    "dsa_sparse_mla_bwd_indexed_workspace_size": (_size_t, [_i64] * 8 + [_i32, _u64]),
+    "dsa_sparse_mla_bwd_build_index": (_i32, [_c_void_p] + [_i64] * 8 + [_i32, _u64, _c_void_p, _size_t,
+                                                                          _c_void_p]),
     "dsa_sparse_mla_bwd_indexed": (_i32, [_c_void_p] * 9 + [_c_void_p, _size_t, _c_void_p, _size_t] + [_i64] * 8
-                                   + [_f32, _i32, _c_void_p, _c_void_p, _i32, _c_void_p]),
+                                   + [_f32, _i32, _c_void_p, _c_void_p, _i32, _u64, _c_void_p]),
     "dsa_sparse_mla_bwd": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                   _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _size_t,
                                   _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-                                  _f32, _i32, _c_void_p, _c_void_p, _i32, _c_void_p]),
+                                  _f32, _i32, _c_void_p, _c_void_p, _i32, _u64, _c_void_p]),
     "dsa_indexer_scores": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                   _i64, _i64, _i64, _i64, _i64, _i32, _i32,
                                   _c_void_p, _c_void_p, _i32, _i32, _c_void_p]),

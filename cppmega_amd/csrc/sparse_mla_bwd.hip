@@ -36,8 +36,6 @@
 //                                 gets runs of 8 consecutive d of one slot;
 //   dQ^T[d][head] = K^T dS^T      M = d, N = head, K = slot: both operands
 //                                 transposed-read (K tile, dS[slot][head] tile).
-#include <atomic>
-
 #include "dsa_common.hpp"
 #include "sparse_mla_csr.hpp"
 #include "sparse_mla_gather.hpp"
@@ -611,7 +609,9 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // carried between them in fp32 (first pass stores, later passes add, the
 // last casts to bf16), in pass order, so the result stays deterministic.
 constexpr uint64_t kBwdPassBytes = 4ull << 30;  // default: partial rows (+ exponents) per pass
-static std::atomic<uint64_t> g_pass_bytes{kBwdPassBytes};
+
+// The per-pass cap of a call: its pass_bytes argument, 0 meaning the default.
+static uint64_t pass_cap(uint64_t pass_bytes) { return pass_bytes == 0 ? kBwdPassBytes : pass_bytes; }
 
 struct BwdPlan {
   int64_t nb;   // batches per pass
@@ -626,12 +626,12 @@ static int64_t partial_elem_bytes(int flags, int64_t D_qk) {
   return (flags & DSA_BWD_FP32_PARTIALS) ? 4 : 2;
 }
 
-static BwdPlan bwd_plan(int64_t B, int64_t S, int64_t H, int64_t G, int64_t D_qk, int64_t topk, int flags) {
+static BwdPlan bwd_plan(int64_t B, int64_t S, int64_t H, int64_t G, int64_t D_qk, int64_t topk, int flags,
+                        uint64_t cap) {
   const int64_t hpg = H / (G > 0 ? G : 1);
   const int64_t ntiles = (hpg + 31) / 32;
   const uint64_t per_token = (uint64_t)(G * topk * ntiles) * (uint64_t)(D_qk * partial_elem_bytes(flags, D_qk) + 1);
   BwdPlan pl;
-  const uint64_t cap = g_pass_bytes.load();
   if ((uint64_t)S * per_token <= cap) {
     pl.ct = S;
     pl.npb = 1;
@@ -661,11 +661,11 @@ struct BwdWorkspace {
 };
 
 static BwdWorkspace bwd_layout(int64_t B, int64_t S, int64_t S_kv, int64_t H, int64_t G, int64_t D_qk,
-                               int64_t topk, int flags) {
+                               int64_t topk, int flags, uint64_t pass_bytes) {
   const int64_t hpg = H / (G > 0 ? G : 1);
   const int ntiles = (int)((hpg + 31) / 32);
   BwdWorkspace L;
-  L.plan = bwd_plan(B, S, H, G, D_qk, topk, flags);
+  L.plan = bwd_plan(B, S, H, G, D_qk, topk, flags, pass_cap(pass_bytes));
   const BwdPlan &pl = L.plan;
   const size_t entries = (size_t)pl.nb * pl.ct * G * topk;  // of one pass
   const int64_t R = S_kv * G;
@@ -769,16 +769,12 @@ static int launch_reduce(const CsrParams &cp, const unsigned char *partials, con
 
 using namespace dsa;
 
-extern "C" int dsa_sparse_mla_bwd_pass_bytes(uint64_t bytes) {
-  g_pass_bytes.store(bytes == 0 ? kBwdPassBytes : bytes);
-  return DSA_OK;
-}
-
 extern "C" size_t dsa_sparse_mla_bwd_workspace_size(int64_t B, int64_t S, int64_t S_kv, int64_t H, int64_t G,
-                                                    int64_t D_qk, int64_t D_v, int64_t topk, int flags) {
+                                                    int64_t D_qk, int64_t D_v, int64_t topk, int flags,
+                                                    uint64_t pass_bytes) {
   (void)D_v;
   if (B <= 0 || S <= 0 || S_kv <= 0 || H <= 0 || G <= 0 || topk <= 0 || D_qk <= 0) return 0;
-  return bwd_layout(B, S, S_kv, H, G, D_qk, topk, flags).total;
+  return bwd_layout(B, S, S_kv, H, G, D_qk, topk, flags, pass_bytes).total;
 }
 
 static int bwd_check(const char *fn, int64_t B, int64_t S, int64_t S_kv, int64_t H, int64_t G, int64_t D_qk,
@@ -902,7 +898,7 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
                                   void *dkv, void *workspace, size_t workspace_bytes, int64_t B, int64_t S,
                                   int64_t S_kv, int64_t H, int64_t G, int64_t D_qk, int64_t D_v, int64_t topk,
                                   float sm_scale, int dtype, const float *q_scale, const float *kv_scale,
-                                  int flags, void *stream) {
+                                  int flags, uint64_t pass_bytes, void *stream) {
   int rc = bwd_check("dsa_sparse_mla_bwd", B, S, S_kv, H, G, D_qk, D_v, topk, dtype, flags);
   if (rc) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -911,7 +907,7 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
   DSA_REQUIRE(q && kv && o && dO && indices && lse2 && dq, "dsa_sparse_mla_bwd: null tensor pointer");
   if (dtype == DSA_DTYPE_E4M3)
     DSA_REQUIRE(q_scale && kv_scale, "dsa_sparse_mla_bwd: e4m3 input needs q_scale and kv_scale");
-  const BwdWorkspace L = bwd_layout(B, S, S_kv, H, G, D_qk, topk, flags);
+  const BwdWorkspace L = bwd_layout(B, S, S_kv, H, G, D_qk, topk, flags, pass_bytes);
   if (!workspace || workspace_bytes < L.total)
     return set_error(DSA_ERR_WORKSPACE, "dsa_sparse_mla_bwd: workspace %zu < required %zu", workspace_bytes,
                      L.total);
@@ -922,28 +918,30 @@ extern "C" int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o, 
 }
 
 extern "C" size_t dsa_sparse_mla_bwd_index_size(int64_t B, int64_t S, int64_t S_kv, int64_t H, int64_t G,
-                                                int64_t D_qk, int64_t D_v, int64_t topk, int flags) {
+                                                int64_t D_qk, int64_t D_v, int64_t topk, int flags,
+                                                uint64_t pass_bytes) {
   (void)D_v;
   if (B <= 0 || S <= 0 || S_kv <= 0 || H <= 0 || G <= 0 || topk <= 0 || D_qk <= 0) return 0;
-  const BwdWorkspace L = bwd_layout(B, S, S_kv, H, G, D_qk, topk, flags);
+  const BwdWorkspace L = bwd_layout(B, S, S_kv, H, G, D_qk, topk, flags, pass_bytes);
   return bwd_passes(L.plan, B) == 1 ? L.index_total : 0;  // several passes rebuild it per pass
 }
 
 extern "C" size_t dsa_sparse_mla_bwd_indexed_workspace_size(int64_t B, int64_t S, int64_t S_kv, int64_t H,
                                                             int64_t G, int64_t D_qk, int64_t D_v, int64_t topk,
-                                                            int flags) {
+                                                            int flags, uint64_t pass_bytes) {
   (void)D_v;
   if (B <= 0 || S <= 0 || S_kv <= 0 || H <= 0 || G <= 0 || topk <= 0 || D_qk <= 0) return 0;
-  return bwd_layout(B, S, S_kv, H, G, D_qk, topk, flags).rows_total;
+  return bwd_layout(B, S, S_kv, H, G, D_qk, topk, flags, pass_bytes).rows_total;
 }
 
 extern "C" int dsa_sparse_mla_bwd_build_index(const int32_t *indices, int64_t B, int64_t S, int64_t S_kv, int64_t H,
                                               int64_t G, int64_t D_qk, int64_t D_v, int64_t topk, int flags,
-                                              void *index, size_t index_bytes, void *stream) {
+                                              uint64_t pass_bytes, void *index, size_t index_bytes,
+                                              void *stream) {
   int rc = bwd_check("dsa_sparse_mla_bwd_build_index", B, S, S_kv, H, G, D_qk, D_v, topk, DSA_DTYPE_BF16, flags);
   if (rc) return rc;
   if (B == 0 || S == 0) return DSA_OK;
-  const BwdWorkspace L = bwd_layout(B, S, S_kv, H, G, D_qk, topk, flags);
+  const BwdWorkspace L = bwd_layout(B, S, S_kv, H, G, D_qk, topk, flags, pass_bytes);
   DSA_REQUIRE(bwd_passes(L.plan, B) == 1,
               "dsa_sparse_mla_bwd_build_index: this backward runs in several passes (no prebuilt index)");
   DSA_REQUIRE(indices, "dsa_sparse_mla_bwd_build_index: null indices");
@@ -961,7 +959,7 @@ extern "C" int dsa_sparse_mla_bwd_indexed(const void *q, const void *kv, const v
                                           size_t workspace_bytes, int64_t B, int64_t S, int64_t S_kv, int64_t H,
                                           int64_t G, int64_t D_qk, int64_t D_v, int64_t topk, float sm_scale,
                                           int dtype, const float *q_scale, const float *kv_scale, int flags,
-                                          void *stream) {
+                                          uint64_t pass_bytes, void *stream) {
   int rc = bwd_check("dsa_sparse_mla_bwd_indexed", B, S, S_kv, H, G, D_qk, D_v, topk, dtype, flags);
   if (rc) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -970,7 +968,7 @@ extern "C" int dsa_sparse_mla_bwd_indexed(const void *q, const void *kv, const v
   DSA_REQUIRE(q && kv && o && dO && indices && lse2 && dq, "dsa_sparse_mla_bwd_indexed: null tensor pointer");
   if (dtype == DSA_DTYPE_E4M3)
     DSA_REQUIRE(q_scale && kv_scale, "dsa_sparse_mla_bwd_indexed: e4m3 input needs q_scale and kv_scale");
-  const BwdWorkspace L = bwd_layout(B, S, S_kv, H, G, D_qk, topk, flags);
+  const BwdWorkspace L = bwd_layout(B, S, S_kv, H, G, D_qk, topk, flags, pass_bytes);
   if (S == 0) return bwd_zero_dkv(dkv, B * S_kv * G, D_qk, st);
   DSA_REQUIRE(bwd_passes(L.plan, B) == 1,
               "dsa_sparse_mla_bwd_indexed: this backward runs in several passes (use dsa_sparse_mla_bwd)");

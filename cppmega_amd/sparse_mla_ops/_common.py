@@ -16,14 +16,31 @@ def normalize_sm_scale(sm_scale, d_qk: int) -> float:
     return float(sm_scale)
 
 
+_NOT_LOOKED_UP = object()
+_QUANTIZED_TENSOR = _NOT_LOOKED_UP
+
+
+def _quantized_tensor_type():
+    """Transformer Engine's QuantizedTensor class, or None without TE.  Looked up
+    once per process: a failed import is not cached by Python, and this runs
+    several times per SparseMLA call."""
+    global _QUANTIZED_TENSOR
+    if _QUANTIZED_TENSOR is _NOT_LOOKED_UP:
+        try:
+            from transformer_engine.pytorch.tensor import QuantizedTensor  # type: ignore
+        except ImportError:
+            QuantizedTensor = None
+        _QUANTIZED_TENSOR = QuantizedTensor
+    return _QUANTIZED_TENSOR
+
+
 def unwrap_quantized(t):
     """Dequantise a Transformer-Engine QuantizedTensor if one is passed (TE is
     optional; plain tensors are returned unchanged)."""
-    try:
-        from transformer_engine.pytorch.tensor import QuantizedTensor  # type: ignore
-    except ImportError:
+    if isinstance(t, torch.Tensor) and type(t) is torch.Tensor:
         return t
-    if isinstance(t, QuantizedTensor):
+    qt = _quantized_tensor_type()
+    if qt is not None and isinstance(t, qt):
         return t.dequantize()
     return t
 

@@ -62,11 +62,21 @@ def _bwd_flags(fp32_partials):
     return _lib.BWD_FP32_PARTIALS if fp32_partials else 0
 
 
-def build_inverse_index(q, kv, indices, d_v, *, fp32_partials=None, stream=None, after=None):
+def _pass_bytes(pass_bytes):
+    """The C-ABI's per-pass cap on the partial dKV rows: 0 selects its default (4 GiB)."""
+    if pass_bytes is None:
+        return 0
+    pass_bytes = int(pass_bytes)
+    if pass_bytes < 0:
+        raise ValueError(f"pass_bytes must be >= 0, got {pass_bytes}")
+    return pass_bytes
+
+
+def build_inverse_index(q, kv, indices, d_v, *, fp32_partials=None, stream=None, after=None, pass_bytes=None):
     """Build the backward's inverse index for q [B,S,H,D] (or 3-D), kv
     [B,S_kv,G,D] and indices [B,S,G,topk] int32; returns an ``InverseIndex``,
     or None when the backward runs in several passes (it then builds its index
-    per pass).  With ``stream`` (e.g. ``side_stream(q.device)``) the build runs
+    per pass; ``pass_bytes`` is the per-pass cap, as for ``sparse_mla_bwd``).  With ``stream`` (e.g. ``side_stream(q.device)``) the build runs
     there after the work already queued on the current stream (or, with
     ``after``, a ``torch.cuda.Event`` recorded on it, after the work up to
     that event: work queued since, such as the forward kernel, does not delay
@@ -78,8 +88,9 @@ def build_inverse_index(q, kv, indices, d_v, *, fp32_partials=None, stream=None,
     _, S_kv, G, _ = kv.shape
     topk = indices.shape[-1]
     flags = _bwd_flags(fp32_partials)
+    cap = _pass_bytes(pass_bytes)
     L = _lib.load()
-    n = int(L.dsa_sparse_mla_bwd_index_size(B, S, S_kv, H, G, D, int(d_v), topk, flags))
+    n = int(L.dsa_sparse_mla_bwd_index_size(B, S, S_kv, H, G, D, int(d_v), topk, flags, cap))
     if n == 0:
         return None
     cur = torch.cuda.current_stream(q.device)
@@ -90,7 +101,7 @@ def build_inverse_index(q, kv, indices, d_v, *, fp32_partials=None, stream=None,
             side.wait_event(after)
         else:
             side.wait_stream(cur)
-    rc = L.dsa_sparse_mla_bwd_build_index(indices.data_ptr(), B, S, S_kv, H, G, D, int(d_v), topk, flags,
+    rc = L.dsa_sparse_mla_bwd_build_index(indices.data_ptr(), B, S, S_kv, H, G, D, int(d_v), topk, flags, cap,
                                           buf.data_ptr(), n, side.cuda_stream)
     _lib.check(rc, "dsa_sparse_mla_bwd_build_index")
     event = None
@@ -100,42 +111,45 @@ def build_inverse_index(q, kv, indices, d_v, *, fp32_partials=None, stream=None,
             indices.record_stream(side)
         event = torch.cuda.Event()
         event.record(side)
-    return InverseIndex(buf, event, (B, S, S_kv, H, G, D, int(d_v), topk, flags, indices.data_ptr()))
+    return InverseIndex(buf, event, (B, S, S_kv, H, G, D, int(d_v), topk, flags, cap, indices.data_ptr()))
 
 
 def _launch_bwd(q, kv, o, do, indices, lse, delta, sm_scale, dtype_code, q_scale=None, kv_scale=None,
-                fp32_partials=None, inverse_index=None):
+                fp32_partials=None, inverse_index=None, pass_bytes=None):
     B, S, H, D = q.shape
     _, S_kv, G, _ = kv.shape
     d_v = o.shape[-1]
     topk = indices.shape[-1]
     flags = _bwd_flags(fp32_partials)
+    cap = _pass_bytes(pass_bytes)
     L = _lib.load()
     dq = torch.empty((B, S, H, D), dtype=torch.bfloat16, device=q.device)
     dkv = torch.empty((B, S_kv, G, D), dtype=torch.bfloat16, device=q.device)
     _, stream = stream_of(q)
     if inverse_index is not None:
-        key = (B, S, S_kv, H, G, D, d_v, topk, flags, indices.data_ptr())
-        assert inverse_index.key == key, "inverse_index was built for another call"
+        key = (B, S, S_kv, H, G, D, d_v, topk, flags, cap, indices.data_ptr())
+        if inverse_index.key != key:
+            raise ValueError(f"inverse_index was built for another call: built for {inverse_index.key}, "
+                             f"called with {key} (B, S, S_kv, H, G, D, d_v, topk, flags, pass_bytes, indices)")
         if inverse_index.event is not None:
             torch.cuda.current_stream(q.device).wait_event(inverse_index.event)
-        ws_bytes = int(L.dsa_sparse_mla_bwd_indexed_workspace_size(B, S, S_kv, H, G, D, d_v, topk, flags))
+        ws_bytes = int(L.dsa_sparse_mla_bwd_indexed_workspace_size(B, S, S_kv, H, G, D, d_v, topk, flags, cap))
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
         ix = inverse_index.buf
         rc = L.dsa_sparse_mla_bwd_indexed(
             q.data_ptr(), kv.data_ptr(), o.data_ptr(), do.data_ptr(), indices.data_ptr(),
             lse.data_ptr(), _lib.ptr(delta), dq.data_ptr(), dkv.data_ptr(), ix.data_ptr(), ix.numel(),
             ws.data_ptr(), ws_bytes, B, S, S_kv, H, G, D, d_v, topk, float(sm_scale), dtype_code,
-            _lib.ptr(q_scale), _lib.ptr(kv_scale), flags, stream)
+            _lib.ptr(q_scale), _lib.ptr(kv_scale), flags, cap, stream)
         _lib.check(rc, "dsa_sparse_mla_bwd_indexed")
         return dq, dkv
-    ws_bytes = int(L.dsa_sparse_mla_bwd_workspace_size(B, S, S_kv, H, G, D, d_v, topk, flags))
+    ws_bytes = int(L.dsa_sparse_mla_bwd_workspace_size(B, S, S_kv, H, G, D, d_v, topk, flags, cap))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     rc = L.dsa_sparse_mla_bwd(
         q.data_ptr(), kv.data_ptr(), o.data_ptr(), do.data_ptr(), indices.data_ptr(),
         lse.data_ptr(), _lib.ptr(delta), dq.data_ptr(), dkv.data_ptr(), ws.data_ptr(), ws_bytes,
         B, S, S_kv, H, G, D, d_v, topk, float(sm_scale), dtype_code,
-        _lib.ptr(q_scale), _lib.ptr(kv_scale), flags, stream)
+        _lib.ptr(q_scale), _lib.ptr(kv_scale), flags, cap, stream)
     _lib.check(rc, "dsa_sparse_mla_bwd")
     return dq, dkv
 
@@ -150,7 +164,7 @@ def _prep_delta(delta, B, S, H):
 
 
 def sparse_mla_bwd(q, kv, o, do, indices, lse, sm_scale=None, d_v=None, is_casual=True,
-                   return_kernel=False, delta=None, *, fp32_partials=None, inverse_index=None):
+                   return_kernel=False, delta=None, *, fp32_partials=None, inverse_index=None, pass_bytes=None):
     """Run the sparse-MLA backward and return (dq, dkv), both bf16.
 
     Accepts 3-D [seq, heads, dim] or 4-D [batch, seq, heads, dim] tensors;
@@ -159,6 +173,9 @@ def sparse_mla_bwd(q, kv, o, do, indices, lse, sm_scale=None, d_v=None, is_casua
     CPPMEGA_AMD_BWD_FP32_PARTIALS) keeps the dKV contribution rows in fp32.
     ``inverse_index`` (keyword only): an ``InverseIndex`` from
     ``build_inverse_index`` for these indices, built ahead of the call.
+    ``pass_bytes`` (keyword only): the per-pass cap on the partial dKV rows
+    (bytes; None or 0 = 4 GiB); the backward runs in passes over token ranges
+    whose rows fit it, so its workspace stays bounded.
     """
     q = unwrap_quantized(q)
     kv = unwrap_quantized(kv)
@@ -195,7 +212,7 @@ def sparse_mla_bwd(q, kv, o, do, indices, lse, sm_scale=None, d_v=None, is_casua
 
     scale = normalize_sm_scale(sm_scale, dim_plus_tail_dim)
     dq, dkv = _launch_bwd(q, kv, o, do, indices, lse, delta, scale, _lib.DTYPE_BF16,
-                          fp32_partials=fp32_partials, inverse_index=inverse_index)
+                          fp32_partials=fp32_partials, inverse_index=inverse_index, pass_bytes=pass_bytes)
     if squeeze_batch:
         dq, dkv = dq.squeeze(0), dkv.squeeze(0)
     return dq, dkv

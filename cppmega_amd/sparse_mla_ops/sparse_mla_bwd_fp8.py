@@ -16,9 +16,9 @@ from .sparse_mla_bwd import _launch_bwd, _prep_delta
 
 
 def sparse_mla_bwd_fp8(q, kv, q_scale, kv_scale, o, do, indices, lse, sm_scale=None, is_casual=True,
-                       return_kernel=False, delta=None, *, inverse_index=None):
+                       return_kernel=False, delta=None, *, inverse_index=None, pass_bytes=None):
     """Return (dq, dkv) bf16 for e4m3 q [B,S,H,D] / kv [B,S_kv,G,D] with scales [B,S] / [B,S_kv].
-    ``inverse_index``: as for ``sparse_mla_bwd``."""
+    ``inverse_index`` and ``pass_bytes``: as for ``sparse_mla_bwd``."""
     squeeze_batch = q.ndim == 3
     if squeeze_batch:
         q, kv, o, do = q.unsqueeze(0), kv.unsqueeze(0), o.unsqueeze(0), do.unsqueeze(0)
@@ -51,7 +51,7 @@ def sparse_mla_bwd_fp8(q, kv, q_scale, kv_scale, o, do, indices, lse, sm_scale=N
     scale = normalize_sm_scale(sm_scale, dim_plus_tail_dim)
     dq, dkv = _launch_bwd(q, kv, o, do, indices, lse, delta, scale, _lib.DTYPE_E4M3,
                           q_scale.to(torch.float32).contiguous(), kv_scale.to(torch.float32).contiguous(),
-                          inverse_index=inverse_index)
+                          inverse_index=inverse_index, pass_bytes=pass_bytes)
     if squeeze_batch:
         dq, dkv = dq.squeeze(0), dkv.squeeze(0)
     return dq, dkv

@@ -120,20 +120,21 @@ enum dsa_bwd_flags {
 };
 
 /*
- * Per-pass cap on the backward's partial dKV rows (bytes; 0 restores the
- * default of 4 GiB).  dsa_sparse_mla_bwd runs in passes over contiguous token
- * ranges sized to this cap, so its workspace stays bounded at any sequence
- * length; a batch split over passes carries its kv rows' sums in fp32 between
- * them.  Process-wide; set it before dsa_sparse_mla_bwd_workspace_size and
- * keep it until the matching dsa_sparse_mla_bwd call.  No counterpart in the
- * reference (whose backward scatters into one fp32 dKV buffer with atomics).
+ * pass_bytes (every backward entry point below): the per-pass cap on the
+ * backward's partial dKV rows, in bytes; 0 means the default of 4 GiB.  The
+ * backward runs in passes over contiguous token ranges sized to this cap, so
+ * its workspace stays bounded at any sequence length; a batch split over
+ * passes carries its kv rows' sums in fp32 between them.  The workspace /
+ * index size queries and the call they size must be given the same value.
+ * No counterpart in the reference (whose backward scatters into one fp32 dKV
+ * buffer with atomics).
  */
-int dsa_sparse_mla_bwd_pass_bytes(uint64_t bytes);
 
-/* Bytes of workspace dsa_sparse_mla_bwd needs for these dimensions and flags. */
+/* Bytes of workspace dsa_sparse_mla_bwd needs for these dimensions, flags and cap. */
 size_t dsa_sparse_mla_bwd_workspace_size(int64_t B, int64_t S, int64_t S_kv,
                                          int64_t H, int64_t G, int64_t D_qk,
-                                         int64_t D_v, int64_t topk, int flags);
+                                         int64_t D_v, int64_t topk, int flags,
+                                         uint64_t pass_bytes);
 
 /*
  * SparseMLA backward.
@@ -153,8 +154,8 @@ size_t dsa_sparse_mla_bwd_workspace_size(int64_t B, int64_t S, int64_t S_kv,
  * ascending (token, kv group, slot) order in fp32, so repeated calls are
  * bitwise identical.  Gradients are with respect to the dequantised values
  * for e4m3 inputs.  The work runs in passes over token ranges whose partial
- * rows fit the per-pass cap (dsa_sparse_mla_bwd_pass_bytes), so the workspace
- * is bounded; results are deterministic for a given cap.
+ * rows fit the per-pass cap pass_bytes, so the workspace is bounded; results
+ * are deterministic for a given cap.
  * Limits: B * S_kv * G < 2^31, B * S * G * topk < 2^31.
  */
 int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o,
@@ -165,7 +166,7 @@ int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o,
                        int64_t S_kv, int64_t H, int64_t G, int64_t D_qk,
                        int64_t D_v, int64_t topk, float sm_scale, int dtype,
                        const float *q_scale, const float *kv_scale,
-                       int flags, void *stream);
+                       int flags, uint64_t pass_bytes, void *stream);
 
 /*
  * The backward's inverse index (kv row -> entries) depends on the indices
@@ -182,17 +183,18 @@ int dsa_sparse_mla_bwd(const void *q, const void *kv, const void *o,
  */
 size_t dsa_sparse_mla_bwd_index_size(int64_t B, int64_t S, int64_t S_kv,
                                      int64_t H, int64_t G, int64_t D_qk,
-                                     int64_t D_v, int64_t topk, int flags);
+                                     int64_t D_v, int64_t topk, int flags,
+                                     uint64_t pass_bytes);
 size_t dsa_sparse_mla_bwd_indexed_workspace_size(int64_t B, int64_t S,
                                                  int64_t S_kv, int64_t H,
                                                  int64_t G, int64_t D_qk,
                                                  int64_t D_v, int64_t topk,
-                                                 int flags);
+                                                 int flags, uint64_t pass_bytes);
 int dsa_sparse_mla_bwd_build_index(const int32_t *indices, int64_t B, int64_t S,
                                    int64_t S_kv, int64_t H, int64_t G,
                                    int64_t D_qk, int64_t D_v, int64_t topk,
-                                   int flags, void *index, size_t index_bytes,
-                                   void *stream);
+                                   int flags, uint64_t pass_bytes, void *index,
+                                   size_t index_bytes, void *stream);
 int dsa_sparse_mla_bwd_indexed(const void *q, const void *kv, const void *o,
                                const void *dO, const int32_t *indices,
                                const float *lse2, const float *delta, void *dq,
@@ -202,7 +204,7 @@ int dsa_sparse_mla_bwd_indexed(const void *q, const void *kv, const void *o,
                                int64_t G, int64_t D_qk, int64_t D_v,
                                int64_t topk, float sm_scale, int dtype,
                                const float *q_scale, const float *kv_scale,
-                               int flags, void *stream);
+                               int flags, uint64_t pass_bytes, void *stream);
 
 /*
  * DSA indexer scores: score[b, t, s] = sum_h w[t, b, h] * act(q[t, b, h, :] . k[s, b, :])

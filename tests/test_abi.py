@@ -44,7 +44,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_status_codes(lib):
-    assert lib.dsa_abi_version() == 100
+    assert lib.dsa_abi_version() == 200
     text = open(HEADER).read()
     for name, val in (("DSA_OK", 0), ("DSA_ERR_INVALID_ARG", -1), ("DSA_ERR_UNSUPPORTED", -2),
                       ("DSA_ERR_HIP", -3), ("DSA_ERR_WORKSPACE", -4)):
@@ -79,15 +79,15 @@ def test_fwd_rejects_bad_arguments(lib):
 
 def test_bwd_workspace_and_validation(lib):
     ws = lib.dsa_sparse_mla_bwd_workspace_size
-    a = ws(2, 4096, 4096, 32, 1, 128, 64, 256, 0)
-    b = ws(2, 4096, 4096, 32, 1, 128, 64, 256, _lib.BWD_FP32_PARTIALS)
-    c = ws(1, 4096, 4096, 32, 1, 128, 64, 256, 0)
+    a = ws(2, 4096, 4096, 32, 1, 128, 64, 256, 0, 0)
+    b = ws(2, 4096, 4096, 32, 1, 128, 64, 256, _lib.BWD_FP32_PARTIALS, 0)
+    c = ws(1, 4096, 4096, 32, 1, 128, 64, 256, 0, 0)
     # fp16 partial rows: 2 * 4096 * 256 entries x 256 B, fp32 doubles them
     assert a >= 2 * 4096 * 256 * 128 * 2 and b > a and c < a
-    assert ws(2, 4096, 4096, 32, 1, 128, 64, 256, 0) == a      # deterministic
-    rc = lib.dsa_sparse_mla_bwd(*([None] * 10), 0, 1, 4, 8, 16, 1, 128, 64, 32, 0.1, 0, None, None, 8, None)
+    assert ws(2, 4096, 4096, 32, 1, 128, 64, 256, 0, 0) == a      # deterministic
+    rc = lib.dsa_sparse_mla_bwd(*([None] * 10), 0, 1, 4, 8, 16, 1, 128, 64, 32, 0.1, 0, None, None, 8, 0, None)
     assert rc == _lib.DSA_ERR_INVALID_ARG and "flags" in _err(lib)
-    rc = lib.dsa_sparse_mla_bwd(*([None] * 10), 0, 1, 4, 70000, 16, 1, 128, 64, 32, 0.1, 0, None, None, 0, None)
+    rc = lib.dsa_sparse_mla_bwd(*([None] * 10), 0, 1, 4, 70000, 16, 1, 128, 64, 32, 0.1, 0, None, None, 0, 0, None)
     assert rc == _lib.DSA_ERR_INVALID_ARG
 
 
@@ -109,20 +109,24 @@ def test_fp8_quantize_validation(lib):
 
 
 def test_bwd_workspace_bounded_by_pass_cap(lib):
-    """The backward runs in passes sized to a cap on its partial dKV rows, so its
-    workspace is bounded: at cfg5 (s = 16384, h = 128, d_qk = 576, topk = 2048)
-    one pass would hold ~155 GB of fp16 rows; with the default 4 GiB cap the
-    workspace stays under 5 GiB, and a smaller cap shrinks it further (down to
-    one 32-token chunk per pass, ~302 MB of rows at cfg5)."""
-    try:
-        ws = int(lib.dsa_sparse_mla_bwd_workspace_size(1, 16384, 16384, 128, 1, 576, 512, 2048, 0))
-        assert 0 < ws < 5 * (1 << 30), ws
-        assert lib.dsa_sparse_mla_bwd_pass_bytes(256 << 20) == _lib.DSA_OK
-        ws_small = int(lib.dsa_sparse_mla_bwd_workspace_size(1, 16384, 16384, 128, 1, 576, 512, 2048, 0))
-        assert ws_small < ws and ws_small < 512 << 20, ws_small
-        # cfg2 fits one pass: its size does not depend on the cap while the cap covers it
-        assert lib.dsa_sparse_mla_bwd_pass_bytes(0) == _lib.DSA_OK
-        one = int(lib.dsa_sparse_mla_bwd_workspace_size(2, 4096, 4096, 32, 1, 128, 64, 256, 0))
-        assert one > 2 * 4096 * 256 * 257
-    finally:
-        lib.dsa_sparse_mla_bwd_pass_bytes(0)
+    """The backward runs in passes sized to a per-call cap on its partial dKV
+    rows (the pass_bytes argument, 0 = 4 GiB), so its workspace is bounded: at
+    cfg5 (s = 16384, h = 128, d_qk = 576, topk = 2048) one pass would hold
+    ~155 GB of fp16 rows; with the default cap the workspace stays under 5 GiB,
+    and a smaller cap shrinks it further (down to one 32-token chunk per pass,
+    ~302 MB of rows at cfg5).  The cap is an argument, not process state: two
+    queries with different caps do not affect each other."""
+    wsz = lib.dsa_sparse_mla_bwd_workspace_size
+    ws = int(wsz(1, 16384, 16384, 128, 1, 576, 512, 2048, 0, 0))
+    assert 0 < ws < 5 * (1 << 30), ws
+    assert int(wsz(1, 16384, 16384, 128, 1, 576, 512, 2048, 0, 4 << 30)) == ws
+    ws_small = int(wsz(1, 16384, 16384, 128, 1, 576, 512, 2048, 0, 256 << 20))
+    assert ws_small < ws and ws_small < 512 << 20, ws_small
+    assert int(wsz(1, 16384, 16384, 128, 1, 576, 512, 2048, 0, 0)) == ws      # no state left behind
+    # cfg2 fits one pass: its size does not depend on the cap while the cap covers it
+    one = int(wsz(2, 4096, 4096, 32, 1, 128, 64, 256, 0, 0))
+    assert one > 2 * 4096 * 256 * 257
+    # the index is prebuilt only for a one-pass plan; its size follows the cap
+    assert int(lib.dsa_sparse_mla_bwd_index_size(2, 4096, 4096, 32, 1, 128, 64, 256, 0, 0)) > 0
+    assert int(lib.dsa_sparse_mla_bwd_index_size(2, 4096, 4096, 32, 1, 128, 64, 256, 0, 64 << 20)) == 0
+    assert int(lib.dsa_sparse_mla_bwd_indexed_workspace_size(2, 4096, 4096, 32, 1, 128, 64, 256, 0, 0)) < one

@@ -9,7 +9,7 @@ through the autograd functions, and across replays of a captured HIP graph.
 import pytest
 import torch
 
-from cppmega_amd import _lib, synthetic
+from cppmega_amd import synthetic
 from cppmega_amd.sparse_mla_ops import (SparseMLA, SparseMLA_FP8, build_inverse_index, side_stream,
                                         sparse_mla_bwd, sparse_mla_bwd_fp8, sparse_mla_fwd_fp8_interface,
                                         sparse_mla_fwd_interface)
@@ -46,7 +46,7 @@ def test_prebuilt_index_is_bit_identical(dev, B, S, H, G, D, DV, topk):
     assert ix2.event is None
     dq2, dkv2 = sparse_mla_bwd(q, kv, out, do, idx, lse, sm_scale=scale, inverse_index=ix2)
     assert torch.equal(dq0, dq2) and torch.equal(dkv0, dkv2)
-    with pytest.raises(AssertionError):
+    with pytest.raises(ValueError, match="another call"):
         sparse_mla_bwd(q, kv, out, do, idx.clone(), lse, sm_scale=scale, inverse_index=ix2)
 
 
@@ -119,9 +119,14 @@ def test_no_prebuilt_index_for_several_passes(dev):
     build_inverse_index returns None and the plain call still works."""
     B, S, H, D, DV, topk = 1, 128, 32, 128, 64, 64
     q, kv, idx, do, scale = _case(dev, B, S, H, 1, D, DV, topk, seed=5)
-    L = _lib.load()
-    try:
-        L.dsa_sparse_mla_bwd_pass_bytes(32 * topk * (2 * D + 1))
-        assert build_inverse_index(q, kv, idx, DV) is None
-    finally:
-        L.dsa_sparse_mla_bwd_pass_bytes(0)
+    cap = 32 * topk * (2 * D + 1)
+    assert build_inverse_index(q, kv, idx, DV, pass_bytes=cap) is None
+    out, lse = sparse_mla_fwd_interface(q, kv, idx, sm_scale=scale, d_v=DV)
+    dq, _ = sparse_mla_bwd(q, kv, out, do, idx, lse, sm_scale=scale, pass_bytes=cap)
+    dq1, _ = sparse_mla_bwd(q, kv, out, do, idx, lse, sm_scale=scale)
+    assert torch.equal(dq, dq1)
+    # an index built for another cap (here the default, one pass) is refused, not misused
+    inv = build_inverse_index(q, kv, idx, DV)
+    assert inv is not None
+    with pytest.raises(ValueError, match="another call"):
+        sparse_mla_bwd(q, kv, out, do, idx, lse, sm_scale=scale, inverse_index=inv, pass_bytes=cap)

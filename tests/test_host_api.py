@@ -468,3 +468,40 @@ def test_bench_refuses_more_than_one_gpu():
                        text=True, timeout=300, cwd=ROOT)
     assert r.returncode != 0
     assert "one GPU" in (r.stdout + r.stderr) or "1 GPU" in (r.stdout + r.stderr)
+
+
+def test_unwrap_quantized_looks_te_up_once(monkeypatch):
+    """unwrap_quantized returns plain tensors untouched without any import, and
+    looks Transformer Engine up at most once per process (a failed import is
+    not cached by Python); a QuantizedTensor is dequantised."""
+    import builtins
+
+    from cppmega_amd.sparse_mla_ops import _common
+
+    monkeypatch.setattr(_common, "_QUANTIZED_TENSOR", _common._NOT_LOOKED_UP)
+    calls = []
+    real_import = builtins.__import__
+
+    def counting(name, *a, **k):
+        if name.startswith("transformer_engine"):
+            calls.append(name)
+        return real_import(name, *a, **k)
+
+    monkeypatch.setattr(builtins, "__import__", counting)
+    t = torch.zeros(2)
+    assert _common.unwrap_quantized(t) is t and calls == []
+
+    class Sub(torch.Tensor):
+        pass
+
+    x = torch.zeros(2).as_subclass(Sub)
+    for _ in range(3):
+        assert _common.unwrap_quantized(x) is x
+    assert len(calls) <= 1
+
+    class FakeQuantized:
+        def dequantize(self):
+            return "dequantised"
+
+    monkeypatch.setattr(_common, "_QUANTIZED_TENSOR", FakeQuantized)
+    assert _common.unwrap_quantized(FakeQuantized()) == "dequantised"
