@@ -29,6 +29,12 @@ h=128, d_qk=576, d_v=512, topk=2048; e4m3 indexer at h=64, d=128; top-2048
 over s=16384) are timed on device-generated inputs and reported under "cfg5"
 (not part of `value`).
 
+The top-k path Megatron runs (fused_qk_topk_naive with its causal float mask:
+mask windows, window-mode indexer, top-k, pick finalisation) and the indexer
+backward its autograd takes (row windows from the mask) are timed at cfg3
+beside the dense lower-triangle path and the causal backward, under
+"megatron_masked".
+
 The DSA indexer KL loss (compute_dsa_indexer_loss_splitk at the NAM56R
 attention shape: query/key [4096, 2, 32, 128] bf16, index scores [2, 4096,
 4096] causal, top-256) is timed dense and sparse and reported under
@@ -339,6 +345,38 @@ def measure_indexer_kl(dev, reps=5):
     return res
 
 
+def measure_megatron_masked(dev, iq, ik, iw, t_dense):
+    """The top-k path Megatron runs after apply_dsa_topk_patch, at cfg3:
+    fused_qk_topk_naive(q, k, w, 256, mask=causal_float_mask) (mask windows,
+    window-mode indexer, top-k, pick finalisation; no gradient), and the
+    backward autograd takes through its IndexScores for an upstream gradient of
+    the [b, s, s] scores (row windows from the mask: the lower-triangle work),
+    beside the headline's dense lower-triangle indexer + top-k (`t_dense`, s)
+    and the causal indexer backward.  HIP-graph replays."""
+    import torch
+
+    from cppmega_amd.dsa_indexer_fused_patch import index_scores_backward
+    from cppmega_amd.dsa_topk import fused_qk_topk_naive, mask_windows
+
+    mask = torch.full((S, S), float("-inf"), device=dev).triu(1)
+    t_fwd = graph_replay_time(lambda: fused_qk_topk_naive(iq, ik, iw, TOPK, mask=mask))
+    gen = torch.Generator(device=dev).manual_seed(11)
+    gsc = torch.randn((B, S, S), generator=gen, device=dev) * 1e-3
+    st, en, _ = mask_windows(mask, B, S, S)
+    t_bwd = graph_replay_time(lambda: index_scores_backward(gsc, iq, iw, ik, use_relu=True, starts=st, ends=en))
+    t_causal = graph_replay_time(lambda: index_scores_backward(gsc, iq, iw, ik, use_relu=True, causal=True))
+    t_mask = graph_replay_time(lambda: mask_windows(mask, B, S, S))
+    del gsc
+    torch.cuda.empty_cache()
+    return {"masked_topk_ms": round(t_fwd * 1e3, 4), "dense_indexer_topk_ms": round(t_dense * 1e3, 4),
+            "masked_over_dense": round(t_fwd / t_dense, 3), "mask_windows_ms": round(t_mask * 1e3, 4),
+            "masked_backward_ms": round(t_bwd * 1e3, 4), "causal_backward_ms": round(t_causal * 1e3, 4),
+            "masked_backward_over_causal": round(t_bwd / t_causal, 3),
+            "note": f"fused_qk_topk_naive(q, k, w, {TOPK}, mask=causal float mask [{S}, {S}]) at cfg3 and the "
+                    f"indexer backward its autograd runs (windows from the mask), as HIP-graph replays; dense = "
+                    f"kernels.indexer + kernels.topk of the step"}
+
+
 def time_graph(step, steps, warmup):
     """Capture one layer step (every kernel, outputs allocated from the
     graph's pool) in a HIP graph and time `steps` replays.  Before timing,
@@ -630,6 +668,7 @@ def main():
     streaming = {"ms": round(t_stream * 1e3, 4), "scratch_mib": 16,
                  "note": "cfg3 indexer + top-256 in 512-row chunks (no [2, 4096, 4096] score matrix); "
                          "HIP-graph replays; dense path = kernels.indexer + kernels.topk"}
+    megatron_masked = measure_megatron_masked(dev, iq, ik, iw, t_idx / 1e3)
     cfg5 = None if args.no_cfg5 else measure_cfg5(dev)
     kl = None if args.no_kl else measure_indexer_kl(dev)
     cfg4 = None if args.no_cfg4 else measure_cfg4(dev)
@@ -674,6 +713,7 @@ def main():
         "kernels": kernels,
         "indexcache_amortised_tokens_per_s": round(amortised, 1),
         "indexer_topk_streaming": streaming,
+        "megatron_masked": megatron_masked,
         "chained_step": chained,
         "launch": ("hip_graph" if graph_info is not None else "eager"),
         "eager_tokens_per_s": round(eager_tokens_per_s, 1),

@@ -45,6 +45,8 @@ EXPORTED_SYMBOLS = (
     "dsa_sparse_mla_bwd",
     "dsa_indexer_scores",
     "dsa_indexer_scores_masked",
+    "dsa_mask_windows",
+    "dsa_topk_finalize",
     "dsa_indexer_scores_backward_workspace_size",
     "dsa_indexer_scores_backward",
     "dsa_indexer_topk_streaming_workspace_size",
@@ -100,9 +102,12 @@ _SIGNATURES = {
     "dsa_indexer_scores_masked": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                          _i64, _i64, _i64, _i64, _i64, _i32, _i32,
                                          _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
-                                         _i32, _c_void_p]),
+                                         _c_void_p, _i32, _c_void_p]),
+    "dsa_mask_windows": (_i32, [_c_void_p, _i64, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
+    "dsa_topk_finalize": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _c_void_p]),
     "dsa_indexer_scores_backward_workspace_size": (_size_t, [_i64] * 5),
-    "dsa_indexer_scores_backward": (_i32, [_c_void_p] * 7 + [_i64] * 5 + [_i32] * 4 + [_c_void_p, _size_t, _c_void_p]),
+    "dsa_indexer_scores_backward": (_i32, [_c_void_p] * 7 + [_i64] * 5 + [_i32] * 4
+                                    + [_c_void_p, _c_void_p, _c_void_p, _size_t, _c_void_p]),
     "dsa_indexer_topk_streaming_workspace_size": (_size_t, [_i64] * 4),
     "dsa_indexer_topk_streaming": (_i32, [_c_void_p] * 5 + [_i64] * 5 + [_i32, _i32, _c_void_p, _c_void_p, _i64,
                                                                          _i32, _i32, _c_void_p, _size_t, _c_void_p]),

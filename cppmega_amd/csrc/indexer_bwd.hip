@@ -24,6 +24,12 @@
 //     sums the chunks in chunk order.
 // Both orders are fixed by the shapes, so results are bitwise reproducible.
 // causal != 0 restricts every sum to s <= t (G above the diagonal is ignored).
+// Row windows (starts / ends, one [start, end) per (batch, query row)) restrict
+// them further to start <= s < end: the window-mode forward writes -inf there
+// whatever the raw score, so G outside the windows carries no gradient, and
+// key tiles outside every window of a workgroup's rows are not computed.  The
+// key-major kernel then marks, per (batch, token chunk, key block), whether it
+// wrote a partial, and the reduction sums only those.
 #include "dsa_common.hpp"
 
 namespace dsa {
@@ -41,7 +47,24 @@ struct IdxBwdParams {
   int w_f32, causal;
   int gvec;                  // G rows 16-byte aligned (Sk % 4 == 0): 16-byte G loads
   int nch, tc;               // token chunks of the key-major kernel and their length
+  const int32_t *starts;     // [B, Sq] row windows [start, end), or NULL (no windows)
+  const int32_t *ends;
+  int32_t *kflags;           // windows: [B][nch][nkb], 1 where the key-major kernel wrote a partial
+  int nkb;                   // key blocks of the key-major kernel
 };
+
+// Key range [lo, hi) of row t of batch b: the causal limit and the row window.
+__device__ __forceinline__ void row_keys(const IdxBwdParams &p, int64_t b, int64_t t, int &lo, int &hi) {
+  const int sk = (int)p.Sk;
+  lo = 0;
+  hi = p.causal ? (t + 1 < p.Sk ? (int)t + 1 : sk) : sk;
+  if (p.ends != nullptr) {
+    const int st = p.starts[b * p.Sq + t], en = p.ends[b * p.Sq + t];
+    lo = st > 0 ? st : 0;
+    hi = en < hi ? en : hi;
+  }
+  if (hi < lo) hi = lo;
+}
 
 template <int H, int D>
 struct IdxBwdCfg {
@@ -101,11 +124,30 @@ indexer_bwd_q_kernel(const IdxBwdParams p) {
   const int tid = threadIdx.x, lane = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
   const int g32 = lane >> 5, l32 = lane & 31;
   const int64_t t_last = (t0 + C::TT < p.Sq ? t0 + C::TT : p.Sq) - 1;
-  const int64_t kend = p.causal ? (t_last + 1 < p.Sk ? t_last + 1 : p.Sk) : p.Sk;
+  int64_t kend = p.causal ? (t_last + 1 < p.Sk ? t_last + 1 : p.Sk) : p.Sk;
+  int64_t kbeg = 0;  // keys below every row's window start are skipped
+  if (p.ends != nullptr) {
+    // the union of the workgroup's row ranges (TT <= 64 tokens: one per lane, in every wave)
+    int lo = 0x7fffffff, hi = 0;
+    if (lane < C::TT && t0 + lane <= t_last) {
+      int a, e;
+      row_keys(p, b, t0 + lane, a, e);
+      if (e > a) { lo = a; hi = e; }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const int lo2 = __shfl_xor(lo, off, 64), hi2 = __shfl_xor(hi, off, 64);
+      lo = lo2 < lo ? lo2 : lo;
+      hi = hi2 > hi ? hi2 : hi;
+    }
+    kend = __builtin_amdgcn_readfirstlane(hi);
+    kbeg = hi > 0 ? __builtin_amdgcn_readfirstlane(lo) : 0;
+  }
+  const int it0 = (int)(kbeg / C::KT);
   const int ntile = (int)((kend + C::KT - 1) / C::KT);
   const int64_t wave_row0 = t0 * H + w * C::RPW;      // (token, head) rows t * H + h
   const int64_t wave_tok_last = (wave_row0 + C::RPW - 1) / H;
-  const int64_t wave_kend = p.causal ? (wave_tok_last + 1 < p.Sk ? wave_tok_last + 1 : p.Sk) : p.Sk;
+  int64_t wave_kend = p.causal ? (wave_tok_last + 1 < p.Sk ? wave_tok_last + 1 : p.Sk) : p.Sk;
 
   // key tiles: rows [first, first + KT) of batch b through a resource ending at the last key
   const uint32_t row_pitch = (uint32_t)(p.B * C::ROWB);
@@ -157,7 +199,7 @@ indexer_bwd_q_kernel(const IdxBwdParams p) {
   };
   i32x4 kreg[C::LOADS];
   f32x4 greg[C::GQ_PER_T];
-  load_tile(0, kreg, greg);
+  load_tile(it0, kreg, greg);
 
   // q rows of the wave as MFMA B operands (row = lane l32 of tile m; d = 16k + 8 g32 + e)
   bf16x8 QB[C::MT][C::KSTEPS];
@@ -177,11 +219,39 @@ indexer_bwd_q_kernel(const IdxBwdParams p) {
       QB[m][k] = as_bf16x8(v);
     }
   }
-  // keys s < klim[m] are in the row's range (causal: s <= t)
-  int klim[C::MT];
+  // keys klo[m] <= s < klim[m] are in the row's range (causal: s <= t; windows)
+  int klim[C::MT], klo[C::MT];
+  int wave_kbeg = 0;
 #pragma unroll
-  for (int m = 0; m < C::MT; ++m)
-    klim[m] = p.causal ? (tok[m] + 1 < p.Sk ? (int)tok[m] + 1 : sk32) : sk32;
+  for (int m = 0; m < C::MT; ++m) {
+    if (p.ends != nullptr) {
+      int a = 0, e = 0;
+      if (tok[m] < p.Sq) row_keys(p, b, tok[m], a, e);
+      klo[m] = a;
+      klim[m] = e;
+    } else {
+      klo[m] = 0;
+      klim[m] = p.causal ? (tok[m] + 1 < p.Sk ? (int)tok[m] + 1 : sk32) : sk32;
+    }
+  }
+  if (p.ends != nullptr) {
+    // the union of the wave's row ranges: sub-tiles outside it are skipped
+    int lo = 0x7fffffff, hi = 0;
+#pragma unroll
+    for (int m = 0; m < C::MT; ++m)
+      if (klim[m] > klo[m]) {
+        lo = klo[m] < lo ? klo[m] : lo;
+        hi = klim[m] > hi ? klim[m] : hi;
+      }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const int lo2 = __shfl_xor(lo, off, 64), hi2 = __shfl_xor(hi, off, 64);
+      lo = lo2 < lo ? lo2 : lo;
+      hi = hi2 > hi ? hi2 : hi;
+    }
+    wave_kend = __builtin_amdgcn_readfirstlane(hi);
+    wave_kbeg = hi > 0 ? __builtin_amdgcn_readfirstlane(lo) : 0;
+  }
   f32x16 dqa[C::MT][C::DT];
   float dwa[C::MT];
 #pragma unroll
@@ -195,14 +265,15 @@ indexer_bwd_q_kernel(const IdxBwdParams p) {
 
   store_tile(0, kreg, greg);
   __syncthreads();
-  for (int it = 0; it < ntile; ++it) {
+  for (int it = it0; it < ntile; ++it) {
     load_tile(it + 1, kreg, greg);  // past the last tile: zeros, unused
-    const unsigned char *ks = KS[it & 1];
-    const float *gs = GS[it & 1];
+    const unsigned char *ks = KS[(it - it0) & 1];
+    const float *gs = GS[(it - it0) & 1];
 #pragma unroll 1
     for (int sub = 0; sub < C::SUBS; ++sub) {
       const int64_t sn = (int64_t)it * C::KT + sub * 32;
       if (sn >= wave_kend) break;  // wave-uniform
+      if (sn + 32 <= wave_kbeg) continue;
       // G of the lane's row token at keys sn + 8i + 4 g32 + (0..3), from the staged tile
       f32x4 gv[C::MT][4];
 #pragma unroll
@@ -237,7 +308,7 @@ indexer_bwd_q_kernel(const IdxBwdParams p) {
           for (int j = 0; j < 4; ++j) {
             const int s = s0 + 8 * i + j;
             const float L = acc[m][4 * i + j];
-            const bool ok = (s < klim[m]) & (!RELU | (L > 0.0f));
+            const bool ok = (s < klim[m]) & (s >= klo[m]) & (!RELU | (L > 0.0f));
             const float v = ok ? gv[m][i][j] : 0.0f;
             dwa[m] = fmaf(v, L, dwa[m]);
             mv[j] = v;
@@ -262,7 +333,7 @@ indexer_bwd_q_kernel(const IdxBwdParams p) {
     }
     if (it + 1 < ntile) {
       // the buffer stored into was last read in iteration it - 1, before that iteration's barrier
-      store_tile((it + 1) & 1, kreg, greg);
+      store_tile((it + 1 - it0) & 1, kreg, greg);
       __syncthreads();
     }
   }
@@ -303,24 +374,68 @@ __device__ __forceinline__ int first_chunk(const IdxBwdParams &p, int64_t kb, in
   return (int)(c < p.nch ? c : p.nch);
 }
 
-template <int H, int D, bool RELU>
+// WIN: row windows (p.starts / p.ends).  The windowed kernel is its own
+// instantiation, so the causal / full kernel's code is unchanged by them.  With
+// windows, G is zeroed outside each token's window as the tile is staged in
+// LDS (so the inner loop needs no window test), and a per-tile bitmask of the
+// 32-row sub-tiles whose token windows meet each wave's keys, built with the
+// tile, skips the others.
+template <int H, int D, bool RELU, bool WIN>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 indexer_bwd_k_kernel(const IdxBwdParams p) {
   using C = IdxBwdCfg<H, D>;
   __shared__ __attribute__((aligned(16))) unsigned char QS[2][C::KT * C::STRIDE];
   __shared__ float WS[2][C::KT];
   __shared__ __attribute__((aligned(16))) float GSk[2][C::TPT * C::KB];
+  constexpr int NSW = C::SUBS * C::WAVES;          // (sub-tile, wave) pairs of a row tile
+  __shared__ int SKIPM[2][WIN ? NSW : 1];          // WIN: 1 where the sub-tile meets the wave's keys
   const int64_t kb = blockIdx.x, b = blockIdx.z;
   const int c = blockIdx.y;
-  if (c < first_chunk(p, kb, C::KB)) return;  // no token of the chunk reaches these keys
+  if (!WIN && c < first_chunk(p, kb, C::KB)) return;  // no token of the chunk reaches these keys
   const int tid = threadIdx.x, lane = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
   const int g32 = lane >> 5, l32 = lane & 31;
   const int64_t key0 = kb * C::KB + w * (C::MT * 32);  // this wave's first key
   const int64_t tc0 = (int64_t)c * p.tc;
-  const int64_t tc1 = (tc0 + p.tc < p.Sq ? tc0 + p.tc : p.Sq);
+  int64_t tc1 = (tc0 + p.tc < p.Sq ? tc0 + p.tc : p.Sq);
   // rows (token, head) of the chunk, from the first token that can reach this workgroup's keys
   int64_t tstart = tc0;
-  if (p.causal && kb * C::KB > tstart) tstart = kb * C::KB;
+  if (!WIN && p.causal && kb * C::KB > tstart) tstart = kb * C::KB;
+  const int kblk0i = (int)(kb * C::KB);
+  if constexpr (WIN) {
+    // the chunk's first and last token whose key range meets [kb * KB, kb * KB + KB)
+    __shared__ int tr[2][C::WAVES];
+    const int kb1 = kblk0i + C::KB;
+    int tmin = 0x7fffffff, tmax = -1;
+    for (int64_t t = tc0 + tid; t < tc1; t += C::NT) {
+      int a, e;
+      row_keys(p, b, t, a, e);
+      if (e > a && a < kb1 && e > kblk0i) {
+        tmin = (int)t < tmin ? (int)t : tmin;
+        tmax = (int)t;
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const int a2 = __shfl_xor(tmin, off, 64), b2 = __shfl_xor(tmax, off, 64);
+      tmin = a2 < tmin ? a2 : tmin;
+      tmax = b2 > tmax ? b2 : tmax;
+    }
+    if (lane == 0) {
+      tr[0][w] = tmin;
+      tr[1][w] = tmax;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < C::WAVES; ++v) {
+      tmin = tr[0][v] < tmin ? tr[0][v] : tmin;
+      tmax = tr[1][v] > tmax ? tr[1][v] : tmax;
+    }
+    const int touched = tmax >= 0 ? 1 : 0;
+    if (tid == 0) p.kflags[((b * p.nch + c) * p.nkb) + kb] = touched;
+    if (!touched) return;  // block-uniform
+    tstart = tmin;
+    tc1 = (int64_t)tmax + 1;
+  }
   const int64_t row0 = tstart * H, row1 = tc1 * H;
   const int ntile = row1 > row0 ? (int)((row1 - row0 + C::KT - 1) / C::KT) : 0;
 
@@ -342,7 +457,7 @@ indexer_bwd_k_kernel(const IdxBwdParams p) {
   const float *g_b = p.g + b * p.Sq * p.Sk;
   const auto g_rs = make_buffer_rsrc(g_b, (uint32_t)(p.Sq * p.Sk * 4));
   const int64_t kblk0 = kb * C::KB;
-  auto load_tile = [&](int it, i32x4 (&r)[C::LOADS], float &wv, f32x4 (&gr)[C::GK_PER_T]) {
+  auto load_tile = [&](int it, i32x4 (&r)[C::LOADS], float &wv, f32x4 (&gr)[C::GK_PER_T], int &meets) {
 #pragma unroll
     for (int l = 0; l < C::LOADS; ++l) {
       const int u = tid + C::NT * l;
@@ -364,15 +479,42 @@ indexer_bwd_k_kernel(const IdxBwdParams p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) gr[l][j] = buffer_load_f32(g_rs, in ? (int)(off + 4 * j) : (int)0xffffffffu, 0);
       }
+      if constexpr (WIN) {  // G outside the token's window carries no gradient
+        int a = 0, e = 0;
+        if (in && tok0 + tl < tc1) row_keys(p, b, tok0 + tl, a, e);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int key = kblk0i + 4 * c + j;
+          gr[l][j] = (key >= a && key < e) ? gr[l][j] : 0.0f;
+        }
+      }
+    }
+    meets = 0;
+    if constexpr (WIN) {  // (sub-tile rs, wave v) = tid: does a token window of rows rs*32.. meet v's keys
+      if (tid < NSW) {
+        const int rs = tid / C::WAVES, v = tid % C::WAVES;
+        const int64_t k0v = kblk0 + v * (C::MT * 32);
+        constexpr int TPS = 32 / H > 0 ? 32 / H : 1;
+#pragma unroll
+        for (int ti = 0; ti < TPS; ++ti) {
+          const int64_t t = (row0 + (int64_t)it * C::KT + rs * 32) / H + ti;
+          int a = 0, e = 0;
+          if (t < tc1) row_keys(p, b, t, a, e);
+          meets |= (e > a && a < k0v + C::MT * 32 && e > k0v) ? 1 : 0;
+        }
+      }
     }
   };
-  auto store_tile = [&](int buf, const i32x4 (&r)[C::LOADS], float wv, const f32x4 (&gr)[C::GK_PER_T]) {
+  auto store_tile = [&](int buf, const i32x4 (&r)[C::LOADS], float wv, const f32x4 (&gr)[C::GK_PER_T], int meets) {
 #pragma unroll
     for (int l = 0; l < C::LOADS; ++l) {
       const int u = tid + C::NT * l;
       *reinterpret_cast<i32x4 *>(&QS[buf][(u / C::CPR) * C::STRIDE + (u % C::CPR) * 16]) = r[l];
     }
     if (tid < C::KT) WS[buf][tid] = wv;
+    if constexpr (WIN) {
+      if (tid < NSW) SKIPM[buf][tid] = meets;
+    }
 #pragma unroll
     for (int l = 0; l < C::GK_PER_T; ++l) {
       const int u = tid + C::NT * l;
@@ -391,22 +533,32 @@ indexer_bwd_k_kernel(const IdxBwdParams p) {
   i32x4 qreg[C::LOADS];
   float wreg = 0.0f;
   f32x4 greg[C::GK_PER_T];
+  int mreg = 0;
   if (ntile > 0) {
-    load_tile(0, qreg, wreg, greg);
-    store_tile(0, qreg, wreg, greg);
+    load_tile(0, qreg, wreg, greg, mreg);
+    store_tile(0, qreg, wreg, greg, mreg);
   }
   __syncthreads();
   for (int it = 0; it < ntile; ++it) {
-    if (it + 1 < ntile) load_tile(it + 1, qreg, wreg, greg);
+    if (it + 1 < ntile) load_tile(it + 1, qreg, wreg, greg, mreg);
     const unsigned char *qs = QS[it & 1];
     const float *ws = WS[it & 1];
     const float *gsk = GSk[it & 1];
+    // WIN: this wave's sub-tiles that meet its keys, one scalar bitmask per tile
+    uint32_t subm = 0xffffffffu;
+    if constexpr (WIN) {
+      subm = 0;
+#pragma unroll
+      for (int rs = 0; rs < C::SUBS; ++rs)
+        subm |= (uint32_t)__builtin_amdgcn_readfirstlane(SKIPM[it & 1][rs * C::WAVES + w]) << rs;
+    }
 #pragma unroll 1
     for (int rs = 0; rs < C::SUBS; ++rs) {
       const int64_t rb = row0 + (int64_t)it * C::KT + rs * 32;  // first row of the sub-tile
       if (rb >= row1) break;
       // the sub-tile's last token is below this wave's first key: nothing (causal)
-      if (p.causal && (rb + 31) / H < key0) continue;
+      if (!WIN && p.causal && (rb + 31) / H < key0) continue;
+      if (WIN && ((subm >> rs) & 1u) == 0) continue;  // no token window meets this wave's keys
       // G[t][key] for the (at most two) tokens of rows rb .. rb + 31
       constexpr int TPS = 32 / H > 0 ? 32 / H : 1;  // tokens per 32-row sub-tile
       float gv[C::MT][TPS];
@@ -447,7 +599,7 @@ indexer_bwd_k_kernel(const IdxBwdParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int ti = H == 16 ? (i >> 1) : 0;
-          const bool in_win = !p.causal | (key <= tb + ti);
+          const bool in_win = WIN | !p.causal | (key <= tb + ti);  // WIN: G is already 0 outside
           const float gw = gv[n][ti];
           float mv[4];
 #pragma unroll
@@ -475,7 +627,7 @@ indexer_bwd_k_kernel(const IdxBwdParams p) {
         }
     }
     if (it + 1 < ntile) {
-      store_tile((it + 1) & 1, qreg, wreg, greg);
+      store_tile((it + 1) & 1, qreg, wreg, greg, mreg);
       __syncthreads();
     }
   }
@@ -500,9 +652,20 @@ __global__ void __launch_bounds__(256) indexer_bwd_dk_reduce_kernel(const IdxBwd
   const int64_t e = blockIdx.x * 256ll + threadIdx.x;  // (b, s, d) with d fastest
   if (e >= p.B * p.Sk * D) return;
   const int64_t d = e % D, s = (e / D) % p.Sk, b = e / (D * p.Sk);
-  const int c0 = first_chunk(p, s / KBK, KBK);
   float acc = 0.0f;
-  for (int c = c0; c < p.nch; ++c) acc += p.dk_part[((b * p.nch + c) * p.Sk + s) * D + d];
+  if (p.kflags != nullptr) {  // windows: the chunks that wrote a partial for this key block
+    // D is a multiple of 64, so a wave's 64 consecutive elements share one
+    // (batch, key): the flags are wave-uniform scalar loads
+    static_assert(D % 64 == 0, "a wave's elements share one key");
+    const int64_t kblk = __builtin_amdgcn_readfirstlane((int)(s / KBK));
+    const int64_t bb = __builtin_amdgcn_readfirstlane((int)b);
+    const int32_t *fl = p.kflags + bb * p.nch * p.nkb + kblk;
+    for (int c = 0; c < p.nch; ++c)
+      if (fl[c * p.nkb]) acc += p.dk_part[((b * p.nch + c) * p.Sk + s) * D + d];
+  } else {
+    const int c0 = first_chunk(p, s / KBK, KBK);
+    for (int c = c0; c < p.nch; ++c) acc += p.dk_part[((b * p.nch + c) * p.Sk + s) * D + d];
+  }
   p.dk[(s * p.B + b) * D + d] = (uint16_t)f32_to_bf16_bits(acc);
 }
 
@@ -524,12 +687,17 @@ static int launch_idx_bwd(IdxBwdParams p, hipStream_t st) {
   using C = IdxBwdCfg<H, D>;
   const int64_t ntb = (p.Sq + C::TT - 1) / C::TT;
   DSA_REQUIRE(ntb * p.B < (1ll << 31), "dsa_indexer_scores_backward: grid too large");
+  const int64_t nkb = (p.Sk + C::KB - 1) / C::KB;
+  p.nkb = (int)nkb;
   hipLaunchKernelGGL((indexer_bwd_q_kernel<H, D, RELU>), dim3((unsigned)(ntb * p.B)), dim3(C::NT), 0, st, p);
   int rc = check_launch("indexer_scores_backward(dq)");
   if (rc) return rc;
-  const int64_t nkb = (p.Sk + C::KB - 1) / C::KB;
-  hipLaunchKernelGGL((indexer_bwd_k_kernel<H, D, RELU>), dim3((unsigned)nkb, (unsigned)p.nch, (unsigned)p.B),
-                     dim3(C::NT), 0, st, p);
+  if (p.ends != nullptr)
+    hipLaunchKernelGGL((indexer_bwd_k_kernel<H, D, RELU, true>), dim3((unsigned)nkb, (unsigned)p.nch, (unsigned)p.B),
+                       dim3(C::NT), 0, st, p);
+  else
+    hipLaunchKernelGGL((indexer_bwd_k_kernel<H, D, RELU, false>), dim3((unsigned)nkb, (unsigned)p.nch, (unsigned)p.B),
+                       dim3(C::NT), 0, st, p);
   rc = check_launch("indexer_scores_backward(dk)");
   if (rc) return rc;
   const int64_t n = p.B * p.Sk * D;
@@ -553,18 +721,23 @@ extern "C" size_t dsa_indexer_scores_backward_workspace_size(int64_t B, int64_t 
   if (B <= 0 || Sq <= 0 || Sk <= 0 || D <= 0) return 0;
   int nch = 1, tc = 1;
   bwd_chunks(Sq, &nch, &tc);
-  return (size_t)B * nch * Sk * D * sizeof(float);
+  // fp32 dk partials per token chunk, then the windows' per-(chunk, key block)
+  // flags (key blocks of at least 128 keys)
+  const size_t part = ((size_t)B * nch * Sk * D * sizeof(float) + 255) & ~(size_t)255;
+  return part + (size_t)B * nch * ((Sk + 127) / 128) * sizeof(int32_t);
 }
 
 extern "C" int dsa_indexer_scores_backward(const float *grad_scores, const void *q, const void *w, const void *k,
                                            void *dq, void *dw, void *dk, int64_t B, int64_t Sq, int64_t Sk,
                                            int64_t H, int64_t D, int dtype, int w_dtype, int causal, int use_relu,
-                                           void *workspace, size_t workspace_bytes, void *stream) {
+                                           const int32_t *starts, const int32_t *ends, void *workspace,
+                                           size_t workspace_bytes, void *stream) {
   DSA_REQUIRE(B >= 0 && Sq >= 0 && Sk >= 0 && H > 0 && D > 0, "dsa_indexer_scores_backward: bad dims");
   DSA_REQUIRE(dtype == DSA_DTYPE_BF16, "dsa_indexer_scores_backward: q / k must be bf16 (dtype %d)", dtype);
   DSA_REQUIRE(w_dtype == DSA_DTYPE_BF16 || w_dtype == DSA_DTYPE_F32, "dsa_indexer_scores_backward: w dtype %d",
               w_dtype);
   DSA_REQUIRE(causal == 0 || causal == 1, "dsa_indexer_scores_backward: causal must be 0 or 1");
+  DSA_REQUIRE((starts == nullptr) == (ends == nullptr), "dsa_indexer_scores_backward: give both starts and ends");
   if (B == 0 || Sq == 0 || Sk == 0) return DSA_OK;
   DSA_REQUIRE(grad_scores && q && w && k && dq && dw && dk, "dsa_indexer_scores_backward: null tensor pointer");
   DSA_REQUIRE(Sq * Sk < (1ll << 30) && Sk < (1ll << 25) && B < 65536,
@@ -590,6 +763,12 @@ extern "C" int dsa_indexer_scores_backward(const float *grad_scores, const void 
   p.causal = causal;
   p.gvec = (Sk % 4 == 0) && (reinterpret_cast<uintptr_t>(grad_scores) & 15u) == 0;
   bwd_chunks(Sq, &p.nch, &p.tc);
+  p.starts = starts;
+  p.ends = ends;
+  p.kflags = starts ? reinterpret_cast<int32_t *>(static_cast<unsigned char *>(workspace) +
+                                                  (((size_t)B * p.nch * Sk * D * sizeof(float) + 255) & ~(size_t)255))
+                    : nullptr;
+  p.nkb = 0;  // set per kernel configuration by the launcher
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool relu = use_relu != 0;
 #define DSA_IDXB_CASE(HH, DD) \

@@ -36,11 +36,14 @@ struct IdxParams {
   const float *k_scale;
   // window mode (causal == 3): row t of batch b keeps columns [starts, ends) of
   // its [B, Sq] windows, plus the additive mask (batch stride mask_bstride
-  // elements, 0 = one mask for every batch; NULL = no mask); -inf elsewhere
+  // elements, 0 = one mask for every batch; NULL = no mask); -inf elsewhere.
+  // row_plain ([B, Sq], or NULL): rows whose mask holds only +0.0 inside the
+  // window; their mask is not read (score + 0.0f has the bits of score + mask)
   const int32_t *starts;
   const int32_t *ends;
   const float *mask;
   int64_t mask_bstride;
+  const int32_t *row_plain;
   int64_t B, Sq, Sk;
   int64_t coff;  // causal modes 1 / 2: row t keeps keys s <= t + coff (q starts coff tokens into the sequence)
   int w_f32;
@@ -73,7 +76,9 @@ struct IdxCfg {
 
 // Scores of token block [t0, t0 + TT) against keys [k0, k_end) of batch b
 // (the keys of one work segment), written to the rows of that token block.
-template <int H, int D, bool FP8, bool RELU>
+// WIN: window mode (causal == kCausalWindow), a separate instantiation so the
+// other modes' register allocation does not carry the window code.
+template <int H, int D, bool FP8, bool RELU, bool WIN = false>
 __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&KS)[2][IdxCfg<H, D, FP8>::KT * IdxCfg<H, D, FP8>::KS_STRIDE],
                                             int64_t b, int64_t t0_in, int64_t k0_in, int64_t k_end_in) {
   using C = IdxCfg<H, D, FP8>;
@@ -226,21 +231,32 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
 
   // window mode: this wave's token windows (wave-uniform scalar loads) and
   // their union; sub-tiles outside the union are not computed
-  const bool win = p.causal == kCausalWindow;
+  constexpr bool win = WIN;
   int wst[C::TPW], wen[C::TPW];
+  bool wpl[C::TPW];  // the row's mask is +0.0 inside its window: not read
   int64_t wmin = 0, wmax = 0;
+  // the intersection of the wave's windows, when every one of its rows is
+  // plain: key tiles inside it take the interior path (score + 0.0f == score)
+  int64_t wisect_lo = 0, wisect_hi = 0;
   if (win) {
     wmin = p.Sk;
+    bool all_plain = true;
+    wisect_hi = p.Sk;
 #pragma unroll
     for (int tl = 0; tl < C::TPW; ++tl) {
       const int64_t t = wave_tok0 + tl;
       wst[tl] = t < p.Sq ? p.starts[b * p.Sq + t] : 0;
       wen[tl] = t < p.Sq ? p.ends[b * p.Sq + t] : 0;
+      wpl[tl] = p.row_plain != nullptr && t < p.Sq && p.row_plain[b * p.Sq + t] != 0;
+      all_plain = all_plain && wpl[tl];
+      wisect_lo = wst[tl] > wisect_lo ? wst[tl] : wisect_lo;
+      wisect_hi = wen[tl] < wisect_hi ? wen[tl] : wisect_hi;
       if (wen[tl] > wst[tl]) {
         wmin = wst[tl] < wmin ? wst[tl] : wmin;
         wmax = wen[tl] > wmax ? wen[tl] : wmax;
       }
     }
+    if (!all_plain) wisect_hi = wisect_lo;  // no interior tiles
   }
   // additive mask rows of this token block (an empty resource without a mask: loads read 0)
   const float *mask_b = (win && p.mask) ? p.mask + b * p.mask_bstride + t0 * p.Sk : nullptr;
@@ -253,7 +269,9 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
     load_tile(it + 1, kreg);  // past the last tile: keys beyond Sk read 0, unused
     const unsigned char *ks = KS[it & 1];
     const int64_t tk = k0 + (int64_t)it * C::KT;
-    const bool interior = !win && wave_in_sq && tk + C::KT <= k_end && (!p.causal || tk + C::KT - 1 <= wave_tok0 + p.coff);
+    const bool interior = wave_in_sq && tk + C::KT <= k_end &&
+                          (win ? (wisect_lo <= tk && tk + C::KT <= wisect_hi)
+                               : (!p.causal || tk + C::KT - 1 <= wave_tok0 + p.coff));
     if (interior) {
 #pragma unroll
       for (int sub = 0; sub < C::SUBS; ++sub) {
@@ -286,7 +304,7 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
 #pragma unroll
         for (int tl = 0; tl < C::TPW; ++tl) {
           const int64_t t = wave_tok0 + tl;
-          const bool ld = win && active && t < p.Sq && s < p.Sk;
+          const bool ld = win && active && t < p.Sq && s < p.Sk && !wpl[tl];
           mv[tl] = buffer_load_f32(mask_rs, ld ? (int)(((t - t0) * p.Sk + s) * 4) : (int)0xffffffffu, 0);
         }
         float part[C::TPW];
@@ -322,6 +340,30 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
   }
 }
 
+// -inf into columns [c0, c1) of rows [t0, t_last] of a [., Sk] score matrix,
+// row by row; 16-byte stores over the 16-byte-aligned middle of each row.
+template <int NT>
+__device__ __forceinline__ void fill_neg_inf_rows(float *out_b, int64_t Sk, int64_t t0, int64_t t_last, int64_t c0,
+                                                  int64_t c1) {
+  if (c1 <= c0) return;
+  const f32x4 ninf4 = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  for (int64_t t = t0; t <= t_last; ++t) {
+    float *row = out_b + t * Sk;
+    int64_t a = c0;
+    while ((reinterpret_cast<uintptr_t>(row + a) & 15) != 0) {  // unaligned head (at most 3 columns)
+      if (a >= c1) break;
+      if (threadIdx.x == 0) row[a] = -INFINITY;
+      ++a;
+    }
+    const int64_t nv = a < c1 ? (c1 - a) / 4 : 0;
+    if ((reinterpret_cast<uintptr_t>(row + a) & 15) == 0) {
+      for (int64_t c = threadIdx.x; c < nv; c += NT) reinterpret_cast<f32x4 *>(row + a)[c] = ninf4;
+      a += 4 * nv;
+    }
+    for (int64_t c = a + threadIdx.x; c < c1; c += NT) row[c] = -INFINITY;
+  }
+}
+
 // Rows of token blocks have different lengths in lower-triangle mode (block tb
 // computes keys [0, last token]), so a grid of fixed key chunks leaves some
 // compute units with 64 times the work of others.  Lower-triangle mode pairs
@@ -329,14 +371,18 @@ __device__ __forceinline__ void idx_segment(const IdxParams &p, unsigned char (&
 // row length is the same for every j, and splitting it into `pieces` equal
 // ranges of 32-key sub-tiles gives every workgroup the same work.  A piece is
 // at most two segments (the end of the long row, the start of the short one).
-// Other modes keep fixed chunks of CHUNK keys (all rows as long as Sk).
-template <int H, int D, bool FP8, bool RELU>
-__global__ void __launch_bounds__((IdxCfg<H, D, FP8>::NT)) __attribute__((amdgpu_waves_per_eu(FP8 || D <= 64 ? 3 : 2)))
+// Window mode pairs the blocks the same way over their window unions (for a
+// causal mask: the lower triangle's balance).  Modes 0 and 1 keep fixed chunks
+// of CHUNK keys (all rows as long as Sk).  WIN selects the window-mode
+// instantiation (launched for causal == kCausalWindow only).
+template <int H, int D, bool FP8, bool RELU, bool WIN>
+__global__ void __launch_bounds__((IdxCfg<H, D, FP8>::NT))
+__attribute__((amdgpu_waves_per_eu(!WIN && (FP8 || D <= 64) ? 3 : 2)))
 indexer_score_kernel(const IdxParams p) {
   using C = IdxCfg<H, D, FP8>;
   __shared__ __attribute__((aligned(16))) unsigned char KS[2][C::KT * C::KS_STRIDE];
   const int64_t b = blockIdx.z;
-  if (p.causal == 2) {
+  if (!WIN && p.causal == 2) {
     const int64_t ntb = (p.Sq + C::TT - 1) / C::TT;
     const int64_t tb_long = ntb - 1 - (int64_t)blockIdx.y, tb_short = blockIdx.y;
     // a block's row: keys [0, min(last token + 1, Sk)), in 32-key sub-tiles
@@ -358,54 +404,102 @@ indexer_score_kernel(const IdxParams p) {
     }
     return;
   }
-  const int64_t t0 = (int64_t)(gridDim.y - 1 - blockIdx.y) * C::TT;
-  const int64_t k0 = (int64_t)blockIdx.x * C::CHUNK;
-  const int64_t t_last = (t0 + C::TT < p.Sq ? t0 + C::TT : p.Sq) - 1;
-  const int64_t chunk_end = k0 + C::CHUNK < p.Sk ? k0 + C::CHUNK : p.Sk;
-  bool outside = p.causal == 1 && k0 > t_last + p.coff;
-  if (p.causal == kCausalWindow) {
-    // union of the block's token windows (TT <= 64 tokens: one per lane of wave 0)
-    __shared__ int blk_win[2];
+  if constexpr (WIN) {
+    // Window mode, paired like the lower triangle: block ntb-1-j with block j,
+    // each computing the 32-key sub-tiles of its token windows' union
+    // [lo, hi) (rounded out to 32 keys), the pair's sub-tiles split into equal
+    // pieces; every piece also writes -inf into its share of the two blocks'
+    // rows outside their unions (rows piece, piece + pieces, ...).
+    const int64_t ntb = (p.Sq + C::TT - 1) / C::TT;
+    const int64_t tb_long = ntb - 1 - (int64_t)blockIdx.y, tb_short = blockIdx.y;
+    const bool has_short = tb_short < tb_long;
+    __shared__ int uni[4];  // lo / hi of the long block, then of the short block
     if (threadIdx.x < 64) {
-      const int64_t t = t0 + threadIdx.x;
-      const bool ok = threadIdx.x < C::TT && t < p.Sq;
+      const int lane = (int)threadIdx.x;
+      const int64_t tb = lane < 32 ? tb_long : tb_short;
+      const int tl = lane & 31;
+      const int64_t t = tb * C::TT + tl;
+      const bool ok = tl < C::TT && t < p.Sq && (lane < 32 || has_short);
       int st = ok ? p.starts[b * p.Sq + t] : 0, en = ok ? p.ends[b * p.Sq + t] : 0;
+      st = st < 0 ? 0 : st;
+      en = en > p.Sk ? (int)p.Sk : en;
       if (en <= st) { st = 0x7fffffff; en = 0; }
-      for (int off = 32; off >= 1; off >>= 1) {
+      for (int off = 16; off >= 1; off >>= 1) {  // within each half of the wave
         const int so = __shfl_xor(st, off, 64), eo = __shfl_xor(en, off, 64);
         st = so < st ? so : st;
         en = eo > en ? eo : en;
       }
-      if (threadIdx.x == 0) { blk_win[0] = st; blk_win[1] = en; }
+      if (tl == 0) {
+        const int lo32 = en > 0 ? st / 32 * 32 : 0;
+        int hi32 = en > 0 ? (en + 31) / 32 * 32 : 0;
+        hi32 = hi32 > p.Sk ? (int)p.Sk : hi32;
+        uni[(lane >> 5) * 2] = lo32;
+        uni[(lane >> 5) * 2 + 1] = hi32;
+      }
     }
     __syncthreads();
-    outside = chunk_end <= blk_win[0] || k0 >= blk_win[1];
-  }
-  if (outside) {
-    // chunk wholly above the block's diagonal (mode 1) or outside every window (mode 3): -inf only
+    const int64_t lo_l = uni[0], hi_l = uni[1], lo_s = uni[2], hi_s = has_short ? uni[3] : uni[2];
+    const int64_t n_long = (hi_l - lo_l + 31) / 32, n = n_long + (hi_s - lo_s + 31) / 32;
+    const int64_t pieces = gridDim.x;
+    const int64_t lo = (int64_t)blockIdx.x * n / pieces, hi = ((int64_t)blockIdx.x + 1) * n / pieces;
+#pragma unroll 1
+    for (int sg = 0; sg < 2; ++sg) {
+      const int64_t a = sg == 0 ? lo : (lo > n_long ? lo : n_long) - n_long;
+      const int64_t e = sg == 0 ? (hi < n_long ? hi : n_long) : hi - n_long;
+      const int64_t k_lo = sg == 0 ? lo_l : lo_s, k_hi = sg == 0 ? hi_l : hi_s;
+      if (e > a) {
+        const int64_t kb_end = k_lo + e * 32;
+        idx_segment<H, D, FP8, RELU, true>(p, KS, b, (sg == 0 ? tb_long : tb_short) * C::TT, k_lo + a * 32,
+                                           kb_end < k_hi ? kb_end : k_hi);
+      }
+    }
+    // -inf outside the unions, rows of both blocks shared out among the pair's pieces
     float *out_b = p.out + b * p.Sq * p.Sk;
-    const int64_t nk = chunk_end - k0;
-    for (int64_t i = threadIdx.x; i < (t_last - t0 + 1) * nk; i += C::NT)
-      out_b[(t0 + i / nk) * p.Sk + k0 + i % nk] = -INFINITY;
+#pragma unroll 1
+    for (int sg = 0; sg < (has_short ? 2 : 1); ++sg) {
+      const int64_t t0s = (sg == 0 ? tb_long : tb_short) * C::TT;
+      const int64_t t_end = t0s + C::TT < p.Sq ? t0s + C::TT : p.Sq;
+      const int64_t k_lo = sg == 0 ? lo_l : lo_s, k_hi = sg == 0 ? hi_l : hi_s;
+      for (int64_t t = t0s + blockIdx.x; t < t_end; t += pieces) {
+        fill_neg_inf_rows<C::NT>(out_b, p.Sk, t, t, 0, k_lo);
+        fill_neg_inf_rows<C::NT>(out_b, p.Sk, t, t, k_hi > k_lo ? k_hi : 0, p.Sk);
+      }
+    }
+    return;
+  } else {
+  const int64_t t0 = (int64_t)(gridDim.y - 1 - blockIdx.y) * C::TT;
+  const int64_t k0 = (int64_t)blockIdx.x * C::CHUNK;
+  const int64_t t_last = (t0 + C::TT < p.Sq ? t0 + C::TT : p.Sq) - 1;
+  const int64_t chunk_end = k0 + C::CHUNK < p.Sk ? k0 + C::CHUNK : p.Sk;
+  const bool outside = p.causal == 1 && k0 > t_last + p.coff;
+  if (outside) {
+    // chunk wholly above the block's diagonal (mode 1): -inf only
+    fill_neg_inf_rows<C::NT>(p.out + b * p.Sq * p.Sk, p.Sk, t0, t_last, k0, chunk_end);
     return;
   }
   idx_segment<H, D, FP8, RELU>(p, KS, b, t0, k0, chunk_end);
+  }
 }
 
 // Workgroups of `kernel` resident at once on the current device (cached per device).
 template <class K>
 static int64_t resident_groups(K kernel, int threads) {
-  static int cache[64] = {0};
+  // cached per (device, kernel): kernels of one signature share the type K
+  struct Entry { const void *k; int dev; int groups; };
+  static Entry cache[256];
+  static int used = 0;
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cache[dev] == 0) {
-    int cus = 0, per_cu = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess)
-      return 0;
-    cache[dev] = cus * (per_cu > 0 ? per_cu : 1);
-  }
-  return cache[dev];
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  const void *kp = reinterpret_cast<const void *>(kernel);
+  for (int i = 0; i < used; ++i)
+    if (cache[i].k == kp && cache[i].dev == dev) return cache[i].groups;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess)
+    return 0;
+  const int groups = cus * (per_cu > 0 ? per_cu : 1);
+  if (used < 256) cache[used++] = Entry{kp, dev, groups};
+  return groups;
 }
 
 // Pieces per block pair: the smallest count (1..8) whose grid fills the
@@ -432,14 +526,19 @@ static int launch_idx_act(const IdxParams &p, hipStream_t st) {
   DSA_REQUIRE(ntb < 65536, "dsa_indexer_scores: %lld query tokens exceed the grid (%d per workgroup)",
               (long long)p.Sq, C::TT);
   dim3 grid;
-  if (p.causal == 2) {
+  if (p.causal == 2 || p.causal == kCausalWindow) {
     const int64_t npairs = (ntb + 1) / 2;
-    const int pieces = pick_pieces(npairs * p.B, resident_groups(indexer_score_kernel<H, D, FP8, RELU>, C::NT));
+    const bool w = p.causal == kCausalWindow;
+    const int pieces = pick_pieces(npairs * p.B, w ? resident_groups(indexer_score_kernel<H, D, FP8, RELU, true>, C::NT)
+                                                   : resident_groups(indexer_score_kernel<H, D, FP8, RELU, false>, C::NT));
     grid = dim3((unsigned)pieces, (unsigned)npairs, (unsigned)p.B);
   } else {
     grid = dim3((unsigned)((p.Sk + C::CHUNK - 1) / C::CHUNK), (unsigned)ntb, (unsigned)p.B);
   }
-  hipLaunchKernelGGL((indexer_score_kernel<H, D, FP8, RELU>), grid, dim3(C::NT), 0, st, p);
+  if (p.causal == kCausalWindow)
+    hipLaunchKernelGGL((indexer_score_kernel<H, D, FP8, RELU, true>), grid, dim3(C::NT), 0, st, p);
+  else
+    hipLaunchKernelGGL((indexer_score_kernel<H, D, FP8, RELU, false>), grid, dim3(C::NT), 0, st, p);
   return check_launch("indexer_scores");
 }
 
@@ -455,8 +554,8 @@ using namespace dsa;
 static int indexer_scores_impl(const void *q, const void *w, const void *k, float *scores, int64_t B, int64_t Sq,
                                int64_t Sk, int64_t H, int64_t D, int dtype, int w_dtype, const float *q_scale,
                                const float *k_scale, int causal, const int32_t *starts, const int32_t *ends,
-                               const float *mask, int64_t mask_bstride, int use_relu, hipStream_t st,
-                               const char *fn, int64_t coff = 0) {
+                               const float *mask, int64_t mask_bstride, const int32_t *row_plain, int use_relu,
+                               hipStream_t st, const char *fn, int64_t coff = 0) {
   DSA_REQUIRE(B >= 0 && Sq >= 0 && Sk >= 0 && H > 0 && D > 0, "%s: bad dims", fn);
   DSA_REQUIRE(dtype == DSA_DTYPE_BF16 || dtype == DSA_DTYPE_E4M3, "%s: dtype %d", fn, dtype);
   DSA_REQUIRE(w_dtype == DSA_DTYPE_BF16 || w_dtype == DSA_DTYPE_F32, "%s: w dtype %d", fn, w_dtype);
@@ -479,6 +578,7 @@ static int indexer_scores_impl(const void *q, const void *w, const void *k, floa
   p.ends = ends;
   p.mask = mask;
   p.mask_bstride = mask_bstride;
+  p.row_plain = row_plain;
   p.B = B;
   p.Sq = Sq;
   p.Sk = Sk;
@@ -504,18 +604,19 @@ extern "C" int dsa_indexer_scores(const void *q, const void *w, const void *k, f
                                   void *stream) {
   DSA_REQUIRE(causal >= 0 && causal <= 2, "dsa_indexer_scores: causal must be 0, 1 or 2");
   return indexer_scores_impl(q, w, k, scores, B, Sq, Sk, H, D, dtype, w_dtype, q_scale, k_scale, causal, nullptr,
-                             nullptr, nullptr, 0, use_relu, static_cast<hipStream_t>(stream), "dsa_indexer_scores");
+                             nullptr, nullptr, 0, nullptr, use_relu, static_cast<hipStream_t>(stream),
+                             "dsa_indexer_scores");
 }
 
 extern "C" int dsa_indexer_scores_masked(const void *q, const void *w, const void *k, float *scores, int64_t B,
                                          int64_t Sq, int64_t Sk, int64_t H, int64_t D, int dtype, int w_dtype,
                                          const float *q_scale, const float *k_scale, const int32_t *starts,
                                          const int32_t *ends, const float *mask, int64_t mask_bstride,
-                                         int use_relu, void *stream) {
+                                         const int32_t *row_plain, int use_relu, void *stream) {
   DSA_REQUIRE(starts && ends, "dsa_indexer_scores_masked: null window arrays");
   DSA_REQUIRE(mask_bstride >= 0, "dsa_indexer_scores_masked: negative mask batch stride");
   return indexer_scores_impl(q, w, k, scores, B, Sq, Sk, H, D, dtype, w_dtype, q_scale, k_scale, kCausalWindow,
-                             starts, ends, mask, mask_bstride, use_relu, static_cast<hipStream_t>(stream),
+                             starts, ends, mask, mask_bstride, row_plain, use_relu, static_cast<hipStream_t>(stream),
                              "dsa_indexer_scores_masked");
 }
 
@@ -596,7 +697,7 @@ extern "C" int dsa_indexer_topk_streaming(const void *q, const void *w, const vo
     const unsigned char *qc = static_cast<const unsigned char *>(q) + r0 * B * H * D * elt;
     const unsigned char *wc = static_cast<const unsigned char *>(w) + r0 * B * H * welt;
     int rc = indexer_scores_impl(qc, wc, k, scratch, B, rows, pitch, H, D, dtype, w_dtype, q_scale, k_scale,
-                                 causal ? 2 : 0, nullptr, nullptr, nullptr, 0, use_relu, st,
+                                 causal ? 2 : 0, nullptr, nullptr, nullptr, 0, nullptr, use_relu, st,
                                  "dsa_indexer_topk_streaming", causal ? r0 : 0);
     if (rc) return rc;
     // every batch's rows in one top-k launch (outputs Sq * topk apart)

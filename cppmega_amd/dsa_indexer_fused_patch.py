@@ -41,14 +41,16 @@ CAUSAL_WINDOW = 3     # per-row [start, end) windows plus an additive mask, -inf
 
 
 def index_scores(q, weights, k, use_relu=True, causal=CAUSAL_NONE, q_scale=None, k_scale=None, out=None,
-                 starts=None, ends=None, mask=None):
+                 starts=None, ends=None, mask=None, row_plain=None):
     """q [sq,b,h,d] (bf16 or e4m3), weights [sq,b,h] (f32 or bf16), k [sk,b,d] -> [b,sq,sk] f32.
 
     For e4m3 q / k, q_scale and k_scale are one-element f32 tensors (per-tensor
     dequant factors, real = fp8 * scale).  causal=CAUSAL_WINDOW keeps, for row t
     of batch b, the columns [starts[b, t], ends[b, t]) (int32 device tensors
     broadcastable to [b, sq]) and adds ``mask`` there (f32, broadcastable to
-    [b, sq, sk], or None); every other element is -inf.
+    [b, sq, sk], or None); every other element is -inf.  ``row_plain`` (int32
+    [b, sq], optional; ``mask_windows``' third output) flags rows whose mask is
+    +0.0 on the whole window: their mask is not read (same result).
     """
     assert q.dim() == 4, f"q must be [sq,b,h,d], got {tuple(q.shape)}"
     assert k.dim() == 3, f"k must be [sk,b,d], got {tuple(k.shape)}"
@@ -86,12 +88,14 @@ def index_scores(q, weights, k, use_relu=True, causal=CAUSAL_NONE, q_scale=None,
                 f"mask {tuple(mask.shape)} does not broadcast to {(b, sq, sk)}"
             mask = mask.contiguous()
             bstride = 0 if mask.shape[0] == 1 else sq * sk
+        if row_plain is not None:
+            row_plain = row_plain.to(device=q.device, dtype=torch.int32).expand(b, sq).contiguous()
         rc = _lib.load().dsa_indexer_scores_masked(
             q.data_ptr(), weights.data_ptr(), k.data_ptr(), out.data_ptr(), b, sq, sk, h, d,
             _lib.DTYPE_E4M3 if fp8 else _lib.DTYPE_BF16,
             _lib.DTYPE_F32 if weights.dtype == torch.float32 else _lib.DTYPE_BF16,
             _lib.ptr(q_scale), _lib.ptr(k_scale), starts.data_ptr(), ends.data_ptr(), _lib.ptr(mask), bstride,
-            1 if use_relu else 0, _lib.stream_ptr(dev))
+            _lib.ptr(row_plain), 1 if use_relu else 0, _lib.stream_ptr(dev))
         _lib.check(rc, "dsa_indexer_scores_masked")
         return out
     rc = _lib.load().dsa_indexer_scores(
@@ -103,11 +107,14 @@ def index_scores(q, weights, k, use_relu=True, causal=CAUSAL_NONE, q_scale=None,
     return out
 
 
-def index_scores_backward(grad, q, weights, k, use_relu=True, causal=False):
+def index_scores_backward(grad, q, weights, k, use_relu=True, causal=False, starts=None, ends=None):
     """Gradients of ``index_scores`` (bf16 q / k) for grad = d loss / d scores
     [b, sq, sk]: returns (dq [sq,b,h,d] bf16, dweights [sq,b,h] in weights'
     dtype, dk [sk,b,d] bf16).  causal=True ignores grad above the diagonal
-    (the entries a lower-triangle forward never wrote)."""
+    (the entries a lower-triangle forward never wrote).  starts / ends (int32,
+    broadcastable to [b, sq]; both or neither): the window-mode forward's row
+    windows; grad outside them is ignored (the forward wrote -inf there
+    whatever the raw score) and key tiles outside every window are skipped."""
     sq, b, h, d = q.shape
     sk = k.shape[0]
     assert q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16, \
@@ -117,6 +124,11 @@ def index_scores_backward(grad, q, weights, k, use_relu=True, causal=False):
         weights = weights.float()
     grad = grad.to(torch.float32).contiguous()
     q, k, weights = q.contiguous(), k.contiguous(), weights.contiguous()
+    if (starts is None) != (ends is None):
+        raise ValueError("give both starts and ends, or neither")
+    if starts is not None:
+        starts = starts.to(device=q.device, dtype=torch.int32).expand(b, sq).contiguous()
+        ends = ends.to(device=q.device, dtype=torch.int32).expand(b, sq).contiguous()
     dq = torch.empty_like(q)
     dw = torch.empty_like(weights)
     dk = torch.empty_like(k)
@@ -128,7 +140,8 @@ def index_scores_backward(grad, q, weights, k, use_relu=True, causal=False):
         grad.data_ptr(), q.data_ptr(), weights.data_ptr(), k.data_ptr(), dq.data_ptr(), dw.data_ptr(),
         dk.data_ptr(), b, sq, sk, h, d, _lib.DTYPE_BF16,
         _lib.DTYPE_F32 if weights.dtype == torch.float32 else _lib.DTYPE_BF16,
-        1 if causal else 0, 1 if use_relu else 0, ws.data_ptr(), ws_bytes, _lib.stream_ptr(dev))
+        1 if causal else 0, 1 if use_relu else 0, _lib.ptr(starts), _lib.ptr(ends), ws.data_ptr(), ws_bytes,
+        _lib.stream_ptr(dev))
     _lib.check(rc, "dsa_indexer_scores_backward")
     return dq, dw, dk
 
@@ -136,20 +149,28 @@ def index_scores_backward(grad, q, weights, k, use_relu=True, causal=False):
 class IndexScores(torch.autograd.Function):
     """Indexer scores with a backward to q, weights and k.
 
-    forward(q, weights, k, use_relu, causal, starts, ends, mask) -> [b, sq, sk]
-    f32 with ``index_scores``' modes (CAUSAL_NONE, CAUSAL_NEG_INF, CAUSAL_LOWER,
-    CAUSAL_WINDOW).  The lower-triangle modes write constants above the
-    diagonal, which carry no gradient (causal backward).  The window mode is
-    Megatron's ``scores + mask``: the raw scores receive the upstream gradient
-    everywhere, masked entries included, as autograd through the add gives
-    them (full backward; the raw scores are recomputed, so entries the forward
-    never computed are no obstacle).
+    forward(q, weights, k, use_relu, causal, starts, ends, mask, row_plain) ->
+    [b, sq, sk] f32 with ``index_scores``' modes (CAUSAL_NONE, CAUSAL_NEG_INF,
+    CAUSAL_LOWER, CAUSAL_WINDOW).  The lower-triangle modes write constants
+    above the diagonal, which carry no gradient (causal backward).  The window
+    mode is Megatron's ``scores + mask`` inside the row windows and the
+    constant -inf outside them: inside, the raw scores receive the upstream
+    gradient as autograd through the add gives it (mask holes included);
+    outside, the output does not depend on the raw scores, so the gradient
+    there is ignored and the backward computes only the key tiles inside the
+    windows (a causal mask costs the lower-triangle backward).  Megatron's
+    torch add would pass a gradient at -inf entries on to the raw scores; a
+    finite loss of the scores (softmax, KL) gives exactly zero there.
     """
 
     @staticmethod
-    def forward(ctx, q, weights, k, use_relu=True, causal=CAUSAL_NONE, starts=None, ends=None, mask=None):
-        out = index_scores(q, weights, k, use_relu=use_relu, causal=causal, starts=starts, ends=ends, mask=mask)
-        ctx.save_for_backward(q, weights, k)
+    def forward(ctx, q, weights, k, use_relu=True, causal=CAUSAL_NONE, starts=None, ends=None, mask=None,
+                row_plain=None):
+        out = index_scores(q, weights, k, use_relu=use_relu, causal=causal, starts=starts, ends=ends, mask=mask,
+                           row_plain=row_plain)
+        win = causal == CAUSAL_WINDOW
+        ctx.save_for_backward(q, weights, k, *((starts, ends) if win else ()))
+        ctx.win = win
         ctx.use_relu = use_relu
         ctx.causal = causal in (CAUSAL_NEG_INF, CAUSAL_LOWER)
         ctx.wdtype = weights.dtype
@@ -157,9 +178,11 @@ class IndexScores(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad):
-        q, weights, k = ctx.saved_tensors
-        dq, dw, dk = index_scores_backward(grad, q, weights, k, use_relu=ctx.use_relu, causal=ctx.causal)
-        return dq, dw.to(ctx.wdtype), dk, None, None, None, None, None
+        q, weights, k, *win = ctx.saved_tensors
+        starts, ends = win if ctx.win else (None, None)
+        dq, dw, dk = index_scores_backward(grad, q, weights, k, use_relu=ctx.use_relu, causal=ctx.causal,
+                                           starts=starts, ends=ends)
+        return dq, dw.to(ctx.wdtype), dk, None, None, None, None, None, None
 
 
 def _needs_grad(*ts):

@@ -18,12 +18,13 @@ from .dsa_indexer_fused_patch import (CAUSAL_LOWER, CAUSAL_NEG_INF, CAUSAL_NONE,
                                       index_scores)
 
 
-def _scores(q, weights, k, use_relu, causal, starts=None, ends=None, mask=None):
+def _scores(q, weights, k, use_relu, causal, starts=None, ends=None, mask=None, row_plain=None):
     """index_scores, through the differentiable IndexScores when grad mode is on
     and q, weights or k requires grad (the scores Megatron's loss consumes)."""
     if torch.is_grad_enabled() and any(t.requires_grad for t in (q, weights, k)):
-        return IndexScores.apply(q, weights, k, use_relu, causal, starts, ends, mask)
-    return index_scores(q, weights, k, use_relu=use_relu, causal=causal, starts=starts, ends=ends, mask=mask)
+        return IndexScores.apply(q, weights, k, use_relu, causal, starts, ends, mask, row_plain)
+    return index_scores(q, weights, k, use_relu=use_relu, causal=causal, starts=starts, ends=ends, mask=mask,
+                        row_plain=row_plain)
 
 
 def topk_indices(scores, topk, causal=True, starts=None, ends=None, causal_offset=0, seq_q=None):
@@ -83,30 +84,43 @@ def _row_windows(x, b, sq, what):
 
 
 def mask_windows(mask, b, sq, sk):
-    """[first, last + 1) span of the finite entries of each row of an additive
-    mask broadcastable to [b, sq, sk], as int32 [b, sq] tensors ((0, 0) for a
-    row without a finite entry).  Device ops only: no host synchronisation."""
-    m = mask.reshape(-1, sq, sk)
-    fin = torch.isfinite(m)
-    fin8 = fin.to(torch.uint8)
-    has = fin.any(-1)
-    first = fin8.argmax(-1)                      # first maximum: the first finite column
-    end = sk - fin8.flip(-1).argmax(-1)          # one past the last finite column
-    zero = torch.zeros_like(first)
-    starts = torch.where(has, first, zero).to(torch.int32)
-    ends = torch.where(has, end, zero).to(torch.int32)
-    return starts.expand(b, sq), ends.expand(b, sq)
+    """Candidate windows of an additive mask broadcastable to [b, sq, sk]:
+    (starts, ends, plain), int32 [b, sq] each -- the first finite column of
+    every row, one past its last ((0, 0) for a row without one), and 1 where
+    every entry in between is +0.0 (no finite bias, no -inf hole).  One kernel
+    (dsa_mask_windows) reads the mask once; no host synchronisation."""
+    m = mask.to(dtype=torch.float32).reshape(-1, sq, sk)
+    if m.shape[0] not in (1, b):
+        raise ValueError(f"mask {tuple(mask.shape)} does not broadcast to {(b, sq, sk)}")
+    m = m.contiguous()
+    starts = torch.empty((b, sq), dtype=torch.int32, device=m.device)
+    ends = torch.empty_like(starts)
+    plain = torch.empty_like(starts)
+    dev = _lib.ensure_device(m)
+    rc = _lib.load().dsa_mask_windows(m.data_ptr(), m.shape[0], b, sq, sk, starts.data_ptr(), ends.data_ptr(),
+                                      plain.data_ptr(), _lib.stream_ptr(dev))
+    _lib.check(rc, "dsa_mask_windows")
+    return starts, ends, plain
 
 
-def drop_masked_picks(scores, idx):
-    """Picks whose score is -inf (an interior hole of a masked row that the
-    window held fewer finite columns than topk around) become -1, and the
-    remaining columns stay ascending with the -1 padding at the end."""
-    sel = scores.gather(-1, idx.clamp(min=0).to(torch.int64))
-    big = torch.iinfo(torch.int32).max
-    key = torch.where((idx < 0) | torch.isneginf(sel), torch.full_like(idx, big), idx)
-    key = key.sort(dim=-1).values
-    return torch.where(key == big, torch.full_like(key, -1), key)
+def finalize_picks(scores, idx, plain=None):
+    """idx [b, sq, k] int32 (ascending, -1 padded) -> int64, with the picks whose
+    score in ``scores`` [b, sq, sk] is -inf (holes inside a window that held
+    fewer finite columns than k) turned into -1 and the rest kept ascending,
+    on every row not flagged in ``plain`` (int32 [b, sq]; None: every row is
+    checked).  One kernel (dsa_topk_finalize)."""
+    assert scores.dtype == torch.float32 and scores.is_contiguous() and idx.dtype == torch.int32
+    sk = scores.shape[-1]
+    rows = idx.numel() // idx.shape[-1]
+    idx = idx.contiguous()
+    out = torch.empty(idx.shape, dtype=torch.int64, device=idx.device)
+    if plain is not None:
+        plain = plain.to(torch.int32).expand(*idx.shape[:-1]).contiguous()
+    dev = _lib.ensure_device(idx)
+    rc = _lib.load().dsa_topk_finalize(scores.data_ptr(), sk, idx.data_ptr(), rows, idx.shape[-1], _lib.ptr(plain),
+                                       out.data_ptr(), _lib.stream_ptr(dev))
+    _lib.check(rc, "dsa_topk_finalize")
+    return out
 
 
 def indexer_topk_streaming(q, k, weights, index_topk, use_relu=True, causal=True, q_scale=None, k_scale=None,
@@ -195,25 +209,25 @@ def fused_qk_topk_naive(q, k, weights, index_topk, mask=None, varlen_starts=None
         ve = _row_windows(varlen_ends.to(dev), b, sq, "varlen_ends")
     if add is not None:
         add = add.reshape(-1, sq, sk)                                                # [1 or b, sq, sk]
+    plain = None
     if varlen and key_positions is not None:
         # a key's position need not be its column: the windows become an additive mask
         kp = key_positions.to(device=dev, dtype=torch.int64).reshape(-1, 1, sk)    # [1 or b, 1, sk]
         ok = (kp >= vs.unsqueeze(-1)) & (kp < ve.unsqueeze(-1))                    # [b, sq, sk]
         kmask = torch.zeros(ok.shape, dtype=torch.float32, device=dev).masked_fill_(~ok, float("-inf"))
         add = kmask if add is None else add + kmask
-        starts, ends = mask_windows(add, b, sq, sk)
+        starts, ends, plain = mask_windows(add, b, sq, sk)
     elif add is not None:
-        starts, ends = mask_windows(add, b, sq, sk)
-        if varlen:
-            starts, ends = torch.maximum(starts, vs), torch.minimum(ends, ve)
+        starts, ends, plain = mask_windows(add, b, sq, sk)
+        if varlen:  # a narrower window of a plain row is still plain
+            starts, ends = torch.maximum(starts, vs).contiguous(), torch.minimum(ends, ve).contiguous()
     else:
-        starts, ends = vs, ve
-    starts, ends = starts.contiguous(), ends.contiguous()
-    scores = _scores(q, weights, k, use_relu, CAUSAL_WINDOW, starts, ends, add)
+        starts, ends = vs.contiguous(), ve.contiguous()
+    scores = _scores(q, weights, k, use_relu, CAUSAL_WINDOW, starts, ends, add, plain)
     idx = topk_indices(scores.detach(), topk_k, causal=False, starts=starts, ends=ends)
-    if add is not None:
-        idx = drop_masked_picks(scores.detach(), idx)
-    return scores, idx.to(torch.int64)
+    if add is None:  # raw scores inside the windows: no -inf pick
+        return scores, idx.to(torch.int64)
+    return scores, finalize_picks(scores.detach(), idx, plain)
 
 
 _TOPK_MARKER = "__cppmega_amd_dsa_topk_patched__"
@@ -244,5 +258,5 @@ def apply_dsa_topk_patch(*, force: bool = False, dsa_module=None) -> bool:
 
 
 __all__ = ["CAUSAL_LOWER", "CAUSAL_NEG_INF", "CAUSAL_NONE", "CAUSAL_WINDOW", "apply_dsa_topk_patch",
-           "drop_masked_picks", "fused_qk_topk_naive", "indexer_topk", "indexer_topk_streaming", "mask_windows",
+           "finalize_picks", "fused_qk_topk_naive", "indexer_topk", "indexer_topk_streaming", "mask_windows",
            "topk_indices"]

@@ -235,7 +235,10 @@ int dsa_indexer_scores(const void *q, const void *w, const void *k,
  *   q, w, k, scores, dtype, w_dtype, q_scale, k_scale, use_relu as in
  *   dsa_indexer_scores; starts, ends [B, Sq] int32 (device);
  *   mask [Mb, Sq, Sk] f32 with batch stride mask_bstride elements (0: one mask
- *   shared by every batch) or NULL (no additive term).
+ *   shared by every batch) or NULL (no additive term);
+ *   row_plain [B, Sq] int32 (device) or NULL: rows flagged nonzero have a mask
+ *   of +0.0 on their whole window (dsa_mask_windows' plain flags), which is
+ *   then not read (score + 0.0f: the same bits as score + mask).
  * Key tiles outside every window of a group of query tokens are not computed,
  * so a causal window costs the lower-triangle work.  Every element is written.
  */
@@ -245,7 +248,37 @@ int dsa_indexer_scores_masked(const void *q, const void *w, const void *k,
                               const float *q_scale, const float *k_scale,
                               const int32_t *starts, const int32_t *ends,
                               const float *mask, int64_t mask_bstride,
-                              int use_relu, void *stream);
+                              const int32_t *row_plain, int use_relu,
+                              void *stream);
+
+/*
+ * Per-row candidate windows of Megatron's additive mask (fused_qk_topk_naive's
+ * mask argument, call shapes cppmega/megatron/lemyx_dsa_warmup.py:169-176):
+ * for every row t of mask [mask_batches, Sq, Sk] f32 (mask_batches 1 = one
+ * mask for every batch, or B), starts / ends [B, Sq] int32 get the first
+ * finite column and one past the last ((0, 0) for a row without one), and
+ * plain [B, Sq] int32 gets 1 when every entry in between is +0.0 (no finite
+ * bias, no -inf / NaN hole), else 0.  One read of the mask, no host
+ * synchronisation.  No counterpart in the reference (Megatron adds the mask
+ * to the dense scores).
+ */
+int dsa_mask_windows(const float *mask, int64_t mask_batches, int64_t B,
+                     int64_t Sq, int64_t Sk, int32_t *starts, int32_t *ends,
+                     int32_t *plain, void *stream);
+
+/*
+ * Last step of the masked top-k: idx [rows, topk] int32 (dsa_topk output,
+ * ascending, -1 padded) -> out [rows, topk] int64.  On rows not flagged in
+ * plain [rows] (NULL: no row is), picks whose score in scores (rows of
+ * row_stride f32) is -inf -- mask holes inside a window that held fewer
+ * finite columns than topk -- become -1 and the remaining picks stay
+ * ascending, padded with -1 at the end.  Megatron returns such picks as
+ * indices (torch.topk over index_scores + mask); this build's contract
+ * returns only the finite-mask columns.
+ */
+int dsa_topk_finalize(const float *scores, int64_t row_stride,
+                      const int32_t *idx, int64_t rows, int64_t topk,
+                      const int32_t *plain, int64_t *out, void *stream);
 
 /*
  * Backward of dsa_indexer_scores (bf16 q / k): given grad_scores G [B, Sq, Sk] f32,
@@ -261,9 +294,15 @@ int dsa_indexer_scores_masked(const void *q, const void *w, const void *k,
  *   q [Sq, B, H, D] bf16, w [Sq, B, H] (w_dtype), k [Sk, B, D] bf16;
  *   dq [Sq, B, H, D] bf16, dw [Sq, B, H] (w_dtype), dk [Sk, B, D] bf16 (written).
  * causal: 0 = every (t, s); 1 = only s <= t (G above the diagonal ignored).
+ * starts / ends [B, Sq] int32 (device; both or neither): row windows, the
+ * backward of dsa_indexer_scores_masked -- G outside [start, end) is ignored
+ * (the masked forward writes -inf there whatever the raw score) and key tiles
+ * outside every window of a group of rows are not computed, so a causal
+ * window costs the lower-triangle work.
  * Deterministic (fixed summation orders, no atomics).  workspace >=
  * dsa_indexer_scores_backward_workspace_size() bytes (fp32 dk partials per
- * token chunk).  Limits: Sq * Sk < 2^30, H in {16, 32, 64}, D in {64, 128}.
+ * token chunk, and the windows' chunk flags).  Limits: Sq * Sk < 2^30,
+ * H in {16, 32, 64}, D in {64, 128}.
  */
 size_t dsa_indexer_scores_backward_workspace_size(int64_t B, int64_t Sq,
                                                   int64_t Sk, int64_t H,
@@ -273,6 +312,7 @@ int dsa_indexer_scores_backward(const float *grad_scores, const void *q,
                                 void *dw, void *dk, int64_t B, int64_t Sq,
                                 int64_t Sk, int64_t H, int64_t D, int dtype,
                                 int w_dtype, int causal, int use_relu,
+                                const int32_t *starts, const int32_t *ends,
                                 void *workspace, size_t workspace_bytes,
                                 void *stream);
 

@@ -78,18 +78,26 @@ def index_scores_diff(q, weights, k, use_relu=True):
     return out
 
 
-def index_scores_backward(grad, q, weights, k, use_relu=True, causal=False):
+def index_scores_backward(grad, q, weights, k, use_relu=True, causal=False, starts=None, ends=None):
     """Gradients (dq, dweights, dk) in float64 of the reference's score loop for
     the upstream gradient `grad` [b, sq, sk], by autograd through
     index_scores_diff (what autograd through the reference's torch loop
     computes).  causal=True zeroes grad above the diagonal first (the entries
-    a lower-triangle forward never computed).  Pinned by
+    a lower-triangle forward never computed); starts / ends ([b, sq] or [sq])
+    zero it outside each row's window [start, end) (the entries a window-mode
+    forward writes as -inf whatever the raw score).  Pinned by
     torch.autograd.gradcheck (finite differences) and a one-head, one-key
     closed form in tests/test_oracle_indexer_topk_fp8.py."""
     g = grad.detach().double()
     if causal:
         sq, sk = g.shape[-2:]
         g = g.masked_fill(torch.ones(sq, sk, dtype=torch.bool).triu(1), 0.0)
+    if starts is not None:
+        b, sq, sk = g.shape
+        col = torch.arange(sk).view(1, 1, sk)
+        st_ = torch.as_tensor(starts).to(torch.int64).expand(b, sq).unsqueeze(-1)
+        en_ = torch.as_tensor(ends).to(torch.int64).expand(b, sq).unsqueeze(-1)
+        g = g.masked_fill((col < st_) | (col >= en_), 0.0)
     with torch.enable_grad():  # also when called from inside another backward
         qd = q.detach().double().requires_grad_(True)
         wd = weights.detach().double().requires_grad_(True)

@@ -86,3 +86,59 @@ def topk_bruteforce_row(row, topk, start=0, end=None, admissible=None):
 def topk_bytes(b, s, topk):
     """Algorithmic HBM bytes of causal top-k: fp32 causal scores read + int32 indices written."""
     return 4 * b * s * (s + 1) // 2 + 4 * b * s * topk
+
+
+def mask_windows(mask):
+    """Candidate windows of an additive mask [R, sq, sk] (numpy, float32):
+    (starts, ends, plain) int32 [R, sq] -- the first finite column of each row,
+    one past its last ((0, 0) when the row has none), and 1 where every entry
+    in between is +0.0 (bit pattern 0: no finite bias, no -inf / NaN hole).
+    The windows are the candidate sets of fused_qk_topk_naive's masked rows
+    (index_scores + mask, call shapes cppmega/megatron/lemyx_dsa_warmup.py:169-176);
+    Megatron itself is not vendored, so this is this build's contract (parity
+    unpinned against Megatron), pinned by a per-element brute force
+    (``mask_windows_bruteforce``) and hypothesis in the CPU tests."""
+    m = np.ascontiguousarray(mask, dtype=np.float32)
+    R, sq, sk = m.shape
+    fin = np.isfinite(m)
+    has = fin.any(-1)
+    first = np.argmax(fin, axis=-1)
+    last = sk - 1 - np.argmax(fin[..., ::-1], axis=-1)
+    starts = np.where(has, first, 0).astype(np.int32)
+    ends = np.where(has, last + 1, 0).astype(np.int32)
+    col = np.arange(sk)[None, None, :]
+    inside = (col >= starts[..., None]) & (col < ends[..., None])
+    pos_zero = m.view(np.uint32) == 0
+    plain = np.all(~inside | pos_zero, axis=-1).astype(np.int32)
+    return starts, ends, plain
+
+
+def mask_windows_bruteforce(row):
+    """One mask row (a list of floats) -> (start, end, plain) by a plain loop."""
+    import struct
+
+    cols = [i for i, v in enumerate(row) if v == v and abs(v) != float("inf")]
+    if not cols:
+        return 0, 0, 1
+    st, en = cols[0], cols[-1] + 1
+    plain = all(struct.pack("<f", row[i]) == b"\0\0\0\0" for i in range(st, en))
+    return st, en, int(plain)
+
+
+def drop_masked_picks(scores, idx, plain=None):
+    """Picks whose score is -inf become -1, the rest stay ascending with the -1
+    padding at the end, on every row not flagged in `plain` (those are
+    returned as they are).  scores [rows, sk] float32, idx [rows, k] (ascending,
+    -1 padded) -> int64 [rows, k].  The repair the sync-free Megatron top-k
+    needs after ranking index_scores + mask (masked picks become -1 as in
+    cppmega/megatron/upstream_patches/apply_dsa_cg_patches.py:267-291)."""
+    scores = np.asarray(scores, dtype=np.float32)
+    idx = np.asarray(idx, dtype=np.int64)
+    out = np.full(idx.shape, -1, dtype=np.int64)
+    for r in range(idx.shape[0]):
+        if plain is not None and plain[r]:
+            out[r] = idx[r]
+            continue
+        keep = [c for c in idx[r] if c >= 0 and scores[r, c] != -np.inf]
+        out[r, :len(keep)] = keep
+    return out

@@ -147,3 +147,57 @@ def test_fused_indexer_loss_matches_oracle(dev, sparse):
     _check(qd.grad, q64.grad, True, "dq through the loss")
     _check(wd.grad, w64.grad, True, "dw through the loss")
     _check(kd.grad, k64.grad, True, "dk through the loss")
+
+
+@pytest.mark.parametrize("S,Sk,B,H,D,relu,kind", [
+    (200, 200, 2, 16, 64, True, "causal"),
+    (160, 160, 1, 32, 128, False, "sliding"),
+    (300, 300, 1, 16, 64, True, "packed"),
+    (130, 257, 2, 64, 64, False, "random"),
+])
+def test_windowed_backward_matches_oracle(dev, S, Sk, B, H, D, relu, kind):
+    """dsa_indexer_scores_backward with row windows: the gradient outside each
+    row's [start, end) is ignored (the window-mode forward writes -inf there),
+    against float64 autograd of the score loop with the upstream gradient
+    zeroed outside the windows; causal, sliding-window, packed-sequence and
+    random windows (empty rows included)."""
+    q, w, k, grad = _inputs(S, Sk, B, H, D, torch.float32, seed=S + D + B)
+    t = torch.arange(S)
+    if kind == "causal":
+        st, en = torch.zeros(S, dtype=torch.int32), (t + 1).clamp(max=Sk).to(torch.int32)
+    elif kind == "sliding":
+        st, en = (t - 40).clamp(min=0).to(torch.int32), (t + 1).to(torch.int32)
+    elif kind == "packed":  # three sequences, causal inside each
+        seq0 = torch.where(t < 90, 0, torch.where(t < 210, 90, 210))
+        st, en = seq0.to(torch.int32), (t + 1).to(torch.int32)
+    else:
+        g = torch.Generator().manual_seed(3)
+        a = torch.randint(0, Sk, (B, S), generator=g)
+        st, en = a.to(torch.int32), (a + torch.randint(-20, 120, (B, S), generator=g)).clamp(0, Sk).to(torch.int32)
+    st = st.expand(B, S).contiguous()
+    en = en.expand(B, S).contiguous()
+    dq, dw, dk = index_scores_backward(grad.to(dev), q.to(dev), w.to(dev), k.to(dev), use_relu=relu,
+                                       starts=st.to(dev), ends=en.to(dev))
+    rq, rw, rk = oix.index_scores_backward(grad, q, w, k, use_relu=relu, starts=st, ends=en)
+    _check(dq, rq, relu, "dq")
+    _check(dw, rw, relu, "dw")
+    _check(dk, rk, relu, "dk")
+    dq2, dw2, dk2 = index_scores_backward(grad.to(dev), q.to(dev), w.to(dev), k.to(dev), use_relu=relu,
+                                          starts=st.to(dev), ends=en.to(dev))
+    assert torch.equal(dq, dq2) and torch.equal(dw, dw2) and torch.equal(dk, dk2), "not bitwise reproducible"
+
+
+def test_causal_mask_autograd_equals_causal_backward(dev):
+    """Autograd through fused_qk_topk_naive with Megatron's causal float mask
+    (window mode) gives the gradients of the lower-triangle backward, bit for
+    bit, for an upstream gradient that is zero above the diagonal (what the KL
+    loss sends: its gradient at -inf scores is exactly 0)."""
+    S, B, H, D, K = 192, 2, 16, 64, 32
+    q, w, k, grad = _inputs(S, S, B, H, D, torch.float32, seed=77)
+    grad = grad.masked_fill(torch.ones(S, S, dtype=torch.bool).triu(1), 0.0).to(dev)
+    qd, wd, kd = (x.to(dev).requires_grad_() for x in (q, w, k))
+    mask = torch.full((S, S), float("-inf"), device=dev).triu(1)
+    scores, _ = fused_qk_topk_naive(qd, kd, wd, K, mask=mask)
+    scores.backward(grad)
+    rq, rw, rk = index_scores_backward(grad, q.to(dev), w.to(dev), k.to(dev), causal=True)
+    assert torch.equal(qd.grad, rq) and torch.equal(wd.grad, rw) and torch.equal(kd.grad, rk)

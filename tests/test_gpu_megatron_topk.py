@@ -189,3 +189,85 @@ def test_nam56r_full_square_indexer(dev):
     low = index_scores(q, w, k, causal=CAUSAL_LOWER, out=torch.zeros_like(got))
     tri = torch.ones(S, S, dtype=torch.bool, device=dev).tril()
     assert torch.equal(low[:, tri], got[:, tri])
+
+
+@pytest.mark.parametrize("R,B,S,Sk", [(1, 2, 96, 128), (2, 2, 64, 77), (1, 3, 40, 300)])
+def test_mask_windows_kernel_matches_oracle(dev, R, B, S, Sk):
+    """dsa_mask_windows: first / one-past-last finite column and the plain flag
+    of every row, bit-exact with the oracle, over causal rows, sliding windows,
+    holes, finite biases, -0.0, +inf / NaN entries and all -inf rows, for one
+    shared mask and one per batch, 16-byte (Sk % 4 == 0) and scalar rows."""
+    from cppmega_amd.dsa_topk import mask_windows
+
+    g = torch.Generator().manual_seed(R * 100 + S + Sk)
+    m = torch.full((R, S, Sk), NINF)
+    for r in range(R):
+        for t in range(S):
+            kind = int(torch.randint(0, 6, (1,), generator=g))
+            a = int(torch.randint(0, Sk, (1,), generator=g))
+            e = int(torch.randint(a, Sk + 1, (1,), generator=g))
+            if kind == 0:
+                m[r, t, :min(t + 1, Sk)] = 0.0                 # causal, plain
+            elif kind == 1:
+                m[r, t, a:e] = 0.0                              # window, plain (possibly empty)
+            elif kind == 2:
+                m[r, t, a:e] = 0.0
+                if e - a > 2:
+                    m[r, t, (a + e) // 2] = NINF                # a hole
+            elif kind == 3:
+                m[r, t, a:e] = torch.randn(e - a, generator=g)  # finite biases
+            elif kind == 4:
+                m[r, t, a:e] = 0.0
+                m[r, t, a] = -0.0                               # -0.0 is not +0.0
+                if e < Sk:
+                    m[r, t, e] = float("nan") if t % 2 else float("inf")
+            # kind 5: all -inf
+    st, en, pl = mask_windows(m.to(dev), B, S, Sk)
+    rs, re_, rp = otk.mask_windows(m.numpy())
+    exp = (lambda a: np.broadcast_to(a, (B, S))) if R == 1 else (lambda a: a)
+    np.testing.assert_array_equal(st.cpu().numpy(), exp(rs))
+    np.testing.assert_array_equal(en.cpu().numpy(), exp(re_))
+    np.testing.assert_array_equal(pl.cpu().numpy(), exp(rp))
+
+
+def test_topk_finalize_matches_oracle(dev):
+    """dsa_topk_finalize: int32 picks -> int64, with -inf picks dropped (the rest
+    ascending, -1 padded) on rows not flagged plain, and plain rows copied."""
+    from cppmega_amd.dsa_topk import finalize_picks, topk_indices
+
+    B, S, Sk, K = 2, 70, 150, 24
+    g = torch.Generator().manual_seed(7)
+    scores = torch.randn((B, S, Sk), generator=g)
+    scores[torch.rand((B, S, Sk), generator=g) < 0.7] = NINF     # many rows with fewer finite than K
+    scores[0, 3] = NINF
+    plain = (torch.rand((B, S), generator=g) < 0.3).to(torch.int32)
+    idx = topk_indices(scores.to(dev), K, causal=False)
+    out = finalize_picks(scores.to(dev), idx, plain.to(dev))
+    assert out.dtype == torch.int64
+    ref = otk.drop_masked_picks(scores.numpy().reshape(B * S, Sk), idx.cpu().numpy().reshape(B * S, K),
+                                plain=plain.numpy().reshape(-1))
+    np.testing.assert_array_equal(out.cpu().numpy().reshape(B * S, K), ref)
+    out2 = finalize_picks(scores.to(dev), idx)                   # no flags: every row checked
+    ref2 = otk.drop_masked_picks(scores.numpy().reshape(B * S, Sk), idx.cpu().numpy().reshape(B * S, K))
+    np.testing.assert_array_equal(out2.cpu().numpy().reshape(B * S, K), ref2)
+
+
+def test_causal_mask_path_reads_no_mask_and_matches_lower_triangle(dev):
+    """Megatron's causal float mask: every row is plain, so the window-mode
+    indexer does not read the mask; scores equal the lower-triangle indexer's
+    (-inf above the diagonal) and the picks equal the causal indexer_topk, bit
+    for bit; the same call with a mask that has one finite bias (not plain)
+    still adds it."""
+    S, K = 256, 64
+    q, k, w = _inputs(dev, S, seed=31)
+    causal = torch.full((S, S), NINF, device=dev).triu(1)
+    scores, idx = fused_qk_topk_naive(q, k, w, K, mask=causal)
+    low = index_scores(q, w, k, causal=CAUSAL_LOWER)
+    tri = torch.ones(S, S, dtype=torch.bool, device=dev).tril()
+    assert torch.equal(scores[:, tri], low[:, tri]) and torch.isneginf(scores[:, ~tri]).all()
+    assert torch.equal(idx, indexer_topk(q, k, w, K, causal=True).to(torch.int64))
+    biased = causal.clone()
+    biased[100, 50] = 0.25
+    s2, _ = fused_qk_topk_naive(q, k, w, K, mask=biased)
+    assert torch.equal(s2[:, 100, 50], low[:, 100, 50] + 0.25)
+    assert torch.equal(s2[:, 101:], scores[:, 101:])

@@ -251,7 +251,8 @@ def test_index_scores_patch_keeps_autograd(monkeypatch):
     def fake_scores(q, weights, k, use_relu=True, causal=0, **kw):
         return oix.compute_index_scores(q, weights, k, use_relu)
 
-    def fake_backward(grad, q, weights, k, use_relu=True, causal=False):
+    def fake_backward(grad, q, weights, k, use_relu=True, causal=False, starts=None, ends=None):
+        assert starts is None and ends is None
         seen.append((use_relu, causal))
         dq, dw, dk = oix.index_scores_backward(grad, q, weights, k, use_relu, causal)
         return dq.to(q.dtype), dw.to(weights.dtype), dk.to(k.dtype)

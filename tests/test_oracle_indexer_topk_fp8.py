@@ -182,28 +182,36 @@ def test_topk_admissible_property_bruteforce(cells, k, data):
 
 
 def test_mask_windows_and_masked_pick_repair():
-    """Host-side pieces of the sync-free fused_qk_topk_naive: per-row spans of the
-    finite mask entries (first / last finite column, (0, 0) for an all -inf row),
-    and the repair that turns picks on -inf holes into trailing -1 padding."""
-    import torch
-    from cppmega_amd.dsa_topk import drop_masked_picks, mask_windows
-
+    """Oracle pieces of the sync-free fused_qk_topk_naive: per-row spans of the
+    finite mask entries (first / last finite column, (0, 0) for an all -inf
+    row), the plain flag (the span holds only +0.0), and the repair that turns
+    picks on -inf holes into trailing -1 padding."""
     ninf = float("-inf")
-    m = torch.tensor([[0, 0, ninf, ninf],          # prefix
-                      [ninf, 0, ninf, 0],          # span with a hole
-                      [ninf, ninf, ninf, ninf],    # nothing admissible
-                      [ninf, ninf, ninf, 0.5]])    # last column only, finite bias
-    st_, en_ = mask_windows(m, 2, 4, 4)
-    assert st_.shape == (2, 4) and st_.dtype == torch.int32
-    assert st_[1].tolist() == [0, 1, 0, 3] and en_[0].tolist() == [2, 4, 0, 4]
-    causal = torch.full((5, 5), ninf).triu(1)
-    cs, ce = mask_windows(causal, 1, 5, 5)
-    assert cs[0].tolist() == [0] * 5 and ce[0].tolist() == [1, 2, 3, 4, 5]
-    scores = torch.tensor([[[1.0, ninf, 3.0, ninf, 5.0]]])
-    idx = torch.tensor([[[0, 1, 2, 3]]], dtype=torch.int32)
-    assert drop_masked_picks(scores, idx).tolist() == [[[0, 2, -1, -1]]]
-    idx = torch.tensor([[[4, -1, -1]]], dtype=torch.int32)
-    assert drop_masked_picks(scores, idx).tolist() == [[[4, -1, -1]]]
+    m = np.array([[[0, 0, ninf, ninf],          # prefix, plain
+                   [ninf, 0, ninf, 0],          # span with a hole
+                   [ninf, ninf, ninf, ninf],    # nothing admissible (plain: adds nothing)
+                   [ninf, ninf, ninf, 0.5]]],   # last column only, finite bias
+                 dtype=np.float32)
+    st_, en_, pl = otk.mask_windows(m)
+    assert st_[0].tolist() == [0, 1, 0, 3] and en_[0].tolist() == [2, 4, 0, 4]
+    assert pl[0].tolist() == [1, 0, 1, 0]
+    neg0 = np.array([[[0.0, -0.0, ninf]]], dtype=np.float32)        # -0.0 is not +0.0
+    assert otk.mask_windows(neg0)[2].tolist() == [[0]]
+    causal = np.triu(np.full((5, 5), ninf, dtype=np.float32), 1)[None]
+    cs, ce, cp = otk.mask_windows(causal)
+    assert cs[0].tolist() == [0] * 5 and ce[0].tolist() == [1, 2, 3, 4, 5] and cp[0].tolist() == [1] * 5
+    scores = np.array([[1.0, ninf, 3.0, ninf, 5.0]], dtype=np.float32)
+    assert otk.drop_masked_picks(scores, [[0, 1, 2, 3]]).tolist() == [[0, 2, -1, -1]]
+    assert otk.drop_masked_picks(scores, [[4, -1, -1]]).tolist() == [[4, -1, -1]]
+    assert otk.drop_masked_picks(scores, [[0, 1, 2, 3]], plain=[1]).tolist() == [[0, 1, 2, 3]]
+
+
+@settings(max_examples=200, deadline=None)
+@given(st.lists(st.sampled_from([0.0, -0.0, 0.5, -2.0, float("-inf"), float("inf"), float("nan")]),
+                min_size=1, max_size=12))
+def test_mask_windows_matches_bruteforce(row):
+    st_, en_, pl = otk.mask_windows(np.array([[row]], dtype=np.float32))
+    assert (int(st_[0, 0]), int(en_[0, 0]), int(pl[0, 0])) == otk.mask_windows_bruteforce(row)
 
 
 # ---------------------------------------------------------------------------
