@@ -209,7 +209,7 @@ def test_cfg4_full_scale(dev):
     sub = lambda x: x[b:b + 1, toks].contiguous()
     ro, rl = orc.sparse_mla_fwd(sub(r8), rk8[b:b + 1], sub(idx), scale, DV, q_scale=sub(rqsv),
                                 kv_scale=rksv[b:b + 1])
-    assert_mostly_close(outc[b:b + 1, toks], ro, what="cfg4 out (sampled)")
+    assert_close(outc[b:b + 1, toks], ro, what="cfg4 out (sampled)")
     assert_close(lsec[b:b + 1, toks], rl, what="cfg4 lse2 (sampled)")
     rdq, _ = orc.sparse_mla_bwd(sub(r8), rk8[b:b + 1], sub(outc), sub(do), sub(idx), sub(lsec), scale, DV,
                                 q_scale=sub(rqsv), kv_scale=rksv[b:b + 1])

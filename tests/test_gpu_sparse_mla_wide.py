@@ -226,8 +226,9 @@ def test_cfg5_fwd_full_scale(dev):
 
 def test_cfg5_bwd_full_scale(dev):
     """cfg5 backward at full size (one pass would hold ~309 GB of partial rows;
-    it runs in passes under the default cap): dq of sampled tokens vs the
-    oracle, every output finite, bitwise repeatable, and the dKV column sums:
+    it runs in passes under the default cap): dq of sampled tokens and the
+    dKV rows 16370..16383 vs the oracle, every output finite, bitwise
+    repeatable, and the dKV column sums:
     summed over all kv rows the V part is sum_{t,h} dO (each softmax row sums
     to one) and the rope tail is 0 (sum over slots of dS is 0)."""
     q, kv, idx, gen = _cfg5_inputs(dev)
@@ -243,6 +244,14 @@ def test_cfg5_bwd_full_scale(dev):
     sub = lambda x: x[:, toks].cpu()
     rdq, _ = orc.sparse_mla_bwd(sub(q), kv.cpu(), sub(out), sub(do), sub(idx), sub(lse), D ** -0.5, DV)
     assert_close(dq[:, toks], rdq, what="cfg5 dq (sampled)")
+    # dKV rows 16370..16383 against the oracle: with causal indices only tokens
+    # t >= row reference a row, so tokens 16370..16383 hold every entry of
+    # these rows and the oracle over those 14 tokens gives their full sums
+    late = torch.arange(16370, 16384, device=dev)
+    ltk = lambda x: x[:, late].cpu()
+    _, rdkv = orc.sparse_mla_bwd(ltk(q), kv.cpu(), ltk(out), ltk(do), ltk(idx), ltk(lse), D ** -0.5, DV)
+    rows = late.cpu()
+    assert_close(dkv[0, late], rdkv[0, rows], what="cfg5 dkv (rows 16370..16383)")
     col = dkv.double().sum(dim=(0, 1, 2)).cpu()
     expect_v = do.double().sum(dim=(0, 1, 2)).cpu()
     scale_v = float(expect_v.norm() / DV ** 0.5)
