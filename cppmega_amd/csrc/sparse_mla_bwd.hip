@@ -134,7 +134,7 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
   const unsigned char *kv_b = p.kv + ((b * p.S_kv) * p.G + g) * Gat::ROWB;
   const float *kv_scale_b = FP8 ? p.kv_scale + b * p.S_kv : nullptr;
   const uint32_t row_pitch = (uint32_t)(p.G * Gat::ROWB);
-  const int nblk = (int)((p.topk + 31) / 32);
+  int nblk = (int)((p.topk + 31) / 32);  // set to the blocks up to the last valid slot below
 
   // this wave's blocks: w, w + WPT, ...
   // Indices, CSR positions and rows of a wave's next block are loaded one block
@@ -177,7 +177,8 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
   };
   const auto kv_rs = make_buffer_rsrc(kv_b, (uint32_t)(p.S_kv * (int64_t)row_pitch));
   const auto sc_rs = make_buffer_rsrc(kv_scale_b, FP8 ? (uint32_t)(p.S_kv * 4) : 0u);
-  const uint64_t trash = (uint64_t)n_entries * (uint64_t)p.ntiles;  // partial row no entry owns
+  // partial row no entry owns (this workgroup's trash row)
+  const uint64_t trash = (uint64_t)n_entries * (uint64_t)p.ntiles + item % (uint32_t)kTrashRows;
 
   // ---------------- prologue (all waves): Q, dO tiles, Delta, LSE ----------------
   // Every load of the prologue is issued at once, through resources that end
@@ -219,6 +220,8 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
   typename Gat::Regs rg;
   gather_issue<Gat>(rg, kv_rs, sc_rs, idx_cur, row_pitch);
   PosParts pp_cur = load_pos_parts(idx_cur, blk);
+  // blocks up to the last valid slot (loads issued after the prologue's, so they overlap)
+  nblk = valid_blocks(idx_rs, p.topk, p.S_kv);
 
   {
     // Q rows: 32 heads x QCH chunks of 8 elements (e4m3: dequantised to bf16)
@@ -469,6 +472,69 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
       }
     }
 
+    if constexpr (C::BEXP) {
+      // ---- c^T[d][slot] = Q^T dS^T + dO^T P^T, one 32-row d-tile at a time ----
+      // dS and P already carry the row's 2^pexp, so each d-tile is converted to
+      // fp16 and staged (over the consumed K tile) right after its MFMAs: one
+      // 16-register accumulator instead of four, which leaves the registers
+      // for the LDS operand reads to run ahead of the MFMAs.
+      wave_lds_sync();  // the dQ GEMM's reads of the K / dS tiles are complete
+      unsigned char *Cs = Kl;
+      int *Lpos = reinterpret_cast<int *>(DS);
+#pragma unroll
+      for (int dt = 0; dt < C::DQT; ++dt) {
+        f32x16 cacc;
+#pragma unroll
+        for (int a = 0; a < 16; ++a) cacc[a] = 0.0f;
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+          const i32x4 av = tr_operand_perm(QL, C::QL_STRIDE, dt * 32, 16 * kc);
+          cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(av), dsB[kc], cacc, 0, 0, 0);
+        }
+        if (dt < C::DVT) {
+#pragma unroll
+          for (int kc = 0; kc < 2; ++kc) {
+            const i32x4 av = tr_operand_perm(DOL, C::DOL_STRIDE, dt * 32, 16 * kc);
+            cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(av), pB[kc], cacc, 0, 0, 0);
+          }
+        }
+        // lane: slot l32, d = dt*32 + 16s + 8*g32 + (0..7): cacc[8s .. 8s+7]
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const int d0 = dt * 32 + 16 * s2 + 8 * g32;
+          *reinterpret_cast<i32x4 *>(Cs + l32 * C::CS_STRIDE + d0 * 2) =
+              i32x4{(int)pack_f16x2(cacc[8 * s2], cacc[8 * s2 + 1]), (int)pack_f16x2(cacc[8 * s2 + 2], cacc[8 * s2 + 3]),
+                    (int)pack_f16x2(cacc[8 * s2 + 4], cacc[8 * s2 + 5]),
+                    (int)pack_f16x2(cacc[8 * s2 + 6], cacc[8 * s2 + 7])};
+        }
+      }
+      if (g32 == 0) Lpos[l32] = wr ? pos : -1;
+      p.partial_exp[prow_me] = (int8_t)pexp;  // both lane halves store the same byte
+      wave_lds_sync();
+      // all LDS reads first, then the stores, so the reads overlap
+      constexpr int ITS = 32 * C::ROW_CHUNKS / 64;
+      int ps[ITS];
+      i32x4 v[ITS];
+#pragma unroll
+      for (int it = 0; it < ITS; ++it) {
+        const int u = it * 64 + lane;
+        const int row = u / C::ROW_CHUNKS, ch = u % C::ROW_CHUNKS;
+        ps[it] = Lpos[row];
+        v[it] = *reinterpret_cast<const i32x4 *>(Cs + row * C::CS_STRIDE + ch * 16);
+      }
+#pragma unroll
+      for (int it = 0; it < ITS; ++it) {
+        const int ch = (it * 64 + lane) % C::ROW_CHUNKS;
+        const uint64_t prow = ps[it] >= 0 ? (uint64_t)(uint32_t)ps[it] * (uint32_t)p.ntiles + tile : trash;
+        st_stream_16(p.partials + prow * (D_QK * 2) + ch * 16, v[it]);
+      }
+      wave_lds_sync();  // K / dS tiles are consumed before the next block's gather lands
+      idx_cur = idx_nxt;
+      raw_nxt = raw_nn;
+      pp_cur = pp_nxt;
+      continue;
+    }
+
     // ---- c^T[d][slot] = Q^T dS^T + dO^T P^T  (M = d, N = slot, K = head, accumulator order) ----
     f32x16 cacc[C::DQT];
 #pragma unroll
@@ -672,9 +738,9 @@ static BwdWorkspace bwd_layout(int64_t B, int64_t S, int64_t S_kv, int64_t H, in
   const size_t psz = (size_t)partial_elem_bytes(flags, D_qk);
   size_t off = 0;
   L.partials = off;
-  off += align256((entries * ntiles + 1) * D_qk * psz);  // + one trash row for masked slots
+  off += align256((entries * ntiles + kTrashRows) * D_qk * psz);  // + trash rows for masked slots
   L.pexp = off;
-  off += align256(entries * ntiles + 1);
+  off += align256(entries * ntiles + kTrashRows);
   L.carry = off;  // fp32 sums of one batch's kv rows, carried across its passes
   off += pl.npb > 1 ? align256((size_t)R * D_qk * 4) : 0;
   L.rows_total = off;

@@ -58,6 +58,32 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t slot_rsrc(const int32_t *row, 
   return make_buffer_rsrc(row, nb < 0x7fffffff ? (uint32_t)nb : 0x7fffffffu);
 }
 
+// Number of 32-slot blocks of this row up to its last valid slot (an index in
+// [0, s_kv)), 0 when it has none: every later block is wholly masked and
+// contributes nothing, so the block loops stop there.  One pass of unconditional
+// bounded loads over the row's indices, then a wave maximum (the same value in
+// every wave of a workgroup).
+__device__ __forceinline__ int valid_blocks(__amdgpu_buffer_rsrc_t idx_rs, int64_t topk, int64_t s_kv) {
+  const int lane = lane_id();
+  int last = -1;
+  for (int64_t s0 = 0; s0 < topk; s0 += 256) {
+    int raw[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) raw[u] = (int)__builtin_amdgcn_raw_buffer_load_b32(idx_rs, (int)((s0 + 64 * u + lane) * 4), 0, 0);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t s = s0 + 64 * u + lane;
+      last = (s < topk && raw[u] >= 0 && raw[u] < s_kv && (int)s > last) ? (int)s : last;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const int o = __shfl_xor(last, off, 64);
+    last = o > last ? o : last;
+  }
+  return __builtin_amdgcn_readfirstlane((last + 32) / 32);
+}
+
 // Index of slot blk*32 + l32 of this row, or -1 when masked / past topk.
 __device__ __forceinline__ int load_slot_index(const int32_t *idx_row, int blk, int l32, int64_t topk,
                                                int64_t s_kv) {

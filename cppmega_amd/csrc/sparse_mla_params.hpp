@@ -6,6 +6,12 @@
 
 namespace dsa {
 
+// Partial rows past the entries that masked slots of the backward write (their
+// stores are unconditional); workgroup `item` uses row entries + item % kTrashRows,
+// so the discarded stores spread over many rows (and memory channels) instead
+// of all landing on one.
+constexpr int kTrashRows = 64;
+
 struct FwdParams {
   const unsigned char *q;
   const unsigned char *kv;

@@ -569,7 +569,6 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
   const unsigned char *kv_b = p.kv + ((b * p.S_kv) * p.G + g) * C::ROWB;
   const float *kv_scale_b = FP8 ? p.kv_scale + b * p.S_kv : nullptr;
   const uint32_t row_pitch = (uint32_t)(p.G * C::ROWB);
-  const int nblk = (int)((p.topk + 31) / 32);
 
   // Indices (two blocks ahead), rows and CSR positions (one block ahead) are
   // loaded unconditionally through resources that end at the item's top-k, and
@@ -584,7 +583,10 @@ sparse_mla_bwd_wide_kernel(const BwdParams p) {
   typename C::Regs rg;
   wide_issue<C, FP8, false, true>(rg, kv_b, kv_scale_b, idx_cur, row_pitch);
   int pos_cur = load_slot_raw(pos_rs, 0, l32);
-  const uint64_t trash = (uint64_t)n_entries * (uint64_t)p.ntiles;  // partial row no entry owns
+  // blocks up to the last valid slot: the same count in every wave (the loop has workgroup barriers)
+  const int nblk = valid_blocks(idx_rs, p.topk, p.S_kv);
+  // partial row no entry owns (this workgroup's trash row)
+  const uint64_t trash = (uint64_t)n_entries * (uint64_t)p.ntiles + (uint64_t)(item % kTrashRows);
 
   float qsc = 1.0f;
   if constexpr (FP8) qsc = p.q_scale[tok];

@@ -128,6 +128,35 @@ def test_bwd_edge_indices(dev):
     assert torch.all(dq[0, 5] == 0)
 
 
+@pytest.mark.parametrize("D,DV,H,topk", [(128, 64, 32, 160), (576, 512, 64, 96)])
+def test_bwd_last_valid_block(dev, D, DV, H, topk):
+    """The block loops end after the last block that holds a valid slot: rows
+    whose valid slots stop early, -1 scattered before valid slots, a wholly
+    masked row, a row whose only valid slot is the last one, and out-of-range
+    entries past the last valid slot (narrow and d_qk = 576 kernels)."""
+    B, S = 1, 96
+    inp = _inputs(B, S, H, D, DV, topk, seed=D + topk)
+    g = torch.Generator().manual_seed(5)
+    idx = torch.full((B, S, 1, topk), -1, dtype=torch.int32)
+    for t in range(S):
+        n = int(torch.randint(0, topk + 1, (1,), generator=g))
+        pos = torch.randperm(topk, generator=g)[:n].sort().values
+        idx[0, t, 0, pos] = torch.randint(0, t + 1, (n,), generator=g, dtype=torch.int32)
+    idx[0, 10] = -1                                   # wholly masked
+    idx[0, 11] = -1
+    idx[0, 11, 0, topk - 1] = 7                       # only the last slot is valid
+    idx[0, 12] = -1
+    idx[0, 12, 0, 3] = 2                              # only the first block holds a valid slot
+    idx[0, 12, 0, 40:] = S + 3                        # out of range past it (masked)
+    q, kv, idxd, do = inp["q"].to(dev), inp["kv"].to(dev), idx.to(dev), inp["do"].to(dev)
+    out, lse = sparse_mla_fwd_interface(q, kv, idxd, sm_scale=inp["scale"], d_v=DV)
+    dq, dkv = sparse_mla_bwd(q, kv, out, do, idxd, lse, sm_scale=inp["scale"])
+    rdq, rdkv = orc.sparse_mla_bwd(inp["q"], inp["kv"], out.cpu(), inp["do"], idx, lse.cpu(), inp["scale"], DV)
+    assert_close(dq, rdq, what="dq")
+    assert_close(dkv, rdkv, what="dkv")
+    assert torch.all(dq[0, 10] == 0)
+
+
 def test_bwd_unsorted_and_duplicate_indices(dev):
     """Unsorted slot order and repeated rows inside a token take the serial CSR path."""
     B, S, H, D, DV, topk = 2, 96, 32, 128, 64, 64
