@@ -30,8 +30,10 @@ HIP_FLAGS = [
 
 
 # Per-file additions.  The indexer's epilogue is one max + one fma per score
-# element; with IEEE mode off and NaN inputs declared undefined, fmaxf is a
-# single v_max_f32 instead of a canonicalise + max pair.
+# element, and the forward's online softmax takes a row max over every score;
+# with IEEE mode off and NaN inputs declared undefined, fmaxf is a single
+# v_max_f32 / v_max3_f32 instead of canonicalising each operand first (a NaN
+# score still reaches the output through its exp2 term).
 #
 # The SparseMLA kernels keep loop-carried MFMA accumulators (O, dQ) that the
 # online softmax also touches with VALU ops; LLVM's default AGPR form for MFMA
@@ -40,7 +42,7 @@ HIP_FLAGS = [
 _MFMA_VGPR = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
 FILE_FLAGS = {
     "indexer_score.hip": ["-fno-honor-nans", "-mno-amdgpu-ieee"],
-    "sparse_mla_fwd.hip": _MFMA_VGPR,
+    "sparse_mla_fwd.hip": _MFMA_VGPR + ["-fno-honor-nans", "-mno-amdgpu-ieee"],
     "sparse_mla_bwd.hip": _MFMA_VGPR,
     "sparse_mla_wide.hip": _MFMA_VGPR,
     "indexer_kl_loss.hip": _MFMA_VGPR,

@@ -857,7 +857,7 @@ static int bwd_check(const char *fn, int64_t B, int64_t S, int64_t S_kv, int64_t
   const int64_t ntiles = (H / G + 31) / 32;
   DSA_REQUIRE(entries < (1ll << 31) && B * R < (1ll << 31) && entries * ntiles < (1ll << 40),
               "%s: too many entries for int32 CSR keys", fn);
-  DSA_REQUIRE(S_kv * G * D_qk * 2 < (1ll << 32), "%s: kv rows of one batch exceed 4 GiB", fn);
+  DSA_REQUIRE(S_kv * G * D_qk * 2 <= (int64_t)kMaskedOff, "%s: kv rows of one batch exceed 4 GiB - 64 KiB", fn);
   const bool f8 = dtype == DSA_DTYPE_E4M3;
   const bool shape_ok = (D_qk == 128 && D_v == 64) || (D_qk == 128 && D_v == 128) || (D_qk == 192 && D_v == 128) ||
                         (D_qk == 64 && D_v == 32 && !f8) || wide_shape(D_qk, D_v);

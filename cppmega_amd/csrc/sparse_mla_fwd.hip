@@ -453,7 +453,7 @@ static int sparse_mla_fwd_impl(const void *q, const void *kv, const int32_t *ind
   p.sl2 = sm_scale * kLog2e;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool f8 = dtype == DSA_DTYPE_E4M3;
-  DSA_REQUIRE(S_kv * G * D_qk * 2 < (1ll << 32), "dsa_sparse_mla_fwd: kv rows of one batch exceed 4 GiB");
+  DSA_REQUIRE(S_kv * G * D_qk * 2 <= (int64_t)kMaskedOff, "dsa_sparse_mla_fwd: kv rows of one batch exceed 4 GiB - 64 KiB");
   if (workspace != nullptr && dtype == DSA_DTYPE_MXFP8 && mx_exact_shape(D_qk, D_v)) {
     // MX: kv rows dequantised once (and the scales checked), then two kernels
     // gated on the check: the bf16 kernel on the dequantised rows with Q

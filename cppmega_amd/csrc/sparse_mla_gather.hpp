@@ -49,9 +49,11 @@ struct GatherCfg {
 __device__ __forceinline__ int load_slot_raw(__amdgpu_buffer_rsrc_t idx_rs, int blk, int l32) {
   return (int)__builtin_amdgcn_raw_buffer_load_b32(idx_rs, (blk * 32 + l32) * 4, 0, 0);
 }
+// topk and s_kv are below 2^31 (checked on the host), so unsigned 32-bit
+// compares cover both bounds of each test.
 __device__ __forceinline__ int slot_index(int raw, int blk, int l32, int64_t topk, int64_t s_kv) {
-  const int64_t sl = (int64_t)blk * 32 + l32;
-  return (sl < topk && raw >= 0 && raw < s_kv) ? raw : -1;
+  const uint32_t sl = (uint32_t)blk * 32u + (uint32_t)l32;
+  return (sl < (uint32_t)topk && (uint32_t)raw < (uint32_t)s_kv) ? raw : -1;
 }
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t slot_rsrc(const int32_t *row, int64_t topk) {
   const int64_t nb = topk * 4;
@@ -93,31 +95,42 @@ __device__ __forceinline__ int load_slot_index(const int32_t *idx_row, int blk, 
   return (v >= 0 && v < s_kv) ? v : -1;
 }
 
+// Byte offset at or past the end of every kv resource (the host keeps a
+// batch's kv rows within it): a masked slot's loads start here and read
+// zeros, and adding a chunk offset (below 64 KiB) cannot wrap.
+constexpr uint32_t kMaskedOff = 0xffff0000u;
+
 // Rows are read through buffer resources: kv_rs covers the kv rows of this
 // (batch, kv group) (row r at byte r * row_pitch, row_pitch = G * ROWB), sc_rs
 // their e4m3 scales (row r at byte r * sc_pitch; MX: the scale of 16-byte
 // chunk c is block c / 2 of the row, 4 bytes apart).  A masked slot reads at an offset past the resource, which
 // the hardware answers with zeros, so masked rows (and their scales) arrive as
-// zeros without selects, and every load is issued on every path.
+// zeros without selects, and every load is issued on every path.  Each lane
+// forms its own slot's row offset once (one multiply per block); a load takes
+// its row's offset from the owner lane and adds its chunk's.
 template <class Gat>
 __device__ __forceinline__ void gather_issue(typename Gat::Regs &rg, __amdgpu_buffer_rsrc_t kv_rs,
                                              __amdgpu_buffer_rsrc_t sc_rs, int my_idx, uint32_t row_pitch,
                                              uint32_t sc_pitch = 4u) {
   const int lane = lane_id();
+  const uint32_t my_off = my_idx >= 0 ? (uint32_t)my_idx * row_pitch : kMaskedOff;
+  uint32_t my_soff = kMaskedOff;
+  if constexpr (Gat::kFp8) my_soff = my_idx >= 0 ? (uint32_t)my_idx * sc_pitch : kMaskedOff;
 #pragma unroll
   for (int uu = 0; uu < Gat::UPL; ++uu) {
     const int u = lane + 64 * uu;
     const int c = u % Gat::NCH;
     const int quad = (u / Gat::NCH) & 7;
+    const bool in = u < Gat::UNITS;  // false only on the lanes past a ragged last unit
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int ri = __shfl(my_idx, quad * 4 + r, 64);
-      const bool ok = ri >= 0 && u < Gat::UNITS;
-      const uint32_t off = ok ? (uint32_t)ri * row_pitch + (uint32_t)c * 16u : 0xffffffffu;
+      const uint32_t ro = (uint32_t)__shfl((int)my_off, quad * 4 + r, 64);
+      const uint32_t off = in ? ro + (uint32_t)c * 16u : kMaskedOff;
       rg.v[uu][r] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(kv_rs, (int)off, 0, 0));
       if constexpr (Gat::kFp8) {
-        const uint32_t so = (uint32_t)ri * sc_pitch + (Gat::kMx ? (uint32_t)(c / 2) * 4u : 0u);
-        rg.sc[uu][r] = buffer_load_f32(sc_rs, ok ? (int)so : (int)0xffffffffu, 0);
+        const uint32_t so = (uint32_t)__shfl((int)my_soff, quad * 4 + r, 64) +
+                            (Gat::kMx ? (uint32_t)(c / 2) * 4u : 0u);
+        rg.sc[uu][r] = buffer_load_f32(sc_rs, in ? (int)so : (int)kMaskedOff, 0);
       }
     }
   }
