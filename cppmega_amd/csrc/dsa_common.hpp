@@ -235,6 +235,20 @@ __device__ __forceinline__ i32x4 tr_operand(const unsigned char *T, int stride, 
   return i32x4{r0[0], r0[1], r1[0], r1[1]};
 }
 
+// tr_operand(T, stride, col0, rows_base, 8, 4) over a tile whose 16-byte
+// chunks are swizzled by row bit 3 (chunk c of row R at c ^ ((R >> 3) & 1),
+// gather_store_k<..., true>): rows_base is a multiple of 16, so the first
+// read's rows have bit 3 clear and the second's (8 rows on) set.
+__device__ __forceinline__ i32x4 tr_operand_swz(const unsigned char *T, int stride, int col0, int rows_base) {
+  const int lane = lane_id();
+  const int k = lane & 15, j = k >> 2, q = k & 3, cb = (lane >> 4) & 1, gg = lane >> 5;
+  const int col = (col0 + cb * 16 + 4 * q) * 2;  // bytes
+  const unsigned char *row0 = T + (rows_base + gg * 4 + j) * stride;
+  const i32x2 r0 = ds_read_tr16(row0 + col);
+  const i32x2 r1 = ds_read_tr16(row0 + 8 * stride + (col ^ 16));
+  return i32x4{r0[0], r0[1], r1[0], r1[1]};
+}
+
 // tr_operand with (h_step, g_step) = (8, 4) and the four 4-column groups of
 // each 16-column half permuted, so that accumulator row m = 8i + 4g + j of the
 // product maps to column col0 + 16(i >> 1) + 8g + 4(i & 1) + j: a lane's 16

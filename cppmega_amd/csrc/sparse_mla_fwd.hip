@@ -42,7 +42,11 @@ struct FwdCfg {
   static constexpr int KD_STRIDE = D_V * 2 + 32;          // e4m3: dequantised V rows (bf16)
   static constexpr int KD_BYTES = FP8 ? 32 * KD_STRIDE : 0;
   static constexpr int SC_BYTES = FP8 ? (MX ? Gat::NBLK : 1) * 32 * 4 : 0;
-  static constexpr int WAVE_BYTES = (KL_BYTES + KD_BYTES + SC_BYTES + 15) / 16 * 16;
+  // bf16 rows: the gather's slot offsets go through LDS (32 ints) and the K
+  // tile's chunks are swizzled by row bit 3 (gather_store_k)
+  static constexpr bool XL = !FP8;
+  static constexpr int OFFS_BYTES = XL ? 32 * 4 : 0;
+  static constexpr int WAVE_BYTES = (KL_BYTES + KD_BYTES + SC_BYTES + OFFS_BYTES + 15) / 16 * 16;
   // bf16 source of the V^T operand: the raw tile, or the dequantised one for e4m3
   static constexpr int V_STRIDE = FP8 ? KD_STRIDE : Gat::KL_STRIDE;
   static constexpr int DT = D_V / 32;
@@ -86,6 +90,7 @@ sparse_mla_fwd_kernel(const FwdParams p) {
   unsigned char *Kl = smem + w * C::WAVE_BYTES;
   unsigned char *Kd = Kl + C::KL_BYTES;
   float *Ksc = reinterpret_cast<float *>(Kd + C::KD_BYTES);
+  int *offs = reinterpret_cast<int *>(Kd + C::KD_BYTES + C::SC_BYTES);
   const unsigned char *Vsrc = FP8 ? Kd : Kl;
 
   const int h_local = tile * 32 + l32;
@@ -107,7 +112,13 @@ sparse_mla_fwd_kernel(const FwdParams p) {
   const auto kv_rs = make_buffer_rsrc(kv_b, (uint32_t)(p.S_kv * (int64_t)row_pitch));
   const auto sc_rs = make_buffer_rsrc(kv_scale_b, FP8 ? (uint32_t)(p.S_kv * sc_pitch) : 0u);
   typename Gat::Regs rg;
-  gather_issue<Gat>(rg, kv_rs, sc_rs, idx_cur, row_pitch, sc_pitch);
+  if constexpr (C::XL) {
+    gather_put_offsets(offs, idx_cur, row_pitch);
+    wave_lds_sync();
+    gather_issue_offs<Gat>(rg, kv_rs, offs);
+  } else {
+    gather_issue<Gat>(rg, kv_rs, sc_rs, idx_cur, row_pitch, sc_pitch);
+  }
   // pre-dequantised V rows of this (batch, group): bf16, v16_ld elements per
   // row of [B, S_kv, G], V in the leading D_V
   const uint32_t v_pitch = (uint32_t)(p.G * p.v16_ld * 2);
@@ -166,7 +177,7 @@ sparse_mla_fwd_kernel(const FwdParams p) {
 
   for (int blk = 0; blk < nblk; ++blk) {
     // ---- stage block blk: K row-major, V transposed (bf16, dequantised for e4m3) ----
-    gather_store_k<Gat>(rg, Kl);
+    gather_store_k<Gat, C::XL>(rg, Kl);
     if constexpr (FP8) {
       if constexpr (VPRE)
         gather_store_k<VGat>(rgv, Kd);
@@ -175,12 +186,16 @@ sparse_mla_fwd_kernel(const FwdParams p) {
       gather_store_scale<Gat>(rg, Ksc);
     }
     const uint64_t vmask = __ballot(idx_cur >= 0);
+    const int idx_nxt = slot_index(raw_nxt, blk + 1, l32, p.topk, p.S_kv);
+    if constexpr (C::XL) gather_put_offsets(offs, idx_nxt, row_pitch);
     wave_lds_sync();
     // ---- prefetch: rows of block blk+1, indices of block blk+2 ----
     // (issued unconditionally, past the last block too, so every wait is counted exactly)
     const int raw_nn = load_slot_raw(idx_rs, blk + 2, l32);
-    const int idx_nxt = slot_index(raw_nxt, blk + 1, l32, p.topk, p.S_kv);
-    gather_issue<Gat>(rg, kv_rs, sc_rs, idx_nxt, row_pitch, sc_pitch);
+    if constexpr (C::XL)
+      gather_issue_offs<Gat>(rg, kv_rs, offs);
+    else
+      gather_issue<Gat>(rg, kv_rs, sc_rs, idx_nxt, row_pitch, sc_pitch);
     if constexpr (VPRE) gather_issue<VGat>(rgv, v_rs, v_rs, idx_nxt, v_pitch);
 
     // ---- S^T = K Q^T  (M = slot, N = head, K = d) ----
@@ -220,7 +235,9 @@ sparse_mla_fwd_kernel(const FwdParams p) {
         const long a = *reinterpret_cast<const long *>(Kl + l32 * Gat::KL_STRIDE + 16 * k + 8 * g32);
         sacc = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(a, qreg[k], sacc, 0, 0, 0);
       } else {
-        const i32x4 a = *reinterpret_cast<const i32x4 *>(Kl + l32 * Gat::KL_STRIDE + (16 * k + 8 * g32) * 2);
+        // chunk 2k + g32 of row l32, at chunk (2k + g32) ^ ((l32 >> 3) & 1) of the swizzled tile
+        const i32x4 a = *reinterpret_cast<const i32x4 *>(Kl + l32 * Gat::KL_STRIDE + 32 * k +
+                                                         16 * (g32 ^ ((l32 >> 3) & 1)));
         sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), qreg[k], sacc, 0, 0, 0);
       }
     }
@@ -286,7 +303,8 @@ sparse_mla_fwd_kernel(const FwdParams p) {
       const bf16x8 bop = as_bf16x8(pb);
 #pragma unroll
       for (int dt = 0; dt < C::DT; ++dt) {
-        const i32x4 av = tr_operand(Vsrc, C::V_STRIDE, dt * 32, 16 * kc, 8, 4);
+        const i32x4 av = C::XL ? tr_operand_swz(Vsrc, C::V_STRIDE, dt * 32, 16 * kc)
+                               : tr_operand(Vsrc, C::V_STRIDE, dt * 32, 16 * kc, 8, 4);
         oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(av), bop, oacc[dt], 0, 0, 0);
       }
     }

@@ -136,10 +136,46 @@ __device__ __forceinline__ void gather_issue(typename Gat::Regs &rg, __amdgpu_bu
   }
 }
 
-// K rows, row-major (raw bf16 / e4m3 bytes): Kl[slot][chunk]; masked slots
-// arrive as zeros from gather_issue.
+// The same issue with the slots' row offsets exchanged through LDS instead of
+// ds_bpermute (bf16 rows, no scales): gather_put_offsets writes each slot's
+// row offset (lane l32 -> offs[l32], 32 ints of the wave's LDS), and after a
+// wave sync gather_issue_offs reads the four offsets of a lane's rows with
+// one broadcast 16-byte read per unit.  LDS time per block is about a third
+// of eight bpermutes'.
+__device__ __forceinline__ void gather_put_offsets(int *offs, int my_idx, uint32_t row_pitch) {
+  const uint32_t my_off = my_idx >= 0 ? (uint32_t)my_idx * row_pitch : kMaskedOff;
+  const int lane = lane_id();
+  if (lane < 32) offs[lane] = (int)my_off;
+}
 template <class Gat>
+__device__ __forceinline__ void gather_issue_offs(typename Gat::Regs &rg, __amdgpu_buffer_rsrc_t kv_rs,
+                                                  const int *offs) {
+  static_assert(!Gat::kFp8, "rows with scales take gather_issue");
+  const int lane = lane_id();
+#pragma unroll
+  for (int uu = 0; uu < Gat::UPL; ++uu) {
+    const int u = lane + 64 * uu;
+    const int c = u % Gat::NCH;
+    const int quad = (u / Gat::NCH) & 7;
+    const bool in = u < Gat::UNITS;
+    const i32x4 o4 = *reinterpret_cast<const i32x4 *>(offs + quad * 4);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t off = in ? (uint32_t)o4[r] + (uint32_t)c * 16u : kMaskedOff;
+      rg.v[uu][r] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(kv_rs, (int)off, 0, 0));
+    }
+  }
+}
+
+// K rows, row-major (raw bf16 / e4m3 bytes): Kl[slot][chunk]; masked slots
+// arrive as zeros from gather_issue.  SWZ: 16-byte chunk c of row R sits at
+// chunk c ^ ((R >> 3) & 1), so rows R and R + 8 (which the 32-byte row pad
+// puts on the same banks) hold a column on different 16-byte halves and the
+// MFMA operand reads (lane = row) are free of bank conflicts; the row count
+// of chunks must be even.
+template <class Gat, bool SWZ = false>
 __device__ __forceinline__ void gather_store_k(const typename Gat::Regs &rg, unsigned char *Kl) {
+  static_assert(!SWZ || Gat::NCH % 2 == 0, "the swizzle pairs chunks");
   const int lane = lane_id();
 #pragma unroll
   for (int uu = 0; uu < Gat::UPL; ++uu) {
@@ -147,8 +183,11 @@ __device__ __forceinline__ void gather_store_k(const typename Gat::Regs &rg, uns
     if (u >= Gat::UNITS) break;
     const int c = u % Gat::NCH, quad = u / Gat::NCH;
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      *reinterpret_cast<i32x4 *>(Kl + (quad * 4 + r) * Gat::KL_STRIDE + c * 16) = rg.v[uu][r];
+    for (int r = 0; r < 4; ++r) {
+      const int row = quad * 4 + r;
+      const int pc = SWZ ? (c ^ ((row >> 3) & 1)) : c;
+      *reinterpret_cast<i32x4 *>(Kl + row * Gat::KL_STRIDE + pc * 16) = rg.v[uu][r];
+    }
   }
 }
 
