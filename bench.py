@@ -10,11 +10,12 @@ Inputs are synthetic, generated on the CPU with a fixed seed and resident in
 HBM before timing.  Prints one JSON line (see the fields below).
 
 The backward is three stages (inverse index, main kernel, dKV reduction).  The
-inverse index depends on the indices alone, so the step builds it on a second
-stream while the forward runs (build_inverse_index) and the backward call runs
+inverse index depends on the indices alone, so the step builds it before the
+forward (build_inverse_index; in training SparseMLA.apply builds it on a second
+stream instead, overlapping the layers that follow) and the backward call runs
 the main kernel and the reduction; their durations come from HIP events the
 library records on its stream during the timed steps (dsa_stage_timing), the
-inverse index's from events on the second stream.  The roofline object is
+inverse index's from events around its build.  The roofline object is
 for the single kernel with the longest median duration; its `traffic` field is
 read from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed under
 profiles/ (null when that kernel has no such summary).
@@ -440,11 +441,11 @@ def algorithmic_work():
         # q, kv, indices read; out, lse written (the kv gather itself hits L2)
         "fwd": {"bound": "max", "flops": 2 * B * S * H * TOPK * (D_QK + D_V),
                 "io_bytes": q_b + kv_b + idx_b + o_b + lse_b},
-        # the backward call: main kernel + reduction (its inverse index is built on a
-        # second stream during the forward; bwd_csr below)
+        # the backward call: main kernel + reduction (its inverse index is built
+        # ahead of the forward; bwd_csr below)
         "bwd": {"bound": "mfma", "flops": bwd_flops, "io_bytes": bwd_io,
                 "design_bytes": bwd_io + csr_planes + 2 * partial_rows},
-        # inverse index (second stream, overlapped with the forward): indices read once;
+        # inverse index (built ahead of the forward): indices read once;
         # per (32-token chunk, kv row) a mask word written and read once and a base word
         # written once (the row scan is small)
         "bwd_csr": {"bound": "hbm", "flops": 0, "io_bytes": 4 * ENTRIES + csr_planes},
@@ -542,7 +543,7 @@ def main():
     from cppmega_amd import _lib, synthetic
     from cppmega_amd.dsa_indexer_fused_patch import CAUSAL_LOWER, index_scores
     from cppmega_amd.dsa_topk import topk_indices
-    from cppmega_amd.sparse_mla_ops import build_inverse_index, side_stream, sparse_mla_bwd, sparse_mla_fwd_interface
+    from cppmega_amd.sparse_mla_ops import build_inverse_index, sparse_mla_bwd, sparse_mla_fwd_interface
 
     dev = torch.device("cuda", 0)
     _lib.load()
@@ -564,8 +565,6 @@ def main():
 
     ev = {k: [] for k in ("indexer", "topk", "fwd", "bwd")}
 
-    side = side_stream(dev)
-
     def step(record):
         marks = [torch.cuda.Event(enable_timing=True) for _ in range(8)] if record else None
         if record:
@@ -576,21 +575,21 @@ def main():
         sel = topk_indices(scores, TOPK, causal=True)
         if record:
             marks[2].record()
-        # the backward's inverse index depends on the indices alone: it is built on
-        # a second stream while the forward runs (marks 5, 6 time it there); the
-        # forward is queued first and the build waits only for the work before it
-        ready = torch.cuda.Event()
-        ready.record()
+        # the backward's inverse index depends on the indices alone.  In a training
+        # step SparseMLA.apply builds it on a second stream, overlapping the layers
+        # that follow the forward; in this isolated layer step nothing follows, and
+        # run beside the forward it stretches the forward by more than it takes
+        # alone (measured: 344-352 us with the overlap, 339 us in order, for
+        # build + forward + backward), so it is built first, in order (marks 5, 6)
         if record:
+            marks[5].record()
+        inv = build_inverse_index(q, kv, idx, D_V)
+        if record:
+            marks[6].record()
             marks[7].record()
         out, lse = sparse_mla_fwd_interface(q, kv, idx, sm_scale=scale, d_v=D_V)
         if record:
             marks[3].record()
-            side.wait_event(ready)
-            marks[5].record(side)
-        inv = build_inverse_index(q, kv, idx, D_V, stream=side, after=ready)
-        if record:
-            marks[6].record(side)
         dq, dkv = sparse_mla_bwd(q, kv, out, do, idx, lse, sm_scale=scale, inverse_index=inv)
         if record:
             marks[4].record()
@@ -616,7 +615,7 @@ def main():
     for back in range(args.steps):
         for k, ms in zip(_lib.BWD_STAGES, _lib.stage_times(back)):
             ev["bwd_" + k].append(ms / 1e3)
-    # the inverse index ran on the side stream (its in-call stage is empty)
+    # the inverse index was built ahead of the forward (its in-call stage is empty)
     ev["bwd_csr"] = [m[5].elapsed_time(m[6]) / 1e3 for m in all_marks]
     ms_per_step = wall / args.steps * 1e3
     tokens = B * S
@@ -652,10 +651,8 @@ def main():
         # the same layer step with SparseMLA consuming the top-k's own indices
         sc = index_scores(iq, iw, ik, use_relu=True, causal=CAUSAL_LOWER)
         sel_c = topk_indices(sc, TOPK, causal=True).view(B, S, 1, TOPK)
-        ready_c = torch.cuda.Event()
-        ready_c.record()
+        inv_c = build_inverse_index(q, kv, sel_c, D_V)
         out_c, lse_c = sparse_mla_fwd_interface(q, kv, sel_c, sm_scale=scale, d_v=D_V)
-        inv_c = build_inverse_index(q, kv, sel_c, D_V, stream=side, after=ready_c)
         return sparse_mla_bwd(q, kv, out_c, do, sel_c, lse_c, sm_scale=scale, inverse_index=inv_c)
 
     t_chain = graph_replay_time(chained_step)
