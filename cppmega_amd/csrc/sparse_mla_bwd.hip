@@ -177,8 +177,11 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
   };
   const auto kv_rs = make_buffer_rsrc(kv_b, (uint32_t)(p.S_kv * (int64_t)row_pitch));
   const auto sc_rs = make_buffer_rsrc(kv_scale_b, FP8 ? (uint32_t)(p.S_kv * 4) : 0u);
-  // partial row no entry owns (this workgroup's trash row)
-  const uint64_t trash = (uint64_t)n_entries * (uint64_t)p.ntiles + item % (uint32_t)kTrashRows;
+  // partial row no entry owns (this workgroup's trash row).  A pass's partial
+  // rows (trash rows included) stay below 4 GiB (the host caps a pass below
+  // it), so row numbers and byte offsets into them are 32-bit, and the stores
+  // take a scalar base plus a 32-bit offset
+  const uint32_t trash = (uint32_t)n_entries * (uint32_t)p.ntiles + item % (uint32_t)kTrashRows;
 
   // ---------------- prologue (all waves): Q, dO tiles, Delta, LSE ----------------
   // Every load of the prologue is issued at once, through resources that end
@@ -360,7 +363,7 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
     const bool valid = idx_cur >= 0;  // slot slot0 + l32
     const int32_t pos = csr_pos(pp_cur);
     const bool wr = valid && pos >= 0 && pos < n_entries;  // (always true for a valid slot; a guard)
-    const uint64_t prow_me = wr ? (uint64_t)(uint32_t)pos * (uint32_t)p.ntiles + tile : trash;
+    const uint32_t prow_me = wr ? (uint32_t)pos * (uint32_t)p.ntiles + (uint32_t)tile : trash;
     wave_lds_sync();
     const int raw_nn = load_slot_raw(idx_rs, blk + 2 * C::WPT, l32);
     const int idx_nxt = slot_index(raw_nxt, blk + C::WPT, l32, p.topk, p.S_kv);
@@ -508,7 +511,7 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
                     (int)pack_f16x2(cacc[8 * s2 + 6], cacc[8 * s2 + 7])};
         }
       }
-      if (g32 == 0) Lpos[l32] = wr ? pos : -1;
+      if (g32 == 0) Lpos[l32] = (int)prow_me;  // the slot's partial row (or its trash row)
       p.partial_exp[prow_me] = (int8_t)pexp;  // both lane halves store the same byte
       wave_lds_sync();
       // all LDS reads first, then the stores, so the reads overlap
@@ -525,8 +528,7 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
 #pragma unroll
       for (int it = 0; it < ITS; ++it) {
         const int ch = (it * 64 + lane) % C::ROW_CHUNKS;
-        const uint64_t prow = ps[it] >= 0 ? (uint64_t)(uint32_t)ps[it] * (uint32_t)p.ntiles + tile : trash;
-        st_stream_16(p.partials + prow * (D_QK * 2) + ch * 16, v[it]);
+        st_stream_16(p.partials + ((uint32_t)ps[it] * (uint32_t)(D_QK * 2) + (uint32_t)ch * 16u), v[it]);
       }
       wave_lds_sync();  // K / dS tiles are consumed before the next block's gather lands
       idx_cur = idx_nxt;
@@ -560,7 +562,7 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
     if constexpr (F32P) {
       // fp32 rows: the two lanes of a slot store adjacent 16-byte pieces, with
       // plain (write-back) stores so that L2 merges a row's pieces into lines
-      unsigned char *dst = p.partials + prow_me * (uint64_t)(D_QK * 4);
+      unsigned char *dst = p.partials + prow_me * (uint32_t)(D_QK * 4);
 #pragma unroll
       for (int dt = 0; dt < C::DQT; ++dt)
 #pragma unroll
@@ -598,7 +600,7 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
                     (int)pack_f16x2(cacc[dt][8 * s + 4] * rscale, cacc[dt][8 * s + 5] * rscale),
                     (int)pack_f16x2(cacc[dt][8 * s + 6] * rscale, cacc[dt][8 * s + 7] * rscale)};
         }
-      if (g32 == 0) Lpos[l32] = wr ? pos : -1;
+      if (g32 == 0) Lpos[l32] = (int)prow_me;  // the slot's partial row (or its trash row)
       p.partial_exp[prow_me] = (int8_t)pexp;  // both lane halves store the same byte
       wave_lds_sync();
       // all LDS reads first, then the stores, so the reads overlap
@@ -615,8 +617,7 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
 #pragma unroll
       for (int it = 0; it < ITS; ++it) {
         const int ch = (it * 64 + lane) % C::ROW_CHUNKS;
-        const uint64_t prow = ps[it] >= 0 ? (uint64_t)(uint32_t)ps[it] * (uint32_t)p.ntiles + tile : trash;
-        st_stream_16(p.partials + prow * (D_QK * 2) + ch * 16, v[it]);
+        st_stream_16(p.partials + ((uint32_t)ps[it] * (uint32_t)(D_QK * 2) + (uint32_t)ch * 16u), v[it]);
       }
     }
     wave_lds_sync();  // K / dS tiles are consumed before the next block's gather lands
@@ -675,9 +676,16 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // carried between them in fp32 (first pass stores, later passes add, the
 // last casts to bf16), in pass order, so the result stays deterministic.
 constexpr uint64_t kBwdPassBytes = 4ull << 30;  // default: partial rows (+ exponents) per pass
+// A pass's partial rows stay below 4 GiB (the main kernel addresses them
+// with 32-bit offsets): caps at or above this are lowered to it.
+constexpr uint64_t kBwdPassMax = (4ull << 30) - (1ull << 20);
 
-// The per-pass cap of a call: its pass_bytes argument, 0 meaning the default.
-static uint64_t pass_cap(uint64_t pass_bytes) { return pass_bytes == 0 ? kBwdPassBytes : pass_bytes; }
+// The per-pass cap of a call: its pass_bytes argument, 0 meaning the default,
+// at most kBwdPassMax.
+static uint64_t pass_cap(uint64_t pass_bytes) {
+  const uint64_t cap = pass_bytes == 0 ? kBwdPassBytes : pass_bytes;
+  return cap < kBwdPassMax ? cap : kBwdPassMax;
+}
 
 struct BwdPlan {
   int64_t nb;   // batches per pass
@@ -884,6 +892,8 @@ static int bwd_run(const void *q, const void *kv, const void *o, const void *dO,
   const size_t qel = f8 ? 1 : 2;  // bytes per q / kv element
   uint16_t *dkv16 = static_cast<uint16_t *>(dkv);
   float *carry = reinterpret_cast<float *>(ws + L.carry);
+  // the main kernel addresses a pass's partial rows with 32-bit offsets
+  DSA_REQUIRE(L.pexp <= 0xffffffffull, "sparse_mla_bwd: one pass's partial rows exceed 4 GiB (topk too large)");
   stage_begin(st);
   for (int64_t ps = 0; ps < npass; ++ps) {
     // this pass: batches [b0, b0 + nbp), tokens [t0, t0 + ctp) of each
