@@ -63,7 +63,8 @@ def _bwd_flags(fp32_partials):
 
 
 def _pass_bytes(pass_bytes):
-    """The C-ABI's per-pass cap on the partial dKV rows: 0 selects its default (4 GiB)."""
+    """The C-ABI's per-pass cap on the partial dKV rows: 0 selects its default (4 GiB); caps are
+    lowered to at most 4 GiB - 1 MiB."""
     if pass_bytes is None:
         return 0
     pass_bytes = int(pass_bytes)

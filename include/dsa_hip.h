@@ -121,8 +121,9 @@ enum dsa_bwd_flags {
 
 /*
  * pass_bytes (every backward entry point below): the per-pass cap on the
- * backward's partial dKV rows, in bytes; 0 means the default of 4 GiB.  The
- * backward runs in passes over contiguous token ranges sized to this cap, so
+ * backward's partial dKV rows, in bytes; 0 means the default of 4 GiB, and
+ * every cap is lowered to at most 4 GiB - 1 MiB (a pass's rows are addressed
+ * with 32-bit offsets).  The backward runs in passes over contiguous token ranges sized to this cap, so
  * its workspace stays bounded at any sequence length; a batch split over
  * passes carries its kv rows' sums in fp32 between them.  The workspace /
  * index size queries and the call they size must be given the same value.
