@@ -146,13 +146,14 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
   const auto idx_rs = slot_rsrc(idx_row, p.topk);
   const int raw0 = load_slot_raw(idx_rs, blk, l32);
   int raw_nxt = load_slot_raw(idx_rs, blk + C::WPT, l32);
-  // CSR position of an entry: its kv row's start (rowptr), plus the row's
+  // CSR position of an entry: its kv row's start (rowstart), plus the row's
   // entries in earlier token chunks (base[b][chunk][row]), plus the chunk's
   // earlier tokens that picked the row (the bits below this token in
-  // mask[b][chunk][row]).  A chunk in which a
-  // token repeats a row has no such closed form: its positions were placed
-  // by the inverse-index scatter and are read from pos_of instead (that
-  // resource is empty for every other chunk, so the load reads nothing).
+  // mask[b][chunk][row]).  Where a token of the chunk repeats a row of the
+  // row's part the bits cannot count the chunk's earlier entries of the row:
+  // the inverse index wrote a zero mask word there and left that count (the
+  // entry's rank in entry order) in pos_of (the resource is empty for chunks
+  // without repeats, so the load reads nothing).
   const int64_t s_in_b = tok - b * p.S;
   const int chunk = (int)(s_in_b / kChunkTokens), tl = (int)(s_in_b % kChunkTokens);
   const uint32_t below = (1u << tl) - 1u;
@@ -160,7 +161,7 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
   const bool dupc = p.dup[b * p.NC + chunk] != 0;
   const auto mask_rs = make_buffer_rsrc(p.mask + plane, (uint32_t)(p.R * 4));
   const auto base_rs = make_buffer_rsrc(p.base + plane, (uint32_t)(p.R * 4));
-  const auto rptr_rs = make_buffer_rsrc(p.rowptr + b * p.R, (uint32_t)(p.R * 4));
+  const auto rptr_rs = make_buffer_rsrc(p.rowstart + b * p.R, (uint32_t)(p.R * 4));
   const auto pos_rs = slot_rsrc(p.pos_of + entry0, dupc ? p.topk : 0);
   struct PosParts { int m, b, s, p; };
   auto load_pos_parts = [&](int idxv, int bk) {
@@ -173,7 +174,7 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
     return r;
   };
   auto csr_pos = [&](const PosParts &r) {
-    return dupc ? r.p : r.s + r.b + (int)__popc((uint32_t)r.m & below);
+    return r.s + r.b + (r.m == 0 ? r.p : (int)__popc((uint32_t)r.m & below));
   };
   const auto kv_rs = make_buffer_rsrc(kv_b, (uint32_t)(p.S_kv * (int64_t)row_pitch));
   const auto sc_rs = make_buffer_rsrc(kv_scale_b, FP8 ? (uint32_t)(p.S_kv * 4) : 0u);
@@ -723,13 +724,13 @@ static BwdPlan bwd_plan(int64_t B, int64_t S, int64_t H, int64_t G, int64_t D_qk
 
 // Workspace: the partial-row section (rows, exponents, carry) and the
 // inverse-index section (per 32-token chunk and kv row a token bitmask and a
-// base word, chunk flags, row totals, rowptr, CSR positions), each sized for
+// base word, chunk flags, row totals and starts, CSR positions), each sized for
 // one pass.  dsa_sparse_mla_bwd takes both in one buffer (rows first);
 // dsa_sparse_mla_bwd_indexed takes the index section as a separate buffer that
 // dsa_sparse_mla_bwd_build_index filled ahead of the call.
 struct BwdWorkspace {
   size_t partials, pexp, carry, rows_total;          // offsets in the rows section
-  size_t mask, base, dup, dupc, tot, rowptr, pos_of, index_total;  // offsets in the index section
+  size_t mask, base, dup, dupc, tot, rowstart, pos_of, next, index_total;  // offsets in the index section
   size_t total;                                      // rows section + index section
   BwdPlan plan;
 };
@@ -766,10 +767,12 @@ static BwdWorkspace bwd_layout(int64_t B, int64_t S, int64_t S_kv, int64_t H, in
   off += align256((size_t)pl.nb * pl.NC * 4);
   L.tot = off;
   off += align256((size_t)pl.nb * R * 4);
-  L.rowptr = off;
-  off += align256(((size_t)pl.nb * R + 1) * 4);
+  L.rowstart = off;
+  off += align256((size_t)pl.nb * R * 4);
   L.pos_of = off;
   off += align256(entries * 4);
+  L.next = off;
+  off += align256((size_t)pl.nb * 4);
   L.index_total = off;
   L.total = L.rows_total + L.index_total;
   return L;
@@ -790,7 +793,7 @@ static CsrParams bwd_csr_params(const int32_t *indices, const BwdWorkspace &L, u
   cp.dup = reinterpret_cast<int32_t *>(ix + L.dup);
   cp.dupc = reinterpret_cast<int32_t *>(ix + L.dupc);
   cp.tot = reinterpret_cast<int32_t *>(ix + L.tot);
-  cp.rowptr = reinterpret_cast<int32_t *>(ix + L.rowptr);
+  cp.rowstart = reinterpret_cast<int32_t *>(ix + L.rowstart);
   cp.pos_of = reinterpret_cast<int32_t *>(ix + L.pos_of);
   cp.S = ctp;
   cp.S_kv = S_kv;
@@ -800,7 +803,8 @@ static CsrParams bwd_csr_params(const int32_t *indices, const BwdWorkspace &L, u
   cp.NC = csr_chunks(ctp);
   cp.SPL = csr_split((int64_t)cp.NC * nbp, cp.R);
   cp.RP = (cp.R + cp.SPL - 1) / cp.SPL;
-  cp.dup_only = wide ? 0 : 1;  // the narrow main kernel derives the positions of chunks without repeats
+  cp.local_ranks = wide ? 0 : 1;  // the narrow main kernel derives every position itself
+  cp.next = reinterpret_cast<int32_t *>(ix + L.next);
   return cp;
 }
 
@@ -831,11 +835,11 @@ static int launch_reduce(const CsrParams &cp, const unsigned char *partials, con
                          float *carry, int mode, int64_t rows, int ntiles, bool f32p, hipStream_t st) {
   const unsigned grid = (unsigned)rows;  // one workgroup per kv row
   if (f32p)
-    hipLaunchKernelGGL((dkv_reduce_kernel<D_QK, true>), dim3(grid), dim3(256), 0, st, cp.rowptr, partials, pexp,
-                       dkv, carry, mode, rows, ntiles);
+    hipLaunchKernelGGL((dkv_reduce_kernel<D_QK, true>), dim3(grid), dim3(256), 0, st, cp.rowstart, cp.tot,
+                       partials, pexp, dkv, carry, mode, rows, ntiles);
   else
-    hipLaunchKernelGGL((dkv_reduce_kernel<D_QK, false>), dim3(grid), dim3(256), 0, st, cp.rowptr, partials, pexp,
-                       dkv, carry, mode, rows, ntiles);
+    hipLaunchKernelGGL((dkv_reduce_kernel<D_QK, false>), dim3(grid), dim3(256), 0, st, cp.rowstart, cp.tot,
+                       partials, pexp, dkv, carry, mode, rows, ntiles);
   return check_launch("sparse_mla_bwd(reduce)");
 }
 
@@ -929,7 +933,7 @@ static int bwd_run(const void *q, const void *kv, const void *o, const void *dO,
     p.base = cp.base;
     p.dup = cp.dupc;
     p.R = cp.R;
-    p.rowptr = cp.rowptr;
+    p.rowstart = cp.rowstart;
     p.NC = cp.NC;
     p.partials = ws + L.partials;
     p.partial_exp = reinterpret_cast<int8_t *>(ws + L.pexp);

@@ -20,20 +20,30 @@ namespace dsa {
 //                                 then the exact counts of the part's rows go
 //                                 to base[b][c][r] (a bit cannot count
 //                                 repeats); count(c, r) below is that count
-//                                 or popcount(mask)
+//                                 or popcount(mask); such a part writes zero
+//                                 masks.  With local ranks, it also writes
+//                                 pos_of[e] = the entry's rank among the
+//                                 chunk's earlier entries of its row (entry
+//                                 order)
 //   csr_colscan  base[b][c][r]  = entries of row r in the chunks before c
 //                                 (exclusive prefix over chunks), tot = row
 //                                 total; dupc[b][c] = any part of chunk c has
-//                                 a repeat
-//   csr_scan     rowptr         = exclusive prefix of tot
-//   csr_scatter  pos_of[e]      = rowptr + base + popcount of the earlier
+//                                 a repeat; rowstart = the row's first CSR
+//                                 position: each workgroup reserves one
+//                                 contiguous range for its rows with an
+//                                 integer atomic and lays its rows out in
+//                                 order inside it
+//   csr_scatter  pos_of[e]      = rowstart + base + popcount of the earlier
 //                                 tokens' bits: entries of a row in ascending
-//                                 entry order
+//                                 entry order (only for consumers that read
+//                                 every position from pos_of)
+// Where a row's range lies depends on the order of the reservations; the
+// entries inside it, and so every dKV sum, do not.
 // Without repeats a row's entries inside a chunk are ordered by token alone,
-// so every entry's position is computed independently (the SparseMLA
-// backward's main kernel computes it itself and the scatter only handles
-// chunks with repeats); a chunk with a repeat is placed by one thread in
-// entry order instead (the same positions the stable sort defines).
+// so every entry's position is computed independently: the narrow SparseMLA
+// backward's main kernel computes rowstart + base + popcount itself, and for
+// a row whose part has a repeat (a zero mask word) rowstart + base + the
+// local rank (the order the stable sort defines), so it needs no scatter.
 
 constexpr int kChunkTokens = 32;  // tokens per chunk: one bit each in a 32-bit mask
 
@@ -43,15 +53,18 @@ struct CsrParams {
   int32_t *base;    // [B][NC][R]
   int32_t *dup;     // [B][NC][SPL]: the part's rows hold a repeat
   int32_t *dupc;    // [B][NC]: some part of the chunk does
-  int32_t *tot;     // [B*R]
-  int32_t *rowptr;  // [B*R + 1]
+  int32_t *tot;     // [B*R] entries of each row
+  int32_t *rowstart;  // [B*R] first CSR position of each row
   int32_t *pos_of;  // [entries]: CSR position of each entry, -1 for a masked slot
   int64_t S, S_kv, G, topk;
   int64_t R;        // rows per batch = S_kv * G
   int NC;           // chunks per batch
   int SPL;          // row parts per chunk
   int64_t RP;       // rows per part (the last part may hold fewer)
-  int dup_only;     // scatter only the chunks with repeats (the main kernel places the rest)
+  int local_ranks;  // 1: chunks with repeats get local ranks in pos_of and no scatter runs;
+                    // 0: the scatter writes every entry's CSR position to pos_of
+  int32_t *next;    // [B] CSR positions reserved so far in each batch's region of S * G * topk
+                    // positions (zeroed by the mask kernel)
 };
 
 // Row parts per chunk: enough that a part's rows fit 64 KiB of LDS, and up to
@@ -79,6 +92,8 @@ __global__ void __launch_bounds__(kMaskThreads) csr_mask_kernel(const CsrParams 
   const int c = blockIdx.x / p.SPL, part = blockIdx.x % p.SPL;
   const int64_t b = blockIdx.y;
   const int tid = threadIdx.x;
+  // the column scan that follows on the stream reserves CSR positions from here
+  if (blockIdx.x == 0 && tid == 0) p.next[b] = 0;
   // parts past the last row (RP * SPL may exceed R) hold no rows
   const int64_t r_lo = part * p.RP, r_hi = r_lo + p.RP < p.R ? r_lo + p.RP : p.R;
   const uint32_t nr = r_hi > r_lo ? (uint32_t)(r_hi - r_lo) : 0u;
@@ -125,8 +140,10 @@ __global__ void __launch_bounds__(kMaskThreads) csr_mask_kernel(const CsrParams 
   }
   if (dup) dflag = 1;  // benign race: every writer stores 1
   __syncthreads();
+  // a part with a repeat writes zero masks: a valid entry's own mask word is
+  // never zero otherwise, so consumers tell such rows apart by it
   uint32_t *m = p.mask + (b * p.NC + c) * p.R + r_lo;
-  for (int64_t r = tid; r < nr; r += kMaskThreads) m[r] = mk[r];
+  for (int64_t r = tid; r < nr; r += kMaskThreads) m[r] = dflag ? 0u : mk[r];
   if (tid == 0) p.dup[(b * p.NC + c) * p.SPL + part] = dflag;
   if (dflag) {  // block-uniform: exact per-row counts of this part's rows
     __syncthreads();
@@ -142,28 +159,61 @@ __global__ void __launch_bounds__(kMaskThreads) csr_mask_kernel(const CsrParams 
     __syncthreads();
     int32_t *dst = p.base + (b * p.NC + c) * p.R + r_lo;
     for (int64_t r = tid; r < nr; r += kMaskThreads) dst[r] = cnt[r];
+    if (p.local_ranks) {
+      // each entry of this part's rows: its rank among the chunk's earlier
+      // entries of the same row, walked in entry order by one thread (a
+      // token that repeats a row is an unusual input; this path is serial)
+      __syncthreads();
+      for (int64_t r = tid; r < nr; r += kMaskThreads) cnt[r] = 0;
+      __syncthreads();
+      if (tid == 0) {
+        int32_t *pos = p.pos_of + ((b * p.S + t0) * p.G) * p.topk;
+        for (int64_t e = 0; e < nseg * p.topk; ++e) {
+          const int64_t g = (e / p.topk) % p.G;
+          const int32_t j = seg_idx[e];
+          const uint32_t rr = (uint32_t)(j * p.G + g - r_lo);
+          if (j >= 0 && j < p.S_kv && rr < nr) pos[e] = cnt[rr]++;
+        }
+      }
+    }
   }
 }
 
-// Entries of row r in chunk c of batch b (mask popcount, or the exact count
-// the mask kernel left in base[] for a chunk with repeats).
-__device__ __forceinline__ int32_t chunk_count(const CsrParams &p, int64_t b, int c, int64_t r, int part) {
-  const int64_t cell = (b * p.NC + c) * p.R + r;
-  return p.dup[(b * p.NC + c) * p.SPL + part] ? p.base[cell] : (int32_t)__popc(p.mask[cell]);
+// Entries of row r in chunks c0 .. c0 + T - 1 (those below c_hi) of batch b:
+// the mask popcount, or the exact count the mask kernel left in base[] where
+// the row's part has a repeat.  The flags and masks load together; base only
+// where a flag is set.
+template <int T>
+__device__ __forceinline__ void tile_counts(const CsrParams &p, int64_t b, int c0, int c_hi, int64_t r, bool rok,
+                                            int part, int32_t (&v)[T]) {
+  int32_t dv[T];
+  uint32_t mv[T];
+#pragma unroll
+  for (int u = 0; u < T; ++u) {
+    const bool ok = c0 + u < c_hi && rok;
+    dv[u] = ok ? p.dup[(b * p.NC + c0 + u) * p.SPL + part] : 0;
+    mv[u] = ok ? p.mask[(b * p.NC + c0 + u) * p.R + r] : 0u;
+  }
+#pragma unroll
+  for (int u = 0; u < T; ++u) v[u] = dv[u] ? p.base[(b * p.NC + c0 + u) * p.R + r] : (int32_t)__popc(mv[u]);
 }
 
-// grid (ceil(R / 16), B), 256 threads: thread t takes row 16 blockIdx.x + t % 16
-// and chunk group t / 16 (a contiguous sixteenth of the chunks).  Each thread
+// grid (ceil(R / 32), B), 512 threads: thread t takes row 32 blockIdx.x + t % 32
+// and chunk group t / 32 (a contiguous sixteenth of the chunks).  Each thread
 // totals its chunks of its row, the groups' totals are combined in LDS, and
 // each thread then writes the exclusive prefix over chunks into base[b][c][r]
 // (a chunk's exact count, kept in base for chunks with repeats, is read before
 // the same thread overwrites it).  A group of at most TILE chunks (every group
 // while NC <= 16 * TILE) keeps its counts in registers between the two steps;
-// longer ranges re-read them.  Four-wave workgroups with few registers fit
-// beside the forward kernel, which this kernel runs next to on a second stream.
-constexpr int kScanRows = 16, kScanGroups = 16;
+// longer ranges re-read them.  Wave 0 reserves one contiguous range of CSR
+// positions for the workgroup's rows (an atomic add of their total to the
+// batch's counter p.next[b]; batch b's positions start at b * S * G * topk,
+// past every entry of the batches before it) and gives each row its start
+// inside it, in row order.  Few atomics to one address matter here: each is a
+// round trip to the memory side, and they queue.
+constexpr int kScanRows = 32, kScanGroups = 16;
 __global__ void __launch_bounds__(kScanRows * kScanGroups) csr_colscan_kernel(const CsrParams p) {
-  constexpr int TILE = 4;
+  constexpr int TILE = 8;
   __shared__ int32_t gtot[kScanGroups][kScanRows];
   const int tid = threadIdx.x, rl = tid % kScanRows, cg = tid / kScanRows;
   const int64_t b = blockIdx.y;
@@ -181,8 +231,7 @@ __global__ void __launch_bounds__(kScanRows * kScanGroups) csr_colscan_kernel(co
   int32_t v[TILE];
   int32_t s = 0;
   for (int c0 = c_lo; c0 < c_hi; c0 += TILE) {
-#pragma unroll
-    for (int u = 0; u < TILE; ++u) v[u] = (c0 + u < c_hi && rok) ? chunk_count(p, b, c0 + u, r, part) : 0;
+    tile_counts<TILE>(p, b, c0, c_hi, r, rok, part, v);
 #pragma unroll
     for (int u = 0; u < TILE; ++u) s += v[u];
   }
@@ -195,81 +244,35 @@ __global__ void __launch_bounds__(kScanRows * kScanGroups) csr_colscan_kernel(co
     run += i < cg ? t : 0;
     tot += t;
   }
+  // lanes 0..15 of wave 0 hold the rows' totals: their inclusive prefix over
+  // the rows, and one reservation for all of them, issued here so that its
+  // round trip overlaps the base stores below
+  int32_t x = 0, at = 0;
+  if (cg == 0) {
+    x = tot;
+#pragma unroll
+    for (int off = 1; off < kScanRows; off <<= 1) {
+      const int32_t o = __shfl_up(x, off, kScanRows);
+      if (rl >= off) x += o;
+    }
+    if (rl == kScanRows - 1) at = atomicAdd(p.next + b, x);
+  }
   const bool one_tile = c_hi - c_lo <= TILE;  // block-uniform
   for (int c0 = c_lo; c0 < c_hi; c0 += TILE) {
-    if (!one_tile) {
-#pragma unroll
-      for (int u = 0; u < TILE; ++u) v[u] = (c0 + u < c_hi && rok) ? chunk_count(p, b, c0 + u, r, part) : 0;
-    }
+    if (!one_tile) tile_counts<TILE>(p, b, c0, c_hi, r, rok, part, v);
 #pragma unroll
     for (int u = 0; u < TILE; ++u) {
       if (c0 + u < c_hi && rok) p.base[(b * p.NC + c0 + u) * p.R + r] = run;
       run += v[u];
     }
   }
-  if (cg == 0 && rok) p.tot[b * p.R + r] = tot;
-}
-
-// Exclusive scan of cnt[0..n) into rowptr[0..n] with one 1024-thread
-// workgroup: tiles of 1024 x 8 elements, each thread scanning 8 contiguous
-// elements in registers (two 16-byte loads when aligned), a wave scan and a
-// cross-wave scan per tile, the running total carried across tiles.
-__global__ void __launch_bounds__(1024) csr_scan_kernel(const int32_t *cnt, int32_t *rowptr, int64_t n) {
-  __shared__ int32_t wsum[16];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  int32_t carry = 0;
-  for (int64_t t0 = 0; t0 < n; t0 += 1024 * 8) {
-    const int64_t lo = t0 + (int64_t)tid * 8;
-    int32_t v[8];
-    if (lo + 8 <= n) {
-      const i32x4 a = *reinterpret_cast<const i32x4 *>(cnt + lo);
-      const i32x4 c = *reinterpret_cast<const i32x4 *>(cnt + lo + 4);
-      v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
-      v[4] = c[0]; v[5] = c[1]; v[6] = c[2]; v[7] = c[3];
-    } else {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = lo + k < n ? cnt[lo + k] : 0;
+  if (cg == 0) {
+    at = __shfl(at, kScanRows - 1, kScanRows);
+    if (rok) {
+      p.tot[b * p.R + r] = tot;
+      p.rowstart[b * p.R + r] = (int32_t)(b * p.S * p.G * p.topk) + at + x - tot;
     }
-    int32_t s = 0;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) s += v[k];
-    int32_t x = s;  // inclusive wave scan
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int32_t o = __shfl_up(x, off, 64);
-      if (lane >= off) x += o;
-    }
-    if (lane == 63) wsum[wv] = x;
-    __syncthreads();
-    if (tid < 16) {
-      int32_t y = wsum[tid];
-      for (int off = 1; off < 16; off <<= 1) {
-        const int32_t o = __shfl_up(y, off, 16);
-        if ((tid & 15) >= off) y += o;
-      }
-      wsum[tid] = y;
-    }
-    __syncthreads();
-    int32_t run = carry + (wv > 0 ? wsum[wv - 1] : 0) + x - s;
-    const int32_t tile_total = wsum[15];
-    int32_t o[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      o[k] = run;
-      run += v[k];
-    }
-    if (lo + 8 <= n) {
-      *reinterpret_cast<i32x4 *>(rowptr + lo) = i32x4{o[0], o[1], o[2], o[3]};
-      *reinterpret_cast<i32x4 *>(rowptr + lo + 4) = i32x4{o[4], o[5], o[6], o[7]};
-    } else {
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (lo + k < n) rowptr[lo + k] = o[k];
-    }
-    carry += tile_total;
-    __syncthreads();  // wsum is reused by the next tile
   }
-  if (tid == 0) rowptr[n] = carry;
 }
 
 // grid (NC * SPL, B), 256 threads; dynamic LDS = RP ints (cursors of the
@@ -288,9 +291,8 @@ __global__ void __launch_bounds__(256) csr_scatter_kernel(const CsrParams p) {
   const int64_t e_first = ((b * p.S + t0) * p.G) * p.topk;
   const uint32_t *m = p.mask + (b * p.NC + c) * p.R;
   const int32_t *bs = p.base + (b * p.NC + c) * p.R;
-  const int32_t *rp = p.rowptr + b * p.R;
+  const int32_t *rp = p.rowstart + b * p.R;
   if (p.dupc[b * p.NC + c] == 0) {
-    if (p.dup_only) return;  // block-uniform
     // row r of (token t0 + tl, group g): position = base + earlier tokens of the chunk in r;
     // work items as in the mask kernel, this part's share of them, eight in flight
     const int spt = (int)((p.topk + 255) / 256);
@@ -353,7 +355,7 @@ __global__ void __launch_bounds__(256) csr_scatter_kernel(const CsrParams p) {
 
 // One workgroup per kv row.  The main kernel wrote each entry's partial rows
 // at its CSR position, so the row's items are the contiguous partial rows
-// [rowptr[r] * ntiles, rowptr[r + 1] * ntiles) in CSR order; they are split
+// [rowstart[r] * ntiles, (rowstart[r] + cnt[r]) * ntiles) in CSR order; they are split
 // into four contiguous quarters, one per wave.  A partial row is read as
 // 16-byte chunks by a group of LPE lanes (rows over 1 KiB: all 64 lanes, CPL
 // chunks each), so one load instruction covers EPI = 64 / LPE items and every
@@ -367,7 +369,7 @@ __global__ void __launch_bounds__(256) csr_scatter_kernel(const CsrParams p) {
 // writes bf16(carried + pass sum); mode 0 (one pass) writes bf16(pass sum).
 template <int D_QK, bool F32P>
 __global__ void __launch_bounds__(256)
-dkv_reduce_kernel(const int32_t *rowptr, const unsigned char *partials, const int8_t *partial_exp,
+dkv_reduce_kernel(const int32_t *rowstart, const int32_t *cnt, const unsigned char *partials, const int8_t *partial_exp,
                   uint16_t *dkv, float *carry, int mode, int64_t nrows, int ntiles) {
   constexpr int ROWB = D_QK * (F32P ? 4 : 2);  // bytes per partial row
   constexpr int NCR = ROWB / 16;                // 16-byte chunks per partial row
@@ -382,7 +384,7 @@ dkv_reduce_kernel(const int32_t *rowptr, const unsigned char *partials, const in
   const int grp = lane / LPE, c = lane % LPE;
   const int64_t r = blockIdx.x;
   if (r >= nrows) return;
-  const int64_t base = rowptr[r], n = (int64_t)(rowptr[r + 1] - rowptr[r]) * ntiles;
+  const int64_t base = rowstart[r], n = (int64_t)cnt[r] * ntiles;
   const int64_t k0 = base * ntiles + n * w / 4, k1 = base * ntiles + n * (w + 1) / 4;
   float acc[CPL][EPC];
 #pragma unroll
@@ -489,13 +491,11 @@ static int launch_csr(const CsrParams &cp, int64_t B, hipStream_t st) {
   if (cp.SPL < 1 || cp.RP * cp.SPL < cp.R || lds > 64 * 1024 || (int64_t)cp.NC * cp.SPL >= (1ll << 31))
     return set_error(DSA_ERR_UNSUPPORTED, "sparse_mla_bwd: inverse index split %d x %lld rows of %lld", cp.SPL,
                      (long long)cp.RP, (long long)cp.R);
-  const int64_t rows = B * cp.R;
   const dim3 cgrid((unsigned)(cp.NC * cp.SPL), (unsigned)B);
   const dim3 sgrid((unsigned)((cp.R + kScanRows - 1) / kScanRows), (unsigned)B);
   hipLaunchKernelGGL(csr_mask_kernel, cgrid, dim3(kMaskThreads), lds, st, cp);
   hipLaunchKernelGGL(csr_colscan_kernel, sgrid, dim3(kScanRows * kScanGroups), 0, st, cp);
-  hipLaunchKernelGGL(csr_scan_kernel, dim3(1), dim3(1024), 0, st, cp.tot, cp.rowptr, rows);
-  hipLaunchKernelGGL(csr_scatter_kernel, cgrid, dim3(256), lds, st, cp);
+  if (!cp.local_ranks) hipLaunchKernelGGL(csr_scatter_kernel, cgrid, dim3(256), lds, st, cp);
   return check_launch("sparse_mla_bwd(csr)");
 }
 

@@ -43,11 +43,13 @@ struct BwdParams {
   uint16_t *dq;
   const float *q_scale;
   const float *kv_scale;
-  const int32_t *pos_of;  // CSR position of each entry (-1: masked slot); chunks with repeats only
+  const int32_t *pos_of;  // narrow kernel: an entry's rank among its chunk's earlier entries of its
+                          // row (chunks with repeats only); wide kernel: every entry's CSR
+                          // position (-1: masked slot)
   const uint32_t *mask;   // inverse index: [B][NC][R] token bits per (chunk, kv row)
   const int32_t *base;    // [B][NC][R] first CSR position of a (chunk, kv row)
   const int32_t *dup;     // [B][NC] chunk has a token repeating a row
-  const int32_t *rowptr;  // [B*R + 1] first CSR position of each kv row
+  const int32_t *rowstart;  // [B*R] first CSR position of each kv row
   int64_t R;              // kv rows per batch (S_kv * G)
   int NC;                 // token chunks per batch
   unsigned char *partials;
