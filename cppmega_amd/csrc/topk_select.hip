@@ -261,7 +261,7 @@ topk_wave_kernel(const TopkParams p) {
   static_assert(IPL % kGroup == 0, "items come in whole groups");
   constexpr int NG = IPL / kGroup;
   constexpr int BPL = kWaveBins / 64;
-  __shared__ int s_hist[4][kWaveBins];
+  __shared__ int s_hist[4][kWaveBins + 64];
   __shared__ float s_list[4][64];
   // the wave index is uniform: make the row and everything derived from it scalar
   const int w = __builtin_amdgcn_readfirstlane(wave_id()), lane = lane_id();
@@ -373,12 +373,17 @@ topk_wave_kernel(const TopkParams p) {
       int *const hist_b = hist - kBinBits;
       int one = 1;
       asm volatile("" : "+v"(one));
+      // lanes whose score is below L count in a bin of their own past the
+      // histogram: no branch around the atomic, distinct addresses
+      const uint32_t dummy = kBinBits + (uint32_t)kWaveBins + (uint32_t)lane;
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
         if (g < ng) {
 #pragma unroll
-          for (int i = g * kGroup; i < (g + 1) * kGroup; ++i)
-            if (x[i] >= L) atomicAdd(&hist_b[lin_bits(x[i], scale, cbin)], one);
+          for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
+            const uint32_t bi = x[i] >= L ? lin_bits(x[i], scale, cbin) : dummy;
+            atomicAdd(&hist_b[bi], one);
+          }
         }
       }
       wave_lds_sync();
