@@ -572,7 +572,7 @@ constexpr int kBlockBins = 2048;
 
 template <int NW>
 struct BlockLds {
-  int hist[kBlockBins];
+  int hist[kBlockBins + 64];  // + one bin per lane for the scores below the bound
   float list[NW][64];   // bucket members, one region per wave
   float redf[2 * NW];
   int redi[2 * NW];
@@ -726,12 +726,17 @@ __global__ void __launch_bounds__(64 * NW) topk_block_kernel(const TopkParams p)
       int *const hist_b = hist - kBinBits;
       int one = 1;
       asm volatile("" : "+v"(one));
+      // scores below L count in their lane's bin past the histogram: no
+      // branch around the atomic, distinct addresses within each wave
+      const uint32_t dummy = kBinBits + (uint32_t)kBlockBins + (uint32_t)lane;
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
         if (g < ng) {
 #pragma unroll
-          for (int i = g * kGroup; i < (g + 1) * kGroup; ++i)
-            if (x[i] >= L) atomicAdd(&hist_b[lin_bits(x[i], scale, cbin)], one);
+          for (int i = g * kGroup; i < (g + 1) * kGroup; ++i) {
+            const uint32_t bi = x[i] >= L ? lin_bits(x[i], scale, cbin) : dummy;
+            atomicAdd(&hist_b[bi], one);
+          }
         }
       }
       __syncthreads();
