@@ -485,32 +485,42 @@ sparse_mla_bwd_main_kernel(const BwdParams p) {
       wave_lds_sync();  // the dQ GEMM's reads of the K / dS tiles are complete
       unsigned char *Cs = Kl;
       int *Lpos = reinterpret_cast<int *>(DS);
+      static_assert(C::DQT % 2 == 0, "d-tiles in pairs");
 #pragma unroll
-      for (int dt = 0; dt < C::DQT; ++dt) {
-        f32x16 cacc;
+      for (int dp = 0; dp < C::DQT; dp += 2) {
+        // two d-tiles' independent MFMA chains, then both conversions
+        f32x16 cacc[2];
 #pragma unroll
-        for (int a = 0; a < 16; ++a) cacc[a] = 0.0f;
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-          const i32x4 av = tr_operand_perm(QL, C::QL_STRIDE, dt * 32, 16 * kc);
-          cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(av), dsB[kc], cacc, 0, 0, 0);
-        }
-        if (dt < C::DVT) {
+          for (int a = 0; a < 16; ++a) cacc[u][a] = 0.0f;
 #pragma unroll
-          for (int kc = 0; kc < 2; ++kc) {
-            const i32x4 av = tr_operand_perm(DOL, C::DOL_STRIDE, dt * 32, 16 * kc);
-            cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(av), pB[kc], cacc, 0, 0, 0);
+        for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const i32x4 av = tr_operand_perm(QL, C::QL_STRIDE, (dp + u) * 32, 16 * kc);
+            cacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(av), dsB[kc], cacc[u], 0, 0, 0);
           }
-        }
-        // lane: slot l32, d = dt*32 + 16s + 8*g32 + (0..7): cacc[8s .. 8s+7]
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          const int d0 = dt * 32 + 16 * s2 + 8 * g32;
-          *reinterpret_cast<i32x4 *>(Cs + l32 * C::CS_STRIDE + d0 * 2) =
-              i32x4{(int)pack_f16x2(cacc[8 * s2], cacc[8 * s2 + 1]), (int)pack_f16x2(cacc[8 * s2 + 2], cacc[8 * s2 + 3]),
-                    (int)pack_f16x2(cacc[8 * s2 + 4], cacc[8 * s2 + 5]),
-                    (int)pack_f16x2(cacc[8 * s2 + 6], cacc[8 * s2 + 7])};
-        }
+        for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            if (dp + u < C::DVT) {
+              const i32x4 av = tr_operand_perm(DOL, C::DOL_STRIDE, (dp + u) * 32, 16 * kc);
+              cacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(av), pB[kc], cacc[u], 0, 0, 0);
+            }
+          }
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) {
+            const int d0 = (dp + u) * 32 + 16 * s2 + 8 * g32;
+            *reinterpret_cast<i32x4 *>(Cs + l32 * C::CS_STRIDE + d0 * 2) =
+                i32x4{(int)pack_f16x2(cacc[u][8 * s2], cacc[u][8 * s2 + 1]),
+                      (int)pack_f16x2(cacc[u][8 * s2 + 2], cacc[u][8 * s2 + 3]),
+                      (int)pack_f16x2(cacc[u][8 * s2 + 4], cacc[u][8 * s2 + 5]),
+                      (int)pack_f16x2(cacc[u][8 * s2 + 6], cacc[u][8 * s2 + 7])};
+          }
       }
       if (g32 == 0) Lpos[l32] = (int)prow_me;  // the slot's partial row (or its trash row)
       p.partial_exp[prow_me] = (int8_t)pexp;  // both lane halves store the same byte
