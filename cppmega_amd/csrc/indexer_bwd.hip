@@ -30,6 +30,8 @@
 // key tiles outside every window of a workgroup's rows are not computed.  The
 // key-major kernel then marks, per (batch, token chunk, key block), whether it
 // wrote a partial, and the reduction sums only those.
+#include <type_traits>
+
 #include "dsa_common.hpp"
 
 namespace dsa {
@@ -101,9 +103,11 @@ __device__ __forceinline__ float ld_w(const IdxBwdParams &p, int64_t i) {
 }
 
 // ---------------------------------------------------------------------------
-// dq, dw: one workgroup per (token block, batch), longest rows first
+// dq, dw: one workgroup per (token block, batch), longest rows first.
+// WIN: row windows (p.starts / p.ends), an instantiation of its own so that the
+// causal / full kernel carries no window bounds in its per-element mask.
 // ---------------------------------------------------------------------------
-template <int H, int D, bool RELU>
+template <int H, int D, bool RELU, bool WIN>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 indexer_bwd_q_kernel(const IdxBwdParams p) {
   using C = IdxBwdCfg<H, D>;
@@ -126,7 +130,7 @@ indexer_bwd_q_kernel(const IdxBwdParams p) {
   const int64_t t_last = (t0 + C::TT < p.Sq ? t0 + C::TT : p.Sq) - 1;
   int64_t kend = p.causal ? (t_last + 1 < p.Sk ? t_last + 1 : p.Sk) : p.Sk;
   int64_t kbeg = 0;  // keys below every row's window start are skipped
-  if (p.ends != nullptr) {
+  if constexpr (WIN) {
     // the union of the workgroup's row ranges (TT <= 64 tokens: one per lane, in every wave)
     int lo = 0x7fffffff, hi = 0;
     if (lane < C::TT && t0 + lane <= t_last) {
@@ -148,6 +152,9 @@ indexer_bwd_q_kernel(const IdxBwdParams p) {
   const int64_t wave_row0 = t0 * H + w * C::RPW;      // (token, head) rows t * H + h
   const int64_t wave_tok_last = (wave_row0 + C::RPW - 1) / H;
   int64_t wave_kend = p.causal ? (wave_tok_last + 1 < p.Sk ? wave_tok_last + 1 : p.Sk) : p.Sk;
+  // keys below every row limit of the wave (causal: its first token + 1); not used with windows
+  const int64_t wave_tok0 = wave_row0 / H;
+  const int64_t wave_kfull = p.causal ? (wave_tok0 + 1 < p.Sk ? wave_tok0 + 1 : p.Sk) : p.Sk;
 
   // key tiles: rows [first, first + KT) of batch b through a resource ending at the last key
   const uint32_t row_pitch = (uint32_t)(p.B * C::ROWB);
@@ -224,7 +231,7 @@ indexer_bwd_q_kernel(const IdxBwdParams p) {
   int wave_kbeg = 0;
 #pragma unroll
   for (int m = 0; m < C::MT; ++m) {
-    if (p.ends != nullptr) {
+    if constexpr (WIN) {
       int a = 0, e = 0;
       if (tok[m] < p.Sq) row_keys(p, b, tok[m], a, e);
       klo[m] = a;
@@ -234,7 +241,7 @@ indexer_bwd_q_kernel(const IdxBwdParams p) {
       klim[m] = p.causal ? (tok[m] + 1 < p.Sk ? (int)tok[m] + 1 : sk32) : sk32;
     }
   }
-  if (p.ends != nullptr) {
+  if constexpr (WIN) {
     // the union of the wave's row ranges: sub-tiles outside it are skipped
     int lo = 0x7fffffff, hi = 0;
 #pragma unroll
@@ -273,7 +280,7 @@ indexer_bwd_q_kernel(const IdxBwdParams p) {
     for (int sub = 0; sub < C::SUBS; ++sub) {
       const int64_t sn = (int64_t)it * C::KT + sub * 32;
       if (sn >= wave_kend) break;  // wave-uniform
-      if (sn + 32 <= wave_kbeg) continue;
+      if (WIN && sn + 32 <= wave_kbeg) continue;
       // G of the lane's row token at keys sn + 8i + 4 g32 + (0..3), from the staged tile
       f32x4 gv[C::MT][4];
 #pragma unroll
@@ -295,31 +302,37 @@ indexer_bwd_q_kernel(const IdxBwdParams p) {
           acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kr), QB[m][k], acc[m], 0, 0, 0);
       }
       // M = G act'(L) (0 off the causal window and past Sk), dw += M L; M -> bf16 B operands.
-      // 32-bit keys and non-short-circuit predicates: one select per element, no branches
+      // 32-bit keys and non-short-circuit predicates: one select per element, no branches.
+      // A sub-tile below every row limit of the wave (the causal interior) needs no key test.
       const int s0 = (int)sn + 4 * g32;
       bf16x8 MB[C::MT][2];
+      auto form_m = [&](auto interior) {
+        constexpr bool IN = decltype(interior)::value;
 #pragma unroll
-      for (int m = 0; m < C::MT; ++m) {
-        uint32_t mw[8];
+        for (int m = 0; m < C::MT; ++m) {
+          uint32_t mw[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float mv[4];
+          for (int i = 0; i < 4; ++i) {
+            float mv[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int s = s0 + 8 * i + j;
-            const float L = acc[m][4 * i + j];
-            const bool ok = (s < klim[m]) & (s >= klo[m]) & (!RELU | (L > 0.0f));
-            const float v = ok ? gv[m][i][j] : 0.0f;
-            dwa[m] = fmaf(v, L, dwa[m]);
-            mv[j] = v;
+            for (int j = 0; j < 4; ++j) {
+              const int s = s0 + 8 * i + j;
+              const float L = acc[m][4 * i + j];
+              const bool ok = (IN | (s < klim[m])) & (!WIN | (s >= klo[m])) & (!RELU | (L > 0.0f));
+              const float v = ok ? gv[m][i][j] : 0.0f;
+              dwa[m] = fmaf(v, L, dwa[m]);
+              mv[j] = v;
+            }
+            mw[2 * i] = pack_bf16x2(mv[0], mv[1]);
+            mw[2 * i + 1] = pack_bf16x2(mv[2], mv[3]);
           }
-          mw[2 * i] = pack_bf16x2(mv[0], mv[1]);
-          mw[2 * i + 1] = pack_bf16x2(mv[2], mv[3]);
-        }
 #pragma unroll
-        for (int kc = 0; kc < 2; ++kc)
-          MB[m][kc] = as_bf16x8(i32x4{(int)mw[4 * kc], (int)mw[4 * kc + 1], (int)mw[4 * kc + 2], (int)mw[4 * kc + 3]});
-      }
+          for (int kc = 0; kc < 2; ++kc)
+            MB[m][kc] = as_bf16x8(i32x4{(int)mw[4 * kc], (int)mw[4 * kc + 1], (int)mw[4 * kc + 2], (int)mw[4 * kc + 3]});
+        }
+      };
+      if (!WIN && sn + 32 <= wave_kfull) form_m(std::true_type{});
+      else form_m(std::false_type{});
       // dq^T[d][row] += K^T[d][key] M[key][row]: keys of k-step kc in the accumulator order
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc)
@@ -689,7 +702,10 @@ static int launch_idx_bwd(IdxBwdParams p, hipStream_t st) {
   DSA_REQUIRE(ntb * p.B < (1ll << 31), "dsa_indexer_scores_backward: grid too large");
   const int64_t nkb = (p.Sk + C::KB - 1) / C::KB;
   p.nkb = (int)nkb;
-  hipLaunchKernelGGL((indexer_bwd_q_kernel<H, D, RELU>), dim3((unsigned)(ntb * p.B)), dim3(C::NT), 0, st, p);
+  if (p.ends != nullptr)
+    hipLaunchKernelGGL((indexer_bwd_q_kernel<H, D, RELU, true>), dim3((unsigned)(ntb * p.B)), dim3(C::NT), 0, st, p);
+  else
+    hipLaunchKernelGGL((indexer_bwd_q_kernel<H, D, RELU, false>), dim3((unsigned)(ntb * p.B)), dim3(C::NT), 0, st, p);
   int rc = check_launch("indexer_scores_backward(dq)");
   if (rc) return rc;
   if (p.ends != nullptr)
