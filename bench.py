@@ -152,13 +152,14 @@ def measure_cfg5(dev, reps=3):
             ts.append(a.elapsed_time(b_))
         return sorted(ts)[len(ts) // 2] / 1e3
 
-    from cppmega_amd.dsa_topk import indexer_topk_streaming
+    from cppmega_amd.dsa_topk import indexer_topk_fused, indexer_topk_streaming
     out, lse = sparse_mla_fwd_interface(q, kv, idx, sm_scale=C5_DQK ** -0.5, d_v=C5_DV)
     do = torch.randn(out.shape, generator=gen, device=dev).to(torch.bfloat16)
     t = {
         "bwd": timed(lambda: sparse_mla_bwd(q, kv, out, do, idx, lse, sm_scale=C5_DQK ** -0.5)),
         "indexer_topk_streaming": timed(lambda: indexer_topk_streaming(iq8, ik8, iw, C5_TOPK, q_scale=iqs, k_scale=iks,
                                                                        max_scratch_bytes=64 << 20)),
+        "indexer_topk_fused": timed(lambda: indexer_topk_fused(iq8, ik8, iw, C5_TOPK, q_scale=iqs, k_scale=iks)),
         "fwd": timed(lambda: sparse_mla_fwd_interface(q, kv, idx, sm_scale=C5_DQK ** -0.5, d_v=C5_DV)),
         "fwd_mxfp8": timed(lambda: sparse_mla_blockscaled_mxfp8_fwd_interface(qmx, kmx, qbs, kbs, idx,
                                                                               sm_scale=C5_DQK ** -0.5, d_v=C5_DV)),
@@ -168,7 +169,10 @@ def measure_cfg5(dev, reps=3):
     }
     res = {"indexer_topk_streaming": {"ms": round(t["indexer_topk_streaming"] * 1e3, 3),
                                       "scratch_mib": 64, "note": "e4m3 indexer + top-2048 in 1024-row chunks, "
-                                      "no [1, 16384, 16384] score matrix (dense path: indexer_fp8 + topk)"}}
+                                      "no [1, 16384, 16384] score matrix (dense path: indexer_fp8 + topk)"},
+           "indexer_topk_fused": {"ms": round(t["indexer_topk_fused"] * 1e3, 3), "scratch_mib": 0,
+                                  "note": "top-2048 kept per row on chip while its keys are scored "
+                                          "(dsa_indexer_topk_fused): no scores, no scratch"}}
     for k, (fl, by, kind) in cfg5_work().items():
         e = {"ms": round(t[k] * 1e3, 3)}
         if kind == "fp8+bf16":
@@ -660,11 +664,13 @@ def main():
                "note": "HIP-graph replays of the step with SparseMLA fed the top-256 the indexer just chose "
                        "(cfg3 scores) instead of cfg2's uniform indices; same work per token"}
 
-    from cppmega_amd.dsa_topk import indexer_topk_streaming
+    from cppmega_amd.dsa_topk import indexer_topk_fused, indexer_topk_streaming
     t_stream = graph_replay_time(lambda: indexer_topk_streaming(iq, ik, iw, TOPK, max_scratch_bytes=16 << 20))
-    streaming = {"ms": round(t_stream * 1e3, 4), "scratch_mib": 16,
+    t_fused = graph_replay_time(lambda: indexer_topk_fused(iq, ik, iw, TOPK))
+    streaming = {"ms": round(t_stream * 1e3, 4), "scratch_mib": 16, "fused_ms": round(t_fused * 1e3, 4),
                  "note": "cfg3 indexer + top-256 in 512-row chunks (no [2, 4096, 4096] score matrix); "
-                         "HIP-graph replays; dense path = kernels.indexer + kernels.topk"}
+                         "fused_ms: the top-256 kept per row on chip while its keys are scored, no scratch "
+                         "(dsa_indexer_topk_fused); HIP-graph replays; dense path = kernels.indexer + kernels.topk"}
     megatron_masked = measure_megatron_masked(dev, iq, ik, iw, t_idx / 1e3)
     cfg5 = None if args.no_cfg5 else measure_cfg5(dev)
     kl = None if args.no_kl else measure_indexer_kl(dev)

@@ -51,6 +51,8 @@ EXPORTED_SYMBOLS = (
     "dsa_indexer_scores_backward",
     "dsa_indexer_topk_streaming_workspace_size",
     "dsa_indexer_topk_streaming",
+    "dsa_indexer_topk_fused_max_topk",
+    "dsa_indexer_topk_fused",
     "dsa_topk",
     "dsa_topk_workspace_size",
     "dsa_topk_ws",
@@ -111,6 +113,9 @@ _SIGNATURES = {
     "dsa_indexer_topk_streaming_workspace_size": (_size_t, [_i64] * 4),
     "dsa_indexer_topk_streaming": (_i32, [_c_void_p] * 5 + [_i64] * 5 + [_i32, _i32, _c_void_p, _c_void_p, _i64,
                                                                          _i32, _i32, _c_void_p, _size_t, _c_void_p]),
+    "dsa_indexer_topk_fused_max_topk": (_i64, [_i64, _i64]),
+    "dsa_indexer_topk_fused": (_i32, [_c_void_p] * 5 + [_i64] * 5 + [_i32, _i32, _c_void_p, _c_void_p, _i64,
+                                                                     _i32, _i32, _c_void_p]),
     "dsa_topk": (_i32, [_c_void_p, _i64, _i64, _i64, _i64, _i32, _i64,
                         _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p]),
     "dsa_topk_workspace_size": (_size_t, [_i64, _i64, _i64]),

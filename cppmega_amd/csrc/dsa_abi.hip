@@ -28,7 +28,7 @@ int check_launch(const char *what) {
 
 extern "C" const char *dsa_last_error(void) { return dsa::g_last_error; }
 
-extern "C" int dsa_abi_version(void) { return 200; }
+extern "C" int dsa_abi_version(void) { return 201; }
 
 extern "C" int dsa_device_check(int device) {
   hipDeviceProp_t prop;

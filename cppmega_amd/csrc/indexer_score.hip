@@ -24,6 +24,8 @@
 #include <type_traits>
 
 #include "dsa_common.hpp"
+#include "wave_ops.hpp"
+#include "topk_list.hpp"
 
 namespace dsa {
 
@@ -713,4 +715,346 @@ extern "C" int dsa_indexer_topk_streaming(const void *q, const void *w, const vo
     }
   }
   return DSA_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Fused indexer + top-k: the top-k of every query row without writing its
+// scores anywhere.  One workgroup walks all keys of a token block (causal:
+// the long block ntb-1-j, then the short block j, so every workgroup does the
+// same work); each wave keeps, per query row of its tokens, a candidate list
+// in LDS, appended in column order as the 32-key sub-tiles are scored (the
+// same scoring code as idx_segment, so the scores are bit-identical to the
+// dense indexer's).  A row's list takes every key until it would overflow;
+// then an exact selection keeps the row's current top-k (under the top-k
+// contract: value descending, NaN as +inf, -0 equal to +0, ties to the lower
+// column) and raises the row's threshold to the k-th kept value.  Later keys
+// enter only above it: a key equal to it has a higher column than every kept
+// equal one and loses the tie.  At the end the list's top-k is the row's.
+// ---------------------------------------------------------------------------
+namespace dsa {
+
+struct FusedTopkOut {
+  int32_t *idx;    // [B, Sq, topk]: ascending columns, -1 padding
+  float *scores;   // [B, Sq, topk] or NULL: the selected scores, -inf padding
+  int topk;
+};
+
+// Candidates held per query row (8 bytes each: raw score bits, column).  The
+// list must keep room for a sub-tile's 32 keys after a selection leaves topk.
+template <int H> struct FusedCap { static constexpr int value = H == 16 ? 896 : (H == 32 ? 1792 : 3584); };
+constexpr int kFusedSlack = 64;
+
+template <int H, int D, bool FP8>
+struct FusedCfg {
+  using C = IdxCfg<H, D, FP8>;
+  static constexpr int CAP = FusedCap<H>::value;
+  static constexpr int KS_BYTES = 2 * C::KT * C::KS_STRIDE;
+  static constexpr int CAND_BYTES = C::WAVES * C::TPW * CAP * 8;
+  static constexpr int HIST_BYTES = C::WAVES * 256 * 4;
+  static constexpr int LDS_BYTES = KS_BYTES + CAND_BYTES + HIST_BYTES;
+  static_assert(LDS_BYTES <= 160 * 1024, "fused indexer + top-k LDS");
+};
+
+// One token block [t0, t0 + TT) of batch b over all of its keys (causal: keys
+// s <= t), its rows' top-k written at the end.
+template <int H, int D, bool FP8, bool RELU>
+__device__ __forceinline__ void idx_block_topk(const IdxParams &p, const FusedTopkOut &o, unsigned char *smem,
+                                               int64_t b, int64_t t0_in) {
+  using F = FusedCfg<H, D, FP8>;
+  using C = IdxCfg<H, D, FP8>;
+  constexpr int CAP = F::CAP;
+  unsigned char (&KS)[2][C::KT * C::KS_STRIDE] = *reinterpret_cast<unsigned char (*)[2][C::KT * C::KS_STRIDE]>(smem);
+  const int64_t t0 = __builtin_amdgcn_readfirstlane((int)t0_in);
+  const int tid = threadIdx.x, lane = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
+  const int g32 = lane >> 5, l32 = lane & 31;
+  uint2 *cand = reinterpret_cast<uint2 *>(smem + F::KS_BYTES) + w * C::TPW * CAP;  // [TPW][CAP] of this wave
+  const uint32_t cand_off = (uint32_t)(F::KS_BYTES + w * C::TPW * CAP * 8);        // the same, in fsmem
+  const uint32_t hist_off = (uint32_t)(F::KS_BYTES + F::CAND_BYTES + w * 256 * 4);  // this wave's 256 ints
+  const int64_t t_last = (t0 + C::TT < p.Sq ? t0 + C::TT : p.Sq) - 1;
+  const int64_t kend = p.causal ? (t_last + 1 < p.Sk ? t_last + 1 : p.Sk) : p.Sk;
+  const int ntile = (int)((kend + C::KT - 1) / C::KT);
+  const int topk = o.topk;
+  __syncthreads();  // the previous block's waves are done with the key tiles
+
+  const uint32_t row_pitch = (uint32_t)(p.B * C::ROWB);
+  const unsigned char *k_b = p.k + b * C::ROWB;
+  static_assert(C::NT % C::CPR == 0, "whole keys per load round");
+  constexpr int KPR = C::NT / C::CPR;
+  const uint32_t loff0 = (uint32_t)(tid / C::CPR) * row_pitch + (uint32_t)(tid % C::CPR) * 16u;
+  const int soff0 = (tid / C::CPR) * C::KS_STRIDE + (tid % C::CPR) * 16;
+  auto load_tile = [&](int it, i32x4 (&r)[C::LOADS]) {
+    const int64_t first = (int64_t)it * C::KT;
+    const int64_t nkeys = p.Sk - first;
+    const uint32_t nb = nkeys > 0 ? (uint32_t)((nkeys - 1) * row_pitch + C::ROWB) : 0u;
+    const auto rs = make_buffer_rsrc(k_b + (nkeys > 0 ? first : 0) * row_pitch, nb);
+#pragma unroll
+    for (int l = 0; l < C::LOADS; ++l)
+      r[l] = __builtin_bit_cast(
+          i32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)loff0, (int)((uint32_t)(l * KPR) * row_pitch), 0));
+  };
+  auto store_tile = [&](int buf, const i32x4 (&r)[C::LOADS]) {
+    unsigned char *dst = &KS[buf][soff0];
+#pragma unroll
+    for (int l = 0; l < C::LOADS; ++l) *reinterpret_cast<i32x4 *>(dst + l * KPR * C::KS_STRIDE) = r[l];
+  };
+  i32x4 kreg[C::LOADS];
+  if (ntile > 0) load_tile(0, kreg);
+
+  // A operands and weights of this wave's rows (as idx_segment)
+  typedef typename std::conditional<FP8, i32x8, bf16x8>::type aop_t;
+  aop_t A[C::MT][C::KSTEPS];
+  const int64_t wave_tok0 = t0 + w * C::TPW;
+#pragma unroll
+  for (int m = 0; m < C::MT; ++m) {
+    const int r = m * 32 + l32;
+    const int64_t t = wave_tok0 + r / H;
+    const bool ok = t < p.Sq;
+    const int64_t qrow = (t * p.B + b) * H + r % H;
+#pragma unroll
+    for (int k = 0; k < C::KSTEPS; ++k) {
+      if constexpr (FP8) {
+        i32x4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
+        if (ok) {
+          lo = ld_global_16(p.q + qrow * D + 64 * k + 16 * g32);
+          hi = ld_global_16(p.q + qrow * D + 64 * k + 32 + 16 * g32);
+        }
+        A[m][k] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      } else {
+        i32x4 v = {0, 0, 0, 0};
+        if (ok) v = ld_global_16(p.q + (qrow * D + 16 * k + 8 * g32) * 2);
+        A[m][k] = as_bf16x8(v);
+      }
+    }
+  }
+  float wl = 0.0f;
+  {
+    const int64_t t = wave_tok0 + lane / H;
+    if (t < p.Sq) {
+      const int64_t wi = (t * p.B + b) * H + lane % H;
+      wl = p.w_f32 ? static_cast<const float *>(p.w)[wi] : bf16_bits_to_f32(static_cast<const uint16_t *>(p.w)[wi]);
+    }
+    if constexpr (FP8) wl *= p.q_scale[0] * p.k_scale[0];
+  }
+  float wv[C::MT][16];
+#pragma unroll
+  for (int m = 0; m < C::MT; ++m)
+#pragma unroll
+    for (int a = 0; a < 16; ++a) wv[m][a] = __shfl(wl, m * 32 + 8 * (a >> 2) + 4 * g32 + (a & 3), 64);
+
+  const int brow_off = l32 * C::KS_STRIDE + 16 * g32;
+  auto subtile = [&](const unsigned char *ks, int sub, float (&part)[C::TPW]) {
+#pragma unroll
+    for (int tl = 0; tl < C::TPW; ++tl) part[tl] = 0.0f;
+#pragma unroll
+    for (int m = 0; m < C::MT; ++m) {
+      f32x16 acc;
+#pragma unroll
+      for (int a = 0; a < 16; ++a) acc[a] = 0.0f;
+#pragma unroll
+      for (int k = 0; k < C::KSTEPS; ++k) {
+        const unsigned char *brow = ks + brow_off + sub * 32 * C::KS_STRIDE;
+        if constexpr (FP8) {
+          const i32x4 lo = *reinterpret_cast<const i32x4 *>(brow + 64 * k);
+          const i32x4 hi = *reinterpret_cast<const i32x4 *>(brow + 64 * k + 32);
+          const i32x8 bv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A[m][k], bv, acc, 0, 0, 0, 127, 0, 127);
+        } else {
+          const i32x4 bv = *reinterpret_cast<const i32x4 *>(brow + 32 * k);
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[m][k], as_bf16x8(bv), acc, 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int a = 0; a < 16; ++a) {
+        const int tl = (m * 32 + 8 * (a >> 2)) / H;
+        const float x = RELU ? fmaxf(acc[a], 0.0f) : acc[a];
+        part[tl] = fmaf(x, wv[m][a], part[tl]);
+      }
+    }
+  };
+
+  // per query row of the wave (wave-uniform): list length, threshold key, and
+  // whether the list still takes every key (no selection yet)
+  int cnt[C::TPW], thr[C::TPW], opn[C::TPW];
+#pragma unroll
+  for (int tl = 0; tl < C::TPW; ++tl) {
+    cnt[tl] = 0;
+    thr[tl] = 0;
+    opn[tl] = 1;
+  }
+  auto select_row = [&](int tl) {  // keep row tl's current top-k (wave-uniform call)
+    const uint32_t K = cand_keep_top<CAP / 64>(cand_off + (uint32_t)(tl * CAP * 8), cnt[tl], topk, hist_off);
+    cnt[tl] = topk;
+    thr[tl] = (int)K;
+    opn[tl] = 0;
+  };
+  // the scores of this lane's row tl at key s (valid: a candidate of the row)
+  constexpr int NPAIR = C::TPW >= 2 ? C::TPW / 2 : 1;
+  auto emit = [&](int j, float v, int64_t s) {
+    const int tl = C::TPW >= 2 ? 2 * j + g32 : 0;
+    const int t_lo = C::TPW >= 2 ? 2 * j : 0, t_hi = C::TPW >= 2 ? 2 * j + 1 : 0;
+    const int64_t t = wave_tok0 + tl;
+    const int64_t lim = p.causal ? (t + 1 < p.Sk ? t + 1 : p.Sk) : p.Sk;
+    const bool valid = t < p.Sq && s < lim && (C::TPW >= 2 || g32 == 0);
+    const uint32_t key = score_okey(__float_as_uint(v));
+    bool in = valid && ((g32 ? opn[t_hi] : opn[t_lo]) != 0 || key > (uint32_t)(g32 ? thr[t_hi] : thr[t_lo]));
+    uint64_t bm = __ballot(in);
+    int n0 = __popc((uint32_t)bm), n1 = __popc((uint32_t)(bm >> 32));
+    if (cnt[t_lo] + n0 > CAP || (C::TPW >= 2 && cnt[t_hi] + n1 > CAP)) {  // rare, wave-uniform
+      if (cnt[t_lo] + n0 > CAP) select_row(t_lo);
+      if (C::TPW >= 2 && cnt[t_hi] + n1 > CAP) select_row(t_hi);
+      in = valid && ((g32 ? opn[t_hi] : opn[t_lo]) != 0 || key > (uint32_t)(g32 ? thr[t_hi] : thr[t_lo]));
+      bm = __ballot(in);
+      n0 = __popc((uint32_t)bm);
+      n1 = __popc((uint32_t)(bm >> 32));
+    }
+    if (in) {
+      const uint32_t half = g32 ? (uint32_t)(bm >> 32) : (uint32_t)bm;
+      const int pos = (g32 ? cnt[t_hi] : cnt[t_lo]) + __popc(half & ((1u << l32) - 1u));
+      cand[tl * CAP + pos] = make_uint2(__float_as_uint(v), (uint32_t)s);
+    }
+    cnt[t_lo] += n0;
+    if (C::TPW >= 2) cnt[t_hi] += n1;
+  };
+
+  if (ntile > 0) store_tile(0, kreg);
+  __syncthreads();
+  const int64_t wave_tok_last = wave_tok0 + C::TPW - 1;
+  for (int it = 0; it < ntile; ++it) {
+    load_tile(it + 1, kreg);  // past the last tile: keys beyond Sk read 0, unused
+    const unsigned char *ks = KS[it & 1];
+#pragma unroll 1
+    for (int sub = 0; sub < C::SUBS; ++sub) {
+      const int64_t sn = (int64_t)it * C::KT + sub * 32;
+      // wave-uniform: the sub-tile exists and is not wholly above the wave's diagonal
+      if (sn >= kend || (p.causal && sn > wave_tok_last)) break;
+      float part[C::TPW];
+      subtile(ks, sub, part);
+      const int64_t s = sn + l32;
+      if constexpr (C::TPW >= 2) {
+#pragma unroll
+        for (int j = 0; j < NPAIR; ++j) {
+          // token 2j's total in lanes 0-31, token 2j+1's in lanes 32-63 (as idx_segment)
+          const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(part[2 * j]),
+                                                          __float_as_uint(part[2 * j + 1]), false, false);
+          emit(j, __uint_as_float(r[0]) + __uint_as_float(r[1]), s);
+        }
+      } else {
+        emit(0, sum_halves(part[0]), s);
+      }
+    }
+    if (it + 1 < ntile) {
+      store_tile((it + 1) & 1, kreg);
+      __syncthreads();
+    }
+  }
+
+  // each row: its list's top-k, in column order
+#pragma unroll
+  for (int tl = 0; tl < C::TPW; ++tl) {
+    if (cnt[tl] > topk) select_row(tl);
+    wave_lds_sync();
+    const int64_t t = wave_tok0 + tl;
+    if (t < p.Sq) {
+      int32_t *oi = o.idx + (b * p.Sq + t) * topk;
+      float *os = o.scores ? o.scores + (b * p.Sq + t) * topk : nullptr;
+      const uint2 *c = cand + tl * CAP;
+      for (int e = lane; e < topk; e += 64) {
+        const bool has = e < cnt[tl];
+        const uint2 v = has ? c[e] : make_uint2(0u, 0u);
+        oi[e] = has ? (int32_t)v.y : -1;
+        if (os) os[e] = has ? __uint_as_float(v.x) : -INFINITY;
+      }
+    }
+  }
+}
+
+template <int H, int D, bool FP8, bool RELU>
+__global__ void __launch_bounds__(256) indexer_topk_fused_kernel(const IdxParams p, const FusedTopkOut o) {
+  using C = IdxCfg<H, D, FP8>;
+  const int64_t b = blockIdx.y;
+  if (p.causal) {
+    const int64_t ntb = (p.Sq + C::TT - 1) / C::TT;
+    const int64_t tb_long = ntb - 1 - (int64_t)blockIdx.x, tb_short = blockIdx.x;
+    idx_block_topk<H, D, FP8, RELU>(p, o, fsmem, b, tb_long * C::TT);
+    if (tb_short < tb_long) idx_block_topk<H, D, FP8, RELU>(p, o, fsmem, b, tb_short * C::TT);
+  } else {
+    idx_block_topk<H, D, FP8, RELU>(p, o, fsmem, b, (int64_t)blockIdx.x * C::TT);
+  }
+}
+
+template <int H, int D, bool FP8, bool RELU>
+static int launch_fused_act(const IdxParams &p, const FusedTopkOut &o, hipStream_t st) {
+  using C = IdxCfg<H, D, FP8>;
+  using F = FusedCfg<H, D, FP8>;
+  const int64_t ntb = (p.Sq + C::TT - 1) / C::TT;
+  DSA_REQUIRE(ntb < (1ll << 31), "dsa_indexer_topk_fused: too many query tokens");
+  const auto kern = indexer_topk_fused_kernel<H, D, FP8, RELU>;
+  const hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           F::LDS_BYTES);
+  if (e != hipSuccess) return set_error(DSA_ERR_HIP, "dsa_indexer_topk_fused: LDS attribute: %s", hipGetErrorString(e));
+  const dim3 grid((unsigned)(p.causal ? (ntb + 1) / 2 : ntb), (unsigned)p.B);
+  hipLaunchKernelGGL(kern, grid, dim3(C::NT), F::LDS_BYTES, st, p, o);
+  return check_launch("dsa_indexer_topk_fused");
+}
+
+template <int H, int D, bool FP8>
+static int launch_fused(const IdxParams &p, const FusedTopkOut &o, hipStream_t st) {
+  return p.relu ? launch_fused_act<H, D, FP8, true>(p, o, st) : launch_fused_act<H, D, FP8, false>(p, o, st);
+}
+
+}  // namespace dsa
+
+extern "C" int64_t dsa_indexer_topk_fused_max_topk(int64_t H, int64_t D) {
+  if (!(D == 64 || D == 128)) return 0;
+  if (H == 16) return FusedCap<16>::value - kFusedSlack;
+  if (H == 32) return FusedCap<32>::value - kFusedSlack;
+  if (H == 64) return FusedCap<64>::value - kFusedSlack;
+  return 0;
+}
+
+extern "C" int dsa_indexer_topk_fused(const void *q, const void *w, const void *k, int32_t *out_idx, float *out_scores,
+                                      int64_t B, int64_t Sq, int64_t Sk, int64_t H, int64_t D, int dtype,
+                                      int w_dtype, const float *q_scale, const float *k_scale, int64_t topk,
+                                      int causal, int use_relu, void *stream) {
+  DSA_REQUIRE(B >= 0 && Sq >= 0 && Sk >= 0 && H > 0 && D > 0 && topk > 0, "dsa_indexer_topk_fused: bad dims");
+  DSA_REQUIRE(causal == 0 || causal == 1, "dsa_indexer_topk_fused: causal must be 0 or 1");
+  DSA_REQUIRE(dtype == DSA_DTYPE_BF16 || dtype == DSA_DTYPE_E4M3, "dsa_indexer_topk_fused: dtype %d", dtype);
+  DSA_REQUIRE(w_dtype == DSA_DTYPE_BF16 || w_dtype == DSA_DTYPE_F32, "dsa_indexer_topk_fused: w dtype %d", w_dtype);
+  const int64_t maxk = dsa_indexer_topk_fused_max_topk(H, D);
+  if (maxk == 0 || topk > maxk)
+    return set_error(DSA_ERR_UNSUPPORTED, "dsa_indexer_topk_fused: h=%lld d=%lld topk=%lld (at most %lld)",
+                     (long long)H, (long long)D, (long long)topk, (long long)maxk);
+  if (B == 0 || Sq == 0) return DSA_OK;
+  DSA_REQUIRE(q && w && (k || Sk == 0) && out_idx, "dsa_indexer_topk_fused: null tensor pointer");
+  DSA_REQUIRE(Sk < (1ll << 25) && B < 65536 && Sk * B * D < (1ll << 31),
+              "dsa_indexer_topk_fused: k (%lld x %lld x %lld) too large for 32-bit offsets", (long long)Sk,
+              (long long)B, (long long)D);
+  const bool f8 = dtype == DSA_DTYPE_E4M3;
+  if (f8) DSA_REQUIRE(q_scale && k_scale, "dsa_indexer_topk_fused: e4m3 input needs q_scale and k_scale");
+  IdxParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = static_cast<const unsigned char *>(q);
+  p.w = w;
+  p.k = static_cast<const unsigned char *>(k);
+  p.q_scale = q_scale;
+  p.k_scale = k_scale;
+  p.B = B;
+  p.Sq = Sq;
+  p.Sk = Sk;
+  p.w_f32 = w_dtype == DSA_DTYPE_F32;
+  p.causal = causal;
+  p.relu = use_relu != 0;
+  FusedTopkOut o{out_idx, out_scores, (int)topk};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+#define DSA_FUSED_CASE(HH, DD) \
+  if (H == HH && D == DD) return f8 ? launch_fused<HH, DD, true>(p, o, st) : launch_fused<HH, DD, false>(p, o, st);
+  DSA_FUSED_CASE(16, 64)
+  DSA_FUSED_CASE(32, 64)
+  DSA_FUSED_CASE(64, 64)
+  DSA_FUSED_CASE(16, 128)
+  DSA_FUSED_CASE(32, 128)
+  DSA_FUSED_CASE(64, 128)
+#undef DSA_FUSED_CASE
+  return set_error(DSA_ERR_UNSUPPORTED, "dsa_indexer_topk_fused: no kernel for h=%lld d=%lld", (long long)H,
+                   (long long)D);
 }

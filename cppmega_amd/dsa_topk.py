@@ -167,6 +167,46 @@ def indexer_topk_streaming(q, k, weights, index_topk, use_relu=True, causal=True
     return (idx, vals) if return_scores else idx
 
 
+def indexer_topk_fused_max_topk(heads, head_dim):
+    """Largest index_topk ``indexer_topk_fused`` takes for this indexer shape (0: none)."""
+    return int(_lib.load().dsa_indexer_topk_fused_max_topk(int(heads), int(head_dim)))
+
+
+def indexer_topk_fused(q, k, weights, index_topk, use_relu=True, causal=True, q_scale=None, k_scale=None,
+                       return_scores=False):
+    """``indexer_topk_streaming``'s result with the top-k folded into the
+    indexer: no score matrix, no scratch.  Each query row keeps a bounded
+    candidate list on chip while its keys are scored; the indices (and
+    scores) are bit-identical to ``topk_indices`` over the full scores.
+    index_topk must not exceed ``indexer_topk_fused_max_topk(h, d)``."""
+    assert q.dim() == 4 and k.dim() == 3 and weights.dim() == 3
+    sq, b, h, d = q.shape
+    sk = k.shape[0]
+    fp8 = q.dtype == torch.float8_e4m3fn
+    if fp8:
+        assert k.dtype == torch.float8_e4m3fn and q_scale is not None and k_scale is not None, \
+            "e4m3 indexer inputs need q_scale and k_scale"
+        q_scale = q_scale.reshape(-1)[:1].to(torch.float32).contiguous()
+        k_scale = k_scale.reshape(-1)[:1].to(torch.float32).contiguous()
+    elif q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
+        raise TypeError(f"indexer q/k must be bf16 or float8_e4m3fn, got {q.dtype}/{k.dtype}")
+    if weights.dtype not in (torch.float32, torch.bfloat16):
+        weights = weights.float()
+    q, k, weights = q.contiguous(), k.contiguous(), weights.contiguous()
+    lib = _lib.load()
+    dev = _lib.ensure_device(q)
+    idx = torch.empty((b, sq, int(index_topk)), dtype=torch.int32, device=q.device)
+    vals = torch.empty((b, sq, int(index_topk)), dtype=torch.float32, device=q.device) if return_scores else None
+    rc = lib.dsa_indexer_topk_fused(
+        q.data_ptr(), weights.data_ptr(), k.data_ptr(), idx.data_ptr(), _lib.ptr(vals), b, sq, sk, h, d,
+        _lib.DTYPE_E4M3 if fp8 else _lib.DTYPE_BF16,
+        _lib.DTYPE_F32 if weights.dtype == torch.float32 else _lib.DTYPE_BF16,
+        _lib.ptr(q_scale), _lib.ptr(k_scale), int(index_topk), 1 if causal else 0, 1 if use_relu else 0,
+        _lib.stream_ptr(dev))
+    _lib.check(rc, "dsa_indexer_topk_fused")
+    return (idx, vals) if return_scores else idx
+
+
 def fused_qk_topk_naive(q, k, weights, index_topk, mask=None, varlen_starts=None, varlen_ends=None,
                         key_positions=None, use_relu=True):
     """Megatron ``fused_qk_topk_naive`` on gfx950 -> (scores [b,sq,sk] f32, indices [b,sq,k] int64).

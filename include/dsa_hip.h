@@ -387,6 +387,29 @@ int dsa_indexer_topk_streaming(const void *q, const void *w, const void *k,
                                size_t workspace_bytes, void *stream);
 
 /*
+ * Fused indexer + top-k: the same indices (and selected scores) as
+ * dsa_indexer_topk_streaming and as dsa_topk over dsa_indexer_scores, bit for
+ * bit, with no score matrix and no workspace at all: each query row keeps a
+ * bounded candidate list in on-chip memory while its keys are scored, and an
+ * exact selection under the top-k contract (value descending, NaN as +inf,
+ * -0 equal to +0, ties to the lower column) keeps its running top-k.  This is
+ * the reference's stated target for its indexer ("fold top-k selection into
+ * the per-head/tiled accumulation so the runtime emits only [b,sq,topk]",
+ * docs/status/cppmega_architecture_status.md:358-359); the reference itself
+ * materialises the scores (dsa_indexer_fused_patch.py:71-133 + topk).
+ * Arguments as in dsa_indexer_topk_streaming (no workspace).  topk is at most
+ * dsa_indexer_topk_fused_max_topk(H, D) (0: no kernel for that shape);
+ * larger requests return DSA_ERR_UNSUPPORTED.
+ */
+int64_t dsa_indexer_topk_fused_max_topk(int64_t H, int64_t D);
+int dsa_indexer_topk_fused(const void *q, const void *w, const void *k,
+                           int32_t *out_idx, float *out_scores, int64_t B,
+                           int64_t Sq, int64_t Sk, int64_t H, int64_t D,
+                           int dtype, int w_dtype, const float *q_scale,
+                           const float *k_scale, int64_t topk, int causal,
+                           int use_relu, void *stream);
+
+/*
  * Tensorwise (current-scaling) quantisation to OCP e4m3:
  *   amax = max|x|, scale = 448 / amax (1 when amax == 0),
  *   out = e4m3(RNE(x * scale)) saturated to +-448, scale_inv = 1 / scale.

@@ -44,7 +44,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_status_codes(lib):
-    assert lib.dsa_abi_version() == 200
+    assert lib.dsa_abi_version() == 201
     text = open(HEADER).read()
     for name, val in (("DSA_OK", 0), ("DSA_ERR_INVALID_ARG", -1), ("DSA_ERR_UNSUPPORTED", -2),
                       ("DSA_ERR_HIP", -3), ("DSA_ERR_WORKSPACE", -4)):
@@ -130,3 +130,23 @@ def test_bwd_workspace_bounded_by_pass_cap(lib):
     assert int(lib.dsa_sparse_mla_bwd_index_size(2, 4096, 4096, 32, 1, 128, 64, 256, 0, 0)) > 0
     assert int(lib.dsa_sparse_mla_bwd_index_size(2, 4096, 4096, 32, 1, 128, 64, 256, 0, 64 << 20)) == 0
     assert int(lib.dsa_sparse_mla_bwd_indexed_workspace_size(2, 4096, 4096, 32, 1, 128, 64, 256, 0, 0)) < one
+
+
+def test_fused_indexer_topk_limits(lib):
+    """The fused indexer + top-k's top-k bound per shape, and its refusals
+    (unsupported shape, top-k past the bound, bad flags, null pointers)
+    before any device work."""
+    assert lib.dsa_indexer_topk_fused_max_topk(16, 64) == 832
+    assert lib.dsa_indexer_topk_fused_max_topk(32, 128) == 1728
+    assert lib.dsa_indexer_topk_fused_max_topk(64, 128) == 3520
+    assert lib.dsa_indexer_topk_fused_max_topk(48, 64) == 0
+    assert lib.dsa_indexer_topk_fused_max_topk(16, 96) == 0
+    args = lambda H, D, k, causal=1, dt=_lib.DTYPE_BF16: (None, None, None, None, None, 2, 8, 8, H, D, dt,
+                                                          _lib.DTYPE_F32, None, None, k, causal, 1, None)
+    assert lib.dsa_indexer_topk_fused(*args(16, 64, 833)) == _lib.DSA_ERR_UNSUPPORTED
+    assert "at most 832" in _err(lib)
+    assert lib.dsa_indexer_topk_fused(*args(48, 64, 8)) == _lib.DSA_ERR_UNSUPPORTED
+    assert lib.dsa_indexer_topk_fused(*args(16, 64, 8, causal=2)) == _lib.DSA_ERR_INVALID_ARG
+    assert lib.dsa_indexer_topk_fused(*args(16, 64, 8, dt=7)) == _lib.DSA_ERR_INVALID_ARG
+    assert lib.dsa_indexer_topk_fused(*args(16, 64, 8)) == _lib.DSA_ERR_INVALID_ARG  # null pointers
+    assert "null tensor pointer" in _err(lib)
