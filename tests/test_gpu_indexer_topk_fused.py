@@ -131,3 +131,23 @@ def test_fused_replays_in_a_graph(dev):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(got, ref)
+
+
+def test_fused_nan_and_inf_scores(dev):
+    """Without the ReLU (which zeroes NaN products here), a key row of +inf and one
+    of NaN make scores +inf and NaN; NaN ranks as +inf with ties to the lower
+    column, as in topk_indices."""
+    Sq, Sk, B, H, D, K = 12, 2000, 1, 16, 64, 64
+    inp = synthetic.indexer_inputs(B, Sk, H, D, seed=199)
+    k = inp["k"].clone()
+    k[700] = float("inf")
+    k[1300] = float("nan")
+    q, w = inp["q"][:Sq].contiguous().abs().to(dev), inp["w"][:Sq].contiguous().abs().to(dev)
+    k = k.to(dev)
+    sc = index_scores(q, w, k, use_relu=False, causal=CAUSAL_NONE)
+    assert torch.isnan(sc).any() and torch.isinf(sc).any()
+    ref = topk_indices(sc, K, causal=False)
+    idx, vals = indexer_topk_fused(q, k, w, K, use_relu=False, causal=False, return_scores=True)
+    assert torch.equal(idx, ref)
+    g = _gathered(sc, ref)
+    assert torch.equal(vals.isnan(), g.isnan()) and torch.equal(vals.nan_to_num(), g.nan_to_num())
