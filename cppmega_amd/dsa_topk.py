@@ -131,7 +131,10 @@ def indexer_topk_streaming(q, k, weights, index_topk, use_relu=True, causal=True
     ``return_scores`` also the selected scores [b, sq, index_topk] f32 (-inf
     on padding).  Query rows go through a scratch of at most
     ``max_scratch_bytes`` (or ``chunk_rows`` rows) in chunks; the indices are
-    bit-identical to ``topk_indices`` over the full scores.  The reference's
+    bit-identical to ``topk_indices`` over the full scores.  With
+    ``max_scratch_bytes=0`` (and no ``chunk_rows``) no scratch is used at all:
+    the top-k runs folded into the score tiles (``indexer_topk_fused``), for
+    index_topk up to ``indexer_topk_fused_max_topk(h, d)``.  The reference's
     stated target for its indexer (docs/status/cppmega_architecture_status.md:340-362)."""
     assert q.dim() == 4 and k.dim() == 3 and weights.dim() == 3
     sq, b, h, d = q.shape
@@ -147,6 +150,12 @@ def indexer_topk_streaming(q, k, weights, index_topk, use_relu=True, causal=True
     if weights.dtype not in (torch.float32, torch.bfloat16):
         weights = weights.float()
     q, k, weights = q.contiguous(), k.contiguous(), weights.contiguous()
+    if chunk_rows is None and int(max_scratch_bytes) == 0:
+        if int(index_topk) > indexer_topk_fused_max_topk(h, d):
+            raise ValueError(f"no scratch: index_topk {index_topk} exceeds the fused path's "
+                             f"{indexer_topk_fused_max_topk(h, d)} for h={h}, d={d}")
+        return indexer_topk_fused(q, k, weights, index_topk, use_relu=use_relu, causal=causal, q_scale=q_scale,
+                                  k_scale=k_scale, return_scores=return_scores)
     if chunk_rows is None:
         chunk_rows = max(1, int(max_scratch_bytes) // max(1, b * sk * 4))
     lib = _lib.load()

@@ -14,7 +14,7 @@ import torch
 
 from cppmega_amd import synthetic
 from cppmega_amd.dsa_indexer_fused_patch import CAUSAL_LOWER, CAUSAL_NONE, index_scores
-from cppmega_amd.dsa_topk import indexer_topk_fused, indexer_topk_fused_max_topk, topk_indices
+from cppmega_amd.dsa_topk import indexer_topk_fused, indexer_topk_fused_max_topk, indexer_topk_streaming, topk_indices
 from cppmega_amd.sparse_mla_ops import tensorwise_quantize
 
 pytestmark = pytest.mark.gpu
@@ -151,3 +151,15 @@ def test_fused_nan_and_inf_scores(dev):
     assert torch.equal(idx, ref)
     g = _gathered(sc, ref)
     assert torch.equal(vals.isnan(), g.isnan()) and torch.equal(vals.nan_to_num(), g.nan_to_num())
+
+
+def test_streaming_without_scratch_is_fused(dev):
+    """indexer_topk_streaming(max_scratch_bytes=0) takes the fused path (same
+    result), and refuses a top-k the fused path cannot hold."""
+    S, B, H, D, K = 600, 2, 16, 64, 100
+    inp = synthetic.indexer_inputs(B, S, H, D, seed=201)
+    q, k, w = inp["q"].to(dev), inp["k"].to(dev), inp["w"].to(dev)
+    _, ref = _full(q, k, w, K, True)
+    assert torch.equal(indexer_topk_streaming(q, k, w, K, max_scratch_bytes=0), ref)
+    with pytest.raises(ValueError):
+        indexer_topk_streaming(q, k, w, indexer_topk_fused_max_topk(H, D) + 1, max_scratch_bytes=0)
