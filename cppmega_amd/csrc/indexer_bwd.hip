@@ -152,9 +152,11 @@ indexer_bwd_q_kernel(const IdxBwdParams p) {
   const int64_t wave_row0 = t0 * H + w * C::RPW;      // (token, head) rows t * H + h
   const int64_t wave_tok_last = (wave_row0 + C::RPW - 1) / H;
   int64_t wave_kend = p.causal ? (wave_tok_last + 1 < p.Sk ? wave_tok_last + 1 : p.Sk) : p.Sk;
-  // keys below every row limit of the wave (causal: its first token + 1); not used with windows
+  // keys [wave_klo, wave_khi) lie in every row's range of the wave (causal: below its
+  // first token + 1; windows: the intersection of the rows' windows, set below)
   const int64_t wave_tok0 = wave_row0 / H;
-  const int64_t wave_kfull = p.causal ? (wave_tok0 + 1 < p.Sk ? wave_tok0 + 1 : p.Sk) : p.Sk;
+  int64_t wave_klo = 0;
+  int64_t wave_khi = p.causal ? (wave_tok0 + 1 < p.Sk ? wave_tok0 + 1 : p.Sk) : p.Sk;
 
   // key tiles: rows [first, first + KT) of batch b through a resource ending at the last key
   const uint32_t row_pitch = (uint32_t)(p.B * C::ROWB);
@@ -242,22 +244,31 @@ indexer_bwd_q_kernel(const IdxBwdParams p) {
     }
   }
   if constexpr (WIN) {
-    // the union of the wave's row ranges: sub-tiles outside it are skipped
-    int lo = 0x7fffffff, hi = 0;
+    // the union of the wave's row ranges (sub-tiles outside it are skipped) and
+    // their intersection (sub-tiles inside it need no key test)
+    int lo = 0x7fffffff, hi = 0, ilo = 0, ihi = 0x7fffffff;
 #pragma unroll
-    for (int m = 0; m < C::MT; ++m)
+    for (int m = 0; m < C::MT; ++m) {
       if (klim[m] > klo[m]) {
         lo = klo[m] < lo ? klo[m] : lo;
         hi = klim[m] > hi ? klim[m] : hi;
       }
+      ilo = klo[m] > ilo ? klo[m] : ilo;
+      ihi = klim[m] < ihi ? klim[m] : ihi;
+    }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
       const int lo2 = __shfl_xor(lo, off, 64), hi2 = __shfl_xor(hi, off, 64);
+      const int ilo2 = __shfl_xor(ilo, off, 64), ihi2 = __shfl_xor(ihi, off, 64);
       lo = lo2 < lo ? lo2 : lo;
       hi = hi2 > hi ? hi2 : hi;
+      ilo = ilo2 > ilo ? ilo2 : ilo;
+      ihi = ihi2 < ihi ? ihi2 : ihi;
     }
     wave_kend = __builtin_amdgcn_readfirstlane(hi);
     wave_kbeg = hi > 0 ? __builtin_amdgcn_readfirstlane(lo) : 0;
+    wave_klo = __builtin_amdgcn_readfirstlane(ilo);
+    wave_khi = __builtin_amdgcn_readfirstlane(ihi);  // below wave_klo: no interior sub-tile
   }
   f32x16 dqa[C::MT][C::DT];
   float dwa[C::MT];
@@ -303,7 +314,8 @@ indexer_bwd_q_kernel(const IdxBwdParams p) {
       }
       // M = G act'(L) (0 off the causal window and past Sk), dw += M L; M -> bf16 B operands.
       // 32-bit keys and non-short-circuit predicates: one select per element, no branches.
-      // A sub-tile below every row limit of the wave (the causal interior) needs no key test.
+      // A sub-tile inside every row range of the wave (the causal interior, or the
+      // intersection of the row windows) needs no key test.
       const int s0 = (int)sn + 4 * g32;
       bf16x8 MB[C::MT][2];
       auto form_m = [&](auto interior) {
@@ -318,7 +330,7 @@ indexer_bwd_q_kernel(const IdxBwdParams p) {
             for (int j = 0; j < 4; ++j) {
               const int s = s0 + 8 * i + j;
               const float L = acc[m][4 * i + j];
-              const bool ok = (IN | (s < klim[m])) & (!WIN | (s >= klo[m])) & (!RELU | (L > 0.0f));
+              const bool ok = (IN | ((s < klim[m]) & (!WIN | (s >= klo[m])))) & (!RELU | (L > 0.0f));
               const float v = ok ? gv[m][i][j] : 0.0f;
               dwa[m] = fmaf(v, L, dwa[m]);
               mv[j] = v;
@@ -331,7 +343,7 @@ indexer_bwd_q_kernel(const IdxBwdParams p) {
             MB[m][kc] = as_bf16x8(i32x4{(int)mw[4 * kc], (int)mw[4 * kc + 1], (int)mw[4 * kc + 2], (int)mw[4 * kc + 3]});
         }
       };
-      if (!WIN && sn + 32 <= wave_kfull) form_m(std::true_type{});
+      if (sn >= wave_klo && sn + 32 <= wave_khi) form_m(std::true_type{});
       else form_m(std::false_type{});
       // dq^T[d][row] += K^T[d][key] M[key][row]: keys of k-step kc in the accumulator order
 #pragma unroll
