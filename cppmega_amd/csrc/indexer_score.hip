@@ -881,10 +881,20 @@ __device__ __forceinline__ void idx_block_topk(const IdxParams &p, const FusedTo
     thr[tl] = 0;
     opn[tl] = 1;
   }
-  auto select_row = [&](int tl) {  // keep row tl's current top-k (wave-uniform call)
-    const uint32_t K = cand_keep_top<CAP / 64>(cand_off + (uint32_t)(tl * CAP * 8), cnt[tl], topk, hist_off);
-    cnt[tl] = topk;
-    thr[tl] = (int)K;
+  // select_row keeps row tl's current top-k (exact), or prunes its list to a
+  // superset of it with a raised threshold (wave-uniform call).
+  // Pruning selections (1/16 of the surplus over the top-k may stay) short of
+  // the final one, at the shortest lists only, where they save the exact
+  // ranking's share of a call: measured 11% faster at 16 heads, no gain at 32,
+  // slower at 64.  Only where the kept list always leaves the slack free.
+  constexpr int PRUNE = CAP / 64 <= 14 ? 16 : 0;
+  const int prune = PRUNE > 0 && topk + (CAP - topk) / PRUNE <= CAP - kFusedSlack ? PRUNE : 0;
+  auto select_row = [&](int tl, bool exact) {
+    const uint2 kk = cand_keep_top<CAP / 64>(cand_off + (uint32_t)(tl * CAP * 8), cnt[tl], topk, hist_off,
+                                             PRUNE > 0 && !exact ? prune : 0);
+    // (the count wave-uniform, so the list tests stay scalar branches)
+    cnt[tl] = PRUNE > 0 ? __builtin_amdgcn_readfirstlane((int)kk.y) : topk;
+    thr[tl] = (int)kk.x;
     opn[tl] = 0;
   };
   // the scores of this lane's row tl at key s (valid: a candidate of the row)
@@ -900,8 +910,8 @@ __device__ __forceinline__ void idx_block_topk(const IdxParams &p, const FusedTo
     uint64_t bm = __ballot(in);
     int n0 = __popc((uint32_t)bm), n1 = __popc((uint32_t)(bm >> 32));
     if (cnt[t_lo] + n0 > CAP || (C::TPW >= 2 && cnt[t_hi] + n1 > CAP)) {  // rare, wave-uniform
-      if (cnt[t_lo] + n0 > CAP) select_row(t_lo);
-      if (C::TPW >= 2 && cnt[t_hi] + n1 > CAP) select_row(t_hi);
+      if (cnt[t_lo] + n0 > CAP) select_row(t_lo, false);
+      if (C::TPW >= 2 && cnt[t_hi] + n1 > CAP) select_row(t_hi, false);
       in = valid && ((g32 ? opn[t_hi] : opn[t_lo]) != 0 || key > (uint32_t)(g32 ? thr[t_hi] : thr[t_lo]));
       bm = __ballot(in);
       n0 = __popc((uint32_t)bm);
@@ -951,7 +961,7 @@ __device__ __forceinline__ void idx_block_topk(const IdxParams &p, const FusedTo
   // each row: its list's top-k, in column order
 #pragma unroll
   for (int tl = 0; tl < C::TPW; ++tl) {
-    if (cnt[tl] > topk) select_row(tl);
+    if (cnt[tl] > topk) select_row(tl, true);
     wave_lds_sync();
     const int64_t t = wave_tok0 + tl;
     if (t < p.Sq) {

@@ -26,7 +26,14 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) { return wv::wave_r
 
 // Keeps the top r entries of list c (1 <= r <= n <= 64 NPL) at its front, in
 // list order, under the top-k contract; returns the order key K of the r-th
-// largest (every kept entry ranks at or above it).  The entries stay in
+// largest (every kept entry ranks at or above it) and the count kept (r).
+// prune > 0 (pruning) stops after the first binning round that leaves at
+// most 1/prune of the n - r surplus: it keeps every entry whose key is at
+// least the least key K of the bin holding the r-th largest (at least r of
+// them) and returns that K and their count: an
+// entry with key K arriving later has a higher column than every kept one of
+// key K and at least r entries rank above it, so later entries need a key
+// above K either way.  The entries stay in
 // registers for the whole call (order key 0 marks an absent one: no score has
 // it).  Selection: each round bins the keys of the current range [lo, hi]
 // into 256 bins linear in the key, keeps the bin holding the r-th largest and
@@ -42,7 +49,8 @@ extern __shared__ __attribute__((aligned(16))) unsigned char fsmem[];
 // ran cold).  The list and histogram are byte offsets into fsmem, so their
 // accesses stay LDS instructions.
 template <int NPL>
-__device__ __noinline__ uint32_t cand_keep_top(uint32_t c_off, int n, int r, uint32_t hist_off) {
+__device__ __noinline__ uint2 cand_keep_top(uint32_t c_off, int n, int r, uint32_t hist_off, int prune) {
+  prune = __builtin_amdgcn_readfirstlane(prune);
   uint2 *c = reinterpret_cast<uint2 *>(fsmem + c_off);
   int *hist = reinterpret_cast<int *>(fsmem + hist_off);
   const int lane = lane_id();
@@ -64,6 +72,7 @@ __device__ __noinline__ uint32_t cand_keep_top(uint32_t c_off, int n, int r, uin
   uint32_t lo = wave_min_u32(mn), hi = wave_max_u32(mx);
   uint32_t K = lo;
   int c_eq = r;
+  const int r0 = r;
 #pragma unroll 1
   for (int round = 0; round < 12; ++round) {
     if (lo == hi) {
@@ -131,7 +140,7 @@ __device__ __noinline__ uint32_t cand_keep_top(uint32_t c_off, int n, int r, uin
     const int incl = (int)wv::wave_incl_scan((uint32_t)local);
     const int excl = incl - local;
     const bool cross = excl < r && incl >= r;
-    int d_l = 0, above_l = 0;
+    int d_l = 0, above_l = 0, inbin_l = 0;
     if (cross) {
       int acc = excl;
 #pragma unroll
@@ -139,6 +148,7 @@ __device__ __noinline__ uint32_t cand_keep_top(uint32_t c_off, int n, int r, uin
         if (acc < r && acc + cq[q] >= r) {
           d_l = 255 - 4 * lane - q;
           above_l = acc;
+          inbin_l = cq[q];
         }
         acc += cq[q];
       }
@@ -147,6 +157,7 @@ __device__ __noinline__ uint32_t cand_keep_top(uint32_t c_off, int n, int r, uin
     const int src = cl < 0 ? 0 : cl;
     const int d = (int)wv::readlane((uint32_t)d_l, src);
     r -= (int)wv::readlane((uint32_t)above_l, src);
+    const int inbin = (int)wv::readlane((uint32_t)inbin_l, src);
     wave_lds_sync();  // the histogram reads finish before it is reused
 #pragma unroll
     for (int i = 0; i < NPL; ++i) asm volatile("" : "+v"(bin[i]));
@@ -161,6 +172,12 @@ __device__ __noinline__ uint32_t cand_keep_top(uint32_t c_off, int n, int r, uin
     hi = wave_max_u32(bmx);
     K = lo;  // (the loop ends on a one-key range well within its bound)
     c_eq = r;
+    // pruning: every key of the bin and above stays, once that frees at
+    // least 1 - 1/prune of what the exact selection would
+    if (prune > 0 && prune * ((r0 - r) + inbin - r0) <= n - r0) {
+      c_eq = 0x7fffffff;
+      break;
+    }
   }
   // keep the entries above K and the first c_eq equal to it, in list order
   // (entry e = lane + 64 i: list order is i-major); every entry is in
@@ -177,7 +194,7 @@ __device__ __noinline__ uint32_t cand_keep_top(uint32_t c_off, int n, int r, uin
     eq_seen += __popcll(em);
   }
   wave_lds_sync();
-  return K;
+  return make_uint2(K, (uint32_t)kept);
 }
 
 }  // namespace dsa
