@@ -725,11 +725,14 @@ extern "C" int dsa_indexer_topk_streaming(const void *q, const void *w, const vo
 // in LDS, appended in column order as the 32-key sub-tiles are scored (the
 // same scoring code as idx_segment, so the scores are bit-identical to the
 // dense indexer's).  A row's list takes every key until it would overflow;
-// then an exact selection keeps the row's current top-k (under the top-k
-// contract: value descending, NaN as +inf, -0 equal to +0, ties to the lower
-// column) and raises the row's threshold to the k-th kept value.  Later keys
-// enter only above it: a key equal to it has a higher column than every kept
-// equal one and loses the tie.  At the end the list's top-k is the row's.
+// then a selection keeps the row's current top-k (under the top-k contract:
+// value descending, NaN as +inf, -0 equal to +0, ties to the lower column)
+// and raises the row's threshold to the k-th kept value.  Later keys enter
+// only above it: a key equal to it has a higher column than every kept equal
+// one and loses the tie.  (At 16 heads a selection short of the last may
+// prune instead: it keeps a superset of the top-k, every key at or above a
+// threshold with at least k kept keys at or above it, so the same argument
+// holds.)  At the end an exact selection leaves the row's top-k.
 // ---------------------------------------------------------------------------
 namespace dsa {
 
