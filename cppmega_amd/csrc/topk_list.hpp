@@ -27,20 +27,19 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) { return wv::wave_r
 // Keeps the top r entries of list c (1 <= r <= n <= 64 NPL) at its front, in
 // list order, under the top-k contract; returns the order key K of the r-th
 // largest (every kept entry ranks at or above it) and the count kept (r).
-// prune > 0 (pruning) stops after the first binning round that leaves at
-// most 1/prune of the n - r surplus: it keeps every entry whose key is at
-// least the least key K of the bin holding the r-th largest (at least r of
-// them) and returns that K and their count: an
-// entry with key K arriving later has a higher column than every kept one of
-// key K and at least r entries rank above it, so later entries need a key
-// above K either way.  The entries stay in
-// registers for the whole call (order key 0 marks an absent one: no score has
-// it).  Selection: each round bins the keys of the current range [lo, hi]
-// into 256 bins linear in the key, keeps the bin holding the r-th largest and
-// narrows the range to that bin's keys, about 256x per round (float bin
-// arithmetic is exact below 2^24 and monotone above), until the range is one
-// key or holds at most 64 keys, which are ranked exactly.  hist: this wave's
-// 256 ints (16-byte aligned).
+// With prune > 0 the call may stop after the first binning round that leaves
+// at most 1/prune of the n - r surplus: it then keeps every entry whose key is
+// at least the least key K of the bin holding the r-th largest (at least r of
+// them), in list order, and returns that K and their count.  A later entry of
+// key K has a higher column than every kept entry of key K and ranks below at
+// least r kept entries, so later entries need a key above K either way.
+// The entries stay in registers for the whole call (order key 0 marks an
+// absent one: no score has it).  Selection: each round bins the keys of the
+// current range [lo, hi] into 256 bins linear in the key, keeps the bin
+// holding the r-th largest and narrows the range to that bin's keys, about
+// 256x per round (float bin arithmetic is exact below 2^24 and monotone
+// above), until the range is one key or holds at most 64 keys, which are
+// ranked exactly.  hist: this wave's 256 ints (16-byte aligned).
 // The workgroup's dynamic LDS (key tiles, candidate lists, histograms).
 extern __shared__ __attribute__((aligned(16))) unsigned char fsmem[];
 
