@@ -729,8 +729,8 @@ extern "C" int dsa_indexer_topk_streaming(const void *q, const void *w, const vo
 // value descending, NaN as +inf, -0 equal to +0, ties to the lower column)
 // and raises the row's threshold to the k-th kept value.  Later keys enter
 // only above it: a key equal to it has a higher column than every kept equal
-// one and loses the tie.  (At 16 heads a selection short of the last may
-// prune instead: it keeps a superset of the top-k, every key at or above a
+// one and loses the tie.  (A selection short of the last may prune
+// instead: it keeps a superset of the top-k, every key at or above a
 // threshold with at least k kept keys at or above it, so the same argument
 // holds.)  At the end an exact selection leaves the row's top-k.
 // ---------------------------------------------------------------------------
@@ -887,16 +887,16 @@ __device__ __forceinline__ void idx_block_topk(const IdxParams &p, const FusedTo
   // select_row keeps row tl's current top-k (exact), or prunes its list to a
   // superset of it with a raised threshold (wave-uniform call).
   // Pruning selections (1/16 of the surplus over the top-k may stay) short of
-  // the final one, at the shortest lists only, where they save the exact
-  // ranking's share of a call: measured 11% faster at 16 heads, no gain at 32,
-  // slower at 64.  Only where the kept list always leaves the slack free.
-  constexpr int PRUNE = CAP / 64 <= 14 ? 16 : 0;
-  const int prune = PRUNE > 0 && topk + (CAP - topk) / PRUNE <= CAP - kFusedSlack ? PRUNE : 0;
+  // the final one save the exact ranking's share of a call: measured 10%
+  // faster at 16 heads (cfg3), 5% at 64 (cfg5), 3% at 32.  Only where the kept
+  // list always leaves the slack free.
+  constexpr int PRUNE = 16;
+  const int prune = topk + (CAP - topk) / PRUNE <= CAP - kFusedSlack ? PRUNE : 0;
   auto select_row = [&](int tl, bool exact) {
     const uint2 kk = cand_keep_top<CAP / 64>(cand_off + (uint32_t)(tl * CAP * 8), cnt[tl], topk, hist_off,
-                                             PRUNE > 0 && !exact ? prune : 0);
+                                             exact ? 0 : prune);
     // (the count wave-uniform, so the list tests stay scalar branches)
-    cnt[tl] = PRUNE > 0 ? __builtin_amdgcn_readfirstlane((int)kk.y) : topk;
+    cnt[tl] = __builtin_amdgcn_readfirstlane((int)kk.y);
     thr[tl] = (int)kk.x;
     opn[tl] = 0;
   };
