@@ -886,11 +886,12 @@ __device__ __forceinline__ void idx_block_topk(const IdxParams &p, const FusedTo
   }
   // select_row keeps row tl's current top-k (exact), or prunes its list to a
   // superset of it with a raised threshold (wave-uniform call).
-  // Pruning selections (1/16 of the surplus over the top-k may stay) short of
-  // the final one save the exact ranking's share of a call: measured 10%
-  // faster at 16 heads (cfg3), 5% at 64 (cfg5), 3% at 32.  Only where the kept
-  // list always leaves the slack free.
-  constexpr int PRUNE = 16;
+  // Pruning selections (1/32 of the surplus over the top-k may stay) short of
+  // the final one save the exact ranking's share of a call: measured 11%
+  // faster at 16 heads (cfg3), 6% at 64 (cfg5), 4% at 32 (1/8 and 1/16 of the
+  // surplus: 1-3% less gain).  Only where the kept list always leaves the
+  // slack free.
+  constexpr int PRUNE = 32;
   const int prune = topk + (CAP - topk) / PRUNE <= CAP - kFusedSlack ? PRUNE : 0;
   auto select_row = [&](int tl, bool exact) {
     const uint2 kk = cand_keep_top<CAP / 64>(cand_off + (uint32_t)(tl * CAP * 8), cnt[tl], topk, hist_off,
